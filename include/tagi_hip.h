@@ -1,0 +1,262 @@
+/*
+ * libtagi_hip — C ABI of the MI355X (gfx950) TAGI step engine.
+ *
+ * One TAGI training step (forward moments -> output innovation -> backward deltas ->
+ * capped parameter update) is built from the entry points below. Every entry point:
+ *   - takes raw device pointers to fp32 buffers, int64 sizes and a hipStream_t
+ *     (passed as void*; NULL means the null stream);
+ *   - queues its kernels on that stream and returns without synchronising;
+ *   - never allocates or frees device memory: outputs and workspaces are the caller's;
+ *   - returns TAGI_OK (0) or a TAGI_ERR_* code, with a message in tagi_last_error().
+ * All tensors are contiguous row-major unless a stride descriptor says otherwise.
+ *
+ * Each declaration names the reference interface it replaces (file:line in
+ * miquelflorensa/triton-tagi).
+ */
+#ifndef TAGI_HIP_H
+#define TAGI_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TAGI_ABI_VERSION 1
+
+enum {
+  TAGI_OK = 0,
+  TAGI_ERR_ARG = 1,         /* bad size, null pointer, or too-small workspace   */
+  TAGI_ERR_LAUNCH = 2,      /* hipGetLastError reported a failure after launch  */
+  TAGI_ERR_UNSUPPORTED = 3  /* shape outside what the kernels implement         */
+};
+
+typedef void* tagi_stream_t; /* a hipStream_t */
+
+/* ---------------------------------------------------------------- housekeeping */
+int tagi_abi_version(void);
+/* Message of the last failing call on this host thread ("" if none). */
+const char* tagi_last_error(void);
+
+/* Live per-kernel-family timer (HIP events around each launch, on the launch stream).
+ * family_mask: bit f enables family f (TAGI_FAM_*). Events are created at begin. */
+int tagi_prof_begin(uint64_t family_mask);
+/* Waits for the recorded events; fills per-family totals (arrays of TAGI_FAM_COUNT):
+ * milliseconds, launches, algorithmic FLOPs and algorithmic bytes. Turns the timer off. */
+int tagi_prof_end(double* ms, int64_t* launches, double* flops, double* bytes);
+enum {
+  TAGI_FAM_CONV_FWD = 0, TAGI_FAM_CONV_BWD_DELTA = 1, TAGI_FAM_CONV_WGRAD = 2,
+  TAGI_FAM_LINEAR_FWD = 3, TAGI_FAM_LINEAR_BWD_DELTA = 4, TAGI_FAM_LINEAR_WGRAD = 5,
+  TAGI_FAM_BMM_FWD = 6, TAGI_FAM_BMM_SHARED = 7, TAGI_FAM_RELU = 8, TAGI_FAM_REMAX = 9,
+  TAGI_FAM_BN_STATS = 10, TAGI_FAM_BN_FWD = 11, TAGI_FAM_BN_BWD = 12, TAGI_FAM_UPDATE = 13,
+  TAGI_FAM_INNOVATION = 14, TAGI_FAM_ADD = 15, TAGI_FAM_AVGPOOL = 16, TAGI_FAM_JACOBIAN = 17,
+  TAGI_FAM_RMSNORM = 18, TAGI_FAM_EMBEDDING = 19, TAGI_FAM_PE = 20, TAGI_FAM_SPLITK_REDUCE = 21,
+  TAGI_FAM_COUNT = 22
+};
+
+/* ------------------------------------------------------------------ Linear ---- */
+/* Fused Linear forward moments, one MFMA pass sharing the A/B tiles:
+ *   mz = ma @ mw + mb
+ *   Sz = ma^2 @ Sw + Sa @ (mw^2 + Sw) + Sb
+ * ma, Sa (M,K); mw, Sw (K,N); mb, Sb (N) or NULL (no bias); mz, Sz (M,N).
+ * mz may be NULL: then only Sz is produced (triton_fused_var_forward).
+ * Replaces linear.py:99-100 (torch.matmul + triton_fused_var_forward, common.py:170). */
+int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw,
+                    const float* mb, const float* Sb, float* mz, float* Sz,
+                    int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes,
+                    tagi_stream_t stream);
+int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N);
+
+/* Backward delta propagation:  dma = dmz @ mw^T ;  dSa = dSz @ (mw^2)^T.
+ * dmz, dSz (M,N); mw (K,N); dma, dSa (M,K).
+ * Replaces triton_fused_backward_delta (common.py:287). */
+int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const float* mw,
+                          float* dma, float* dSa, int64_t M, int64_t K, int64_t N,
+                          tagi_stream_t stream);
+
+/* Parameter deltas of a Linear layer (reduction over the M rows):
+ *   gmw = ma^T @ dmz, gSw = (ma^2)^T @ dSz, gmb = sum_rows dmz, gSb = sum_rows dSz
+ *   dmw = Sw * gmw, dSw = Sw^2 * gSw, dmb = Sb * gmb, dSb = Sb^2 * gSb
+ * Sw == NULL gives the raw gmw/gSw (triton_fused_weight_grad, common.py:410);
+ * dmb == NULL skips the bias. ws: split-K partials, size from tagi_linear_wgrad_ws_bytes.
+ * Replaces linear.py:138-151. */
+int tagi_linear_wgrad(const float* ma, const float* dmz, const float* dSz, const float* Sw,
+                      const float* Sb, float* dmw, float* dSw, float* dmb, float* dSb,
+                      int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes,
+                      tagi_stream_t stream);
+int64_t tagi_linear_wgrad_ws_bytes(int64_t M, int64_t K, int64_t N);
+
+/* ------------------------------------------------------- batched products ---- */
+/* A strided batched operand: element (z, i, j) of batch z sits at
+ *   base + (z / zdiv) * sz1 + (z % zdiv) * sz2 + i * si + j * sj
+ * which covers (B,H,S,D) head views of a (B,S,E) tensor and transposed views. */
+typedef struct {
+  int64_t zdiv, sz1, sz2, si, sj;
+} tagi_view;
+
+/* TAGI product of two Gaussian batched matrices, mean and variance in one pass:
+ *   mean[z,m,l] = scale    * sum_k mu_a[z,m,k] mu_b[z,k,l]
+ *   var [z,m,l] = scale_sq * sum_k ( var_a (mu_b^2 + var_b) + mu_a^2 var_b )
+ * mean may be NULL (bmm_tagi_var). Views: a (i=m, j=k), b (i=k, j=l), out (i=m, j=l).
+ * Replaces bmm_tagi_var (attention.py:149) plus the mean torch.matmul
+ * (multihead_attention.py:180,192). */
+int tagi_bmm_tagi(const float* mu_a, const float* var_a, const float* mu_b, const float* var_b,
+                  float* mean, float* var, int64_t batch, int64_t M, int64_t K, int64_t L,
+                  const tagi_view* va, const tagi_view* vb, const tagi_view* vo, float scale,
+                  float scale_sq, tagi_stream_t stream);
+
+/* Batched product with one deterministic operand.
+ * shared_left == 0 (bmm_shared_right, attention.py:286):
+ *   mean = scale * a_mean @ b ;  var = scale_sq * a_var @ b^2   (a: mean/var, b: shared)
+ * shared_left == 1 (bmm_shared_left, attention.py:339):
+ *   mean = scale * a @ b_mean ;  var = scale_sq * a^2 @ b_var   (a: shared, b: mean/var)
+ * p0/p1 are the mean/var pair of the non-shared side, p2 the shared operand. */
+int tagi_bmm_shared(const float* p0, const float* p1, const float* p2, float* mean, float* var,
+                    int64_t batch, int64_t M, int64_t K, int64_t L, const tagi_view* va,
+                    const tagi_view* vb, const tagi_view* vo, float scale, float scale_sq,
+                    int shared_left, tagi_stream_t stream);
+
+/* ------------------------------------------------------------------ Conv2D ---- */
+/* Geometry of a square-kernel 2-D convolution on NCHW tensors. pad_top/pad_left are the
+ * zero rows/cols before the image; rows/cols past H/W read as zero. padding_type 1
+ * (symmetric p) is pad_top = pad_left = p, Ho = (H + 2p - k)/s + 1; padding_type 2
+ * (right/bottom only, conv2d.py:280-291) is pad_top = pad_left = 0, Ho = (H + p - k)/s + 1. */
+typedef struct {
+  int64_t N, C, H, W, Cout, k, stride, pad_top, pad_left, Ho, Wo;
+} tagi_conv_geom;
+
+/* Implicit-GEMM forward: patches are gathered into LDS, never materialised.
+ *   mz = P(ma) @ mw + mb ; Sz = P(ma)^2 @ Sw + P(Sa) @ (mw^2 + Sw) + Sb, written NCHW.
+ * mw, Sw (C*k*k, Cout) with rows ordered (c, kh, kw); mb, Sb (Cout).
+ * Replaces Conv2D.forward (conv2d.py:254-309: im2col + matmul + fused var + permute). */
+int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw,
+                    const float* mb, const float* Sb, float* mz, float* Sz,
+                    const tagi_conv_geom* g, float* ws, int64_t ws_bytes, tagi_stream_t stream);
+int64_t tagi_conv2d_fwd_ws_bytes(const tagi_conv_geom* g);
+
+/* Transposed implicit GEMM for the input deltas (no patch matrix, no col2im):
+ *   dma = fold(dmz_rows @ mw^T), dSa = fold(dSz_rows @ (mw^2)^T), NCHW (N,C,H,W).
+ * Replaces conv2d.py:357-370 (fused backward delta + col2im + crop). */
+int tagi_conv2d_bwd_delta(const float* dmz, const float* dSz, const float* mw, float* dma,
+                          float* dSa, const tagi_conv_geom* g, tagi_stream_t stream);
+
+/* Parameter deltas of a Conv2D layer (reduction over N*Ho*Wo patches, split-K):
+ *   dmw = Sw * P^T @ dmz, dSw = Sw^2 * (P^2)^T @ dSz, dmb = Sb * sum dmz, dSb = Sb^2 * sum dSz.
+ * Replaces conv2d.py:341-354. */
+int tagi_conv2d_wgrad(const float* ma, const float* dmz, const float* dSz, const float* Sw,
+                      const float* Sb, float* dmw, float* dSw, float* dmb, float* dSb,
+                      const tagi_conv_geom* g, float* ws, int64_t ws_bytes, tagi_stream_t stream);
+int64_t tagi_conv2d_wgrad_ws_bytes(const tagi_conv_geom* g);
+
+/* ------------------------------------------------------------- elementwise ---- */
+/* Rectified-Gaussian moments: ma, Sa, J = Phi(alpha) (Phi ~ pdf/(-alpha) for alpha < -5).
+ * Replaces bayesian_relu / _bayesian_relu_kernel (relu.py:43-122). */
+int tagi_relu_fwd(const float* mz, const float* Sz, float* ma, float* Sa, float* J, int64_t n,
+                  tagi_stream_t stream);
+
+/* Jacobian backward shared by ReLU and Remax: dm_out = dm * J, dS_out = dS * J^2.
+ * Replaces relu.py:152-169 and remax.py:185-188. */
+int tagi_jacobian_bwd(const float* dm, const float* dS, const float* J, float* dm_out,
+                      float* dS_out, int64_t n, tagi_stream_t stream);
+
+/* Remax over the last dim of a (rows, K) tensor: mu_a, var_a, J.
+ * Replaces triton_remax / _remax_kernel (remax.py:33-159). */
+int tagi_remax_fwd(const float* mz, const float* Sz, float* ma, float* Sa, float* J,
+                   int64_t rows, int64_t K, tagi_stream_t stream);
+
+/* Dense output innovation: dm = (y - mu)/(var + sv2), dS = -1/(var + sv2).
+ * Replaces compute_innovation / _output_innovation_kernel (observation.py:24-46,119-163). */
+int tagi_innovation(const float* y, const float* mu, const float* var, float sigma_v2,
+                    float* dm, float* dS, int64_t n, tagi_stream_t stream);
+
+/* In-place capped update (both caps use the pre-update S):
+ *   bar = sqrt(max(S,1e-10))/cap; m += sign(dm) min(|dm|,bar);
+ *   S' = S + sign(dS) min(|dS|,bar); S = S' <= 0 ? 1e-5 : S'.
+ * Replaces update_parameters / _capped_param_update_kernel (parameters.py:58-128). */
+int tagi_capped_update(float* m, float* S, const float* dm, const float* dS, float cap_factor,
+                       int64_t n, tagi_stream_t stream);
+
+/* Many capped updates in one launch: tensor t has n[t] elements at m[t], S[t], dm[t], dS[t].
+ * The pointer/size tables live in host memory and are copied into the kernel arguments
+ * (at most 64 tensors per call). Same arithmetic as tagi_capped_update. */
+int tagi_capped_update_multi(float* const* m, float* const* S, const float* const* dm,
+                             const float* const* dS, const int64_t* n, int64_t count,
+                             float cap_factor, tagi_stream_t stream);
+
+/* In-place moment add: mu_a += mu_s ; var_a += var_s.
+ * Replaces triton_add_shortcut and triton_delta_merge (resblock.py:138,157). */
+int tagi_add_inplace(const float* mu_s, const float* var_s, float* mu_a, float* var_a, int64_t n,
+                     tagi_stream_t stream);
+
+/* Non-overlapping k x k average pool of NCHW moments: mean scaled by 1/k^2, variance by
+ * var_scale (1/k^4 default, 1/k^2 with spatial_correlation). Replaces avgpool2d.py:38-130. */
+int tagi_avgpool2d_fwd(const float* ma, const float* Sa, float* ma_out, float* Sa_out, int64_t N,
+                       int64_t C, int64_t H, int64_t W, int64_t k, float var_scale,
+                       tagi_stream_t stream);
+int tagi_avgpool2d_bwd(const float* dm, const float* dS, float* dm_out, float* dS_out, int64_t N,
+                       int64_t C, int64_t H, int64_t W, int64_t k, float var_scale,
+                       tagi_stream_t stream);
+
+/* ----------------------------------------------------------- BatchNorm2D ---- */
+/* Per-channel batch statistics of NCHW moments (batchnorm2d.py:307-339):
+ *   mean_c = E[mu], var_c = (E[S] + E[mu^2] - mean_c^2) * n/(n-1), n = N*H*W,
+ * and the running-stat / gamma bookkeeping of batchnorm2d.py:341-355:
+ *   first_call: running := batch, and if preserve_var: mg := sqrt(var + eps);
+ *   otherwise running := (1-momentum) running + momentum batch.
+ * ws: per-block partial sums, size from tagi_bn_stats_ws_bytes. */
+int tagi_bn_stats(const float* mz, const float* Sz, float* batch_mean, float* batch_var,
+                  float* running_mean, float* running_var, float* mg, int64_t N, int64_t C,
+                  int64_t HW, float momentum, float eps, int first_call, int preserve_var,
+                  float* ws, int64_t ws_bytes, tagi_stream_t stream);
+int64_t tagi_bn_stats_ws_bytes(int64_t N, int64_t C, int64_t HW);
+
+/* Normalise + Gaussian affine (batchnorm2d.py:59-126):
+ *   mhat = (mu - mean)/sqrt(var+eps), Shat = S/(var+eps),
+ *   ma = mg mhat + mb, Sa = mg^2 Shat + Sg (mhat^2 + Shat) + Sb.  Shat may be NULL. */
+int tagi_bn_fwd(const float* mz, const float* Sz, const float* mean, const float* var,
+                const float* mg, const float* Sg, const float* mb, const float* Sb, float* ma,
+                float* Sa, float* mhat, float* Shat, int64_t N, int64_t C, int64_t HW, float eps,
+                tagi_stream_t stream);
+
+/* Backward (batchnorm2d.py:134-192, 465-513): dmz = dma mg/sqrt(var+eps),
+ * dSz = dSa mg^2/(var+eps), and the parameter deltas
+ * dmg = Sg sum(dma mhat), dSg = Sg^2 sum(dSa mhat^2), dmb = Sb sum dma, dSb = Sb^2 sum dSa. */
+int tagi_bn_bwd(const float* dma, const float* dSa, const float* mhat, const float* var,
+                const float* mg, const float* Sg, const float* Sb, float* dmz, float* dSz,
+                float* dmg, float* dSg, float* dmb, float* dSb, int64_t N, int64_t C, int64_t HW,
+                float eps, float* ws, int64_t ws_bytes, tagi_stream_t stream);
+int64_t tagi_bn_bwd_ws_bytes(int64_t N, int64_t C, int64_t HW);
+
+/* -------------------------------------------------- RMSNorm / Embedding / PE ---- */
+/* RMSNorm forward over rows of length D (rms_norm.py:93-110); inv_rms (rows) is cached. */
+int tagi_rmsnorm_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw,
+                     float* mz, float* Sz, float* inv_rms, int64_t rows, int64_t D, float eps,
+                     tagi_stream_t stream);
+/* RMSNorm backward (rms_norm.py:115-134): propagated deltas and gamma deltas. */
+int tagi_rmsnorm_bwd(const float* dmz, const float* dSz, const float* ma, const float* inv_rms,
+                     const float* mw, const float* Sw, float* dma, float* dSa, float* dmw,
+                     float* dSw, int64_t rows, int64_t D, float* ws, int64_t ws_bytes,
+                     tagi_stream_t stream);
+int64_t tagi_rmsnorm_bwd_ws_bytes(int64_t rows, int64_t D);
+
+/* Embedding lookup (embedding.py:88-106): tokens are float ids (cast toward zero).
+ * Rows equal to padding_idx (>= 0) emit zeros. */
+int tagi_embedding_fwd(const float* tokens, const float* mw, const float* Sw, float* mz,
+                       float* Sz, int64_t n_tokens, int64_t V, int64_t D, int64_t padding_idx,
+                       tagi_stream_t stream);
+/* Embedding deltas (embedding.py:111-150): dmw[cat] = sum dm Sw[cat], dSw[cat] = sum dS Sw[cat]^2
+ * over the tokens of each category; dmw/dSw (V,D) are overwritten. Deterministic two-stage
+ * reduction through ws (size from tagi_embedding_bwd_ws_bytes); V <= 256. */
+int tagi_embedding_bwd(const float* tokens, const float* dmz, const float* dSz, const float* Sw,
+                       float* dmw, float* dSw, int64_t n_tokens, int64_t V, int64_t D,
+                       int64_t padding_idx, float* ws, int64_t ws_bytes, tagi_stream_t stream);
+int64_t tagi_embedding_bwd_ws_bytes(int64_t n_tokens, int64_t V, int64_t D);
+
+/* Sinusoidal positional encoding add (positional_encoding.py:62): out = ma + pe[:S]. */
+int tagi_pe_add(const float* ma, const float* pe, float* out, int64_t B, int64_t S, int64_t E,
+                tagi_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TAGI_HIP_H */

@@ -1,0 +1,375 @@
+"""Kernel-level parity: every HIP entry point against the float64 CPU oracle.
+
+Inputs are seeded fp32 tensors; the oracle evaluates the reference's equations on the
+same values in float64. Tolerance (the engine's bar): |gpu - oracle| <= 1e-6 + 1e-4 *
+scale, where scale is |oracle| for variances and elementwise results, and the sum of
+absolute products for GEMM means (fp32 rounding is relative to that sum when terms
+cancel).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import assert_scaled_close
+from oracle import tagi_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-4, 1e-6
+
+
+def g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def d64(t):
+    return t.detach().to("cpu", torch.float64)
+
+
+LINEAR_SHAPES = [(1, 3, 2), (37, 29, 13), (128, 512, 10), (256, 784, 256), (64, 2048, 96), (300, 64, 700),
+                 (16, 4096, 64)]
+
+
+@pytest.mark.parametrize("M,K,N", LINEAR_SHAPES)
+def test_linear_forward(dev, M, K, N):
+    from triton_tagi_amd.kernels.common import fused_var_forward, linear_forward
+
+    r = g(M * 131 + K * 7 + N)
+    ma, Sa = torch.randn(M, K, generator=r), 0.01 + 0.09 * torch.rand(M, K, generator=r)
+    mw, Sw = torch.randn(K, N, generator=r) / K**0.5, torch.rand(K, N, generator=r) / K
+    mb, Sb = torch.randn(1, N, generator=r), 1e-3 * torch.rand(1, N, generator=r)
+    mz, Sz = linear_forward(*(t.to(dev) for t in (ma, Sa, mw, Sw, mb, Sb)))
+    rm, rS = O.linear_moments(*(d64(t) for t in (ma, Sa, mw, Sw, mb, Sb)))
+    scale = d64(ma).abs() @ d64(mw).abs() + d64(mb).abs()
+    assert_scaled_close(mz, rm, scale, RTOL, ATOL, "mz")
+    assert_scaled_close(Sz, rS, None, RTOL, ATOL, "Sz")
+    Sz2 = fused_var_forward(*(t.to(dev) for t in (ma, Sa, mw, Sw, Sb)))
+    assert torch.equal(Sz2.cpu(), Sz.cpu())
+
+
+@pytest.mark.parametrize("M,K,N", LINEAR_SHAPES)
+def test_linear_backward_delta(dev, M, K, N):
+    from triton_tagi_amd.kernels.common import fused_backward_delta
+
+    r = g(M + 17 * K + 3 * N)
+    dmz, dSz = torch.randn(M, N, generator=r), -torch.rand(M, N, generator=r)
+    mw = torch.randn(K, N, generator=r) / K**0.5
+    dma, dSa = fused_backward_delta(dmz.to(dev), dSz.to(dev), mw.to(dev))
+    rm, rS = O.linear_backward_delta(d64(dmz), d64(dSz), d64(mw))
+    assert_scaled_close(dma, rm, d64(dmz).abs() @ d64(mw).abs().T, RTOL, ATOL, "dma")
+    assert_scaled_close(dSa, rS, None, RTOL, ATOL, "dSa")
+
+
+@pytest.mark.parametrize("M,K,N", LINEAR_SHAPES + [(8192, 64, 32), (65536, 27, 16)])
+def test_linear_param_deltas(dev, M, K, N):
+    from triton_tagi_amd.kernels.common import fused_weight_grad, linear_param_deltas
+
+    r = g(5 * M + K + 11 * N)
+    a = torch.randn(M, K, generator=r)
+    dmz, dSz = 0.1 * torch.randn(M, N, generator=r), -1e-2 * torch.rand(M, N, generator=r)
+    Sw, Sb = torch.rand(K, N, generator=r) / K, torch.rand(1, N, generator=r) / K
+    dmw, dSw, dmb, dSb = linear_param_deltas(a.to(dev), dmz.to(dev), dSz.to(dev), Sw.to(dev), Sb.to(dev))
+    gmw, gmb, gSw, gSb = O.linear_param_grads(d64(a), d64(dmz), d64(dSz))
+    S64, Sb64 = d64(Sw), d64(Sb)
+    assert_scaled_close(dmw, S64 * gmw, S64 * (d64(a).abs().T @ d64(dmz).abs()), RTOL, ATOL, "delta_mw")
+    assert_scaled_close(dSw, S64 * S64 * gSw, None, RTOL, ATOL, "delta_Sw")
+    assert_scaled_close(dmb, Sb64 * gmb, Sb64 * d64(dmz).abs().sum(0, keepdim=True), RTOL, ATOL, "delta_mb")
+    assert_scaled_close(dSb, Sb64 * Sb64 * gSb, None, RTOL, ATOL, "delta_Sb")
+    raw_m, raw_S = fused_weight_grad(a.to(dev), dmz.to(dev), dSz.to(dev))
+    assert_scaled_close(raw_m, gmw, d64(a).abs().T @ d64(dmz).abs(), RTOL, ATOL, "raw grad mw")
+    assert_scaled_close(raw_S, gSw, None, RTOL, ATOL, "raw grad Sw")
+
+
+def test_relu(dev):
+    from triton_tagi_amd.layers.relu import bayesian_relu
+
+    r = g(3)
+    mz = 3 * torch.randn(1000, 37, generator=r)
+    Sz = torch.rand(1000, 37, generator=r) * 2 + 1e-4
+    mz[0, :8] = torch.tensor([-20.0, -6.0, -5.01, -4.99, 0.0, 5.0, 40.0, -1e-3])
+    Sz[0, :8] = torch.tensor([1.0, 1.0, 1.0, 1.0, 1e-8, 1e-6, 1.0, 1e-2])
+    ma, Sa, J = bayesian_relu(mz.to(dev), Sz.to(dev))
+    rm, rS, rJ = O.relu_moments(d64(mz), d64(Sz))
+    assert_scaled_close(ma, rm, None, RTOL, ATOL, "relu mean")
+    assert_scaled_close(Sa, rS, rS.abs() + d64(mz) ** 2 * 1e-3, RTOL, ATOL, "relu var")
+    assert_scaled_close(J, rJ, None, RTOL, ATOL, "relu J")
+
+
+@pytest.mark.parametrize("B,K", [(128, 10), (7, 1), (4096, 64), (300, 77), (512, 256), (3, 1000)])
+def test_remax(dev, B, K):
+    from triton_tagi_amd.layers.remax import remax
+
+    r = g(B * 7 + K)
+    mz = torch.randn(B, K, generator=r)
+    Sz = 0.05 + torch.rand(B, K, generator=r)
+    ma, Sa, J = remax(mz.to(dev), Sz.to(dev))
+    rm, rS, rJ = O.remax_moments(d64(mz), d64(Sz))
+    assert_scaled_close(ma, rm, None, RTOL, ATOL, "remax mean")
+    assert_scaled_close(Sa, rS, None, RTOL, ATOL, "remax var")
+    assert_scaled_close(J, rJ, None, RTOL, ATOL, "remax J")
+
+
+def test_innovation_update_add_jacobian(dev):
+    from triton_tagi_amd.layers.relu import jacobian_backward
+    from triton_tagi_amd.layers.resblock import add_shortcut
+    from triton_tagi_amd.update.observation import compute_innovation
+    from triton_tagi_amd.update.parameters import update_parameters, update_parameters_multi
+
+    r = g(9)
+    y, mu, var = torch.randn(257, 13, generator=r), torch.randn(257, 13, generator=r), torch.rand(257, 13, generator=r)
+    dm, dS = compute_innovation(y.to(dev), mu.to(dev), var.to(dev), 0.05)
+    rdm, rdS = O.innovation(d64(y), d64(mu), d64(var), 0.05)
+    assert_scaled_close(dm, rdm, None, RTOL, ATOL, "innovation dm")
+    assert_scaled_close(dS, rdS, None, RTOL, ATOL, "innovation dS")
+
+    for n in (1, 5, 4096, 100003):
+        m, S = torch.randn(n, generator=r), torch.rand(n, generator=r) * 1e-2
+        S[: min(n, 3)] = torch.tensor([1e-12, 1e-4, 0.5])[: min(n, 3)]
+        ddm = torch.randn(n, generator=r) * 0.1
+        ddS = torch.randn(n, generator=r) * 1e-2
+        ddm[0], ddS[0] = 0.0, -1.0  # zero mean delta, variance pushed below zero
+        mg, Sg = m.to(dev), S.to(dev)
+        update_parameters(mg, Sg, ddm.to(dev), ddS.to(dev), 2.0)
+        rm, rS = O.capped_update(d64(m), d64(S), d64(ddm), d64(ddS), 2.0)
+        assert_scaled_close(mg, rm, None, RTOL, ATOL, f"update m n={n}")
+        assert_scaled_close(Sg, rS, None, RTOL, ATOL, f"update S n={n}")
+
+    groups, refs = [], []
+    for n in (3, 4096 * 3 + 1, 17, 70000):
+        m, S = torch.randn(n, generator=r), 1e-3 + torch.rand(n, generator=r) * 1e-2
+        ddm, ddS = torch.randn(n, generator=r) * 0.05, torch.randn(n, generator=r) * 1e-2
+        groups.append(tuple(t.to(dev) for t in (m, S, ddm, ddS)))
+        refs.append(O.capped_update(d64(m), d64(S), d64(ddm), d64(ddS), 3.0))
+    update_parameters_multi(groups, 3.0)
+    for (mg, Sg, _, _), (rm, rS) in zip(groups, refs):
+        assert_scaled_close(mg, rm, None, RTOL, ATOL, "multi update m")
+        assert_scaled_close(Sg, rS, None, RTOL, ATOL, "multi update S")
+
+    a, b, c, d = (torch.randn(1001, generator=r) for _ in range(4))
+    ag, bg = a.to(dev), b.to(dev)
+    add_shortcut(c.to(dev), d.to(dev), ag, bg)
+    assert torch.equal(ag.cpu(), a + c) and torch.equal(bg.cpu(), b + d)
+
+    J = torch.rand(333, generator=r)
+    om, oS = jacobian_backward(a[:333].to(dev), b[:333].to(dev), J.to(dev))
+    assert_scaled_close(om, d64(a[:333]) * d64(J), None, RTOL, ATOL, "jacobian mean")
+    assert_scaled_close(oS, d64(b[:333]) * d64(J) ** 2, None, RTOL, ATOL, "jacobian var")
+
+
+@pytest.mark.parametrize("k,sc", [(2, False), (4, False), (2, True), (3, False)])
+def test_avgpool(dev, k, sc):
+    from triton_tagi_amd.layers.avgpool2d import AvgPool2D
+
+    r = g(k)
+    ma, Sa = torch.randn(3, 5, 12, 12, generator=r), torch.rand(3, 5, 12, 12, generator=r)
+    layer, ref = AvgPool2D(k, sc), O.OAvgPool2D(k, sc)
+    mo, So = layer.forward(ma.to(dev), Sa.to(dev))
+    rm, rS = ref.forward(d64(ma), d64(Sa))
+    assert_scaled_close(mo, rm, d64(ma).abs().mean() * torch.ones_like(rm), RTOL, ATOL, "pool mean")
+    assert_scaled_close(So, rS, None, RTOL, ATOL, "pool var")
+    dm, dS = torch.randn(rm.shape, generator=r), torch.rand(rm.shape, generator=r)
+    om, oS = layer.backward(dm.to(dev), dS.to(dev))
+    qm, qS = ref.backward(d64(dm), d64(dS))
+    assert_scaled_close(om, qm, None, RTOL, ATOL, "pool bwd mean")
+    assert_scaled_close(oS, qS, None, RTOL, ATOL, "pool bwd var")
+
+
+CONV_CASES = [
+    # N, C, H, W, Cout, k, stride, padding, padding_type
+    (2, 3, 8, 8, 5, 3, 1, 1, 1),
+    (2, 3, 32, 32, 32, 5, 1, 2, 1),
+    (3, 4, 9, 7, 6, 3, 2, 1, 2),
+    (2, 8, 16, 16, 16, 3, 2, 1, 2),
+    (2, 8, 16, 16, 16, 2, 2, 0, 1),
+    (1, 16, 8, 8, 32, 3, 1, 1, 1),
+    (4, 64, 8, 8, 128, 3, 2, 1, 2),
+    (2, 5, 11, 11, 7, 4, 3, 2, 1),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=[str(c) for c in CONV_CASES])
+def test_conv2d_forward_backward(dev, case):
+    from triton_tagi_amd.layers.conv2d import Conv2D
+
+    N, C, H, W, Cout, k, s, p, pt = case
+    torch.manual_seed(sum(case))
+    layer = Conv2D(C, Cout, k, stride=s, padding=p, padding_type=pt, device="cpu")
+    ref = O.mirror(layer)
+    for a in ("mw", "Sw", "mb", "Sb"):
+        setattr(layer, a, getattr(layer, a).to(dev))
+    r = g(sum(case) + 1)
+    ma, Sa = torch.randn(N, C, H, W, generator=r), torch.rand(N, C, H, W, generator=r)
+    mz, Sz = layer.forward(ma.to(dev), Sa.to(dev))
+    rm, rS = ref.forward(d64(ma), d64(Sa))
+    P = ref.patches
+    scale = (P.abs() @ ref.mw.abs() + ref.mb.abs()).view(N, *ref.spatial, Cout).permute(0, 3, 1, 2)
+    assert_scaled_close(mz, rm, scale, RTOL, ATOL, "conv mz")
+    assert_scaled_close(Sz, rS, None, RTOL, ATOL, "conv Sz")
+    dmz, dSz = 0.1 * torch.randn(rm.shape, generator=r), -1e-2 * torch.rand(rm.shape, generator=r)
+    dma, dSa = layer.backward(dmz.to(dev), dSz.to(dev))
+    qm, qS = ref.backward(d64(dmz), d64(dSz))
+    dm_rows = d64(dmz).permute(0, 2, 3, 1).reshape(-1, Cout)
+    sc_in = O.col2im(dm_rows.abs() @ ref.mw.abs().T, N, C, H, W, k, s, p, pt)
+    assert_scaled_close(dma, qm, sc_in, RTOL, ATOL, "conv delta ma")
+    assert_scaled_close(dSa, qS, None, RTOL, ATOL, "conv delta Sa")
+    sc_w = ref.Sw * (P.abs().T @ dm_rows.abs())
+    assert_scaled_close(layer.delta_mw, ref.delta_mw, sc_w, RTOL, ATOL, "conv delta mw")
+    assert_scaled_close(layer.delta_Sw, ref.delta_Sw, None, RTOL, ATOL, "conv delta Sw")
+    assert_scaled_close(layer.delta_mb, ref.delta_mb, ref.Sb * dm_rows.abs().sum(0, keepdim=True), RTOL, ATOL,
+                        "conv delta mb")
+    assert_scaled_close(layer.delta_Sb, ref.delta_Sb, None, RTOL, ATOL, "conv delta Sb")
+
+
+@pytest.mark.parametrize("shape,first,preserve", [((4, 6, 5, 5), True, True), ((8, 64, 8, 8), True, False),
+                                                  ((3, 5, 4, 4), False, False), ((128, 16, 4, 4), True, True)])
+def test_batchnorm(dev, shape, first, preserve):
+    from triton_tagi_amd.layers.batchnorm2d import BatchNorm2D
+
+    N, C, H, W = shape
+    torch.manual_seed(N + C)
+    layer = BatchNorm2D(C, device="cpu", gain_w=0.3, gain_b=0.2, preserve_var=preserve)
+    r = g(C)
+    layer.mw = 1.0 + 0.1 * torch.randn(C, generator=r)
+    if not first:
+        layer._is_initialized = True
+        layer.running_mean = torch.randn(C, generator=r)
+        layer.running_var = torch.rand(C, generator=r) + 0.5
+    ref = O.mirror(layer)
+    for a in ("mw", "Sw", "mb", "Sb", "running_mean", "running_var"):
+        setattr(layer, a, getattr(layer, a).to(dev))
+    mz, Sz = 2 + torch.randn(shape, generator=r), torch.rand(shape, generator=r)
+    ma, Sa = layer.forward(mz.to(dev), Sz.to(dev))
+    rm, rS = ref.forward(d64(mz), d64(Sz))
+    assert_scaled_close(layer.running_mean, ref.running_mean, None, RTOL, ATOL, "running mean")
+    assert_scaled_close(layer.running_var, ref.running_var, None, RTOL, ATOL, "running var")
+    assert_scaled_close(layer.mw, ref.mw, None, RTOL, ATOL, "gamma after first call")
+    assert_scaled_close(ma, rm, rm.abs() + 1.0, RTOL, ATOL, "bn mean")
+    assert_scaled_close(Sa, rS, None, RTOL, ATOL, "bn var")
+    dma, dSa = torch.randn(shape, generator=r), -torch.rand(shape, generator=r)
+    om, oS = layer.backward(dma.to(dev), dSa.to(dev))
+    qm, qS = ref.backward(d64(dma), d64(dSa))
+    assert_scaled_close(om, qm, None, RTOL, ATOL, "bn bwd mean")
+    assert_scaled_close(oS, qS, None, RTOL, ATOL, "bn bwd var")
+    mh = ref.m_hat
+    assert_scaled_close(layer.delta_mw, ref.delta_mw, ref.Sw * (d64(dma) * mh).abs().sum((0, 2, 3)), RTOL, ATOL,
+                        "bn delta gamma")
+    assert_scaled_close(layer.delta_Sw, ref.delta_Sw, None, RTOL, ATOL, "bn delta Sgamma")
+    assert_scaled_close(layer.delta_mb, ref.delta_mb, ref.Sb * d64(dma).abs().sum((0, 2, 3)), RTOL, ATOL,
+                        "bn delta beta")
+    assert_scaled_close(layer.delta_Sb, ref.delta_Sb, None, RTOL, ATOL, "bn delta Sbeta")
+
+
+def test_rmsnorm_embedding_pe(dev):
+    from triton_tagi_amd.layers import Embedding, PositionalEncoding, RMSNorm
+
+    torch.manual_seed(4)
+    r = g(4)
+    rms = RMSNorm([96], device="cpu")
+    rms.mw = 1 + 0.1 * torch.randn(96, generator=r)
+    ref = O.mirror(rms)
+    rms.mw, rms.Sw = rms.mw.to(dev), rms.Sw.to(dev)
+    ma, Sa = torch.randn(5, 33, 96, generator=r), torch.rand(5, 33, 96, generator=r)
+    mz, Sz = rms.forward(ma.to(dev), Sa.to(dev))
+    rm, rS = ref.forward(d64(ma), d64(Sa))
+    assert_scaled_close(mz, rm, None, RTOL, ATOL, "rms mean")
+    assert_scaled_close(Sz, rS, None, RTOL, ATOL, "rms var")
+    dm, dS = torch.randn(5, 33, 96, generator=r), -torch.rand(5, 33, 96, generator=r)
+    om, oS = rms.backward(dm.to(dev), dS.to(dev))
+    qm, qS = ref.backward(d64(dm), d64(dS))
+    assert_scaled_close(om, qm, None, RTOL, ATOL, "rms bwd mean")
+    assert_scaled_close(oS, qS, None, RTOL, ATOL, "rms bwd var")
+    sc = (ref.inv * ref.m_in * d64(dm).reshape(-1, 96)).abs().sum(0) * ref.Sw
+    assert_scaled_close(rms.delta_mw, ref.delta_mw, sc, RTOL, ATOL, "rms delta gamma")
+    assert_scaled_close(rms.delta_Sw, ref.delta_Sw, None, RTOL, ATOL, "rms delta Sgamma")
+
+    for pad in (-1, 3):
+        emb = Embedding(17, 40, scale=0.25, padding_idx=pad, device="cpu")
+        eref = O.mirror(emb)
+        emb.mw, emb.Sw = emb.mw.to(dev), emb.Sw.to(dev)
+        tok = torch.randint(0, 17, (6, 300), generator=r).to(torch.float32)
+        mz, Sz = emb.forward(tok.to(dev), torch.zeros_like(tok).to(dev))
+        rm, rS = eref.forward(d64(tok), d64(tok) * 0)
+        assert torch.equal(mz.cpu().double(), rm) and torch.equal(Sz.cpu().double(), rS)
+        dm, dS = torch.randn(6, 300, 40, generator=r), -torch.rand(6, 300, 40, generator=r)
+        zm, zS = emb.backward(dm.to(dev), dS.to(dev))
+        eref.backward(d64(dm), d64(dS))
+        assert float(zm.abs().sum()) == 0.0 and tuple(zm.shape) == (6, 300)
+        sc = torch.zeros(17, 40, dtype=torch.float64).index_add_(
+            0, tok.long().reshape(-1), (d64(dm).reshape(-1, 40) * eref.Sw[tok.long().reshape(-1)]).abs())
+        assert_scaled_close(emb.delta_mw, eref.delta_mw, sc, RTOL, ATOL, "emb delta mw")
+        assert_scaled_close(emb.delta_Sw, eref.delta_Sw, None, RTOL, ATOL, "emb delta Sw")
+
+    pe = PositionalEncoding(64, max_seq_len=512, device="cpu")
+    pref = O.OPositionalEncoding(O.sinusoidal_table(512, 64))
+    pe.pe_cache = pe.pe_cache.to(dev)
+    ma = torch.randn(3, 200, 64, generator=r)
+    out, _ = pe.forward(ma.to(dev), ma.to(dev))
+    ro, _ = pref.forward(d64(ma), d64(ma))
+    assert_scaled_close(out, ro, ro.abs() + 1, RTOL, ATOL, "pe add")
+
+
+@pytest.mark.parametrize("B,S,E,H", [(2, 16, 32, 2), (3, 40, 64, 8), (2, 256, 256, 8)])
+def test_attention_layer(dev, B, S, E, H):
+    from triton_tagi_amd.layers import MultiheadAttentionV2
+
+    torch.manual_seed(B + S)
+    att = MultiheadAttentionV2(E, H, S, gain_weight=0.25, gain_bias=0.5, device="cpu")
+    ref = O.mirror(att)
+    for lin in (att.q_proj, att.k_proj, att.v_proj):
+        for a in ("mw", "Sw", "mb", "Sb"):
+            setattr(lin, a, getattr(lin, a).to(dev))
+    r = g(S)
+    ma, Sa = torch.randn(B, S, E, generator=r), 0.1 * torch.rand(B, S, E, generator=r)
+    mo, So = att.forward(ma.to(dev), Sa.to(dev))
+    rm, rS = ref.forward(d64(ma), d64(Sa))
+    msc, vsc = att.get_attention_scores()
+    assert_scaled_close(msc, ref.attn[0], None, RTOL, ATOL, "scores mean")
+    assert_scaled_close(vsc, ref.attn[1], None, RTOL, ATOL, "scores var")
+    assert_scaled_close(mo, rm, rm.abs() + rm.abs().mean(), 1e-3, 1e-6, "attn out mean")
+    assert_scaled_close(So, rS, None, 1e-3, 1e-6, "attn out var")
+    dm, dS = 0.1 * torch.randn(B, S, E, generator=r), -1e-2 * torch.rand(B, S, E, generator=r)
+    om, oS = att.backward(dm.to(dev), dS.to(dev))
+    qm, qS = ref.backward(d64(dm), d64(dS))
+    assert_scaled_close(om, qm, qm.abs() + qm.abs().mean(), 1e-3, 1e-6, "attn bwd mean")
+    assert_scaled_close(oS, qS, qS.abs() + qS.abs().mean(), 1e-3, 1e-6, "attn bwd var")
+    for name in ("q_proj", "k_proj", "v_proj"):
+        gl, rl = getattr(att, name), getattr(ref, name[0])
+        assert_scaled_close(gl.delta_mw, rl.delta_mw, rl.delta_mw.abs() + rl.delta_mw.abs().mean(), 1e-3, 1e-6,
+                            f"{name} delta mw")
+        assert_scaled_close(gl.delta_Sw, rl.delta_Sw, rl.delta_Sw.abs() + rl.delta_Sw.abs().mean(), 1e-3, 1e-6,
+                            f"{name} delta Sw")
+
+
+@pytest.mark.parametrize("transpose_a,transpose_b", [(False, False), (True, False), (False, True), (True, True)])
+def test_bmm_wrappers_strided(dev, transpose_a, transpose_b):
+    from triton_tagi_amd.kernels.attention import bmm_shared_left, bmm_shared_right, bmm_tagi, bmm_tagi_var
+
+    r = g(int(transpose_a) * 2 + int(transpose_b))
+    B, H, M, K, L = 2, 3, 33, 20, 45
+
+    def mk(shape, t):
+        x = torch.randn(*shape, generator=r)
+        return x.transpose(-1, -2).contiguous().transpose(-1, -2) if t else x
+
+    ma, va = mk((B, H, M, K), transpose_a), mk((B, H, M, K), transpose_a).abs()
+    mb, vb = mk((B, H, K, L), transpose_b), mk((B, H, K, L), transpose_b).abs()
+    if transpose_a:
+        va = va.transpose(-1, -2).contiguous().transpose(-1, -2)
+    if transpose_b:
+        vb = vb.transpose(-1, -2).contiguous().transpose(-1, -2)
+    mean, var = bmm_tagi(ma.to(dev), va.to(dev), mb.to(dev), vb.to(dev), scale=0.7)
+    rm, rv = O.bmm_tagi(d64(ma), d64(va), d64(mb), d64(vb), 0.7)
+    assert_scaled_close(mean, rm, 0.7 * d64(ma).abs() @ d64(mb).abs(), RTOL, ATOL, "bmm mean")
+    assert_scaled_close(var, rv, None, RTOL, ATOL, "bmm var")
+    v2 = bmm_tagi_var(ma.to(dev), va.to(dev), mb.to(dev), vb.to(dev), scale_sq=0.49)
+    assert_scaled_close(v2, rv, None, RTOL, ATOL, "bmm_tagi_var")
+    m3, v3 = bmm_shared_right(ma.to(dev), va.to(dev), mb.to(dev), scale=0.5)
+    rm3, rv3 = O.bmm_shared_right(d64(ma), d64(va), d64(mb), 0.5)
+    assert_scaled_close(m3, rm3, 0.5 * d64(ma).abs() @ d64(mb).abs(), RTOL, ATOL, "shared right mean")
+    assert_scaled_close(v3, rv3, None, RTOL, ATOL, "shared right var")
+    m4, v4 = bmm_shared_left(ma.to(dev), mb.to(dev), vb.to(dev), scale=2.0)
+    rm4, rv4 = O.bmm_shared_left(d64(ma), d64(mb), d64(vb), 2.0)
+    assert_scaled_close(m4, rm4, 2.0 * d64(ma).abs() @ d64(mb).abs(), RTOL, ATOL, "shared left mean")
+    assert_scaled_close(v4, rv4, None, RTOL, ATOL, "shared left var")

@@ -1,0 +1,496 @@
+// Bandwidth-bound TAGI kernels: rectified-Gaussian moments, Remax, output innovation,
+// capped parameter update, moment add, average pooling and the Jacobian backward.
+//
+// Elementwise kernels are grid-stride loops over float4 when every pointer is 16-byte
+// aligned (the torch caching allocator's normal case), scalar otherwise. One lane owns
+// four consecutive elements, so a wavefront moves 1 KiB per access.
+#include "tagi_common.h"
+
+namespace tagi {
+
+#define INV_SQRT_2PI 0.3989422804014327f
+#define INV_SQRT_2 0.7071067811865476f
+
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <typename F>
+__device__ __forceinline__ void for_each_vec(int64_t n, F f) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) f(i);
+}
+
+// ------------------------------------------------------------------------------ ReLU
+// relu.py:43-86: exact rectified-Gaussian moments; Phi by erf, replaced by the
+// asymptotic pdf/(-alpha) when alpha < -5; variance floored at 0.
+__device__ __forceinline__ void relu_moments(float mz, float Sz, float& ma, float& Sa, float& J) {
+  const float Ss = fmaxf(Sz, 1e-30f);
+  const float sig = sqrtf(Ss);
+  const float alpha = mz / sig;
+  const float pdf = expf(-0.5f * alpha * alpha) * INV_SQRT_2PI;
+  // Phi(alpha) = 0.5 (1 + erf(alpha/sqrt2)) evaluated as 0.5 erfc(-alpha/sqrt2): equal in
+  // exact arithmetic, without the fp32 cancellation of the erf form for alpha < 0.
+  const float cdf_erf = 0.5f * erfcf(-alpha * INV_SQRT_2);
+  const float cdf_asym = pdf / (-alpha);
+  const float cdf = (alpha < -5.0f) ? cdf_asym : cdf_erf;
+  const float mu = sig * pdf + mz * cdf;
+  float var = -mu * mu + 2.0f * mu * mz - mz * sig * pdf + (Ss - mz * mz) * cdf;
+  ma = mu;
+  Sa = fmaxf(var, 0.0f);
+  J = cdf;
+}
+
+template <bool VEC>
+__global__ void relu_kernel(const float* __restrict__ mz, const float* __restrict__ Sz, float* __restrict__ ma,
+                            float* __restrict__ Sa, float* __restrict__ J, int64_t n) {
+  if constexpr (VEC) {
+    const int64_t n4 = n >> 2;
+    for_each_vec(n4, [&](int64_t i) {
+      const float4 m = reinterpret_cast<const float4*>(mz)[i];
+      const float4 s = reinterpret_cast<const float4*>(Sz)[i];
+      float4 a, b, j;
+      relu_moments(m.x, s.x, a.x, b.x, j.x);
+      relu_moments(m.y, s.y, a.y, b.y, j.y);
+      relu_moments(m.z, s.z, a.z, b.z, j.z);
+      relu_moments(m.w, s.w, a.w, b.w, j.w);
+      reinterpret_cast<float4*>(ma)[i] = a;
+      reinterpret_cast<float4*>(Sa)[i] = b;
+      reinterpret_cast<float4*>(J)[i] = j;
+    });
+    // tail
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+      const int64_t i = (n4 << 2) + threadIdx.x;
+      relu_moments(mz[i], Sz[i], ma[i], Sa[i], J[i]);
+    }
+  } else {
+    for_each_vec(n, [&](int64_t i) { relu_moments(mz[i], Sz[i], ma[i], Sa[i], J[i]); });
+  }
+}
+
+// -------------------------------------------------------------- Jacobian backward
+template <bool VEC>
+__global__ void jacobian_kernel(const float* __restrict__ dm, const float* __restrict__ dS,
+                                const float* __restrict__ J, float* __restrict__ om, float* __restrict__ oS,
+                                int64_t n) {
+  if constexpr (VEC) {
+    const int64_t n4 = n >> 2;
+    for_each_vec(n4, [&](int64_t i) {
+      const float4 a = reinterpret_cast<const float4*>(dm)[i];
+      const float4 b = reinterpret_cast<const float4*>(dS)[i];
+      const float4 j = reinterpret_cast<const float4*>(J)[i];
+      reinterpret_cast<float4*>(om)[i] = make_float4(a.x * j.x, a.y * j.y, a.z * j.z, a.w * j.w);
+      reinterpret_cast<float4*>(oS)[i] =
+          make_float4(b.x * j.x * j.x, b.y * j.y * j.y, b.z * j.z * j.z, b.w * j.w * j.w);
+    });
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+      const int64_t i = (n4 << 2) + threadIdx.x;
+      om[i] = dm[i] * J[i];
+      oS[i] = dS[i] * J[i] * J[i];
+    }
+  } else {
+    for_each_vec(n, [&](int64_t i) {
+      om[i] = dm[i] * J[i];
+      oS[i] = dS[i] * J[i] * J[i];
+    });
+  }
+}
+
+// ------------------------------------------------------------------------ Innovation
+template <bool VEC>
+__global__ void innovation_kernel(const float* __restrict__ y, const float* __restrict__ mu,
+                                  const float* __restrict__ var, float sv2, float* __restrict__ dm,
+                                  float* __restrict__ dS, int64_t n) {
+  for_each_vec(n, [&](int64_t i) {
+    const float Sy = var[i] + sv2;
+    dm[i] = (y[i] - mu[i]) / Sy;
+    dS[i] = -1.0f / Sy;
+  });
+}
+
+// -------------------------------------------------------------------- Capped update
+__device__ __forceinline__ float signf_(float x) { return x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f); }
+
+__device__ __forceinline__ void capped(float& m, float& S, float dm, float dS, float cap) {
+  const float bar = sqrtf(fmaxf(S, 1e-10f)) / cap;
+  m = m + signf_(dm) * fminf(fabsf(dm), bar);
+  const float Sr = S + signf_(dS) * fminf(fabsf(dS), bar);
+  S = (Sr <= 0.f) ? 1e-5f : Sr;
+}
+
+template <bool VEC>
+__global__ void update_kernel(float* __restrict__ m, float* __restrict__ S, const float* __restrict__ dm,
+                              const float* __restrict__ dS, float cap, int64_t n) {
+  if constexpr (VEC) {
+    const int64_t n4 = n >> 2;
+    for_each_vec(n4, [&](int64_t i) {
+      float4 a = reinterpret_cast<float4*>(m)[i];
+      float4 b = reinterpret_cast<float4*>(S)[i];
+      const float4 c = reinterpret_cast<const float4*>(dm)[i];
+      const float4 d = reinterpret_cast<const float4*>(dS)[i];
+      capped(a.x, b.x, c.x, d.x, cap);
+      capped(a.y, b.y, c.y, d.y, cap);
+      capped(a.z, b.z, c.z, d.z, cap);
+      capped(a.w, b.w, c.w, d.w, cap);
+      reinterpret_cast<float4*>(m)[i] = a;
+      reinterpret_cast<float4*>(S)[i] = b;
+    });
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+      const int64_t i = (n4 << 2) + threadIdx.x;
+      capped(m[i], S[i], dm[i], dS[i], cap);
+    }
+  } else {
+    for_each_vec(n, [&](int64_t i) { capped(m[i], S[i], dm[i], dS[i], cap); });
+  }
+}
+
+constexpr int kMultiMax = 32;
+constexpr int kMultiChunk = 4096;  // elements per block
+struct MultiUpdateArgs {
+  float* m[kMultiMax];
+  float* S[kMultiMax];
+  const float* dm[kMultiMax];
+  const float* dS[kMultiMax];
+  int64_t n[kMultiMax];
+  int64_t block_start[kMultiMax + 1];
+  int count;
+  float cap;
+};
+
+// One launch for many parameter tensors: blocks are dealt to tensors by a prefix table.
+__global__ void update_multi_kernel(MultiUpdateArgs a) {
+  const int64_t b = blockIdx.x;
+  int t = 0;
+  while (t + 1 < a.count && a.block_start[t + 1] <= b) ++t;
+  const int64_t base = (b - a.block_start[t]) * kMultiChunk;
+  const int64_t n = a.n[t];
+  float* m = a.m[t];
+  float* S = a.S[t];
+  const float* dm = a.dm[t];
+  const float* dS = a.dS[t];
+  for (int64_t i = base + threadIdx.x; i < base + kMultiChunk && i < n; i += blockDim.x) {
+    float mm = m[i], ss = S[i];
+    capped(mm, ss, dm[i], dS[i], a.cap);
+    m[i] = mm;
+    S[i] = ss;
+  }
+}
+
+// ------------------------------------------------------------------------ Add
+template <bool VEC>
+__global__ void add_kernel(const float* __restrict__ ms, const float* __restrict__ vs, float* __restrict__ ma,
+                           float* __restrict__ va, int64_t n) {
+  if constexpr (VEC) {
+    const int64_t n4 = n >> 2;
+    for_each_vec(n4, [&](int64_t i) {
+      float4 a = reinterpret_cast<float4*>(ma)[i];
+      float4 b = reinterpret_cast<float4*>(va)[i];
+      const float4 c = reinterpret_cast<const float4*>(ms)[i];
+      const float4 d = reinterpret_cast<const float4*>(vs)[i];
+      a.x += c.x; a.y += c.y; a.z += c.z; a.w += c.w;
+      b.x += d.x; b.y += d.y; b.z += d.z; b.w += d.w;
+      reinterpret_cast<float4*>(ma)[i] = a;
+      reinterpret_cast<float4*>(va)[i] = b;
+    });
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+      const int64_t i = (n4 << 2) + threadIdx.x;
+      ma[i] += ms[i];
+      va[i] += vs[i];
+    }
+  } else {
+    for_each_vec(n, [&](int64_t i) {
+      ma[i] += ms[i];
+      va[i] += vs[i];
+    });
+  }
+}
+
+// -------------------------------------------------------------------- AvgPool2D
+__global__ void avgpool_fwd_kernel(const float* __restrict__ ma, const float* __restrict__ Sa,
+                                   float* __restrict__ mo, float* __restrict__ So, int64_t NC, int H, int W, int k,
+                                   float inv_k2, float var_scale) {
+  const int Ho = H / k, Wo = W / k;
+  const int64_t total = NC * Ho * Wo;
+  for_each_vec(total, [&](int64_t i) {
+    const int64_t nc = i / (Ho * Wo);
+    const int r = (int)(i - nc * (Ho * Wo));
+    const int oh = r / Wo, ow = r - (r / Wo) * Wo;
+    const float* pm = ma + nc * H * W + (int64_t)(oh * k) * W + ow * k;
+    const float* ps = Sa + nc * H * W + (int64_t)(oh * k) * W + ow * k;
+    float sm = 0.f, ss = 0.f;
+    for (int a = 0; a < k; ++a)
+      for (int b = 0; b < k; ++b) {
+        sm += pm[a * W + b];
+        ss += ps[a * W + b];
+      }
+    mo[i] = sm * inv_k2;
+    So[i] = ss * var_scale;
+  });
+}
+
+__global__ void avgpool_bwd_kernel(const float* __restrict__ dm, const float* __restrict__ dS,
+                                   float* __restrict__ om, float* __restrict__ oS, int64_t NC, int H, int W, int k,
+                                   float inv_k2, float var_scale) {
+  const int Ho = H / k, Wo = W / k;
+  const int64_t total = NC * H * W;
+  for_each_vec(total, [&](int64_t i) {
+    const int64_t nc = i / (H * W);
+    const int r = (int)(i - nc * (H * W));
+    const int h = r / W, w = r - (r / W) * W;
+    const int oh = h / k, ow = w / k;
+    if (oh < Ho && ow < Wo) {
+      const int64_t j = nc * Ho * Wo + oh * Wo + ow;
+      om[i] = dm[j] * inv_k2;
+      oS[i] = dS[j] * var_scale;
+    } else {
+      om[i] = 0.f;
+      oS[i] = 0.f;
+    }
+  });
+}
+
+// ------------------------------------------------------------------------ Remax
+// remax.py:33-114. One wavefront per row; each lane keeps EPT classes in registers.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int EPT>
+__global__ void __launch_bounds__(256) remax_kernel(const float* __restrict__ mz, const float* __restrict__ Sz,
+                                                    float* __restrict__ ma, float* __restrict__ Sa,
+                                                    float* __restrict__ Jo, int64_t rows, int K) {
+  const float EPS = 1e-6f;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* pm = mz + row * K;
+  const float* ps = Sz + row * K;
+  float mu_z[EPT], var_z[EPT], mu_m[EPT], var_m[EPT], jcb[EPT];
+  float s_mu = 0.f, s_var = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int c = lane + 64 * e;
+    const bool ok = c < K;
+    const float m = ok ? pm[c] : 0.f;
+    const float v = ok ? ps[c] : 1.f;
+    const float sd = sqrtf(v);
+    const float al = m / sd;
+    const float pdf = INV_SQRT_2PI * expf(-0.5f * al * al);
+    const float cdf = 0.5f * erfcf(-al * INV_SQRT_2);
+    float mm = fmaxf(m * cdf + sd * pdf, EPS);
+    float vm = fmaxf(-mm * mm + 2.0f * mm * m - m * sd * pdf + (v - m * m) * cdf, EPS);
+    mu_z[e] = m;
+    var_z[e] = v;
+    mu_m[e] = mm;
+    var_m[e] = vm;
+    jcb[e] = cdf;
+    if (ok) {
+      s_mu += mm;
+      s_var += vm;
+    }
+  }
+  const float mu_mt = fmaxf(wave_sum(s_mu), EPS);
+  const float var_mt = fmaxf(wave_sum(s_var), EPS);
+  // log1p/expm1 below are the reference's log(1 + x) / exp(x) - 1 without fp32 cancellation
+  const float var_log_mt = log1pf(var_mt / (mu_mt * mu_mt));
+  const float mu_log_mt = logf(mu_mt) - 0.5f * var_log_mt;
+  float var_log_m[EPT], cov_m_mt[EPT], mu_a_raw[EPT], var_log_a[EPT];
+  float s_a = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int c = lane + 64 * e;
+    const float vlm = log1pf(var_m[e] / (mu_m[e] * mu_m[e]));
+    const float mlm = logf(mu_m[e]) - 0.5f * vlm;
+    const float cov = log1pf(var_m[e] / (mu_m[e] * mu_mt));
+    const float mla = mlm - mu_log_mt;
+    const float vla = fmaxf(vlm + var_log_mt - 2.0f * cov, 0.0f);
+    const float mar = fmaxf(expf(mla + 0.5f * vla), EPS);
+    var_log_m[e] = vlm;
+    cov_m_mt[e] = cov;
+    var_log_a[e] = vla;
+    mu_a_raw[e] = mar;
+    if (c < K) s_a += mar;
+  }
+  const float sum_a = fmaxf(wave_sum(s_a), EPS);
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int c = lane + 64 * e;
+    if (c >= K) continue;
+    const float mua = mu_a_raw[e] / sum_a;
+    const float vara = expm1f(var_log_a[e]) * mua * mua;
+    const float cov_la_lm = var_log_m[e] - cov_m_mt[e];
+    const float cov_am = expm1f(cov_la_lm) * mua * mu_m[e];
+    const float cs = sqrtf(vara * var_z[e]);
+    const float cov_az = fminf(cs, cov_am / fmaxf(jcb[e], EPS));
+    ma[row * K + c] = mua;
+    Sa[row * K + c] = vara;
+    Jo[row * K + c] = cov_az / var_z[e];
+    (void)mu_z;
+  }
+}
+
+}  // namespace tagi
+
+using namespace tagi;
+
+static inline hipStream_t as_stream(tagi_stream_t s) { return (hipStream_t)s; }
+
+extern "C" int tagi_relu_fwd(const float* mz, const float* Sz, float* ma, float* Sa, float* J, int64_t n,
+                             tagi_stream_t stream) {
+  TAGI_REQUIRE(n >= 0, "tagi_relu_fwd: n < 0");
+  if (n == 0) return TAGI_OK;
+  TAGI_REQUIRE(mz && Sz && ma && Sa && J, "tagi_relu_fwd: null pointer");
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_RELU, s, 0.0, 20.0 * n);
+  const bool vec = aligned16(mz) && aligned16(Sz) && aligned16(ma) && aligned16(Sa) && aligned16(J);
+  if (vec)
+    hipLaunchKernelGGL(relu_kernel<true>, dim3(ew_blocks(n / 4 + 1, 256)), dim3(256), 0, s, mz, Sz, ma, Sa, J, n);
+  else
+    hipLaunchKernelGGL(relu_kernel<false>, dim3(ew_blocks(n, 256)), dim3(256), 0, s, mz, Sz, ma, Sa, J, n);
+  return check_launch("tagi_relu_fwd");
+}
+
+extern "C" int tagi_jacobian_bwd(const float* dm, const float* dS, const float* J, float* dm_out, float* dS_out,
+                                 int64_t n, tagi_stream_t stream) {
+  TAGI_REQUIRE(n >= 0, "tagi_jacobian_bwd: n < 0");
+  if (n == 0) return TAGI_OK;
+  TAGI_REQUIRE(dm && dS && J && dm_out && dS_out, "tagi_jacobian_bwd: null pointer");
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_JACOBIAN, s, 0.0, 20.0 * n);
+  const bool vec = aligned16(dm) && aligned16(dS) && aligned16(J) && aligned16(dm_out) && aligned16(dS_out);
+  if (vec)
+    hipLaunchKernelGGL(jacobian_kernel<true>, dim3(ew_blocks(n / 4 + 1, 256)), dim3(256), 0, s, dm, dS, J, dm_out,
+                       dS_out, n);
+  else
+    hipLaunchKernelGGL(jacobian_kernel<false>, dim3(ew_blocks(n, 256)), dim3(256), 0, s, dm, dS, J, dm_out, dS_out,
+                       n);
+  return check_launch("tagi_jacobian_bwd");
+}
+
+extern "C" int tagi_innovation(const float* y, const float* mu, const float* var, float sigma_v2, float* dm,
+                               float* dS, int64_t n, tagi_stream_t stream) {
+  TAGI_REQUIRE(n >= 0, "tagi_innovation: n < 0");
+  if (n == 0) return TAGI_OK;
+  TAGI_REQUIRE(y && mu && var && dm && dS, "tagi_innovation: null pointer");
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_INNOVATION, s, 0.0, 20.0 * n);
+  hipLaunchKernelGGL(innovation_kernel<false>, dim3(ew_blocks(n, 256)), dim3(256), 0, s, y, mu, var, sigma_v2, dm,
+                     dS, n);
+  return check_launch("tagi_innovation");
+}
+
+extern "C" int tagi_capped_update(float* m, float* S, const float* dm, const float* dS, float cap_factor, int64_t n,
+                                  tagi_stream_t stream) {
+  TAGI_REQUIRE(n >= 0, "tagi_capped_update: n < 0");
+  if (n == 0) return TAGI_OK;
+  TAGI_REQUIRE(m && S && dm && dS, "tagi_capped_update: null pointer");
+  TAGI_REQUIRE(cap_factor > 0.f, "tagi_capped_update: cap_factor must be positive");
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_UPDATE, s, 0.0, 24.0 * n);
+  const bool vec = aligned16(m) && aligned16(S) && aligned16(dm) && aligned16(dS);
+  if (vec)
+    hipLaunchKernelGGL(update_kernel<true>, dim3(ew_blocks(n / 4 + 1, 256)), dim3(256), 0, s, m, S, dm, dS,
+                       cap_factor, n);
+  else
+    hipLaunchKernelGGL(update_kernel<false>, dim3(ew_blocks(n, 256)), dim3(256), 0, s, m, S, dm, dS, cap_factor, n);
+  return check_launch("tagi_capped_update");
+}
+
+extern "C" int tagi_capped_update_multi(float* const* m, float* const* S, const float* const* dm,
+                                        const float* const* dS, const int64_t* n, int64_t count, float cap_factor,
+                                        tagi_stream_t stream) {
+  TAGI_REQUIRE(count >= 0, "tagi_capped_update_multi: count < 0");
+  TAGI_REQUIRE(count == 0 || (m && S && dm && dS && n), "tagi_capped_update_multi: null table");
+  TAGI_REQUIRE(cap_factor > 0.f, "tagi_capped_update_multi: cap_factor must be positive");
+  hipStream_t s = as_stream(stream);
+  int64_t total = 0;
+  for (int64_t t = 0; t < count; ++t) {
+    TAGI_REQUIRE(n[t] >= 0, "tagi_capped_update_multi: negative size at %lld", (long long)t);
+    TAGI_REQUIRE(n[t] == 0 || (m[t] && S[t] && dm[t] && dS[t]), "tagi_capped_update_multi: null pointer at %lld",
+                 (long long)t);
+    total += n[t];
+  }
+  ProfScope ps(FAM_UPDATE, s, 0.0, 24.0 * total);
+  for (int64_t t0 = 0; t0 < count; t0 += kMultiMax) {
+    MultiUpdateArgs a{};
+    a.cap = cap_factor;
+    int c = 0;
+    int64_t blocks = 0;
+    for (int64_t t = t0; t < count && c < kMultiMax; ++t) {
+      if (n[t] == 0) continue;
+      a.m[c] = m[t];
+      a.S[c] = S[t];
+      a.dm[c] = dm[t];
+      a.dS[c] = dS[t];
+      a.n[c] = n[t];
+      a.block_start[c] = blocks;
+      blocks += cdiv(n[t], kMultiChunk);
+      ++c;
+    }
+    a.block_start[c] = blocks;
+    a.count = c;
+    if (c == 0) continue;
+    hipLaunchKernelGGL(update_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    int rc = check_launch("tagi_capped_update_multi");
+    if (rc) return rc;
+  }
+  return TAGI_OK;
+}
+
+extern "C" int tagi_add_inplace(const float* mu_s, const float* var_s, float* mu_a, float* var_a, int64_t n,
+                                tagi_stream_t stream) {
+  TAGI_REQUIRE(n >= 0, "tagi_add_inplace: n < 0");
+  if (n == 0) return TAGI_OK;
+  TAGI_REQUIRE(mu_s && var_s && mu_a && var_a, "tagi_add_inplace: null pointer");
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_ADD, s, 0.0, 24.0 * n);
+  const bool vec = aligned16(mu_s) && aligned16(var_s) && aligned16(mu_a) && aligned16(var_a);
+  if (vec)
+    hipLaunchKernelGGL(add_kernel<true>, dim3(ew_blocks(n / 4 + 1, 256)), dim3(256), 0, s, mu_s, var_s, mu_a, var_a,
+                       n);
+  else
+    hipLaunchKernelGGL(add_kernel<false>, dim3(ew_blocks(n, 256)), dim3(256), 0, s, mu_s, var_s, mu_a, var_a, n);
+  return check_launch("tagi_add_inplace");
+}
+
+extern "C" int tagi_avgpool2d_fwd(const float* ma, const float* Sa, float* ma_out, float* Sa_out, int64_t N,
+                                  int64_t C, int64_t H, int64_t W, int64_t k, float var_scale, tagi_stream_t stream) {
+  TAGI_REQUIRE(ma && Sa && ma_out && Sa_out, "tagi_avgpool2d_fwd: null pointer");
+  TAGI_REQUIRE(N > 0 && C > 0 && H > 0 && W > 0 && k > 0 && H >= k && W >= k, "tagi_avgpool2d_fwd: bad sizes");
+  hipStream_t s = as_stream(stream);
+  const int64_t out = N * C * (H / k) * (W / k);
+  ProfScope ps(FAM_AVGPOOL, s, 0.0, 8.0 * (N * C * H * W + out));
+  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(ew_blocks(out, 256)), dim3(256), 0, s, ma, Sa, ma_out, Sa_out, N * C,
+                     (int)H, (int)W, (int)k, 1.0f / (float)(k * k), var_scale);
+  return check_launch("tagi_avgpool2d_fwd");
+}
+
+extern "C" int tagi_avgpool2d_bwd(const float* dm, const float* dS, float* dm_out, float* dS_out, int64_t N,
+                                  int64_t C, int64_t H, int64_t W, int64_t k, float var_scale, tagi_stream_t stream) {
+  TAGI_REQUIRE(dm && dS && dm_out && dS_out, "tagi_avgpool2d_bwd: null pointer");
+  TAGI_REQUIRE(N > 0 && C > 0 && H > 0 && W > 0 && k > 0 && H >= k && W >= k, "tagi_avgpool2d_bwd: bad sizes");
+  hipStream_t s = as_stream(stream);
+  const int64_t total = N * C * H * W;
+  ProfScope ps(FAM_AVGPOOL, s, 0.0, 8.0 * (total + N * C * (H / k) * (W / k)));
+  hipLaunchKernelGGL(avgpool_bwd_kernel, dim3(ew_blocks(total, 256)), dim3(256), 0, s, dm, dS, dm_out, dS_out, N * C,
+                     (int)H, (int)W, (int)k, 1.0f / (float)(k * k), var_scale);
+  return check_launch("tagi_avgpool2d_bwd");
+}
+
+extern "C" int tagi_remax_fwd(const float* mz, const float* Sz, float* ma, float* Sa, float* J, int64_t rows,
+                              int64_t K, tagi_stream_t stream) {
+  TAGI_REQUIRE(mz && Sz && ma && Sa && J, "tagi_remax_fwd: null pointer");
+  TAGI_REQUIRE(rows >= 0 && K > 0, "tagi_remax_fwd: bad sizes");
+  if (rows == 0) return TAGI_OK;
+  if (K > 1024) return fail(TAGI_ERR_UNSUPPORTED, "tagi_remax_fwd: rows longer than 1024 classes (K=%lld)", (long long)K);
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_REMAX, s, 0.0, 20.0 * rows * K);
+  const unsigned blocks = (unsigned)cdiv(rows, 4);
+  if (K <= 64)
+    hipLaunchKernelGGL(remax_kernel<1>, dim3(blocks), dim3(256), 0, s, mz, Sz, ma, Sa, J, rows, (int)K);
+  else if (K <= 256)
+    hipLaunchKernelGGL(remax_kernel<4>, dim3(blocks), dim3(256), 0, s, mz, Sz, ma, Sa, J, rows, (int)K);
+  else
+    hipLaunchKernelGGL(remax_kernel<16>, dim3(blocks), dim3(256), 0, s, mz, Sz, ma, Sa, J, rows, (int)K);
+  return check_launch("tagi_remax_fwd");
+}

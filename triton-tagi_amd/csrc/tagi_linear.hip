@@ -1,0 +1,86 @@
+// Linear layer entry points (forward moments, backward deltas, parameter deltas).
+#include "tagi_gemm_core.h"
+
+using namespace tagi;
+
+static inline hipStream_t as_stream(tagi_stream_t s) { return (hipStream_t)s; }
+
+// ====================================================================== Linear
+extern "C" int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N) {
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  return plan_ws_bytes(linear_fwd_plan(M, K, N), M, N, 1);
+}
+
+extern "C" int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw, const float* mb,
+                               const float* Sb, float* mz, float* Sz, int64_t M, int64_t K, int64_t N, float* ws,
+                               int64_t ws_bytes, tagi_stream_t stream) {
+  const char* what = "tagi_linear_fwd";
+  TAGI_REQUIRE(ma && Sa && mw && Sw && Sz, "%s: null pointer", what);
+  TAGI_REQUIRE(M > 0 && K > 0 && N > 0, "%s: sizes must be positive (M=%lld K=%lld N=%lld)", what, (long long)M,
+               (long long)K, (long long)N);
+  TAGI_REQUIRE(fits_i32(M * K) && fits_i32(K * N) && fits_i32(M * N), "%s: too large for 32-bit tiles", what);
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_LINEAR_FWD, s, 2.0 * 3 * M * K * N, 4.0 * (2 * M * K + 2 * K * N + 2 * M * N));
+  GemmArgs g{};
+  g.a = strided_operand(ma, Sa, 1, 0, 0, K, 1, M, K);
+  g.b = strided_operand(mw, Sw, 1, 0, 0, 1, N, N, K);
+  g.epi = epi_store(mz, Sz, mb, Sb, 0, 1, 1.f, 1.f, 1, 0, 0, N, N, 0, 1);
+  g.R = (int)M;
+  g.C = (int)N;
+  g.Kred = (int)K;
+  Plan p = linear_fwd_plan(M, K, N);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, N, 1))) p = choose_plan(M, N, K, 1, 3, false, 1);
+  return run_gemm<PROD_FWD, LD_STRIDED_K, LD_STRIDED_MN>(g, 1, p, ws, ws_bytes, s, what);
+}
+
+extern "C" int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const float* mw, float* dma, float* dSa,
+                                     int64_t M, int64_t K, int64_t N, tagi_stream_t stream) {
+  const char* what = "tagi_linear_bwd_delta";
+  TAGI_REQUIRE(dmz && dSz && mw && dma && dSa, "%s: null pointer", what);
+  TAGI_REQUIRE(M > 0 && K > 0 && N > 0, "%s: sizes must be positive", what);
+  TAGI_REQUIRE(fits_i32(M * K) && fits_i32(K * N) && fits_i32(M * N), "%s: too large for 32-bit tiles", what);
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_LINEAR_BWD_DELTA, s, 2.0 * 2 * M * K * N, 4.0 * (2 * M * N + K * N + 2 * M * K));
+  GemmArgs g{};
+  g.a = strided_operand(dmz, dSz, 1, 0, 0, N, 1, M, N);
+  g.b = strided_operand(mw, nullptr, 1, 0, 0, N, 1, K, N);
+  g.epi = epi_store(dma, dSa, nullptr, nullptr, 0, 0, 1.f, 1.f, 1, 0, 0, K, K, 0, 1);
+  g.R = (int)M;
+  g.C = (int)K;
+  g.Kred = (int)N;
+  Plan p = choose_plan(M, K, N, 1, 2, false, 1);
+  return run_gemm<PROD_SHARED_B, LD_STRIDED_K, LD_STRIDED_K>(g, 1, p, nullptr, 0, s, what);
+}
+
+extern "C" int64_t tagi_linear_wgrad_ws_bytes(int64_t M, int64_t K, int64_t N) {
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  return plan_ws_bytes(linear_wgrad_plan(M, K, N), K + 1, N, 1);
+}
+
+extern "C" int tagi_linear_wgrad(const float* ma, const float* dmz, const float* dSz, const float* Sw, const float* Sb,
+                                 float* dmw, float* dSw, float* dmb, float* dSb, int64_t M, int64_t K, int64_t N,
+                                 float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+  const char* what = "tagi_linear_wgrad";
+  TAGI_REQUIRE(ma && dmz && dSz && dmw && dSw, "%s: null pointer", what);
+  TAGI_REQUIRE((dmb == nullptr) == (dSb == nullptr), "%s: dmb and dSb must both be given or both be NULL", what);
+  TAGI_REQUIRE(M > 0 && K > 0 && N > 0, "%s: sizes must be positive", what);
+  TAGI_REQUIRE(fits_i32(M * K) && fits_i32((K + 1) * N) && fits_i32(M * N), "%s: too large for 32-bit tiles", what);
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_LINEAR_WGRAD, s, 2.0 * 2 * M * K * N, 4.0 * (M * K + 2 * M * N + 3 * K * N));
+  const bool bias = dmb != nullptr;
+  GemmArgs g{};
+  g.a = strided_operand(ma, nullptr, 1, 0, 0, 1, K, K, M);
+  if (bias) g.a.ones_row = (int)K;
+  g.b = strided_operand(dmz, dSz, 1, 0, 0, 1, N, N, M);
+  g.epi = epi_wgrad(dmw, dSw, dmb, dSb, Sw, Sb, K, N);
+  g.R = (int)(K + (bias ? 1 : 0));
+  g.C = (int)N;
+  g.Kred = (int)M;
+  Plan p = linear_wgrad_plan(M, K, N);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, K + 1, N, 1)))
+    p = choose_plan(K + 1, N, M, 1, 2, false, 1);
+  // the plan was made for K+1 rows; tiles_m must follow the actual row count
+  p.tiles_m = (int)cdiv(g.R, kCfg[p.cfg].BM);
+  return run_gemm<PROD_SHARED_A, LD_STRIDED_MN, LD_STRIDED_MN>(g, 1, p, ws, ws_bytes, s, what);
+}
+

@@ -1,0 +1,122 @@
+// Error state and the live per-family event timer of libtagi_hip.
+#include <stdarg.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "tagi_common.h"
+
+namespace tagi {
+
+static thread_local char g_err[512] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TAGI_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return TAGI_OK;
+}
+
+// ---------------------------------------------------------------------------------
+// Timer: a fixed pool of event pairs, created when the timer is switched on.
+// ---------------------------------------------------------------------------------
+namespace {
+constexpr int kMaxSlots = 16384;
+struct Prof {
+  std::mutex mu;
+  bool on = false;
+  uint64_t mask = 0;
+  std::vector<hipEvent_t> ev;  // 2 per slot
+  std::vector<int> fam;
+  std::vector<double> flops, bytes;
+  int used = 0;
+};
+Prof& prof() {
+  static Prof p;
+  return p;
+}
+}  // namespace
+
+int prof_start(int f, hipStream_t s) {
+  Prof& p = prof();
+  if (!p.on || !((p.mask >> f) & 1ull)) return -1;
+  std::lock_guard<std::mutex> lk(p.mu);
+  if (p.used >= kMaxSlots) return -1;
+  int slot = p.used++;
+  p.fam[slot] = f;
+  hipEventRecord(p.ev[2 * slot], s);
+  return slot;
+}
+
+void prof_end(int slot, hipStream_t s, double flops, double bytes) {
+  if (slot < 0) return;
+  Prof& p = prof();
+  hipEventRecord(p.ev[2 * slot + 1], s);
+  p.flops[slot] = flops;
+  p.bytes[slot] = bytes;
+}
+
+}  // namespace tagi
+
+using namespace tagi;
+
+extern "C" int tagi_abi_version(void) { return TAGI_ABI_VERSION; }
+
+extern "C" const char* tagi_last_error(void) { return g_err; }
+
+extern "C" int tagi_prof_begin(uint64_t family_mask) {
+  Prof& p = prof();
+  std::lock_guard<std::mutex> lk(p.mu);
+  if (p.ev.empty()) {
+    p.ev.resize(2 * kMaxSlots);
+    for (auto& e : p.ev) {
+      if (hipEventCreate(&e) != hipSuccess) return fail(TAGI_ERR_LAUNCH, "tagi_prof_begin: hipEventCreate failed");
+    }
+    p.fam.resize(kMaxSlots);
+    p.flops.resize(kMaxSlots);
+    p.bytes.resize(kMaxSlots);
+  }
+  p.used = 0;
+  p.mask = family_mask;
+  p.on = true;
+  return TAGI_OK;
+}
+
+extern "C" int tagi_prof_end(double* ms, int64_t* launches, double* flops, double* bytes) {
+  Prof& p = prof();
+  std::lock_guard<std::mutex> lk(p.mu);
+  p.on = false;
+  for (int f = 0; f < FAM_COUNT; ++f) {
+    if (ms) ms[f] = 0;
+    if (launches) launches[f] = 0;
+    if (flops) flops[f] = 0;
+    if (bytes) bytes[f] = 0;
+  }
+  for (int i = 0; i < p.used; ++i) {
+    if (hipEventSynchronize(p.ev[2 * i + 1]) != hipSuccess) return fail(TAGI_ERR_LAUNCH, "tagi_prof_end: event sync failed");
+    float t = 0.f;
+    if (hipEventElapsedTime(&t, p.ev[2 * i], p.ev[2 * i + 1]) != hipSuccess) return fail(TAGI_ERR_LAUNCH, "tagi_prof_end: elapsed time failed");
+    int f = p.fam[i];
+    if (ms) ms[f] += t;
+    if (launches) launches[f] += 1;
+    if (flops) flops[f] += p.flops[i];
+    if (bytes) bytes[f] += p.bytes[i];
+  }
+  p.used = 0;
+  return TAGI_OK;
+}

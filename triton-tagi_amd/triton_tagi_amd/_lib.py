@@ -1,0 +1,195 @@
+"""ctypes binding of libtagi_hip.so (the C ABI declared in include/tagi_hip.h).
+
+The library is loaded lazily on first use, after torch has loaded its HIP runtime, so
+both share one runtime (the library's DT_NEEDED soname resolves to the copy torch
+already mapped). There is no fallback: if the library or a GPU is missing, every
+kernel call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_uint64, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(os.environ.get("TAGI_HIP_LIB", Path(__file__).resolve().parent / "libtagi_hip.so"))
+
+TAGI_OK = 0
+FAMILIES = [
+    "conv_fwd", "conv_bwd_delta", "conv_wgrad", "linear_fwd", "linear_bwd_delta",
+    "linear_wgrad", "bmm_fwd", "bmm_shared", "relu", "remax", "bn_stats", "bn_fwd",
+    "bn_bwd", "update", "innovation", "add", "avgpool", "jacobian", "rmsnorm",
+    "embedding", "pe", "splitk_reduce",
+]
+FAM_COUNT = len(FAMILIES)
+
+
+class TagiView(ctypes.Structure):
+    """tagi_view: element (z, i, j) at (z/zdiv)*sz1 + (z%zdiv)*sz2 + i*si + j*sj."""
+
+    _fields_ = [("zdiv", c_int64), ("sz1", c_int64), ("sz2", c_int64), ("si", c_int64), ("sj", c_int64)]
+
+
+class ConvGeom(ctypes.Structure):
+    """tagi_conv_geom."""
+
+    _fields_ = [
+        (n, c_int64)
+        for n in ("N", "C", "H", "W", "Cout", "k", "stride", "pad_top", "pad_left", "Ho", "Wo")
+    ]
+
+
+P = c_void_p
+I64 = c_int64
+F = c_float
+VP = POINTER(TagiView)
+GP = POINTER(ConvGeom)
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "tagi_abi_version": (c_int, []),
+    "tagi_last_error": (c_char_p, []),
+    "tagi_prof_begin": (c_int, [c_uint64]),
+    "tagi_prof_end": (c_int, [P, P, P, P]),
+    "tagi_linear_fwd": (c_int, [P, P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
+    "tagi_linear_fwd_ws_bytes": (I64, [I64, I64, I64]),
+    "tagi_linear_bwd_delta": (c_int, [P, P, P, P, P, I64, I64, I64, P]),
+    "tagi_linear_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
+    "tagi_linear_wgrad_ws_bytes": (I64, [I64, I64, I64]),
+    "tagi_bmm_tagi": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, P]),
+    "tagi_bmm_shared": (c_int, [P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),
+    "tagi_conv2d_fwd": (c_int, [P, P, P, P, P, P, P, P, GP, P, I64, P]),
+    "tagi_conv2d_fwd_ws_bytes": (I64, [GP]),
+    "tagi_conv2d_bwd_delta": (c_int, [P, P, P, P, P, GP, P]),
+    "tagi_conv2d_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, GP, P, I64, P]),
+    "tagi_conv2d_wgrad_ws_bytes": (I64, [GP]),
+    "tagi_relu_fwd": (c_int, [P, P, P, P, P, I64, P]),
+    "tagi_jacobian_bwd": (c_int, [P, P, P, P, P, I64, P]),
+    "tagi_remax_fwd": (c_int, [P, P, P, P, P, I64, I64, P]),
+    "tagi_innovation": (c_int, [P, P, P, F, P, P, I64, P]),
+    "tagi_capped_update": (c_int, [P, P, P, P, F, I64, P]),
+    "tagi_capped_update_multi": (c_int, [P, P, P, P, P, I64, F, P]),
+    "tagi_add_inplace": (c_int, [P, P, P, P, I64, P]),
+    "tagi_avgpool2d_fwd": (c_int, [P, P, P, P, I64, I64, I64, I64, I64, F, P]),
+    "tagi_avgpool2d_bwd": (c_int, [P, P, P, P, I64, I64, I64, I64, I64, F, P]),
+    "tagi_bn_stats": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, F, F, c_int, c_int, P, I64, P]),
+    "tagi_bn_stats_ws_bytes": (I64, [I64, I64, I64]),
+    "tagi_bn_fwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P]),
+    "tagi_bn_bwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P, I64, P]),
+    "tagi_bn_bwd_ws_bytes": (I64, [I64, I64, I64]),
+    "tagi_rmsnorm_fwd": (c_int, [P, P, P, P, P, P, P, I64, I64, F, P]),
+    "tagi_rmsnorm_bwd": (c_int, [P, P, P, P, P, P, P, P, P, P, I64, I64, P, I64, P]),
+    "tagi_rmsnorm_bwd_ws_bytes": (I64, [I64, I64]),
+    "tagi_embedding_fwd": (c_int, [P, P, P, P, P, I64, I64, I64, I64, P]),
+    "tagi_embedding_bwd": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, P, I64, P]),
+    "tagi_embedding_bwd_ws_bytes": (I64, [I64, I64, I64]),
+    "tagi_pe_add": (c_int, [P, P, P, I64, I64, I64, P]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+_lib: ctypes.CDLL | None = None
+
+
+def load(path: Path | str | None = None) -> ctypes.CDLL:
+    """Load the library (once) and declare every entry point's signature."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(
+            f"libtagi_hip.so not found at {p}; build it with `python triton-tagi_amd/build.py`"
+        )
+    lib = ctypes.CDLL(str(p), mode=ctypes.RTLD_GLOBAL)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = load().tagi_last_error()
+    return msg.decode() if msg else ""
+
+
+def call(name: str, *args) -> None:
+    """Invoke a status-returning entry point; raise RuntimeError on failure."""
+    rc = getattr(load(), name)(*args)
+    if rc != TAGI_OK:
+        raise RuntimeError(f"{name} failed (status {rc}): {last_error()}")
+
+
+def query(name: str, *args) -> int:
+    return int(getattr(load(), name)(*args))
+
+
+# ---------------------------------------------------------------------------------
+# Tensor plumbing
+# ---------------------------------------------------------------------------------
+def stream_of(t: torch.Tensor) -> int:
+    """Handle of torch's current stream on t's device (the stream kernels are queued on)."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def check(t: torch.Tensor, name: str, contiguous: bool = True) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name}: expected float32, got {t.dtype}")
+    if t.device.type != "cuda":
+        raise ValueError(
+            f"{name}: tensor is on {t.device}; the TAGI HIP kernels run on the GPU only"
+        )
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous")
+    return t
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+    """Scratch buffer from torch's caching allocator (the library never allocates)."""
+    if nbytes <= 0:
+        return None
+    return torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
+
+
+def ws_args(ws: torch.Tensor | None) -> tuple[int | None, int]:
+    return (None, 0) if ws is None else (ws.data_ptr(), ws.numel() * 4)
+
+
+def view(zdiv: int, sz1: int, sz2: int, si: int, sj: int) -> TagiView:
+    return TagiView(int(max(zdiv, 1)), int(sz1), int(sz2), int(si), int(sj))
+
+
+# ---------------------------------------------------------------------------------
+# Live kernel-family timer
+# ---------------------------------------------------------------------------------
+def prof_begin(families: list[str] | None = None) -> None:
+    mask = 0
+    for i, f in enumerate(FAMILIES):
+        if families is None or f in families:
+            mask |= 1 << i
+    call("tagi_prof_begin", mask)
+
+
+def prof_end() -> dict[str, dict[str, float]]:
+    ms = (ctypes.c_double * FAM_COUNT)()
+    n = (ctypes.c_int64 * FAM_COUNT)()
+    fl = (ctypes.c_double * FAM_COUNT)()
+    by = (ctypes.c_double * FAM_COUNT)()
+    call("tagi_prof_end", ctypes.addressof(ms), ctypes.addressof(n), ctypes.addressof(fl), ctypes.addressof(by))
+    out = {}
+    for i, f in enumerate(FAMILIES):
+        if n[i]:
+            out[f] = {"ms": ms[i], "launches": int(n[i]), "flops": fl[i], "bytes": by[i]}
+    return out

@@ -1,0 +1,45 @@
+"""Layer contracts of the TAGI step (mirrors triton_tagi/base.py:21-67).
+
+``Layer``: forward(ma, Sa) -> (ma, Sa) and backward(delta_ma, delta_Sa) -> deltas.
+``LearnableLayer``: adds update(cap_factor) applying deltas stored by backward, and
+the num_parameters property. ``Sequential`` dispatches on these two classes.
+"""
+
+from __future__ import annotations
+
+from abc import ABC, abstractmethod
+
+from torch import Tensor
+
+
+class Layer(ABC):
+    """Base class for all TAGI layers."""
+
+    @abstractmethod
+    def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
+        """Propagate Gaussian moments (means, variances) forward."""
+
+    @abstractmethod
+    def backward(self, delta_ma: Tensor, delta_Sa: Tensor) -> tuple[Tensor, Tensor]:
+        """Propagate innovation deltas backward; return the deltas for the previous layer."""
+
+
+class LearnableLayer(Layer):
+    """Base class for layers with parameters updated by the capped TAGI rule."""
+
+    @abstractmethod
+    def update(self, cap_factor: float) -> None:
+        """Apply the parameter deltas stored by ``backward``."""
+
+    @property
+    @abstractmethod
+    def num_parameters(self) -> int:
+        """Total number of learnable scalars (means + variances)."""
+
+    def _update_items(self):
+        """(m, S, delta_m, delta_S) quadruples ``update`` would apply, in order.
+
+        ``Sequential.step`` uses these to apply every layer's update in one launch; a
+        layer that returns None is updated through its own ``update`` instead.
+        """
+        return None

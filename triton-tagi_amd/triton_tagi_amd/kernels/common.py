@@ -1,0 +1,100 @@
+"""Linear moment GEMMs (mirrors triton_tagi/kernels/common.py).
+
+    forward:  mz = ma @ mw + mb,  Sz = ma^2 @ Sw + Sa @ (mw^2 + Sw) + Sb
+    backward: dma = dmz @ mw^T,   dSa = dSz @ (mw^2)^T
+    deltas:   gmw = ma^T @ dmz,   gSw = (ma^2)^T @ dSz
+
+Each is one fp32-MFMA kernel launch (two accumulators) behind the C ABI; the
+``triton_*`` names of the reference are kept as aliases.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+
+def _2d(t, name):
+    _lib.check(t, name)
+    if t.dim() != 2:
+        raise ValueError(f"{name}: expected a 2-D tensor, got shape {tuple(t.shape)}")
+    return t
+
+
+def linear_forward(ma, Sa, mw, Sw, mb=None, Sb=None, need_mean=True):
+    """Fused mean and variance of z = a W + b (linear.py:99-100)."""
+    _2d(ma, "ma"), _2d(Sa, "Sa"), _2d(mw, "mw"), _2d(Sw, "Sw")
+    M, K = ma.shape
+    K2, N = mw.shape
+    if K2 != K or Sa.shape != ma.shape or Sw.shape != mw.shape:
+        raise ValueError(f"linear_forward: shapes ma {tuple(ma.shape)} mw {tuple(mw.shape)} disagree")
+    for t, n in ((mb, "mb"), (Sb, "Sb")):
+        if t is not None:
+            _lib.check(t, n)
+            if t.numel() != N:
+                raise ValueError(f"{n}: expected {N} elements, got {t.numel()}")
+    mz = torch.empty(M, N, device=ma.device, dtype=torch.float32) if need_mean else None
+    Sz = torch.empty(M, N, device=ma.device, dtype=torch.float32)
+    ws = _lib.workspace(_lib.query("tagi_linear_fwd_ws_bytes", M, K, N), ma.device)
+    wp, wb = _lib.ws_args(ws)
+    _lib.call("tagi_linear_fwd", ma.data_ptr(), Sa.data_ptr(), mw.data_ptr(), Sw.data_ptr(), _lib.ptr(mb),
+              _lib.ptr(Sb), _lib.ptr(mz), Sz.data_ptr(), M, K, N, wp, wb, _lib.stream_of(ma))
+    return mz, Sz
+
+
+def fused_var_forward(ma, Sa, mw, Sw, Sb):
+    """Sz = ma^2 @ Sw + Sa @ (mw^2 + Sw) + Sb (common.py:170-210)."""
+    return linear_forward(ma, Sa, mw, Sw, None, Sb, need_mean=False)[1]
+
+
+def fused_backward_delta(dmz, dSz, mw):
+    """(dmz @ mw^T, dSz @ (mw^2)^T) (common.py:287-327)."""
+    _2d(dmz, "dmz"), _2d(dSz, "dSz"), _2d(mw, "mw")
+    M, N = dmz.shape
+    K = mw.shape[0]
+    if mw.shape[1] != N or dSz.shape != dmz.shape:
+        raise ValueError(f"fused_backward_delta: dmz {tuple(dmz.shape)} vs mw {tuple(mw.shape)}")
+    dma = torch.empty(M, K, device=dmz.device, dtype=torch.float32)
+    dSa = torch.empty(M, K, device=dmz.device, dtype=torch.float32)
+    _lib.call("tagi_linear_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), mw.data_ptr(), dma.data_ptr(),
+              dSa.data_ptr(), M, K, N, _lib.stream_of(dmz))
+    return dma, dSa
+
+
+def _wgrad(a, dmz, dSz, Sw, Sb, bias):
+    _2d(a, "a"), _2d(dmz, "dmz"), _2d(dSz, "dSz")
+    M, K = a.shape
+    M2, N = dmz.shape
+    if M2 != M or dSz.shape != dmz.shape:
+        raise ValueError(f"weight deltas: a {tuple(a.shape)} vs dmz {tuple(dmz.shape)}")
+    dev = a.device
+    dmw = torch.empty(K, N, device=dev, dtype=torch.float32)
+    dSw = torch.empty(K, N, device=dev, dtype=torch.float32)
+    dmb = torch.empty(1, N, device=dev, dtype=torch.float32) if bias else None
+    dSb = torch.empty(1, N, device=dev, dtype=torch.float32) if bias else None
+    ws = _lib.workspace(_lib.query("tagi_linear_wgrad_ws_bytes", M, K, N), dev)
+    wp, wb = _lib.ws_args(ws)
+    _lib.call("tagi_linear_wgrad", a.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), _lib.ptr(Sw), _lib.ptr(Sb),
+              dmw.data_ptr(), dSw.data_ptr(), _lib.ptr(dmb), _lib.ptr(dSb), M, K, N, wp, wb, _lib.stream_of(a))
+    return dmw, dSw, dmb, dSb
+
+
+def fused_weight_grad(a, dmz, dSz):
+    """Raw (a^T @ dmz, (a^2)^T @ dSz) (common.py:410-451)."""
+    dmw, dSw, _, _ = _wgrad(a, dmz, dSz, None, None, False)
+    return dmw, dSw
+
+
+def linear_param_deltas(ma_in, dmz, dSz, Sw, Sb=None):
+    """Parameter deltas of a Linear layer (linear.py:138-151):
+    (Sw*gmw, Sw^2*gSw, Sb*gmb, Sb^2*gSb); the bias pair is None when Sb is None."""
+    _lib.check(Sw, "Sw")
+    if Sb is not None:
+        _lib.check(Sb, "Sb")
+    return _wgrad(ma_in, dmz, dSz, Sw, Sb, Sb is not None)
+
+
+triton_fused_var_forward = fused_var_forward
+triton_fused_backward_delta = fused_backward_delta
+triton_fused_weight_grad = fused_weight_grad

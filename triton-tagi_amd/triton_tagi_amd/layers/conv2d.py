@@ -1,0 +1,112 @@
+"""Bayesian Conv2D layer as implicit GEMM (mirrors triton_tagi/layers/conv2d.py:189-390).
+
+The reference unfolds patches (im2col), runs the Linear kernels on them and folds the
+input deltas back (col2im). Here the three GEMMs gather patches straight from the NCHW
+tensors inside the kernels:
+    forward      mu_z = P(mu_a) @ mw + mb ;  S_z = P(mu_a)^2 @ Sw + P(S_a) @ (mw^2 + Sw) + Sb
+    input delta  fold(delta_z @ mw^T) as a transposed implicit GEMM (no col2im)
+    deltas       delta_mw = Sw * P^T @ delta_mz, delta_Sw = Sw^2 * (P^2)^T @ delta_Sz (+ bias)
+padding_type 1 pads p on every side; padding_type 2 pads p on the right/bottom only
+(conv2d.py:280-291).
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+from ..base import LearnableLayer
+from ..param_init import init_weight_bias_conv2d
+from ..update.parameters import update_parameters
+
+
+class Conv2D(LearnableLayer):
+    """2-D convolution with Gaussian weights; mw, Sw are (C_in*k*k, C_out), rows (c, kh, kw)."""
+
+    def __init__(self, C_in: int, C_out: int, kernel_size: int, stride: int = 1, padding: int = 0,
+                 padding_type: int = 1, device: str = "cuda", init_method: str = "He", gain_w: float = 1.0,
+                 gain_b: float = 1.0) -> None:
+        self.C_in = C_in
+        self.C_out = C_out
+        self.kH = self.kW = kernel_size
+        self.stride = stride
+        self.padding = padding
+        self.padding_type = padding_type
+        self.device = torch.device(device)
+        self.mw, self.Sw, self.mb, self.Sb = init_weight_bias_conv2d(
+            kernel_size, C_in, C_out, init_method=init_method, gain_w=gain_w, gain_b=gain_b, device=self.device
+        )
+        self.has_bias = True
+        self.ma_in = None
+        self.input_shape = None
+        self.spatial = None
+        self.delta_mw = self.delta_Sw = self.delta_mb = self.delta_Sb = None
+
+    def _geom(self, N, C, H, W) -> _lib.ConvGeom:
+        k, s, p = self.kH, self.stride, self.padding
+        if self.padding_type == 2 and p > 0:
+            Ho, Wo, pt = (H + p - k) // s + 1, (W + p - k) // s + 1, 0
+        else:
+            Ho, Wo, pt = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1, p
+        if Ho <= 0 or Wo <= 0:
+            raise ValueError(f"Conv2D: input {H}x{W} too small for kernel {k} stride {s} padding {p}")
+        return _lib.ConvGeom(N, C, H, W, self.C_out, k, s, pt, pt, Ho, Wo)
+
+    def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
+        if ma.dim() != 4 or ma.shape[1] != self.C_in:
+            raise ValueError(f"Conv2D: expected (N, {self.C_in}, H, W), got {tuple(ma.shape)}")
+        ma = _lib.check(ma.contiguous(), "ma")
+        Sa = _lib.check(Sa.contiguous(), "Sa")
+        N, C, H, W = ma.shape
+        self.input_shape = (N, C, H, W)
+        g = self._geom(N, C, H, W)
+        self.spatial = (g.Ho, g.Wo)
+        self.ma_in = ma
+        mz = torch.empty(N, self.C_out, g.Ho, g.Wo, device=ma.device, dtype=torch.float32)
+        Sz = torch.empty_like(mz)
+        ws = _lib.workspace(_lib.query("tagi_conv2d_fwd_ws_bytes", g), ma.device)
+        wp, wb = _lib.ws_args(ws)
+        _lib.call("tagi_conv2d_fwd", ma.data_ptr(), Sa.data_ptr(), self.mw.data_ptr(), self.Sw.data_ptr(),
+                  self.mb.data_ptr(), self.Sb.data_ptr(), mz.data_ptr(), Sz.data_ptr(), g, wp, wb,
+                  _lib.stream_of(ma))
+        return mz, Sz
+
+    def backward(self, delta_mz: Tensor, delta_Sz: Tensor) -> tuple[Tensor, Tensor]:
+        dmz = _lib.check(delta_mz.contiguous(), "delta_mz")
+        dSz = _lib.check(delta_Sz.contiguous(), "delta_Sz")
+        N, C, H, W = self.input_shape
+        g = self._geom(N, C, H, W)
+        if tuple(dmz.shape) != (N, self.C_out, g.Ho, g.Wo):
+            raise ValueError(f"Conv2D.backward: delta shape {tuple(dmz.shape)} != output shape")
+        dev = dmz.device
+        K = self.C_in * self.kH * self.kW
+        self.delta_mw = torch.empty(K, self.C_out, device=dev, dtype=torch.float32)
+        self.delta_Sw = torch.empty_like(self.delta_mw)
+        self.delta_mb = torch.empty(1, self.C_out, device=dev, dtype=torch.float32)
+        self.delta_Sb = torch.empty_like(self.delta_mb)
+        ws = _lib.workspace(_lib.query("tagi_conv2d_wgrad_ws_bytes", g), dev)
+        wp, wb = _lib.ws_args(ws)
+        st = _lib.stream_of(dmz)
+        _lib.call("tagi_conv2d_wgrad", self.ma_in.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), self.Sw.data_ptr(),
+                  self.Sb.data_ptr(), self.delta_mw.data_ptr(), self.delta_Sw.data_ptr(), self.delta_mb.data_ptr(),
+                  self.delta_Sb.data_ptr(), g, wp, wb, st)
+        d_ma = torch.empty(N, C, H, W, device=dev, dtype=torch.float32)
+        d_Sa = torch.empty_like(d_ma)
+        _lib.call("tagi_conv2d_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), self.mw.data_ptr(), d_ma.data_ptr(),
+                  d_Sa.data_ptr(), g, st)
+        return d_ma, d_Sa
+
+    def _update_items(self):
+        return [(self.mw, self.Sw, self.delta_mw, self.delta_Sw), (self.mb, self.Sb, self.delta_mb, self.delta_Sb)]
+
+    def update(self, cap_factor: float) -> None:
+        for m, S, dm, dS in self._update_items():
+            update_parameters(m, S, dm, dS, cap_factor)
+
+    @property
+    def num_parameters(self) -> int:
+        return 2 * (self.mw.numel() + self.mb.numel())
+
+    def __repr__(self):
+        return f"Conv2D({self.C_in}, {self.C_out}, kernel={self.kH}, stride={self.stride}, pad={self.padding})"

@@ -1,0 +1,75 @@
+"""Bayesian Linear layer (mirrors triton_tagi/layers/linear.py:30-181).
+
+Forward (one fused fp32-MFMA launch):
+    mu_z = mu_a @ mu_w + mu_b
+    S_z  = mu_a^2 @ S_w + S_a @ (mu_w^2 + S_w) + S_b
+Backward (deltas stored, applied by ``update``):
+    delta_mw = S_w * (mu_a^T @ delta_mz)        delta_mb = S_b * sum delta_mz
+    delta_Sw = S_w^2 * ((mu_a^2)^T @ delta_Sz)  delta_Sb = S_b^2 * sum delta_Sz
+    delta_ma = delta_mz @ mu_w^T,  delta_Sa = delta_Sz @ (mu_w^2)^T
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from ..base import LearnableLayer
+from ..kernels.common import fused_backward_delta, linear_forward, linear_param_deltas
+from ..param_init import init_weight_bias_linear
+from ..update.parameters import update_parameters
+
+
+class Linear(LearnableLayer):
+    """Fully connected layer with Gaussian weights; mw, Sw are (in, out), mb, Sb (1, out)."""
+
+    def __init__(self, in_features: int, out_features: int, device: str = "cuda", init_method: str = "He",
+                 gain_w: float = 1.0, gain_b: float = 1.0, bias: bool = True) -> None:
+        self.in_features = in_features
+        self.out_features = out_features
+        self.device = torch.device(device)
+        self.has_bias = bias
+        self.mw, self.Sw, self.mb, self.Sb = init_weight_bias_linear(
+            in_features, out_features, init_method=init_method, gain_w=gain_w, gain_b=gain_b, bias=bias,
+            device=self.device,
+        )
+        self.ma_in = None
+        self.delta_mw = self.delta_Sw = self.delta_mb = self.delta_Sb = None
+
+    def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
+        self._input_shape = ma.shape
+        ma_flat = ma.reshape(-1, self.in_features).contiguous()
+        Sa_flat = Sa.reshape(-1, self.in_features).contiguous()
+        self.ma_in = ma_flat
+        mz, Sz = linear_forward(ma_flat, Sa_flat, self.mw, self.Sw, self.mb, self.Sb)
+        out_shape = (*self._input_shape[:-1], self.out_features)
+        return mz.reshape(out_shape), Sz.reshape(out_shape)
+
+    def backward(self, delta_mz: Tensor, delta_Sz: Tensor) -> tuple[Tensor, Tensor]:
+        dmz = delta_mz.reshape(-1, self.out_features).contiguous()
+        dSz = delta_Sz.reshape(-1, self.out_features).contiguous()
+        dmw, dSw, dmb, dSb = linear_param_deltas(self.ma_in, dmz, dSz, self.Sw, self.Sb if self.has_bias else None)
+        self.delta_mw, self.delta_Sw = dmw, dSw
+        if self.has_bias:
+            self.delta_mb, self.delta_Sb = dmb, dSb
+        dma, dSa = fused_backward_delta(dmz, dSz, self.mw)
+        in_shape = (*self._input_shape[:-1], self.in_features)
+        return dma.reshape(in_shape), dSa.reshape(in_shape)
+
+    def _update_items(self):
+        items = [(self.mw, self.Sw, self.delta_mw, self.delta_Sw)]
+        if self.has_bias:
+            items.append((self.mb, self.Sb, self.delta_mb, self.delta_Sb))
+        return items
+
+    def update(self, cap_factor: float) -> None:
+        for m, S, dm, dS in self._update_items():
+            update_parameters(m, S, dm, dS, cap_factor)
+
+    @property
+    def num_parameters(self) -> int:
+        n = self.mw.numel() + (self.mb.numel() if self.has_bias else 0)
+        return 2 * n
+
+    def __repr__(self):
+        return f"Linear(in={self.in_features}, out={self.out_features}, bias={self.has_bias})"

@@ -1,0 +1,126 @@
+"""Sequential container and the TAGI step (mirrors triton_tagi/network.py:40-267).
+
+``step(x, y, sigma_v)``: forward moments -> output innovation -> reversed backward
+(deltas stored on the layers) -> capped update of every learnable layer with the cap
+factor of the batch size. The updates of all layers that expose their parameter groups
+go out as one multi-tensor launch; the arithmetic is the per-layer rule.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from .base import Layer, LearnableLayer
+from .layers.multihead_attention import MultiheadAttentionV2
+from .layers.resblock import ResBlock
+from .update.observation import compute_innovation
+from .update.parameters import get_cap_factor, update_parameters_multi
+
+
+class Sequential:
+    def __init__(self, layers: list, device: str = "cuda") -> None:
+        self.device = torch.device(device)
+        self.layers = layers
+        for layer in self.layers:
+            if isinstance(layer, ResBlock):
+                layer.device = self.device
+                for sub in layer._learnable:
+                    self._move_layer_to_device(sub)
+            elif isinstance(layer, LearnableLayer):
+                self._move_layer_to_device(layer)
+            if hasattr(layer, "running_mean"):
+                layer.running_mean = layer.running_mean.to(self.device)
+                layer.running_var = layer.running_var.to(self.device)
+            if getattr(layer, "pe_cache", None) is not None:
+                layer.pe_cache = layer.pe_cache.to(self.device)
+                layer.device = self.device
+
+    def _move_layer_to_device(self, layer):
+        if isinstance(layer, MultiheadAttentionV2):
+            layer.device = self.device
+            for sub in (layer.q_proj, layer.k_proj, layer.v_proj):
+                self._move_layer_to_device(sub)
+            return
+        if not hasattr(layer, "mw") or layer.mw is None:
+            return
+        layer.device = self.device
+        layer.mw = layer.mw.to(self.device)
+        if getattr(layer, "Sw", None) is not None:
+            layer.Sw = layer.Sw.to(self.device)
+        if getattr(layer, "mb", None) is not None:
+            layer.mb = layer.mb.to(self.device)
+            if getattr(layer, "Sb", None) is not None:
+                layer.Sb = layer.Sb.to(self.device)
+        if getattr(layer, "running_mean", None) is not None:
+            layer.running_mean = layer.running_mean.to(self.device)
+            layer.running_var = layer.running_var.to(self.device)
+
+    def forward(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        ma = x
+        Sa = torch.zeros_like(x)
+        for layer in self.layers:
+            if isinstance(layer, Layer):
+                ma, Sa = layer.forward(ma, Sa)
+            else:
+                raise TypeError(f"Unknown layer type: {type(layer)}")
+        return ma, Sa
+
+    def backward(self, delta_mu: Tensor, delta_var: Tensor) -> tuple[Tensor, Tensor]:
+        for layer in reversed(self.layers):
+            delta_mu, delta_var = layer.backward(delta_mu, delta_var)
+        return delta_mu, delta_var
+
+    def update(self, cap_factor: float) -> None:
+        """Capped update of every learnable layer (one launch for all exposed groups)."""
+        items = []
+        for layer in self.layers:
+            if not isinstance(layer, LearnableLayer):
+                continue
+            got = layer._update_items()
+            if got is None:
+                if items:
+                    update_parameters_multi(items, cap_factor)
+                    items = []
+                layer.update(cap_factor)
+            else:
+                items.extend(got)
+        if items:
+            update_parameters_multi(items, cap_factor)
+
+    def step(self, x_batch: Tensor, y_batch: Tensor, sigma_v: float) -> tuple[Tensor, Tensor]:
+        batch_size = x_batch.shape[0]
+        y_pred_mu, y_pred_var = self.forward(x_batch)
+        delta_mu, delta_var = compute_innovation(y_batch, y_pred_mu, y_pred_var, sigma_v)
+        self.backward(delta_mu, delta_var)
+        self.update(get_cap_factor(batch_size))
+        return y_pred_mu, y_pred_var
+
+    def train(self) -> None:
+        for layer in self.layers:
+            if hasattr(layer, "training"):
+                layer.train()
+
+    def eval(self) -> None:
+        for layer in self.layers:
+            if hasattr(layer, "training"):
+                layer.eval()
+
+    def __repr__(self):
+        lines = ["Sequential("]
+        for i, layer in enumerate(self.layers):
+            lines.append(f"  ({i}): {layer}")
+        lines.append(")")
+        return "\n".join(lines)
+
+    def num_parameters(self) -> int:
+        return sum(layer.num_parameters for layer in self.layers if isinstance(layer, LearnableLayer))
+
+    def get_attention_scores(self) -> dict[int, tuple[Tensor, Tensor]]:
+        out: dict[int, tuple[Tensor, Tensor]] = {}
+        for i, layer in enumerate(self.layers):
+            if isinstance(layer, MultiheadAttentionV2):
+                out[i] = layer.get_attention_scores()
+        if not out:
+            raise RuntimeError("No attention layers in this Sequential.")
+        return out
