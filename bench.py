@@ -1,0 +1,202 @@
+#!/usr/bin/env python3
+"""TAGI step throughput on one MI355X: forward moments + innovation + backward deltas +
+capped update, ResNet-18 at batch 128 on 3x32x32 synthetic inputs (fp32).
+
+    python bench.py [--steps K] [--warmup W] [--workload resnet18|cnn|mlp|transformer]
+
+Prints one JSON line. ``value`` is samples/s over the K timed steps (inputs already in
+HBM). ``roofline`` is computed live: the engine's HIP-event timer brackets every kernel
+launch on its stream during the timed steps, and the dominant MFMA kernel family's
+algorithmic FLOPs are divided by its measured time. ``cpu_baseline`` times the float32
+CPU oracle (the reference's moment equations in torch CPU ops) on a bounded sample of
+the same workload, on the host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "triton-tagi_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "TAGI step samples/sec (fwd+bwd+update) ResNet-18 b128 fp32; % MFMA/HBM peak"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+MFMA_FAMILIES = ("conv_fwd", "conv_bwd_delta", "conv_wgrad", "linear_fwd", "linear_bwd_delta", "linear_wgrad",
+                 "bmm_fwd", "bmm_shared")
+WORKLOAD_DESC = {
+    "resnet18": "TAGI ResNet-18 (BasicBlock 64/128/256/512, BatchNorm2D, Add, AvgPool4, Linear 512-10, Remax), "
+                "batch 128, 3x32x32 ~ N(0,1), gain 0.1, sigma_v 0.05, full fwd+bwd+update step",
+    "cnn": "TAGI CNN (3x Conv5x5 pad2/ReLU/AvgPool2, Linear 1024-256-10, Remax), batch 128, 3x32x32",
+    "mlp": "TAGI MLP 784-256-128-10 ReLU + Remax, batch 256",
+    "transformer": "TAGI transformer block (Embedding 64x256 + PE + MHA-V2 8 heads + RMSNorm + Linear 256-64), "
+                   "batch 64, seq 256",
+}
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(workload: str, sample_batch: int, steps: int = 3):
+    """Float32 CPU oracle step on a bounded sample; samples/s (median of ``steps``)."""
+    import torch
+
+    from oracle import tagi_oracle as O
+    from triton_tagi_amd import workloads
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    w = workloads.build(workload, device="cpu", batch=sample_batch)
+    onet = O.mirror_net(w.net, dtype=torch.float32)
+    x, y = w.x.float(), w.y.float()
+    onet.step(x, y, w.sigma_v)  # warm-up
+    times = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        onet.step(x, y, w.sigma_v)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": sample_batch / med,
+        "unit": "samples/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{workload} step at batch {sample_batch} (same architecture, priors and input distribution), "
+                  f"fp32 torch CPU ops, 1 warm-up + median of {steps} steps ({med:.2f} s/step); cpu: {cpu_model}",
+    }
+
+
+def load_traffic(workload: str, family: str):
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        d = json.loads(p.read_text())
+        return d.get(workload, {}).get(family)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="resnet18", choices=sorted(WORKLOAD_DESC))
+    ap.add_argument("--batch", type=int, default=None)
+    ap.add_argument("--cpu-batch", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this engine runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the step shards over the batch only in the design notes, no multi-GPU path is built)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from triton_tagi_amd import _lib, workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = "cuda:0"
+    log(f"[bench] building {args.workload} on {dev}")
+    w = workloads.build(args.workload, device=dev, batch=args.batch)
+    net, x, y, sv = w.net, w.x, w.y, w.sigma_v
+
+    log(f"[bench] warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        net.step(x, y, sv)
+    torch.cuda.synchronize()
+
+    log(f"[bench] timing {args.steps} steps")
+    _lib.prof_begin()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        net.step(x, y, sv)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    fams = _lib.prof_end()
+    elapsed = t1 - t0
+    ms_per_step = 1e3 * elapsed / args.steps
+    value = w.batch * args.steps / elapsed
+
+    mfma = {f: v for f, v in fams.items() if f in MFMA_FAMILIES}
+    dom = max(mfma, key=lambda f: mfma[f]["ms"]) if mfma else None
+    roofline = None
+    if dom:
+        d = mfma[dom]
+        per_launch_s = d["ms"] / 1e3 / d["launches"]
+        flops_per_launch = d["flops"] / d["launches"]
+        achieved = flops_per_launch / per_launch_s / 1e12
+        roofline = {
+            "bound": "mfma",
+            "kernel": dom,
+            "achieved": round(achieved, 2),
+            "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+            "traffic": load_traffic(args.workload, dom),
+            "launches_per_step": d["launches"] / args.steps,
+            "avg_launch_us": round(per_launch_s * 1e6, 2),
+        }
+    breakdown = {}
+    gpu_ms = sum(v["ms"] for v in fams.values())
+    for f, v in sorted(fams.items(), key=lambda kv: -kv[1]["ms"]):
+        e = {"ms_per_step": round(v["ms"] / args.steps, 4), "launches_per_step": v["launches"] / args.steps}
+        if v["flops"]:
+            e["tflops"] = round(v["flops"] / (v["ms"] / 1e3) / 1e12, 2)
+            e["mfma_frac"] = round(e["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4)
+        elif v["bytes"]:
+            e["gbs"] = round(v["bytes"] / (v["ms"] / 1e3) / 1e9, 1)
+            e["hbm_frac"] = round(e["gbs"] / PEAK_HBM_GBS, 4)
+        breakdown[f] = e
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"[bench] cpu baseline (oracle fp32, batch {args.cpu_batch})")
+        cpu = cpu_baseline(args.workload, args.cpu_batch)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded N(0,1) inputs, one-hot targets, random-init priors of the architecture)",
+        "config": {"workload": WORKLOAD_DESC[args.workload], "global_batch": w.batch, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernel_ms_per_step": round(gpu_ms / args.steps, 4),
+        "families": breakdown,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
