@@ -22,6 +22,15 @@ __device__ __forceinline__ void for_each_vec(int64_t n, F f) {
 // ------------------------------------------------------------------------------ ReLU
 // relu.py:43-86: exact rectified-Gaussian moments; Phi by erf, replaced by the
 // asymptotic pdf/(-alpha) when alpha < -5; variance floored at 0.
+// Variance of max(0, z) given its mean mu = sigma (phi + alpha Phi):
+//   -mu^2 + 2 mu mz - mz sigma phi + (S - mz^2) Phi          (the reference's form)
+//   = S [Phi + alpha^2 Phi Q + alpha phi (Q - Phi) - phi^2],   Q = 1 - Phi
+// The identity holds for any Phi value (it only uses mu = sigma phi + mz Phi), so it also
+// covers the asymptotic branch; the second form has no O(alpha^2) cancellation in fp32.
+__device__ __forceinline__ float rect_var(float S, float alpha, float pdf, float cdf, float Q) {
+  return S * (cdf + alpha * alpha * cdf * Q + alpha * pdf * (Q - cdf) - pdf * pdf);
+}
+
 __device__ __forceinline__ void relu_moments(float mz, float Sz, float& ma, float& Sa, float& J) {
   const float Ss = fmaxf(Sz, 1e-30f);
   const float sig = sqrtf(Ss);
@@ -29,13 +38,11 @@ __device__ __forceinline__ void relu_moments(float mz, float Sz, float& ma, floa
   const float pdf = expf(-0.5f * alpha * alpha) * INV_SQRT_2PI;
   // Phi(alpha) = 0.5 (1 + erf(alpha/sqrt2)) evaluated as 0.5 erfc(-alpha/sqrt2): equal in
   // exact arithmetic, without the fp32 cancellation of the erf form for alpha < 0.
-  const float cdf_erf = 0.5f * erfcf(-alpha * INV_SQRT_2);
-  const float cdf_asym = pdf / (-alpha);
-  const float cdf = (alpha < -5.0f) ? cdf_asym : cdf_erf;
-  const float mu = sig * pdf + mz * cdf;
-  float var = -mu * mu + 2.0f * mu * mz - mz * sig * pdf + (Ss - mz * mz) * cdf;
-  ma = mu;
-  Sa = fmaxf(var, 0.0f);
+  const bool asym = alpha < -5.0f;
+  const float cdf = asym ? pdf / (-alpha) : 0.5f * erfcf(-alpha * INV_SQRT_2);
+  const float Q = asym ? 1.0f - cdf : 0.5f * erfcf(alpha * INV_SQRT_2);
+  ma = sig * pdf + mz * cdf;
+  Sa = fmaxf(rect_var(Ss, alpha, pdf, cdf, Q), 0.0f);
   J = cdf;
 }
 
@@ -277,8 +284,13 @@ __global__ void __launch_bounds__(256) remax_kernel(const float* __restrict__ mz
     const float al = m / sd;
     const float pdf = INV_SQRT_2PI * expf(-0.5f * al * al);
     const float cdf = 0.5f * erfcf(-al * INV_SQRT_2);
-    float mm = fmaxf(m * cdf + sd * pdf, EPS);
-    float vm = fmaxf(-mm * mm + 2.0f * mm * m - m * sd * pdf + (v - m * m) * cdf, EPS);
+    const float mraw = m * cdf + sd * pdf;
+    const float mm = fmaxf(mraw, EPS);
+    // same variance as -mm^2 + 2 mm m - m sd pdf + (v - m^2) cdf while the mean floor is
+    // inactive (see rect_var); the floored case keeps the reference's expression
+    const float vraw = (mraw >= EPS) ? rect_var(v, al, pdf, cdf, 0.5f * erfcf(al * INV_SQRT_2))
+                                     : -mm * mm + 2.0f * mm * m - m * sd * pdf + (v - m * m) * cdf;
+    const float vm = fmaxf(vraw, EPS);
     mu_z[e] = m;
     var_z[e] = v;
     mu_m[e] = mm;
