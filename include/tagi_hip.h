@@ -68,11 +68,12 @@ int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw, const flo
 int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N);
 
 /* Backward delta propagation:  dma = dmz @ mw^T ;  dSa = dSz @ (mw^2)^T.
- * dmz, dSz (M,N); mw (K,N); dma, dSa (M,K).
+ * dmz, dSz (M,N); mw (K,N); dma, dSa (M,K). ws: split-K partials (size from the query).
  * Replaces triton_fused_backward_delta (common.py:287). */
 int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const float* mw,
                           float* dma, float* dSa, int64_t M, int64_t K, int64_t N,
-                          tagi_stream_t stream);
+                          float* ws, int64_t ws_bytes, tagi_stream_t stream);
+int64_t tagi_linear_bwd_delta_ws_bytes(int64_t M, int64_t K, int64_t N);
 
 /* Parameter deltas of a Linear layer (reduction over the M rows):
  *   gmw = ma^T @ dmz, gSw = (ma^2)^T @ dSz, gmb = sum_rows dmz, gSb = sum_rows dSz
@@ -117,7 +118,11 @@ int tagi_bmm_shared(const float* p0, const float* p1, const float* p2, float* me
                     int shared_left, tagi_stream_t stream);
 
 /* ------------------------------------------------------------------ Conv2D ---- */
-/* Geometry of a square-kernel 2-D convolution on NCHW tensors. pad_top/pad_left are the
+/* 4-D activations and deltas of the conv path (Conv2D, BatchNorm2D, AvgPool2D) are
+ * channels-last: element (n, c, h, w) of an (N, C, H, W) tensor sits at ((n*H + h)*W + w)*C + c
+ * (torch.channels_last). Weights keep the reference layout.
+ *
+ * Geometry of a square-kernel 2-D convolution. pad_top/pad_left are the
  * zero rows/cols before the image; rows/cols past H/W read as zero. padding_type 1
  * (symmetric p) is pad_top = pad_left = p, Ho = (H + 2p - k)/s + 1; padding_type 2
  * (right/bottom only, conv2d.py:280-291) is pad_top = pad_left = 0, Ho = (H + p - k)/s + 1. */
@@ -126,7 +131,7 @@ typedef struct {
 } tagi_conv_geom;
 
 /* Implicit-GEMM forward: patches are gathered into LDS, never materialised.
- *   mz = P(ma) @ mw + mb ; Sz = P(ma)^2 @ Sw + P(Sa) @ (mw^2 + Sw) + Sb, written NCHW.
+ *   mz = P(ma) @ mw + mb ; Sz = P(ma)^2 @ Sw + P(Sa) @ (mw^2 + Sw) + Sb (channels-last).
  * mw, Sw (C*k*k, Cout) with rows ordered (c, kh, kw); mb, Sb (Cout).
  * Replaces Conv2D.forward (conv2d.py:254-309: im2col + matmul + fused var + permute). */
 int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw,
@@ -135,10 +140,14 @@ int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw, const flo
 int64_t tagi_conv2d_fwd_ws_bytes(const tagi_conv_geom* g);
 
 /* Transposed implicit GEMM for the input deltas (no patch matrix, no col2im):
- *   dma = fold(dmz_rows @ mw^T), dSa = fold(dSz_rows @ (mw^2)^T), NCHW (N,C,H,W).
+ *   dma = fold(dmz_rows @ mw^T), dSa = fold(dSz_rows @ (mw^2)^T), channels-last (N,C,H,W).
+ * Split by stride phase: each phase multiplies only the kernel taps that reach it.
+ * ws holds the transposed weights (+ split-K partials); size from the query.
  * Replaces conv2d.py:357-370 (fused backward delta + col2im + crop). */
 int tagi_conv2d_bwd_delta(const float* dmz, const float* dSz, const float* mw, float* dma,
-                          float* dSa, const tagi_conv_geom* g, tagi_stream_t stream);
+                          float* dSa, const tagi_conv_geom* g, float* ws, int64_t ws_bytes,
+                          tagi_stream_t stream);
+int64_t tagi_conv2d_bwd_delta_ws_bytes(const tagi_conv_geom* g);
 
 /* Parameter deltas of a Conv2D layer (reduction over N*Ho*Wo patches, split-K):
  *   dmw = Sw * P^T @ dmz, dSw = Sw^2 * (P^2)^T @ dSz, dmb = Sb * sum dmz, dSb = Sb^2 * sum dSz.
@@ -188,8 +197,9 @@ int tagi_capped_update_multi(float* const* m, float* const* S, const float* cons
 int tagi_add_inplace(const float* mu_s, const float* var_s, float* mu_a, float* var_a, int64_t n,
                      tagi_stream_t stream);
 
-/* Non-overlapping k x k average pool of NCHW moments: mean scaled by 1/k^2, variance by
- * var_scale (1/k^4 default, 1/k^2 with spatial_correlation). Replaces avgpool2d.py:38-130. */
+/* Non-overlapping k x k average pool of channels-last moments: mean scaled by 1/k^2,
+ * variance by var_scale (1/k^4 default, 1/k^2 with spatial_correlation); input pixels past
+ * the last full window get zero deltas. Replaces avgpool2d.py:38-130. */
 int tagi_avgpool2d_fwd(const float* ma, const float* Sa, float* ma_out, float* Sa_out, int64_t N,
                        int64_t C, int64_t H, int64_t W, int64_t k, float var_scale,
                        tagi_stream_t stream);
@@ -198,7 +208,7 @@ int tagi_avgpool2d_bwd(const float* dm, const float* dS, float* dm_out, float* d
                        tagi_stream_t stream);
 
 /* ----------------------------------------------------------- BatchNorm2D ---- */
-/* Per-channel batch statistics of NCHW moments (batchnorm2d.py:307-339):
+/* Per-channel batch statistics of channels-last moments (batchnorm2d.py:307-339):
  *   mean_c = E[mu], var_c = (E[S] + E[mu^2] - mean_c^2) * n/(n-1), n = N*H*W,
  * and the running-stat / gamma bookkeeping of batchnorm2d.py:341-355:
  *   first_call: running := batch, and if preserve_var: mg := sqrt(var + eps);

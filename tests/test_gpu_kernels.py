@@ -186,6 +186,9 @@ CONV_CASES = [
     (1, 16, 8, 8, 32, 3, 1, 1, 1),
     (4, 64, 8, 8, 128, 3, 2, 1, 2),
     (2, 5, 11, 11, 7, 4, 3, 2, 1),
+    (2, 4, 9, 9, 8, 1, 2, 0, 1),      # 1x1 stride 2: odd pixels get no taps
+    (2, 8, 10, 7, 12, 2, 3, 1, 1),    # kernel smaller than the stride, uneven sizes
+    (128, 3, 32, 32, 64, 3, 1, 1, 1),  # ResNet-18 stem at full batch
 ]
 
 

@@ -1,15 +1,115 @@
-// Conv2D entry points: implicit-GEMM forward, transposed implicit GEMM for input deltas,
-// split-K parameter deltas.
+// Conv2D entry points on NHWC (channels-last) activations:
+//   forward      implicit GEMM  rows = output pixels, cols = C_out, reduction (kh, kw, c)
+//   input delta  transposed implicit GEMM split by stride phase (only the kernel taps that
+//                reach a phase's pixels are multiplied; no col2im, no zero taps)
+//   deltas       split-K GEMM over output pixels, rows (kh, kw, c) + a ones row for the bias
 #include "tagi_gemm_core.h"
 
 using namespace tagi;
 
 static inline hipStream_t as_stream(tagi_stream_t s) { return (hipStream_t)s; }
 
-// ====================================================================== Conv2D
+static ConvG to_g(const tagi_conv_geom* g) {
+  ConvG c;
+  c.N = (int)g->N;
+  c.C = (int)g->C;
+  c.H = (int)g->H;
+  c.W = (int)g->W;
+  c.Cout = (int)g->Cout;
+  c.kk = (int)g->k;
+  c.stride = (int)g->stride;
+  c.pt = (int)g->pad_top;
+  c.pl = (int)g->pad_left;
+  c.Ho = (int)g->Ho;
+  c.Wo = (int)g->Wo;
+  return c;
+}
+
+static Operand conv_operand(const float* p0, const float* p1, const tagi_conv_geom* g, int64_t MN, int64_t K) {
+  Operand o{};
+  o.p0 = p0;
+  o.p1 = p1;
+  o.zdiv = 1;
+  o.MN = (int)MN;
+  o.K = (int)K;
+  o.ones_row = -1;
+  o.g = to_g(g);
+  return o;
+}
+
+static int check_geom(const tagi_conv_geom* g, const char* what) {
+  TAGI_REQUIRE(g != nullptr, "%s: null geometry", what);
+  TAGI_REQUIRE(g->N > 0 && g->C > 0 && g->H > 0 && g->W > 0 && g->Cout > 0 && g->k > 0 && g->stride > 0,
+               "%s: sizes must be positive", what);
+  // every gathered element is bounds-checked against H and W, so any output extent is
+  // memory-safe; only the caller's output buffers must match Ho and Wo
+  TAGI_REQUIRE(g->pad_top >= 0 && g->pad_left >= 0 && g->Ho > 0 && g->Wo > 0, "%s: bad padding/output size", what);
+  TAGI_REQUIRE(g->stride <= 8 && g->k <= 16, "%s: stride/kernel out of range", what);
+  TAGI_REQUIRE(fits_i32(g->N * g->C * g->H * g->W) && fits_i32(g->N * g->Cout * g->Ho * g->Wo) &&
+                   fits_i32(g->C * g->k * g->k * g->Cout + g->Cout),
+               "%s: tensor too large for 32-bit indexing", what);
+  return TAGI_OK;
+}
+
+static Plan conv_fwd_plan(const tagi_conv_geom* g) {
+  return choose_plan(g->N * g->Ho * g->Wo, g->Cout, g->C * g->k * g->k, 1, 3, true, 16);
+}
+
+// Largest row count (phase 0) and largest reduction over the stride phases of the
+// input-delta GEMM; the launch is sized for both.
+static void bwd_phase0(const tagi_conv_geom* g, int64_t* R, int64_t* K) {
+  const ConvG cg = to_g(g);
+  const Phase p0 = make_phase(cg, 0);
+  *R = g->N * (int64_t)p0.Hq * p0.Wq;
+  int64_t kmax = 0;
+  for (int ph = 0; ph < cg.stride * cg.stride; ++ph) {
+    const Phase p = make_phase(cg, ph);
+    const int64_t k = (int64_t)p.nkh * p.nkw * g->Cout;
+    if (k > kmax) kmax = k;
+  }
+  *K = kmax;
+}
+
+static Plan conv_bwd_plan(const tagi_conv_geom* g) {
+  int64_t R, K;
+  bwd_phase0(g, &R, &K);
+  if (K <= 0) K = 1;
+  return choose_plan(R, g->C, K, (int64_t)g->stride * g->stride, 2, g->stride == 1, 16);
+}
+
+static Plan conv_wgrad_plan(const tagi_conv_geom* g) {
+  return choose_plan(g->C * g->k * g->k + 1, g->Cout, g->N * g->Ho * g->Wo, 1, 2, true, 64);
+}
+
+static int64_t wt_floats(const tagi_conv_geom* g) { return ((g->C * g->k * g->k * g->Cout) + 3) / 4 * 4; }
+
+// Plain transpose of a rows x cols matrix (LDS-tiled 32 x 32, coalesced both ways).
+__global__ void transpose_kernel(const float* __restrict__ in, float* __restrict__ out, int rows, int cols) {
+  __shared__ float tile[32][33];
+  const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 8 rows per pass
+  for (int j = ty; j < 32; j += 8) {
+    const int r = by + j, c = bx + tx;
+    if (r < rows && c < cols) tile[j][tx] = in[(int64_t)r * cols + c];
+  }
+  __syncthreads();
+  for (int j = ty; j < 32; j += 8) {
+    const int r = bx + j, c = by + tx;  // out is cols x rows
+    if (r < cols && c < rows) out[(int64_t)r * rows + c] = tile[tx][j];
+  }
+}
+
+__global__ void zero2_kernel(float* __restrict__ a, float* __restrict__ b, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    a[i] = 0.f;
+    b[i] = 0.f;
+  }
+}
+
+// ====================================================================== forward
 extern "C" int64_t tagi_conv2d_fwd_ws_bytes(const tagi_conv_geom* g) {
-  if (!g || g->N <= 0 || g->Cout <= 0 || g->Ho <= 0 || g->Wo <= 0) return 0;
-  return plan_ws_bytes(conv_fwd_plan(g), g->Cout, g->N * g->Ho * g->Wo, 1);
+  if (!g || g->N <= 0 || g->Cout <= 0 || g->Ho <= 0 || g->Wo <= 0 || g->C <= 0 || g->k <= 0) return 0;
+  return plan_ws_bytes(conv_fwd_plan(g), g->N * g->Ho * g->Wo, g->Cout, 1);
 }
 
 extern "C" int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw, const float* mb,
@@ -20,45 +120,96 @@ extern "C" int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw
   if (rc) return rc;
   TAGI_REQUIRE(ma && Sa && mw && Sw && mz && Sz, "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
-  const int64_t R = g->Cout, C = g->N * g->Ho * g->Wo, K = g->C * g->k * g->k;
-  ProfScope ps(FAM_CONV_FWD, s, 2.0 * 3 * R * C * K,
-               4.0 * (2 * g->N * g->C * g->H * g->W + 2 * K * R + 2 * R * C));
+  const int64_t R = g->N * g->Ho * g->Wo, C = g->Cout, K = g->C * g->k * g->k;
+  ProfScope ps(FAM_CONV_FWD, s, 2.0 * 3 * R * C * K, 4.0 * (2 * g->N * g->C * g->H * g->W + 2 * K * C + 2 * R * C));
   GemmArgs a{};
-  a.a = strided_operand(mw, Sw, 1, 0, 0, 1, R, R, K);
-  a.b = conv_operand(ma, Sa, g, C, K);
-  const int64_t howo = g->Ho * g->Wo;
-  a.epi = epi_store(mz, Sz, mb, Sb, 1, 0, 1.f, 1.f, 1, 0, 0, howo, howo, R * howo, 1);
+  a.a = conv_operand(ma, Sa, g, R, K);
+  a.b = conv_operand(mw, Sw, g, C, K);
+  a.epi = epi_store(mz, Sz, mb, Sb, 0, 1, 1.f, 1.f, 1, 0, 0, C, 1);
   a.R = (int)R;
   a.C = (int)C;
   a.Kred = (int)K;
   Plan p = conv_fwd_plan(g);
   if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, R, C, 1))) p = choose_plan(R, C, K, 1, 3, false, 1);
-  return run_gemm<PROD_FWD, LD_STRIDED_MN, LD_CONV_PATCH_MN>(a, 1, p, ws, ws_bytes, s, what);
+  const bool va = g->C % 4 == 0 && al16(ma) && al16(Sa);
+  const bool vb = g->Cout % 4 == 0 && al16(mw) && al16(Sw);
+  if (va && vb) return run_gemm<PROD_FWD, LD_CFWD_A4, LD_CFWD_B4>(a, 1, p, ws, ws_bytes, s, what);
+  if (vb) return run_gemm<PROD_FWD, LD_CFWD_A_S, LD_CFWD_B4>(a, 1, p, ws, ws_bytes, s, what);
+  return run_gemm<PROD_FWD, LD_CFWD_A_S, LD_CFWD_B_S>(a, 1, p, ws, ws_bytes, s, what);
+}
+
+// ================================================================== input delta
+extern "C" int64_t tagi_conv2d_bwd_delta_ws_bytes(const tagi_conv_geom* g) {
+  if (!g || g->N <= 0 || g->Cout <= 0 || g->C <= 0 || g->k <= 0 || g->stride <= 0) return 0;
+  int64_t R, K;
+  bwd_phase0(g, &R, &K);
+  return wt_floats(g) * (int64_t)sizeof(float) + plan_ws_bytes(conv_bwd_plan(g), R, g->C, 1);
 }
 
 extern "C" int tagi_conv2d_bwd_delta(const float* dmz, const float* dSz, const float* mw, float* dma, float* dSa,
-                                     const tagi_conv_geom* g, tagi_stream_t stream) {
+                                     const tagi_conv_geom* g, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
   const char* what = "tagi_conv2d_bwd_delta";
   int rc = check_geom(g, what);
   if (rc) return rc;
   TAGI_REQUIRE(dmz && dSz && mw && dma && dSa, "%s: null pointer", what);
+  TAGI_REQUIRE(ws && ws_bytes >= wt_floats(g) * (int64_t)sizeof(float), "%s: workspace too small", what);
   hipStream_t s = as_stream(stream);
-  const int64_t hw = g->H * g->W;
-  const int64_t R = g->C, C = g->N * hw, K = g->k * g->k * g->Cout;
+  const int64_t Kw = g->C * g->k * g->k;
   // algorithmic work of the patch-space product (what an explicit col2im path computes)
-  const double alg = 2.0 * 2 * (g->N * g->Ho * g->Wo) * (g->C * g->k * g->k) * g->Cout;
-  ProfScope ps(FAM_CONV_BWD_DELTA, s, alg, 4.0 * (2 * g->N * g->Cout * g->Ho * g->Wo + K * R + 2 * R * C));
+  const double alg = 2.0 * 2 * (g->N * g->Ho * g->Wo) * Kw * g->Cout;
+  ProfScope ps(FAM_CONV_BWD_DELTA, s, alg,
+               4.0 * (2 * g->N * g->Cout * g->Ho * g->Wo + Kw * g->Cout + 2 * g->N * g->C * g->H * g->W));
+  // weights (c, kh, kw) x co  ->  (kh, kw, co) x c: a transpose of the C x (k*k*Cout) matrix
+  const int rows = (int)g->C, cols = (int)(g->k * g->k * g->Cout);
+  float* wt = ws;
+  hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32)), dim3(256), 0, s, mw,
+                     wt, rows, cols);
+  if ((rc = check_launch(what))) return rc;
+  // any input pixel a stride phase leaves without taps gets zero deltas (k < stride)
+  const int nph = (int)(g->stride * g->stride);
+  bool holes = false;
+  for (int ph = 0; ph < nph; ++ph) {
+    const Phase p = make_phase(to_g(g), ph);
+    if (p.Hq > 0 && p.Wq > 0 && (p.nkh == 0 || p.nkw == 0)) holes = true;
+  }
+  if (holes) {
+    const int64_t n = g->N * g->C * g->H * g->W;
+    hipLaunchKernelGGL(zero2_kernel, dim3(ew_blocks(n, 256)), dim3(256), 0, s, dma, dSa, n);
+    if ((rc = check_launch(what))) return rc;
+  }
+  int64_t R0, K0;
+  bwd_phase0(g, &R0, &K0);
   GemmArgs a{};
-  a.a = conv_operand(mw, nullptr, g, R, K);
-  a.b = conv_operand(dmz, dSz, g, C, K);
-  a.epi = epi_store(dma, dSa, nullptr, nullptr, 0, 0, 1.f, 1.f, 1, 0, 0, hw, hw, R * hw, 1);
-  a.R = (int)R;
-  a.C = (int)C;
-  a.Kred = (int)K;
-  Plan p = choose_plan(R, C, K, 1, 2, false, 1);
-  return run_gemm<PROD_SHARED_A, LD_CONV_WT_K, LD_CONV_DY_MN>(a, 1, p, nullptr, 0, s, what);
+  a.a = conv_operand(dmz, dSz, g, R0, K0);
+  a.b = conv_operand(wt, nullptr, g, g->C, K0);
+  a.epi = Epi{};
+  a.epi.kind = 2;
+  a.epi.om = dma;
+  a.epi.ov = dSa;
+  a.epi.zdiv = 1;
+  a.epi.g = to_g(g);
+  a.R = (int)R0;
+  a.C = (int)g->C;
+  a.Kred = (int)K0;
+  a.phased = 1;
+  Plan p = conv_bwd_plan(g);
+  float* part = ws + wt_floats(g);
+  const int64_t part_bytes = ws_bytes - wt_floats(g) * (int64_t)sizeof(float);
+  if (p.splits > 1 && part_bytes < plan_ws_bytes(p, R0, g->C, 1)) p = choose_plan(R0, g->C, K0, nph, 2, false, 1);
+  if (nph > 1) {
+    // phases never split; one chunk covers the longest phase reduction
+    p.splits = 1;
+    p.k_chunk = (int)(cdiv(K0 > 0 ? K0 : 1, 16) * 16);
+  }
+  const int64_t gx = (int64_t)p.tiles_m * p.tiles_n;  // phase 0 is the largest
+  const bool va = g->Cout % 4 == 0 && al16(dmz) && al16(dSz);
+  const bool vb = g->C % 4 == 0;
+  if (va && vb) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B4>(a, nph, p, part, part_bytes, s, what, gx);
+  if (va) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B_S>(a, nph, p, part, part_bytes, s, what, gx);
+  return run_gemm<PROD_SHARED_B, LD_CBWD_A_S, LD_CBWD_B_S>(a, nph, p, part, part_bytes, s, what, gx);
 }
 
+// ============================================================== parameter deltas
 extern "C" int64_t tagi_conv2d_wgrad_ws_bytes(const tagi_conv_geom* g) {
   if (!g || g->N <= 0 || g->Cout <= 0 || g->Ho <= 0 || g->Wo <= 0 || g->C <= 0 || g->k <= 0) return 0;
   return plan_ws_bytes(conv_wgrad_plan(g), g->C * g->k * g->k + 1, g->Cout, 1);
@@ -79,8 +230,10 @@ extern "C" int tagi_conv2d_wgrad(const float* ma, const float* dmz, const float*
   GemmArgs a{};
   a.a = conv_operand(ma, nullptr, g, K, M);
   if (bias) a.a.ones_row = (int)K;
-  a.b = conv_operand(dmz, dSz, g, N, M);
+  a.b = strided_operand(dmz, dSz, 1, 0, 0, 1, N, N, M);
   a.epi = epi_wgrad(dmw, dSw, dmb, dSb, Sw, Sb, K, N);
+  a.epi.perm_C = (int)g->C;
+  a.epi.perm_kk2 = (int)(g->k * g->k);
   a.R = (int)(K + (bias ? 1 : 0));
   a.C = (int)N;
   a.Kred = (int)M;
@@ -88,5 +241,9 @@ extern "C" int tagi_conv2d_wgrad(const float* ma, const float* dmz, const float*
   if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, K + 1, N, 1)))
     p = choose_plan(K + 1, N, M, 1, 2, false, 1);
   p.tiles_m = (int)cdiv(a.R, kCfg[p.cfg].BM);
-  return run_gemm<PROD_SHARED_A, LD_CONV_PATCH_K, LD_CONV_DYROW_K>(a, 1, p, ws, ws_bytes, s, what);
+  const bool va = g->C % 4 == 0 && al16(ma);
+  const bool vb = g->Cout % 4 == 0 && al16(dmz) && al16(dSz);
+  if (va && vb) return run_gemm<PROD_SHARED_A, LD_CWG_A4, LD_STR_MN4>(a, 1, p, ws, ws_bytes, s, what);
+  if (vb) return run_gemm<PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN4>(a, 1, p, ws, ws_bytes, s, what);
+  return run_gemm<PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN_S>(a, 1, p, ws, ws_bytes, s, what);
 }

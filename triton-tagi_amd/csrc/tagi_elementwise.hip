@@ -211,22 +211,26 @@ __global__ void add_kernel(const float* __restrict__ ms, const float* __restrict
 }
 
 // -------------------------------------------------------------------- AvgPool2D
+// Channels-last: one lane per (output pixel, channel); consecutive lanes walk channels,
+// so every window read is a coalesced row of C floats.
 __global__ void avgpool_fwd_kernel(const float* __restrict__ ma, const float* __restrict__ Sa,
-                                   float* __restrict__ mo, float* __restrict__ So, int64_t NC, int H, int W, int k,
-                                   float inv_k2, float var_scale) {
+                                   float* __restrict__ mo, float* __restrict__ So, int64_t N, int H, int W, int C,
+                                   int k, float inv_k2, float var_scale) {
   const int Ho = H / k, Wo = W / k;
-  const int64_t total = NC * Ho * Wo;
+  const int64_t total = N * Ho * Wo * C;
   for_each_vec(total, [&](int64_t i) {
-    const int64_t nc = i / (Ho * Wo);
-    const int r = (int)(i - nc * (Ho * Wo));
+    const int c = (int)(i % C);
+    const int64_t pix = i / C;
+    const int64_t n = pix / (Ho * Wo);
+    const int r = (int)(pix - n * (Ho * Wo));
     const int oh = r / Wo, ow = r - (r / Wo) * Wo;
-    const float* pm = ma + nc * H * W + (int64_t)(oh * k) * W + ow * k;
-    const float* ps = Sa + nc * H * W + (int64_t)(oh * k) * W + ow * k;
+    const int64_t base = ((n * H + (int64_t)oh * k) * W + (int64_t)ow * k) * C + c;
     float sm = 0.f, ss = 0.f;
     for (int a = 0; a < k; ++a)
       for (int b = 0; b < k; ++b) {
-        sm += pm[a * W + b];
-        ss += ps[a * W + b];
+        const int64_t off = base + ((int64_t)a * W + b) * C;
+        sm += ma[off];
+        ss += Sa[off];
       }
     mo[i] = sm * inv_k2;
     So[i] = ss * var_scale;
@@ -234,17 +238,19 @@ __global__ void avgpool_fwd_kernel(const float* __restrict__ ma, const float* __
 }
 
 __global__ void avgpool_bwd_kernel(const float* __restrict__ dm, const float* __restrict__ dS,
-                                   float* __restrict__ om, float* __restrict__ oS, int64_t NC, int H, int W, int k,
-                                   float inv_k2, float var_scale) {
+                                   float* __restrict__ om, float* __restrict__ oS, int64_t N, int H, int W, int C,
+                                   int k, float inv_k2, float var_scale) {
   const int Ho = H / k, Wo = W / k;
-  const int64_t total = NC * H * W;
+  const int64_t total = N * H * W * C;
   for_each_vec(total, [&](int64_t i) {
-    const int64_t nc = i / (H * W);
-    const int r = (int)(i - nc * (H * W));
+    const int c = (int)(i % C);
+    const int64_t pix = i / C;
+    const int64_t n = pix / (H * W);
+    const int r = (int)(pix - n * (H * W));
     const int h = r / W, w = r - (r / W) * W;
     const int oh = h / k, ow = w / k;
     if (oh < Ho && ow < Wo) {
-      const int64_t j = nc * Ho * Wo + oh * Wo + ow;
+      const int64_t j = ((n * Ho + oh) * Wo + ow) * C + c;
       om[i] = dm[j] * inv_k2;
       oS[i] = dS[j] * var_scale;
     } else {
@@ -472,8 +478,8 @@ extern "C" int tagi_avgpool2d_fwd(const float* ma, const float* Sa, float* ma_ou
   hipStream_t s = as_stream(stream);
   const int64_t out = N * C * (H / k) * (W / k);
   ProfScope ps(FAM_AVGPOOL, s, 0.0, 8.0 * (N * C * H * W + out));
-  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(ew_blocks(out, 256)), dim3(256), 0, s, ma, Sa, ma_out, Sa_out, N * C,
-                     (int)H, (int)W, (int)k, 1.0f / (float)(k * k), var_scale);
+  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(ew_blocks(out, 256)), dim3(256), 0, s, ma, Sa, ma_out, Sa_out, N, (int)H,
+                     (int)W, (int)C, (int)k, 1.0f / (float)(k * k), var_scale);
   return check_launch("tagi_avgpool2d_fwd");
 }
 
@@ -484,8 +490,8 @@ extern "C" int tagi_avgpool2d_bwd(const float* dm, const float* dS, float* dm_ou
   hipStream_t s = as_stream(stream);
   const int64_t total = N * C * H * W;
   ProfScope ps(FAM_AVGPOOL, s, 0.0, 8.0 * (total + N * C * (H / k) * (W / k)));
-  hipLaunchKernelGGL(avgpool_bwd_kernel, dim3(ew_blocks(total, 256)), dim3(256), 0, s, dm, dS, dm_out, dS_out, N * C,
-                     (int)H, (int)W, (int)k, 1.0f / (float)(k * k), var_scale);
+  hipLaunchKernelGGL(avgpool_bwd_kernel, dim3(ew_blocks(total, 256)), dim3(256), 0, s, dm, dS, dm_out, dS_out, N,
+                     (int)H, (int)W, (int)C, (int)k, 1.0f / (float)(k * k), var_scale);
   return check_launch("tagi_avgpool2d_bwd");
 }
 

@@ -1,5 +1,5 @@
-// fp32-MFMA moment GEMMs for gfx950 (CDNA4): Linear, Conv2D (implicit GEMM) and the
-// batched attention products all run through one templated kernel.
+// fp32-MFMA moment GEMMs for gfx950 (CDNA4): Linear, Conv2D (implicit GEMM on NHWC
+// activations) and the batched attention products all run through one templated kernel.
 //
 // A TAGI product carries two accumulators per output tile -- the mean and the variance --
 // fed from shared LDS tiles of both operands, with the squared operands formed in
@@ -10,13 +10,13 @@
 //
 // Matrix core: v_mfma_f32_32x32x2f32 (64 lanes; lane l supplies A[l%32][l/32] and
 // B[l/32][l%32]; accumulator register v of lane l is D[8(v/4)+4(l/32)+v%4][l%32]).
-// LDS tiles are stored reduction-major ([k][row] and [k][col]) so both operand reads are
-// 32 consecutive floats per half-wave. Global tiles are prefetched into registers one
-// k-tile ahead of the MFMA work on the current LDS tile.
+// LDS tiles are reduction-major ([k][row], [k][col]) and double-buffered: the global loads
+// of k-tile t+1 are in flight while the MFMAs consume tile t, one barrier per k-tile.
 //
-// Operand loaders gather straight from the caller's tensors: strided views (Linear,
-// attention heads, transposes) or the convolution index maps (patches, transposed
-// patches, weight gathers) -- no im2col / col2im buffers exist anywhere.
+// Operand loaders read the caller's tensors in place -- strided views (Linear, attention
+// heads, transposes) or the NHWC convolution index maps (patches, transposed patches,
+// pre-transposed weights) -- with float4 accesses along whichever dim is contiguous.
+// No im2col / col2im buffer exists anywhere.
 #pragma once
 #include <float.h>
 
@@ -28,200 +28,368 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 enum { PROD_FWD = 0, PROD_SHARED_B = 1, PROD_SHARED_A = 2 };
 
-// Loader kinds. "MN" kinds map consecutive threads to consecutive rows/cols of the tile
-// (global memory contiguous along the output dim); "K" kinds map consecutive threads to
-// consecutive reduction indices (global memory contiguous along the reduction).
+// Loader kinds ("MN": consecutive threads walk the tile's row/col dim, float4 along it;
+// "K": consecutive threads walk the reduction, float4 along it; "S": scalar element gather).
 enum {
-  LD_STRIDED_MN = 0,  // p[zoff + mn*s_mn + k*s_k]
-  LD_STRIDED_K = 1,   // same element, k-fast thread map
-  LD_CONV_PATCH_MN = 2,  // mn = output pixel (n,oh,ow), k = (c,kh,kw): x[n,c,oh*s-pt+kh,ow*s-pl+kw]
-  LD_CONV_PATCH_K = 3,   // mn = (c,kh,kw) [+ ones row], k = output pixel: same element
-  LD_CONV_DY_MN = 4,     // mn = input pixel (n,h,w), k = (kh,kw,co): dy[n,co,oh,ow] with oh*s = h+pt-kh
-  LD_CONV_WT_K = 5,      // mn = c, k = (kh,kw,co): w[(c*kk*kk + kh*kk + kw)*Cout + co]
-  LD_CONV_DYROW_K = 6    // mn = co, k = output pixel (n,p): dy[(n*Cout+co)*HoWo + p]
+  LD_STR_MN4 = 0,     // p[zoff + mn + k*s_k]                   (s_mn == 1)
+  LD_STR_K4 = 1,      // p[zoff + mn*s_mn + k]                  (s_k == 1)
+  LD_STR_MN_S = 2,    // p[zoff + mn*s_mn + k*s_k], scalar, mn-fast
+  LD_STR_K_S = 3,     // same, k-fast
+  LD_CFWD_A4 = 4,     // conv fwd patches: mn = out pixel m, k = (kh,kw,c)  (NHWC, C%4==0)
+  LD_CFWD_A_S = 5,    //   scalar version (any C)
+  LD_CFWD_B4 = 6,     // conv fwd weights: mn = co, k = (kh,kw,c): w[(c*kk2 + kh*kk + kw)*Cout + co]
+  LD_CBWD_A4 = 7,     // conv input delta: mn = phase pixel q, k = (ikh,ikw,co): dy[n,oh,ow,co]
+  LD_CBWD_A_S = 8,    //   scalar version
+  LD_CBWD_B4 = 9,     // transposed weights wt[((kh*kk+kw)*Cout + co)*C + c]: mn = c, k = (ikh,ikw,co)
+  LD_CBWD_B_S = 10,   //   scalar version
+  LD_CWG_A4 = 11,     // conv weight delta patches: mn = (kh,kw,c) [+ ones row], k = out pixel m
+  LD_CWG_A_S = 12,    //   scalar version
+  LD_CFWD_B_S = 13,   // conv fwd weights, scalar (any Cout)
 };
 
 template <int KIND>
 struct KindTraits {
-  static inline constexpr bool mn_fast = (KIND == LD_STRIDED_MN || KIND == LD_CONV_PATCH_MN || KIND == LD_CONV_DY_MN);
+  static constexpr bool mn_fast = (KIND == LD_STR_MN4 || KIND == LD_STR_MN_S || KIND == LD_CFWD_B4 ||
+                                   KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CWG_A4 ||
+                                   KIND == LD_CWG_A_S || KIND == LD_CFWD_B_S);
+  static constexpr bool vec4 = (KIND == LD_STR_MN4 || KIND == LD_STR_K4 || KIND == LD_CFWD_A4 || KIND == LD_CFWD_B4 ||
+                                KIND == LD_CBWD_A4 || KIND == LD_CBWD_B4 || KIND == LD_CWG_A4);
 };
+
+struct ConvG {
+  int N, C, H, W, Cout, kk, stride, pt, pl, Ho, Wo;
+};
+
+// Phase of the stride-s input-delta GEMM: input pixels (h, w) with h % s == a, w % s == b;
+// only kernel taps kh = kh0 + i*s (kw = kw0 + j*s) reach them.
+struct Phase {
+  int a, b, kh0, kw0, nkh, nkw, Hq, Wq;
+};
+
+__host__ __device__ inline Phase make_phase(const ConvG& g, int phase) {
+  Phase p;
+  const int s = g.stride;
+  p.a = phase / s;
+  p.b = phase % s;
+  p.kh0 = (p.a + g.pt) % s;
+  p.kw0 = (p.b + g.pl) % s;
+  p.nkh = p.kh0 < g.kk ? (g.kk - p.kh0 + s - 1) / s : 0;
+  p.nkw = p.kw0 < g.kk ? (g.kk - p.kw0 + s - 1) / s : 0;
+  p.Hq = p.a < g.H ? (g.H - p.a + s - 1) / s : 0;
+  p.Wq = p.b < g.W ? (g.W - p.b + s - 1) / s : 0;
+  return p;
+}
 
 struct Operand {
   const float* p0;
   const float* p1;
-  int64_t zdiv, sz1, sz2;  // batch offset (z/zdiv)*sz1 + (z%zdiv)*sz2
+  int64_t zdiv, sz1, sz2;  // batch offset (z/zdiv)*sz1 + (z%zdiv)*sz2 (strided kinds)
   int64_t s_mn, s_k;       // strided kinds
   int MN, K;               // extents along the tile dim and the reduction
   int ones_row;            // tile index that reads as 1.0 for valid k (bias row), -1 = none
-  // convolution geometry (conv kinds)
-  int C, H, W, Cout, kk, stride, pt, pl, Ho, Wo;
+  ConvG g;                 // conv kinds
 };
 
 struct Epi {
-  int kind;  // 0: strided store (+bias, scale); 1: weight deltas (+bias row)
+  int kind;  // 0: strided store (+bias, scale); 1: weight deltas (+bias row); 2: conv input-delta rows
   float* om;
   float* ov;
   const float* bm;
   const float* bv;
   int64_t b_sr, b_sc;
   float sm, sv;
-  int64_t zdiv, sz1, sz2, srow, cdiv, sc1, sc2;
+  int64_t zdiv, sz1, sz2, srow, scol;
+  // kind 1
   const float* Sw;
   const float* Sb;
   float* dmb;
   float* dSb;
   int wrows;
   int64_t ldw;
+  int perm_C, perm_kk2;  // conv: row r = (kh*kk+kw)*C + c maps to weight row c*kk2 + kh*kk + kw
+  // kind 2
+  ConvG g;
 };
 
 struct GemmArgs {
   Operand a, b;
   Epi epi;
-  int R, C, Kred;
+  int R, C, Kred;  // rows, cols, reduction (per phase for the conv input delta)
   int tiles_m, tiles_n;
   int splits, k_chunk;
+  int phased;      // conv input delta: z indexes the stride phase
   float* partial;  // split-K partial sums, or null to apply the epilogue in place
 };
 
 template <int BM_, int BN_, int WM_, int WN_>
 struct Cfg {
-  static inline constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, BK = 16;
-  static inline constexpr int NTH = (BM / WM) * (BN / WN) * 64;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, BK = 16;
+  static constexpr int NTH = (BM / WM) * (BN / WN) * 64;
 };
 
 // ------------------------------------------------------------------------------------
-// Element gather for each loader kind. Returns the two tensor values at (mn, k).
+// Operand loaders. Each thread owns NC chunks (float4 or scalar) of the BMN x BK tile;
+// the chunk -> (mn, k) map is fixed per thread, so per-row / per-k invariants are
+// computed once in init().
 // ------------------------------------------------------------------------------------
-template <int KIND, int NT>
-__device__ __forceinline__ void gather(const Operand& o, int64_t zoff, int mn, int k, float& v0, float& v1) {
-  v0 = 0.f;
-  v1 = 0.f;
-  if (k >= o.K) return;
-  if constexpr (KIND == LD_STRIDED_MN || KIND == LD_STRIDED_K) {
-    if (mn < o.MN) {
-      int64_t off = zoff + (int64_t)mn * o.s_mn + (int64_t)k * o.s_k;
-      v0 = o.p0[off];
-      if constexpr (NT == 2) v1 = o.p1[off];
-    } else if (mn == o.ones_row) {
-      v0 = 1.f;
-      v1 = 1.f;
-    }
-  } else if constexpr (KIND == LD_CONV_PATCH_MN || KIND == LD_CONV_PATCH_K) {
-    // (pixel, feature) of the implicit patch matrix
-    int m, f;
-    if constexpr (KIND == LD_CONV_PATCH_MN) {
-      m = mn;
-      f = k;
-      if (m >= o.MN) return;
-    } else {
-      m = k;
-      f = mn;
-      if (f >= o.MN) {
-        if (f == o.ones_row) { v0 = 1.f; v1 = 1.f; }
-        return;
+template <int KIND, int NT, int BMN, int BK, int NTH>
+struct Loader {
+  static constexpr bool V4 = KindTraits<KIND>::vec4;
+  static constexpr bool MNF = KindTraits<KIND>::mn_fast;
+  static constexpr int W = V4 ? 4 : 1;  // elements per chunk
+  static constexpr int NC = BMN * BK / (W * NTH);
+  static_assert(NC * W * NTH == BMN * BK, "tile does not split evenly over threads");
+  static constexpr int LD = BMN + 4;
+
+  float4 v[NT][NC];
+  int mnmax, kmax;           // extents checked by fetch (per phase for the conv input delta)
+  int cmn[NC], ck[NC];       // chunk origin within the tile
+  int64_t rowbase[NC];       // per-chunk row invariant (conv kinds)
+  int r0[NC], r1[NC], r2[NC];
+
+  __device__ __forceinline__ void map(int tid) {
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = tid + i * NTH;
+      if constexpr (MNF) {
+        cmn[i] = (c % (BMN / W)) * W;
+        ck[i] = c / (BMN / W);
+      } else {
+        cmn[i] = c / (BK / W);
+        ck[i] = (c % (BK / W)) * W;
       }
     }
-    const int howo = o.Ho * o.Wo;
-    const int n = m / howo;
-    const int p = m - n * howo;
-    const int oh = p / o.Wo;
-    const int ow = p - oh * o.Wo;
-    const int kk2 = o.kk * o.kk;
-    const int c = f / kk2;
-    const int r = f - c * kk2;
-    const int kh = r / o.kk;
-    const int kw = r - kh * o.kk;
-    const int ih = oh * o.stride - o.pt + kh;
-    const int iw = ow * o.stride - o.pl + kw;
-    if (ih < 0 || ih >= o.H || iw < 0 || iw >= o.W) return;
-    int64_t off = ((int64_t)(n * o.C + c) * o.H + ih) * o.W + iw;
-    v0 = o.p0[off];
-    if constexpr (NT == 2) v1 = o.p1[off];
-  } else if constexpr (KIND == LD_CONV_DY_MN) {
-    if (mn >= o.MN) return;
-    const int hw = o.H * o.W;
-    const int n = mn / hw;
-    const int q = mn - n * hw;
-    const int h = q / o.W;
-    const int w = q - h * o.W;
-    const int kidx = k / o.Cout;
-    const int co = k - kidx * o.Cout;
-    const int kh = kidx / o.kk;
-    const int kw = kidx - kh * o.kk;
-    const int ohn = h + o.pt - kh;
-    const int own = w + o.pl - kw;
-    if (ohn < 0 || own < 0) return;
-    const int oh = ohn / o.stride;
-    const int ow = own / o.stride;
-    if (oh * o.stride != ohn || ow * o.stride != own || oh >= o.Ho || ow >= o.Wo) return;
-    int64_t off = ((int64_t)(n * o.Cout + co) * o.Ho + oh) * o.Wo + ow;
-    v0 = o.p0[off];
-    if constexpr (NT == 2) v1 = o.p1[off];
-  } else if constexpr (KIND == LD_CONV_WT_K) {
-    if (mn >= o.MN) return;
-    const int kidx = k / o.Cout;
-    const int co = k - kidx * o.Cout;
-    int64_t off = ((int64_t)mn * (o.kk * o.kk) + kidx) * o.Cout + co;
-    v0 = o.p0[off];
-    if constexpr (NT == 2) v1 = o.p1[off];
-  } else if constexpr (KIND == LD_CONV_DYROW_K) {
-    if (mn >= o.MN) return;
-    const int howo = o.Ho * o.Wo;
-    const int n = k / howo;
-    const int p = k - n * howo;
-    int64_t off = (int64_t)(n * o.Cout + mn) * howo + p;
-    v0 = o.p0[off];
-    if constexpr (NT == 2) v1 = o.p1[off];
   }
-}
 
-// Fetch one BMN x BK tile of NT tensors into registers (E values per tensor per thread).
-template <int KIND, int NT, int BMN, int BK, int NTH>
-__device__ __forceinline__ void fetch_tile(const Operand& o, int64_t zoff, int mn0, int k0, int tid,
-                                           float (&r)[NT][BMN * BK / NTH]) {
-  constexpr int E = BMN * BK / NTH;
-#pragma unroll
-  for (int i = 0; i < E; ++i) {
-    const int e = tid + i * NTH;
-    int mn, k;
-    if constexpr (KindTraits<KIND>::mn_fast) {
-      mn = e % BMN;
-      k = e / BMN;
-    } else {
-      mn = e / BK;
-      k = e % BK;
+  // per-block / per-thread invariants
+  __device__ __forceinline__ void init(const Operand& o, int z, int mn0, int tid) {
+    map(tid);
+    mnmax = o.MN;
+    kmax = o.K;
+    if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S || KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S) {
+      const Phase ph = make_phase(o.g, z);
+      kmax = ph.nkh * ph.nkw * o.g.Cout;
+      if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S) mnmax = o.g.N * ph.Hq * ph.Wq;
     }
-    float v0, v1;
-    gather<KIND, NT>(o, zoff, mn0 + mn, k0 + k, v0, v1);
-    r[0][i] = v0;
-    if constexpr (NT == 2) r[1][i] = v1;
-  }
-}
-
-template <int KIND, int NT, int BMN, int BK, int NTH>
-__device__ __forceinline__ void store_tile(float* s, int tid, const float (&r)[NT][BMN * BK / NTH]) {
-  constexpr int E = BMN * BK / NTH;
-  constexpr int LD = BMN + 4;
+    if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
+      // rows are output pixels: base of image n and the top-left input corner
+      const int howo = o.g.Ho * o.g.Wo;
 #pragma unroll
-  for (int i = 0; i < E; ++i) {
-    const int e = tid + i * NTH;
-    int mn, k;
-    if constexpr (KindTraits<KIND>::mn_fast) {
-      mn = e % BMN;
-      k = e / BMN;
+      for (int i = 0; i < NC; ++i) {
+        const int m = mn0 + cmn[i];
+        if (m < o.MN) {
+          const int n = m / howo, p = m - n * howo;
+          const int oh = p / o.g.Wo, ow = p - oh * o.g.Wo;
+          rowbase[i] = (int64_t)n * o.g.H * o.g.W * o.g.C;
+          r0[i] = oh * o.g.stride - o.g.pt;
+          r1[i] = ow * o.g.stride - o.g.pl;
+        } else {
+          rowbase[i] = 0;
+          r0[i] = -(1 << 28);
+          r1[i] = -(1 << 28);
+        }
+      }
+    } else if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S) {
+      // rows are the phase's input pixels: image base and output coordinates of tap kh0,kw0
+      const Phase ph = make_phase(o.g, z);
+      const int hq = ph.Hq * ph.Wq;
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int q = mn0 + cmn[i];
+        if (q < mnmax && hq > 0) {
+          const int n = q / hq, rr = q - n * hq;
+          const int hh = rr / ph.Wq, ww = rr - hh * ph.Wq;
+          const int h = hh * o.g.stride + ph.a, w = ww * o.g.stride + ph.b;
+          rowbase[i] = (int64_t)n * o.g.Ho * o.g.Wo * o.g.Cout;
+          r0[i] = (h + o.g.pt - ph.kh0) / o.g.stride;
+          r1[i] = (w + o.g.pl - ph.kw0) / o.g.stride;
+        } else {
+          rowbase[i] = 0;
+          r0[i] = -(1 << 28);
+          r1[i] = -(1 << 28);
+        }
+        r2[i] = ph.nkw;
+      }
+    } else if constexpr (KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S) {
+      // tap offsets of this phase
+      const Phase ph = make_phase(o.g, z);
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        r0[i] = ph.kh0;
+        r1[i] = ph.kw0;
+        r2[i] = ph.nkw;
+      }
+    } else if constexpr (KIND == LD_CWG_A4 || KIND == LD_CWG_A_S) {
+      // rows are weight rows r = (kh*kk + kw)*C + c: split once
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int r = mn0 + cmn[i];
+        const int kidx = r / o.g.C;
+        const int c = r - kidx * o.g.C;
+        const int kh = kidx / o.g.kk;
+        r0[i] = kh;
+        r1[i] = kidx - kh * o.g.kk;
+        r2[i] = c;
+      }
     } else {
-      mn = e / BK;
-      k = e % BK;
+      const int64_t zoff = (z / o.zdiv) * o.sz1 + (z % o.zdiv) * o.sz2;
+#pragma unroll
+      for (int i = 0; i < NC; ++i) rowbase[i] = zoff;
     }
-    s[k * LD + mn] = r[0][i];
-    if constexpr (NT == 2) s[BK * LD + k * LD + mn] = r[1][i];
   }
-}
 
+  __device__ __forceinline__ float4 ld4(const float* p, int64_t off) const {
+    return *reinterpret_cast<const float4*>(p + off);
+  }
+
+  __device__ __forceinline__ void fetch(const Operand& o, int z, int mn0, int k0) {
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int mn = mn0 + cmn[i];
+      const int k = k0 + ck[i];
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+      if constexpr (KIND == LD_STR_MN4) {
+        if (k < o.K) {
+          if (mn < o.MN) {
+            const int64_t off = rowbase[i] + mn + (int64_t)k * o.s_k;
+            a = ld4(o.p0, off);
+            if constexpr (NT == 2) b = ld4(o.p1, off);
+          } else if (mn == o.ones_row) {
+            a = make_float4(1.f, 0.f, 0.f, 0.f);
+          }
+        }
+      } else if constexpr (KIND == LD_STR_K4) {
+        if (mn < o.MN && k < o.K) {
+          const int64_t off = rowbase[i] + (int64_t)mn * o.s_mn + k;
+          a = ld4(o.p0, off);
+          if constexpr (NT == 2) b = ld4(o.p1, off);
+        }
+      } else if constexpr (KIND == LD_STR_MN_S || KIND == LD_STR_K_S) {
+        if (k < o.K) {
+          if (mn < o.MN) {
+            const int64_t off = rowbase[i] + (int64_t)mn * o.s_mn + (int64_t)k * o.s_k;
+            a.x = o.p0[off];
+            if constexpr (NT == 2) b.x = o.p1[off];
+          } else if (mn == o.ones_row) {
+            a.x = 1.f;
+          }
+        }
+      } else if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
+        if (k < o.K) {
+          const int kidx = k / o.g.C;
+          const int c = k - kidx * o.g.C;
+          const int kh = kidx / o.g.kk, kw = kidx - (kidx / o.g.kk) * o.g.kk;
+          const int ih = r0[i] + kh, iw = r1[i] + kw;
+          if (ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W) {
+            const int64_t off = rowbase[i] + ((int64_t)ih * o.g.W + iw) * o.g.C + c;
+            if constexpr (V4) {
+              a = ld4(o.p0, off);
+              if constexpr (NT == 2) b = ld4(o.p1, off);
+            } else {
+              a.x = o.p0[off];
+              if constexpr (NT == 2) b.x = o.p1[off];
+            }
+          }
+        }
+      } else if constexpr (KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
+        if (k < o.K && mn < o.MN) {
+          const int kidx = k / o.g.C;
+          const int c = k - kidx * o.g.C;
+          const int64_t off = ((int64_t)c * (o.g.kk * o.g.kk) + kidx) * o.g.Cout + mn;
+          if constexpr (V4) {
+            a = ld4(o.p0, off);
+            if constexpr (NT == 2) b = ld4(o.p1, off);
+          } else {
+            a.x = o.p0[off];
+            if constexpr (NT == 2) b.x = o.p1[off];
+          }
+        }
+      } else if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S) {
+        if (k < kmax) {
+          const int kidx = k / o.g.Cout;
+          const int co = k - kidx * o.g.Cout;
+          const int ikh = kidx / r2[i];
+          const int ikw = kidx - ikh * r2[i];
+          const int oh = r0[i] - ikh, ow = r1[i] - ikw;
+          if (oh >= 0 && oh < o.g.Ho && ow >= 0 && ow < o.g.Wo) {
+            const int64_t off = rowbase[i] + ((int64_t)oh * o.g.Wo + ow) * o.g.Cout + co;
+            if constexpr (V4) {
+              a = ld4(o.p0, off);
+              if constexpr (NT == 2) b = ld4(o.p1, off);
+            } else {
+              a.x = o.p0[off];
+              if constexpr (NT == 2) b.x = o.p1[off];
+            }
+          }
+        }
+      } else if constexpr (KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S) {
+        if (k < kmax && mn < mnmax) {
+          const int kidx = k / o.g.Cout;
+          const int co = k - kidx * o.g.Cout;
+          const int ikh = kidx / r2[i];
+          const int kh = r0[i] + ikh * o.g.stride;
+          const int kw = r1[i] + (kidx - ikh * r2[i]) * o.g.stride;
+          const int64_t off = (((int64_t)(kh * o.g.kk + kw) * o.g.Cout + co)) * o.g.C + mn;
+          if constexpr (V4) {
+            a = ld4(o.p0, off);
+          } else {
+            a.x = o.p0[off];
+          }
+        }
+      } else if constexpr (KIND == LD_CWG_A4 || KIND == LD_CWG_A_S) {
+        if (k < o.K) {
+          if (mn < o.MN) {
+            const int howo = o.g.Ho * o.g.Wo;
+            const int n = k / howo, p = k - n * howo;
+            const int oh = p / o.g.Wo, ow = p - oh * o.g.Wo;
+            const int ih = oh * o.g.stride - o.g.pt + r0[i];
+            const int iw = ow * o.g.stride - o.g.pl + r1[i];
+            if (ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W) {
+              const int64_t off = (((int64_t)n * o.g.H + ih) * o.g.W + iw) * o.g.C + r2[i];
+              if constexpr (V4) {
+                a = ld4(o.p0, off);
+              } else {
+                a.x = o.p0[off];
+              }
+            }
+          } else if (mn == o.ones_row) {
+            a.x = 1.f;
+          }
+        }
+      }
+      v[0][i] = a;
+      if constexpr (NT == 2) v[1][i] = b;
+    }
+  }
+
+  __device__ __forceinline__ void store(float* s) const {
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        float* st = s + t * BK * LD;
+        const float4 x = v[t][i];
+        if constexpr (!V4) {
+          st[ck[i] * LD + cmn[i]] = x.x;
+        } else if constexpr (MNF) {
+          *reinterpret_cast<float4*>(st + ck[i] * LD + cmn[i]) = x;
+        } else {
+          st[(ck[i] + 0) * LD + cmn[i]] = x.x;
+          st[(ck[i] + 1) * LD + cmn[i]] = x.y;
+          st[(ck[i] + 2) * LD + cmn[i]] = x.z;
+          st[(ck[i] + 3) * LD + cmn[i]] = x.w;
+        }
+      }
+    }
+  }
+};
+
+// ------------------------------------------------------------------------------------
+// Epilogue
+// ------------------------------------------------------------------------------------
 __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col, float m, float v) {
   if (e.kind == 0) {
-    const int64_t off = (z / e.zdiv) * e.sz1 + (z % e.zdiv) * e.sz2 + (int64_t)row * e.srow +
-                        (col / e.cdiv) * e.sc1 + (col % e.cdiv) * e.sc2;
+    const int64_t off = (z / e.zdiv) * e.sz1 + (z % e.zdiv) * e.sz2 + (int64_t)row * e.srow + (int64_t)col * e.scol;
     float rm = m * e.sm;
     float rv = v * e.sv;
     const int64_t bi = (int64_t)row * e.b_sr + (int64_t)col * e.b_sc;
@@ -229,9 +397,14 @@ __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col,
     if (e.bv) rv += e.bv[bi];
     if (e.om) e.om[off] = rm;
     e.ov[off] = rv;
-  } else {
+  } else if (e.kind == 1) {
     if (row < e.wrows) {
-      const int64_t idx = (int64_t)row * e.ldw + col;
+      int wr = row;
+      if (e.perm_C > 0) {
+        const int kidx = row / e.perm_C;
+        wr = (row - kidx * e.perm_C) * e.perm_kk2 + kidx;
+      }
+      const int64_t idx = (int64_t)wr * e.ldw + col;
       const float s = e.Sw ? e.Sw[idx] : 1.f;
       e.om[idx] = s * m;
       e.ov[idx] = (s * s) * v;
@@ -240,22 +413,42 @@ __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col,
       e.dmb[col] = s * m;
       e.dSb[col] = (s * s) * v;
     }
+  } else {
+    // conv input delta: row = pixel q of phase z, col = input channel
+    const Phase ph = make_phase(e.g, z);
+    const int hq = ph.Hq * ph.Wq;
+    const int n = row / hq, rr = row - n * hq;
+    const int hh = rr / ph.Wq, ww = rr - hh * ph.Wq;
+    const int h = hh * e.g.stride + ph.a, w = ww * e.g.stride + ph.b;
+    const int64_t off = (((int64_t)n * e.g.H + h) * e.g.W + w) * e.g.C + col;
+    e.om[off] = m;
+    e.ov[off] = v;
   }
 }
 
+// Rows of the output tile in GEMM z (phase-dependent for the conv input delta).
+__device__ __forceinline__ int rows_of(const GemmArgs& g, int z) {
+  if (!g.phased) return g.R;
+  const Phase ph = make_phase(g.a.g, z);
+  return g.a.g.N * ph.Hq * ph.Wq;
+}
+
+__device__ __forceinline__ int kred_of(const GemmArgs& g, int z) {
+  if (!g.phased) return g.Kred;
+  const Phase ph = make_phase(g.a.g, z);
+  return ph.nkh * ph.nkw * g.a.g.Cout;
+}
+
 template <int PROD, class CFG, int KA, int KB>
-__global__ void __launch_bounds__(CFG::NTH) gemm_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(CFG::NTH, (CFG::NTH <= 256 ? 2 : 1)) gemm_kernel(GemmArgs g) {
   constexpr int BM = CFG::BM, BN = CFG::BN, BK = CFG::BK, WM = CFG::WM, WN = CFG::WN, NTH = CFG::NTH;
   constexpr int NA = (PROD == PROD_SHARED_A) ? 1 : 2;
   constexpr int NB = (PROD == PROD_SHARED_B) ? 1 : 2;
   constexpr int LDA = BM + 4, LDB = BN + 4;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int EA = BM * BK / NTH, EB = BN * BK / NTH;
-  static_assert(NTH % BM == 0 && NTH % BN == 0 && NTH % BK == 0, "thread map");
-  static_assert(EA * NTH == BM * BK && EB * NTH == BN * BK, "tile split");
+  constexpr int SA = NA * BK * LDA, SB = NB * BK * LDB;
 
-  __shared__ float sA[NA * BK * LDA];
-  __shared__ float sB[NB * BK * LDB];
+  __shared__ __attribute__((aligned(16))) float smem[2 * (SA + SB)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -265,25 +458,32 @@ __global__ void __launch_bounds__(CFG::NTH) gemm_kernel(GemmArgs g) {
   const int hl = lane >> 5;
   const int rl = lane & 31;
 
+  const int zz = blockIdx.y;
+  const int z = zz / g.splits;
+  const int split = zz - z * g.splits;
+  const int R = rows_of(g, z);
+  const int Kred = kred_of(g, z);
+  const int tiles_m = g.phased ? (R + BM - 1) / BM : g.tiles_m;
+
   // XCD-aware tile order: workgroups are dealt round-robin over the 8 XCDs, so map
   // consecutive block ids of one XCD onto consecutive tiles (shared operand panels stay
   // in that XCD's L2).
-  const int nt = g.tiles_m * g.tiles_n;
+  const int nt = tiles_m * g.tiles_n;
   const int bid = blockIdx.x;
+  if (bid >= nt) return;  // phased launches size the grid for the largest phase
   const int per = nt >> 3;
   const int t = (bid < (per << 3)) ? ((bid & 7) * per + (bid >> 3)) : bid;
   const int tmi = t / g.tiles_n;
   const int tni = t - tmi * g.tiles_n;
   const int m0 = tmi * BM;
   const int n0 = tni * BN;
-  const int zz = blockIdx.y;
-  const int z = zz / g.splits;
-  const int split = zz - z * g.splits;
   const int kbeg = split * g.k_chunk;
-  const int kend = min(g.Kred, kbeg + g.k_chunk);
+  const int kend = min(Kred, kbeg + g.k_chunk);
 
-  const int64_t zoa = (z / g.a.zdiv) * g.a.sz1 + (z % g.a.zdiv) * g.a.sz2;
-  const int64_t zob = (z / g.b.zdiv) * g.b.sz1 + (z % g.b.zdiv) * g.b.sz2;
+  Loader<KA, NA, BM, BK, NTH> la;
+  Loader<KB, NB, BN, BK, NTH> lb;
+  la.init(g.a, z, m0, tid);
+  lb.init(g.b, z, n0, tid);
 
   floatx16 accM[TM][TN], accV[TM][TN];
 #pragma unroll
@@ -296,20 +496,21 @@ __global__ void __launch_bounds__(CFG::NTH) gemm_kernel(GemmArgs g) {
         accV[i][j][v] = 0.f;
       }
 
-  float ra[NA][EA];
-  float rb[NB][EB];
-  if (kbeg < kend) {
-    fetch_tile<KA, NA, BM, BK, NTH>(g.a, zoa, m0, kbeg, tid, ra);
-    fetch_tile<KB, NB, BN, BK, NTH>(g.b, zob, n0, kbeg, tid, rb);
+  const int nk = kbeg < kend ? (kend - kbeg + BK - 1) / BK : 0;
+  if (nk > 0) {
+    la.fetch(g.a, z, m0, kbeg);
+    lb.fetch(g.b, z, n0, kbeg);
+    la.store(smem);
+    lb.store(smem + SA);
   }
+  __syncthreads();
 
-  for (int k0 = kbeg; k0 < kend; k0 += BK) {
-    store_tile<KA, NA, BM, BK, NTH>(sA, tid, ra);
-    store_tile<KB, NB, BN, BK, NTH>(sB, tid, rb);
-    __syncthreads();
-    if (k0 + BK < kend) {
-      fetch_tile<KA, NA, BM, BK, NTH>(g.a, zoa, m0, k0 + BK, tid, ra);
-      fetch_tile<KB, NB, BN, BK, NTH>(g.b, zob, n0, k0 + BK, tid, rb);
+  for (int kt = 0; kt < nk; ++kt) {
+    const float* sA = smem + (kt & 1) * (SA + SB);
+    const float* sB = sA + SA;
+    if (kt + 1 < nk) {
+      la.fetch(g.a, z, m0, kbeg + (kt + 1) * BK);
+      lb.fetch(g.b, z, n0, kbeg + (kt + 1) * BK);
     }
 #pragma unroll
     for (int s = 0; s < BK / 2; ++s) {
@@ -365,10 +566,15 @@ __global__ void __launch_bounds__(CFG::NTH) gemm_kernel(GemmArgs g) {
           }
       }
     }
+    if (kt + 1 < nk) {
+      float* nA = smem + ((kt + 1) & 1) * (SA + SB);
+      la.store(nA);
+      lb.store(nA + SA);
+    }
     __syncthreads();
   }
 
-  // Epilogue: direct store, or split-K partials.
+  // Epilogue: direct store, or split-K partials (phased launches never split).
   const int64_t plane = (int64_t)g.R * g.C;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -378,7 +584,7 @@ __global__ void __launch_bounds__(CFG::NTH) gemm_kernel(GemmArgs g) {
       for (int v = 0; v < 16; ++v) {
         const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
         const int col = n0 + wn * WN + j * 32 + rl;
-        if (row < g.R && col < g.C) {
+        if (row < R && col < g.C) {
           if (g.partial) {
             const int64_t base = ((int64_t)zz * 2) * plane + (int64_t)row * g.C + col;
             g.partial[base] = accM[i][j][v];
@@ -392,8 +598,7 @@ __global__ void __launch_bounds__(CFG::NTH) gemm_kernel(GemmArgs g) {
 
 // Deterministic split-K reduction (fixed split order) followed by the epilogue.
 template <int UNUSED = 0>
-__global__ void splitk_reduce_kernel(const float* __restrict__ partial, Epi epi, int batch, int splits, int R,
-                                     int C) {
+__global__ void splitk_reduce_kernel(const float* __restrict__ partial, Epi epi, int batch, int splits, int R, int C) {
   const int64_t plane = (int64_t)R * C;
   const int64_t total = plane * batch;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
@@ -416,6 +621,7 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ partial, Epi epi,
 // Host side: tile-config choice, split-K choice and launch.
 // ------------------------------------------------------------------------------------
 using C128x128 = Cfg<128, 128, 64, 64>;
+using C256x64 = Cfg<256, 64, 64, 64>;
 using C64x256 = Cfg<64, 256, 64, 64>;
 using C128x64 = Cfg<128, 64, 64, 32>;
 using C64x128 = Cfg<64, 128, 32, 64>;
@@ -425,8 +631,8 @@ using C32x32 = Cfg<32, 32, 32, 32>;
 struct CfgDesc {
   int BM, BN;
 };
-static const CfgDesc kCfg[] = {{128, 128}, {64, 256}, {128, 64}, {64, 128}, {64, 64}, {32, 32}};
-static const int kNumCfg = 6;
+static const CfgDesc kCfg[] = {{128, 128}, {256, 64}, {64, 256}, {128, 64}, {64, 128}, {64, 64}, {32, 32}};
+static const int kNumCfg = 7;
 
 struct Plan {
   int cfg;
@@ -439,8 +645,8 @@ struct Plan {
 // the busiest wave of blocks (two resident blocks per CU) inflated by the per-tile load
 // overhead, plus the HBM time of the split-K partial round trip.
 static inline Plan choose_plan(int64_t R, int64_t C, int64_t Kred, int64_t batch, int products, bool allow_split,
-                        int64_t max_splits) {
-  Plan best{5, 1, (int)Kred, 1, 1};
+                               int64_t max_splits) {
+  Plan best{6, 1, (int)Kred, 1, 1};
   double best_t = DBL_MAX;
   const double flops_per_block_s = 157.3e12 / 256.0 / 2.0;
   for (int ci = 0; ci < kNumCfg; ++ci) {
@@ -449,12 +655,12 @@ static inline Plan choose_plan(int64_t R, int64_t C, int64_t Kred, int64_t batch
     for (int64_t sp = 1; sp <= 64; sp *= 2) {
       if (sp > 1 && (!allow_split || sp > max_splits)) break;
       int64_t kc = cdiv(cdiv(Kred, sp), 16) * 16;
-      if (kc < 1) kc = 16;
+      if (kc < 16) kc = 16;
       const int64_t actual = cdiv(Kred, kc);
       if (sp > 1 && actual < sp) break;
       const int64_t blocks = tm * tn * batch * actual;
       const int64_t waves = cdiv(blocks, 512);
-      const double eff = 1.0 + 32.0 / BM + 32.0 / BN;
+      const double eff = 1.0 + 32.0 / BM + 32.0 / BN + (BM * BN < 64 * 64 ? 1.0 : 0.0);
       double t = waves * (2.0 * BM * BN * kc * products * eff) / flops_per_block_s;
       if (actual > 1) t += (double)(actual * 2 + 2) * R * C * batch * 4.0 / 5.0e12 + 4e-6;
       if (t < best_t * 0.999) {
@@ -472,12 +678,15 @@ static inline int64_t plan_ws_bytes(const Plan& p, int64_t R, int64_t C, int64_t
 
 template <int PROD, class CFG, int KA, int KB>
 static inline void launch_cfg(const GemmArgs& g, int64_t grid_x, int64_t grid_y, hipStream_t s) {
-  hipLaunchKernelGGL((gemm_kernel<PROD, CFG, KA, KB>), dim3((unsigned)grid_x, (unsigned)grid_y), dim3(CFG::NTH), 0, s, g);
+  hipLaunchKernelGGL((gemm_kernel<PROD, CFG, KA, KB>), dim3((unsigned)grid_x, (unsigned)grid_y), dim3(CFG::NTH), 0, s,
+                     g);
 }
 
+// Launch with plan p. For phased (conv input-delta) launches grid_x covers the largest
+// phase and blocks past a phase's tiles exit at once.
 template <int PROD, int KA, int KB>
 static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, int64_t ws_bytes, hipStream_t s,
-                    const char* what) {
+                           const char* what, int64_t grid_x_override = 0) {
   g.tiles_m = p.tiles_m;
   g.tiles_n = p.tiles_n;
   g.splits = p.splits;
@@ -489,15 +698,17 @@ static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, 
                  (long long)ws_bytes);
     g.partial = ws;
   }
-  const int64_t gx = (int64_t)p.tiles_m * p.tiles_n;
+  const int64_t gx = grid_x_override > 0 ? grid_x_override : (int64_t)p.tiles_m * p.tiles_n;
   const int64_t gy = batch * p.splits;
-  TAGI_REQUIRE(gx < (1ll << 31) && gy < 65536, "%s: grid too large (%lld x %lld)", what, (long long)gx, (long long)gy);
+  TAGI_REQUIRE(gx > 0 && gx < (1ll << 31) && gy < 65536, "%s: grid out of range (%lld x %lld)", what, (long long)gx,
+               (long long)gy);
   switch (p.cfg) {
     case 0: launch_cfg<PROD, C128x128, KA, KB>(g, gx, gy, s); break;
-    case 1: launch_cfg<PROD, C64x256, KA, KB>(g, gx, gy, s); break;
-    case 2: launch_cfg<PROD, C128x64, KA, KB>(g, gx, gy, s); break;
-    case 3: launch_cfg<PROD, C64x128, KA, KB>(g, gx, gy, s); break;
-    case 4: launch_cfg<PROD, C64x64, KA, KB>(g, gx, gy, s); break;
+    case 1: launch_cfg<PROD, C256x64, KA, KB>(g, gx, gy, s); break;
+    case 2: launch_cfg<PROD, C64x256, KA, KB>(g, gx, gy, s); break;
+    case 3: launch_cfg<PROD, C128x64, KA, KB>(g, gx, gy, s); break;
+    case 4: launch_cfg<PROD, C64x128, KA, KB>(g, gx, gy, s); break;
+    case 5: launch_cfg<PROD, C64x64, KA, KB>(g, gx, gy, s); break;
     default: launch_cfg<PROD, C32x32, KA, KB>(g, gx, gy, s); break;
   }
   int rc = check_launch(what);
@@ -512,7 +723,7 @@ static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, 
 }
 
 static inline Operand strided_operand(const float* p0, const float* p1, int64_t zdiv, int64_t sz1, int64_t sz2,
-                               int64_t s_mn, int64_t s_k, int64_t MN, int64_t K) {
+                                      int64_t s_mn, int64_t s_k, int64_t MN, int64_t K) {
   Operand o{};
   o.p0 = p0;
   o.p1 = p1;
@@ -527,9 +738,8 @@ static inline Operand strided_operand(const float* p0, const float* p1, int64_t 
   return o;
 }
 
-static inline Epi epi_store(float* om, float* ov, const float* bm, const float* bv, int64_t b_sr, int64_t b_sc, float sm,
-                     float sv, int64_t zdiv, int64_t sz1, int64_t sz2, int64_t srow, int64_t cdiv_, int64_t sc1,
-                     int64_t sc2) {
+static inline Epi epi_store(float* om, float* ov, const float* bm, const float* bv, int64_t b_sr, int64_t b_sc,
+                            float sm, float sv, int64_t zdiv, int64_t sz1, int64_t sz2, int64_t srow, int64_t scol) {
   Epi e{};
   e.kind = 0;
   e.om = om;
@@ -544,14 +754,12 @@ static inline Epi epi_store(float* om, float* ov, const float* bm, const float* 
   e.sz1 = sz1;
   e.sz2 = sz2;
   e.srow = srow;
-  e.cdiv = cdiv_ > 0 ? cdiv_ : 1;
-  e.sc1 = sc1;
-  e.sc2 = sc2;
+  e.scol = scol;
   return e;
 }
 
-static inline Epi epi_wgrad(float* dmw, float* dSw, float* dmb, float* dSb, const float* Sw, const float* Sb, int64_t wrows,
-                     int64_t ldw) {
+static inline Epi epi_wgrad(float* dmw, float* dSw, float* dmb, float* dSb, const float* Sw, const float* Sb,
+                            int64_t wrows, int64_t ldw) {
   Epi e{};
   e.kind = 1;
   e.om = dmw;
@@ -563,56 +771,11 @@ static inline Epi epi_wgrad(float* dmw, float* dSw, float* dmb, float* dSb, cons
   e.wrows = (int)wrows;
   e.ldw = ldw;
   e.zdiv = 1;
-  e.cdiv = 1;
   return e;
 }
 
 static inline bool fits_i32(int64_t v) { return v >= 0 && v < (1ll << 31); }
 
-// Plans are shared by the entry points and their workspace queries.
-static inline Plan linear_fwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, N, K, 1, 3, true, 16); }
-static inline Plan linear_wgrad_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(K + 1, N, M, 1, 2, true, 64); }
-
-static inline Operand conv_operand(const float* p0, const float* p1, const tagi_conv_geom* g, int64_t MN, int64_t K) {
-  Operand o{};
-  o.p0 = p0;
-  o.p1 = p1;
-  o.zdiv = 1;
-  o.MN = (int)MN;
-  o.K = (int)K;
-  o.ones_row = -1;
-  o.C = (int)g->C;
-  o.H = (int)g->H;
-  o.W = (int)g->W;
-  o.Cout = (int)g->Cout;
-  o.kk = (int)g->k;
-  o.stride = (int)g->stride;
-  o.pt = (int)g->pad_top;
-  o.pl = (int)g->pad_left;
-  o.Ho = (int)g->Ho;
-  o.Wo = (int)g->Wo;
-  return o;
-}
-
-static inline int check_geom(const tagi_conv_geom* g, const char* what) {
-  TAGI_REQUIRE(g != nullptr, "%s: null geometry", what);
-  TAGI_REQUIRE(g->N > 0 && g->C > 0 && g->H > 0 && g->W > 0 && g->Cout > 0 && g->k > 0 && g->stride > 0,
-               "%s: sizes must be positive", what);
-  // every gathered element is bounds-checked against H and W, so any output extent is
-  // memory-safe; only the caller's output buffers must match Ho and Wo
-  TAGI_REQUIRE(g->pad_top >= 0 && g->pad_left >= 0 && g->Ho > 0 && g->Wo > 0, "%s: bad padding/output size", what);
-  TAGI_REQUIRE(fits_i32(g->N * g->C * g->H * g->W) && fits_i32(g->N * g->Cout * g->Ho * g->Wo) &&
-                   fits_i32(g->C * g->k * g->k * g->Cout),
-               "%s: tensor too large for 32-bit indexing", what);
-  return TAGI_OK;
-}
-
-static inline Plan conv_fwd_plan(const tagi_conv_geom* g) {
-  return choose_plan(g->Cout, g->N * g->Ho * g->Wo, g->C * g->k * g->k, 1, 3, true, 16);
-}
-static inline Plan conv_wgrad_plan(const tagi_conv_geom* g) {
-  return choose_plan(g->C * g->k * g->k + 1, g->Cout, g->N * g->Ho * g->Wo, 1, 2, true, 64);
-}
+static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace tagi
-

@@ -5,7 +5,10 @@ using namespace tagi;
 
 static inline hipStream_t as_stream(tagi_stream_t s) { return (hipStream_t)s; }
 
-// ====================================================================== Linear
+static Plan linear_fwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, N, K, 1, 3, true, 16); }
+static Plan linear_bwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, K, N, 1, 2, true, 16); }
+static Plan linear_wgrad_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(K + 1, N, M, 1, 2, true, 64); }
+
 extern "C" int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N) {
   if (M <= 0 || K <= 0 || N <= 0) return 0;
   return plan_ws_bytes(linear_fwd_plan(M, K, N), M, N, 1);
@@ -24,17 +27,25 @@ extern "C" int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw
   GemmArgs g{};
   g.a = strided_operand(ma, Sa, 1, 0, 0, K, 1, M, K);
   g.b = strided_operand(mw, Sw, 1, 0, 0, 1, N, N, K);
-  g.epi = epi_store(mz, Sz, mb, Sb, 0, 1, 1.f, 1.f, 1, 0, 0, N, N, 0, 1);
+  g.epi = epi_store(mz, Sz, mb, Sb, 0, 1, 1.f, 1.f, 1, 0, 0, N, 1);
   g.R = (int)M;
   g.C = (int)N;
   g.Kred = (int)K;
   Plan p = linear_fwd_plan(M, K, N);
   if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, N, 1))) p = choose_plan(M, N, K, 1, 3, false, 1);
-  return run_gemm<PROD_FWD, LD_STRIDED_K, LD_STRIDED_MN>(g, 1, p, ws, ws_bytes, s, what);
+  const bool v4 = K % 4 == 0 && N % 4 == 0 && al16(ma) && al16(Sa) && al16(mw) && al16(Sw);
+  if (v4) return run_gemm<PROD_FWD, LD_STR_K4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
+  return run_gemm<PROD_FWD, LD_STR_K_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
+}
+
+extern "C" int64_t tagi_linear_bwd_delta_ws_bytes(int64_t M, int64_t K, int64_t N) {
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  return plan_ws_bytes(linear_bwd_plan(M, K, N), M, K, 1);
 }
 
 extern "C" int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const float* mw, float* dma, float* dSa,
-                                     int64_t M, int64_t K, int64_t N, tagi_stream_t stream) {
+                                     int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes,
+                                     tagi_stream_t stream) {
   const char* what = "tagi_linear_bwd_delta";
   TAGI_REQUIRE(dmz && dSz && mw && dma && dSa, "%s: null pointer", what);
   TAGI_REQUIRE(M > 0 && K > 0 && N > 0, "%s: sizes must be positive", what);
@@ -44,12 +55,15 @@ extern "C" int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const f
   GemmArgs g{};
   g.a = strided_operand(dmz, dSz, 1, 0, 0, N, 1, M, N);
   g.b = strided_operand(mw, nullptr, 1, 0, 0, N, 1, K, N);
-  g.epi = epi_store(dma, dSa, nullptr, nullptr, 0, 0, 1.f, 1.f, 1, 0, 0, K, K, 0, 1);
+  g.epi = epi_store(dma, dSa, nullptr, nullptr, 0, 0, 1.f, 1.f, 1, 0, 0, K, 1);
   g.R = (int)M;
   g.C = (int)K;
   g.Kred = (int)N;
-  Plan p = choose_plan(M, K, N, 1, 2, false, 1);
-  return run_gemm<PROD_SHARED_B, LD_STRIDED_K, LD_STRIDED_K>(g, 1, p, nullptr, 0, s, what);
+  Plan p = linear_bwd_plan(M, K, N);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, K, 1))) p = choose_plan(M, K, N, 1, 2, false, 1);
+  const bool v4 = N % 4 == 0 && al16(dmz) && al16(dSz) && al16(mw);
+  if (v4) return run_gemm<PROD_SHARED_B, LD_STR_K4, LD_STR_K4>(g, 1, p, ws, ws_bytes, s, what);
+  return run_gemm<PROD_SHARED_B, LD_STR_K_S, LD_STR_K_S>(g, 1, p, ws, ws_bytes, s, what);
 }
 
 extern "C" int64_t tagi_linear_wgrad_ws_bytes(int64_t M, int64_t K, int64_t N) {
@@ -79,8 +93,8 @@ extern "C" int tagi_linear_wgrad(const float* ma, const float* dmz, const float*
   Plan p = linear_wgrad_plan(M, K, N);
   if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, K + 1, N, 1)))
     p = choose_plan(K + 1, N, M, 1, 2, false, 1);
-  // the plan was made for K+1 rows; tiles_m must follow the actual row count
   p.tiles_m = (int)cdiv(g.R, kCfg[p.cfg].BM);
-  return run_gemm<PROD_SHARED_A, LD_STRIDED_MN, LD_STRIDED_MN>(g, 1, p, ws, ws_bytes, s, what);
+  const bool v4 = K % 4 == 0 && N % 4 == 0 && al16(ma) && al16(dmz) && al16(dSz);
+  if (v4) return run_gemm<PROD_SHARED_A, LD_STR_MN4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
+  return run_gemm<PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
 }
-

@@ -7,80 +7,133 @@
 
 namespace tagi {
 
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  // 256-thread block: wave reduction, then across the 4 waves through LDS.
+
+// BatchNorm2D on channels-last data: a (rows = N*H*W) x C matrix, channel = column.
+// Blocks own contiguous row ranges; in the float4 path each thread keeps one group of 4
+// channels for the whole block (C divides 1024), so per-channel constants and partial
+// sums stay in registers and every load is a coalesced float4.
+static inline int bn_blocks(int64_t rows, int64_t C) {
+  int64_t b = cdiv(rows * C, 32768);
+  if (b > 1024) b = 1024;
+  if (b > rows) b = rows;
+  return (int)(b < 1 ? 1 : b);
+}
+
+static inline bool bn_vec(int64_t C) { return C % 4 == 0 && C <= 1024 && 1024 % C == 0; }
+
+template <int NQ, bool VEC>
+__global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict__ x0, const float* __restrict__ x1,
+                                                        const float* __restrict__ x2, float* __restrict__ ws,
+                                                        int64_t rows, int C, int nblk, int mode,
+                                                        const float* __restrict__ var, const float* __restrict__ mg,
+                                                        float* __restrict__ y0, float* __restrict__ y1, float eps) {
+  // mode 0 (stats):    x0 = mu, x1 = S;            sums mu, S, mu^2
+  // mode 1 (backward): x0 = dmu, x1 = dS, x2 = mhat; sums dmu mhat, dS mhat^2, dmu, dS, and
+  //                    writes y0 = dmu g/sqrt(var+eps), y1 = dS g^2/(var+eps)
+  __shared__ float red[256 * 4 * NQ];
+  const int64_t r0 = rows * blockIdx.x / nblk, r1 = rows * (blockIdx.x + 1) / nblk;
+  const int t = threadIdx.x;
+  if constexpr (VEC) {
+    const int cq = C >> 2, rpi = 256 / cq;
+    const int c4 = t % cq, rr = t / cq;
+    float acc[4][NQ];
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  float t = 0.f;
-  const int nw = blockDim.x >> 6;
-  for (int i = 0; i < nw; ++i) t += red[i];
-  return t;
-}
-
-// Split of the N images of one channel over `splits` blocks.
-static inline int bn_splits(int64_t N, int64_t C, int64_t HW) {
-  int64_t per_channel = N * HW;
-  int64_t want = cdiv(2048, C);  // aim for >= 2048 blocks in total
-  int64_t by_size = cdiv(per_channel, 8192);
-  int64_t sp = want < by_size ? want : by_size;
-  if (sp > N) sp = N;
-  if (sp < 1) sp = 1;
-  return (int)sp;
-}
-
-// ----------------------------------------------------------------- BN statistics
-// grid (C, splits); block sums mu, S, mu^2 over its slice of images of channel c.
-__global__ void __launch_bounds__(256) bn_stats_partial_kernel(const float* __restrict__ mz,
-                                                               const float* __restrict__ Sz, float* __restrict__ ws,
-                                                               int N, int C, int HW, int splits) {
-  __shared__ float red[4];
-  const int c = blockIdx.x, sp = blockIdx.y;
-  const int n0 = (int)((int64_t)N * sp / splits), n1 = (int)((int64_t)N * (sp + 1) / splits);
-  float a = 0.f, b = 0.f, q = 0.f;
-  for (int n = n0; n < n1; ++n) {
-    const float* pm = mz + ((int64_t)n * C + c) * HW;
-    const float* ps = Sz + ((int64_t)n * C + c) * HW;
-    if ((HW & 3) == 0 && (((uintptr_t)pm | (uintptr_t)ps) & 15) == 0) {
-      for (int i = threadIdx.x; i < (HW >> 2); i += blockDim.x) {
-        const float4 m = reinterpret_cast<const float4*>(pm)[i];
-        const float4 s = reinterpret_cast<const float4*>(ps)[i];
-        a += (m.x + m.y) + (m.z + m.w);
-        b += (s.x + s.y) + (s.z + s.w);
-        q += (m.x * m.x + m.y * m.y) + (m.z * m.z + m.w * m.w);
-      }
-    } else {
-      for (int i = threadIdx.x; i < HW; i += blockDim.x) {
-        const float m = pm[i];
-        a += m;
-        b += ps[i];
-        q += m * m;
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) acc[j][q] = 0.f;
+    float km[4] = {0, 0, 0, 0}, kS[4] = {0, 0, 0, 0};
+    if (mode == 1) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = 4 * c4 + j;
+        const float rv = var[c] + eps;
+        km[j] = mg[c] * (1.0f / sqrtf(rv));
+        kS[j] = mg[c] * mg[c] * (1.0f / rv);
       }
     }
-  }
-  a = block_sum(a, red);
-  b = block_sum(b, red);
-  q = block_sum(q, red);
-  if (threadIdx.x == 0) {
-    float* o = ws + ((int64_t)c * splits + sp) * 3;
-    o[0] = a;
-    o[1] = b;
-    o[2] = q;
+    if (rr < rpi) {
+      for (int64_t row = r0 + rr; row < r1; row += rpi) {
+        const int64_t off = row * C + 4 * c4;
+        const float4 a = *reinterpret_cast<const float4*>(x0 + off);
+        const float4 b = *reinterpret_cast<const float4*>(x1 + off);
+        const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+        if (mode == 0) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[j][0] += av[j];
+            acc[j][1] += bv[j];
+            acc[j][2] += av[j] * av[j];
+          }
+        } else {
+          const float4 h = *reinterpret_cast<const float4*>(x2 + off);
+          const float hv[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[j][0] += av[j] * hv[j];
+            acc[j][1] += bv[j] * hv[j] * hv[j];
+            acc[j][2] += av[j];
+            if constexpr (NQ == 4) acc[j][3] += bv[j];
+          }
+          *reinterpret_cast<float4*>(y0 + off) = make_float4(a.x * km[0], a.y * km[1], a.z * km[2], a.w * km[3]);
+          *reinterpret_cast<float4*>(y1 + off) = make_float4(b.x * kS[0], b.y * kS[1], b.z * kS[2], b.w * kS[3]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) red[(t * 4 + j) * NQ + q] = acc[j][q];
+    __syncthreads();
+    for (int c = t; c < C; c += 256) {
+      const int g4 = c >> 2, j = c & 3;
+      for (int q = 0; q < NQ; ++q) {
+        float sum = 0.f;
+        for (int r = 0; r < rpi; ++r) sum += red[((r * cq + g4) * 4 + j) * NQ + q];
+        ws[((int64_t)blockIdx.x * C + c) * NQ + q] = sum;
+      }
+    }
+  } else {
+    for (int c = t; c < C; c += 256) {
+      float acc[NQ];
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) acc[q] = 0.f;
+      float kmc = 0.f, kSc = 0.f;
+      if (mode == 1) {
+        const float rv = var[c] + eps;
+        kmc = mg[c] * (1.0f / sqrtf(rv));
+        kSc = mg[c] * mg[c] * (1.0f / rv);
+      }
+      for (int64_t row = r0; row < r1; ++row) {
+        const int64_t off = row * C + c;
+        const float a = x0[off], b = x1[off];
+        if (mode == 0) {
+          acc[0] += a;
+          acc[1] += b;
+          acc[2] += a * a;
+        } else {
+          const float h = x2[off];
+          acc[0] += a * h;
+          acc[1] += b * h * h;
+          acc[2] += a;
+          if constexpr (NQ == 4) acc[3] += b;
+          y0[off] = a * kmc;
+          y1[off] = b * kSc;
+        }
+      }
+      for (int q = 0; q < NQ; ++q) ws[((int64_t)blockIdx.x * C + c) * NQ + q] = acc[q];
+    }
   }
 }
 
 __global__ void bn_stats_finalize_kernel(const float* __restrict__ ws, float* __restrict__ bmean,
                                          float* __restrict__ bvar, float* __restrict__ rmean,
-                                         float* __restrict__ rvar, float* __restrict__ mg, int C, int splits,
+                                         float* __restrict__ rvar, float* __restrict__ mg, int C, int nblk,
                                          double n, float momentum, float eps, int first_call, int preserve_var) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= C) return;
   float a = 0.f, b = 0.f, q = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    const float* p = ws + ((int64_t)c * splits + s) * 3;
+  for (int s = 0; s < nblk; ++s) {
+    const float* p = ws + ((int64_t)s * C + c) * 3;
     a += p[0];
     b += p[1];
     q += p[2];
@@ -109,33 +162,35 @@ __global__ void bn_fwd_kernel(const float* __restrict__ mz, const float* __restr
                               const float* __restrict__ mg, const float* __restrict__ Sg,
                               const float* __restrict__ mb, const float* __restrict__ Sb, float* __restrict__ ma,
                               float* __restrict__ Sa, float* __restrict__ mhat, float* __restrict__ Shat, int64_t total,
-                              int C, int HW, float eps, bool vec) {
+                              int C, float eps, bool vec) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   if (vec) {
     const int64_t t4 = total >> 2;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < t4; i += stride) {
-      const int c = (int)(((i << 2) / HW) % C);
-      const float rv = var[c] + eps;
-      const float inv_std = 1.0f / sqrtf(rv);
-      const float mu = mean[c], g = mg[c], sg = Sg[c], b = mb[c], sb = Sb[c];
+      const int c0 = (int)((i << 2) % C);
       const float4 m = reinterpret_cast<const float4*>(mz)[i];
       const float4 s = reinterpret_cast<const float4*>(Sz)[i];
-      float4 mh, sh, om, os;
-#define BNF(X)                                           \
-  mh.X = (m.X - mu) * inv_std;                           \
-  sh.X = s.X / rv;                                       \
-  om.X = g * mh.X + b;                                   \
-  os.X = g * g * sh.X + sg * mh.X * mh.X + sg * sh.X + sb;
-      BNF(x) BNF(y) BNF(z) BNF(w)
-#undef BNF
-      reinterpret_cast<float4*>(ma)[i] = om;
-      reinterpret_cast<float4*>(Sa)[i] = os;
-      reinterpret_cast<float4*>(mhat)[i] = mh;
-      if (Shat) reinterpret_cast<float4*>(Shat)[i] = sh;
+      const float mv[4] = {m.x, m.y, m.z, m.w}, sv[4] = {s.x, s.y, s.z, s.w};
+      float mh[4], sh[4], om[4], os[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = c0 + j;
+        const float rv = var[c] + eps;
+        const float inv_std = 1.0f / sqrtf(rv);
+        const float g = mg[c], sg = Sg[c];
+        mh[j] = (mv[j] - mean[c]) * inv_std;
+        sh[j] = sv[j] / rv;
+        om[j] = g * mh[j] + mb[c];
+        os[j] = g * g * sh[j] + sg * mh[j] * mh[j] + sg * sh[j] + Sb[c];
+      }
+      reinterpret_cast<float4*>(ma)[i] = make_float4(om[0], om[1], om[2], om[3]);
+      reinterpret_cast<float4*>(Sa)[i] = make_float4(os[0], os[1], os[2], os[3]);
+      reinterpret_cast<float4*>(mhat)[i] = make_float4(mh[0], mh[1], mh[2], mh[3]);
+      if (Shat) reinterpret_cast<float4*>(Shat)[i] = make_float4(sh[0], sh[1], sh[2], sh[3]);
     }
   } else {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-      const int c = (int)((i / HW) % C);
+      const int c = (int)(i % C);
       const float rv = var[c] + eps;
       const float inv_std = 1.0f / sqrtf(rv);
       const float g = mg[c], sg = Sg[c];
@@ -149,53 +204,14 @@ __global__ void bn_fwd_kernel(const float* __restrict__ mz, const float* __restr
   }
 }
 
-// ------------------------------------------------------------------- BN backward
-// grid (C, splits): propagated deltas for the block's slice + 4 partial channel sums.
-__global__ void __launch_bounds__(256) bn_bwd_partial_kernel(
-    const float* __restrict__ dma, const float* __restrict__ dSa, const float* __restrict__ mhat,
-    const float* __restrict__ var, const float* __restrict__ mg, float* __restrict__ dmz, float* __restrict__ dSz,
-    float* __restrict__ ws, int N, int C, int HW, int splits, float eps) {
-  __shared__ float red[4];
-  const int c = blockIdx.x, sp = blockIdx.y;
-  const int n0 = (int)((int64_t)N * sp / splits), n1 = (int)((int64_t)N * (sp + 1) / splits);
-  const float rv = var[c] + eps;
-  const float g = mg[c];
-  const float km = g * (1.0f / sqrtf(rv));
-  const float kS = g * g * (1.0f / rv);
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  for (int n = n0; n < n1; ++n) {
-    const int64_t base = ((int64_t)n * C + c) * HW;
-    for (int i = threadIdx.x; i < HW; i += blockDim.x) {
-      const float dm = dma[base + i], ds = dSa[base + i], mh = mhat[base + i];
-      s0 += dm * mh;
-      s1 += ds * mh * mh;
-      s2 += dm;
-      s3 += ds;
-      dmz[base + i] = dm * km;
-      dSz[base + i] = ds * kS;
-    }
-  }
-  s0 = block_sum(s0, red);
-  s1 = block_sum(s1, red);
-  s2 = block_sum(s2, red);
-  s3 = block_sum(s3, red);
-  if (threadIdx.x == 0) {
-    float* o = ws + ((int64_t)c * splits + sp) * 4;
-    o[0] = s0;
-    o[1] = s1;
-    o[2] = s2;
-    o[3] = s3;
-  }
-}
-
 __global__ void bn_bwd_finalize_kernel(const float* __restrict__ ws, const float* __restrict__ Sg,
                                        const float* __restrict__ Sb, float* __restrict__ dmg, float* __restrict__ dSg,
-                                       float* __restrict__ dmb, float* __restrict__ dSb, int C, int splits) {
+                                       float* __restrict__ dmb, float* __restrict__ dSb, int C, int nblk) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= C) return;
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    const float* p = ws + ((int64_t)c * splits + s) * 4;
+  for (int s = 0; s < nblk; ++s) {
+    const float* p = ws + ((int64_t)s * C + c) * 4;
     s0 += p[0];
     s1 += p[1];
     s2 += p[2];
@@ -371,8 +387,10 @@ static inline hipStream_t as_stream(tagi_stream_t s) { return (hipStream_t)s; }
 
 extern "C" int64_t tagi_bn_stats_ws_bytes(int64_t N, int64_t C, int64_t HW) {
   if (N <= 0 || C <= 0 || HW <= 0) return 0;
-  return (int64_t)C * bn_splits(N, C, HW) * 3 * (int64_t)sizeof(float);
+  return (int64_t)bn_blocks(N * HW, C) * C * 3 * (int64_t)sizeof(float);
 }
+
+static inline bool al16p(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 extern "C" int tagi_bn_stats(const float* mz, const float* Sz, float* batch_mean, float* batch_var,
                              float* running_mean, float* running_var, float* mg, int64_t N, int64_t C, int64_t HW,
@@ -381,17 +399,22 @@ extern "C" int tagi_bn_stats(const float* mz, const float* Sz, float* batch_mean
   const char* what = "tagi_bn_stats";
   TAGI_REQUIRE(mz && Sz && batch_mean && batch_var && ws, "%s: null pointer", what);
   TAGI_REQUIRE(N > 0 && C > 0 && HW > 0 && N * HW > 1, "%s: bad sizes", what);
-  TAGI_REQUIRE(N * C * HW < (1ll << 40) && C < 65536, "%s: too large", what);
+  TAGI_REQUIRE(N * C * HW < (1ll << 40), "%s: too large", what);
   TAGI_REQUIRE(ws_bytes >= tagi_bn_stats_ws_bytes(N, C, HW), "%s: workspace too small", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_BN_STATS, s, 0.0, 8.0 * N * C * HW);
-  const int sp = bn_splits(N, C, HW);
-  hipLaunchKernelGGL(bn_stats_partial_kernel, dim3((unsigned)C, (unsigned)sp), dim3(256), 0, s, mz, Sz, ws, (int)N,
-                     (int)C, (int)HW, sp);
+  const int64_t rows = N * HW;
+  const int nblk = bn_blocks(rows, C);
+  if (bn_vec(C) && al16p(mz) && al16p(Sz))
+    hipLaunchKernelGGL((bn_reduce_kernel<3, true>), dim3(nblk), dim3(256), 0, s, mz, Sz, nullptr, ws, rows, (int)C,
+                       nblk, 0, nullptr, nullptr, nullptr, nullptr, 0.f);
+  else
+    hipLaunchKernelGGL((bn_reduce_kernel<3, false>), dim3(nblk), dim3(256), 0, s, mz, Sz, nullptr, ws, rows, (int)C,
+                       nblk, 0, nullptr, nullptr, nullptr, nullptr, 0.f);
   int rc = check_launch(what);
   if (rc) return rc;
   hipLaunchKernelGGL(bn_stats_finalize_kernel, dim3((unsigned)cdiv(C, 256)), dim3(256), 0, s, (const float*)ws,
-                     batch_mean, batch_var, running_mean, running_var, mg, (int)C, sp, (double)(N * HW), momentum, eps,
+                     batch_mean, batch_var, running_mean, running_var, mg, (int)C, nblk, (double)rows, momentum, eps,
                      first_call, preserve_var);
   return check_launch(what);
 }
@@ -405,16 +428,16 @@ extern "C" int tagi_bn_fwd(const float* mz, const float* Sz, const float* mean, 
   hipStream_t s = as_stream(stream);
   const int64_t total = N * C * HW;
   ProfScope ps(FAM_BN_FWD, s, 0.0, 4.0 * total * (Shat ? 6 : 5));
-  const bool vec = (HW % 4 == 0) && ((((uintptr_t)mz | (uintptr_t)Sz | (uintptr_t)ma | (uintptr_t)Sa |
-                                       (uintptr_t)mhat | (uintptr_t)(Shat ? Shat : ma)) & 15) == 0);
+  const bool vec = (C % 4 == 0) && al16p(mz) && al16p(Sz) && al16p(ma) && al16p(Sa) && al16p(mhat) &&
+                   (Shat == nullptr || al16p(Shat));
   hipLaunchKernelGGL(bn_fwd_kernel, dim3(ew_blocks(vec ? total / 4 : total, 256)), dim3(256), 0, s, mz, Sz, mean, var,
-                     mg, Sg, mb, Sb, ma, Sa, mhat, Shat, total, (int)C, (int)HW, eps, vec);
+                     mg, Sg, mb, Sb, ma, Sa, mhat, Shat, total, (int)C, eps, vec);
   return check_launch(what);
 }
 
 extern "C" int64_t tagi_bn_bwd_ws_bytes(int64_t N, int64_t C, int64_t HW) {
   if (N <= 0 || C <= 0 || HW <= 0) return 0;
-  return (int64_t)C * bn_splits(N, C, HW) * 4 * (int64_t)sizeof(float);
+  return (int64_t)bn_blocks(N * HW, C) * C * 4 * (int64_t)sizeof(float);
 }
 
 extern "C" int tagi_bn_bwd(const float* dma, const float* dSa, const float* mhat, const float* var, const float* mg,
@@ -424,17 +447,23 @@ extern "C" int tagi_bn_bwd(const float* dma, const float* dSa, const float* mhat
   const char* what = "tagi_bn_bwd";
   TAGI_REQUIRE(dma && dSa && mhat && var && mg && Sg && Sb && dmz && dSz && dmg && dSg && dmb && dSb && ws,
                "%s: null pointer", what);
-  TAGI_REQUIRE(N > 0 && C > 0 && HW > 0 && C < 65536, "%s: bad sizes", what);
+  TAGI_REQUIRE(N > 0 && C > 0 && HW > 0, "%s: bad sizes", what);
   TAGI_REQUIRE(ws_bytes >= tagi_bn_bwd_ws_bytes(N, C, HW), "%s: workspace too small", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_BN_BWD, s, 0.0, 20.0 * N * C * HW);
-  const int sp = bn_splits(N, C, HW);
-  hipLaunchKernelGGL(bn_bwd_partial_kernel, dim3((unsigned)C, (unsigned)sp), dim3(256), 0, s, dma, dSa, mhat, var, mg,
-                     dmz, dSz, ws, (int)N, (int)C, (int)HW, sp, eps);
+  const int64_t rows = N * HW;
+  const int nblk = bn_blocks(rows, C);
+  const bool vec = bn_vec(C) && al16p(dma) && al16p(dSa) && al16p(mhat) && al16p(dmz) && al16p(dSz);
+  if (vec)
+    hipLaunchKernelGGL((bn_reduce_kernel<4, true>), dim3(nblk), dim3(256), 0, s, dma, dSa, mhat, ws, rows, (int)C,
+                       nblk, 1, var, mg, dmz, dSz, eps);
+  else
+    hipLaunchKernelGGL((bn_reduce_kernel<4, false>), dim3(nblk), dim3(256), 0, s, dma, dSa, mhat, ws, rows, (int)C,
+                       nblk, 1, var, mg, dmz, dSz, eps);
   int rc = check_launch(what);
   if (rc) return rc;
   hipLaunchKernelGGL(bn_bwd_finalize_kernel, dim3((unsigned)cdiv(C, 256)), dim3(256), 0, s, (const float*)ws, Sg, Sb,
-                     dmg, dSg, dmb, dSb, (int)C, sp);
+                     dmg, dSg, dmb, dSb, (int)C, nblk);
   return check_launch(what);
 }
 

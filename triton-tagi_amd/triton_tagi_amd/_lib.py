@@ -56,14 +56,16 @@ _SIGS = {
     "tagi_prof_end": (c_int, [P, P, P, P]),
     "tagi_linear_fwd": (c_int, [P, P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
     "tagi_linear_fwd_ws_bytes": (I64, [I64, I64, I64]),
-    "tagi_linear_bwd_delta": (c_int, [P, P, P, P, P, I64, I64, I64, P]),
+    "tagi_linear_bwd_delta": (c_int, [P, P, P, P, P, I64, I64, I64, P, I64, P]),
+    "tagi_linear_bwd_delta_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_linear_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
     "tagi_linear_wgrad_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_bmm_tagi": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, P]),
     "tagi_bmm_shared": (c_int, [P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),
     "tagi_conv2d_fwd": (c_int, [P, P, P, P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_fwd_ws_bytes": (I64, [GP]),
-    "tagi_conv2d_bwd_delta": (c_int, [P, P, P, P, P, GP, P]),
+    "tagi_conv2d_bwd_delta": (c_int, [P, P, P, P, P, GP, P, I64, P]),
+    "tagi_conv2d_bwd_delta_ws_bytes": (I64, [GP]),
     "tagi_conv2d_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_wgrad_ws_bytes": (I64, [GP]),
     "tagi_relu_fwd": (c_int, [P, P, P, P, P, I64, P]),
@@ -147,9 +149,37 @@ def check(t: torch.Tensor, name: str, contiguous: bool = True) -> torch.Tensor:
         raise ValueError(
             f"{name}: tensor is on {t.device}; the TAGI HIP kernels run on the GPU only"
         )
-    if contiguous and not t.is_contiguous():
-        raise ValueError(f"{name}: tensor must be contiguous")
+    if contiguous and not (t.is_contiguous() or (t.dim() == 4 and t.is_contiguous(memory_format=torch.channels_last))):
+        raise ValueError(f"{name}: tensor must be dense (contiguous or channels-last)")
     return t
+
+
+def dense(t: torch.Tensor) -> torch.Tensor:
+    """t itself when its storage is dense in its own dim order (row-major or channels-last)."""
+    if t.is_contiguous() or (t.dim() == 4 and t.is_contiguous(memory_format=torch.channels_last)):
+        return t
+    return t.contiguous()
+
+
+def channels_last(t: torch.Tensor) -> torch.Tensor:
+    """4-D tensor in channels-last storage (a copy only when it is not already)."""
+    if t.is_contiguous(memory_format=torch.channels_last):
+        return t
+    return t.contiguous(memory_format=torch.channels_last)
+
+
+def like(t: torch.Tensor, ref: torch.Tensor) -> torch.Tensor:
+    """t with the same storage order as ref (elementwise kernels walk raw storage)."""
+    t = dense(t)
+    if t.stride() == ref.stride():
+        return t
+    if ref.dim() == 4 and ref.is_contiguous(memory_format=torch.channels_last):
+        return t.contiguous(memory_format=torch.channels_last)
+    return t.contiguous()
+
+
+def empty_cl(N: int, C: int, H: int, W: int, device) -> torch.Tensor:
+    return torch.empty((N, C, H, W), device=device, dtype=torch.float32, memory_format=torch.channels_last)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -57,8 +57,10 @@ def fused_backward_delta(dmz, dSz, mw):
         raise ValueError(f"fused_backward_delta: dmz {tuple(dmz.shape)} vs mw {tuple(mw.shape)}")
     dma = torch.empty(M, K, device=dmz.device, dtype=torch.float32)
     dSa = torch.empty(M, K, device=dmz.device, dtype=torch.float32)
+    ws = _lib.workspace(_lib.query("tagi_linear_bwd_delta_ws_bytes", M, K, N), dmz.device)
+    wp, wb = _lib.ws_args(ws)
     _lib.call("tagi_linear_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), mw.data_ptr(), dma.data_ptr(),
-              dSa.data_ptr(), M, K, N, _lib.stream_of(dmz))
+              dSa.data_ptr(), M, K, N, wp, wb, _lib.stream_of(dmz))
     return dma, dSa
 
 

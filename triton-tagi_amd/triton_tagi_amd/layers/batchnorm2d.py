@@ -8,7 +8,7 @@ preserve_var, sets gamma := sqrt(var + eps)); later calls apply an EMA with mome
     mu_out = g mhat + b,  S_out = g^2 Shat + Sg (mhat^2 + Shat) + Sb
 Backward: delta_mz = delta_mu g/sqrt(var+eps), delta_Sz = delta_S g^2/(var+eps), and
 delta_g = Sg sum(delta_mu mhat), delta_Sg = Sg^2 sum(delta_S mhat^2), delta_b = Sb sum
-delta_mu, delta_Sb = Sb^2 sum delta_S (sums over N, H, W).
+delta_mu, delta_Sb = Sb^2 sum delta_S (sums over N, H, W). Activations are kept channels-last.
 """
 
 from __future__ import annotations
@@ -51,8 +51,8 @@ class BatchNorm2D(LearnableLayer):
         self.training = False
 
     def forward(self, mz: Tensor, Sz: Tensor) -> tuple[Tensor, Tensor]:
-        mz = _lib.check(mz.contiguous(), "mz")
-        Sz = _lib.check(Sz.contiguous(), "Sz")
+        mz = _lib.check(_lib.channels_last(mz), "mz")
+        Sz = _lib.check(_lib.channels_last(Sz), "Sz")
         self.input_shape = mz.shape
         N, C, H, W = mz.shape
         if C != self.num_features:
@@ -84,8 +84,8 @@ class BatchNorm2D(LearnableLayer):
         return ma, Sa
 
     def backward(self, delta_ma: Tensor, delta_Sa: Tensor) -> tuple[Tensor, Tensor]:
-        dma = _lib.check(delta_ma.contiguous(), "delta_ma")
-        dSa = _lib.check(delta_Sa.contiguous(), "delta_Sa")
+        dma = _lib.check(_lib.channels_last(delta_ma.reshape(self.input_shape)), "delta_ma")
+        dSa = _lib.check(_lib.channels_last(delta_Sa.reshape(self.input_shape)), "delta_Sa")
         N, C, H, W = self.input_shape
         HW = H * W
         dev = dma.device

@@ -7,7 +7,8 @@ tensors inside the kernels:
     input delta  fold(delta_z @ mw^T) as a transposed implicit GEMM (no col2im)
     deltas       delta_mw = Sw * P^T @ delta_mz, delta_Sw = Sw^2 * (P^2)^T @ delta_Sz (+ bias)
 padding_type 1 pads p on every side; padding_type 2 pads p on the right/bottom only
-(conv2d.py:280-291).
+(conv2d.py:280-291). Activations and deltas are kept channels-last (NHWC storage of the
+(N, C, H, W) tensors) so every patch row the kernels gather is a contiguous run of channels.
 """
 
 from __future__ import annotations
@@ -56,15 +57,15 @@ class Conv2D(LearnableLayer):
     def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
         if ma.dim() != 4 or ma.shape[1] != self.C_in:
             raise ValueError(f"Conv2D: expected (N, {self.C_in}, H, W), got {tuple(ma.shape)}")
-        ma = _lib.check(ma.contiguous(), "ma")
-        Sa = _lib.check(Sa.contiguous(), "Sa")
+        ma = _lib.check(_lib.channels_last(ma), "ma")
+        Sa = _lib.check(_lib.channels_last(Sa), "Sa")
         N, C, H, W = ma.shape
         self.input_shape = (N, C, H, W)
         g = self._geom(N, C, H, W)
         self.spatial = (g.Ho, g.Wo)
         self.ma_in = ma
-        mz = torch.empty(N, self.C_out, g.Ho, g.Wo, device=ma.device, dtype=torch.float32)
-        Sz = torch.empty_like(mz)
+        mz = _lib.empty_cl(N, self.C_out, g.Ho, g.Wo, ma.device)
+        Sz = _lib.empty_cl(N, self.C_out, g.Ho, g.Wo, ma.device)
         ws = _lib.workspace(_lib.query("tagi_conv2d_fwd_ws_bytes", g), ma.device)
         wp, wb = _lib.ws_args(ws)
         _lib.call("tagi_conv2d_fwd", ma.data_ptr(), Sa.data_ptr(), self.mw.data_ptr(), self.Sw.data_ptr(),
@@ -73,10 +74,10 @@ class Conv2D(LearnableLayer):
         return mz, Sz
 
     def backward(self, delta_mz: Tensor, delta_Sz: Tensor) -> tuple[Tensor, Tensor]:
-        dmz = _lib.check(delta_mz.contiguous(), "delta_mz")
-        dSz = _lib.check(delta_Sz.contiguous(), "delta_Sz")
         N, C, H, W = self.input_shape
         g = self._geom(N, C, H, W)
+        dmz = _lib.check(_lib.channels_last(delta_mz.reshape(N, self.C_out, g.Ho, g.Wo)), "delta_mz")
+        dSz = _lib.check(_lib.channels_last(delta_Sz.reshape(N, self.C_out, g.Ho, g.Wo)), "delta_Sz")
         if tuple(dmz.shape) != (N, self.C_out, g.Ho, g.Wo):
             raise ValueError(f"Conv2D.backward: delta shape {tuple(dmz.shape)} != output shape")
         dev = dmz.device
@@ -91,10 +92,12 @@ class Conv2D(LearnableLayer):
         _lib.call("tagi_conv2d_wgrad", self.ma_in.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), self.Sw.data_ptr(),
                   self.Sb.data_ptr(), self.delta_mw.data_ptr(), self.delta_Sw.data_ptr(), self.delta_mb.data_ptr(),
                   self.delta_Sb.data_ptr(), g, wp, wb, st)
-        d_ma = torch.empty(N, C, H, W, device=dev, dtype=torch.float32)
-        d_Sa = torch.empty_like(d_ma)
+        d_ma = _lib.empty_cl(N, C, H, W, dev)
+        d_Sa = _lib.empty_cl(N, C, H, W, dev)
+        ws = _lib.workspace(_lib.query("tagi_conv2d_bwd_delta_ws_bytes", g), dev)
+        wp, wb = _lib.ws_args(ws)
         _lib.call("tagi_conv2d_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), self.mw.data_ptr(), d_ma.data_ptr(),
-                  d_Sa.data_ptr(), g, st)
+                  d_Sa.data_ptr(), g, wp, wb, st)
         return d_ma, d_Sa
 
     def _update_items(self):

@@ -18,8 +18,8 @@ from ..base import Layer
 
 def bayesian_relu(mz, Sz):
     """(ma, Sa, J) of max(0, z), z ~ N(mz, Sz), elementwise (relu.py:94-122)."""
-    mz = _lib.check(mz.contiguous(), "mz")
-    Sz = _lib.check(Sz.contiguous(), "Sz")
+    mz = _lib.check(_lib.dense(mz), "mz")
+    Sz = _lib.check(_lib.like(Sz, mz), "Sz")
     if Sz.shape != mz.shape:
         raise ValueError("bayesian_relu: mz and Sz shapes differ")
     ma, Sa, J = torch.empty_like(mz), torch.empty_like(mz), torch.empty_like(mz)
@@ -30,8 +30,8 @@ def bayesian_relu(mz, Sz):
 
 def jacobian_backward(delta_m, delta_S, J):
     """(delta_m * J, delta_S * J^2), one HIP launch."""
-    dm = _lib.check(delta_m.contiguous(), "delta_m")
-    dS = _lib.check(delta_S.contiguous(), "delta_S")
+    dm = _lib.check(_lib.like(delta_m.reshape(J.shape), J), "delta_m")
+    dS = _lib.check(_lib.like(delta_S.reshape(J.shape), J), "delta_S")
     if dm.numel() != J.numel() or dS.numel() != J.numel():
         raise ValueError(f"Jacobian backward: delta {tuple(dm.shape)} vs stored Jacobian {tuple(J.shape)}")
     om, oS = torch.empty_like(dm), torch.empty_like(dS)

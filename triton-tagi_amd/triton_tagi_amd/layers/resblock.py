@@ -24,9 +24,11 @@ from .relu import ReLU
 def add_shortcut(mu_s, var_s, mu_a, var_a) -> None:
     """In place: mu_a += mu_s, var_a += var_s (resblock.py:138-154)."""
     assert mu_s.shape == mu_a.shape, f"Shape mismatch: shortcut={mu_s.shape} vs output={mu_a.shape}"
-    mu_s = _lib.check(mu_s.contiguous(), "mu_s")
-    var_s = _lib.check(var_s.contiguous(), "var_s")
     _lib.check(mu_a, "mu_a"), _lib.check(var_a, "var_a")
+    if var_a.stride() != mu_a.stride():
+        raise ValueError("add_shortcut: mu_a and var_a must share one storage order")
+    mu_s = _lib.check(_lib.like(mu_s, mu_a), "mu_s")
+    var_s = _lib.check(_lib.like(var_s, mu_a), "var_s")
     _lib.call("tagi_add_inplace", mu_s.data_ptr(), var_s.data_ptr(), mu_a.data_ptr(), var_a.data_ptr(),
               mu_s.numel(), _lib.stream_of(mu_a))
 
