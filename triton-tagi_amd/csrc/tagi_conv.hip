@@ -78,7 +78,7 @@ static Plan conv_bwd_plan(const tagi_conv_geom* g) {
 }
 
 static Plan conv_wgrad_plan(const tagi_conv_geom* g) {
-  return choose_plan(g->C * g->k * g->k + 1, g->Cout, g->N * g->Ho * g->Wo, 1, 2, true, 64);
+  return choose_plan(g->C * g->k * g->k + 1, g->Cout, g->N * g->Ho * g->Wo, 1, 2, true, 512);
 }
 
 static int64_t wt_floats(const tagi_conv_geom* g) { return ((g->C * g->k * g->k * g->Cout) + 3) / 4 * 4; }

@@ -39,8 +39,11 @@ __device__ __forceinline__ void relu_moments(float mz, float Sz, float& ma, floa
   // Phi(alpha) = 0.5 (1 + erf(alpha/sqrt2)) evaluated as 0.5 erfc(-alpha/sqrt2): equal in
   // exact arithmetic, without the fp32 cancellation of the erf form for alpha < 0.
   const bool asym = alpha < -5.0f;
-  const float cdf = asym ? pdf / (-alpha) : 0.5f * erfcf(-alpha * INV_SQRT_2);
-  const float Q = asym ? 1.0f - cdf : 0.5f * erfcf(alpha * INV_SQRT_2);
+  // one erfc gives the smaller tail; the other side is its complement (no cancellation)
+  const float tail = 0.5f * erfcf(fabsf(alpha) * INV_SQRT_2);
+  const float cdf_e = alpha >= 0.0f ? 1.0f - tail : tail;
+  const float cdf = asym ? pdf / (-alpha) : cdf_e;
+  const float Q = asym ? 1.0f - cdf : (alpha >= 0.0f ? tail : 1.0f - tail);
   ma = sig * pdf + mz * cdf;
   Sa = fmaxf(rect_var(Ss, alpha, pdf, cdf, Q), 0.0f);
   J = cdf;

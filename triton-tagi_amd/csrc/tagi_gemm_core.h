@@ -20,6 +20,8 @@
 #pragma once
 #include <float.h>
 
+#include <type_traits>
+
 #include "tagi_common.h"
 
 namespace tagi {
@@ -125,6 +127,8 @@ template <int BM_, int BN_, int WM_, int WN_>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, BK = 16;
   static constexpr int NTH = (BM / WM) * (BN / WN) * 64;
+  // blocks per CU the register budget is sized for (2 x 256-thread blocks = 2 waves/SIMD)
+  static constexpr int MINB = NTH >= 512 ? 1 : 2;
 };
 
 // ------------------------------------------------------------------------------------
@@ -141,11 +145,19 @@ struct Loader {
   static_assert(NC * W * NTH == BMN * BK, "tile does not split evenly over threads");
   static constexpr int LD = BMN + 4;
 
-  float4 v[NT][NC];
+  using Vt = typename std::conditional<V4, float4, float>::type;
+  static constexpr bool CONV_ROWS = (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S || KIND == LD_CBWD_A4 ||
+                                     KIND == LD_CBWD_A_S);
+  static constexpr bool CONV_R = CONV_ROWS || KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CWG_A4 ||
+                                 KIND == LD_CWG_A_S;
+  static constexpr int NRB = CONV_ROWS ? NC : 1;  // per-chunk row bases only where rows differ
+  static constexpr int NR = CONV_R ? NC : 1;
+
+  Vt v[NT][NC];
   int mnmax, kmax;           // extents checked by fetch (per phase for the conv input delta)
   int cmn[NC], ck[NC];       // chunk origin within the tile
-  int64_t rowbase[NC];       // per-chunk row invariant (conv kinds)
-  int r0[NC], r1[NC], r2[NC];
+  int64_t rowbase[NRB];      // batch offset (strided kinds) or per-chunk image base (conv rows)
+  int r0[NR], r1[NR], r2[NR];
 
   __device__ __forceinline__ void map(int tid) {
 #pragma unroll
@@ -232,9 +244,7 @@ struct Loader {
         r2[i] = c;
       }
     } else {
-      const int64_t zoff = (z / o.zdiv) * o.sz1 + (z % o.zdiv) * o.sz2;
-#pragma unroll
-      for (int i = 0; i < NC; ++i) rowbase[i] = zoff;
+      rowbase[0] = (z / o.zdiv) * o.sz1 + (z % o.zdiv) * o.sz2;
     }
   }
 
@@ -251,7 +261,7 @@ struct Loader {
       if constexpr (KIND == LD_STR_MN4) {
         if (k < o.K) {
           if (mn < o.MN) {
-            const int64_t off = rowbase[i] + mn + (int64_t)k * o.s_k;
+            const int64_t off = rowbase[0] + mn + (int64_t)k * o.s_k;
             a = ld4(o.p0, off);
             if constexpr (NT == 2) b = ld4(o.p1, off);
           } else if (mn == o.ones_row) {
@@ -260,14 +270,14 @@ struct Loader {
         }
       } else if constexpr (KIND == LD_STR_K4) {
         if (mn < o.MN && k < o.K) {
-          const int64_t off = rowbase[i] + (int64_t)mn * o.s_mn + k;
+          const int64_t off = rowbase[0] + (int64_t)mn * o.s_mn + k;
           a = ld4(o.p0, off);
           if constexpr (NT == 2) b = ld4(o.p1, off);
         }
       } else if constexpr (KIND == LD_STR_MN_S || KIND == LD_STR_K_S) {
         if (k < o.K) {
           if (mn < o.MN) {
-            const int64_t off = rowbase[i] + (int64_t)mn * o.s_mn + (int64_t)k * o.s_k;
+            const int64_t off = rowbase[0] + (int64_t)mn * o.s_mn + (int64_t)k * o.s_k;
             a.x = o.p0[off];
             if constexpr (NT == 2) b.x = o.p1[off];
           } else if (mn == o.ones_row) {
@@ -357,8 +367,13 @@ struct Loader {
           }
         }
       }
-      v[0][i] = a;
-      if constexpr (NT == 2) v[1][i] = b;
+      if constexpr (V4) {
+        v[0][i] = a;
+        if constexpr (NT == 2) v[1][i] = b;
+      } else {
+        v[0][i] = a.x;
+        if constexpr (NT == 2) v[1][i] = b.x;
+      }
     }
   }
 
@@ -368,9 +383,9 @@ struct Loader {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         float* st = s + t * BK * LD;
-        const float4 x = v[t][i];
+        const Vt x = v[t][i];
         if constexpr (!V4) {
-          st[ck[i] * LD + cmn[i]] = x.x;
+          st[ck[i] * LD + cmn[i]] = x;
         } else if constexpr (MNF) {
           *reinterpret_cast<float4*>(st + ck[i] * LD + cmn[i]) = x;
         } else {
@@ -440,7 +455,7 @@ __device__ __forceinline__ int kred_of(const GemmArgs& g, int z) {
 }
 
 template <int PROD, class CFG, int KA, int KB>
-__global__ void __launch_bounds__(CFG::NTH, (CFG::NTH <= 256 ? 2 : 1)) gemm_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   constexpr int BM = CFG::BM, BN = CFG::BN, BK = CFG::BK, WM = CFG::WM, WN = CFG::WN, NTH = CFG::NTH;
   constexpr int NA = (PROD == PROD_SHARED_A) ? 1 : 2;
   constexpr int NB = (PROD == PROD_SHARED_B) ? 1 : 2;
@@ -620,19 +635,17 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ partial, Epi epi,
 // ------------------------------------------------------------------------------------
 // Host side: tile-config choice, split-K choice and launch.
 // ------------------------------------------------------------------------------------
-using C128x128 = Cfg<128, 128, 64, 64>;
-using C256x64 = Cfg<256, 64, 64, 64>;
-using C64x256 = Cfg<64, 256, 64, 64>;
-using C128x64 = Cfg<128, 64, 64, 32>;
-using C64x128 = Cfg<64, 128, 32, 64>;
-using C64x64 = Cfg<64, 64, 32, 32>;
-using C32x32 = Cfg<32, 32, 32, 32>;
+using C128x128 = Cfg<128, 128, 64, 32>;  // 8 waves, 64x32 per wave
+using C128x64 = Cfg<128, 64, 64, 32>;    // 4 waves
+using C64x128 = Cfg<64, 128, 32, 64>;    // 4 waves
+using C64x64 = Cfg<64, 64, 32, 32>;      // 4 waves
+using C32x32 = Cfg<32, 32, 32, 32>;      // 1 wave
 
 struct CfgDesc {
   int BM, BN;
 };
-static const CfgDesc kCfg[] = {{128, 128}, {256, 64}, {64, 256}, {128, 64}, {64, 128}, {64, 64}, {32, 32}};
-static const int kNumCfg = 7;
+static const CfgDesc kCfg[] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}, {32, 32}};
+static const int kNumCfg = 5;
 
 struct Plan {
   int cfg;
@@ -641,28 +654,37 @@ struct Plan {
   int tiles_m, tiles_n;
 };
 
-// Pick the tile shape and split-K factor minimising a simple time model: MFMA time of
-// the busiest wave of blocks (two resident blocks per CU) inflated by the per-tile load
-// overhead, plus the HBM time of the split-K partial round trip.
+// Pick the tile shape and split-K factor minimising a simple time model: the busiest CU
+// holds ceil(blocks / 256) blocks; its MFMA time is inflated by the per-tile load
+// overhead (small tiles re-read more operand bytes per flop) and by low occupancy
+// (fewer than ~3 waves per SIMD leave load latency exposed). Split-K adds the HBM round
+// trip of the partial sums plus one launch.
 static inline Plan choose_plan(int64_t R, int64_t C, int64_t Kred, int64_t batch, int products, bool allow_split,
                                int64_t max_splits) {
-  Plan best{6, 1, (int)Kred, 1, 1};
+  // resident blocks per CU (LDS / register limited) and waves per block, per config
+  static const int kBpc[] = {2, 3, 3, 4, 8};
+  static const int kWaves[] = {8, 4, 4, 4, 1};
+  Plan best{kNumCfg - 1, 1, (int)Kred, 1, 1};
   double best_t = DBL_MAX;
-  const double flops_per_block_s = 157.3e12 / 256.0 / 2.0;
+  const double peak_cu = 157.3e12 / 256.0;
   for (int ci = 0; ci < kNumCfg; ++ci) {
     const int BM = kCfg[ci].BM, BN = kCfg[ci].BN;
     const int64_t tm = cdiv(R, BM), tn = cdiv(C, BN);
-    for (int64_t sp = 1; sp <= 64; sp *= 2) {
+    for (int64_t sp = 1; sp <= 512; sp *= 2) {
       if (sp > 1 && (!allow_split || sp > max_splits)) break;
       int64_t kc = cdiv(cdiv(Kred, sp), 16) * 16;
       if (kc < 16) kc = 16;
       const int64_t actual = cdiv(Kred, kc);
       if (sp > 1 && actual < sp) break;
+      if (sp > 1 && kc < 64) break;  // splits below 4 k-tiles only add reduction traffic
       const int64_t blocks = tm * tn * batch * actual;
-      const int64_t waves = cdiv(blocks, 512);
-      const double eff = 1.0 + 32.0 / BM + 32.0 / BN + (BM * BN < 64 * 64 ? 1.0 : 0.0);
-      double t = waves * (2.0 * BM * BN * kc * products * eff) / flops_per_block_s;
-      if (actual > 1) t += (double)(actual * 2 + 2) * R * C * batch * 4.0 / 5.0e12 + 4e-6;
+      const int64_t rounds = cdiv(blocks, 256);
+      const int64_t resident = rounds < kBpc[ci] ? rounds : kBpc[ci];
+      const double wps = (double)resident * kWaves[ci] / 4.0;  // waves per SIMD
+      const double occ = wps >= 3.0 ? 1.0 : (wps >= 2.0 ? 0.85 : (wps >= 1.0 ? 0.6 : 0.35));
+      const double tile = 1.0 / (1.0 + 32.0 / BM + 32.0 / BN);
+      double t = rounds * (2.0 * BM * BN * kc * products) / (peak_cu * tile * occ);
+      if (actual > 1) t += (double)(actual * 2 + 2) * R * C * batch * 4.0 / 5.0e12 + 5e-6;
       if (t < best_t * 0.999) {
         best_t = t;
         best = Plan{ci, (int)actual, (int)kc, (int)tm, (int)tn};
@@ -704,11 +726,9 @@ static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, 
                (long long)gy);
   switch (p.cfg) {
     case 0: launch_cfg<PROD, C128x128, KA, KB>(g, gx, gy, s); break;
-    case 1: launch_cfg<PROD, C256x64, KA, KB>(g, gx, gy, s); break;
-    case 2: launch_cfg<PROD, C64x256, KA, KB>(g, gx, gy, s); break;
-    case 3: launch_cfg<PROD, C128x64, KA, KB>(g, gx, gy, s); break;
-    case 4: launch_cfg<PROD, C64x128, KA, KB>(g, gx, gy, s); break;
-    case 5: launch_cfg<PROD, C64x64, KA, KB>(g, gx, gy, s); break;
+    case 1: launch_cfg<PROD, C128x64, KA, KB>(g, gx, gy, s); break;
+    case 2: launch_cfg<PROD, C64x128, KA, KB>(g, gx, gy, s); break;
+    case 3: launch_cfg<PROD, C64x64, KA, KB>(g, gx, gy, s); break;
     default: launch_cfg<PROD, C32x32, KA, KB>(g, gx, gy, s); break;
   }
   int rc = check_launch(what);

@@ -7,7 +7,7 @@ static inline hipStream_t as_stream(tagi_stream_t s) { return (hipStream_t)s; }
 
 static Plan linear_fwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, N, K, 1, 3, true, 16); }
 static Plan linear_bwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, K, N, 1, 2, true, 16); }
-static Plan linear_wgrad_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(K + 1, N, M, 1, 2, true, 64); }
+static Plan linear_wgrad_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(K + 1, N, M, 1, 2, true, 512); }
 
 extern "C" int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N) {
   if (M <= 0 || K <= 0 || N <= 0) return 0;

@@ -13,8 +13,8 @@ namespace tagi {
 // channels for the whole block (C divides 1024), so per-channel constants and partial
 // sums stay in registers and every load is a coalesced float4.
 static inline int bn_blocks(int64_t rows, int64_t C) {
-  int64_t b = cdiv(rows * C, 32768);
-  if (b > 1024) b = 1024;
+  int64_t b = cdiv(rows * C, 8192);
+  if (b > 2048) b = 2048;
   if (b > rows) b = rows;
   return (int)(b < 1 ? 1 : b);
 }
@@ -52,6 +52,7 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
       }
     }
     if (rr < rpi) {
+#pragma unroll 4
       for (int64_t row = r0 + rr; row < r1; row += rpi) {
         const int64_t off = row * C + 4 * c4;
         const float4 a = *reinterpret_cast<const float4*>(x0 + off);
@@ -125,19 +126,31 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
   }
 }
 
+// One wavefront per channel: lanes take partials lane, lane+64, ... then a butterfly sum
+// (a fixed order, so the result does not depend on timing).
+__device__ __forceinline__ float wave_reduce(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 __global__ void bn_stats_finalize_kernel(const float* __restrict__ ws, float* __restrict__ bmean,
                                          float* __restrict__ bvar, float* __restrict__ rmean,
                                          float* __restrict__ rvar, float* __restrict__ mg, int C, int nblk,
                                          double n, float momentum, float eps, int first_call, int preserve_var) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= C) return;
+  const int c = blockIdx.x;
+  const int lane = threadIdx.x;
   float a = 0.f, b = 0.f, q = 0.f;
-  for (int s = 0; s < nblk; ++s) {
+  for (int s = lane; s < nblk; s += 64) {
     const float* p = ws + ((int64_t)s * C + c) * 3;
     a += p[0];
     b += p[1];
     q += p[2];
   }
+  a = wave_reduce(a);
+  b = wave_reduce(b);
+  q = wave_reduce(q);
+  if (lane != 0) return;
   const float inv = (float)(1.0 / n);
   const float mean = a * inv;
   const float bessel = (float)(n / (n - 1.0));
@@ -207,16 +220,21 @@ __global__ void bn_fwd_kernel(const float* __restrict__ mz, const float* __restr
 __global__ void bn_bwd_finalize_kernel(const float* __restrict__ ws, const float* __restrict__ Sg,
                                        const float* __restrict__ Sb, float* __restrict__ dmg, float* __restrict__ dSg,
                                        float* __restrict__ dmb, float* __restrict__ dSb, int C, int nblk) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= C) return;
+  const int c = blockIdx.x;
+  const int lane = threadIdx.x;
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  for (int s = 0; s < nblk; ++s) {
+  for (int s = lane; s < nblk; s += 64) {
     const float* p = ws + ((int64_t)s * C + c) * 4;
     s0 += p[0];
     s1 += p[1];
     s2 += p[2];
     s3 += p[3];
   }
+  s0 = wave_reduce(s0);
+  s1 = wave_reduce(s1);
+  s2 = wave_reduce(s2);
+  s3 = wave_reduce(s3);
+  if (lane != 0) return;
   const float g = Sg[c], b = Sb[c];
   dmg[c] = g * s0;
   dSg[c] = g * g * s1;
@@ -413,7 +431,7 @@ extern "C" int tagi_bn_stats(const float* mz, const float* Sz, float* batch_mean
                        nblk, 0, nullptr, nullptr, nullptr, nullptr, 0.f);
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(bn_stats_finalize_kernel, dim3((unsigned)cdiv(C, 256)), dim3(256), 0, s, (const float*)ws,
+  hipLaunchKernelGGL(bn_stats_finalize_kernel, dim3((unsigned)C), dim3(64), 0, s, (const float*)ws,
                      batch_mean, batch_var, running_mean, running_var, mg, (int)C, nblk, (double)rows, momentum, eps,
                      first_call, preserve_var);
   return check_launch(what);
@@ -462,7 +480,7 @@ extern "C" int tagi_bn_bwd(const float* dma, const float* dSa, const float* mhat
                        nblk, 1, var, mg, dmz, dSz, eps);
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(bn_bwd_finalize_kernel, dim3((unsigned)cdiv(C, 256)), dim3(256), 0, s, (const float*)ws, Sg, Sb,
+  hipLaunchKernelGGL(bn_bwd_finalize_kernel, dim3((unsigned)C), dim3(64), 0, s, (const float*)ws, Sg, Sb,
                      dmg, dSg, dmb, dSb, (int)C, nblk);
   return check_launch(what);
 }

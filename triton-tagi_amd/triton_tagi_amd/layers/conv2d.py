@@ -74,6 +74,13 @@ class Conv2D(LearnableLayer):
         return mz, Sz
 
     def backward(self, delta_mz: Tensor, delta_Sz: Tensor) -> tuple[Tensor, Tensor]:
+        return self._backward(delta_mz, delta_Sz, True)
+
+    def backward_param_deltas(self, delta_mz: Tensor, delta_Sz: Tensor) -> None:
+        """The parameter deltas of ``backward`` without forming the input deltas."""
+        self._backward(delta_mz, delta_Sz, False)
+
+    def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool):
         N, C, H, W = self.input_shape
         g = self._geom(N, C, H, W)
         dmz = _lib.check(_lib.channels_last(delta_mz.reshape(N, self.C_out, g.Ho, g.Wo)), "delta_mz")
@@ -92,6 +99,8 @@ class Conv2D(LearnableLayer):
         _lib.call("tagi_conv2d_wgrad", self.ma_in.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), self.Sw.data_ptr(),
                   self.Sb.data_ptr(), self.delta_mw.data_ptr(), self.delta_Sw.data_ptr(), self.delta_mb.data_ptr(),
                   self.delta_Sb.data_ptr(), g, wp, wb, st)
+        if not input_deltas:
+            return None
         d_ma = _lib.empty_cl(N, C, H, W, dev)
         d_Sa = _lib.empty_cl(N, C, H, W, dev)
         ws = _lib.workspace(_lib.query("tagi_conv2d_bwd_delta_ws_bytes", g), dev)

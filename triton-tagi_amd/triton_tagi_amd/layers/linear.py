@@ -46,12 +46,21 @@ class Linear(LearnableLayer):
         return mz.reshape(out_shape), Sz.reshape(out_shape)
 
     def backward(self, delta_mz: Tensor, delta_Sz: Tensor) -> tuple[Tensor, Tensor]:
+        return self._backward(delta_mz, delta_Sz, True)
+
+    def backward_param_deltas(self, delta_mz: Tensor, delta_Sz: Tensor) -> None:
+        """The parameter deltas of ``backward`` without forming the input deltas."""
+        self._backward(delta_mz, delta_Sz, False)
+
+    def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool):
         dmz = delta_mz.reshape(-1, self.out_features).contiguous()
         dSz = delta_Sz.reshape(-1, self.out_features).contiguous()
         dmw, dSw, dmb, dSb = linear_param_deltas(self.ma_in, dmz, dSz, self.Sw, self.Sb if self.has_bias else None)
         self.delta_mw, self.delta_Sw = dmw, dSw
         if self.has_bias:
             self.delta_mb, self.delta_Sb = dmb, dSb
+        if not input_deltas:
+            return None
         dma, dSa = fused_backward_delta(dmz, dSz, self.mw)
         in_shape = (*self._input_shape[:-1], self.in_features)
         return dma.reshape(in_shape), dSa.reshape(in_shape)

@@ -89,10 +89,20 @@ class Sequential:
             update_parameters_multi(items, cap_factor)
 
     def step(self, x_batch: Tensor, y_batch: Tensor, sigma_v: float) -> tuple[Tensor, Tensor]:
+        """forward -> innovation -> backward -> capped update (network.py:119-152).
+
+        The deltas the first layer would pass back to the network input reach no one, so
+        a first layer that can skip them (Linear, Conv2D) only forms its parameter deltas.
+        """
         batch_size = x_batch.shape[0]
         y_pred_mu, y_pred_var = self.forward(x_batch)
         delta_mu, delta_var = compute_innovation(y_batch, y_pred_mu, y_pred_var, sigma_v)
-        self.backward(delta_mu, delta_var)
+        for i in range(len(self.layers) - 1, -1, -1):
+            layer = self.layers[i]
+            if i == 0 and hasattr(layer, "backward_param_deltas"):
+                layer.backward_param_deltas(delta_mu, delta_var)
+            else:
+                delta_mu, delta_var = layer.backward(delta_mu, delta_var)
         self.update(get_cap_factor(batch_size))
         return y_pred_mu, y_pred_var
 
