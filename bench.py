@@ -102,6 +102,9 @@ def main():
     ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--cpu-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="before warm-up, run one device copy of this many MiB (a known-size kernel for "
+                         "calibrating the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -121,6 +124,16 @@ def main():
     log(f"[bench] building {args.workload} on {dev}")
     w = workloads.build(args.workload, device=dev, batch=args.batch)
     net, x, y, sv = w.net, w.x, w.y, w.sigma_v
+
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy of {args.copy_calibration_mib} MiB done")
+        del src, dst
 
     log(f"[bench] warmup {args.warmup} steps")
     for _ in range(args.warmup):
@@ -158,6 +171,8 @@ def main():
             "traffic": load_traffic(args.workload, dom),
             "launches_per_step": d["launches"] / args.steps,
             "avg_launch_us": round(per_launch_s * 1e6, 2),
+            "flops_per_launch": round(flops_per_launch),
+            "alg_bytes_per_launch": round(d["bytes"] / d["launches"]),
         }
     breakdown = {}
     gpu_ms = sum(v["ms"] for v in fams.values())
