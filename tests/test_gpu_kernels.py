@@ -111,6 +111,28 @@ def test_remax(dev, B, K):
     assert_scaled_close(J, rJ, None, RTOL, ATOL, "remax J")
 
 
+def test_remax_on_reference_golden_inputs(dev):
+    """HIP Remax on the inputs of the reference-generated fixture: within 1e-4 of the
+    float64 oracle, and within the reference's own fp32 rounding of its stored outputs."""
+    from pathlib import Path
+
+    import numpy as np
+
+    from triton_tagi_amd.layers.remax import remax
+
+    d = np.load(Path(__file__).resolve().parent / "golden" / "remax_golden.npz")
+    names = sorted({k[: -len("_mu_z")] for k in d.files if k.endswith("_mu_z")})
+    for n in names:
+        mu, var = torch.tensor(d[n + "_mu_z"]), torch.tensor(d[n + "_var_z"])
+        got = remax(mu.to(dev), var.to(dev))
+        ref64 = O.remax_moments(d64(mu), d64(var))
+        for key, gt, rt in zip(("mu_a", "var_a", "J"), got, ref64):
+            assert_scaled_close(gt, rt, None, RTOL, ATOL, f"remax {n} {key} vs oracle")
+            stored = torch.tensor(d[f"{n}_{key}"], dtype=torch.float64)
+            rel = ((gt.cpu().double() - stored).norm() / stored.norm()).item()
+            assert rel < (2e-3 if key == "mu_a" else 3e-2), f"remax {n} {key}: {rel:.2e} from the reference output"
+
+
 def test_innovation_update_add_jacobian(dev):
     from triton_tagi_amd.layers.relu import jacobian_backward
     from triton_tagi_amd.layers.resblock import add_shortcut

@@ -1,0 +1,580 @@
+"""Pins of the CPU oracle (oracle/tagi_oracle.py) -- CPU only.
+
+Each oracle function is checked against something that does not restate its formula:
+  * Linear / attention products / BN affine / RMSNorm scale: Monte Carlo moments of the
+    same random computation (independent Gaussians), within standard-error bounds;
+  * every backward rule: the TAGI delta rule evaluated with autograd Jacobians of the
+    layer's mean map (delta_mu_in = sum J delta_mu_out, delta_S_in = sum J^2 delta_S_out,
+    parameter deltas S_p sum J_p delta_mu, S_p^2 sum J_p^2 delta_S);
+  * Conv2D: torch.nn.functional.conv2d / conv_transpose2d and a brute-force loop
+    convolution, with the padding_type-2 right/bottom padding done by F.pad;
+  * ReLU: numerical quadrature of E[max(0,z)] and E[max(0,z)^2]; the alpha < -5 branch
+    against the asymptotic's own error bound;
+  * Remax: golden vectors written by the reference implementation itself
+    (tests/golden/make_remax_golden.py), exact normalisation and the deterministic limit;
+  * capped update / innovation / cap factor / priors: the reference's known-answer
+    values and closed-form special cases.
+Planted-mistake checks at the end mutate the oracle on the CPU and confirm that a pin fails.
+"""
+
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import tagi_oracle as O
+
+D = torch.float64
+GOLDEN = Path(__file__).resolve().parent / "golden" / "remax_golden.npz"
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def mc_linear(ma, Sa, mw, Sw, mb, Sb, n, seed):
+    """Monte Carlo mean/var of z = a @ w + b, all entries independent Gaussians."""
+    g = gen(seed)
+    M, K = ma.shape
+    N = mw.shape[1]
+    zs = []
+    for _ in range(n // 2000):
+        a = ma + Sa.sqrt() * torch.randn(2000, M, K, generator=g, dtype=D)
+        w = mw + Sw.sqrt() * torch.randn(2000, K, N, generator=g, dtype=D)
+        b = mb + Sb.sqrt() * torch.randn(2000, 1, N, generator=g, dtype=D)
+        zs.append(a @ w + b)
+    z = torch.cat(zs)
+    return z.mean(0), z.var(0), z.shape[0]
+
+
+def assert_mc(est_mean, est_var, n, mean, var, k=5.0):
+    """Oracle moments within k standard errors of the Monte Carlo estimates."""
+    se_mean = (var / n).sqrt()
+    assert ((est_mean - mean).abs() <= k * se_mean + 1e-12).all(), "mean outside MC error bound"
+    se_var = var * math.sqrt(2.0 / (n - 1))
+    assert ((est_var - var).abs() <= k * se_var + 1e-12).all(), "variance outside MC error bound"
+
+
+# ------------------------------------------------------------------------- Linear
+def test_linear_moments_monte_carlo():
+    g = gen(1)
+    ma, Sa = torch.randn(3, 4, generator=g, dtype=D), 0.3 + torch.rand(3, 4, generator=g, dtype=D)
+    mw, Sw = torch.randn(4, 2, generator=g, dtype=D), 0.3 + torch.rand(4, 2, generator=g, dtype=D)
+    mb, Sb = torch.randn(1, 2, generator=g, dtype=D), 0.2 + torch.rand(1, 2, generator=g, dtype=D)
+    mz, Sz = O.linear_moments(ma, Sa, mw, Sw, mb, Sb)
+    em, ev, n = mc_linear(ma, Sa, mw, Sw, mb, Sb, 400_000, 2)
+    assert_mc(em, ev, n, mz, Sz)
+
+
+def jac(f, x):
+    return torch.autograd.functional.jacobian(f, x)
+
+
+def test_linear_backward_jacobian_rule():
+    g = gen(3)
+    M, K, N = 3, 5, 4
+    ma = torch.randn(M, K, generator=g, dtype=D)
+    mw, Sw = torch.randn(K, N, generator=g, dtype=D), torch.rand(K, N, generator=g, dtype=D)
+    mb, Sb = torch.randn(1, N, generator=g, dtype=D), torch.rand(1, N, generator=g, dtype=D)
+    dmz, dSz = torch.randn(M, N, generator=g, dtype=D), -torch.rand(M, N, generator=g, dtype=D)
+    layer = O.OLinear(mw, Sw, mb, Sb)
+    layer.forward(ma, torch.zeros_like(ma))
+    dma, dSa = layer.backward(dmz, dSz)
+    Ja = jac(lambda a: a @ mw + mb, ma)  # (M,N,M,K)
+    Jw = jac(lambda w: ma @ w + mb, mw)  # (M,N,K,N)
+    Jb = jac(lambda b: ma @ mw + b, mb)  # (M,N,1,N)
+    torch.testing.assert_close(dma, torch.einsum("mnik,mn->ik", Ja, dmz))
+    torch.testing.assert_close(dSa, torch.einsum("mnik,mn->ik", Ja**2, dSz))
+    torch.testing.assert_close(layer.delta_mw, Sw * torch.einsum("mnkj,mn->kj", Jw, dmz))
+    torch.testing.assert_close(layer.delta_Sw, Sw**2 * torch.einsum("mnkj,mn->kj", Jw**2, dSz))
+    torch.testing.assert_close(layer.delta_mb, Sb * torch.einsum("mnkj,mn->kj", Jb, dmz))
+    torch.testing.assert_close(layer.delta_Sb, Sb**2 * torch.einsum("mnkj,mn->kj", Jb**2, dSz))
+
+
+# ------------------------------------------------------------------------- Conv2D
+def brute_conv(x, w, k, s, pt, Ho, Wo):
+    """Direct convolution by loops: out[n,o,i,j] = sum_{c,u,v} x[n,c,i*s-pt+u,j*s-pt+v] w[(c,u,v),o]."""
+    N, C, H, W = x.shape
+    Co = w.shape[1]
+    out = torch.zeros(N, Co, Ho, Wo, dtype=D)
+    for i in range(Ho):
+        for j in range(Wo):
+            for c in range(C):
+                for u in range(k):
+                    for v in range(k):
+                        h, ww = i * s - pt + u, j * s - pt + v
+                        if 0 <= h < H and 0 <= ww < W:
+                            out[:, :, i, j] += x[:, c, h, ww][:, None] * w[c * k * k + u * k + v][None, :]
+    return out
+
+
+CONV = [(2, 3, 6, 5, 4, 3, 1, 1, 1), (2, 2, 7, 7, 3, 3, 2, 1, 2), (1, 2, 6, 6, 3, 2, 2, 0, 1),
+        (2, 3, 8, 8, 2, 5, 1, 2, 1)]
+
+
+@pytest.mark.parametrize("case", CONV)
+def test_conv_forward_against_library_and_loops(case):
+    N, C, H, W, Co, k, s, p, pt = case
+    g = gen(sum(case))
+    K = C * k * k
+    ma, Sa = torch.randn(N, C, H, W, generator=g, dtype=D), torch.rand(N, C, H, W, generator=g, dtype=D)
+    mw, Sw = torch.randn(K, Co, generator=g, dtype=D), torch.rand(K, Co, generator=g, dtype=D)
+    mb, Sb = torch.randn(1, Co, generator=g, dtype=D), torch.rand(1, Co, generator=g, dtype=D)
+    layer = O.OConv2D(mw, Sw, mb, Sb, Co, k, s, p, pt)
+    mz, Sz = layer.forward(ma, Sa)
+    kern = lambda w: w.T.reshape(Co, C, k, k)  # noqa: E731
+    if pt == 2:
+        conv = lambda x, w: F.conv2d(F.pad(x, (0, p, 0, p)), kern(w), stride=s)  # noqa: E731
+    else:
+        conv = lambda x, w: F.conv2d(x, kern(w), stride=s, padding=p)  # noqa: E731
+    b4 = lambda b: b.view(1, Co, 1, 1)  # noqa: E731
+    torch.testing.assert_close(mz, conv(ma, mw) + b4(mb))
+    torch.testing.assert_close(Sz, conv(ma * ma, Sw) + conv(Sa, mw * mw + Sw) + b4(Sb))
+    pad = 0 if pt == 2 else p
+    torch.testing.assert_close(mz, brute_conv(ma, mw, k, s, pad, *layer.spatial) + b4(mb))
+
+
+@pytest.mark.parametrize("case", CONV)
+def test_conv_backward_jacobian_rule(case):
+    N, C, H, W, Co, k, s, p, pt = case
+    g = gen(7 + sum(case))
+    K = C * k * k
+    ma = torch.randn(N, C, H, W, generator=g, dtype=D)
+    mw, Sw = torch.randn(K, Co, generator=g, dtype=D), torch.rand(K, Co, generator=g, dtype=D)
+    mb, Sb = torch.randn(1, Co, generator=g, dtype=D), torch.rand(1, Co, generator=g, dtype=D)
+    layer = O.OConv2D(mw, Sw, mb, Sb, Co, k, s, p, pt)
+    mz, _ = layer.forward(ma, torch.zeros_like(ma))
+    dmz, dSz = torch.randn(mz.shape, generator=g, dtype=D), -torch.rand(mz.shape, generator=g, dtype=D)
+    dma, dSa = layer.backward(dmz, dSz)
+
+    def mean_map(x, w, b):
+        kern = w.T.reshape(Co, C, k, k)
+        if pt == 2:
+            return F.conv2d(F.pad(x, (0, p, 0, p)), kern, stride=s) + b.view(1, Co, 1, 1)
+        return F.conv2d(x, kern, stride=s, padding=p) + b.view(1, Co, 1, 1)
+
+    Jx = jac(lambda x: mean_map(x, mw, mb), ma)
+    Jw = jac(lambda w: mean_map(ma, w, mb), mw)
+    Jb = jac(lambda b: mean_map(ma, mw, b), mb)
+    od = list(range(4))
+    red = lambda J, d: torch.tensordot(d, J, dims=(od, od))  # noqa: E731
+    torch.testing.assert_close(dma, red(Jx, dmz))
+    torch.testing.assert_close(dSa, red(Jx**2, dSz))
+    torch.testing.assert_close(layer.delta_mw, Sw * red(Jw, dmz))
+    torch.testing.assert_close(layer.delta_Sw, Sw**2 * red(Jw**2, dSz))
+    torch.testing.assert_close(layer.delta_mb, Sb * red(Jb, dmz))
+    torch.testing.assert_close(layer.delta_Sb, Sb**2 * red(Jb**2, dSz))
+
+
+# --------------------------------------------------------------------------- ReLU
+@pytest.mark.parametrize("mu,S", [(0.7, 0.5), (-1.3, 2.0), (3.0, 0.04), (0.0, 1.0), (-4.0, 1.0)])
+def test_relu_against_quadrature(mu, S):
+    from scipy import integrate
+
+    sig = math.sqrt(S)
+    pdf = lambda z: math.exp(-0.5 * ((z - mu) / sig) ** 2) / (sig * math.sqrt(2 * math.pi))  # noqa: E731
+    lo, hi = 0.0, max(mu, 0.0) + 12 * sig
+    e1 = integrate.quad(lambda z: z * pdf(z), lo, hi, epsabs=1e-14, epsrel=1e-12)[0]
+    e2 = integrate.quad(lambda z: z * z * pdf(z), lo, hi, epsabs=1e-14, epsrel=1e-12)[0]
+    ma, Sa, J = O.relu_moments(torch.tensor([mu], dtype=D), torch.tensor([S], dtype=D))
+    assert abs(ma.item() - e1) < 1e-9 * max(1, e1)
+    assert abs(Sa.item() - (e2 - e1 * e1)) < 1e-9 * max(1, e2)
+    # J is d E[max(0,z)] / d mu
+    h = 1e-5
+    mp = O.relu_moments(torch.tensor([mu + h], dtype=D), torch.tensor([S], dtype=D))[0].item()
+    mm = O.relu_moments(torch.tensor([mu - h], dtype=D), torch.tensor([S], dtype=D))[0].item()
+    assert abs(J.item() - (mp - mm) / (2 * h)) < 1e-6
+
+
+def test_relu_asymptotic_branch_error_bound():
+    from scipy.special import ndtr
+
+    alpha = torch.tensor([-5.0001, -6.0, -8.0, -20.0], dtype=D)
+    _, _, J = O.relu_moments(alpha, torch.ones_like(alpha))
+    exact = torch.tensor(ndtr(alpha.numpy()))
+    rel = (J / exact - 1).abs()
+    # phi(a)/|a| overestimates Phi(a) by a relative 1/a^2 to leading order
+    assert (rel < 1.2 / alpha**2).all() and (rel > 0.5 / alpha**2).all()
+    _, _, J5 = O.relu_moments(torch.tensor([-4.999], dtype=D), torch.ones(1, dtype=D))
+    assert abs(J5.item() / ndtr(-4.999) - 1) < 1e-10  # erf branch just above the switch
+
+
+# -------------------------------------------------------------------------- Remax
+def golden_cases():
+    d = np.load(GOLDEN)
+    names = sorted({k[: -len("_mu_z")] for k in d.files if k.endswith("_mu_z")})
+    return d, names
+
+
+# The reference's own fp32 evaluation of these formulas carries up to ~3% rounding error on
+# individual variance/Jacobian elements (log-normal cancellations), so the golden pin is
+# norm-wise: mean within 2e-3, variance and Jacobian within 3e-2 relative in the 2-norm.
+REMAX_TOL = {"mu_a": 2e-3, "var_a": 3e-2, "J": 3e-2}
+
+
+def remax_golden_errors(fn=None):
+    fn = fn or O.remax_moments
+    d, names = golden_cases()
+    worst = {}
+    for n in names:
+        out = fn(torch.tensor(d[n + "_mu_z"], dtype=D), torch.tensor(d[n + "_var_z"], dtype=D))
+        for key, t in zip(("mu_a", "var_a", "J"), out):
+            ref = torch.tensor(d[f"{n}_{key}"], dtype=D)
+            e = ((t - ref).norm() / ref.norm()).item()
+            worst[key] = max(worst.get(key, 0.0), e)
+    return worst
+
+
+def test_remax_matches_reference_golden():
+    worst = remax_golden_errors()
+    for k, tol in REMAX_TOL.items():
+        assert worst[k] < tol, f"{k}: norm-wise relative error {worst[k]:.2e} vs reference output"
+
+
+def test_remax_normalisation_and_deterministic_limit():
+    g = gen(5)
+    mu = torch.randn(50, 10, generator=g, dtype=D)
+    var = 0.1 + torch.rand(50, 10, generator=g, dtype=D)
+    ma, Sa, J = O.remax_moments(mu, var)
+    torch.testing.assert_close(ma.sum(-1), torch.ones(50, dtype=D))
+    assert (Sa >= 0).all()
+    # variances -> 0 with positive logits: A -> mu / sum(mu), Var A -> 0
+    mu = 0.5 + torch.rand(20, 7, generator=g, dtype=D)
+    ma, Sa, _ = O.remax_moments(mu, torch.full_like(mu, 1e-12))
+    torch.testing.assert_close(ma, mu / mu.sum(-1, keepdim=True), rtol=1e-5, atol=1e-8)
+    assert Sa.max() < 1e-5
+
+
+# ------------------------------------------------------------------------ BatchNorm
+def test_batchnorm_stats_and_affine():
+    g = gen(9)
+    N, C, H, W = 4, 3, 5, 5
+    mz, Sz = 1 + torch.randn(N, C, H, W, generator=g, dtype=D), torch.rand(N, C, H, W, generator=g, dtype=D)
+    n = N * H * W
+    mean, var = O.bn_batch_stats(mz, Sz)
+    torch.testing.assert_close(mean, mz.mean((0, 2, 3)))
+    # pooled variance of the Gaussian inputs with Bessel's factor on both parts
+    ref = mz.permute(1, 0, 2, 3).reshape(C, -1).var(dim=1, unbiased=True) + Sz.mean((0, 2, 3)) * n / (n - 1)
+    torch.testing.assert_close(var, ref)
+    mg, Sg = torch.rand(C, dtype=D) + 0.5, torch.rand(C, dtype=D)
+    mb, Sb = torch.randn(C, dtype=D), torch.rand(C, dtype=D)
+    bn = O.OBatchNorm2D(mg.clone(), Sg, mb, Sb, torch.zeros(C, dtype=D), torch.ones(C, dtype=D), 0.1, 1e-5,
+                        preserve_var=True, initialized=False)
+    ma, Sa = bn.forward(mz, Sz)
+    torch.testing.assert_close(bn.mw, torch.sqrt(var + 1e-5))  # first call re-initialises gamma
+    torch.testing.assert_close(bn.running_mean, mean)
+    bn.forward(mz, Sz * 2)  # second call: EMA with momentum 0.1
+    _, var2 = O.bn_batch_stats(mz, Sz * 2)
+    torch.testing.assert_close(bn.running_var, 0.9 * var + 0.1 * var2)
+    # affine moments by Monte Carlo on one channel-position: g*xhat + b, independent Gaussians
+    mh = (mz[0, 0, 0, 0] - mean[0]) / torch.sqrt(var[0] + 1e-5)
+    sh = Sz[0, 0, 0, 0] / (var[0] + 1e-5)
+    gg = gen(10)
+    gam = torch.sqrt(var[0] + 1e-5) + Sg[0].sqrt() * torch.randn(400_000, generator=gg, dtype=D)
+    xh = mh + sh.sqrt() * torch.randn(400_000, generator=gg, dtype=D)
+    bet = mb[0] + Sb[0].sqrt() * torch.randn(400_000, generator=gg, dtype=D)
+    y = gam * xh + bet
+    bn2 = O.OBatchNorm2D(mg.clone(), Sg, mb, Sb, None, None, 0.1, 1e-5, True, False)
+    ma2, Sa2 = bn2.forward(mz, Sz)
+    assert_mc(y.mean(), y.var(), y.numel(), ma2[0, 0, 0, 0], Sa2[0, 0, 0, 0])
+
+
+def test_batchnorm_backward_jacobian_rule():
+    g = gen(11)
+    N, C, H, W = 3, 2, 4, 4
+    mz, Sz = torch.randn(N, C, H, W, generator=g, dtype=D), torch.rand(N, C, H, W, generator=g, dtype=D)
+    mg, Sg = 1 + 0.1 * torch.randn(C, generator=g, dtype=D), torch.rand(C, generator=g, dtype=D)
+    mb, Sb = torch.randn(C, generator=g, dtype=D), torch.rand(C, generator=g, dtype=D)
+    bn = O.OBatchNorm2D(mg, Sg, mb, Sb, torch.zeros(C, dtype=D), torch.ones(C, dtype=D), 0.1, 1e-5, False, False)
+    bn.forward(mz, Sz)
+    mean, var = O.bn_batch_stats(mz, Sz)
+    dm, dS = torch.randn(mz.shape, generator=g, dtype=D), -torch.rand(mz.shape, generator=g, dtype=D)
+    om, oS = bn.backward(dm, dS)
+
+    def f(x, gam, bet):  # batch statistics held fixed, as in the reference backward
+        v = lambda t: t.view(1, -1, 1, 1)  # noqa: E731
+        return v(gam) * (x - v(mean)) / torch.sqrt(v(var) + 1e-5) + v(bet)
+
+    od = list(range(4))
+    red = lambda J, d: torch.tensordot(d, J, dims=(od, od))  # noqa: E731
+    Jx, Jg, Jb = jac(lambda x: f(x, mg, mb), mz), jac(lambda t: f(mz, t, mb), mg), jac(lambda t: f(mz, mg, t), mb)
+    torch.testing.assert_close(om, red(Jx, dm))
+    torch.testing.assert_close(oS, red(Jx**2, dS))
+    torch.testing.assert_close(bn.delta_mw, Sg * red(Jg, dm))
+    torch.testing.assert_close(bn.delta_Sw, Sg**2 * red(Jg**2, dS))
+    torch.testing.assert_close(bn.delta_mb, Sb * red(Jb, dm))
+    torch.testing.assert_close(bn.delta_Sb, Sb**2 * red(Jb**2, dS))
+
+
+# --------------------------------------------------------------- AvgPool / ResBlock
+@pytest.mark.parametrize("k,sc", [(2, False), (3, False), (2, True)])
+def test_avgpool_against_library(k, sc):
+    g = gen(k)
+    ma, Sa = torch.randn(2, 3, 7, 6, generator=g, dtype=D), torch.rand(2, 3, 7, 6, generator=g, dtype=D)
+    pool = O.OAvgPool2D(k, sc)
+    mo, So = pool.forward(ma, Sa)
+    torch.testing.assert_close(mo, F.avg_pool2d(ma, k))
+    torch.testing.assert_close(So, F.avg_pool2d(Sa, k) / (1 if sc else k * k))
+    dm, dS = torch.randn(mo.shape, generator=g, dtype=D), torch.rand(mo.shape, generator=g, dtype=D)
+    om, oS = pool.backward(dm, dS)
+    Jx = jac(lambda x: F.avg_pool2d(x, k), ma)
+    od = list(range(4))
+    torch.testing.assert_close(om, torch.tensordot(dm, Jx, dims=(od, od)))
+    if not sc:  # the 1/k^4 variance scale is the squared-Jacobian rule
+        torch.testing.assert_close(oS, torch.tensordot(dS, Jx**2, dims=(od, od)))
+
+
+def test_resblock_composition():
+    g = gen(12)
+    C = 2
+    mk = lambda: O.OConv2D(0.3 * torch.randn(C * 9, C, generator=g, dtype=D), 0.01 * torch.rand(C * 9, C, generator=g, dtype=D),  # noqa: E731
+                           torch.zeros(1, C, dtype=D), 0.01 * torch.ones(1, C, dtype=D), C, 3, 1, 1, 1)
+    mkbn = lambda: O.OBatchNorm2D(torch.ones(C, dtype=D), 0.01 * torch.ones(C, dtype=D), torch.zeros(C, dtype=D),  # noqa: E731
+                                  0.01 * torch.ones(C, dtype=D), torch.zeros(C, dtype=D), torch.ones(C, dtype=D), 0.1,
+                                  1e-5, False, False)
+    main = [mk(), O.OReLU(), mkbn(), mk(), O.OReLU(), mkbn()]
+    blk = O.OResBlock(main, [])
+    x, S = torch.randn(2, C, 5, 5, generator=g, dtype=D), torch.rand(2, C, 5, 5, generator=g, dtype=D)
+    mo, So = blk.forward(x, S)
+    m2, S2 = x, S
+    for layer in main:
+        m2, S2 = layer.forward(m2, S2)
+    torch.testing.assert_close(mo, m2 + x)  # identity shortcut adds means and variances
+    torch.testing.assert_close(So, S2 + S)
+    dm, dS = torch.randn(mo.shape, generator=g, dtype=D), -torch.rand(mo.shape, generator=g, dtype=D)
+    am, aS = blk.backward(dm, dS)
+    b1, b2 = dm, dS
+    for layer in reversed(main):
+        b1, b2 = layer.backward(b1, b2)
+    torch.testing.assert_close(am, b1 + dm)
+    torch.testing.assert_close(aS, b2 + dS)
+
+
+# --------------------------------------------------------------------- attention
+def test_bmm_tagi_monte_carlo_and_shared_rules():
+    g = gen(13)
+    ma, Sa = torch.randn(2, 3, generator=g, dtype=D), 0.2 + torch.rand(2, 3, generator=g, dtype=D)
+    mb, Sb = torch.randn(3, 2, generator=g, dtype=D), 0.2 + torch.rand(3, 2, generator=g, dtype=D)
+    mean, var = O.bmm_tagi(ma, Sa, mb, Sb, scale=0.5)
+    em, ev, n = mc_linear(ma, Sa, mb, Sb, torch.zeros(1, 2, dtype=D), torch.zeros(1, 2, dtype=D), 400_000, 14)
+    assert_mc(0.5 * em, 0.25 * ev, n, mean, var)
+    # shared-operand products are the delta rule of a bilinear map with one fixed factor
+    a, b = torch.randn(4, 3, generator=g, dtype=D), torch.randn(3, 5, generator=g, dtype=D)
+    dm, dS = torch.randn(4, 3, generator=g, dtype=D), torch.rand(4, 3, generator=g, dtype=D)
+    m, v = O.bmm_shared_right(dm, dS, b, scale=0.7)
+    J = jac(lambda x: 0.7 * x @ b, a)  # (4,5,4,3): d out / d a
+    torch.testing.assert_close(m, torch.einsum("ikxy,xy->ik", J, dm))
+    torch.testing.assert_close(v, torch.einsum("ikxy,xy->ik", J**2, dS))
+    em2, eS2 = torch.randn(3, 5, generator=g, dtype=D), torch.rand(3, 5, generator=g, dtype=D)
+    m, v = O.bmm_shared_left(a, em2, eS2, scale=1.3)
+    J = jac(lambda y: 1.3 * a @ y, b)  # (4,5,3,5)
+    torch.testing.assert_close(m, torch.einsum("ikxy,xy->ik", J, em2))
+    torch.testing.assert_close(v, torch.einsum("ikxy,xy->ik", J**2, eS2))
+
+
+def test_attention_forward_reconstruction_and_backward_rule():
+    """Forward: the step-by-step reconstruction of the reference's own test
+    (test_attention.py:328-398) built from library matmuls; backward: delta rule on the
+    mean map with Remax linearised by its Jacobian (per-layer squared Jacobians for S)."""
+    g = gen(15)
+    B, S, E, H = 2, 4, 6, 2
+    Dh = E // H
+    lin = lambda: O.OLinear(torch.randn(E, E, generator=g, dtype=D) / E**0.5, 0.01 * torch.rand(E, E, generator=g, dtype=D),  # noqa: E731
+                            torch.zeros(1, E, dtype=D), torch.zeros(1, E, dtype=D), False)
+    att = O.OMultiheadAttentionV2(lin(), lin(), lin(), H)
+    x, Sx = torch.randn(B, S, E, generator=g, dtype=D), 0.1 * torch.rand(B, S, E, generator=g, dtype=D)
+    mo, So = att.forward(x, Sx)
+    s = 1 / math.sqrt(Dh)
+    hd = lambda t: t.reshape(B, S, H, Dh).transpose(1, 2)  # noqa: E731
+    q, k, v = (hd(x @ lyr.mw) for lyr in (att.q, att.k, att.v))
+    Sq, Sk, Sv = (hd((x * x) @ lyr.Sw + Sx @ (lyr.mw**2 + lyr.Sw)) for lyr in (att.q, att.k, att.v))
+    mqk = s * torch.matmul(q, k.transpose(-1, -2))
+    vqk = s * s * (torch.matmul(Sq, (k * k + Sk).transpose(-1, -2)) + torch.matmul(q * q, Sk.transpose(-1, -2)))
+    msc, vsc, J = O.remax_moments(mqk, vqk)
+    torch.testing.assert_close(att.attn[0], msc)
+    out = torch.matmul(msc, v).transpose(1, 2).reshape(B, S, E)
+    torch.testing.assert_close(mo, out)
+    vout = (torch.matmul(vsc, v * v + Sv) + torch.matmul(msc * msc, Sv)).transpose(1, 2).reshape(B, S, E)
+    torch.testing.assert_close(So, vout)
+    # backward of the attention core w.r.t. the head projections
+    dmo, dSo = torch.randn(B, S, E, generator=g, dtype=D), -torch.rand(B, S, E, generator=g, dtype=D)
+    c = att.cache
+    dm_h, dS_h = hd(dmo), hd(dSo)
+
+    def core(qq, kk, vv):  # mean map with Remax replaced by its linearisation (slope J)
+        z = s * torch.matmul(qq, kk.transpose(-1, -2))
+        a = c["msc"] + J * (z - mqk)
+        return torch.matmul(a, vv)
+
+    Jv = jac(lambda vv: torch.matmul(c["msc"], vv), v)
+    od = list(range(4))
+    red = lambda J_, d: torch.tensordot(d, J_, dims=(od, od))  # noqa: E731
+    dV = red(Jv, dm_h)
+    dSV = red(Jv**2, dS_h)
+    dA = red(jac(lambda a: torch.matmul(a, v), c["msc"]), dm_h)
+    dSA = red(jac(lambda a: torch.matmul(a, v), c["msc"]) ** 2, dS_h)
+    sm, sv = dA * J, dSA * J * J
+    Jq = jac(lambda qq: s * torch.matmul(qq, k.transpose(-1, -2)), q)
+    Jk = jac(lambda kk: s * torch.matmul(q, kk.transpose(-1, -2)), k)
+    dQ, dSQ, dK, dSK = red(Jq, sm), red(Jq**2, sv), red(Jk, sm), red(Jk**2, sv)
+    # the full-chain mean rule agrees with the per-layer composition
+    torch.testing.assert_close(dQ, red(jac(lambda qq: core(qq, k, v), q), dm_h))
+    unh = lambda t: t.transpose(1, 2).reshape(B, S, E)  # noqa: E731
+    dx, dSx = att.backward(dmo, dSo)
+    exp_m = sum(unh(dd) @ lyr.mw.T for dd, lyr in ((dQ, att.q), (dK, att.k), (dV, att.v)))
+    exp_S = sum(unh(dd) @ (lyr.mw**2).T for dd, lyr in ((dSQ, att.q), (dSK, att.k), (dSV, att.v)))
+    torch.testing.assert_close(dx, exp_m)
+    torch.testing.assert_close(dSx, exp_S)
+
+
+# ---------------------------------------------------------- RMSNorm / Embedding / PE
+def test_rmsnorm_moments_and_rule():
+    g = gen(16)
+    D_ = 5
+    ma, Sa = torch.randn(3, D_, generator=g, dtype=D), torch.rand(3, D_, generator=g, dtype=D)
+    mw, Sw = 1 + 0.2 * torch.randn(D_, generator=g, dtype=D), 0.3 * torch.rand(D_, generator=g, dtype=D)
+    r = O.ORMSNorm(mw, Sw, 1e-6)
+    mz, Sz = r.forward(ma, Sa)
+    inv = 1 / torch.sqrt((ma * ma + Sa).mean(1, keepdim=True) + 1e-6)
+    gg = gen(17)
+    a = ma[1, 2] + Sa[1, 2].sqrt() * torch.randn(400_000, generator=gg, dtype=D)
+    gam = mw[2] + Sw[2].sqrt() * torch.randn(400_000, generator=gg, dtype=D)
+    z = inv[1, 0] * a * gam  # inv_rms is a statistic of the moments, not of the sample
+    assert_mc(z.mean(), z.var(), z.numel(), mz[1, 2], Sz[1, 2])
+    dm, dS = torch.randn(3, D_, generator=g, dtype=D), -torch.rand(3, D_, generator=g, dtype=D)
+    om, oS = r.backward(dm, dS)
+    f = lambda x, w: inv.detach() * x * w  # noqa: E731
+    Jx, Jw = jac(lambda x: f(x, mw), ma), jac(lambda w: f(ma, w), mw)
+    torch.testing.assert_close(om, torch.einsum("ijkl,ij->kl", Jx, dm))
+    torch.testing.assert_close(oS, torch.einsum("ijkl,ij->kl", Jx**2, dS))
+    torch.testing.assert_close(r.delta_mw, Sw * torch.einsum("ijk,ij->k", Jw, dm))
+    torch.testing.assert_close(r.delta_Sw, Sw**2 * torch.einsum("ijk,ij->k", Jw**2, dS))
+
+
+def test_embedding_gather_scatter_by_loops():
+    g = gen(18)
+    V, Dm = 5, 3
+    mw, Sw = torch.randn(V, Dm, generator=g, dtype=D), torch.rand(V, Dm, generator=g, dtype=D)
+    tok = torch.tensor([[0, 3, 3, 4], [1, 3, 0, 2]], dtype=D)
+    for pad in (-1, 3):
+        e = O.OEmbedding(mw, Sw, pad)
+        mz, Sz = e.forward(tok, torch.zeros_like(tok))
+        dm, dS = torch.randn(2, 4, Dm, generator=g, dtype=D), torch.randn(2, 4, Dm, generator=g, dtype=D)
+        e.backward(dm, dS)
+        em, eS = torch.zeros(V, Dm, dtype=D), torch.zeros(V, Dm, dtype=D)
+        for b in range(2):
+            for t in range(4):
+                c = int(tok[b, t])
+                if c == pad:
+                    assert (mz[b, t] == 0).all() and (Sz[b, t] == 0).all()
+                    continue
+                assert torch.equal(mz[b, t], mw[c]) and torch.equal(Sz[b, t], Sw[c])
+                em[c] += dm[b, t] * Sw[c]
+                eS[c] += dS[b, t] * Sw[c] ** 2
+        torch.testing.assert_close(e.delta_mw, em)
+        torch.testing.assert_close(e.delta_Sw, eS)
+
+
+def test_positional_encoding_table():
+    pe = O.sinusoidal_table(7, 6)
+    for t in range(7):
+        for d in range(6):
+            a = t / (10000.0 ** (d / 6))
+            assert abs(pe[t, d].item() - (math.sin(a) if d % 2 == 0 else math.cos(a))) < 1e-12
+
+
+# -------------------------------------------------------- update / innovation / priors
+def test_capped_update_known_answers():
+    S = torch.tensor([0.04, 0.04, 0.04, 0.04, 1e-12, 0.01], dtype=D)
+    m = torch.zeros(6, dtype=D)
+    dm = torch.tensor([0.05, 0.5, -0.5, 0.0, 1.0, 0.01], dtype=D)
+    dS = torch.tensor([0.01, -0.5, 0.2, 0.0, 0.0, -0.06], dtype=D)
+    nm, nS = O.capped_update(m, S, dm, dS, cap=2.0)
+    bar = torch.sqrt(torch.clamp(S, min=1e-10)) / 2.0  # 0.1 for S = 0.04, 5e-6 for S ~ 0
+    torch.testing.assert_close(nm, torch.tensor([0.05, 0.1, -0.1, 0.0, 5e-6, 0.01], dtype=D))
+    torch.testing.assert_close(nS, torch.tensor([0.05, 1e-5, 0.14, 0.04, 1e-12, 1e-5], dtype=D))
+    assert bar[0].item() == pytest.approx(0.1)
+    # the reference's own restatement of the capped mean update (test_conv2d.py:255-262)
+    g = gen(19)
+    mw, Sw, dmw = torch.randn(7, 3, generator=g, dtype=D), torch.rand(7, 3, generator=g, dtype=D), torch.randn(7, 3, generator=g, dtype=D)
+    nm, _ = O.capped_update(mw, Sw, dmw, torch.zeros_like(Sw), 3.0)
+    delta_bar = Sw.sqrt() / 3.0
+    torch.testing.assert_close(nm, mw + torch.sign(dmw) * torch.minimum(dmw.abs(), delta_bar))
+
+
+def test_innovation_and_cap_factor():
+    dm, dS = O.innovation(torch.tensor([1.0], dtype=D), torch.tensor([0.5], dtype=D), torch.tensor([0.25], dtype=D), 0.5)
+    assert dm.item() == pytest.approx(1.0) and dS.item() == pytest.approx(-2.0)
+    assert [O.get_cap_factor(b) for b in (1, 2, 128, 255, 256, 1024)] == [0.1, 2.0, 2.0, 2.0, 3.0, 3.0]
+
+
+def test_engine_priors_match_reference_init_rules():
+    """test_init.py:38-192: Sw = gain^2/fan_in exactly, norm layers gamma=1, beta=0, S = gain^2/C."""
+    from triton_tagi_amd.param_init import init_weight_bias_conv2d, init_weight_bias_linear, init_weight_bias_norm
+
+    mw, Sw, mb, Sb = init_weight_bias_linear(50, 7, gain_w=0.3, gain_b=0.5, device="cpu")
+    assert mw.shape == (50, 7) and mb.shape == (1, 7)
+    assert torch.allclose(Sw, torch.full_like(Sw, 0.09 / 50), rtol=1e-7, atol=0)
+    assert torch.allclose(Sb, torch.full_like(Sb, 0.25 / 50), rtol=1e-7, atol=0)
+    mw, Sw, mb, Sb = init_weight_bias_conv2d(3, 4, 8, gain_w=0.1, device="cpu")
+    assert mw.shape == (36, 8) and torch.allclose(Sw, torch.full_like(Sw, 0.01 / 36), rtol=1e-7, atol=0)
+    g, Sg, b, Sbb = init_weight_bias_norm(16, gain_w=0.1, device="cpu")
+    assert torch.all(g == 1) and torch.all(b == 0)
+    assert torch.allclose(Sg, torch.full_like(Sg, 0.01 / 16), rtol=1e-7, atol=0)
+    assert torch.allclose(Sbb, torch.full_like(Sbb, 1 / 16), rtol=1e-7, atol=0)
+
+
+# ------------------------------------------------------------- planted mistakes
+def test_pins_catch_planted_mistakes(monkeypatch):
+    """Mutations of the oracle (on the CPU) must trip the pins above."""
+    # 1. Remax: a 50% variance error (the size a dropped log-normal term produces) and a
+    #    sign flip of the Jacobian
+    def bad_remax(mu_z, var_z):
+        out = O.remax_moments(mu_z, var_z)
+        return out[0], out[1] * 1.5, out[2]  # a 50% variance error, what a dropped term gives
+
+    worst = remax_golden_errors(bad_remax)
+    assert worst["var_a"] > REMAX_TOL["var_a"]
+
+    def sign_flip(mu_z, var_z):
+        ma, Sa, J = O.remax_moments(mu_z, var_z)
+        return ma, Sa, -J
+
+    assert remax_golden_errors(sign_flip)["J"] > REMAX_TOL["J"]
+
+    # 2. Linear variance without the Sa*Sw term must fail the Monte Carlo pin
+    g = gen(1)
+    ma, Sa = torch.randn(3, 4, generator=g, dtype=D), 0.3 + torch.rand(3, 4, generator=g, dtype=D)
+    mw, Sw = torch.randn(4, 2, generator=g, dtype=D), 0.3 + torch.rand(4, 2, generator=g, dtype=D)
+    mb, Sb = torch.randn(1, 2, generator=g, dtype=D), 0.2 + torch.rand(1, 2, generator=g, dtype=D)
+    bad_S = (ma * ma) @ Sw + Sa @ (mw * mw) + Sb
+    em, ev, n = mc_linear(ma, Sa, mw, Sw, mb, Sb, 400_000, 2)
+    with pytest.raises(AssertionError):
+        assert_mc(em, ev, n, ma @ mw + mb, bad_S)
+
+    # 3. a transposed weight in the backward delta must fail the Jacobian rule
+    mw2 = torch.randn(5, 5, generator=g, dtype=D)
+    dmz = torch.randn(3, 5, generator=g, dtype=D)
+    Ja = jac(lambda a: a @ mw2, torch.randn(3, 5, generator=g, dtype=D))
+    assert not torch.allclose(dmz @ mw2, torch.einsum("mnik,mn->ik", Ja, dmz))
+
+    # 4. ReLU variance with the sign of the mu*sigma*phi term flipped fails quadrature
+    monkeypatch.setattr(O, "relu_moments", lambda mz, Sz: _relu_flipped(mz, Sz))
+    with pytest.raises(AssertionError):
+        test_relu_against_quadrature(0.7, 0.5)
+
+
+def _relu_flipped(mz, Sz):
+    Ss = torch.clamp(Sz, min=1e-30)
+    sig = torch.sqrt(Ss)
+    alpha = mz / sig
+    pdf = torch.exp(-0.5 * alpha * alpha) * O.INV_SQRT_2PI
+    cdf = 0.5 * (1.0 + torch.erf(alpha * O.INV_SQRT_2))
+    mu = sig * pdf + mz * cdf
+    var = -mu * mu + 2.0 * mu * mz + mz * sig * pdf + (Ss - mz * mz) * cdf
+    return mu, torch.clamp(var, min=0.0), cdf
