@@ -578,3 +578,34 @@ def _relu_flipped(mz, Sz):
     mu = sig * pdf + mz * cdf
     var = -mu * mu + 2.0 * mu * mz + mz * sig * pdf + (Ss - mz * mz) * cdf
     return mu, torch.clamp(var, min=0.0), cdf
+
+
+def test_step_composition_matches_reference_chain():
+    """ONet.step on a one-Conv2D network equals the reference's own one-step chain
+    (test_conv2d.py:218-262): conv moments with Sa = 0, innovation, patch-space parameter
+    deltas, capped update with the batch's cap factor -- here written with F.conv2d and
+    autograd instead of im2col."""
+    g = gen(20)
+    N, C, H, W, Co, k = 4, 3, 8, 8, 8, 3
+    K = C * k * k
+    mw, Sw = 0.2 * torch.randn(K, Co, generator=g, dtype=D), 0.05 * torch.rand(K, Co, generator=g, dtype=D)
+    mb, Sb = 0.1 * torch.randn(1, Co, generator=g, dtype=D), 0.05 * torch.rand(1, Co, generator=g, dtype=D)
+    x, y = torch.randn(N, C, H, W, generator=g, dtype=D), torch.randn(N, Co, H, W, generator=g, dtype=D)
+    sv = 0.1
+    net = O.ONet([O.OConv2D(mw.clone(), Sw.clone(), mb.clone(), Sb.clone(), Co, k, 1, 1, 1)])
+    net.step(x, y, sv)
+    kern = lambda w: w.T.reshape(Co, C, k, k)  # noqa: E731
+    mean_map = lambda w, b: F.conv2d(x, kern(w), padding=1) + b.view(1, Co, 1, 1)  # noqa: E731
+    mz = mean_map(mw, mb)
+    Sz = F.conv2d(x * x, kern(Sw), padding=1) + Sb.view(1, Co, 1, 1)
+    dmz, dSz = (y - mz) / (Sz + sv**2), -1.0 / (Sz + sv**2)
+    od = list(range(4))
+    Jw = jac(lambda w: mean_map(w, mb), mw)
+    d_mw = Sw * torch.tensordot(dmz, Jw, dims=(od, od))
+    d_Sw = Sw**2 * torch.tensordot(dSz, Jw**2, dims=(od, od))
+    cap = 2.0  # batch 4
+    bar = Sw.sqrt() / cap
+    mw_ref = mw + torch.sign(d_mw) * torch.minimum(d_mw.abs(), bar)
+    S_raw = Sw + torch.sign(d_Sw) * torch.minimum(d_Sw.abs(), bar)
+    torch.testing.assert_close(net.layers[0].mw, mw_ref)
+    torch.testing.assert_close(net.layers[0].Sw, torch.where(S_raw <= 0, torch.full_like(S_raw, 1e-5), S_raw))
