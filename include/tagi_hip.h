@@ -149,6 +149,15 @@ int tagi_conv2d_bwd_delta(const float* dmz, const float* dSz, const float* mw, f
                           tagi_stream_t stream);
 int64_t tagi_conv2d_bwd_delta_ws_bytes(const tagi_conv_geom* g);
 
+/* tagi_conv2d_bwd_delta plus an addend of the output's layout and shape:
+ *   dma = fold(...) + add_m, dSa = fold(...) + add_S
+ * (the input deltas of a residual block's first convolution merged with the deltas of the
+ * shortcut branch in the same pass). Workspace as tagi_conv2d_bwd_delta.
+ * Replaces conv2d.py:357-370 followed by triton_delta_merge (resblock.py:157, 421-423). */
+int tagi_conv2d_bwd_delta_add(const float* dmz, const float* dSz, const float* mw, const float* add_m,
+                              const float* add_S, float* dma, float* dSa, const tagi_conv_geom* g,
+                              float* ws, int64_t ws_bytes, tagi_stream_t stream);
+
 /* Parameter deltas of a Conv2D layer (reduction over N*Ho*Wo patches, split-K):
  *   dmw = Sw * P^T @ dmz, dSw = Sw^2 * (P^2)^T @ dSz, dmb = Sb * sum dmz, dSb = Sb^2 * sum dSz.
  * Replaces conv2d.py:341-354. */
@@ -236,6 +245,33 @@ int tagi_bn_bwd(const float* dma, const float* dSa, const float* mhat, const flo
                 float* dmg, float* dSg, float* dmb, float* dSb, int64_t N, int64_t C, int64_t HW,
                 float eps, float* ws, int64_t ws_bytes, tagi_stream_t stream);
 int64_t tagi_bn_bwd_ws_bytes(int64_t N, int64_t C, int64_t HW);
+
+/* ReLU followed by BatchNorm2D (relu.py:135-140, then batchnorm2d.py:307-355), first pass:
+ * the batch statistics of the rectified moments of (mz, Sz), with the same running-stat /
+ * gamma bookkeeping as tagi_bn_stats, and J = Phi(alpha) for the ReLU backward. The
+ * rectified moments themselves are not stored. ws: size from tagi_bn_stats_ws_bytes. */
+int tagi_relu_bn_stats(const float* mz, const float* Sz, float* J, float* batch_mean, float* batch_var,
+                       float* running_mean, float* running_var, float* mg, int64_t N, int64_t C,
+                       int64_t HW, float momentum, float eps, int first_call, int preserve_var,
+                       float* ws, int64_t ws_bytes, tagi_stream_t stream);
+
+/* ReLU followed by BatchNorm2D, second pass: recomputes the rectified moments of (mz, Sz)
+ * and normalises them as tagi_bn_fwd (Shat not stored). When add_m/add_S are given the
+ * Gaussian stream (add_m, add_S) is added to the output: the residual add that closes a
+ * block (resblock.py:380, triton_add_shortcut resblock.py:138). */
+int tagi_relu_bn_fwd(const float* mz, const float* Sz, const float* mean, const float* var,
+                     const float* mg, const float* Sg, const float* mb, const float* Sb,
+                     const float* add_m, const float* add_S, float* ma, float* Sa, float* mhat,
+                     int64_t N, int64_t C, int64_t HW, float eps, tagi_stream_t stream);
+
+/* BatchNorm2D backward followed by the Jacobian of the ReLU in front of it
+ * (batchnorm2d.py:134-192 then relu.py:152-169):
+ *   dmz = (dma mg/sqrt(var+eps)) J,  dSz = (dSa mg^2/(var+eps)) J^2,
+ * parameter deltas as tagi_bn_bwd. ws: size from tagi_bn_bwd_ws_bytes. */
+int tagi_bn_relu_bwd(const float* dma, const float* dSa, const float* mhat, const float* J,
+                     const float* var, const float* mg, const float* Sg, const float* Sb, float* dmz,
+                     float* dSz, float* dmg, float* dSg, float* dmb, float* dSb, int64_t N, int64_t C,
+                     int64_t HW, float eps, float* ws, int64_t ws_bytes, tagi_stream_t stream);
 
 /* -------------------------------------------------- RMSNorm / Embedding / PE ---- */
 /* RMSNorm forward over rows of length D (rms_norm.py:93-110); inv_rms (rows) is cached. */

@@ -1,0 +1,197 @@
+"""Fused multi-layer passes against the float64 oracle and against the unfused layers.
+
+The fused passes (ReLU -> BatchNorm2D forward with an optional residual add, BatchNorm2D
+-> ReLU backward, conv input deltas with the shortcut deltas added in the epilogue) must
+give the reference's results: checked against the oracle's layer-by-layer chain at the
+engine's bar (|gpu - oracle| <= 1e-6 + 1e-4 * scale), and against the engine's own
+unfused kernels (same fp32 formulas, so they agree to a few ulps).
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from conftest import assert_scaled_close
+from oracle import tagi_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-4, 1e-6
+
+
+def g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def d64(t):
+    return t.detach().to("cpu", torch.float64)
+
+
+def close_unfused(a, b, what):
+    a, b = a.detach().cpu().double(), b.detach().cpu().double()
+    err = (a - b).abs().max().item()
+    lim = 1e-6 * (b.abs().max().item() + 1e-30) + 1e-12
+    assert err <= lim, f"{what}: fused vs unfused max err {err:.3e} > {lim:.3e}"
+
+
+def make_bn(C, first, preserve, seed, dev):
+    from triton_tagi_amd.layers.batchnorm2d import BatchNorm2D
+
+    torch.manual_seed(seed)
+    bn = BatchNorm2D(C, device="cpu", gain_w=0.3, gain_b=0.2, preserve_var=preserve)
+    r = g(seed)
+    bn.mw = 1.0 + 0.1 * torch.randn(C, generator=r)
+    if not first:
+        bn._is_initialized = True
+        bn.running_mean = torch.randn(C, generator=r)
+        bn.running_var = torch.rand(C, generator=r) + 0.5
+    ref = O.mirror(bn)
+    for a in ("mw", "Sw", "mb", "Sb", "running_mean", "running_var"):
+        setattr(bn, a, getattr(bn, a).to(dev))
+    return bn, ref
+
+
+FUSED_CASES = [
+    # shape, first call, preserve_var, residual add
+    ((16, 64, 8, 8), True, False, True),
+    ((16, 64, 8, 8), False, False, False),
+    ((8, 128, 4, 4), True, True, True),
+    ((3, 6, 5, 5), True, True, True),      # channel count off the float4 path
+    ((128, 16, 4, 4), False, True, False),
+    ((2, 512, 2, 2), True, False, True),
+]
+
+
+@pytest.mark.parametrize("shape,first,preserve,add", FUSED_CASES, ids=[str(c) for c in FUSED_CASES])
+def test_relu_bn_fused(dev, shape, first, preserve, add):
+    from triton_tagi_amd.layers.fused import bn_relu_backward, relu_bn_forward
+    from triton_tagi_amd.layers.relu import ReLU
+
+    N, C, H, W = shape
+    seed = N * 7 + C
+    bn, rbn = make_bn(C, first, preserve, seed, dev)
+    bn_u = copy.deepcopy(bn)
+    relu, relu_u, rrelu = ReLU(), ReLU(), O.OReLU()
+    r = g(seed + 1)
+    mz, Sz = torch.randn(shape, generator=r), 0.05 + torch.rand(shape, generator=r)
+    mz[0, 0, 0, 0] = -40.0  # deep in the asymptotic branch of the ReLU
+    am, aS = torch.randn(shape, generator=r), torch.rand(shape, generator=r)
+    addend = (am.to(dev), aS.to(dev)) if add else None
+
+    ma, Sa = relu_bn_forward(relu, bn, mz.to(dev), Sz.to(dev), addend)
+    # oracle: ReLU, BN, then the add
+    qa, qS = rrelu.forward(d64(mz), d64(Sz))
+    rm, rS = rbn.forward(qa, qS)
+    if add:
+        rm, rS = rm + d64(am), rS + d64(aS)
+    assert_scaled_close(ma, rm, rm.abs() + 1.0, RTOL, ATOL, "fused mean")
+    assert_scaled_close(Sa, rS, None, RTOL, ATOL, "fused var")
+    assert_scaled_close(bn.running_mean, rbn.running_mean, rbn.running_mean.abs() + 1.0, RTOL, ATOL, "running mean")
+    assert_scaled_close(bn.running_var, rbn.running_var, None, RTOL, ATOL, "running var")
+    assert_scaled_close(bn.mw, rbn.mw, None, RTOL, ATOL, "gamma")
+    assert_scaled_close(relu.J, rrelu.J, None, RTOL, ATOL, "ReLU Jacobian")
+
+    # the engine's unfused layers on the same inputs
+    um, uS = relu_u.forward(mz.to(dev), Sz.to(dev))
+    um, uS = bn_u.forward(um, uS)
+    if add:
+        um, uS = um + addend[0], uS + addend[1]
+    close_unfused(ma, um, "mean")
+    close_unfused(Sa, uS, "var")
+    close_unfused(bn.m_hat, bn_u.m_hat, "mhat")
+
+    dma, dSa = torch.randn(shape, generator=r), -torch.rand(shape, generator=r)
+    om, oS = bn_relu_backward(bn, relu, dma.to(dev), dSa.to(dev))
+    qm, qS = rbn.backward(d64(dma), d64(dSa))
+    qm, qS = rrelu.backward(qm, qS)
+    assert_scaled_close(om, qm, None, RTOL, ATOL, "fused bwd mean")
+    assert_scaled_close(oS, qS, None, RTOL, ATOL, "fused bwd var")
+    mh = rbn.m_hat
+    assert_scaled_close(bn.delta_mw, rbn.delta_mw, rbn.Sw * (d64(dma) * mh).abs().sum((0, 2, 3)), RTOL, ATOL,
+                        "delta gamma")
+    assert_scaled_close(bn.delta_Sw, rbn.delta_Sw, None, RTOL, ATOL, "delta Sgamma")
+    assert_scaled_close(bn.delta_mb, rbn.delta_mb, rbn.Sb * d64(dma).abs().sum((0, 2, 3)), RTOL, ATOL, "delta beta")
+    assert_scaled_close(bn.delta_Sb, rbn.delta_Sb, None, RTOL, ATOL, "delta Sbeta")
+
+    vm, vS = bn_u.backward(dma.to(dev), dSa.to(dev))
+    vm, vS = relu_u.backward(vm, vS)
+    close_unfused(om, vm, "bwd mean")
+    close_unfused(oS, vS, "bwd var")
+    close_unfused(bn.delta_mw, bn_u.delta_mw, "delta gamma")
+
+
+ADD_CASES = [
+    # N, C, H, W, Cout, k, stride, padding, padding_type
+    (4, 16, 8, 8, 16, 3, 1, 1, 1),
+    (4, 16, 8, 8, 32, 3, 2, 1, 2),
+    (2, 8, 10, 7, 12, 2, 3, 1, 1),   # stride phases without taps
+    (8, 64, 16, 16, 128, 3, 2, 1, 2),
+]
+
+
+@pytest.mark.parametrize("case", ADD_CASES, ids=[str(c) for c in ADD_CASES])
+def test_conv_bwd_delta_with_addend(dev, case):
+    from triton_tagi_amd.layers.conv2d import Conv2D
+
+    N, C, H, W, Cout, k, s, p, pt = case
+    torch.manual_seed(sum(case))
+    layer = Conv2D(C, Cout, k, stride=s, padding=p, padding_type=pt, device="cpu")
+    ref = O.mirror(layer)
+    for a in ("mw", "Sw", "mb", "Sb"):
+        setattr(layer, a, getattr(layer, a).to(dev))
+    r = g(sum(case) + 5)
+    ma, Sa = torch.randn(N, C, H, W, generator=r), torch.rand(N, C, H, W, generator=r)
+    mz, _ = layer.forward(ma.to(dev), Sa.to(dev))
+    ref.forward(d64(ma), d64(Sa))
+    dm, dS = torch.randn(mz.shape, generator=r), -torch.rand(mz.shape, generator=r)
+    am, aS = torch.randn(N, C, H, W, generator=r), torch.rand(N, C, H, W, generator=r)
+    om, oS = layer._backward(dm.to(dev), dS.to(dev), True, add=(am.to(dev), aS.to(dev)))
+    qm, qS = ref.backward(d64(dm), d64(dS))
+    scale_m = (O.col2im(d64(dm).permute(0, 2, 3, 1).reshape(-1, Cout).abs() @ ref.mw.abs().T, N, C, H, W, k, s, p,
+                        pt)) + d64(am).abs()
+    assert_scaled_close(om, qm + d64(am), scale_m, RTOL, ATOL, "dma + addend")
+    assert_scaled_close(oS, qS + d64(aS), None, RTOL, ATOL, "dSa + addend")
+    um, uS = layer.backward(dm.to(dev), dS.to(dev))
+    close_unfused(om, um + am.to(dev), "dma")
+    close_unfused(oS, uS + aS.to(dev), "dSa")
+
+
+def test_fused_step_matches_oracle(dev):
+    """Sequential.step (fused passes) on ResNet-18 at batch 16 against the oracle's step:
+    predictions, every updated parameter and the BN running statistics."""
+    from triton_tagi_amd import workloads
+
+    w = workloads.build("resnet18", device="cuda:0", batch=16)
+    onet = O.mirror_net(w.net)
+    mu, var = w.net.step(w.x, w.y, w.sigma_v)
+    torch.cuda.synchronize()
+    rmu, rvar = onet.step(w.x.cpu().double(), w.y.cpu().double(), w.sigma_v)
+    failures = []
+
+    def chk(*a):
+        try:
+            assert_scaled_close(*a)
+        except AssertionError as e:
+            failures.append(str(e))
+
+    chk(mu, rmu, rmu.abs() + rmu.abs().mean(), RTOL, ATOL, "predicted mean")
+    chk(var, rvar, None, RTOL, ATOL, "predicted var")
+    gp = []
+    for layer in w.net.layers:
+        items = layer._update_items() if hasattr(layer, "_update_items") else None
+        gp.extend((m, S) for m, S, _, _ in items or [])
+    rp = []
+    for layer in onet.layers:
+        rp.extend((getattr(o, m), getattr(o, S)) for o, m, S, _, _ in layer.param_groups())
+    assert len(gp) == len(rp)
+    for j, ((gm, gS), (rm, rS)) in enumerate(zip(gp, rp)):
+        chk(gm, rm, rm.abs() + rm.abs().mean(), RTOL, ATOL, f"param group {j} mean")
+        chk(gS, rS, None, RTOL, ATOL, f"param group {j} variance")
+    bn, rbn = w.net.layers[2], onet.layers[2]
+    chk(bn.running_mean, rbn.running_mean, rbn.running_mean.abs() + 1.0, RTOL, ATOL, "stem BN running mean")
+    chk(bn.running_var, rbn.running_var, None, RTOL, ATOL, "stem BN running var")
+    assert not failures, "\n".join(failures)
+    assert torch.equal(mu.argmax(-1).cpu(), rmu.argmax(-1))

@@ -74,7 +74,19 @@ static Plan conv_bwd_plan(const tagi_conv_geom* g) {
   int64_t R, K;
   bwd_phase0(g, &R, &K);
   if (K <= 0) K = 1;
-  return choose_plan(R, g->C, K, (int64_t)g->stride * g->stride, 2, g->stride == 1, 16);
+  const ConvG cg = to_g(g);
+  const int nph = cg.stride * cg.stride;
+  int64_t pk[64];
+  if (nph > 64) return choose_plan(R, g->C, K, nph, 2, true, 16);
+  for (int ph = 0; ph < nph; ++ph) {
+    const Phase p = make_phase(cg, ph);
+    pk[ph] = (int64_t)p.nkh * p.nkw * g->Cout;
+  }
+  // Splitting the phases pays only when the unsplit launch leaves CUs idle: the phases
+  // already differ in length, and their partial sums cost more than the balance gains.
+  const Plan p1 = choose_plan(R, g->C, K, nph, 2, false, 1, pk);
+  if ((int64_t)p1.tiles_m * p1.tiles_n * nph >= 512) return p1;
+  return choose_plan(R, g->C, K, nph, 2, true, 16, pk);
 }
 
 static Plan conv_wgrad_plan(const tagi_conv_geom* g) {
@@ -143,12 +155,14 @@ extern "C" int64_t tagi_conv2d_bwd_delta_ws_bytes(const tagi_conv_geom* g) {
   if (!g || g->N <= 0 || g->Cout <= 0 || g->C <= 0 || g->k <= 0 || g->stride <= 0) return 0;
   int64_t R, K;
   bwd_phase0(g, &R, &K);
-  return wt_floats(g) * (int64_t)sizeof(float) + plan_ws_bytes(conv_bwd_plan(g), R, g->C, 1);
+  return wt_floats(g) * (int64_t)sizeof(float) + plan_ws_bytes(conv_bwd_plan(g), R, g->C, g->stride * g->stride);
 }
 
-extern "C" int tagi_conv2d_bwd_delta(const float* dmz, const float* dSz, const float* mw, float* dma, float* dSa,
-                                     const tagi_conv_geom* g, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
-  const char* what = "tagi_conv2d_bwd_delta";
+static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* dSz, const float* mw,
+                               const float* add_m, const float* add_S, float* dma, float* dSa, const tagi_conv_geom* g,
+                               float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+  TAGI_REQUIRE((add_m == nullptr) == (add_S == nullptr), "%s: add_m and add_S must both be given or both be NULL",
+               what);
   int rc = check_geom(g, what);
   if (rc) return rc;
   TAGI_REQUIRE(dmz && dSz && mw && dma && dSa, "%s: null pointer", what);
@@ -188,25 +202,50 @@ extern "C" int tagi_conv2d_bwd_delta(const float* dmz, const float* dSz, const f
   a.epi.ov = dSa;
   a.epi.zdiv = 1;
   a.epi.g = to_g(g);
+  a.epi.am = add_m;
+  a.epi.av = add_S;
   a.R = (int)R0;
   a.C = (int)g->C;
   a.Kred = (int)K0;
   a.phased = 1;
+  {
+    // longest phase reductions first (stable for equal lengths)
+    int64_t kz[64];
+    for (int ph = 0; ph < nph; ++ph) {
+      const Phase q = make_phase(to_g(g), ph);
+      kz[ph] = (int64_t)q.nkh * q.nkw;
+      a.phase_order[ph] = (unsigned char)ph;
+    }
+    for (int i = 1; i < nph; ++i)
+      for (int j = i; j > 0 && kz[a.phase_order[j]] > kz[a.phase_order[j - 1]]; --j) {
+        const unsigned char t = a.phase_order[j];
+        a.phase_order[j] = a.phase_order[j - 1];
+        a.phase_order[j - 1] = t;
+      }
+  }
   Plan p = conv_bwd_plan(g);
   float* part = ws + wt_floats(g);
   const int64_t part_bytes = ws_bytes - wt_floats(g) * (int64_t)sizeof(float);
-  if (p.splits > 1 && part_bytes < plan_ws_bytes(p, R0, g->C, 1)) p = choose_plan(R0, g->C, K0, nph, 2, false, 1);
-  if (nph > 1) {
-    // phases never split; one chunk covers the longest phase reduction
-    p.splits = 1;
-    p.k_chunk = (int)(cdiv(K0 > 0 ? K0 : 1, 16) * 16);
-  }
+  if (p.splits > 1 && part_bytes < plan_ws_bytes(p, R0, g->C, nph)) p = choose_plan(R0, g->C, K0, nph, 2, false, 1);
   const int64_t gx = (int64_t)p.tiles_m * p.tiles_n;  // phase 0 is the largest
   const bool va = g->Cout % 4 == 0 && al16(dmz) && al16(dSz);
   const bool vb = g->C % 4 == 0;
   if (va && vb) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B4>(a, nph, p, part, part_bytes, s, what, gx);
   if (va) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B_S>(a, nph, p, part, part_bytes, s, what, gx);
   return run_gemm<PROD_SHARED_B, LD_CBWD_A_S, LD_CBWD_B_S>(a, nph, p, part, part_bytes, s, what, gx);
+}
+
+extern "C" int tagi_conv2d_bwd_delta(const float* dmz, const float* dSz, const float* mw, float* dma, float* dSa,
+                                     const tagi_conv_geom* g, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+  return conv_bwd_delta_impl("tagi_conv2d_bwd_delta", dmz, dSz, mw, nullptr, nullptr, dma, dSa, g, ws, ws_bytes,
+                             stream);
+}
+
+extern "C" int tagi_conv2d_bwd_delta_add(const float* dmz, const float* dSz, const float* mw, const float* add_m,
+                                         const float* add_S, float* dma, float* dSa, const tagi_conv_geom* g,
+                                         float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+  return conv_bwd_delta_impl("tagi_conv2d_bwd_delta_add", dmz, dSz, mw, add_m, add_S, dma, dSa, g, ws, ws_bytes,
+                             stream);
 }
 
 // ============================================================== parameter deltas

@@ -111,6 +111,8 @@ struct Epi {
   int perm_C, perm_kk2;  // conv: row r = (kh*kk+kw)*C + c maps to weight row c*kk2 + kh*kk + kw
   // kind 2
   ConvG g;
+  const float* am;  // optional addend (same layout as the output): out = delta + addend
+  const float* av;
 };
 
 struct GemmArgs {
@@ -121,6 +123,9 @@ struct GemmArgs {
   int splits, k_chunk;
   int phased;      // conv input delta: z indexes the stride phase
   float* partial;  // split-K partial sums, or null to apply the epilogue in place
+  // phased launches: blockIdx.y / splits -> phase, longest reductions first so the short
+  // phases fill in behind them
+  unsigned char phase_order[64];
 };
 
 template <int BM_, int BN_, int WM_, int WN_>
@@ -432,10 +437,15 @@ __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col,
     // conv input delta: row = pixel q of phase z, col = input channel
     const Phase ph = make_phase(e.g, z);
     const int hq = ph.Hq * ph.Wq;
+    if (row >= e.g.N * hq) return;  // rows past this phase's pixels (split-K reduction covers phase 0's rows)
     const int n = row / hq, rr = row - n * hq;
     const int hh = rr / ph.Wq, ww = rr - hh * ph.Wq;
     const int h = hh * e.g.stride + ph.a, w = ww * e.g.stride + ph.b;
     const int64_t off = (((int64_t)n * e.g.H + h) * e.g.W + w) * e.g.C + col;
+    if (e.am) {
+      m = m + e.am[off];
+      v = v + e.av[off];
+    }
     e.om[off] = m;
     e.ov[off] = v;
   }
@@ -473,9 +483,10 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   const int hl = lane >> 5;
   const int rl = lane & 31;
 
-  const int zz = blockIdx.y;
-  const int z = zz / g.splits;
-  const int split = zz - z * g.splits;
+  const int zq = blockIdx.y / g.splits;
+  const int split = blockIdx.y - zq * g.splits;
+  const int z = g.phased ? (int)g.phase_order[zq] : zq;
+  const int zz = z * g.splits + split;  // partial-sum slot
   const int R = rows_of(g, z);
   const int Kred = kred_of(g, z);
   const int tiles_m = g.phased ? (R + BM - 1) / BM : g.tiles_m;
@@ -512,6 +523,8 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
       }
 
   const int nk = kbeg < kend ? (kend - kbeg + BK - 1) / BK : 0;
+  // a split past this phase's reduction contributes nothing; the reduction skips it
+  if (g.phased && g.partial && nk == 0) return;
   if (nk > 0) {
     la.fetch(g.a, z, m0, kbeg);
     lb.fetch(g.b, z, n0, kbeg);
@@ -611,24 +624,97 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
       }
 }
 
-// Deterministic split-K reduction (fixed split order) followed by the epilogue.
-template <int UNUSED = 0>
-__global__ void splitk_reduce_kernel(const float* __restrict__ partial, Epi epi, int batch, int splits, int R, int C) {
+// Deterministic split-K reduction followed by the epilogue. A block owns 64*V consecutive
+// output elements; its G waves each sum the splits s = g, g+G, g+2G, ... of those
+// elements (V at a time), then wave 0 adds the G wave sums in order g = 0..G-1. The
+// summation order depends only on (splits, G), so results repeat bit for bit.
+// For the phased conv input delta (k_chunk > 0) phase z sums only the splits that
+// cover its own reduction length.
+template <int G, int V>
+__global__ void __launch_bounds__(64 * G) splitk_reduce_kernel(const float* __restrict__ partial, Epi epi, int batch,
+                                                                int splits, int R, int C, int k_chunk) {
+  __shared__ float red[G > 1 ? 2 * (G - 1) * 64 * V : 1];
   const int64_t plane = (int64_t)R * C;
   const int64_t total = plane * batch;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int z = (int)(idx / plane);
-    const int64_t rc = idx - (int64_t)z * plane;
-    const int row = (int)(rc / C);
-    const int col = (int)(rc - (int64_t)row * C);
-    float m = 0.f, v = 0.f;
+  const int lane = threadIdx.x & 63;
+  const int g = threadIdx.x >> 6;
+  const int64_t idx0 = ((int64_t)blockIdx.x * 64 + lane) * V;
+  float m[V], v[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) m[e] = v[e] = 0.f;
+  int z = 0;
+  int64_t rc = 0;
+  if (idx0 < total) {
+    z = (int)(idx0 / plane);
+    rc = idx0 - (int64_t)z * plane;
     const float* p = partial + ((int64_t)z * splits * 2) * plane + rc;
-    for (int s = 0; s < splits; ++s) {
-      m += p[(2 * s) * plane];
-      v += p[(2 * s + 1) * plane];
+    int ns = splits;
+    if (k_chunk > 0) {
+      const Phase ph = make_phase(epi.g, z);
+      const int kz = ph.nkh * ph.nkw * epi.g.Cout;
+      ns = min(splits, (kz + k_chunk - 1) / k_chunk);
     }
-    epi_apply(epi, z, row, col, m, v);
+    if constexpr (V == 4) {
+      // plane % 4 == 0: the 4 elements lie in one plane, 16-byte aligned
+      for (int s = g; s < ns; s += G) {
+        const float4 a = *reinterpret_cast<const float4*>(p + (int64_t)(2 * s) * plane);
+        const float4 b = *reinterpret_cast<const float4*>(p + (int64_t)(2 * s + 1) * plane);
+        m[0] += a.x; m[1] += a.y; m[2] += a.z; m[3] += a.w;
+        v[0] += b.x; v[1] += b.y; v[2] += b.z; v[3] += b.w;
+      }
+    } else {
+      for (int s = g; s < ns; s += G) {
+        m[0] += p[(int64_t)(2 * s) * plane];
+        v[0] += p[(int64_t)(2 * s + 1) * plane];
+      }
+    }
+  }
+  if constexpr (G > 1) {
+    if (g > 0) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        red[((g - 1) * 2) * 64 * V + lane * V + e] = m[e];
+        red[((g - 1) * 2 + 1) * 64 * V + lane * V + e] = v[e];
+      }
+    }
+    __syncthreads();
+    if (g != 0) return;
+#pragma unroll
+    for (int h = 1; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        m[e] += red[((h - 1) * 2) * 64 * V + lane * V + e];
+        v[e] += red[((h - 1) * 2 + 1) * 64 * V + lane * V + e];
+      }
+  }
+  if (idx0 >= total) return;
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    const int64_t r = rc + e;
+    if (V > 1 && idx0 + e >= total) break;
+    const int row = (int)(r / C);
+    const int col = (int)(r - (int64_t)row * C);
+    epi_apply(epi, z, row, col, m[e], v[e]);
+  }
+}
+
+static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <int V>
+static inline void launch_reduce(const float* ws, const Epi& epi, int64_t batch, int splits, int R, int C,
+                                 int k_chunk, hipStream_t s) {
+  const int64_t total = (int64_t)R * C * batch;
+  const int64_t blocks = cdiv(total, 64 * V);
+  // enough waves in flight to cover HBM latency: aim for ~4096 waves over the chip
+  int G = 1;
+  while (G < 16 && G * 2 <= splits && blocks * G < 4096) G *= 2;
+  const dim3 grid((unsigned)blocks);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((splitk_reduce_kernel<1, V>), grid, dim3(64), 0, s, ws, epi, (int)batch, splits, R, C, k_chunk); break;
+    case 2: hipLaunchKernelGGL((splitk_reduce_kernel<2, V>), grid, dim3(128), 0, s, ws, epi, (int)batch, splits, R, C, k_chunk); break;
+    case 4: hipLaunchKernelGGL((splitk_reduce_kernel<4, V>), grid, dim3(256), 0, s, ws, epi, (int)batch, splits, R, C, k_chunk); break;
+    case 8: hipLaunchKernelGGL((splitk_reduce_kernel<8, V>), grid, dim3(512), 0, s, ws, epi, (int)batch, splits, R, C, k_chunk); break;
+    default: hipLaunchKernelGGL((splitk_reduce_kernel<16, V>), grid, dim3(1024), 0, s, ws, epi, (int)batch, splits, R, C, k_chunk); break;
   }
 }
 
@@ -658,33 +744,45 @@ struct Plan {
 // holds ceil(blocks / 256) blocks; its MFMA time is inflated by the per-tile load
 // overhead (small tiles re-read more operand bytes per flop) and by low occupancy
 // (fewer than ~3 waves per SIMD leave load latency exposed). Split-K adds the HBM round
-// trip of the partial sums plus one launch.
-static inline Plan choose_plan(int64_t R, int64_t C, int64_t Kred, int64_t batch, int products, bool allow_split,
-                               int64_t max_splits) {
+// trip of the partial sums (written by the GEMM, read back by the reduction) plus one
+// launch. Every split count up to max_splits is tried (not only powers of two), so the
+// block count can match the CU count without extra partial sums.
+//
+// phase_k (optional, batch entries): per-GEMM reduction lengths when they differ (stride
+// phases of the conv input delta); splits past a GEMM's own length launch no work.
+static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int64_t batch, int products,
+                                        bool allow_split, int64_t max_splits, const int64_t* phase_k) {
   // resident blocks per CU (LDS / register limited) and waves per block, per config
   static const int kBpc[] = {2, 3, 3, 4, 8};
   static const int kWaves[] = {8, 4, 4, 4, 1};
   Plan best{kNumCfg - 1, 1, (int)Kred, 1, 1};
   double best_t = DBL_MAX;
   const double peak_cu = 157.3e12 / 256.0;
+  const int64_t max_sp = allow_split ? (max_splits < 512 ? max_splits : 512) : 1;
   for (int ci = 0; ci < kNumCfg; ++ci) {
     const int BM = kCfg[ci].BM, BN = kCfg[ci].BN;
     const int64_t tm = cdiv(R, BM), tn = cdiv(C, BN);
-    for (int64_t sp = 1; sp <= 512; sp *= 2) {
-      if (sp > 1 && (!allow_split || sp > max_splits)) break;
+    int64_t prev_actual = -1;
+    for (int64_t sp = 1; sp <= max_sp; ++sp) {
       int64_t kc = cdiv(cdiv(Kred, sp), 16) * 16;
       if (kc < 16) kc = 16;
       const int64_t actual = cdiv(Kred, kc);
-      if (sp > 1 && actual < sp) break;
-      if (sp > 1 && kc < 64) break;  // splits below 4 k-tiles only add reduction traffic
-      const int64_t blocks = tm * tn * batch * actual;
+      if (actual == prev_actual) continue;
+      prev_actual = actual;
+      if (actual > 1 && kc < 64) break;  // splits below 4 k-tiles only add reduction traffic
+      int64_t blocks = tm * tn * batch * actual;
+      if (phase_k) {
+        blocks = 0;
+        for (int64_t z = 0; z < batch; ++z) blocks += tm * tn * (phase_k[z] > 0 ? cdiv(phase_k[z], kc) : 1);
+      }
       const int64_t rounds = cdiv(blocks, 256);
       const int64_t resident = rounds < kBpc[ci] ? rounds : kBpc[ci];
       const double wps = (double)resident * kWaves[ci] / 4.0;  // waves per SIMD
       const double occ = wps >= 3.0 ? 1.0 : (wps >= 2.0 ? 0.85 : (wps >= 1.0 ? 0.6 : 0.35));
       const double tile = 1.0 / (1.0 + 32.0 / BM + 32.0 / BN);
       double t = rounds * (2.0 * BM * BN * kc * products) / (peak_cu * tile * occ);
-      if (actual > 1) t += (double)(actual * 2 + 2) * R * C * batch * 4.0 / 5.0e12 + 5e-6;
+      // partial sums: 8 bytes per element and split, written once and read back once
+      if (actual > 1) t += (double)actual * 16.0 * R * C * batch / 5.0e12 + 4e-6;
       if (t < best_t * 0.999) {
         best_t = t;
         best = Plan{ci, (int)actual, (int)kc, (int)tm, (int)tn};
@@ -692,6 +790,37 @@ static inline Plan choose_plan(int64_t R, int64_t C, int64_t Kred, int64_t batch
     }
   }
   return best;
+}
+
+// Plans are pure functions of the problem shape; memoise them per host thread (the
+// search above costs a few microseconds and the same shapes recur every step).
+static inline Plan choose_plan(int64_t R, int64_t C, int64_t Kred, int64_t batch, int products, bool allow_split,
+                               int64_t max_splits, const int64_t* phase_k = nullptr) {
+  struct Key {
+    int64_t R, C, K, batch, max_splits, salt;
+    int products, allow;
+  };
+  int64_t salt = 0;
+  if (phase_k)
+    for (int64_t z = 0; z < batch; ++z) salt = salt * 1000003 + phase_k[z] + 1;
+  struct Entry {
+    Key k;
+    Plan p;
+  };
+  static thread_local Entry cache[64];
+  static thread_local int used = 0, next = 0;
+  const Key key{R, C, Kred, batch, max_splits, salt, products, allow_split ? 1 : 0};
+  for (int i = 0; i < used; ++i) {
+    const Key& k = cache[i].k;
+    if (k.R == R && k.C == C && k.K == Kred && k.batch == batch && k.max_splits == max_splits && k.salt == salt &&
+        k.products == products && k.allow == key.allow)
+      return cache[i].p;
+  }
+  const Plan p = choose_plan_uncached(R, C, Kred, batch, products, allow_split, max_splits, phase_k);
+  cache[next] = Entry{key, p};
+  next = (next + 1) % 64;
+  if (used < 64) ++used;
+  return p;
 }
 
 static inline int64_t plan_ws_bytes(const Plan& p, int64_t R, int64_t C, int64_t batch) {
@@ -734,9 +863,10 @@ static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, 
   int rc = check_launch(what);
   if (rc != TAGI_OK) return rc;
   if (p.splits > 1) {
-    const int64_t total = (int64_t)g.R * g.C * batch;
-    hipLaunchKernelGGL(splitk_reduce_kernel<0>, dim3(ew_blocks(total, 256)), dim3(256), 0, s, (const float*)ws, g.epi,
-                       (int)batch, p.splits, g.R, g.C);
+    if (((int64_t)g.R * g.C) % 4 == 0 && al16(ws))
+      launch_reduce<4>(ws, g.epi, batch, p.splits, g.R, g.C, g.phased ? p.k_chunk : 0, s);
+    else
+      launch_reduce<1>(ws, g.epi, batch, p.splits, g.R, g.C, g.phased ? p.k_chunk : 0, s);
     rc = check_launch(what);
   }
   return rc;
@@ -796,6 +926,5 @@ static inline Epi epi_wgrad(float* dmw, float* dSw, float* dmb, float* dSb, cons
 
 static inline bool fits_i32(int64_t v) { return v >= 0 && v < (1ll << 31); }
 
-static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace tagi

@@ -4,6 +4,7 @@
 // partial sums to a caller-provided workspace in a fixed layout, and a small finalize
 // kernel adds them in a fixed order (no float atomics anywhere).
 #include "tagi_common.h"
+#include "tagi_moments.h"
 
 namespace tagi {
 
@@ -21,15 +22,52 @@ static inline int bn_blocks(int64_t rows, int64_t C) {
 
 static inline bool bn_vec(int64_t C) { return C % 4 == 0 && C <= 1024 && 1024 % C == 0; }
 
-template <int NQ, bool VEC>
+// Per-block partial sums over the block's rows (finalized by the kernels below).
+//   MODE 0  statistics of (mu, S):                   sums mu, S, mu^2
+//   MODE 1  statistics of ReLU(mu, S), writes y0 = J: sums mu_a, S_a, mu_a^2
+//   MODE 2  backward, x0 = dmu, x1 = dS, x2 = mhat:   y0 = dmu g/sqrt(var+eps),
+//           y1 = dS g^2/(var+eps); sums dmu mhat, dS mhat^2, dmu, dS
+//   MODE 3  MODE 2 followed by the Jacobian of the ReLU in front of the BN (x3 = J):
+//           y0 = (dmu g/sqrt(var+eps)) J, y1 = (dS g^2/(var+eps)) J^2; same sums
+template <int MODE>
+struct BnRed {
+  static constexpr int NQ = MODE >= 2 ? 4 : 3;
+  __device__ __forceinline__ static void elem(float a, float b, float h, float j, float km, float kS, float* acc,
+                                              float& o0, float& o1) {
+    if constexpr (MODE == 0) {
+      acc[0] += a;
+      acc[1] += b;
+      acc[2] += a * a;
+    } else if constexpr (MODE == 1) {
+      float ma, Sa, J;
+      relu_moments(a, b, ma, Sa, J);
+      acc[0] += ma;
+      acc[1] += Sa;
+      acc[2] += ma * ma;
+      o0 = J;
+    } else {
+      acc[0] += a * h;
+      acc[1] += b * h * h;
+      acc[2] += a;
+      acc[3] += b;
+      o0 = a * km;
+      o1 = b * kS;
+      if constexpr (MODE == 3) {
+        o0 = o0 * j;
+        o1 = o1 * j * j;
+      }
+    }
+  }
+};
+
+template <int MODE, bool VEC>
 __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict__ x0, const float* __restrict__ x1,
-                                                        const float* __restrict__ x2, float* __restrict__ ws,
-                                                        int64_t rows, int C, int nblk, int mode,
+                                                        const float* __restrict__ x2, const float* __restrict__ x3,
+                                                        float* __restrict__ ws, int64_t rows, int C, int nblk,
                                                         const float* __restrict__ var, const float* __restrict__ mg,
                                                         float* __restrict__ y0, float* __restrict__ y1, float eps) {
-  // mode 0 (stats):    x0 = mu, x1 = S;            sums mu, S, mu^2
-  // mode 1 (backward): x0 = dmu, x1 = dS, x2 = mhat; sums dmu mhat, dS mhat^2, dmu, dS, and
-  //                    writes y0 = dmu g/sqrt(var+eps), y1 = dS g^2/(var+eps)
+  using R = BnRed<MODE>;
+  constexpr int NQ = R::NQ;
   __shared__ float red[256 * 4 * NQ];
   const int64_t r0 = rows * blockIdx.x / nblk, r1 = rows * (blockIdx.x + 1) / nblk;
   const int t = threadIdx.x;
@@ -42,7 +80,7 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
 #pragma unroll
       for (int q = 0; q < NQ; ++q) acc[j][q] = 0.f;
     float km[4] = {0, 0, 0, 0}, kS[4] = {0, 0, 0, 0};
-    if (mode == 1) {
+    if constexpr (MODE >= 2) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int c = 4 * c4 + j;
@@ -51,34 +89,21 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
         kS[j] = mg[c] * mg[c] * (1.0f / rv);
       }
     }
-    if (rr < rpi) {
-#pragma unroll 4
-      for (int64_t row = r0 + rr; row < r1; row += rpi) {
-        const int64_t off = row * C + 4 * c4;
-        const float4 a = *reinterpret_cast<const float4*>(x0 + off);
-        const float4 b = *reinterpret_cast<const float4*>(x1 + off);
-        const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-        if (mode == 0) {
+#pragma unroll 2
+    for (int64_t row = r0 + rr; row < r1; row += rpi) {
+      const int64_t off = row * C + 4 * c4;
+      const float4 a = *reinterpret_cast<const float4*>(x0 + off);
+      const float4 b = *reinterpret_cast<const float4*>(x1 + off);
+      float4 h = make_float4(0.f, 0.f, 0.f, 0.f), jj = h;
+      if constexpr (MODE >= 2) h = *reinterpret_cast<const float4*>(x2 + off);
+      if constexpr (MODE == 3) jj = *reinterpret_cast<const float4*>(x3 + off);
+      const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+      const float hv[4] = {h.x, h.y, h.z, h.w}, jv[4] = {jj.x, jj.y, jj.z, jj.w};
+      float o0[4], o1[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc[j][0] += av[j];
-            acc[j][1] += bv[j];
-            acc[j][2] += av[j] * av[j];
-          }
-        } else {
-          const float4 h = *reinterpret_cast<const float4*>(x2 + off);
-          const float hv[4] = {h.x, h.y, h.z, h.w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc[j][0] += av[j] * hv[j];
-            acc[j][1] += bv[j] * hv[j] * hv[j];
-            acc[j][2] += av[j];
-            if constexpr (NQ == 4) acc[j][3] += bv[j];
-          }
-          *reinterpret_cast<float4*>(y0 + off) = make_float4(a.x * km[0], a.y * km[1], a.z * km[2], a.w * km[3]);
-          *reinterpret_cast<float4*>(y1 + off) = make_float4(b.x * kS[0], b.y * kS[1], b.z * kS[2], b.w * kS[3]);
-        }
-      }
+      for (int j = 0; j < 4; ++j) R::elem(av[j], bv[j], hv[j], jv[j], km[j], kS[j], acc[j], o0[j], o1[j]);
+      if constexpr (MODE >= 1) *reinterpret_cast<float4*>(y0 + off) = make_float4(o0[0], o0[1], o0[2], o0[3]);
+      if constexpr (MODE >= 2) *reinterpret_cast<float4*>(y1 + off) = make_float4(o1[0], o1[1], o1[2], o1[3]);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -99,27 +124,19 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
 #pragma unroll
       for (int q = 0; q < NQ; ++q) acc[q] = 0.f;
       float kmc = 0.f, kSc = 0.f;
-      if (mode == 1) {
+      if constexpr (MODE >= 2) {
         const float rv = var[c] + eps;
         kmc = mg[c] * (1.0f / sqrtf(rv));
         kSc = mg[c] * mg[c] * (1.0f / rv);
       }
       for (int64_t row = r0; row < r1; ++row) {
         const int64_t off = row * C + c;
-        const float a = x0[off], b = x1[off];
-        if (mode == 0) {
-          acc[0] += a;
-          acc[1] += b;
-          acc[2] += a * a;
-        } else {
-          const float h = x2[off];
-          acc[0] += a * h;
-          acc[1] += b * h * h;
-          acc[2] += a;
-          if constexpr (NQ == 4) acc[3] += b;
-          y0[off] = a * kmc;
-          y1[off] = b * kSc;
-        }
+        const float h = MODE >= 2 ? x2[off] : 0.f;
+        const float j = MODE == 3 ? x3[off] : 0.f;
+        float o0 = 0.f, o1 = 0.f;
+        R::elem(x0[off], x1[off], h, j, kmc, kSc, acc, o0, o1);
+        if constexpr (MODE >= 1) y0[off] = o0;
+        if constexpr (MODE >= 2) y1[off] = o1;
       }
       for (int q = 0; q < NQ; ++q) ws[((int64_t)blockIdx.x * C + c) * NQ + q] = acc[q];
     }
@@ -170,50 +187,105 @@ __global__ void bn_stats_finalize_kernel(const float* __restrict__ ws, float* __
 }
 
 // --------------------------------------------------------------------- BN apply
-__global__ void bn_fwd_kernel(const float* __restrict__ mz, const float* __restrict__ Sz,
-                              const float* __restrict__ mean, const float* __restrict__ var,
-                              const float* __restrict__ mg, const float* __restrict__ Sg,
-                              const float* __restrict__ mb, const float* __restrict__ Sb, float* __restrict__ ma,
-                              float* __restrict__ Sa, float* __restrict__ mhat, float* __restrict__ Shat, int64_t total,
-                              int C, float eps, bool vec) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  if (vec) {
-    const int64_t t4 = total >> 2;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < t4; i += stride) {
-      const int c0 = (int)((i << 2) % C);
-      const float4 m = reinterpret_cast<const float4*>(mz)[i];
-      const float4 s = reinterpret_cast<const float4*>(Sz)[i];
-      const float mv[4] = {m.x, m.y, m.z, m.w}, sv[4] = {s.x, s.y, s.z, s.w};
-      float mh[4], sh[4], om[4], os[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = c0 + j;
-        const float rv = var[c] + eps;
-        const float inv_std = 1.0f / sqrtf(rv);
-        const float g = mg[c], sg = Sg[c];
-        mh[j] = (mv[j] - mean[c]) * inv_std;
-        sh[j] = sv[j] / rv;
-        om[j] = g * mh[j] + mb[c];
-        os[j] = g * g * sh[j] + sg * mh[j] * mh[j] + sg * sh[j] + Sb[c];
-      }
-      reinterpret_cast<float4*>(ma)[i] = make_float4(om[0], om[1], om[2], om[3]);
-      reinterpret_cast<float4*>(Sa)[i] = make_float4(os[0], os[1], os[2], os[3]);
-      reinterpret_cast<float4*>(mhat)[i] = make_float4(mh[0], mh[1], mh[2], mh[3]);
-      if (Shat) reinterpret_cast<float4*>(Shat)[i] = make_float4(sh[0], sh[1], sh[2], sh[3]);
-    }
+// Normalise + Gaussian affine (batchnorm2d.py:59-126), optionally on the ReLU moments of
+// the input (RELU: the rectified moments are recomputed from mu, S instead of being
+// read back) and optionally adding a second Gaussian stream to the output (ADD: the
+// residual shortcut of the block the BN closes).
+template <bool RELU>
+__device__ __forceinline__ void bn_in(float m, float s, float& x, float& v) {
+  if constexpr (RELU) {
+    float J;
+    relu_moments(m, s, x, v, J);
   } else {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-      const int c = (int)(i % C);
-      const float rv = var[c] + eps;
-      const float inv_std = 1.0f / sqrtf(rv);
-      const float g = mg[c], sg = Sg[c];
-      const float mh = (mz[i] - mean[c]) * inv_std;
-      const float sh = Sz[i] / rv;
-      ma[i] = g * mh + mb[c];
-      Sa[i] = g * g * sh + sg * mh * mh + sg * sh + Sb[c];
-      mhat[i] = mh;
-      if (Shat) Shat[i] = sh;
+    x = m;
+    v = s;
+  }
+}
+
+template <bool RELU, bool ADD>
+__global__ void __launch_bounds__(256) bn_apply_vec_kernel(
+    const float* __restrict__ mz, const float* __restrict__ Sz, const float* __restrict__ mean,
+    const float* __restrict__ var, const float* __restrict__ mg, const float* __restrict__ Sg,
+    const float* __restrict__ mb, const float* __restrict__ Sb, const float* __restrict__ am,
+    const float* __restrict__ aS, float* __restrict__ ma, float* __restrict__ Sa, float* __restrict__ mhat,
+    float* __restrict__ Shat, int64_t rows, int C, int64_t rows_per_block, float eps) {
+  const int cq = C >> 2, rpi = 256 / cq;
+  const int t = threadIdx.x, c4 = t % cq, rr = t / cq;
+  float k_mean[4], k_rv[4], k_is[4], k_g[4], k_sg[4], k_b[4], k_sb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = 4 * c4 + j;
+    k_mean[j] = mean[c];
+    k_rv[j] = var[c] + eps;
+    k_is[j] = 1.0f / sqrtf(k_rv[j]);
+    k_g[j] = mg[c];
+    k_sg[j] = Sg[c];
+    k_b[j] = mb[c];
+    k_sb[j] = Sb[c];
+  }
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
+#pragma unroll 2
+  for (int64_t row = r0 + rr; row < r1; row += rpi) {
+    const int64_t off = row * C + 4 * c4;
+    const float4 m4 = *reinterpret_cast<const float4*>(mz + off);
+    const float4 s4 = *reinterpret_cast<const float4*>(Sz + off);
+    float4 a4 = make_float4(0.f, 0.f, 0.f, 0.f), b4 = a4;
+    if constexpr (ADD) {
+      a4 = *reinterpret_cast<const float4*>(am + off);
+      b4 = *reinterpret_cast<const float4*>(aS + off);
     }
+    const float mv[4] = {m4.x, m4.y, m4.z, m4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+    const float av[4] = {a4.x, a4.y, a4.z, a4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+    float mh[4], sh[4], om[4], os[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x, v;
+      bn_in<RELU>(mv[j], sv[j], x, v);
+      mh[j] = (x - k_mean[j]) * k_is[j];
+      sh[j] = v / k_rv[j];
+      om[j] = k_g[j] * mh[j] + k_b[j];
+      os[j] = k_g[j] * k_g[j] * sh[j] + k_sg[j] * mh[j] * mh[j] + k_sg[j] * sh[j] + k_sb[j];
+      if constexpr (ADD) {
+        om[j] = om[j] + av[j];
+        os[j] = os[j] + bv[j];
+      }
+    }
+    *reinterpret_cast<float4*>(ma + off) = make_float4(om[0], om[1], om[2], om[3]);
+    *reinterpret_cast<float4*>(Sa + off) = make_float4(os[0], os[1], os[2], os[3]);
+    *reinterpret_cast<float4*>(mhat + off) = make_float4(mh[0], mh[1], mh[2], mh[3]);
+    if (Shat) *reinterpret_cast<float4*>(Shat + off) = make_float4(sh[0], sh[1], sh[2], sh[3]);
+  }
+}
+
+template <bool RELU, bool ADD>
+__global__ void bn_apply_scalar_kernel(const float* __restrict__ mz, const float* __restrict__ Sz,
+                                       const float* __restrict__ mean, const float* __restrict__ var,
+                                       const float* __restrict__ mg, const float* __restrict__ Sg,
+                                       const float* __restrict__ mb, const float* __restrict__ Sb,
+                                       const float* __restrict__ am, const float* __restrict__ aS,
+                                       float* __restrict__ ma, float* __restrict__ Sa, float* __restrict__ mhat,
+                                       float* __restrict__ Shat, int64_t total, int C, float eps) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int c = (int)(i % C);
+    const float rv = var[c] + eps;
+    const float inv_std = 1.0f / sqrtf(rv);
+    const float g = mg[c], sg = Sg[c];
+    float x, v;
+    bn_in<RELU>(mz[i], Sz[i], x, v);
+    const float mh = (x - mean[c]) * inv_std;
+    const float sh = v / rv;
+    float om = g * mh + mb[c];
+    float os = g * g * sh + sg * mh * mh + sg * sh + Sb[c];
+    if constexpr (ADD) {
+      om = om + am[i];
+      os = os + aS[i];
+    }
+    ma[i] = om;
+    Sa[i] = os;
+    mhat[i] = mh;
+    if (Shat) Shat[i] = sh;
   }
 }
 
@@ -410,25 +482,36 @@ extern "C" int64_t tagi_bn_stats_ws_bytes(int64_t N, int64_t C, int64_t HW) {
 
 static inline bool al16p(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-extern "C" int tagi_bn_stats(const float* mz, const float* Sz, float* batch_mean, float* batch_var,
-                             float* running_mean, float* running_var, float* mg, int64_t N, int64_t C, int64_t HW,
-                             float momentum, float eps, int first_call, int preserve_var, float* ws, int64_t ws_bytes,
-                             tagi_stream_t stream) {
-  const char* what = "tagi_bn_stats";
-  TAGI_REQUIRE(mz && Sz && batch_mean && batch_var && ws, "%s: null pointer", what);
+// Statistics pass (MODE 0 or 1) + finalize: batch mean/var and running-stat bookkeeping.
+static int bn_stats_impl(const char* what, bool relu, const float* mz, const float* Sz, float* J, float* batch_mean,
+                         float* batch_var, float* running_mean, float* running_var, float* mg, int64_t N, int64_t C,
+                         int64_t HW, float momentum, float eps, int first_call, int preserve_var, float* ws,
+                         int64_t ws_bytes, tagi_stream_t stream) {
+  TAGI_REQUIRE(mz && Sz && batch_mean && batch_var && ws && (!relu || J), "%s: null pointer", what);
   TAGI_REQUIRE(N > 0 && C > 0 && HW > 0 && N * HW > 1, "%s: bad sizes", what);
   TAGI_REQUIRE(N * C * HW < (1ll << 40), "%s: too large", what);
   TAGI_REQUIRE(ws_bytes >= tagi_bn_stats_ws_bytes(N, C, HW), "%s: workspace too small", what);
   hipStream_t s = as_stream(stream);
-  ProfScope ps(FAM_BN_STATS, s, 0.0, 8.0 * N * C * HW);
+  ProfScope ps(FAM_BN_STATS, s, 0.0, (relu ? 12.0 : 8.0) * N * C * HW);
   const int64_t rows = N * HW;
   const int nblk = bn_blocks(rows, C);
-  if (bn_vec(C) && al16p(mz) && al16p(Sz))
-    hipLaunchKernelGGL((bn_reduce_kernel<3, true>), dim3(nblk), dim3(256), 0, s, mz, Sz, nullptr, ws, rows, (int)C,
-                       nblk, 0, nullptr, nullptr, nullptr, nullptr, 0.f);
-  else
-    hipLaunchKernelGGL((bn_reduce_kernel<3, false>), dim3(nblk), dim3(256), 0, s, mz, Sz, nullptr, ws, rows, (int)C,
-                       nblk, 0, nullptr, nullptr, nullptr, nullptr, 0.f);
+  const bool vec = bn_vec(C) && al16p(mz) && al16p(Sz) && (!relu || al16p(J));
+  const dim3 grid(nblk), blk(256);
+  if (relu) {
+    if (vec)
+      hipLaunchKernelGGL((bn_reduce_kernel<1, true>), grid, blk, 0, s, mz, Sz, nullptr, nullptr, ws, rows, (int)C,
+                         nblk, nullptr, nullptr, J, nullptr, 0.f);
+    else
+      hipLaunchKernelGGL((bn_reduce_kernel<1, false>), grid, blk, 0, s, mz, Sz, nullptr, nullptr, ws, rows, (int)C,
+                         nblk, nullptr, nullptr, J, nullptr, 0.f);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((bn_reduce_kernel<0, true>), grid, blk, 0, s, mz, Sz, nullptr, nullptr, ws, rows, (int)C,
+                         nblk, nullptr, nullptr, nullptr, nullptr, 0.f);
+    else
+      hipLaunchKernelGGL((bn_reduce_kernel<0, false>), grid, blk, 0, s, mz, Sz, nullptr, nullptr, ws, rows, (int)C,
+                         nblk, nullptr, nullptr, nullptr, nullptr, 0.f);
+  }
   int rc = check_launch(what);
   if (rc) return rc;
   hipLaunchKernelGGL(bn_stats_finalize_kernel, dim3((unsigned)C), dim3(64), 0, s, (const float*)ws,
@@ -437,20 +520,77 @@ extern "C" int tagi_bn_stats(const float* mz, const float* Sz, float* batch_mean
   return check_launch(what);
 }
 
-extern "C" int tagi_bn_fwd(const float* mz, const float* Sz, const float* mean, const float* var, const float* mg,
-                           const float* Sg, const float* mb, const float* Sb, float* ma, float* Sa, float* mhat,
-                           float* Shat, int64_t N, int64_t C, int64_t HW, float eps, tagi_stream_t stream) {
-  const char* what = "tagi_bn_fwd";
+extern "C" int tagi_bn_stats(const float* mz, const float* Sz, float* batch_mean, float* batch_var,
+                             float* running_mean, float* running_var, float* mg, int64_t N, int64_t C, int64_t HW,
+                             float momentum, float eps, int first_call, int preserve_var, float* ws, int64_t ws_bytes,
+                             tagi_stream_t stream) {
+  return bn_stats_impl("tagi_bn_stats", false, mz, Sz, nullptr, batch_mean, batch_var, running_mean, running_var, mg,
+                       N, C, HW, momentum, eps, first_call, preserve_var, ws, ws_bytes, stream);
+}
+
+extern "C" int tagi_relu_bn_stats(const float* mz, const float* Sz, float* J, float* batch_mean, float* batch_var,
+                                  float* running_mean, float* running_var, float* mg, int64_t N, int64_t C, int64_t HW,
+                                  float momentum, float eps, int first_call, int preserve_var, float* ws,
+                                  int64_t ws_bytes, tagi_stream_t stream) {
+  return bn_stats_impl("tagi_relu_bn_stats", true, mz, Sz, J, batch_mean, batch_var, running_mean, running_var, mg,
+                       N, C, HW, momentum, eps, first_call, preserve_var, ws, ws_bytes, stream);
+}
+
+static int bn_apply_impl(const char* what, bool relu, const float* mz, const float* Sz, const float* mean,
+                         const float* var, const float* mg, const float* Sg, const float* mb, const float* Sb,
+                         const float* am, const float* aS, float* ma, float* Sa, float* mhat, float* Shat, int64_t N,
+                         int64_t C, int64_t HW, float eps, tagi_stream_t stream) {
   TAGI_REQUIRE(mz && Sz && mean && var && mg && Sg && mb && Sb && ma && Sa && mhat, "%s: null pointer", what);
+  TAGI_REQUIRE((am == nullptr) == (aS == nullptr), "%s: add_m and add_S must both be given or both be NULL", what);
   TAGI_REQUIRE(N > 0 && C > 0 && HW > 0, "%s: bad sizes", what);
   hipStream_t s = as_stream(stream);
   const int64_t total = N * C * HW;
-  ProfScope ps(FAM_BN_FWD, s, 0.0, 4.0 * total * (Shat ? 6 : 5));
-  const bool vec = (C % 4 == 0) && al16p(mz) && al16p(Sz) && al16p(ma) && al16p(Sa) && al16p(mhat) &&
-                   (Shat == nullptr || al16p(Shat));
-  hipLaunchKernelGGL(bn_fwd_kernel, dim3(ew_blocks(vec ? total / 4 : total, 256)), dim3(256), 0, s, mz, Sz, mean, var,
-                     mg, Sg, mb, Sb, ma, Sa, mhat, Shat, total, (int)C, eps, vec);
+  const bool add = am != nullptr;
+  ProfScope ps(FAM_BN_FWD, s, 0.0, 4.0 * total * ((Shat ? 6 : 5) + (add ? 2 : 0)));
+  const bool vec = bn_vec(C) && al16p(mz) && al16p(Sz) && al16p(ma) && al16p(Sa) && al16p(mhat) &&
+                   (Shat == nullptr || al16p(Shat)) && (!add || (al16p(am) && al16p(aS)));
+  if (vec) {
+    const int64_t rows = N * HW;
+    const int rpi = (int)(256 / (C / 4));
+    // about four float4 rows per thread, at least one row slot per block
+    int64_t rpb = (int64_t)rpi * 4;
+    const int64_t blocks = cdiv(rows, rpb);
+    const dim3 grid((unsigned)blocks), blk(256);
+#define TAGI_BN_APPLY(R, A)                                                                                         \
+  hipLaunchKernelGGL((bn_apply_vec_kernel<R, A>), grid, blk, 0, s, mz, Sz, mean, var, mg, Sg, mb, Sb, am, aS, ma, \
+                     Sa, mhat, Shat, rows, (int)C, rpb, eps)
+    if (relu && add) TAGI_BN_APPLY(true, true);
+    else if (relu) TAGI_BN_APPLY(true, false);
+    else if (add) TAGI_BN_APPLY(false, true);
+    else TAGI_BN_APPLY(false, false);
+#undef TAGI_BN_APPLY
+  } else {
+    const dim3 grid(ew_blocks(total, 256)), blk(256);
+#define TAGI_BN_APPLY(R, A)                                                                                           \
+  hipLaunchKernelGGL((bn_apply_scalar_kernel<R, A>), grid, blk, 0, s, mz, Sz, mean, var, mg, Sg, mb, Sb, am, aS, ma, \
+                     Sa, mhat, Shat, total, (int)C, eps)
+    if (relu && add) TAGI_BN_APPLY(true, true);
+    else if (relu) TAGI_BN_APPLY(true, false);
+    else if (add) TAGI_BN_APPLY(false, true);
+    else TAGI_BN_APPLY(false, false);
+#undef TAGI_BN_APPLY
+  }
   return check_launch(what);
+}
+
+extern "C" int tagi_bn_fwd(const float* mz, const float* Sz, const float* mean, const float* var, const float* mg,
+                           const float* Sg, const float* mb, const float* Sb, float* ma, float* Sa, float* mhat,
+                           float* Shat, int64_t N, int64_t C, int64_t HW, float eps, tagi_stream_t stream) {
+  return bn_apply_impl("tagi_bn_fwd", false, mz, Sz, mean, var, mg, Sg, mb, Sb, nullptr, nullptr, ma, Sa, mhat, Shat,
+                       N, C, HW, eps, stream);
+}
+
+extern "C" int tagi_relu_bn_fwd(const float* mz, const float* Sz, const float* mean, const float* var,
+                                const float* mg, const float* Sg, const float* mb, const float* Sb, const float* add_m,
+                                const float* add_S, float* ma, float* Sa, float* mhat, int64_t N, int64_t C,
+                                int64_t HW, float eps, tagi_stream_t stream) {
+  return bn_apply_impl("tagi_relu_bn_fwd", true, mz, Sz, mean, var, mg, Sg, mb, Sb, add_m, add_S, ma, Sa, mhat,
+                       nullptr, N, C, HW, eps, stream);
 }
 
 extern "C" int64_t tagi_bn_bwd_ws_bytes(int64_t N, int64_t C, int64_t HW) {
@@ -458,31 +598,58 @@ extern "C" int64_t tagi_bn_bwd_ws_bytes(int64_t N, int64_t C, int64_t HW) {
   return (int64_t)bn_blocks(N * HW, C) * C * 4 * (int64_t)sizeof(float);
 }
 
-extern "C" int tagi_bn_bwd(const float* dma, const float* dSa, const float* mhat, const float* var, const float* mg,
-                           const float* Sg, const float* Sb, float* dmz, float* dSz, float* dmg, float* dSg,
-                           float* dmb, float* dSb, int64_t N, int64_t C, int64_t HW, float eps, float* ws,
-                           int64_t ws_bytes, tagi_stream_t stream) {
-  const char* what = "tagi_bn_bwd";
-  TAGI_REQUIRE(dma && dSa && mhat && var && mg && Sg && Sb && dmz && dSz && dmg && dSg && dmb && dSb && ws,
+static int bn_bwd_impl(const char* what, const float* dma, const float* dSa, const float* mhat, const float* J,
+                       const float* var, const float* mg, const float* Sg, const float* Sb, float* dmz, float* dSz,
+                       float* dmg, float* dSg, float* dmb, float* dSb, int64_t N, int64_t C, int64_t HW, float eps,
+                       float* ws, int64_t ws_bytes, tagi_stream_t stream, bool jac) {
+  TAGI_REQUIRE(dma && dSa && mhat && var && mg && Sg && Sb && dmz && dSz && dmg && dSg && dmb && dSb && ws &&
+                   (!jac || J),
                "%s: null pointer", what);
   TAGI_REQUIRE(N > 0 && C > 0 && HW > 0, "%s: bad sizes", what);
   TAGI_REQUIRE(ws_bytes >= tagi_bn_bwd_ws_bytes(N, C, HW), "%s: workspace too small", what);
   hipStream_t s = as_stream(stream);
-  ProfScope ps(FAM_BN_BWD, s, 0.0, 20.0 * N * C * HW);
+  ProfScope ps(FAM_BN_BWD, s, 0.0, (jac ? 24.0 : 20.0) * N * C * HW);
   const int64_t rows = N * HW;
   const int nblk = bn_blocks(rows, C);
-  const bool vec = bn_vec(C) && al16p(dma) && al16p(dSa) && al16p(mhat) && al16p(dmz) && al16p(dSz);
-  if (vec)
-    hipLaunchKernelGGL((bn_reduce_kernel<4, true>), dim3(nblk), dim3(256), 0, s, dma, dSa, mhat, ws, rows, (int)C,
-                       nblk, 1, var, mg, dmz, dSz, eps);
-  else
-    hipLaunchKernelGGL((bn_reduce_kernel<4, false>), dim3(nblk), dim3(256), 0, s, dma, dSa, mhat, ws, rows, (int)C,
-                       nblk, 1, var, mg, dmz, dSz, eps);
+  const bool vec = bn_vec(C) && al16p(dma) && al16p(dSa) && al16p(mhat) && al16p(dmz) && al16p(dSz) &&
+                   (!jac || al16p(J));
+  const dim3 grid(nblk), blk(256);
+  if (jac) {
+    if (vec)
+      hipLaunchKernelGGL((bn_reduce_kernel<3, true>), grid, blk, 0, s, dma, dSa, mhat, J, ws, rows, (int)C, nblk, var,
+                         mg, dmz, dSz, eps);
+    else
+      hipLaunchKernelGGL((bn_reduce_kernel<3, false>), grid, blk, 0, s, dma, dSa, mhat, J, ws, rows, (int)C, nblk,
+                         var, mg, dmz, dSz, eps);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((bn_reduce_kernel<2, true>), grid, blk, 0, s, dma, dSa, mhat, nullptr, ws, rows, (int)C,
+                         nblk, var, mg, dmz, dSz, eps);
+    else
+      hipLaunchKernelGGL((bn_reduce_kernel<2, false>), grid, blk, 0, s, dma, dSa, mhat, nullptr, ws, rows, (int)C,
+                         nblk, var, mg, dmz, dSz, eps);
+  }
   int rc = check_launch(what);
   if (rc) return rc;
   hipLaunchKernelGGL(bn_bwd_finalize_kernel, dim3((unsigned)C), dim3(64), 0, s, (const float*)ws, Sg, Sb,
                      dmg, dSg, dmb, dSb, (int)C, nblk);
   return check_launch(what);
+}
+
+extern "C" int tagi_bn_bwd(const float* dma, const float* dSa, const float* mhat, const float* var, const float* mg,
+                           const float* Sg, const float* Sb, float* dmz, float* dSz, float* dmg, float* dSg,
+                           float* dmb, float* dSb, int64_t N, int64_t C, int64_t HW, float eps, float* ws,
+                           int64_t ws_bytes, tagi_stream_t stream) {
+  return bn_bwd_impl("tagi_bn_bwd", dma, dSa, mhat, nullptr, var, mg, Sg, Sb, dmz, dSz, dmg, dSg, dmb, dSb, N, C, HW,
+                     eps, ws, ws_bytes, stream, false);
+}
+
+extern "C" int tagi_bn_relu_bwd(const float* dma, const float* dSa, const float* mhat, const float* J,
+                                const float* var, const float* mg, const float* Sg, const float* Sb, float* dmz,
+                                float* dSz, float* dmg, float* dSg, float* dmb, float* dSb, int64_t N, int64_t C,
+                                int64_t HW, float eps, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+  return bn_bwd_impl("tagi_bn_relu_bwd", dma, dSa, mhat, J, var, mg, Sg, Sb, dmz, dSz, dmg, dSg, dmb, dSb, N, C, HW,
+                     eps, ws, ws_bytes, stream, true);
 }
 
 extern "C" int tagi_rmsnorm_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw, float* mz,

@@ -66,6 +66,7 @@ _SIGS = {
     "tagi_conv2d_fwd_ws_bytes": (I64, [GP]),
     "tagi_conv2d_bwd_delta": (c_int, [P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_bwd_delta_ws_bytes": (I64, [GP]),
+    "tagi_conv2d_bwd_delta_add": (c_int, [P, P, P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_wgrad_ws_bytes": (I64, [GP]),
     "tagi_relu_fwd": (c_int, [P, P, P, P, P, I64, P]),
@@ -82,6 +83,9 @@ _SIGS = {
     "tagi_bn_fwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P]),
     "tagi_bn_bwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P, I64, P]),
     "tagi_bn_bwd_ws_bytes": (I64, [I64, I64, I64]),
+    "tagi_relu_bn_stats": (c_int, [P, P, P, P, P, P, P, P, I64, I64, I64, F, F, c_int, c_int, P, I64, P]),
+    "tagi_relu_bn_fwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P]),
+    "tagi_bn_relu_bwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P, I64, P]),
     "tagi_rmsnorm_fwd": (c_int, [P, P, P, P, P, P, P, I64, I64, F, P]),
     "tagi_rmsnorm_bwd": (c_int, [P, P, P, P, P, P, P, P, P, P, I64, I64, P, I64, P]),
     "tagi_rmsnorm_bwd_ws_bytes": (I64, [I64, I64]),

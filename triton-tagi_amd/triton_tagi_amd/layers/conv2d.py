@@ -1,8 +1,8 @@
 """Bayesian Conv2D layer as implicit GEMM (mirrors triton_tagi/layers/conv2d.py:189-390).
 
 The reference unfolds patches (im2col), runs the Linear kernels on them and folds the
-input deltas back (col2im). Here the three GEMMs gather patches straight from the NCHW
-tensors inside the kernels:
+input deltas back (col2im). Here the three GEMMs gather patches straight from the
+activation tensors inside the kernels:
     forward      mu_z = P(mu_a) @ mw + mb ;  S_z = P(mu_a)^2 @ Sw + P(S_a) @ (mw^2 + Sw) + Sb
     input delta  fold(delta_z @ mw^T) as a transposed implicit GEMM (no col2im)
     deltas       delta_mw = Sw * P^T @ delta_mz, delta_Sw = Sw^2 * (P^2)^T @ delta_Sz (+ bias)
@@ -80,7 +80,9 @@ class Conv2D(LearnableLayer):
         """The parameter deltas of ``backward`` without forming the input deltas."""
         self._backward(delta_mz, delta_Sz, False)
 
-    def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool):
+    def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool,
+                  add: tuple[Tensor, Tensor] | None = None):
+        """Parameter deltas, then (if asked) the input deltas, plus ``add`` when given."""
         N, C, H, W = self.input_shape
         g = self._geom(N, C, H, W)
         dmz = _lib.check(_lib.channels_last(delta_mz.reshape(N, self.C_out, g.Ho, g.Wo)), "delta_mz")
@@ -105,8 +107,14 @@ class Conv2D(LearnableLayer):
         d_Sa = _lib.empty_cl(N, C, H, W, dev)
         ws = _lib.workspace(_lib.query("tagi_conv2d_bwd_delta_ws_bytes", g), dev)
         wp, wb = _lib.ws_args(ws)
-        _lib.call("tagi_conv2d_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), self.mw.data_ptr(), d_ma.data_ptr(),
-                  d_Sa.data_ptr(), g, wp, wb, st)
+        if add is None:
+            _lib.call("tagi_conv2d_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), self.mw.data_ptr(), d_ma.data_ptr(),
+                      d_Sa.data_ptr(), g, wp, wb, st)
+        else:
+            am = _lib.check(_lib.like(add[0].reshape(N, C, H, W), d_ma), "add_m")
+            aS = _lib.check(_lib.like(add[1].reshape(N, C, H, W), d_ma), "add_S")
+            _lib.call("tagi_conv2d_bwd_delta_add", dmz.data_ptr(), dSz.data_ptr(), self.mw.data_ptr(),
+                      am.data_ptr(), aS.data_ptr(), d_ma.data_ptr(), d_Sa.data_ptr(), g, wp, wb, st)
         return d_ma, d_Sa
 
     def _update_items(self):

@@ -1,0 +1,162 @@
+"""Fused passes over consecutive layers of the step.
+
+Running a layer list through ``forward_chain`` / ``backward_chain`` gives the same
+results as calling every layer's own ``forward`` / ``backward`` in turn. It differs only
+in how often activations cross HBM:
+
+* ReLU followed by a training-mode BatchNorm2D (relu.py:135-140, batchnorm2d.py:360-431)
+  runs as two passes over the ReLU input: the first forms the batch statistics of the
+  rectified moments (and the ReLU Jacobian), the second recomputes the rectified moments
+  and normalises them. The ReLU output is never written.
+* The residual add that closes a block (resblock.py:380) is folded into that second pass.
+* Backward through BatchNorm2D and the ReLU in front of it (batchnorm2d.py:465-513,
+  relu.py:152-169) is one pass.
+* The merge of the shortcut deltas into the main branch (resblock.py:421-423) is folded
+  into the input-delta GEMM of the block's first convolution.
+
+Every layer still ends up holding the state its own ``backward`` reads (ReLU.J,
+BatchNorm2D.m_hat and its normalisation variance, Conv2D.ma_in), so per-layer calls keep
+working after a fused pass.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+from .batchnorm2d import BatchNorm2D
+from .conv2d import Conv2D
+from .relu import ReLU
+
+
+def _add_in_place(src_m: Tensor, src_S: Tensor, dst_m: Tensor, dst_S: Tensor) -> None:
+    from .resblock import add_shortcut
+
+    add_shortcut(src_m, src_S, dst_m, dst_S)
+
+
+def relu_bn_forward(relu: ReLU, bn: BatchNorm2D, mz: Tensor, Sz: Tensor,
+                    add: tuple[Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor]:
+    """BatchNorm2D(ReLU(mz, Sz)) in training mode, plus ``add`` when given."""
+    if not bn.training:
+        raise ValueError("relu_bn_forward: the BatchNorm2D must be in training mode")
+    mz = _lib.check(_lib.channels_last(mz), "mz")
+    Sz = _lib.check(_lib.channels_last(Sz), "Sz")
+    if mz.dim() != 4 or Sz.shape != mz.shape:
+        raise ValueError(f"relu_bn_forward: expected matching (N, C, H, W) moments, got {tuple(mz.shape)}")
+    N, C, H, W = mz.shape
+    if C != bn.num_features:
+        raise ValueError(f"BatchNorm2D: expected {bn.num_features} channels, got {C}")
+    HW = H * W
+    dev = mz.device
+    st = _lib.stream_of(mz)
+    J = torch.empty_like(mz)
+    bmean = torch.empty(C, device=dev, dtype=torch.float32)
+    bvar = torch.empty(C, device=dev, dtype=torch.float32)
+    first = not bn._is_initialized
+    ws = _lib.workspace(_lib.query("tagi_bn_stats_ws_bytes", N, C, HW), dev)
+    wp, wb = _lib.ws_args(ws)
+    _lib.call("tagi_relu_bn_stats", mz.data_ptr(), Sz.data_ptr(), J.data_ptr(), bmean.data_ptr(), bvar.data_ptr(),
+              _lib.check(bn.running_mean, "running_mean").data_ptr(),
+              _lib.check(bn.running_var, "running_var").data_ptr(), _lib.check(bn.mw, "mw").data_ptr(),
+              N, C, HW, float(bn.momentum), float(bn.eps), int(first), int(bn.preserve_var), wp, wb, st)
+    bn._is_initialized = True
+    relu.J = J
+    am = aS = None
+    if add is not None:
+        am = _lib.check(_lib.like(add[0], mz), "add_m")
+        aS = _lib.check(_lib.like(add[1], mz), "add_S")
+        if am.shape != mz.shape or aS.shape != mz.shape:
+            raise ValueError(f"relu_bn_forward: addend {tuple(am.shape)} vs output {tuple(mz.shape)}")
+    ma, Sa, mhat = torch.empty_like(mz), torch.empty_like(mz), torch.empty_like(mz)
+    _lib.call("tagi_relu_bn_fwd", mz.data_ptr(), Sz.data_ptr(), bmean.data_ptr(), bvar.data_ptr(), bn.mw.data_ptr(),
+              _lib.check(bn.Sw, "Sw").data_ptr(), _lib.check(bn.mb, "mb").data_ptr(),
+              _lib.check(bn.Sb, "Sb").data_ptr(), _lib.ptr(am), _lib.ptr(aS), ma.data_ptr(), Sa.data_ptr(),
+              mhat.data_ptr(), N, C, HW, float(bn.eps), st)
+    bn.input_shape = mz.shape
+    bn._norm_var = bvar
+    bn.m_hat = mhat
+    return ma, Sa
+
+
+def bn_relu_backward(bn: BatchNorm2D, relu: ReLU, delta_ma: Tensor, delta_Sa: Tensor) -> tuple[Tensor, Tensor]:
+    """relu.backward(*bn.backward(delta_ma, delta_Sa)) in one pass; stores the BN deltas."""
+    dma = _lib.check(_lib.channels_last(delta_ma.reshape(bn.input_shape)), "delta_ma")
+    dSa = _lib.check(_lib.channels_last(delta_Sa.reshape(bn.input_shape)), "delta_Sa")
+    J = _lib.check(_lib.like(relu.J, dma), "J")
+    if J.shape != dma.shape:
+        raise ValueError(f"bn_relu_backward: stored Jacobian {tuple(J.shape)} vs delta {tuple(dma.shape)}")
+    N, C, H, W = bn.input_shape
+    HW = H * W
+    dev = dma.device
+    dmz, dSz = torch.empty_like(dma), torch.empty_like(dSa)
+    bn.delta_mw = torch.empty(C, device=dev, dtype=torch.float32)
+    bn.delta_Sw = torch.empty_like(bn.delta_mw)
+    bn.delta_mb = torch.empty_like(bn.delta_mw)
+    bn.delta_Sb = torch.empty_like(bn.delta_mw)
+    ws = _lib.workspace(_lib.query("tagi_bn_bwd_ws_bytes", N, C, HW), dev)
+    wp, wb = _lib.ws_args(ws)
+    _lib.call("tagi_bn_relu_bwd", dma.data_ptr(), dSa.data_ptr(), bn.m_hat.data_ptr(), J.data_ptr(),
+              bn._norm_var.data_ptr(), bn.mw.data_ptr(), bn.Sw.data_ptr(), bn.Sb.data_ptr(), dmz.data_ptr(),
+              dSz.data_ptr(), bn.delta_mw.data_ptr(), bn.delta_Sw.data_ptr(), bn.delta_mb.data_ptr(),
+              bn.delta_Sb.data_ptr(), N, C, HW, float(bn.eps), wp, wb, _lib.stream_of(dma))
+    return dmz, dSz
+
+
+def _fusable_forward(layer, nxt, mu: Tensor) -> bool:
+    return isinstance(layer, ReLU) and isinstance(nxt, BatchNorm2D) and nxt.training and mu.dim() == 4
+
+
+def _fusable_backward(layer, prev) -> bool:
+    return (isinstance(layer, BatchNorm2D) and isinstance(prev, ReLU) and prev.J is not None
+            and layer.m_hat is not None and tuple(prev.J.shape) == tuple(layer.m_hat.shape))
+
+
+def forward_chain(layers, mu: Tensor, var: Tensor,
+                  add: tuple[Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor]:
+    """Forward through ``layers`` in order; ``add`` is added to the final output."""
+    i, n = 0, len(layers)
+    while i < n:
+        layer = layers[i]
+        nxt = layers[i + 1] if i + 1 < n else None
+        if _fusable_forward(layer, nxt, mu):
+            last = i + 2 == n
+            mu, var = relu_bn_forward(layer, nxt, mu, var, add if last else None)
+            if last:
+                add = None
+            i += 2
+        else:
+            mu, var = layer.forward(mu, var)
+            i += 1
+    if add is not None:
+        _add_in_place(add[0], add[1], mu, var)
+    return mu, var
+
+
+def backward_chain(layers, delta_mu: Tensor, delta_var: Tensor, add: tuple[Tensor, Tensor] | None = None,
+                   first_params_only: bool = False):
+    """Backward through ``layers`` in reverse; ``add`` is added to the returned deltas.
+
+    With ``first_params_only`` the first layer forms only its parameter deltas (when it
+    can) and None is returned.
+    """
+    i = len(layers) - 1
+    while i >= 0:
+        layer = layers[i]
+        prev = layers[i - 1] if i >= 1 else None
+        if _fusable_backward(layer, prev):
+            delta_mu, delta_var = bn_relu_backward(layer, prev, delta_mu, delta_var)
+            i -= 2
+            continue
+        if i == 0:
+            if first_params_only and hasattr(layer, "backward_param_deltas"):
+                layer.backward_param_deltas(delta_mu, delta_var)
+                return None
+            if add is not None and isinstance(layer, Conv2D):
+                return layer._backward(delta_mu, delta_var, True, add=add)
+        delta_mu, delta_var = layer.backward(delta_mu, delta_var)
+        i -= 1
+    if add is not None:
+        _add_in_place(add[0], add[1], delta_mu, delta_var)
+    return delta_mu, delta_var

@@ -102,24 +102,23 @@ class ResBlock(LearnableLayer):
                 layer.eval()
 
     def forward(self, mu_in: Tensor, var_in: Tensor) -> tuple[Tensor, Tensor]:
-        mu_z, var_z = mu_in, var_in
-        for layer in self._main_layers:
-            mu_z, var_z = layer.forward(mu_z, var_z)
-        mu_x, var_x = mu_in, var_in
-        for layer in self._proj_layers:
-            mu_x, var_x = layer.forward(mu_x, var_x)
-        add_shortcut(mu_x, var_x, mu_z, var_z)
-        return mu_z, var_z
+        """main(x) + shortcut(x) (resblock.py:354-385). The shortcut runs first so its
+        output can be added inside the main branch's last pass."""
+        from .fused import forward_chain
+
+        mu_x, var_x = forward_chain(self._proj_layers, mu_in, var_in) if self._proj_layers else (mu_in, var_in)
+        return forward_chain(self._main_layers, mu_in, var_in, add=(mu_x, var_x))
 
     def backward(self, delta_mu: Tensor, delta_var: Tensor) -> tuple[Tensor, Tensor]:
-        d_mu_main, d_var_main = delta_mu, delta_var
-        for layer in reversed(self._main_layers):
-            d_mu_main, d_var_main = layer.backward(d_mu_main, d_var_main)
-        d_mu_skip, d_var_skip = delta_mu, delta_var
-        for layer in reversed(self._proj_layers):
-            d_mu_skip, d_var_skip = layer.backward(d_mu_skip, d_var_skip)
-        delta_merge(d_mu_skip, d_var_skip, d_mu_main, d_var_main)
-        return d_mu_main, d_var_main
+        """Deltas through both branches, summed (resblock.py:387-430); the shortcut's
+        deltas are added inside the main branch's first input-delta GEMM."""
+        from .fused import backward_chain
+
+        if self._proj_layers:
+            d_skip = backward_chain(self._proj_layers, delta_mu, delta_var)
+        else:
+            d_skip = (delta_mu, delta_var)
+        return backward_chain(self._main_layers, delta_mu, delta_var, add=d_skip)
 
     def _update_items(self):
         items = []

@@ -3,7 +3,8 @@
 ``step(x, y, sigma_v)``: forward moments -> output innovation -> reversed backward
 (deltas stored on the layers) -> capped update of every learnable layer with the cap
 factor of the batch size. The updates of all layers that expose their parameter groups
-go out as one multi-tensor launch; the arithmetic is the per-layer rule.
+go out as one multi-tensor launch; the arithmetic is the per-layer rule. Consecutive
+ReLU -> BatchNorm2D pairs run as fused passes (same results as the layers one by one).
 """
 
 from __future__ import annotations
@@ -12,6 +13,8 @@ import torch
 from torch import Tensor
 
 from .base import Layer, LearnableLayer
+from .layers.conv2d import Conv2D
+from .layers.fused import backward_chain, forward_chain
 from .layers.multihead_attention import MultiheadAttentionV2
 from .layers.resblock import ResBlock
 from .update.observation import compute_innovation
@@ -57,19 +60,20 @@ class Sequential:
             layer.running_var = layer.running_var.to(self.device)
 
     def forward(self, x: Tensor) -> tuple[Tensor, Tensor]:
-        ma = x
-        Sa = torch.zeros_like(x)
+        """Layer-by-layer moment propagation from a deterministic input (S_a = 0)."""
         for layer in self.layers:
-            if isinstance(layer, Layer):
-                ma, Sa = layer.forward(ma, Sa)
-            else:
+            if not isinstance(layer, Layer):
                 raise TypeError(f"Unknown layer type: {type(layer)}")
-        return ma, Sa
+        if x.dim() == 4 and self.layers and isinstance(self.layers[0], Conv2D):
+            # the conv path keeps activations channels-last: start both moments that way
+            x = x.contiguous(memory_format=torch.channels_last)
+            Sa = torch.zeros_like(x, memory_format=torch.channels_last)
+        else:
+            Sa = torch.zeros_like(x)
+        return forward_chain(self.layers, x, Sa)
 
     def backward(self, delta_mu: Tensor, delta_var: Tensor) -> tuple[Tensor, Tensor]:
-        for layer in reversed(self.layers):
-            delta_mu, delta_var = layer.backward(delta_mu, delta_var)
-        return delta_mu, delta_var
+        return backward_chain(self.layers, delta_mu, delta_var)
 
     def update(self, cap_factor: float) -> None:
         """Capped update of every learnable layer (one launch for all exposed groups)."""
@@ -97,12 +101,7 @@ class Sequential:
         batch_size = x_batch.shape[0]
         y_pred_mu, y_pred_var = self.forward(x_batch)
         delta_mu, delta_var = compute_innovation(y_batch, y_pred_mu, y_pred_var, sigma_v)
-        for i in range(len(self.layers) - 1, -1, -1):
-            layer = self.layers[i]
-            if i == 0 and hasattr(layer, "backward_param_deltas"):
-                layer.backward_param_deltas(delta_mu, delta_var)
-            else:
-                delta_mu, delta_var = layer.backward(delta_mu, delta_var)
+        backward_chain(self.layers, delta_mu, delta_var, first_params_only=True)
         self.update(get_cap_factor(batch_size))
         return y_pred_mu, y_pred_var
 
