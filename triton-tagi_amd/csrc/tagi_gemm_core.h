@@ -158,7 +158,17 @@ struct Loader {
   static constexpr int NRB = CONV_ROWS ? NC : 1;  // per-chunk row bases only where rows differ
   static constexpr int NR = CONV_R ? NC : 1;
 
+  // Conv kinds walk the reduction index k in steps of BK; its decoded form (a tap and a
+  // channel, or an image and a pixel) is carried from one k-tile to the next instead of
+  // being divided out again for every chunk of every tile.
+  static constexpr bool CONV_K = (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S || KIND == LD_CFWD_B4 ||
+                                  KIND == LD_CFWD_B_S || KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S ||
+                                  KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CWG_A4 ||
+                                  KIND == LD_CWG_A_S);
+  static constexpr int NKS = CONV_K ? NC : 1;
+
   Vt v[NT][NC];
+  int ks0[NKS], ks1[NKS], ks2[NKS];  // decoded k of each chunk at the next tile to fetch
   int mnmax, kmax;           // extents checked by fetch (per phase for the conv input delta)
   int cmn[NC], ck[NC];       // chunk origin within the tile
   int64_t rowbase[NRB];      // batch offset (strided kinds) or per-chunk image base (conv rows)
@@ -253,6 +263,90 @@ struct Loader {
     }
   }
 
+  // Decode k = k0 + ck[i] for every chunk (once per block).
+  //   CFWD_A: (kh, kw, c)  with k = (kh*kk + kw)*C + c
+  //   CFWD_B: (kidx, -, c) with k = kidx*C + c
+  //   CBWD_*: (ikh, ikw, co) with k = (ikh*nkw + ikw)*Cout + co over the phase's taps
+  //   CWG_A:  (n, oh, ow)  with k = (n*Ho + oh)*Wo + ow
+  __device__ __forceinline__ void init_k(const Operand& o, int k0) {
+    if constexpr (CONV_K) {
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int k = k0 + ck[i];
+        int a = 0, b = 0, c = 0;
+        if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
+          const int kidx = k / o.g.C;
+          c = k - kidx * o.g.C;
+          a = kidx / o.g.kk;
+          b = kidx - a * o.g.kk;
+        } else if constexpr (KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
+          a = k / o.g.C;
+          c = k - a * o.g.C;
+        } else if constexpr (KIND == LD_CWG_A4 || KIND == LD_CWG_A_S) {
+          const int howo = o.g.Ho * o.g.Wo;
+          a = k / howo;
+          const int p = k - a * howo;
+          b = p / o.g.Wo;
+          c = p - b * o.g.Wo;
+        } else {
+          const int nkw = r2[i];
+          if (nkw > 0) {
+            const int kidx = k / o.g.Cout;
+            c = k - kidx * o.g.Cout;
+            a = kidx / nkw;
+            b = kidx - a * nkw;
+          }
+        }
+        ks0[i] = a;
+        ks1[i] = b;
+        ks2[i] = c;
+      }
+    }
+  }
+
+  // Move every chunk's decoded k forward by BK (carries at most BK / extent + 1 times).
+  __device__ __forceinline__ void advance_k(const Operand& o) {
+    if constexpr (CONV_K) {
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
+          ks2[i] += BK;
+          while (ks2[i] >= o.g.C) {
+            ks2[i] -= o.g.C;
+            if (++ks1[i] == o.g.kk) {
+              ks1[i] = 0;
+              ++ks0[i];
+            }
+          }
+        } else if constexpr (KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
+          ks2[i] += BK;
+          while (ks2[i] >= o.g.C) {
+            ks2[i] -= o.g.C;
+            ++ks0[i];
+          }
+        } else if constexpr (KIND == LD_CWG_A4 || KIND == LD_CWG_A_S) {
+          ks2[i] += BK;
+          while (ks2[i] >= o.g.Wo) {
+            ks2[i] -= o.g.Wo;
+            if (++ks1[i] == o.g.Ho) {
+              ks1[i] = 0;
+              ++ks0[i];
+            }
+          }
+        } else {
+          ks2[i] += BK;
+          while (ks2[i] >= o.g.Cout) {
+            ks2[i] -= o.g.Cout;
+            if (++ks1[i] == r2[i]) {
+              ks1[i] = 0;
+              ++ks0[i];
+            }
+          }
+        }
+      }
+    }
+  }
+
   __device__ __forceinline__ float4 ld4(const float* p, int64_t off) const {
     return *reinterpret_cast<const float4*>(p + off);
   }
@@ -291,12 +385,10 @@ struct Loader {
         }
       } else if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
         if (k < o.K) {
-          const int kidx = k / o.g.C;
-          const int c = k - kidx * o.g.C;
-          const int kh = kidx / o.g.kk, kw = kidx - (kidx / o.g.kk) * o.g.kk;
-          const int ih = r0[i] + kh, iw = r1[i] + kw;
+          const int ih = r0[i] + ks0[i], iw = r1[i] + ks1[i];
           if (ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W) {
-            const int64_t off = rowbase[i] + ((int64_t)ih * o.g.W + iw) * o.g.C + c;
+            // in-image offset fits int32 (checked on the host)
+            const int64_t off = rowbase[i] + ((ih * o.g.W + iw) * o.g.C + ks2[i]);
             if constexpr (V4) {
               a = ld4(o.p0, off);
               if constexpr (NT == 2) b = ld4(o.p1, off);
@@ -308,9 +400,7 @@ struct Loader {
         }
       } else if constexpr (KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
         if (k < o.K && mn < o.MN) {
-          const int kidx = k / o.g.C;
-          const int c = k - kidx * o.g.C;
-          const int64_t off = ((int64_t)c * (o.g.kk * o.g.kk) + kidx) * o.g.Cout + mn;
+          const int off = (ks2[i] * (o.g.kk * o.g.kk) + ks0[i]) * o.g.Cout + mn;
           if constexpr (V4) {
             a = ld4(o.p0, off);
             if constexpr (NT == 2) b = ld4(o.p1, off);
@@ -321,13 +411,9 @@ struct Loader {
         }
       } else if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S) {
         if (k < kmax) {
-          const int kidx = k / o.g.Cout;
-          const int co = k - kidx * o.g.Cout;
-          const int ikh = kidx / r2[i];
-          const int ikw = kidx - ikh * r2[i];
-          const int oh = r0[i] - ikh, ow = r1[i] - ikw;
+          const int oh = r0[i] - ks0[i], ow = r1[i] - ks1[i];
           if (oh >= 0 && oh < o.g.Ho && ow >= 0 && ow < o.g.Wo) {
-            const int64_t off = rowbase[i] + ((int64_t)oh * o.g.Wo + ow) * o.g.Cout + co;
+            const int64_t off = rowbase[i] + ((oh * o.g.Wo + ow) * o.g.Cout + ks2[i]);
             if constexpr (V4) {
               a = ld4(o.p0, off);
               if constexpr (NT == 2) b = ld4(o.p1, off);
@@ -339,12 +425,9 @@ struct Loader {
         }
       } else if constexpr (KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S) {
         if (k < kmax && mn < mnmax) {
-          const int kidx = k / o.g.Cout;
-          const int co = k - kidx * o.g.Cout;
-          const int ikh = kidx / r2[i];
-          const int kh = r0[i] + ikh * o.g.stride;
-          const int kw = r1[i] + (kidx - ikh * r2[i]) * o.g.stride;
-          const int64_t off = (((int64_t)(kh * o.g.kk + kw) * o.g.Cout + co)) * o.g.C + mn;
+          const int kh = r0[i] + ks0[i] * o.g.stride;
+          const int kw = r1[i] + ks1[i] * o.g.stride;
+          const int off = ((kh * o.g.kk + kw) * o.g.Cout + ks2[i]) * o.g.C + mn;
           if constexpr (V4) {
             a = ld4(o.p0, off);
           } else {
@@ -354,13 +437,10 @@ struct Loader {
       } else if constexpr (KIND == LD_CWG_A4 || KIND == LD_CWG_A_S) {
         if (k < o.K) {
           if (mn < o.MN) {
-            const int howo = o.g.Ho * o.g.Wo;
-            const int n = k / howo, p = k - n * howo;
-            const int oh = p / o.g.Wo, ow = p - oh * o.g.Wo;
-            const int ih = oh * o.g.stride - o.g.pt + r0[i];
-            const int iw = ow * o.g.stride - o.g.pl + r1[i];
+            const int ih = ks1[i] * o.g.stride - o.g.pt + r0[i];
+            const int iw = ks2[i] * o.g.stride - o.g.pl + r1[i];
             if (ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W) {
-              const int64_t off = (((int64_t)n * o.g.H + ih) * o.g.W + iw) * o.g.C + r2[i];
+              const int64_t off = (int64_t)ks0[i] * (o.g.H * o.g.W * o.g.C) + ((ih * o.g.W + iw) * o.g.C + r2[i]);
               if constexpr (V4) {
                 a = ld4(o.p0, off);
               } else {
@@ -380,6 +460,7 @@ struct Loader {
         if constexpr (NT == 2) v[1][i] = b.x;
       }
     }
+    advance_k(o);
   }
 
   __device__ __forceinline__ void store(float* s) const {
@@ -510,6 +591,8 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   Loader<KB, NB, BN, BK, NTH> lb;
   la.init(g.a, z, m0, tid);
   lb.init(g.b, z, n0, tid);
+  la.init_k(g.a, kbeg);
+  lb.init_k(g.b, kbeg);
 
   floatx16 accM[TM][TN], accV[TM][TN];
 #pragma unroll
