@@ -82,10 +82,6 @@ static Plan conv_bwd_plan(const tagi_conv_geom* g) {
     const Phase p = make_phase(cg, ph);
     pk[ph] = (int64_t)p.nkh * p.nkw * g->Cout;
   }
-  // Splitting the phases pays only when the unsplit launch leaves CUs idle: the phases
-  // already differ in length, and their partial sums cost more than the balance gains.
-  const Plan p1 = choose_plan(R, g->C, K, nph, 2, false, 1, pk);
-  if ((int64_t)p1.tiles_m * p1.tiles_n * nph >= 512) return p1;
   return choose_plan(R, g->C, K, nph, 2, true, 16, pk);
 }
 

@@ -823,21 +823,27 @@ struct Plan {
   int tiles_m, tiles_n;
 };
 
-// Pick the tile shape and split-K factor minimising a simple time model: the busiest CU
-// holds ceil(blocks / 256) blocks; its MFMA time is inflated by the per-tile load
-// overhead (small tiles re-read more operand bytes per flop) and by low occupancy
-// (fewer than ~3 waves per SIMD leave load latency exposed). Split-K adds the HBM round
-// trip of the partial sums (written by the GEMM, read back by the reduction) plus one
-// launch. Every split count up to max_splits is tried (not only powers of two), so the
-// block count can match the CU count without extra partial sums.
+// Pick the tile shape and split-K factor minimising a time model of the launch:
+//   * blocks run in rounds of 256 CUs x (resident blocks per CU); a partial last round
+//     runs at the occupancy of the blocks it holds (a lone block per CU leaves the MFMA
+//     pipes half idle);
+//   * each tile shape sustains a fraction of the fp32 MFMA peak (operand loads, LDS
+//     traffic and epilogue per flop), and fewer than ~3 waves per SIMD expose latency;
+//   * split-K adds the partial sums' round trip (8 bytes per element and split, written
+//     and read back, mostly through the last-level cache) plus the reduction launch.
+// The constants were fitted to measured conv/linear GEMM timings on MI355X. Every
+// split count up to max_splits is tried (not only powers of two).
 //
 // phase_k (optional, batch entries): per-GEMM reduction lengths when they differ (stride
 // phases of the conv input delta); splits past a GEMM's own length launch no work.
 static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int64_t batch, int products,
                                         bool allow_split, int64_t max_splits, const int64_t* phase_k) {
-  // resident blocks per CU (LDS / register limited) and waves per block, per config
+  // resident blocks per CU (LDS / register limited), waves per block and sustained
+  // fraction of peak, per config
   static const int kBpc[] = {2, 3, 3, 4, 8};
   static const int kWaves[] = {8, 4, 4, 4, 1};
+  static const double kEff[] = {0.67, 0.58, 0.61, 0.57, 0.33};
+  const double kSplitSecPerByte = 1.07e-13, kSplitLaunch = 8.9e-6;
   Plan best{kNumCfg - 1, 1, (int)Kred, 1, 1};
   double best_t = DBL_MAX;
   const double peak_cu = 157.3e12 / 256.0;
@@ -858,14 +864,17 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
         blocks = 0;
         for (int64_t z = 0; z < batch; ++z) blocks += tm * tn * (phase_k[z] > 0 ? cdiv(phase_k[z], kc) : 1);
       }
-      const int64_t rounds = cdiv(blocks, 256);
-      const int64_t resident = rounds < kBpc[ci] ? rounds : kBpc[ci];
-      const double wps = (double)resident * kWaves[ci] / 4.0;  // waves per SIMD
-      const double occ = wps >= 3.0 ? 1.0 : (wps >= 2.0 ? 0.85 : (wps >= 1.0 ? 0.6 : 0.35));
-      const double tile = 1.0 / (1.0 + 32.0 / BM + 32.0 / BN);
-      double t = rounds * (2.0 * BM * BN * kc * products) / (peak_cu * tile * occ);
-      // partial sums: 8 bytes per element and split, written once and read back once
-      if (actual > 1) t += (double)actual * 16.0 * R * C * batch / 5.0e12 + 4e-6;
+      const double block_s = (2.0 * BM * BN * kc * products) / (peak_cu * kEff[ci]);
+      // time for one CU to finish r co-resident blocks
+      auto round_s = [&](int64_t r) {
+        const double wps = (double)r * kWaves[ci] / 4.0;  // waves per SIMD
+        const double occ = wps >= 3.0 ? 1.0 : (wps >= 2.0 ? 0.85 : (wps >= 1.0 ? 0.6 : 0.35));
+        return (double)r * block_s / occ;
+      };
+      const int64_t slots = 256 * (int64_t)kBpc[ci];
+      const int64_t full = blocks / slots, rem = blocks - full * slots;
+      double t = (double)full * round_s(kBpc[ci]) + (rem > 0 ? round_s(cdiv(rem, 256)) : 0.0);
+      if (actual > 1) t += (double)actual * 16.0 * R * C * batch * kSplitSecPerByte + kSplitLaunch;
       if (t < best_t * 0.999) {
         best_t = t;
         best = Plan{ci, (int)actual, (int)kc, (int)tm, (int)tn};
