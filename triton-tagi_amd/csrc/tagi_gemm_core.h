@@ -623,58 +623,78 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
       la.fetch(g.a, z, m0, kbeg + (kt + 1) * BK);
       lb.fetch(g.b, z, n0, kbeg + (kt + 1) * BK);
     }
+    {
+      // Fragments of k-step s+2 are read from LDS while the MFMAs of k-step s run; the
+      // scheduling barriers keep the compiler from sinking the reads next to their use.
+      constexpr int NS = BK / 2;
+      constexpr int PD = 2;
+      float fa0[NS][TM], fa1[NS][TM], fb0[NS][TN], fb1[NS][TN];
+      auto load = [&](int s) {
+        const int kr = 2 * s + hl;
 #pragma unroll
-    for (int s = 0; s < BK / 2; ++s) {
-      const int kr = 2 * s + hl;
-      float a0[TM], a1[TM], b0[TN], b1[TN];
+        for (int i = 0; i < TM; ++i) {
+          const int c = kr * LDA + wm * WM + i * 32 + rl;
+          fa0[s][i] = sA[c];
+          if constexpr (NA == 2) fa1[s][i] = sA[BK * LDA + c];
+        }
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int c = kr * LDA + wm * WM + i * 32 + rl;
-        a0[i] = sA[c];
-        if constexpr (NA == 2) a1[i] = sA[BK * LDA + c];
-      }
+        for (int j = 0; j < TN; ++j) {
+          const int c = kr * LDB + wn * WN + j * 32 + rl;
+          fb0[s][j] = sB[c];
+          if constexpr (NB == 2) fb1[s][j] = sB[BK * LDB + c];
+        }
+      };
+      auto mma = [&](int s) {
+        float* a0 = fa0[s];
+        float* a1 = fa1[s];
+        float* b0 = fb0[s];
+        float* b1 = fb1[s];
+        if constexpr (PROD == PROD_FWD) {
+          float asq[TM], bvar[TN];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int c = kr * LDB + wn * WN + j * 32 + rl;
-        b0[j] = sB[c];
-        if constexpr (NB == 2) b1[j] = sB[BK * LDB + c];
-      }
-      if constexpr (PROD == PROD_FWD) {
-        float asq[TM], bvar[TN];
+          for (int i = 0; i < TM; ++i) asq[i] = a0[i] * a0[i];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) asq[i] = a0[i] * a0[i];
+          for (int j = 0; j < TN; ++j) bvar[j] = b0[j] * b0[j] + b1[j];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bvar[j] = b0[j] * b0[j] + b1[j];
+          for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int j = 0; j < TN; ++j) {
+              accM[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i], b0[j], accM[i][j], 0, 0, 0);
+              accV[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(asq[i], b1[j], accV[i][j], 0, 0, 0);
+              accV[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[i], bvar[j], accV[i][j], 0, 0, 0);
+            }
+        } else if constexpr (PROD == PROD_SHARED_B) {
+          float bsq[TN];
 #pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            accM[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i], b0[j], accM[i][j], 0, 0, 0);
-            accV[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(asq[i], b1[j], accV[i][j], 0, 0, 0);
-            accV[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[i], bvar[j], accV[i][j], 0, 0, 0);
-          }
-      } else if constexpr (PROD == PROD_SHARED_B) {
-        float bsq[TN];
+          for (int j = 0; j < TN; ++j) bsq[j] = b0[j] * b0[j];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bsq[j] = b0[j] * b0[j];
+          for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int j = 0; j < TN; ++j) {
+              accM[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i], b0[j], accM[i][j], 0, 0, 0);
+              accV[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[i], bsq[j], accV[i][j], 0, 0, 0);
+            }
+        } else {
+          float asq[TM];
 #pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            accM[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i], b0[j], accM[i][j], 0, 0, 0);
-            accV[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[i], bsq[j], accV[i][j], 0, 0, 0);
-          }
-      } else {
-        float asq[TM];
+          for (int i = 0; i < TM; ++i) asq[i] = a0[i] * a0[i];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) asq[i] = a0[i] * a0[i];
+          for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int j = 0; j < TN; ++j) {
+              accM[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i], b0[j], accM[i][j], 0, 0, 0);
+              accV[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(asq[i], b1[j], accV[i][j], 0, 0, 0);
+            }
+        }
+      };
 #pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            accM[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i], b0[j], accM[i][j], 0, 0, 0);
-            accV[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(asq[i], b1[j], accV[i][j], 0, 0, 0);
-          }
+      for (int s = 0; s < PD; ++s) load(s);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        if (s + PD < NS) load(s + PD);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(s);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     if (kt + 1 < nk) {
