@@ -13,14 +13,16 @@ namespace tagi {
 // Blocks own contiguous row ranges; in the float4 path each thread keeps one group of 4
 // channels for the whole block (C divides 1024), so per-channel constants and partial
 // sums stay in registers and every load is a coalesced float4.
+static inline bool bn_vec(int64_t C) { return C % 4 == 0 && C <= 1024 && 1024 % C == 0; }
+
+// Reduction blocks: about 8192 elements each, at most 2048 (the finalize pass reads one
+// partial per block and channel, so more blocks make it slower than they save).
 static inline int bn_blocks(int64_t rows, int64_t C) {
   int64_t b = cdiv(rows * C, 8192);
   if (b > 2048) b = 2048;
   if (b > rows) b = rows;
   return (int)(b < 1 ? 1 : b);
 }
-
-static inline bool bn_vec(int64_t C) { return C % 4 == 0 && C <= 1024 && 1024 % C == 0; }
 
 // Per-block partial sums over the block's rows (finalized by the kernels below).
 //   MODE 0  statistics of (mu, S):                   sums mu, S, mu^2
@@ -552,8 +554,10 @@ static int bn_apply_impl(const char* what, bool relu, const float* mz, const flo
   if (vec) {
     const int64_t rows = N * HW;
     const int rpi = (int)(256 / (C / 4));
-    // about four float4 rows per thread, at least one row slot per block
-    int64_t rpb = (int64_t)rpi * 4;
+    // up to four float4 rows per thread, fewer when that leaves under ~1024 blocks
+    int64_t per = cdiv(rows, (int64_t)rpi * 1024);
+    per = per < 1 ? 1 : (per > 4 ? 4 : per);
+    const int64_t rpb = (int64_t)rpi * per;
     const int64_t blocks = cdiv(rows, rpb);
     const dim3 grid((unsigned)blocks), blk(256);
 #define TAGI_BN_APPLY(R, A)                                                                                         \
