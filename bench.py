@@ -85,6 +85,55 @@ def cpu_baseline(workload: str, sample_batch: int, steps: int = 3):
     }
 
 
+def measure_ceilings(dev: str) -> dict:
+    """Measured ceilings of this GPU: the fp32 MFMA issue loop at 1, 2 and 4 waves per
+    SIMD (the engine's probe kernel), a 1 GiB device-to-device copy (the HIP runtime's copy
+    kernel) and an fp32 GEMM through torch.matmul (hipBLASLt) for comparison."""
+    import torch
+
+    from triton_tagi_amd import _lib
+
+    props = torch.cuda.get_device_properties(dev)
+    cus = props.multi_processor_count
+    st = torch.cuda.current_stream().cuda_stream
+    out = {"gpu": props.name, "cus": cus}
+    buf = torch.empty(cus * 4 * 256, device=dev)
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        t_end = time.perf_counter() + 0.5  # clock warm-up
+        while time.perf_counter() < t_end:
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / reps
+
+    iters = 4000
+    for w in (1, 2, 4):
+        blocks = cus * w
+        s = timed(lambda: _lib.call("tagi_probe_mfma_loop", buf.data_ptr(), blocks, iters, st), 20)
+        flops = blocks * 4 * iters * 4 * (32 * 32 * 2 * 2)
+        out[f"mfma_fp32_loop_tflops_{w}_waves_per_simd"] = round(flops / s / 1e12, 1)
+    n = (1 << 30) // 4
+    src = torch.ones(n, device=dev)
+    dst = torch.empty_like(src)
+    s = timed(lambda: dst.copy_(src), 10)
+    out["copy_1gib_gbs_read_plus_write"] = round(2 * (1 << 30) / s / 1e9, 1)
+    del src, dst
+    torch.backends.cuda.matmul.allow_tf32 = False
+    a = torch.randn(8192, 8192, device=dev)
+    b = torch.randn(8192, 8192, device=dev)
+    s = timed(lambda: torch.matmul(a, b), 5)
+    out["torch_matmul_fp32_8192_tflops"] = round(2 * 8192**3 / s / 1e12, 1)
+    return out
+
+
 def load_traffic(workload: str, family: str):
     p = ROOT / "profiles" / "traffic.json"
     if not p.exists():
@@ -105,6 +154,8 @@ def main():
     ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--cpu-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="print measured MFMA / copy / vendor-GEMM ceilings as one JSON line and exit")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="before warm-up, run one device copy of this many MiB (a known-size kernel for "
                          "calibrating the FETCH_SIZE / WRITE_SIZE counters)")
@@ -124,6 +175,10 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     dev = "cuda:0"
+    if args.ceilings:
+        log("[bench] measuring ceilings")
+        print(json.dumps({"ceilings": measure_ceilings(dev)}), flush=True)
+        return
     log(f"[bench] building {args.workload} on {dev}")
     w = workloads.build(args.workload, device=dev, batch=args.batch)
     net, x, y, sv = w.net, w.x, w.y, w.sigma_v

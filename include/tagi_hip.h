@@ -54,6 +54,12 @@ enum {
   TAGI_FAM_COUNT = 22
 };
 
+/* Ceiling probe (no counterpart in the reference; measurement only): `blocks` blocks of
+ * four 64-lane waves, each wave running `iters` rounds of four independent fp32
+ * 32x32x2 MFMAs with no memory traffic (16384 flops per wave per round). out receives
+ * blocks*256 floats. blocks = 256*w on a 256-CU GPU gives w waves per SIMD. */
+int tagi_probe_mfma_loop(float* out, int64_t blocks, int64_t iters, tagi_stream_t stream);
+
 /* ------------------------------------------------------------------ Linear ---- */
 /* Fused Linear forward moments, one MFMA pass sharing the A/B tiles:
  *   mz = ma @ mw + mb

@@ -22,6 +22,11 @@ static ConvG to_g(const tagi_conv_geom* g) {
   c.pl = (int)g->pad_left;
   c.Ho = (int)g->Ho;
   c.Wo = (int)g->Wo;
+  c.dC = make_fastdiv(c.C);
+  c.dCout = make_fastdiv(c.Cout);
+  c.dkk = make_fastdiv(c.kk);
+  c.dHW = make_fastdiv(c.Ho * c.Wo);
+  c.dWo = make_fastdiv(c.Wo);
   return c;
 }
 

@@ -58,8 +58,30 @@ struct KindTraits {
                                 KIND == LD_CBWD_A4 || KIND == LD_CBWD_B4 || KIND == LD_CWG_A4);
 };
 
+// Exact division by an invariant d >= 1 for dividends 0 <= n < 2^31 (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994): with
+// l = ceil(log2 d), p = 31 + l and m = ceil(2^p / d) (which fits 32 bits),
+// floor(n / d) = (n * m) >> p, because 0 <= m d - 2^p < d <= 2^(p - 31).
+struct FastDiv {
+  uint32_t m;
+  int p;
+};
+
+__host__ __device__ inline FastDiv make_fastdiv(int d) {
+  int l = 0;
+  while ((1ll << l) < (long long)d) ++l;
+  const int p = 31 + l;
+  const uint64_t two_p = 1ull << p;
+  return FastDiv{(uint32_t)((two_p + (uint64_t)d - 1) / (uint64_t)d), p};
+}
+
+__device__ __forceinline__ int fdiv(int n, FastDiv f) {
+  return (int)(((uint64_t)(uint32_t)n * f.m) >> f.p);
+}
+
 struct ConvG {
   int N, C, H, W, Cout, kk, stride, pt, pl, Ho, Wo;
+  FastDiv dC, dCout, dkk, dHW, dWo;  // dividers for C, Cout, kk, Ho*Wo and Wo
 };
 
 // Phase of the stride-s input-delta GEMM: input pixels (h, w) with h % s == a, w % s == b;
@@ -158,17 +180,8 @@ struct Loader {
   static constexpr int NRB = CONV_ROWS ? NC : 1;  // per-chunk row bases only where rows differ
   static constexpr int NR = CONV_R ? NC : 1;
 
-  // Conv kinds walk the reduction index k in steps of BK; its decoded form (a tap and a
-  // channel, or an image and a pixel) is carried from one k-tile to the next instead of
-  // being divided out again for every chunk of every tile.
-  static constexpr bool CONV_K = (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S || KIND == LD_CFWD_B4 ||
-                                  KIND == LD_CFWD_B_S || KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S ||
-                                  KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CWG_A4 ||
-                                  KIND == LD_CWG_A_S);
-  static constexpr int NKS = CONV_K ? NC : 1;
-
   Vt v[NT][NC];
-  int ks0[NKS], ks1[NKS], ks2[NKS];  // decoded k of each chunk at the next tile to fetch
+  FastDiv dnkw;              // divider for the phase's taps per row (conv input delta)
   int mnmax, kmax;           // extents checked by fetch (per phase for the conv input delta)
   int cmn[NC], ck[NC];       // chunk origin within the tile
   int64_t rowbase[NRB];      // batch offset (strided kinds) or per-chunk image base (conv rows)
@@ -196,6 +209,7 @@ struct Loader {
     if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S || KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S) {
       const Phase ph = make_phase(o.g, z);
       kmax = ph.nkh * ph.nkw * o.g.Cout;
+      dnkw = make_fastdiv(ph.nkw > 0 ? ph.nkw : 1);
       if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S) mnmax = o.g.N * ph.Hq * ph.Wq;
     }
     if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
@@ -263,195 +277,71 @@ struct Loader {
     }
   }
 
-  // Decode k = k0 + ck[i] for every chunk (once per block).
-  //   CFWD_A: (kh, kw, c)  with k = (kh*kk + kw)*C + c
-  //   CFWD_B: (kidx, -, c) with k = kidx*C + c
-  //   CBWD_*: (ikh, ikw, co) with k = (ikh*nkw + ikw)*Cout + co over the phase's taps
-  //   CWG_A:  (n, oh, ow)  with k = (n*Ho + oh)*Wo + ow
-  __device__ __forceinline__ void init_k(const Operand& o, int k0) {
-    if constexpr (CONV_K) {
-#pragma unroll
-      for (int i = 0; i < NC; ++i) {
-        const int k = k0 + ck[i];
-        int a = 0, b = 0, c = 0;
-        if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
-          const int kidx = k / o.g.C;
-          c = k - kidx * o.g.C;
-          a = kidx / o.g.kk;
-          b = kidx - a * o.g.kk;
-        } else if constexpr (KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
-          a = k / o.g.C;
-          c = k - a * o.g.C;
-        } else if constexpr (KIND == LD_CWG_A4 || KIND == LD_CWG_A_S) {
-          const int howo = o.g.Ho * o.g.Wo;
-          a = k / howo;
-          const int p = k - a * howo;
-          b = p / o.g.Wo;
-          c = p - b * o.g.Wo;
-        } else {
-          const int nkw = r2[i];
-          if (nkw > 0) {
-            const int kidx = k / o.g.Cout;
-            c = k - kidx * o.g.Cout;
-            a = kidx / nkw;
-            b = kidx - a * nkw;
-          }
-        }
-        ks0[i] = a;
-        ks1[i] = b;
-        ks2[i] = c;
-      }
-    }
+  template <bool VV>
+  __device__ __forceinline__ static float4 ldv(const float* p, int64_t off) {
+    if constexpr (VV) return *reinterpret_cast<const float4*>(p + off);
+    else return make_float4(p[off], 0.f, 0.f, 0.f);
   }
 
-  // Move every chunk's decoded k forward by BK (carries at most BK / extent + 1 times).
-  __device__ __forceinline__ void advance_k(const Operand& o) {
-    if constexpr (CONV_K) {
-#pragma unroll
-      for (int i = 0; i < NC; ++i) {
-        if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
-          ks2[i] += BK;
-          while (ks2[i] >= o.g.C) {
-            ks2[i] -= o.g.C;
-            if (++ks1[i] == o.g.kk) {
-              ks1[i] = 0;
-              ++ks0[i];
-            }
-          }
-        } else if constexpr (KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
-          ks2[i] += BK;
-          while (ks2[i] >= o.g.C) {
-            ks2[i] -= o.g.C;
-            ++ks0[i];
-          }
-        } else if constexpr (KIND == LD_CWG_A4 || KIND == LD_CWG_A_S) {
-          ks2[i] += BK;
-          while (ks2[i] >= o.g.Wo) {
-            ks2[i] -= o.g.Wo;
-            if (++ks1[i] == o.g.Ho) {
-              ks1[i] = 0;
-              ++ks0[i];
-            }
-          }
-        } else {
-          ks2[i] += BK;
-          while (ks2[i] >= o.g.Cout) {
-            ks2[i] -= o.g.Cout;
-            if (++ks1[i] == r2[i]) {
-              ks1[i] = 0;
-              ++ks0[i];
-            }
-          }
-        }
-      }
-    }
-  }
-
-  __device__ __forceinline__ float4 ld4(const float* p, int64_t off) const {
-    return *reinterpret_cast<const float4*>(p + off);
-  }
-
+  // Gather of one k tile: each chunk's reduction index is decoded with exact
+  // multiply-high divisions; chunks outside the operand or in the zero padding read as 0.
   __device__ __forceinline__ void fetch(const Operand& o, int z, int mn0, int k0) {
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const int mn = mn0 + cmn[i];
       const int k = k0 + ck[i];
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-      if constexpr (KIND == LD_STR_MN4) {
-        if (k < o.K) {
-          if (mn < o.MN) {
-            const int64_t off = rowbase[0] + mn + (int64_t)k * o.s_k;
-            a = ld4(o.p0, off);
-            if constexpr (NT == 2) b = ld4(o.p1, off);
-          } else if (mn == o.ones_row) {
-            a = make_float4(1.f, 0.f, 0.f, 0.f);
-          }
-        }
+      bool ok = false, one = false;
+      int64_t off = 0;
+      if constexpr (KIND == LD_STR_MN4 || KIND == LD_STR_MN_S || KIND == LD_STR_K_S) {
+        ok = k < o.K && mn < o.MN;
+        one = k < o.K && mn == o.ones_row;
+        if constexpr (KIND == LD_STR_MN4) off = rowbase[0] + mn + (int64_t)k * o.s_k;
+        else off = rowbase[0] + (int64_t)mn * o.s_mn + (int64_t)k * o.s_k;
       } else if constexpr (KIND == LD_STR_K4) {
-        if (mn < o.MN && k < o.K) {
-          const int64_t off = rowbase[0] + (int64_t)mn * o.s_mn + k;
-          a = ld4(o.p0, off);
-          if constexpr (NT == 2) b = ld4(o.p1, off);
-        }
-      } else if constexpr (KIND == LD_STR_MN_S || KIND == LD_STR_K_S) {
-        if (k < o.K) {
-          if (mn < o.MN) {
-            const int64_t off = rowbase[0] + (int64_t)mn * o.s_mn + (int64_t)k * o.s_k;
-            a.x = o.p0[off];
-            if constexpr (NT == 2) b.x = o.p1[off];
-          } else if (mn == o.ones_row) {
-            a.x = 1.f;
-          }
-        }
+        ok = mn < o.MN && k < o.K;
+        off = rowbase[0] + (int64_t)mn * o.s_mn + k;
       } else if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
-        if (k < o.K) {
-          const int ih = r0[i] + ks0[i], iw = r1[i] + ks1[i];
-          if (ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W) {
-            // in-image offset fits int32 (checked on the host)
-            const int64_t off = rowbase[i] + ((ih * o.g.W + iw) * o.g.C + ks2[i]);
-            if constexpr (V4) {
-              a = ld4(o.p0, off);
-              if constexpr (NT == 2) b = ld4(o.p1, off);
-            } else {
-              a.x = o.p0[off];
-              if constexpr (NT == 2) b.x = o.p1[off];
-            }
-          }
-        }
+        // k = (kh*kk + kw)*C + c
+        const int kidx = fdiv(k, o.g.dC), c = k - kidx * o.g.C;
+        const int kh = fdiv(kidx, o.g.dkk), kw = kidx - kh * o.g.kk;
+        const int ih = r0[i] + kh, iw = r1[i] + kw;
+        ok = k < o.K && ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W;
+        // in-image offset fits int32 (checked on the host)
+        off = rowbase[i] + ((ih * o.g.W + iw) * o.g.C + c);
       } else if constexpr (KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
-        if (k < o.K && mn < o.MN) {
-          const int off = (ks2[i] * (o.g.kk * o.g.kk) + ks0[i]) * o.g.Cout + mn;
-          if constexpr (V4) {
-            a = ld4(o.p0, off);
-            if constexpr (NT == 2) b = ld4(o.p1, off);
-          } else {
-            a.x = o.p0[off];
-            if constexpr (NT == 2) b.x = o.p1[off];
-          }
-        }
+        // k = kidx*C + c; weight row (c, kh, kw)
+        const int kidx = fdiv(k, o.g.dC), c = k - kidx * o.g.C;
+        ok = k < o.K && mn < o.MN;
+        off = (c * (o.g.kk * o.g.kk) + kidx) * o.g.Cout + mn;
       } else if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S) {
-        if (k < kmax) {
-          const int oh = r0[i] - ks0[i], ow = r1[i] - ks1[i];
-          if (oh >= 0 && oh < o.g.Ho && ow >= 0 && ow < o.g.Wo) {
-            const int64_t off = rowbase[i] + ((oh * o.g.Wo + ow) * o.g.Cout + ks2[i]);
-            if constexpr (V4) {
-              a = ld4(o.p0, off);
-              if constexpr (NT == 2) b = ld4(o.p1, off);
-            } else {
-              a.x = o.p0[off];
-              if constexpr (NT == 2) b.x = o.p1[off];
-            }
-          }
-        }
+        // k = (ikh*nkw + ikw)*Cout + co over the phase's taps
+        const int kidx = fdiv(k, o.g.dCout), co = k - kidx * o.g.Cout;
+        const int ikh = fdiv(kidx, dnkw), ikw = kidx - ikh * r2[i];
+        const int oh = r0[i] - ikh, ow = r1[i] - ikw;
+        ok = k < kmax && oh >= 0 && oh < o.g.Ho && ow >= 0 && ow < o.g.Wo;
+        off = rowbase[i] + ((oh * o.g.Wo + ow) * o.g.Cout + co);
       } else if constexpr (KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S) {
-        if (k < kmax && mn < mnmax) {
-          const int kh = r0[i] + ks0[i] * o.g.stride;
-          const int kw = r1[i] + ks1[i] * o.g.stride;
-          const int off = ((kh * o.g.kk + kw) * o.g.Cout + ks2[i]) * o.g.C + mn;
-          if constexpr (V4) {
-            a = ld4(o.p0, off);
-          } else {
-            a.x = o.p0[off];
-          }
-        }
+        const int kidx = fdiv(k, o.g.dCout), co = k - kidx * o.g.Cout;
+        const int ikh = fdiv(kidx, dnkw), ikw = kidx - ikh * r2[i];
+        const int kh = r0[i] + ikh * o.g.stride;
+        const int kw = r1[i] + ikw * o.g.stride;
+        ok = k < kmax && mn < mnmax;
+        off = ((kh * o.g.kk + kw) * o.g.Cout + co) * o.g.C + mn;
       } else if constexpr (KIND == LD_CWG_A4 || KIND == LD_CWG_A_S) {
-        if (k < o.K) {
-          if (mn < o.MN) {
-            const int ih = ks1[i] * o.g.stride - o.g.pt + r0[i];
-            const int iw = ks2[i] * o.g.stride - o.g.pl + r1[i];
-            if (ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W) {
-              const int64_t off = (int64_t)ks0[i] * (o.g.H * o.g.W * o.g.C) + ((ih * o.g.W + iw) * o.g.C + r2[i]);
-              if constexpr (V4) {
-                a = ld4(o.p0, off);
-              } else {
-                a.x = o.p0[off];
-              }
-            }
-          } else if (mn == o.ones_row) {
-            a.x = 1.f;
-          }
-        }
+        // k = (n*Ho + oh)*Wo + ow
+        const int n = fdiv(k, o.g.dHW), pix = k - n * (o.g.Ho * o.g.Wo);
+        const int oh = fdiv(pix, o.g.dWo), ow = pix - oh * o.g.Wo;
+        const int ih = oh * o.g.stride - o.g.pt + r0[i];
+        const int iw = ow * o.g.stride - o.g.pl + r1[i];
+        ok = k < o.K && mn < o.MN && ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W;
+        one = k < o.K && mn == o.ones_row;
+        off = (int64_t)n * (o.g.H * o.g.W * o.g.C) + ((ih * o.g.W + iw) * o.g.C + r2[i]);
       }
+      const int64_t so = ok ? off : 0;
+      float4 a = ldv<V4>(o.p0, so), b = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (NT == 2) b = ldv<V4>(o.p1, so);
+      a = make_float4(ok ? a.x : (one ? 1.f : 0.f), ok ? a.y : 0.f, ok ? a.z : 0.f, ok ? a.w : 0.f);
+      b = make_float4(ok ? b.x : 0.f, ok ? b.y : 0.f, ok ? b.z : 0.f, ok ? b.w : 0.f);
       if constexpr (V4) {
         v[0][i] = a;
         if constexpr (NT == 2) v[1][i] = b;
@@ -460,7 +350,6 @@ struct Loader {
         if constexpr (NT == 2) v[1][i] = b.x;
       }
     }
-    advance_k(o);
   }
 
   __device__ __forceinline__ void store(float* s) const {
@@ -591,8 +480,6 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   Loader<KB, NB, BN, BK, NTH> lb;
   la.init(g.a, z, m0, tid);
   lb.init(g.b, z, n0, tid);
-  la.init_k(g.a, kbeg);
-  lb.init_k(g.b, kbeg);
 
   floatx16 accM[TM][TN], accV[TM][TN];
 #pragma unroll
@@ -862,8 +749,8 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
   // fraction of peak, per config
   static const int kBpc[] = {2, 3, 3, 4, 8};
   static const int kWaves[] = {8, 4, 4, 4, 1};
-  static const double kEff[] = {0.67, 0.58, 0.61, 0.57, 0.33};
-  const double kSplitSecPerByte = 1.07e-13, kSplitLaunch = 8.9e-6;
+  static const double kEff[] = {0.65, 0.58, 0.61, 0.61, 0.33};
+  const double kSplitSecPerByte = 9.65e-14, kSplitLaunch = 8.9e-6;
   Plan best{kNumCfg - 1, 1, (int)Kred, 1, 1};
   double best_t = DBL_MAX;
   const double peak_cu = 157.3e12 / 256.0;
@@ -888,7 +775,7 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
       // time for one CU to finish r co-resident blocks
       auto round_s = [&](int64_t r) {
         const double wps = (double)r * kWaves[ci] / 4.0;  // waves per SIMD
-        const double occ = wps >= 3.0 ? 1.0 : (wps >= 2.0 ? 0.85 : (wps >= 1.0 ? 0.6 : 0.35));
+        const double occ = wps >= 3.0 ? 1.0 : (wps >= 2.0 ? 0.93 : (wps >= 1.0 ? 0.55 : 0.35));
         return (double)r * block_s / occ;
       };
       const int64_t slots = 256 * (int64_t)kBpc[ci];

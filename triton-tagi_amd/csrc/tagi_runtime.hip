@@ -120,3 +120,37 @@ extern "C" int tagi_prof_end(double* ms, int64_t* launches, double* flops, doubl
   p.used = 0;
   return TAGI_OK;
 }
+
+// ------------------------------------------------------------------ ceiling probe
+// A loop of independent fp32 MFMAs with no memory traffic: each 64-lane wave keeps four
+// 32x32 accumulators in flight. Its rate bounds what any fp32 MFMA kernel can sustain at
+// the same number of waves per SIMD.
+namespace {
+typedef float probe_floatx16 __attribute__((ext_vector_type(16)));
+__global__ void __launch_bounds__(256) mfma_loop_kernel(float* __restrict__ out, int iters) {
+  probe_floatx16 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
+  const float x = 1.0f + threadIdx.x * 1e-6f, y = 1.0f;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc[i], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s += acc[i][v];
+  out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+}  // namespace
+
+extern "C" int tagi_probe_mfma_loop(float* out, int64_t blocks, int64_t iters, tagi_stream_t stream) {
+  const char* what = "tagi_probe_mfma_loop";
+  TAGI_REQUIRE(out != nullptr && blocks > 0 && blocks <= (1 << 20) && iters > 0 && iters < (1ll << 31),
+               "%s: bad arguments", what);
+  hipLaunchKernelGGL(mfma_loop_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, out, (int)iters);
+  return check_launch(what);
+}
