@@ -274,6 +274,7 @@ extern "C" int tagi_conv2d_wgrad(const float* ma, const float* dmz, const float*
   a.epi = epi_wgrad(dmw, dSw, dmb, dSb, Sw, Sb, K, N);
   a.epi.perm_C = (int)g->C;
   a.epi.perm_kk2 = (int)(g->k * g->k);
+  a.epi.dperm = make_fastdiv((int)g->C);
   a.R = (int)(K + (bias ? 1 : 0));
   a.C = (int)N;
   a.Kred = (int)M;

@@ -131,6 +131,7 @@ struct Epi {
   int wrows;
   int64_t ldw;
   int perm_C, perm_kk2;  // conv: row r = (kh*kk+kw)*C + c maps to weight row c*kk2 + kh*kk + kw
+  FastDiv dperm;         // divider for perm_C
   // kind 2
   ConvG g;
   const float* am;  // optional addend (same layout as the output): out = delta + addend
@@ -391,7 +392,7 @@ __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col,
     if (row < e.wrows) {
       int wr = row;
       if (e.perm_C > 0) {
-        const int kidx = row / e.perm_C;
+        const int kidx = fdiv(row, e.dperm);
         wr = (row - kidx * e.perm_C) * e.perm_kk2 + kidx;
       }
       const int64_t idx = (int64_t)wr * e.ldw + col;
@@ -592,26 +593,88 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
     __syncthreads();
   }
 
-  // Epilogue: direct store, or split-K partials (phased launches never split).
-  const int64_t plane = (int64_t)g.R * g.C;
+  // Epilogue: split-K partial sums, or the layer's epilogue. The epilogue kind is the same
+  // for the whole launch, so each kind gets its own unrolled loop with the per-block
+  // invariants (bias columns, the stride phase and its pixel dividers) hoisted out.
+  const Epi& e = g.epi;
+  if (g.partial) {
+    const int64_t plane = (int64_t)g.R * g.C;
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
-        const int col = n0 + wn * WN + j * 32 + rl;
-        if (row < R && col < g.C) {
-          if (g.partial) {
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+          const int col = n0 + wn * WN + j * 32 + rl;
+          if (row < R && col < g.C) {
             const int64_t base = ((int64_t)zz * 2) * plane + (int64_t)row * g.C + col;
             g.partial[base] = accM[i][j][v];
             g.partial[base + plane] = accV[i][j][v];
-          } else {
-            epi_apply(g.epi, z, row, col, accM[i][j][v], accV[i][j][v]);
+          }
+        }
+  } else if (e.kind == 0 && e.b_sr == 0) {
+    // plain store with an optional per-column bias (Linear, Conv2D forward, bmm)
+    const int64_t zoff = (z / e.zdiv) * e.sz1 + (z % e.zdiv) * e.sz2;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * WN + j * 32 + rl;
+      const bool cok = col < g.C;
+      const float bmj = (e.bm && cok) ? e.bm[(int64_t)col * e.b_sc] : 0.f;
+      const float bvj = (e.bv && cok) ? e.bv[(int64_t)col * e.b_sc] : 0.f;
+      const int64_t coff = zoff + (int64_t)col * e.scol;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+          if (row < R && cok) {
+            const int64_t off = coff + (int64_t)row * e.srow;
+            if (e.om) e.om[off] = accM[i][j][v] * e.sm + bmj;
+            e.ov[off] = accV[i][j][v] * e.sv + bvj;
+          }
+        }
+    }
+  } else if (e.kind == 2) {
+    // conv input delta: row q of stride phase z is input pixel (n, hh*s + a, ww*s + b)
+    const Phase ph = make_phase(e.g, z);
+    const int hq = ph.Hq * ph.Wq;
+    const FastDiv dhq = make_fastdiv(hq > 0 ? hq : 1), dwq = make_fastdiv(ph.Wq > 0 ? ph.Wq : 1);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+        const int n = fdiv(row, dhq), rr = row - n * hq;
+        const int hh = fdiv(rr, dwq), ww = rr - hh * ph.Wq;
+        const int64_t pix = ((int64_t)n * e.g.H + (hh * e.g.stride + ph.a)) * e.g.W + (ww * e.g.stride + ph.b);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int col = n0 + wn * WN + j * 32 + rl;
+          if (row < R && col < g.C) {
+            const int64_t off = pix * e.g.C + col;
+            float m = accM[i][j][v], vv = accV[i][j][v];
+            if (e.am) {
+              m = m + e.am[off];
+              vv = vv + e.av[off];
+            }
+            e.om[off] = m;
+            e.ov[off] = vv;
           }
         }
       }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+          const int col = n0 + wn * WN + j * 32 + rl;
+          if (row < R && col < g.C) epi_apply(e, z, row, col, accM[i][j][v], accV[i][j][v]);
+        }
+  }
 }
 
 // Deterministic split-K reduction followed by the epilogue. A block owns 64*V consecutive
