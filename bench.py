@@ -41,6 +41,8 @@ WORKLOAD_DESC = {
     "mlp": "TAGI MLP 784-256-128-10 ReLU + Remax, batch 256",
     "transformer": "TAGI transformer block (Embedding 64x256 + PE + MHA-V2 8 heads + RMSNorm + Linear 256-64), "
                    "batch 64, seq 256",
+    "linear": "TAGI Linear layer microbench, (batch, in, out) = (4096,4096,4096), (8192,1024,4096), "
+              "(256,4096,11008): forward moments + backward deltas + capped update",
 }
 
 
@@ -134,6 +136,41 @@ def measure_ceilings(dev: str) -> dict:
     return out
 
 
+def linear_bench(args) -> dict:
+    """Linear microbenchmark: per shape, W warm-up then K timed steps of forward moments,
+    backward deltas (input deltas and parameter deltas) and the capped update."""
+    import torch
+
+    from triton_tagi_amd import workloads
+    from triton_tagi_amd.update.parameters import get_cap_factor
+
+    shapes, total_flops, total_s = [], 0.0, 0.0
+    for (B, K, N) in workloads.LINEAR_SHAPES:
+        layer, ma, Sa, dmz, dSz = workloads.linear_microbench(B, K, N)
+        cap = get_cap_factor(B)
+
+        def step():
+            layer.forward(ma, Sa)
+            layer.backward(dmz, dSz)
+            layer.update(cap)
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / args.steps
+        flops = 7 * 2.0 * B * K * N
+        total_flops += flops
+        total_s += dt
+        shapes.append({"batch": B, "in": K, "out": N, "ms_per_step": round(dt * 1e3, 4),
+                       "tflops": round(flops / dt / 1e12, 2), "mfma_frac": round(flops / dt / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)})
+        del layer, ma, Sa, dmz, dSz
+    return {"tflops": total_flops / total_s / 1e12, "ms": total_s * 1e3, "shapes": shapes}
+
+
 def load_traffic(workload: str, family: str):
     p = ROOT / "profiles" / "traffic.json"
     if not p.exists():
@@ -178,6 +215,19 @@ def main():
     if args.ceilings:
         log("[bench] measuring ceilings")
         print(json.dumps({"ceilings": measure_ceilings(dev)}), flush=True)
+        return
+    if args.workload == "linear":
+        log("[bench] Linear microbenchmark")
+        r = linear_bench(args)
+        print(json.dumps({
+            "metric": "TAGI Linear microbench step (fwd+bwd+update) TFLOP/s, 7 x 2MKN flops per shape",
+            "value": round(r["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(r["ms"], 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp32", "data": "synthetic (seeded moments and priors as described in config)",
+            "config": {"workload": WORKLOAD_DESC["linear"], "parallelism": "single GPU"},
+            "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2), "peak": PEAK_FP32_MFMA_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None},
+            "cpu_baseline": None, "shapes": r["shapes"]}), flush=True)
         return
     log(f"[bench] building {args.workload} on {dev}")
     w = workloads.build(args.workload, device=dev, batch=args.batch)
