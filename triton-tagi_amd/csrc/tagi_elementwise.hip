@@ -249,7 +249,7 @@ __global__ void __launch_bounds__(256) remax_kernel(const float* __restrict__ mz
   if (row >= rows) return;
   const float* pm = mz + row * K;
   const float* ps = Sz + row * K;
-  float mu_z[EPT], var_z[EPT], mu_m[EPT], var_m[EPT], jcb[EPT];
+  float var_z[EPT], mu_m[EPT], var_m[EPT], jcb[EPT];
   float s_mu = 0.f, s_var = 0.f;
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
@@ -257,18 +257,19 @@ __global__ void __launch_bounds__(256) remax_kernel(const float* __restrict__ mz
     const bool ok = c < K;
     const float m = ok ? pm[c] : 0.f;
     const float v = ok ? ps[c] : 1.f;
-    const float sd = sqrtf(v);
-    const float al = m / sd;
-    const float pdf = INV_SQRT_2PI * expf(-0.5f * al * al);
-    const float cdf = 0.5f * erfcf(-al * INV_SQRT_2);
+    const float rs = fast_rsqrt(v);
+    const float sd = v * rs;
+    const float al = m * rs;
+    const float pdf = INV_SQRT_2PI * fast_exp(-0.5f * al * al);
+    float cdf, ccdf;
+    normal_cdf_pair(al, cdf, ccdf);
     const float mraw = m * cdf + sd * pdf;
     const float mm = fmaxf(mraw, EPS);
     // same variance as -mm^2 + 2 mm m - m sd pdf + (v - m^2) cdf while the mean floor is
     // inactive (see rect_var); the floored case keeps the reference's expression
-    const float vraw = (mraw >= EPS) ? rect_var(v, al, pdf, cdf, 0.5f * erfcf(al * INV_SQRT_2))
+    const float vraw = (mraw >= EPS) ? rect_var(v, al, pdf, cdf, ccdf)
                                      : -mm * mm + 2.0f * mm * m - m * sd * pdf + (v - m * m) * cdf;
     const float vm = fmaxf(vraw, EPS);
-    mu_z[e] = m;
     var_z[e] = v;
     mu_m[e] = mm;
     var_m[e] = vm;
@@ -280,41 +281,42 @@ __global__ void __launch_bounds__(256) remax_kernel(const float* __restrict__ mz
   }
   const float mu_mt = fmaxf(wave_sum(s_mu), EPS);
   const float var_mt = fmaxf(wave_sum(s_var), EPS);
+  const float inv_mt = fast_rcp(mu_mt);
   // log1p/expm1 below are the reference's log(1 + x) / exp(x) - 1 without fp32 cancellation
-  const float var_log_mt = log1pf(var_mt / (mu_mt * mu_mt));
+  const float var_log_mt = log1p_pos(var_mt * inv_mt * inv_mt);
   const float mu_log_mt = logf(mu_mt) - 0.5f * var_log_mt;
   float var_log_m[EPT], cov_m_mt[EPT], mu_a_raw[EPT], var_log_a[EPT];
   float s_a = 0.f;
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const int c = lane + 64 * e;
-    const float vlm = log1pf(var_m[e] / (mu_m[e] * mu_m[e]));
+    const float rm = fast_rcp(mu_m[e]);
+    const float vlm = log1p_pos(var_m[e] * rm * rm);
     const float mlm = logf(mu_m[e]) - 0.5f * vlm;
-    const float cov = log1pf(var_m[e] / (mu_m[e] * mu_mt));
+    const float cov = log1p_pos(var_m[e] * rm * inv_mt);
     const float mla = mlm - mu_log_mt;
     const float vla = fmaxf(vlm + var_log_mt - 2.0f * cov, 0.0f);
-    const float mar = fmaxf(expf(mla + 0.5f * vla), EPS);
+    const float mar = fmaxf(fast_exp(mla + 0.5f * vla), EPS);
     var_log_m[e] = vlm;
     cov_m_mt[e] = cov;
     var_log_a[e] = vla;
     mu_a_raw[e] = mar;
     if (c < K) s_a += mar;
   }
-  const float sum_a = fmaxf(wave_sum(s_a), EPS);
+  const float inv_sum_a = fast_rcp(fmaxf(wave_sum(s_a), EPS));
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const int c = lane + 64 * e;
     if (c >= K) continue;
-    const float mua = mu_a_raw[e] / sum_a;
+    const float mua = mu_a_raw[e] * inv_sum_a;
     const float vara = expm1f(var_log_a[e]) * mua * mua;
     const float cov_la_lm = var_log_m[e] - cov_m_mt[e];
     const float cov_am = expm1f(cov_la_lm) * mua * mu_m[e];
-    const float cs = sqrtf(vara * var_z[e]);
-    const float cov_az = fminf(cs, cov_am / fmaxf(jcb[e], EPS));
+    const float cs = __builtin_amdgcn_sqrtf(vara * var_z[e]);
+    const float cov_az = fminf(cs, cov_am * fast_rcp(fmaxf(jcb[e], EPS)));
     ma[row * K + c] = mua;
     Sa[row * K + c] = vara;
-    Jo[row * K + c] = cov_az / var_z[e];
-    (void)mu_z;
+    Jo[row * K + c] = cov_az * fast_rcp(var_z[e]);
   }
 }
 

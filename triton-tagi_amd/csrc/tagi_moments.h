@@ -7,6 +7,64 @@ namespace tagi {
 #define INV_SQRT_2PI 0.3989422804014327f
 #define INV_SQRT_2 0.7071067811865476f
 
+// ------------------------------------------------------------------------ fast fp32 math
+// The hardware transcendental instructions (v_rcp_f32, v_rsq_f32, v_exp_f32, v_log_f32)
+// are accurate to about 1 ulp on normal operands. The library forms add range reduction,
+// denormal scaling and correct rounding that the moment formulas below do not need: their
+// results are checked at a relative tolerance of 1e-4, and every use here is a few ulp.
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_rsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
+__device__ __forceinline__ float fast_div(float a, float b) { return a * __builtin_amdgcn_rcpf(b); }
+
+// exp(x) = 2^(x log2 e). The product x log2 e is carried as p + e (e from an fma and the
+// low part of log2 e), so its rounding (up to |x| 2^-24 absolute) does not reach the
+// result: 2^(p + e) = 2^p (1 + e ln 2) to second order in e. Relative error about 2 ulp
+// for results above 2^-126; smaller results (x < -87.3) flush to 0.
+__device__ __forceinline__ float fast_exp(float x) {
+  const float L2E = 1.44269502162933349609375f;   // log2(e) rounded to fp32
+  const float L2E_LO = 1.925963033500011e-8f;     // log2(e) - L2E
+  const float p = x * L2E;
+  const float e = fmaf(x, L2E, -p) + x * L2E_LO;
+  return __builtin_amdgcn_exp2f(p) * fmaf(e, 0.6931471805599453f, 1.0f);
+}
+
+// log(1 + x) for x >= 0 (finite) from one logarithm: with u = fl(1 + x), the factor
+// x / (u - 1) corrects the rounding of u (Goldberg, "What every computer scientist should
+// know about floating-point arithmetic", 1991, theorem 4), a few ulp for every x >= 0.
+__device__ __forceinline__ float log1p_pos(float x) {
+  const float u = 1.0f + x;
+  const float d = u - 1.0f;
+  return d == 0.0f ? x : logf(u) * fast_div(x, d);
+}
+
+// Upper tail of the standard normal, Q(a) = 0.5 erfc(a / sqrt 2), for a >= 0, by the
+// Chebyshev-fitted erfc of Press et al., Numerical Recipes in C, 2nd ed., sec. 6.2
+// ("erfcc": fractional error below 1.2e-7 in exact arithmetic; about 2e-6 evaluated in
+// fp32 for a < 5, 1e-5 for a < 13; 0 beyond a = 13, where Q < 1e-38).
+__device__ __forceinline__ float normal_tail(float a) {
+  const float z = a * INV_SQRT_2;
+  const float t = fast_rcp(fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = fmaf(p, t, -0.82215223f);
+  p = fmaf(p, t, 1.48851587f);
+  p = fmaf(p, t, -1.13520398f);
+  p = fmaf(p, t, 0.27886807f);
+  p = fmaf(p, t, -0.18628806f);
+  p = fmaf(p, t, 0.09678418f);
+  p = fmaf(p, t, 0.37409196f);
+  p = fmaf(p, t, 1.00002368f);
+  p = fmaf(p, t, -1.26551223f);
+  return 0.5f * t * fast_exp(fmaf(-z, z, p));
+}
+
+// Phi(alpha) and 1 - Phi(alpha) from one tail evaluation: the smaller of the two is the
+// tail itself and the other its complement, so neither side cancels.
+__device__ __forceinline__ void normal_cdf_pair(float alpha, float& cdf, float& ccdf) {
+  const float tail = normal_tail(fabsf(alpha));
+  cdf = alpha >= 0.0f ? 1.0f - tail : tail;
+  ccdf = alpha >= 0.0f ? tail : 1.0f - tail;
+}
+
 // ------------------------------------------------------------------------------ ReLU
 // relu.py:43-86: exact rectified-Gaussian moments; Phi by erf, replaced by the
 // asymptotic pdf/(-alpha) when alpha < -5; variance floored at 0.
@@ -21,17 +79,17 @@ __device__ __forceinline__ float rect_var(float S, float alpha, float pdf, float
 
 __device__ __forceinline__ void relu_moments(float mz, float Sz, float& ma, float& Sa, float& J) {
   const float Ss = fmaxf(Sz, 1e-30f);
-  const float sig = sqrtf(Ss);
-  const float alpha = mz / sig;
-  const float pdf = expf(-0.5f * alpha * alpha) * INV_SQRT_2PI;
-  // Phi(alpha) = 0.5 (1 + erf(alpha/sqrt2)) evaluated as 0.5 erfc(-alpha/sqrt2): equal in
-  // exact arithmetic, without the fp32 cancellation of the erf form for alpha < 0.
+  const float rs = fast_rsqrt(Ss);
+  const float sig = Ss * rs;
+  const float alpha = mz * rs;
+  const float pdf = fast_exp(-0.5f * alpha * alpha) * INV_SQRT_2PI;
+  // Phi(alpha) = 0.5 (1 + erf(alpha/sqrt2)) is taken from the normal tail: equal in exact
+  // arithmetic, without the fp32 cancellation of the erf form for alpha < 0.
   const bool asym = alpha < -5.0f;
-  // one erfc gives the smaller tail; the other side is its complement (no cancellation)
-  const float tail = 0.5f * erfcf(fabsf(alpha) * INV_SQRT_2);
-  const float cdf_e = alpha >= 0.0f ? 1.0f - tail : tail;
-  const float cdf = asym ? pdf / (-alpha) : cdf_e;
-  const float Q = asym ? 1.0f - cdf : (alpha >= 0.0f ? tail : 1.0f - tail);
+  float cdf_e, Q_e;
+  normal_cdf_pair(alpha, cdf_e, Q_e);
+  const float cdf = asym ? fast_div(pdf, -alpha) : cdf_e;
+  const float Q = asym ? 1.0f - cdf : Q_e;
   ma = sig * pdf + mz * cdf;
   Sa = fmaxf(rect_var(Ss, alpha, pdf, cdf, Q), 0.0f);
   J = cdf;

@@ -15,13 +15,22 @@ namespace tagi {
 // sums stay in registers and every load is a coalesced float4.
 static inline bool bn_vec(int64_t C) { return C % 4 == 0 && C <= 1024 && 1024 % C == 0; }
 
-// Reduction blocks: about 8192 elements each, at most 2048 (the finalize pass reads one
-// partial per block and channel, so more blocks make it slower than they save).
-static inline int bn_blocks(int64_t rows, int64_t C) {
-  int64_t b = cdiv(rows * C, 8192);
-  if (b > 2048) b = 2048;
-  if (b > rows) b = rows;
+// Reduction grid: blocks own contiguous ranges of about 32 or more rows (at most 1024
+// ranges, so a channel has at most 1024 partials) and, in the float4 path, a chunk of the
+// channels: chunks halve (down to 16 channels) until the grid has 512 blocks, which keeps
+// small layers spread over the CUs while the partials stay a few percent of the traffic.
+// Partials are stored quantity-major then channel then row range,
+// ws[(q * C + c) * nbr + b], so the finalize pass reads each channel's contiguously.
+static inline int red_rows(int64_t rows) {
+  int64_t b = cdiv(rows, 32);
+  if (b > 1024) b = 1024;
   return (int)(b < 1 ? 1 : b);
+}
+static inline int red_chunks(int nbr, int64_t C, bool vec) {
+  int ncc = 1;
+  if (!vec) return ncc;
+  for (int64_t W = C; (int64_t)nbr * ncc < 512 && W >= 32; W >>= 1) ncc <<= 1;
+  return ncc;
 }
 
 // Per-block partial sums over the block's rows (finalized by the kernels below).
@@ -74,7 +83,8 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
   const int64_t r0 = rows * blockIdx.x / nblk, r1 = rows * (blockIdx.x + 1) / nblk;
   const int t = threadIdx.x;
   if constexpr (VEC) {
-    const int cq = C >> 2, rpi = 256 / cq;
+    const int W = C / (int)gridDim.y, c0 = (int)blockIdx.y * W;  // this block's channel chunk
+    const int cq = W >> 2, rpi = 256 / cq;
     const int c4 = t % cq, rr = t / cq;
     float acc[4][NQ];
 #pragma unroll
@@ -85,7 +95,7 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
     if constexpr (MODE >= 2) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int c = 4 * c4 + j;
+        const int c = c0 + 4 * c4 + j;
         const float rv = var[c] + eps;
         km[j] = mg[c] * (1.0f / sqrtf(rv));
         kS[j] = mg[c] * mg[c] * (1.0f / rv);
@@ -93,7 +103,7 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
     }
 #pragma unroll 2
     for (int64_t row = r0 + rr; row < r1; row += rpi) {
-      const int64_t off = row * C + 4 * c4;
+      const int64_t off = row * C + c0 + 4 * c4;
       const float4 a = *reinterpret_cast<const float4*>(x0 + off);
       const float4 b = *reinterpret_cast<const float4*>(x1 + off);
       float4 h = make_float4(0.f, 0.f, 0.f, 0.f), jj = h;
@@ -112,12 +122,12 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
 #pragma unroll
       for (int q = 0; q < NQ; ++q) red[(t * 4 + j) * NQ + q] = acc[j][q];
     __syncthreads();
-    for (int c = t; c < C; c += 256) {
-      const int g4 = c >> 2, j = c & 3;
+    for (int cl = t; cl < W; cl += 256) {
+      const int g4 = cl >> 2, j = cl & 3;
       for (int q = 0; q < NQ; ++q) {
         float sum = 0.f;
         for (int r = 0; r < rpi; ++r) sum += red[((r * cq + g4) * 4 + j) * NQ + q];
-        ws[((int64_t)blockIdx.x * C + c) * NQ + q] = sum;
+        ws[((int64_t)q * C + c0 + cl) * nblk + blockIdx.x] = sum;
       }
     }
   } else {
@@ -140,36 +150,53 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
         if constexpr (MODE >= 1) y0[off] = o0;
         if constexpr (MODE >= 2) y1[off] = o1;
       }
-      for (int q = 0; q < NQ; ++q) ws[((int64_t)blockIdx.x * C + c) * NQ + q] = acc[q];
+      for (int q = 0; q < NQ; ++q) ws[((int64_t)q * C + c) * nblk + blockIdx.x] = acc[q];
     }
   }
 }
 
-// One wavefront per channel: lanes take partials lane, lane+64, ... then a butterfly sum
-// (a fixed order, so the result does not depend on timing).
+// One 256-thread block per channel: thread t adds partials t, t + 256, ... (contiguous
+// across the block), then a fixed butterfly within each wave and a fixed-order sum over
+// the four waves, so the result does not depend on timing.
 __device__ __forceinline__ float wave_reduce(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
 
-__global__ void bn_stats_finalize_kernel(const float* __restrict__ ws, float* __restrict__ bmean,
+template <int NQ>
+__device__ __forceinline__ void channel_sums(const float* __restrict__ ws, int C, int c, int nblk, float* out) {
+  __shared__ float part[4][NQ];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  float acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) acc[q] = 0.f;
+  // at most 1024 partials: up to 4 iterations, all loads issued together
+#pragma unroll 4
+  for (int b = t; b < nblk; b += 256) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) acc[q] += ws[((int64_t)q * C + c) * nblk + b];
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) acc[q] = wave_reduce(acc[q]);
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) part[w][q] = acc[q];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) out[q] = (part[0][q] + part[1][q]) + (part[2][q] + part[3][q]);
+}
+
+__global__ void __launch_bounds__(256) bn_stats_finalize_kernel(const float* __restrict__ ws, float* __restrict__ bmean,
                                          float* __restrict__ bvar, float* __restrict__ rmean,
                                          float* __restrict__ rvar, float* __restrict__ mg, int C, int nblk,
                                          double n, float momentum, float eps, int first_call, int preserve_var) {
   const int c = blockIdx.x;
-  const int lane = threadIdx.x;
-  float a = 0.f, b = 0.f, q = 0.f;
-  for (int s = lane; s < nblk; s += 64) {
-    const float* p = ws + ((int64_t)s * C + c) * 3;
-    a += p[0];
-    b += p[1];
-    q += p[2];
-  }
-  a = wave_reduce(a);
-  b = wave_reduce(b);
-  q = wave_reduce(q);
-  if (lane != 0) return;
+  float sums[3];
+  channel_sums<3>(ws, C, c, nblk, sums);
+  const float a = sums[0], b = sums[1], q = sums[2];
+  if (threadIdx.x != 0) return;
   const float inv = (float)(1.0 / n);
   const float mean = a * inv;
   const float bessel = (float)(n / (n - 1.0));
@@ -213,13 +240,14 @@ __global__ void __launch_bounds__(256) bn_apply_vec_kernel(
     float* __restrict__ Shat, int64_t rows, int C, int64_t rows_per_block, float eps) {
   const int cq = C >> 2, rpi = 256 / cq;
   const int t = threadIdx.x, c4 = t % cq, rr = t / cq;
-  float k_mean[4], k_rv[4], k_is[4], k_g[4], k_sg[4], k_b[4], k_sb[4];
+  float k_mean[4], k_irv[4], k_is[4], k_g[4], k_sg[4], k_b[4], k_sb[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = 4 * c4 + j;
     k_mean[j] = mean[c];
-    k_rv[j] = var[c] + eps;
-    k_is[j] = 1.0f / sqrtf(k_rv[j]);
+    const float rv = var[c] + eps;
+    k_irv[j] = 1.0f / rv;
+    k_is[j] = 1.0f / sqrtf(rv);
     k_g[j] = mg[c];
     k_sg[j] = Sg[c];
     k_b[j] = mb[c];
@@ -245,7 +273,7 @@ __global__ void __launch_bounds__(256) bn_apply_vec_kernel(
       float x, v;
       bn_in<RELU>(mv[j], sv[j], x, v);
       mh[j] = (x - k_mean[j]) * k_is[j];
-      sh[j] = v / k_rv[j];
+      sh[j] = v * k_irv[j];
       om[j] = k_g[j] * mh[j] + k_b[j];
       os[j] = k_g[j] * k_g[j] * sh[j] + k_sg[j] * mh[j] * mh[j] + k_sg[j] * sh[j] + k_sb[j];
       if constexpr (ADD) {
@@ -277,7 +305,7 @@ __global__ void bn_apply_scalar_kernel(const float* __restrict__ mz, const float
     float x, v;
     bn_in<RELU>(mz[i], Sz[i], x, v);
     const float mh = (x - mean[c]) * inv_std;
-    const float sh = v / rv;
+    const float sh = v * (1.0f / rv);
     float om = g * mh + mb[c];
     float os = g * g * sh + sg * mh * mh + sg * sh + Sb[c];
     if constexpr (ADD) {
@@ -291,24 +319,14 @@ __global__ void bn_apply_scalar_kernel(const float* __restrict__ mz, const float
   }
 }
 
-__global__ void bn_bwd_finalize_kernel(const float* __restrict__ ws, const float* __restrict__ Sg,
+__global__ void __launch_bounds__(256) bn_bwd_finalize_kernel(const float* __restrict__ ws, const float* __restrict__ Sg,
                                        const float* __restrict__ Sb, float* __restrict__ dmg, float* __restrict__ dSg,
                                        float* __restrict__ dmb, float* __restrict__ dSb, int C, int nblk) {
   const int c = blockIdx.x;
-  const int lane = threadIdx.x;
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  for (int s = lane; s < nblk; s += 64) {
-    const float* p = ws + ((int64_t)s * C + c) * 4;
-    s0 += p[0];
-    s1 += p[1];
-    s2 += p[2];
-    s3 += p[3];
-  }
-  s0 = wave_reduce(s0);
-  s1 = wave_reduce(s1);
-  s2 = wave_reduce(s2);
-  s3 = wave_reduce(s3);
-  if (lane != 0) return;
+  float sums[4];
+  channel_sums<4>(ws, C, c, nblk, sums);
+  const float s0 = sums[0], s1 = sums[1], s2 = sums[2], s3 = sums[3];
+  if (threadIdx.x != 0) return;
   const float g = Sg[c], b = Sb[c];
   dmg[c] = g * s0;
   dSg[c] = g * g * s1;
@@ -352,15 +370,65 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const float* __restric
   }
 }
 
-// Backward: each block owns a slab of rows; threads stride over the D columns, so the
-// per-column partial sums need no cross-thread reduction.
-__global__ void rmsnorm_bwd_partial_kernel(const float* __restrict__ dmz, const float* __restrict__ dSz,
-                                           const float* __restrict__ ma, const float* __restrict__ inv_rms,
-                                           const float* __restrict__ mw, float* __restrict__ dma,
-                                           float* __restrict__ dSa, float* __restrict__ ws, int64_t rows, int D,
-                                           int rows_per_block) {
-  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
-  const int64_t r1 = min(rows, r0 + rows_per_block);
+// Backward (rms_norm.py:115-134): per-row scaling of the deltas plus two per-column sums
+// (the weight deltas). Blocks own contiguous row ranges, rows * b / nblk ..; partial sums
+// go to ws[(q * D + c) * nblk + b] and are added by the finalize kernel in a fixed order.
+// Float4 path (D % 4 == 0 and D divides 1024): each thread keeps one group of 4 columns
+// for the block's whole row range, as the BatchNorm reductions do.
+__global__ void __launch_bounds__(256) rmsnorm_bwd_partial_vec_kernel(
+    const float* __restrict__ dmz, const float* __restrict__ dSz, const float* __restrict__ ma,
+    const float* __restrict__ inv_rms, const float* __restrict__ mw, float* __restrict__ dma,
+    float* __restrict__ dSa, float* __restrict__ ws, int64_t rows, int D, int nblk) {
+  __shared__ float red[256 * 4 * 2];
+  const int64_t r0 = rows * blockIdx.x / nblk, r1 = rows * (blockIdx.x + 1) / nblk;
+  const int W = D / (int)gridDim.y, c0 = (int)blockIdx.y * W;  // this block's column chunk
+  const int cq = W >> 2, rpi = 256 / cq;
+  const int t = threadIdx.x, c4 = t % cq, rr = t / cq;
+  const float4 w4 = *reinterpret_cast<const float4*>(mw + c0 + 4 * c4);
+  const float w[4] = {w4.x, w4.y, w4.z, w4.w};
+  float am[4] = {0.f, 0.f, 0.f, 0.f}, as[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+  for (int64_t row = r0 + rr; row < r1; row += rpi) {
+    const float inv = inv_rms[row];
+    const int64_t off = row * D + c0 + 4 * c4;
+    const float4 d4 = *reinterpret_cast<const float4*>(dmz + off);
+    const float4 s4 = *reinterpret_cast<const float4*>(dSz + off);
+    const float4 m4 = *reinterpret_cast<const float4*>(ma + off);
+    const float dm[4] = {d4.x, d4.y, d4.z, d4.w}, ds[4] = {s4.x, s4.y, s4.z, s4.w}, m[4] = {m4.x, m4.y, m4.z, m4.w};
+    float o0[4], o1[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float k = inv * w[j];
+      o0[j] = k * dm[j];
+      o1[j] = k * k * ds[j];
+      am[j] += inv * m[j] * dm[j];
+      as[j] += inv * inv * m[j] * m[j] * ds[j];
+    }
+    *reinterpret_cast<float4*>(dma + off) = make_float4(o0[0], o0[1], o0[2], o0[3]);
+    *reinterpret_cast<float4*>(dSa + off) = make_float4(o1[0], o1[1], o1[2], o1[3]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    red[(t * 4 + j) * 2] = am[j];
+    red[(t * 4 + j) * 2 + 1] = as[j];
+  }
+  __syncthreads();
+  for (int cl = t; cl < W; cl += 256) {
+    const int g4 = cl >> 2, j = cl & 3;
+    for (int q = 0; q < 2; ++q) {
+      float sum = 0.f;
+      for (int r = 0; r < rpi; ++r) sum += red[((r * cq + g4) * 4 + j) * 2 + q];
+      ws[((int64_t)q * D + c0 + cl) * nblk + blockIdx.x] = sum;
+    }
+  }
+}
+
+// Scalar path: threads stride over the columns and walk the block's rows.
+__global__ void __launch_bounds__(256) rmsnorm_bwd_partial_kernel(
+    const float* __restrict__ dmz, const float* __restrict__ dSz, const float* __restrict__ ma,
+    const float* __restrict__ inv_rms, const float* __restrict__ mw, float* __restrict__ dma,
+    float* __restrict__ dSa, float* __restrict__ ws, int64_t rows, int D, int nblk) {
+  const int64_t r0 = rows * blockIdx.x / nblk, r1 = rows * (blockIdx.x + 1) / nblk;
   for (int c = threadIdx.x; c < D; c += blockDim.x) {
     const float w = mw[c];
     float s_mu = 0.f, s_var = 0.f;
@@ -368,29 +436,29 @@ __global__ void rmsnorm_bwd_partial_kernel(const float* __restrict__ dmz, const 
       const float inv = inv_rms[r];
       const int64_t i = r * D + c;
       const float dm = dmz[i], ds = dSz[i], m = ma[i];
-      const float t = inv * w;
-      dma[i] = t * dm;
-      dSa[i] = t * t * ds;
+      const float k = inv * w;
+      dma[i] = k * dm;
+      dSa[i] = k * k * ds;
       s_mu += inv * m * dm;
       s_var += inv * inv * m * m * ds;
     }
-    ws[((int64_t)blockIdx.x * 2) * D + c] = s_mu;
-    ws[((int64_t)blockIdx.x * 2 + 1) * D + c] = s_var;
+    ws[(int64_t)c * nblk + blockIdx.x] = s_mu;
+    ws[((int64_t)D + c) * nblk + blockIdx.x] = s_var;
   }
 }
 
-__global__ void rmsnorm_bwd_finalize_kernel(const float* __restrict__ ws, const float* __restrict__ Sw,
-                                            float* __restrict__ dmw, float* __restrict__ dSw, int D, int nblk) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= D) return;
-  float a = 0.f, b = 0.f;
-  for (int k = 0; k < nblk; ++k) {
-    a += ws[((int64_t)k * 2) * D + c];
-    b += ws[((int64_t)k * 2 + 1) * D + c];
-  }
+// One 256-thread block per column (same fixed-order sum as the BatchNorm finalize).
+__global__ void __launch_bounds__(256) rmsnorm_bwd_finalize_kernel(const float* __restrict__ ws,
+                                                                   const float* __restrict__ Sw,
+                                                                   float* __restrict__ dmw, float* __restrict__ dSw,
+                                                                   int D, int nblk) {
+  const int c = blockIdx.x;
+  float sums[2];
+  channel_sums<2>(ws, D, c, nblk, sums);
+  if (threadIdx.x != 0) return;
   const float sw = Sw[c];
-  dmw[c] = a * sw;
-  dSw[c] = b * sw * sw;
+  dmw[c] = sums[0] * sw;
+  dSw[c] = sums[1] * sw * sw;
 }
 
 // ------------------------------------------------------------------- Embedding
@@ -479,7 +547,7 @@ static inline hipStream_t as_stream(tagi_stream_t s) { return (hipStream_t)s; }
 
 extern "C" int64_t tagi_bn_stats_ws_bytes(int64_t N, int64_t C, int64_t HW) {
   if (N <= 0 || C <= 0 || HW <= 0) return 0;
-  return (int64_t)bn_blocks(N * HW, C) * C * 3 * (int64_t)sizeof(float);
+  return (int64_t)red_rows(N * HW) * C * 3 * (int64_t)sizeof(float);
 }
 
 static inline bool al16p(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -496,9 +564,9 @@ static int bn_stats_impl(const char* what, bool relu, const float* mz, const flo
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_BN_STATS, s, 0.0, (relu ? 12.0 : 8.0) * N * C * HW);
   const int64_t rows = N * HW;
-  const int nblk = bn_blocks(rows, C);
+  const int nblk = red_rows(rows);
   const bool vec = bn_vec(C) && al16p(mz) && al16p(Sz) && (!relu || al16p(J));
-  const dim3 grid(nblk), blk(256);
+  const dim3 grid(nblk, red_chunks(nblk, C, vec)), blk(256);
   if (relu) {
     if (vec)
       hipLaunchKernelGGL((bn_reduce_kernel<1, true>), grid, blk, 0, s, mz, Sz, nullptr, nullptr, ws, rows, (int)C,
@@ -516,7 +584,7 @@ static int bn_stats_impl(const char* what, bool relu, const float* mz, const flo
   }
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(bn_stats_finalize_kernel, dim3((unsigned)C), dim3(64), 0, s, (const float*)ws,
+  hipLaunchKernelGGL(bn_stats_finalize_kernel, dim3((unsigned)C), dim3(256), 0, s, (const float*)ws,
                      batch_mean, batch_var, running_mean, running_var, mg, (int)C, nblk, (double)rows, momentum, eps,
                      first_call, preserve_var);
   return check_launch(what);
@@ -599,7 +667,7 @@ extern "C" int tagi_relu_bn_fwd(const float* mz, const float* Sz, const float* m
 
 extern "C" int64_t tagi_bn_bwd_ws_bytes(int64_t N, int64_t C, int64_t HW) {
   if (N <= 0 || C <= 0 || HW <= 0) return 0;
-  return (int64_t)bn_blocks(N * HW, C) * C * 4 * (int64_t)sizeof(float);
+  return (int64_t)red_rows(N * HW) * C * 4 * (int64_t)sizeof(float);
 }
 
 static int bn_bwd_impl(const char* what, const float* dma, const float* dSa, const float* mhat, const float* J,
@@ -614,10 +682,10 @@ static int bn_bwd_impl(const char* what, const float* dma, const float* dSa, con
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_BN_BWD, s, 0.0, (jac ? 24.0 : 20.0) * N * C * HW);
   const int64_t rows = N * HW;
-  const int nblk = bn_blocks(rows, C);
+  const int nblk = red_rows(rows);
   const bool vec = bn_vec(C) && al16p(dma) && al16p(dSa) && al16p(mhat) && al16p(dmz) && al16p(dSz) &&
                    (!jac || al16p(J));
-  const dim3 grid(nblk), blk(256);
+  const dim3 grid(nblk, red_chunks(nblk, C, vec)), blk(256);
   if (jac) {
     if (vec)
       hipLaunchKernelGGL((bn_reduce_kernel<3, true>), grid, blk, 0, s, dma, dSa, mhat, J, ws, rows, (int)C, nblk, var,
@@ -635,7 +703,7 @@ static int bn_bwd_impl(const char* what, const float* dma, const float* dSa, con
   }
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(bn_bwd_finalize_kernel, dim3((unsigned)C), dim3(64), 0, s, (const float*)ws, Sg, Sb,
+  hipLaunchKernelGGL(bn_bwd_finalize_kernel, dim3((unsigned)C), dim3(256), 0, s, (const float*)ws, Sg, Sb,
                      dmg, dSg, dmb, dSb, (int)C, nblk);
   return check_launch(what);
 }
@@ -678,14 +746,9 @@ extern "C" int tagi_rmsnorm_fwd(const float* ma, const float* Sa, const float* m
   return check_launch(what);
 }
 
-static inline int rms_rows_per_block(int64_t rows) {
-  int64_t r = cdiv(rows, 1024);
-  return (int)(r < 16 ? 16 : r);
-}
-
 extern "C" int64_t tagi_rmsnorm_bwd_ws_bytes(int64_t rows, int64_t D) {
   if (rows <= 0 || D <= 0) return 0;
-  return cdiv(rows, rms_rows_per_block(rows)) * 2 * D * (int64_t)sizeof(float);
+  return (int64_t)red_rows(rows) * 2 * D * (int64_t)sizeof(float);
 }
 
 extern "C" int tagi_rmsnorm_bwd(const float* dmz, const float* dSz, const float* ma, const float* inv_rms,
@@ -697,14 +760,19 @@ extern "C" int tagi_rmsnorm_bwd(const float* dmz, const float* dSz, const float*
   TAGI_REQUIRE(ws_bytes >= tagi_rmsnorm_bwd_ws_bytes(rows, D), "%s: workspace too small", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_RMSNORM, s, 0.0, 20.0 * rows * D);
-  const int rpb = rms_rows_per_block(rows);
-  const int nblk = (int)cdiv(rows, rpb);
-  hipLaunchKernelGGL(rmsnorm_bwd_partial_kernel, dim3((unsigned)nblk), dim3(256), 0, s, dmz, dSz, ma, inv_rms, mw, dma,
-                     dSa, ws, rows, (int)D, rpb);
+  const int nblk = red_rows(rows);
+  const bool vec = bn_vec(D) && al16p(dmz) && al16p(dSz) && al16p(ma) && al16p(mw) && al16p(dma) && al16p(dSa);
+  if (vec)
+    hipLaunchKernelGGL(rmsnorm_bwd_partial_vec_kernel, dim3((unsigned)nblk, red_chunks(nblk, D, true)), dim3(256), 0,
+                       s, dmz, dSz, ma, inv_rms,
+                       mw, dma, dSa, ws, rows, (int)D, nblk);
+  else
+    hipLaunchKernelGGL(rmsnorm_bwd_partial_kernel, dim3((unsigned)nblk), dim3(256), 0, s, dmz, dSz, ma, inv_rms, mw,
+                       dma, dSa, ws, rows, (int)D, nblk);
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(rmsnorm_bwd_finalize_kernel, dim3((unsigned)cdiv(D, 256)), dim3(256), 0, s, (const float*)ws, Sw,
-                     dmw, dSw, (int)D, nblk);
+  hipLaunchKernelGGL(rmsnorm_bwd_finalize_kernel, dim3((unsigned)D), dim3(256), 0, s, (const float*)ws, Sw, dmw, dSw,
+                     (int)D, nblk);
   return check_launch(what);
 }
 
