@@ -111,6 +111,23 @@ def test_remax(dev, B, K):
     assert_scaled_close(J, rJ, None, RTOL, ATOL, "remax J")
 
 
+@pytest.mark.parametrize("B,K", [(256, 256), (64, 10)])
+def test_remax_wide_range(dev, B, K):
+    """Remax where the rectified means span the normal tails: |mz|/sqrt(Sz) up to about
+    60, variances over four decades (both sides of the 1e-6 floors)."""
+    from triton_tagi_amd.layers.remax import remax
+
+    r = g(B + 3 * K)
+    mz = 6.0 * torch.randn(B, K, generator=r)
+    Sz = 10.0 ** (4.0 * torch.rand(B, K, generator=r) - 3.0)
+    mz[0, :6] = torch.tensor([-30.0, -8.0, -4.0, 0.0, 4.0, 30.0])
+    ma, Sa, J = remax(mz.to(dev), Sz.to(dev))
+    rm, rS, rJ = O.remax_moments(d64(mz), d64(Sz))
+    assert_scaled_close(ma, rm, None, RTOL, ATOL, "remax mean")
+    assert_scaled_close(Sa, rS, None, RTOL, ATOL, "remax var")
+    assert_scaled_close(J, rJ, None, RTOL, ATOL, "remax J")
+
+
 def test_remax_on_reference_golden_inputs(dev):
     """HIP Remax on the inputs of the reference-generated fixture: within 1e-4 of the
     float64 oracle, and within the reference's own fp32 rounding of its stored outputs."""

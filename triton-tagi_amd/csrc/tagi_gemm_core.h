@@ -422,6 +422,51 @@ __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col,
   }
 }
 
+// Four consecutive columns of one output row (the split-K reduction's float4 groups) with
+// vector loads and stores where the layout allows it; false sends the caller to the
+// per-element path.
+__device__ __forceinline__ bool epi_apply4(const Epi& e, int z, int row, int col, const float* m, const float* v) {
+  if (e.kind == 2) {
+    const Phase ph = make_phase(e.g, z);
+    const int hq = ph.Hq * ph.Wq;
+    if (row >= e.g.N * hq) return true;  // rows past this phase's pixels
+    const int n = row / hq, rr = row - n * hq;
+    const int hh = rr / ph.Wq, ww = rr - hh * ph.Wq;
+    const int h = hh * e.g.stride + ph.a, w = ww * e.g.stride + ph.b;
+    const int64_t off = (((int64_t)n * e.g.H + h) * e.g.W + w) * e.g.C + col;
+    uintptr_t al = (uintptr_t)(e.om + off) | (uintptr_t)(e.ov + off);
+    if (e.am) al |= (uintptr_t)(e.am + off) | (uintptr_t)(e.av + off);
+    if (al & 15u) return false;
+    float4 om4 = make_float4(m[0], m[1], m[2], m[3]), ov4 = make_float4(v[0], v[1], v[2], v[3]);
+    if (e.am) {
+      const float4 a = *reinterpret_cast<const float4*>(e.am + off);
+      const float4 b = *reinterpret_cast<const float4*>(e.av + off);
+      om4 = make_float4(om4.x + a.x, om4.y + a.y, om4.z + a.z, om4.w + a.w);
+      ov4 = make_float4(ov4.x + b.x, ov4.y + b.y, ov4.z + b.z, ov4.w + b.w);
+    }
+    *reinterpret_cast<float4*>(e.om + off) = om4;
+    *reinterpret_cast<float4*>(e.ov + off) = ov4;
+    return true;
+  }
+  if (e.kind == 0 && e.scol == 1) {
+    const int64_t off = (z / e.zdiv) * e.sz1 + (z % e.zdiv) * e.sz2 + (int64_t)row * e.srow + col;
+    uintptr_t al = (uintptr_t)(e.ov + off);
+    if (e.om) al |= (uintptr_t)(e.om + off);
+    if (al & 15u) return false;
+    float rm[4], rv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t bi = (int64_t)row * e.b_sr + (int64_t)(col + j) * e.b_sc;
+      rm[j] = m[j] * e.sm + (e.bm ? e.bm[bi] : 0.f);
+      rv[j] = v[j] * e.sv + (e.bv ? e.bv[bi] : 0.f);
+    }
+    if (e.om) *reinterpret_cast<float4*>(e.om + off) = make_float4(rm[0], rm[1], rm[2], rm[3]);
+    *reinterpret_cast<float4*>(e.ov + off) = make_float4(rv[0], rv[1], rv[2], rv[3]);
+    return true;
+  }
+  return false;
+}
+
 // Rows of the output tile in GEMM z (phase-dependent for the conv input delta).
 __device__ __forceinline__ int rows_of(const GemmArgs& g, int z) {
   if (!g.phased) return g.R;
@@ -741,6 +786,13 @@ __global__ void __launch_bounds__(64 * G) splitk_reduce_kernel(const float* __re
       }
   }
   if (idx0 >= total) return;
+  if constexpr (V == 4) {
+    if (C % 4 == 0) {
+      // the 4 elements are consecutive columns of one row
+      const int row = (int)(rc / C);
+      if (epi_apply4(epi, z, row, (int)(rc - (int64_t)row * C), m, v)) return;
+    }
+  }
 #pragma unroll
   for (int e = 0; e < V; ++e) {
     const int64_t r = rc + e;
@@ -831,8 +883,11 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
       if (actual > 1 && kc < 64) break;  // splits below 4 k-tiles only add reduction traffic
       int64_t blocks = tm * tn * batch * actual;
       if (phase_k) {
-        blocks = 0;
-        for (int64_t z = 0; z < batch; ++z) blocks += tm * tn * (phase_k[z] > 0 ? cdiv(phase_k[z], kc) : 1);
+        // a phase with a shorter reduction (or the short last chunk of one) does that
+        // fraction of a kc block's work; tap-less phases only write zeros
+        double eq = 0.0;
+        for (int64_t z = 0; z < batch; ++z) eq += (double)(tm * tn) * (phase_k[z] > 0 ? (double)phase_k[z] / kc : 0.1);
+        blocks = (int64_t)ceil(eq);
       }
       const double block_s = (2.0 * BM * BN * kc * products) / (peak_cu * kEff[ci]);
       // time for one CU to finish r co-resident blocks
