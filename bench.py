@@ -58,8 +58,9 @@ def cpu_baseline(workload: str, sample_batch: int, steps: int = 3):
     from oracle import tagi_oracle as O
     from triton_tagi_amd import workloads
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
+    # the host's share of cores for one GPU (OMP_NUM_THREADS where the job sets it)
+    cores = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
+    torch.set_num_threads(max(cores, 1))
     w = workloads.build(workload, device="cpu", batch=sample_batch)
     onet = O.mirror_net(w.net, dtype=torch.float32)
     x, y = w.x.float(), w.y.float()
