@@ -316,7 +316,8 @@ def main():
         cpu = cpu_baseline(args.workload, args.cpu_batch)
 
     out = {
-        "metric": METRIC,
+        "metric": METRIC if args.workload == "resnet18" else
+        f"TAGI step samples/sec (fwd+bwd+update) {args.workload} b{w.batch} fp32; % MFMA/HBM peak",
         "value": round(value, 2),
         "unit": "samples/s",
         "n_gpus": 1,

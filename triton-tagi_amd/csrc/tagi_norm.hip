@@ -478,25 +478,71 @@ __global__ void embedding_fwd_kernel(const float* __restrict__ tokens, const flo
   }
 }
 
-// grid (slabs of columns, chunks of tokens); block threads own one column each and walk
-// the chunk's tokens in order, accumulating into an LDS table [V][slab].
+// Float4 gather (D % 4 == 0 and D / 4 dividing 256): D/4 threads per token, 256 / (D/4)
+// tokens per block.
+__global__ void __launch_bounds__(256) embedding_fwd_vec_kernel(const float* __restrict__ tokens,
+                                                                const float* __restrict__ mw,
+                                                                const float* __restrict__ Sw, float* __restrict__ mz,
+                                                                float* __restrict__ Sz, int64_t n_tokens, int64_t V,
+                                                                int D, int64_t padding_idx) {
+  const int D4 = D >> 2, tpb = 256 / D4;
+  const int64_t t = (int64_t)blockIdx.x * tpb + threadIdx.x / D4;
+  const int d = (threadIdx.x % D4) * 4;
+  if (t >= n_tokens) return;
+  const int64_t cat = token_id(tokens[t]);
+  const bool ok = cat >= 0 && cat < V && cat != padding_idx;
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4 m = ok ? *reinterpret_cast<const float4*>(mw + cat * D + d) : z;
+  const float4 v = ok ? *reinterpret_cast<const float4*>(Sw + cat * D + d) : z;
+  *reinterpret_cast<float4*>(mz + t * D + d) = m;
+  *reinterpret_cast<float4*>(Sz + t * D + d) = v;
+}
+
+// Backward (embedding.py:111-145): delta_mw[cat, d] = sum over the category's tokens of
+// dmz[t, d] Sw[cat, d], and delta_Sw with dSz and Sw^2. Sw[cat, d] is the same for every
+// token of a category, so the raw sums are formed first and weighted once at the end
+// (equal in exact arithmetic). grid (slabs of columns, chunks of tokens): a thread owns
+// column d of the slab and adds the chunk's deltas into an LDS table [2][V][slab], eight
+// tokens' loads in flight at a time; tokens outside [0, V) and the padding index add
+// nothing.
 __global__ void embedding_bwd_partial_kernel(const float* __restrict__ tokens, const float* __restrict__ dmz,
-                                             const float* __restrict__ dSz, const float* __restrict__ Sw,
-                                             float* __restrict__ ws, int64_t n_tokens, int V, int D,
-                                             int64_t padding_idx, int slab, int chunk) {
+                                             const float* __restrict__ dSz, float* __restrict__ ws, int64_t n_tokens,
+                                             int V, int D, int64_t padding_idx, int slab, int chunk) {
   extern __shared__ float tab[];  // [2][V][slab]
   const int d = blockIdx.x * slab + threadIdx.x;
   const int64_t t0 = (int64_t)blockIdx.y * chunk;
-  const int64_t t1 = min(n_tokens, t0 + chunk);
+  const int n = (int)(min(n_tokens, t0 + chunk) - t0);
   for (int i = threadIdx.x; i < 2 * V * slab; i += blockDim.x) tab[i] = 0.f;
   __syncthreads();
   if (threadIdx.x < slab && d < D) {
-    for (int64_t t = t0; t < t1; ++t) {
+    float* tm = tab + threadIdx.x;
+    float* ts = tab + V * slab + threadIdx.x;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+      float dm[8], ds[8];
+      int c[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t t = t0 + i + u;
+        const int64_t cat = token_id(tokens[t]);
+        c[u] = (cat < 0 || cat >= V || cat == padding_idx) ? -1 : (int)cat;
+        dm[u] = dmz[t * D + d];
+        ds[u] = dSz[t * D + d];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (c[u] >= 0) {
+          tm[c[u] * slab] += dm[u];
+          ts[c[u] * slab] += ds[u];
+        }
+      }
+    }
+    for (; i < n; ++i) {
+      const int64_t t = t0 + i;
       const int64_t cat = token_id(tokens[t]);
       if (cat < 0 || cat >= V || cat == padding_idx) continue;
-      const float sw = Sw[cat * D + d];
-      tab[cat * slab + threadIdx.x] += dmz[t * D + d] * sw;
-      tab[(V + cat) * slab + threadIdx.x] += dSz[t * D + d] * sw * sw;
+      tm[cat * slab] += dmz[t * D + d];
+      ts[cat * slab] += dSz[t * D + d];
     }
   }
   __syncthreads();
@@ -508,17 +554,21 @@ __global__ void embedding_bwd_partial_kernel(const float* __restrict__ tokens, c
   }
 }
 
-__global__ void embedding_bwd_finalize_kernel(const float* __restrict__ ws, float* __restrict__ dmw,
-                                              float* __restrict__ dSw, int V, int D, int nchunks) {
+// Adds the chunk partials in chunk order and applies the Sw, Sw^2 weights.
+__global__ void embedding_bwd_finalize_kernel(const float* __restrict__ ws, const float* __restrict__ Sw,
+                                              float* __restrict__ dmw, float* __restrict__ dSw, int V, int D,
+                                              int nchunks) {
   const int64_t total = (int64_t)V * D;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     float a = 0.f, b = 0.f;
+#pragma unroll 8
     for (int k = 0; k < nchunks; ++k) {
       a += ws[((int64_t)k * 2) * total + i];
       b += ws[((int64_t)k * 2 + 1) * total + i];
     }
-    dmw[i] = a;
-    dSw[i] = b;
+    const float sw = Sw[i];
+    dmw[i] = a * sw;
+    dSw[i] = b * (sw * sw);
   }
 }
 
@@ -535,8 +585,8 @@ static inline void emb_plan(int64_t n_tokens, int64_t V, int64_t D, int* slab, i
   if (s > 256) s = 256;
   if (s > D) s = (int)(((D + 31) / 32) * 32);
   *slab = s;
-  *chunk = 256;
-  *nchunks = (int)cdiv(n_tokens, 256);
+  *chunk = 128;
+  *nchunks = (int)cdiv(n_tokens, 128);
 }
 
 }  // namespace tagi
@@ -784,8 +834,13 @@ extern "C" int tagi_embedding_fwd(const float* tokens, const float* mw, const fl
   if (n_tokens == 0) return TAGI_OK;
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_EMBEDDING, s, 0.0, 4.0 * n_tokens + 16.0 * n_tokens * D);
-  hipLaunchKernelGGL(embedding_fwd_kernel, dim3(ew_blocks(n_tokens * D, 256)), dim3(256), 0, s, tokens, mw, Sw, mz, Sz,
-                     n_tokens, V, (int)D, padding_idx);
+  const bool vec = D % 4 == 0 && D <= 1024 && 256 % (D / 4) == 0 && al16p(mw) && al16p(Sw) && al16p(mz) && al16p(Sz);
+  if (vec)
+    hipLaunchKernelGGL(embedding_fwd_vec_kernel, dim3((unsigned)cdiv(n_tokens, 256 / (D / 4))), dim3(256), 0, s, tokens,
+                       mw, Sw, mz, Sz, n_tokens, V, (int)D, padding_idx);
+  else
+    hipLaunchKernelGGL(embedding_fwd_kernel, dim3(ew_blocks(n_tokens * D, 256)), dim3(256), 0, s, tokens, mw, Sw, mz,
+                       Sz, n_tokens, V, (int)D, padding_idx);
   return check_launch(what);
 }
 
@@ -810,10 +865,10 @@ extern "C" int tagi_embedding_bwd(const float* tokens, const float* dmz, const f
   emb_plan(n_tokens, V, D, &slab, &chunk, &nch);
   const size_t lds = (size_t)2 * V * slab * sizeof(float);
   hipLaunchKernelGGL(embedding_bwd_partial_kernel, dim3((unsigned)cdiv(D, slab), (unsigned)nch), dim3(slab), lds, s,
-                     tokens, dmz, dSz, Sw, ws, n_tokens, (int)V, (int)D, padding_idx, slab, chunk);
+                     tokens, dmz, dSz, ws, n_tokens, (int)V, (int)D, padding_idx, slab, chunk);
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(embedding_bwd_finalize_kernel, dim3(ew_blocks(V * D, 256)), dim3(256), 0, s, (const float*)ws,
+  hipLaunchKernelGGL(embedding_bwd_finalize_kernel, dim3(ew_blocks(V * D, 256)), dim3(256), 0, s, (const float*)ws, Sw,
                      dmw, dSw, (int)V, (int)D, nch);
   return check_launch(what);
 }
