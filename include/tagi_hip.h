@@ -81,6 +81,17 @@ int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const float* mw,
                           float* ws, int64_t ws_bytes, tagi_stream_t stream);
 int64_t tagi_linear_bwd_delta_ws_bytes(int64_t M, int64_t K, int64_t N);
 
+/* tagi_linear_bwd_delta plus an addend in the epilogue: dma = dmz @ mw^T + add_m,
+ * dSa = dSz @ (mw^2)^T + add_S (add_* laid out like dma; they may alias dma/dSa, each
+ * element is read and then written by one thread). The workspace query is
+ * tagi_linear_bwd_delta_ws_bytes. Replaces one projection's triton_fused_backward_delta
+ * plus the sum of the projections' input deltas in MultiheadAttentionV2.backward
+ * (multihead_attention.py:262-267). */
+int tagi_linear_bwd_delta_add(const float* dmz, const float* dSz, const float* mw,
+                              const float* add_m, const float* add_S, float* dma, float* dSa,
+                              int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes,
+                              tagi_stream_t stream);
+
 /* Parameter deltas of a Linear layer (reduction over the M rows):
  *   gmw = ma^T @ dmz, gSw = (ma^2)^T @ dSz, gmb = sum_rows dmz, gSb = sum_rows dSz
  *   dmw = Sw * gmw, dSw = Sw^2 * gSw, dmb = Sb * gmb, dSb = Sb^2 * gSb
@@ -122,6 +133,16 @@ int tagi_bmm_shared(const float* p0, const float* p1, const float* p2, float* me
                     int64_t batch, int64_t M, int64_t K, int64_t L, const tagi_view* va,
                     const tagi_view* vb, const tagi_view* vo, float scale, float scale_sq,
                     int shared_left, tagi_stream_t stream);
+
+/* tagi_bmm_shared followed by an elementwise Jacobian J laid out like the output (view vo):
+ *   mean *= J ;  var *= J^2
+ * Replaces bmm_shared_right (attention.py:286) and the Remax Jacobian applied to the
+ * score deltas in MultiheadAttentionV2.backward (multihead_attention.py:239-243). */
+int tagi_bmm_shared_jacobian(const float* p0, const float* p1, const float* p2, const float* J,
+                             float* mean, float* var, int64_t batch, int64_t M, int64_t K,
+                             int64_t L, const tagi_view* va, const tagi_view* vb,
+                             const tagi_view* vo, float scale, float scale_sq, int shared_left,
+                             tagi_stream_t stream);
 
 /* ------------------------------------------------------------------ Conv2D ---- */
 /* 4-D activations and deltas of the conv path (Conv2D, BatchNorm2D, AvgPool2D) are

@@ -195,3 +195,39 @@ def test_fused_step_matches_oracle(dev):
     chk(bn.running_var, rbn.running_var, None, RTOL, ATOL, "stem BN running var")
     assert not failures, "\n".join(failures)
     assert torch.equal(mu.argmax(-1).cpu(), rmu.argmax(-1))
+
+
+@pytest.mark.parametrize("B,H,M,K,L", [(2, 3, 33, 20, 45), (4, 8, 64, 32, 64)])
+def test_bmm_shared_with_jacobian(dev, B, H, M, K, L):
+    """Score deltas times the Remax Jacobian in the product's epilogue, against the oracle's
+    product followed by the elementwise Jacobian (multihead_attention.py:239-243)."""
+    from triton_tagi_amd.kernels.attention import bmm_shared_right
+
+    r = g(B * H + M)
+    am, av = torch.randn(B, H, M, K, generator=r), torch.rand(B, H, M, K, generator=r)
+    b = torch.randn(B, H, K, L, generator=r)
+    J = torch.rand(B, H, M, L, generator=r)
+    m, v = bmm_shared_right(am.to(dev), av.to(dev), b.to(dev), jacobian=J.to(dev))
+    rm, rv = O.bmm_shared_right(d64(am), d64(av), d64(b), 1.0)
+    J64 = d64(J)
+    assert_scaled_close(m, rm * J64, (d64(am).abs() @ d64(b).abs()) * J64, RTOL, ATOL, "mean * J")
+    assert_scaled_close(v, rv * J64 * J64, None, RTOL, ATOL, "var * J^2")
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 70, 45), (16384, 256, 256), (256, 4096, 1024)])
+def test_linear_bwd_delta_with_addend(dev, M, K, N):
+    """Input deltas added in place to an existing pair in the GEMM epilogue (the sum of the
+    attention projections' input deltas), against the oracle plus the addend."""
+    from triton_tagi_amd.kernels.common import fused_backward_delta
+
+    r = g(M + K + N)
+    dmz, dSz = 0.1 * torch.randn(M, N, generator=r), -1e-2 * torch.rand(M, N, generator=r)
+    mw = torch.randn(K, N, generator=r) / N ** 0.5
+    am, aS = torch.randn(M, K, generator=r), torch.rand(M, K, generator=r)
+    gm, gS = am.to(dev), aS.to(dev)
+    om, oS = fused_backward_delta(dmz.to(dev), dSz.to(dev), mw.to(dev), add=(gm, gS))
+    assert om.data_ptr() == gm.data_ptr() and oS.data_ptr() == gS.data_ptr()
+    rm, rS = O.linear_backward_delta(d64(dmz), d64(dSz), d64(mw))
+    assert_scaled_close(om, rm + d64(am), d64(dmz).abs() @ d64(mw).abs().T + d64(am).abs(), RTOL, ATOL,
+                        "dma + addend")
+    assert_scaled_close(oS, rS + d64(aS), None, RTOL, ATOL, "dSa + addend")

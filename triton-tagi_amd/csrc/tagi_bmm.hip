@@ -71,11 +71,10 @@ extern "C" int tagi_bmm_tagi(const float* mu_a, const float* var_a, const float*
   return bmm_dispatch<PROD_FWD>(g, ka, kb, batch, p, s, what);
 }
 
-extern "C" int tagi_bmm_shared(const float* p0, const float* p1, const float* p2, float* mean, float* var,
-                               int64_t batch, int64_t M, int64_t K, int64_t L, const tagi_view* va, const tagi_view* vb,
-                               const tagi_view* vo, float scale, float scale_sq, int shared_left,
-                               tagi_stream_t stream) {
-  const char* what = "tagi_bmm_shared";
+static int bmm_shared_impl(const char* what, const float* p0, const float* p1, const float* p2, const float* J,
+                           float* mean, float* var, int64_t batch, int64_t M, int64_t K, int64_t L,
+                           const tagi_view* va, const tagi_view* vb, const tagi_view* vo, float scale,
+                           float scale_sq, int shared_left, tagi_stream_t stream) {
   TAGI_REQUIRE(p0 && p1 && p2 && mean && var, "%s: null pointer", what);
   TAGI_REQUIRE(batch > 0 && M > 0 && K > 0 && L > 0 && batch < 65536, "%s: bad sizes", what);
   TAGI_REQUIRE(fits_i32(M * L) && fits_i32(M * K) && fits_i32(K * L), "%s: matrices too large", what);
@@ -89,6 +88,7 @@ extern "C" int tagi_bmm_shared(const float* p0, const float* p1, const float* p2
                4.0 * batch * ((shared_left ? 1 : 2) * M * K + (shared_left ? 2 : 1) * K * L + 2 * M * L));
   GemmArgs g{};
   g.epi = epi_store(mean, var, nullptr, nullptr, 0, 0, scale, scale_sq, vo->zdiv, vo->sz1, vo->sz2, vo->si, vo->sj);
+  g.epi.jm = J;
   g.R = (int)M;
   g.C = (int)L;
   g.Kred = (int)K;
@@ -105,4 +105,22 @@ extern "C" int tagi_bmm_shared(const float* p0, const float* p1, const float* p2
   if (b1 && !al16(b1)) kb = LD_STR_MN_S;
   if (!shared_left) return bmm_dispatch<PROD_SHARED_B>(g, ka, kb, batch, p, s, what);
   return bmm_dispatch<PROD_SHARED_A>(g, ka, kb, batch, p, s, what);
+}
+
+extern "C" int tagi_bmm_shared(const float* p0, const float* p1, const float* p2, float* mean, float* var,
+                               int64_t batch, int64_t M, int64_t K, int64_t L, const tagi_view* va, const tagi_view* vb,
+                               const tagi_view* vo, float scale, float scale_sq, int shared_left,
+                               tagi_stream_t stream) {
+  return bmm_shared_impl("tagi_bmm_shared", p0, p1, p2, nullptr, mean, var, batch, M, K, L, va, vb, vo, scale,
+                         scale_sq, shared_left, stream);
+}
+
+extern "C" int tagi_bmm_shared_jacobian(const float* p0, const float* p1, const float* p2, const float* J,
+                                        float* mean, float* var, int64_t batch, int64_t M, int64_t K, int64_t L,
+                                        const tagi_view* va, const tagi_view* vb, const tagi_view* vo, float scale,
+                                        float scale_sq, int shared_left, tagi_stream_t stream) {
+  const char* what = "tagi_bmm_shared_jacobian";
+  TAGI_REQUIRE(J != nullptr, "%s: null Jacobian", what);
+  return bmm_shared_impl(what, p0, p1, p2, J, mean, var, batch, M, K, L, va, vb, vo, scale, scale_sq, shared_left,
+                         stream);
 }

@@ -134,8 +134,13 @@ struct Epi {
   FastDiv dperm;         // divider for perm_C
   // kind 2
   ConvG g;
-  const float* am;  // optional addend (same layout as the output): out = delta + addend
+  // kinds 0 and 2: optional addend laid out like the output (out = result + addend; may
+  // alias the output, each element is read and written by one thread)
+  const float* am;
   const float* av;
+  // kind 0: optional multiplier laid out like the output (mean * j, variance * j^2: the
+  // Jacobian of an elementwise layer applied to the product's deltas)
+  const float* jm;
 };
 
 struct GemmArgs {
@@ -386,6 +391,15 @@ __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col,
     const int64_t bi = (int64_t)row * e.b_sr + (int64_t)col * e.b_sc;
     if (e.bm) rm += e.bm[bi];
     if (e.bv) rv += e.bv[bi];
+    if (e.jm) {
+      const float j = e.jm[off];
+      rm *= j;
+      rv *= j * j;
+    }
+    if (e.am) {
+      rm += e.am[off];
+      rv += e.av[off];
+    }
     if (e.om) e.om[off] = rm;
     e.ov[off] = rv;
   } else if (e.kind == 1) {
@@ -448,7 +462,7 @@ __device__ __forceinline__ bool epi_apply4(const Epi& e, int z, int row, int col
     *reinterpret_cast<float4*>(e.ov + off) = ov4;
     return true;
   }
-  if (e.kind == 0 && e.scol == 1) {
+  if (e.kind == 0 && e.scol == 1 && !e.jm && !e.am) {
     const int64_t off = (z / e.zdiv) * e.sz1 + (z % e.zdiv) * e.sz2 + (int64_t)row * e.srow + col;
     uintptr_t al = (uintptr_t)(e.ov + off);
     if (e.om) al |= (uintptr_t)(e.om + off);
@@ -675,8 +689,18 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
           const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
           if (row < R && cok) {
             const int64_t off = coff + (int64_t)row * e.srow;
-            if (e.om) e.om[off] = accM[i][j][v] * e.sm + bmj;
-            e.ov[off] = accV[i][j][v] * e.sv + bvj;
+            float m = accM[i][j][v] * e.sm + bmj, vv = accV[i][j][v] * e.sv + bvj;
+            if (e.jm) {
+              const float jj = e.jm[off];
+              m *= jj;
+              vv *= jj * jj;
+            }
+            if (e.am) {
+              m += e.am[off];
+              vv += e.av[off];
+            }
+            if (e.om) e.om[off] = m;
+            e.ov[off] = vv;
           }
         }
     }

@@ -43,11 +43,12 @@ extern "C" int64_t tagi_linear_bwd_delta_ws_bytes(int64_t M, int64_t K, int64_t 
   return plan_ws_bytes(linear_bwd_plan(M, K, N), M, K, 1);
 }
 
-extern "C" int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const float* mw, float* dma, float* dSa,
-                                     int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes,
-                                     tagi_stream_t stream) {
-  const char* what = "tagi_linear_bwd_delta";
+static int linear_bwd_delta_impl(const char* what, const float* dmz, const float* dSz, const float* mw,
+                                 const float* add_m, const float* add_S, float* dma, float* dSa, int64_t M, int64_t K,
+                                 int64_t N, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
   TAGI_REQUIRE(dmz && dSz && mw && dma && dSa, "%s: null pointer", what);
+  TAGI_REQUIRE((add_m == nullptr) == (add_S == nullptr), "%s: add_m and add_S must both be given or both be NULL",
+               what);
   TAGI_REQUIRE(M > 0 && K > 0 && N > 0, "%s: sizes must be positive", what);
   TAGI_REQUIRE(fits_i32(M * K) && fits_i32(K * N) && fits_i32(M * N), "%s: too large for 32-bit tiles", what);
   hipStream_t s = as_stream(stream);
@@ -56,6 +57,8 @@ extern "C" int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const f
   g.a = strided_operand(dmz, dSz, 1, 0, 0, N, 1, M, N);
   g.b = strided_operand(mw, nullptr, 1, 0, 0, N, 1, K, N);
   g.epi = epi_store(dma, dSa, nullptr, nullptr, 0, 0, 1.f, 1.f, 1, 0, 0, K, 1);
+  g.epi.am = add_m;
+  g.epi.av = add_S;
   g.R = (int)M;
   g.C = (int)K;
   g.Kred = (int)N;
@@ -64,6 +67,20 @@ extern "C" int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const f
   const bool v4 = N % 4 == 0 && al16(dmz) && al16(dSz) && al16(mw);
   if (v4) return run_gemm<PROD_SHARED_B, LD_STR_K4, LD_STR_K4>(g, 1, p, ws, ws_bytes, s, what);
   return run_gemm<PROD_SHARED_B, LD_STR_K_S, LD_STR_K_S>(g, 1, p, ws, ws_bytes, s, what);
+}
+
+extern "C" int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const float* mw, float* dma, float* dSa,
+                                     int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes,
+                                     tagi_stream_t stream) {
+  return linear_bwd_delta_impl("tagi_linear_bwd_delta", dmz, dSz, mw, nullptr, nullptr, dma, dSa, M, K, N, ws,
+                               ws_bytes, stream);
+}
+
+extern "C" int tagi_linear_bwd_delta_add(const float* dmz, const float* dSz, const float* mw, const float* add_m,
+                                         const float* add_S, float* dma, float* dSa, int64_t M, int64_t K, int64_t N,
+                                         float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+  return linear_bwd_delta_impl("tagi_linear_bwd_delta_add", dmz, dSz, mw, add_m, add_S, dma, dSa, M, K, N, ws,
+                               ws_bytes, stream);
 }
 
 extern "C" int64_t tagi_linear_wgrad_ws_bytes(int64_t M, int64_t K, int64_t N) {

@@ -59,10 +59,12 @@ _SIGS = {
     "tagi_linear_fwd_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_linear_bwd_delta": (c_int, [P, P, P, P, P, I64, I64, I64, P, I64, P]),
     "tagi_linear_bwd_delta_ws_bytes": (I64, [I64, I64, I64]),
+    "tagi_linear_bwd_delta_add": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
     "tagi_linear_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
     "tagi_linear_wgrad_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_bmm_tagi": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, P]),
     "tagi_bmm_shared": (c_int, [P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),
+    "tagi_bmm_shared_jacobian": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),
     "tagi_conv2d_fwd": (c_int, [P, P, P, P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_fwd_ws_bytes": (I64, [GP]),
     "tagi_conv2d_bwd_delta": (c_int, [P, P, P, P, P, GP, P, I64, P]),

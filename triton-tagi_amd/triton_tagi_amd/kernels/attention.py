@@ -79,8 +79,13 @@ def bmm_tagi_var(mu_a, var_a, mu_b, var_b, scale_sq: float = 1.0):
     return var
 
 
-def bmm_shared_right(a_mean, a_var, b, scale: float = 1.0):
-    """(s a_mean @ b, s^2 a_var @ b^2) (attention.py:286-336)."""
+def bmm_shared_right(a_mean, a_var, b, scale: float = 1.0, jacobian=None):
+    """(s a_mean @ b, s^2 a_var @ b^2) (attention.py:286-336).
+
+    With ``jacobian`` (a contiguous tensor shaped like the output) the results are
+    multiplied by it and its square in the product's epilogue (the Remax Jacobian applied
+    to the score deltas, multihead_attention.py:239-243).
+    """
     va, n, batch = _view_of(a_mean, "a_mean")
     vb, nb, _ = _view_of(b, "b")
     if a_var.stride() != a_mean.stride() or a_var.shape != a_mean.shape:
@@ -92,6 +97,13 @@ def bmm_shared_right(a_mean, a_var, b, scale: float = 1.0):
     mean, var = _out(batch, M, L, a_mean), _out(batch, M, L, a_mean)
     vo = _lib.view(1, M * L, 0, L, 1)
     s = float(scale)
+    if jacobian is not None:
+        J = _lib.check(jacobian, "jacobian")
+        if tuple(J.shape) != tuple(mean.shape) or not J.is_contiguous():
+            raise ValueError(f"jacobian must be a contiguous {tuple(mean.shape)} tensor, got {tuple(J.shape)}")
+        _lib.call("tagi_bmm_shared_jacobian", a_mean.data_ptr(), a_var.data_ptr(), b.data_ptr(), J.data_ptr(),
+                  mean.data_ptr(), var.data_ptr(), n, M, K, L, va, vb, vo, s, s * s, 0, _lib.stream_of(a_mean))
+        return mean, var
     _lib.call("tagi_bmm_shared", a_mean.data_ptr(), a_var.data_ptr(), b.data_ptr(), mean.data_ptr(),
               var.data_ptr(), n, M, K, L, va, vb, vo, s, s * s, 0, _lib.stream_of(a_mean))
     return mean, var

@@ -48,17 +48,28 @@ def fused_var_forward(ma, Sa, mw, Sw, Sb):
     return linear_forward(ma, Sa, mw, Sw, None, Sb, need_mean=False)[1]
 
 
-def fused_backward_delta(dmz, dSz, mw):
-    """(dmz @ mw^T, dSz @ (mw^2)^T) (common.py:287-327)."""
+def fused_backward_delta(dmz, dSz, mw, add=None):
+    """(dmz @ mw^T, dSz @ (mw^2)^T) (common.py:287-327).
+
+    With ``add = (am, aS)`` (contiguous (M, K) tensors) the products are added to them in
+    place, in the GEMM epilogue, and ``add`` is returned.
+    """
     _2d(dmz, "dmz"), _2d(dSz, "dSz"), _2d(mw, "mw")
     M, N = dmz.shape
     K = mw.shape[0]
     if mw.shape[1] != N or dSz.shape != dmz.shape:
         raise ValueError(f"fused_backward_delta: dmz {tuple(dmz.shape)} vs mw {tuple(mw.shape)}")
-    dma = torch.empty(M, K, device=dmz.device, dtype=torch.float32)
-    dSa = torch.empty(M, K, device=dmz.device, dtype=torch.float32)
     ws = _lib.workspace(_lib.query("tagi_linear_bwd_delta_ws_bytes", M, K, N), dmz.device)
     wp, wb = _lib.ws_args(ws)
+    if add is not None:
+        dma, dSa = (_lib.check(t, n) for t, n in zip(add, ("add_m", "add_S")))
+        if tuple(dma.shape) != (M, K) or tuple(dSa.shape) != (M, K) or not (dma.is_contiguous() and dSa.is_contiguous()):
+            raise ValueError(f"fused_backward_delta: addend {tuple(dma.shape)} is not a contiguous ({M}, {K}) tensor")
+        _lib.call("tagi_linear_bwd_delta_add", dmz.data_ptr(), dSz.data_ptr(), mw.data_ptr(), dma.data_ptr(),
+                  dSa.data_ptr(), dma.data_ptr(), dSa.data_ptr(), M, K, N, wp, wb, _lib.stream_of(dmz))
+        return dma, dSa
+    dma = torch.empty(M, K, device=dmz.device, dtype=torch.float32)
+    dSa = torch.empty(M, K, device=dmz.device, dtype=torch.float32)
     _lib.call("tagi_linear_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), mw.data_ptr(), dma.data_ptr(),
               dSa.data_ptr(), M, K, N, wp, wb, _lib.stream_of(dmz))
     return dma, dSa

@@ -52,7 +52,10 @@ class Linear(LearnableLayer):
         """The parameter deltas of ``backward`` without forming the input deltas."""
         self._backward(delta_mz, delta_Sz, False)
 
-    def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool):
+    def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool, add=None):
+        """Parameter deltas, and the input deltas when ``input_deltas``; with ``add`` (a pair
+        of contiguous tensors shaped like the input deltas) those are added to it in place
+        and ``add`` is returned."""
         dmz = delta_mz.reshape(-1, self.out_features).contiguous()
         dSz = delta_Sz.reshape(-1, self.out_features).contiguous()
         dmw, dSw, dmb, dSb = linear_param_deltas(self.ma_in, dmz, dSz, self.Sw, self.Sb if self.has_bias else None)
@@ -61,6 +64,10 @@ class Linear(LearnableLayer):
             self.delta_mb, self.delta_Sb = dmb, dSb
         if not input_deltas:
             return None
+        if add is not None:
+            fused_backward_delta(dmz, dSz, self.mw, add=(add[0].view(-1, self.in_features),
+                                                         add[1].view(-1, self.in_features)))
+            return add
         dma, dSa = fused_backward_delta(dmz, dSz, self.mw)
         in_shape = (*self._input_shape[:-1], self.in_features)
         return dma.reshape(in_shape), dSa.reshape(in_shape)

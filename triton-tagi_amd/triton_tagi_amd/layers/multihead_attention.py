@@ -22,7 +22,6 @@ from torch import Tensor
 from .. import _lib
 from ..base import LearnableLayer
 from .linear import Linear
-from .relu import jacobian_backward
 from .remax import remax
 
 
@@ -115,12 +114,16 @@ class MultiheadAttentionV2(LearnableLayer):
         dv, dSv = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
         _lib.call("tagi_bmm_shared", d_mu.data_ptr(), d_var.data_ptr(), c["mu_score"].data_ptr(), dv.data_ptr(),
                   dSv.data_ptr(), B * H, S, S, D, svt, hv, hv, 1.0, 1.0, 1, st)
-        # dscore = d_out @ mu_v^T (mu_v shared on the right)
-        dsc = torch.empty(B, H, S, S, device=dev)
-        dSsc = torch.empty_like(dsc)
-        _lib.call("tagi_bmm_shared", d_mu.data_ptr(), d_var.data_ptr(), c["mu_v"].data_ptr(), dsc.data_ptr(),
-                  dSsc.data_ptr(), B * H, S, D, S, hv, hvt, sv, 1.0, 1.0, 0, st)
-        scaled_mu, scaled_var = jacobian_backward(dsc, dSsc, c["jcb"])
+        # dscore = d_out @ mu_v^T (mu_v shared on the right), times the Remax Jacobian in the
+        # product's epilogue (multihead_attention.py:239-243)
+        jcb = _lib.check(c["jcb"], "jcb")
+        if tuple(jcb.shape) != (B, H, S, S):
+            raise ValueError(f"MultiheadAttentionV2: stored Remax Jacobian {tuple(jcb.shape)} vs {(B, H, S, S)}")
+        scaled_mu = torch.empty(B, H, S, S, device=dev)
+        scaled_var = torch.empty_like(scaled_mu)
+        _lib.call("tagi_bmm_shared_jacobian", d_mu.data_ptr(), d_var.data_ptr(), c["mu_v"].data_ptr(),
+                  jcb.data_ptr(), scaled_mu.data_ptr(), scaled_var.data_ptr(), B * H, S, D, S, hv, hvt, sv, 1.0, 1.0,
+                  0, st)
         # dQ = s scaled @ mu_k ; dK = s scaled^T @ mu_q
         dq, dSq = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
         _lib.call("tagi_bmm_shared", scaled_mu.data_ptr(), scaled_var.data_ptr(), c["mu_k"].data_ptr(),
@@ -128,12 +131,10 @@ class MultiheadAttentionV2(LearnableLayer):
         dk, dSk = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
         _lib.call("tagi_bmm_shared", scaled_mu.data_ptr(), scaled_var.data_ptr(), c["mu_q"].data_ptr(),
                   dk.data_ptr(), dSk.data_ptr(), B * H, S, S, D, svt, hv, hv, s, s * s, 0, st)
+        # the projections' input deltas summed in the GEMM epilogues: (q + k) + v
         d_ma_q, d_Sa_q = self.q_proj.backward(dq, dSq)
-        d_ma_k, d_Sa_k = self.k_proj.backward(dk, dSk)
-        d_ma_v, d_Sa_v = self.v_proj.backward(dv, dSv)
-        n = d_ma_q.numel()
-        _lib.call("tagi_add_inplace", d_ma_k.data_ptr(), d_Sa_k.data_ptr(), d_ma_q.data_ptr(), d_Sa_q.data_ptr(), n, st)
-        _lib.call("tagi_add_inplace", d_ma_v.data_ptr(), d_Sa_v.data_ptr(), d_ma_q.data_ptr(), d_Sa_q.data_ptr(), n, st)
+        self.k_proj._backward(dk, dSk, True, add=(d_ma_q, d_Sa_q))
+        self.v_proj._backward(dv, dSv, True, add=(d_ma_q, d_Sa_q))
         return d_ma_q, d_Sa_q
 
     def _update_items(self):
