@@ -1,6 +1,6 @@
 """CPU oracle of the TAGI step: a restatement of triton-tagi's moment equations.
 
-TEST INFRASTRUCTURE ONLY. This module is the checker for the HIP engine; only tests/,
+TEST INFRASTRUCTURE ONLY. The HIP engine is tested against this oracle; only tests/,
 ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import it. The
 engine (package ``triton_tagi_amd``) never imports it and has no CPU path.
 
