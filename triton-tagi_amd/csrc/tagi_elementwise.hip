@@ -284,7 +284,7 @@ __global__ void __launch_bounds__(256) remax_kernel(const float* __restrict__ mz
   const float inv_mt = fast_rcp(mu_mt);
   // log1p/expm1 below are the reference's log(1 + x) / exp(x) - 1 without fp32 cancellation
   const float var_log_mt = log1p_pos(var_mt * inv_mt * inv_mt);
-  const float mu_log_mt = logf(mu_mt) - 0.5f * var_log_mt;
+  const float mu_log_mt = fast_log(mu_mt) - 0.5f * var_log_mt;
   float var_log_m[EPT], cov_m_mt[EPT], mu_a_raw[EPT], var_log_a[EPT];
   float s_a = 0.f;
 #pragma unroll
@@ -292,7 +292,7 @@ __global__ void __launch_bounds__(256) remax_kernel(const float* __restrict__ mz
     const int c = lane + 64 * e;
     const float rm = fast_rcp(mu_m[e]);
     const float vlm = log1p_pos(var_m[e] * rm * rm);
-    const float mlm = logf(mu_m[e]) - 0.5f * vlm;
+    const float mlm = fast_log(mu_m[e]) - 0.5f * vlm;
     const float cov = log1p_pos(var_m[e] * rm * inv_mt);
     const float mla = mlm - mu_log_mt;
     const float vla = fmaxf(vlm + var_log_mt - 2.0f * cov, 0.0f);
@@ -309,9 +309,10 @@ __global__ void __launch_bounds__(256) remax_kernel(const float* __restrict__ mz
     const int c = lane + 64 * e;
     if (c >= K) continue;
     const float mua = mu_a_raw[e] * inv_sum_a;
-    const float vara = expm1f(var_log_a[e]) * mua * mua;
-    const float cov_la_lm = var_log_m[e] - cov_m_mt[e];
-    const float cov_am = expm1f(cov_la_lm) * mua * mu_m[e];
+    const float vara = expm1_pos(var_log_a[e]) * mua * mua;
+    // log-space covariance of a and m: vlm - cov >= 0 up to rounding, since mu_m <= mu_mt
+    const float cov_la_lm = fmaxf(var_log_m[e] - cov_m_mt[e], 0.0f);
+    const float cov_am = expm1_pos(cov_la_lm) * mua * mu_m[e];
     const float cs = __builtin_amdgcn_sqrtf(vara * var_z[e]);
     const float cov_az = fminf(cs, cov_am * fast_rcp(fmaxf(jcb[e], EPS)));
     ma[row * K + c] = mua;

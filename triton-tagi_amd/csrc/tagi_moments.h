@@ -28,13 +28,31 @@ __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(p) * fmaf(e, 0.6931471805599453f, 1.0f);
 }
 
+// Natural logarithm of a normal positive x: log2 from v_log_f32 (accurate to about 1 ulp
+// relative, also next to x = 1) times ln 2.
+__device__ __forceinline__ float fast_log(float x) { return __builtin_amdgcn_logf(x) * 0.6931471805599453f; }
+
 // log(1 + x) for x >= 0 (finite) from one logarithm: with u = fl(1 + x), the factor
 // x / (u - 1) corrects the rounding of u (Goldberg, "What every computer scientist should
 // know about floating-point arithmetic", 1991, theorem 4), a few ulp for every x >= 0.
 __device__ __forceinline__ float log1p_pos(float x) {
   const float u = 1.0f + x;
   const float d = u - 1.0f;
-  return d == 0.0f ? x : logf(u) * fast_div(x, d);
+  return d == 0.0f ? x : fast_log(u) * fast_div(x, d);
+}
+
+// exp(x) - 1 for x >= 0: the Taylor polynomial through x^7 below 0.35 (truncation below
+// 3e-9 relative there), exp(x) - 1 above (no cancellation: e^x - 1 > 0.41).
+__device__ __forceinline__ float expm1_pos(float x) {
+  if (x >= 0.35f) return fast_exp(x) - 1.0f;
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, x, 1.0f / 720.0f);
+  p = fmaf(p, x, 1.0f / 120.0f);
+  p = fmaf(p, x, 1.0f / 24.0f);
+  p = fmaf(p, x, 1.0f / 6.0f);
+  p = fmaf(p, x, 0.5f);
+  p = fmaf(p, x, 1.0f);
+  return p * x;
 }
 
 // Upper tail of the standard normal, Q(a) = 0.5 erfc(a / sqrt 2), for a >= 0, by the
