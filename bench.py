@@ -193,6 +193,9 @@ def main():
     ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--cpu-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="time replays of a HIP graph of the step (Sequential.capture_step) instead of eager "
+                         "steps; the roofline then comes from the warm-up steps' live timer")
     ap.add_argument("--ceilings", action="store_true",
                     help="print measured MFMA / copy / vendor-GEMM ceilings as one JSON line and exit")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -263,16 +266,30 @@ def main():
     # event record holds the queue for a few microseconds, so it runs on the last few
     # timed steps only (same shapes every step) instead of inflating all of them.
     timer_steps = min(args.steps, TIMER_STEPS)
-    log(f"[bench] timing {args.steps} steps (timer on {dom or 'no family'} for the last {timer_steps})")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        if dom and i == args.steps - timer_steps:
-            _lib.prof_begin([dom])
-        net.step(x, y, sv)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    timed = _lib.prof_end() if dom else {}
+    if args.graph:
+        log("[bench] recording the step into a HIP graph (one more eager step)")
+        graph = net.capture_step(x, y, sv)
+        torch.cuda.synchronize()
+        log(f"[bench] timing {args.steps} graph replays")
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        # kernels inside a graph carry no per-launch events: use the warm-up steps' timer
+        timed = {dom: fams[dom]} if dom else {}
+        timer_steps = max(prof_steps, 1)
+    else:
+        log(f"[bench] timing {args.steps} steps (timer on {dom or 'no family'} for the last {timer_steps})")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            if dom and i == args.steps - timer_steps:
+                _lib.prof_begin([dom])
+            net.step(x, y, sv)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        timed = _lib.prof_end() if dom else {}
     elapsed = t1 - t0
     ms_per_step = 1e3 * elapsed / args.steps
     value = w.batch * args.steps / elapsed
@@ -329,7 +346,8 @@ def main():
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic (seeded N(0,1) inputs, one-hot targets, random-init priors of the architecture)",
-        "config": {"workload": WORKLOAD_DESC[args.workload], "global_batch": w.batch, "parallelism": "single GPU"},
+        "config": {"workload": WORKLOAD_DESC[args.workload], "global_batch": w.batch, "parallelism": "single GPU",
+                   "launch": "hip graph replay" if args.graph else "eager"},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernel_ms_per_step_warmup": round(gpu_ms / nps, 4),

@@ -105,6 +105,25 @@ class Sequential:
         self.update(get_cap_factor(batch_size))
         return y_pred_mu, y_pred_var
 
+    def capture_step(self, x_batch: Tensor, y_batch: Tensor, sigma_v: float) -> "StepGraph":
+        """Record one ``step`` into a HIP graph for replay without host launch overhead.
+
+        Runs one eager ``step`` first (so that first-call behaviour, such as BatchNorm2D's
+        gamma re-initialisation, is not recorded), then records the next step. Each
+        ``replay()`` of the returned graph is one more training step on the tensors that
+        were passed here: copy new data into ``x_batch`` / ``y_batch`` in place before a
+        replay. Replays give the same results as eager steps (the kernels and their order
+        are the same, and every reduction is deterministic).
+        """
+        if not x_batch.is_cuda:
+            raise ValueError("capture_step: the batch must be on a GPU")
+        self.step(x_batch, y_batch, sigma_v)
+        torch.cuda.synchronize(x_batch.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            mu, var = self.step(x_batch, y_batch, sigma_v)
+        return StepGraph(graph, mu, var)
+
     def train(self) -> None:
         for layer in self.layers:
             if hasattr(layer, "training"):
@@ -133,3 +152,17 @@ class Sequential:
         if not out:
             raise RuntimeError("No attention layers in this Sequential.")
         return out
+
+
+class StepGraph:
+    """A recorded training step (``Sequential.capture_step``): ``replay()`` runs it and
+    returns the predicted moments (tensors reused by every replay)."""
+
+    def __init__(self, graph, mu: Tensor, var: Tensor) -> None:
+        self.graph = graph
+        self.mu = mu
+        self.var = var
+
+    def replay(self) -> tuple[Tensor, Tensor]:
+        self.graph.replay()
+        return self.mu, self.var
