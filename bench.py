@@ -299,20 +299,30 @@ def main():
         d = timed[dom]
         per_launch_s = d["ms"] / 1e3 / d["launches"]
         flops_per_launch = d["flops"] / d["launches"]
-        achieved = flops_per_launch / per_launch_s / 1e12
+        bytes_per_launch = d["bytes"] / d["launches"]
+        # the bound is set by the kernel's algorithmic intensity against the ridge point
+        # (157.3 TFLOP/s / 8 TB/s = 19.7 flop/B): products with a short reduction (the
+        # attention score products, K = head_dim) are bound by moving their outputs
+        hbm_bound = bytes_per_launch > 0 and flops_per_launch / bytes_per_launch < (
+            PEAK_FP32_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9))
+        if hbm_bound:
+            achieved, peak, unit = bytes_per_launch / per_launch_s / 1e9, PEAK_HBM_GBS, "GB/s"
+        else:
+            achieved, peak, unit = flops_per_launch / per_launch_s / 1e12, PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
         roofline = {
-            "bound": "mfma",
+            "bound": "hbm" if hbm_bound else "mfma",
             "kernel": dom,
             "achieved": round(achieved, 2),
-            "peak": PEAK_FP32_MFMA_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+            "peak": peak,
+            "unit": unit,
+            "frac": round(achieved / peak, 4),
             "traffic": load_traffic(args.workload, dom),
             "launches_per_step": d["launches"] / timer_steps,
             "timer_steps": timer_steps,
             "avg_launch_us": round(per_launch_s * 1e6, 2),
             "flops_per_launch": round(flops_per_launch),
-            "alg_bytes_per_launch": round(d["bytes"] / d["launches"]),
+            "alg_bytes_per_launch": round(bytes_per_launch),
+            "alg_flop_per_byte": round(flops_per_launch / bytes_per_launch, 1) if bytes_per_launch else None,
         }
     breakdown = {}
     nps = max(prof_steps, 1)
