@@ -169,7 +169,7 @@ struct Cfg {
 // the chunk -> (mn, k) map is fixed per thread, so per-row / per-k invariants are
 // computed once in init().
 // ------------------------------------------------------------------------------------
-template <int KIND, int NT, int BMN, int BK, int NTH>
+template <int KIND, int NT, int BMN, int BK, int NTH, int PF = 1>
 struct Loader {
   static constexpr bool V4 = KindTraits<KIND>::vec4;
   static constexpr bool MNF = KindTraits<KIND>::mn_fast;
@@ -186,7 +186,7 @@ struct Loader {
   static constexpr int NRB = CONV_ROWS ? NC : 1;  // per-chunk row bases only where rows differ
   static constexpr int NR = CONV_R ? NC : 1;
 
-  Vt v[NT][NC];
+  Vt v[PF][NT][NC];  // PF register stages of fetched chunks
   FastDiv dnkw;              // divider for the phase's taps per row (conv input delta)
   int mnmax, kmax;           // extents checked by fetch (per phase for the conv input delta)
   int cmn[NC], ck[NC];       // chunk origin within the tile
@@ -291,6 +291,7 @@ struct Loader {
 
   // Gather of one k tile: each chunk's reduction index is decoded with exact
   // multiply-high divisions; chunks outside the operand or in the zero padding read as 0.
+  template <int ST = 0>
   __device__ __forceinline__ void fetch(const Operand& o, int z, int mn0, int k0) {
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
@@ -349,22 +350,23 @@ struct Loader {
       a = make_float4(ok ? a.x : (one ? 1.f : 0.f), ok ? a.y : 0.f, ok ? a.z : 0.f, ok ? a.w : 0.f);
       b = make_float4(ok ? b.x : 0.f, ok ? b.y : 0.f, ok ? b.z : 0.f, ok ? b.w : 0.f);
       if constexpr (V4) {
-        v[0][i] = a;
-        if constexpr (NT == 2) v[1][i] = b;
+        v[ST][0][i] = a;
+        if constexpr (NT == 2) v[ST][1][i] = b;
       } else {
-        v[0][i] = a.x;
-        if constexpr (NT == 2) v[1][i] = b.x;
+        v[ST][0][i] = a.x;
+        if constexpr (NT == 2) v[ST][1][i] = b.x;
       }
     }
   }
 
+  template <int ST = 0>
   __device__ __forceinline__ void store(float* s) const {
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         float* st = s + t * BK * LD;
-        const Vt x = v[t][i];
+        const Vt x = v[ST][t][i];
         if constexpr (!V4) {
           st[ck[i] * LD + cmn[i]] = x;
         } else if constexpr (MNF) {
@@ -536,8 +538,11 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   const int kbeg = split * g.k_chunk;
   const int kend = min(Kred, kbeg + g.k_chunk);
 
-  Loader<KA, NA, BM, BK, NTH> la;
-  Loader<KB, NB, BN, BK, NTH> lb;
+  // register stages of operand prefetch: the parameter-delta products stream both
+  // operands from HBM over long reductions, so their k-tiles are fetched two tiles ahead
+  constexpr int PF = PROD == PROD_SHARED_A ? 2 : 1;
+  Loader<KA, NA, BM, BK, NTH, PF> la;
+  Loader<KB, NB, BN, BK, NTH, PF> lb;
   la.init(g.a, z, m0, tid);
   lb.init(g.b, z, n0, tid);
 
@@ -561,15 +566,17 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
     la.store(smem);
     lb.store(smem + SA);
   }
+  if constexpr (PF == 2) {
+    if (nk > 1) {
+      la.template fetch<1>(g.a, z, m0, kbeg + BK);
+      lb.template fetch<1>(g.b, z, n0, kbeg + BK);
+    }
+  }
   __syncthreads();
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const float* sA = smem + (kt & 1) * (SA + SB);
+  // one k-tile of MFMAs on LDS buffer sA
+  auto compute_tile = [&](const float* sA) {
     const float* sB = sA + SA;
-    if (kt + 1 < nk) {
-      la.fetch(g.a, z, m0, kbeg + (kt + 1) * BK);
-      lb.fetch(g.b, z, n0, kbeg + (kt + 1) * BK);
-    }
     {
       // Fragments of k-step s+2 are read from LDS while the MFMAs of k-step s run; the
       // scheduling barriers keep the compiler from sinking the reads next to their use.
@@ -644,12 +651,47 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (kt + 1 < nk) {
-      float* nA = smem + ((kt + 1) & 1) * (SA + SB);
-      la.store(nA);
-      lb.store(nA + SA);
+  };
+  if constexpr (PF == 1) {
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 < nk) {
+        la.fetch(g.a, z, m0, kbeg + (kt + 1) * BK);
+        lb.fetch(g.b, z, n0, kbeg + (kt + 1) * BK);
+      }
+      compute_tile(smem + (kt & 1) * (SA + SB));
+      if (kt + 1 < nk) {
+        float* nA = smem + ((kt + 1) & 1) * (SA + SB);
+        la.store(nA);
+        lb.store(nA + SA);
+      }
+      __syncthreads();
     }
-    __syncthreads();
+  } else {
+    // tile kt is in LDS buffer kt & 1 and tile kt + 1 in register stage (kt + 1) & 1; the
+    // stage that held tile kt is free for tile kt + 2
+    for (int kt = 0; kt < nk; kt += 2) {
+      if (kt + 2 < nk) {
+        la.template fetch<0>(g.a, z, m0, kbeg + (kt + 2) * BK);
+        lb.template fetch<0>(g.b, z, n0, kbeg + (kt + 2) * BK);
+      }
+      compute_tile(smem);
+      if (kt + 1 < nk) {
+        la.template store<1>(smem + SA + SB);
+        lb.template store<1>(smem + SA + SB + SA);
+      }
+      __syncthreads();
+      if (kt + 1 >= nk) break;
+      if (kt + 3 < nk) {
+        la.template fetch<1>(g.a, z, m0, kbeg + (kt + 3) * BK);
+        lb.template fetch<1>(g.b, z, n0, kbeg + (kt + 3) * BK);
+      }
+      compute_tile(smem + SA + SB);
+      if (kt + 2 < nk) {
+        la.template store<0>(smem);
+        lb.template store<0>(smem + SA);
+      }
+      __syncthreads();
+    }
   }
 
   // Epilogue: split-K partial sums, or the layer's epilogue. The epilogue kind is the same
