@@ -538,11 +538,10 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   const int kbeg = split * g.k_chunk;
   const int kend = min(Kred, kbeg + g.k_chunk);
 
-  // register stages of operand prefetch: the two-product kinds (input and parameter
-  // deltas) have a third less MFMA work per k-tile to hide a fetch behind, so their
-  // k-tiles are fetched two tiles ahead (the forward's are one tile ahead: a second stage
-  // would cost the 8-wave tiles their second resident block)
-  constexpr int PF = PROD != PROD_FWD ? 2 : 1;
+  // register stages of operand prefetch: k-tiles are fetched two tiles ahead, except in
+  // the forward product's 8-wave tiles, where a second stage would cost the tile its
+  // second resident block per CU
+  constexpr int PF = (PROD != PROD_FWD || NTH <= 256) ? 2 : 1;
   Loader<KA, NA, BM, BK, NTH, PF> la;
   Loader<KB, NB, BN, BK, NTH, PF> lb;
   la.init(g.a, z, m0, tid);
