@@ -164,6 +164,15 @@ struct Cfg {
   static constexpr int MINB = NTH >= 512 ? 1 : 2;
 };
 
+// Compile-time loop: f(std::integral_constant<int, I>) for I = B .. E-1, in order.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 // ------------------------------------------------------------------------------------
 // Operand loaders. Each thread owns NC chunks (float4 or scalar) of the BMN x BK tile;
 // the chunk -> (mn, k) map is fixed per thread, so per-row / per-k invariants are
@@ -567,12 +576,14 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
     la.store(smem);
     lb.store(smem + SA);
   }
-  if constexpr (PF == 2) {
-    if (nk > 1) {
-      la.template fetch<1>(g.a, z, m0, kbeg + BK);
-      lb.template fetch<1>(g.b, z, n0, kbeg + BK);
+  // tiles 1 .. PF-1 go to register stages 1 .. PF-1
+  static_for<1, PF>([&](auto U) {
+    constexpr int u = decltype(U)::value;
+    if (u < nk) {
+      la.template fetch<u>(g.a, z, m0, kbeg + u * BK);
+      lb.template fetch<u>(g.b, z, n0, kbeg + u * BK);
     }
-  }
+  });
   __syncthreads();
 
   // one k-tile of MFMAs on LDS buffer sA
@@ -653,46 +664,29 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
       }
     }
   };
-  if constexpr (PF == 1) {
-    for (int kt = 0; kt < nk; ++kt) {
-      if (kt + 1 < nk) {
-        la.fetch(g.a, z, m0, kbeg + (kt + 1) * BK);
-        lb.fetch(g.b, z, n0, kbeg + (kt + 1) * BK);
+  // Tile t is in LDS buffer t & 1 while tiles t+1 .. t+PF-1 sit in register stages
+  // (t+1) % PF ..; the stage that held tile t (stored at the end of step t-1) takes the
+  // fetch of tile t+PF. The loop runs in periods of lcm(2, PF) steps so that every
+  // buffer and stage index is a compile-time constant.
+  constexpr int PERIOD = PF % 2 == 0 ? PF : 2 * PF;
+  for (int kt = 0; kt < nk; kt += PERIOD) {
+    static_for<0, PERIOD>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      const int t = kt + u;
+      if (t < nk) {
+        if (t + PF < nk) {
+          la.template fetch<u % PF>(g.a, z, m0, kbeg + (t + PF) * BK);
+          lb.template fetch<u % PF>(g.b, z, n0, kbeg + (t + PF) * BK);
+        }
+        compute_tile(smem + (u & 1) * (SA + SB));
+        if (t + 1 < nk) {
+          float* nA = smem + ((u + 1) & 1) * (SA + SB);
+          la.template store<(u + 1) % PF>(nA);
+          lb.template store<(u + 1) % PF>(nA + SA);
+        }
+        __syncthreads();
       }
-      compute_tile(smem + (kt & 1) * (SA + SB));
-      if (kt + 1 < nk) {
-        float* nA = smem + ((kt + 1) & 1) * (SA + SB);
-        la.store(nA);
-        lb.store(nA + SA);
-      }
-      __syncthreads();
-    }
-  } else {
-    // tile kt is in LDS buffer kt & 1 and tile kt + 1 in register stage (kt + 1) & 1; the
-    // stage that held tile kt is free for tile kt + 2
-    for (int kt = 0; kt < nk; kt += 2) {
-      if (kt + 2 < nk) {
-        la.template fetch<0>(g.a, z, m0, kbeg + (kt + 2) * BK);
-        lb.template fetch<0>(g.b, z, n0, kbeg + (kt + 2) * BK);
-      }
-      compute_tile(smem);
-      if (kt + 1 < nk) {
-        la.template store<1>(smem + SA + SB);
-        lb.template store<1>(smem + SA + SB + SA);
-      }
-      __syncthreads();
-      if (kt + 1 >= nk) break;
-      if (kt + 3 < nk) {
-        la.template fetch<1>(g.a, z, m0, kbeg + (kt + 3) * BK);
-        lb.template fetch<1>(g.b, z, n0, kbeg + (kt + 3) * BK);
-      }
-      compute_tile(smem + SA + SB);
-      if (kt + 2 < nk) {
-        la.template store<0>(smem);
-        lb.template store<0>(smem + SA);
-      }
-      __syncthreads();
-    }
+    });
   }
 
   // Epilogue: split-K partial sums, or the layer's epilogue. The epilogue kind is the same
