@@ -51,8 +51,9 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(workload: str, sample_batch: int, steps: int = 3):
-    """Float32 CPU oracle step on a bounded sample; samples/s (median of ``steps``)."""
+def cpu_baseline(workload: str, sample_batch: int, min_steps: int = 3, budget_s: float = 12.0):
+    """Float32 CPU oracle steps on a bounded sample: at least ``min_steps`` steps and
+    about ``budget_s`` seconds of CPU work; samples/s from the median step time."""
     import torch
 
     from oracle import tagi_oracle as O
@@ -66,11 +67,12 @@ def cpu_baseline(workload: str, sample_batch: int, steps: int = 3):
     x, y = w.x.float(), w.y.float()
     onet.step(x, y, w.sigma_v)  # warm-up
     times = []
-    for _ in range(steps):
+    while len(times) < min_steps or sum(times) < budget_s:
         t0 = time.perf_counter()
         onet.step(x, y, w.sigma_v)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
+    steps = len(times)
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -85,7 +87,8 @@ def cpu_baseline(workload: str, sample_batch: int, steps: int = 3):
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"{workload} step at batch {sample_batch} (same architecture, priors and input distribution), "
-                  f"fp32 torch CPU ops, 1 warm-up + median of {steps} steps ({med:.2f} s/step); cpu: {cpu_model}",
+                  f"fp32 torch CPU ops, 1 warm-up + median of {steps} steps ({med:.2f} s/step, "
+                  f"{sum(times):.1f} s measured); cpu: {cpu_model}",
     }
 
 
