@@ -176,10 +176,11 @@ def test_innovation_update_add_jacobian(dev):
         assert_scaled_close(Sg, rS, None, RTOL, ATOL, f"update S n={n}")
 
     groups, refs = [], []
-    for n in (3, 4096 * 3 + 1, 17, 70000):
+    for n, offset in ((3, 0), (4096 * 3 + 1, 0), (17, 0), (70000, 0), (9001, 1), (4099, 2)):
+        # offset > 0: the tensors are views starting off a 16-byte boundary (scalar path)
         m, S = torch.randn(n, generator=r), 1e-3 + torch.rand(n, generator=r) * 1e-2
         ddm, ddS = torch.randn(n, generator=r) * 0.05, torch.randn(n, generator=r) * 1e-2
-        groups.append(tuple(t.to(dev) for t in (m, S, ddm, ddS)))
+        groups.append(tuple(torch.cat([torch.zeros(offset), t]).to(dev)[offset:] for t in (m, S, ddm, ddS)))
         refs.append(O.capped_update(d64(m), d64(S), d64(ddm), d64(ddS), 3.0))
     update_parameters_multi(groups, 3.0)
     for (mg, Sg, _, _), (rm, rS) in zip(groups, refs):

@@ -120,8 +120,8 @@ __global__ void update_kernel(float* __restrict__ m, float* __restrict__ S, cons
   }
 }
 
-constexpr int kMultiMax = 32;
-constexpr int kMultiChunk = 4096;  // elements per block
+constexpr int kMultiMax = 48;
+constexpr int kMultiChunk = 4096;  // elements per block (a multiple of 4)
 struct MultiUpdateArgs {
   float* m[kMultiMax];
   float* S[kMultiMax];
@@ -129,6 +129,7 @@ struct MultiUpdateArgs {
   const float* dS[kMultiMax];
   int64_t n[kMultiMax];
   int64_t block_start[kMultiMax + 1];
+  unsigned long long vec_mask;  // bit t: tensor t's four arrays are 16-byte aligned
   int count;
   float cap;
 };
@@ -144,7 +145,31 @@ __global__ void update_multi_kernel(MultiUpdateArgs a) {
   float* S = a.S[t];
   const float* dm = a.dm[t];
   const float* dS = a.dS[t];
-  for (int64_t i = base + threadIdx.x; i < base + kMultiChunk && i < n; i += blockDim.x) {
+  const int64_t end = base + kMultiChunk < n ? base + kMultiChunk : n;
+  if ((a.vec_mask >> t) & 1ull) {
+    // float4 groups of the chunk, then the tensor's last n % 4 elements one by one
+    const int64_t e4 = base + ((end - base) & ~(int64_t)3);
+    for (int64_t i = base + 4 * (int64_t)threadIdx.x; i < e4; i += 4 * (int64_t)blockDim.x) {
+      float4 x = *reinterpret_cast<float4*>(m + i);
+      float4 y = *reinterpret_cast<float4*>(S + i);
+      const float4 c = *reinterpret_cast<const float4*>(dm + i);
+      const float4 d = *reinterpret_cast<const float4*>(dS + i);
+      capped(x.x, y.x, c.x, d.x, a.cap);
+      capped(x.y, y.y, c.y, d.y, a.cap);
+      capped(x.z, y.z, c.z, d.z, a.cap);
+      capped(x.w, y.w, c.w, d.w, a.cap);
+      *reinterpret_cast<float4*>(m + i) = x;
+      *reinterpret_cast<float4*>(S + i) = y;
+    }
+    for (int64_t i = e4 + threadIdx.x; i < end; i += blockDim.x) {
+      float mm = m[i], ss = S[i];
+      capped(mm, ss, dm[i], dS[i], a.cap);
+      m[i] = mm;
+      S[i] = ss;
+    }
+    return;
+  }
+  for (int64_t i = base + threadIdx.x; i < end; i += blockDim.x) {
     float mm = m[i], ss = S[i];
     capped(mm, ss, dm[i], dS[i], a.cap);
     m[i] = mm;
@@ -415,6 +440,7 @@ extern "C" int tagi_capped_update_multi(float* const* m, float* const* S, const 
       a.dm[c] = dm[t];
       a.dS[c] = dS[t];
       a.n[c] = n[t];
+      if (aligned16(m[t]) && aligned16(S[t]) && aligned16(dm[t]) && aligned16(dS[t])) a.vec_mask |= 1ull << c;
       a.block_start[c] = blocks;
       blocks += cdiv(n[t], kMultiChunk);
       ++c;
