@@ -174,12 +174,17 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
   const double alg = 2.0 * 2 * (g->N * g->Ho * g->Wo) * Kw * g->Cout;
   ProfScope ps(FAM_CONV_BWD_DELTA, s, alg,
                4.0 * (2 * g->N * g->Cout * g->Ho * g->Wo + Kw * g->Cout + 2 * g->N * g->C * g->H * g->W));
-  // weights (c, kh, kw) x co  ->  (kh, kw, co) x c: a transpose of the C x (k*k*Cout) matrix
-  const int rows = (int)g->C, cols = (int)(g->k * g->k * g->Cout);
+  // With Cout % 4 == 0 the weights are read in place, float4 along co (the reduction
+  // index); otherwise they are first transposed, (c, kh, kw) x co -> (kh, kw, co) x c,
+  // for float4 (or scalar) reads along c.
+  const bool in_place = g->Cout % 4 == 0 && al16(mw);
   float* wt = ws;
-  hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32)), dim3(256), 0, s, mw,
-                     wt, rows, cols);
-  if ((rc = check_launch(what))) return rc;
+  if (!in_place) {
+    const int rows = (int)g->C, cols = (int)(g->k * g->k * g->Cout);
+    hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32)), dim3(256), 0, s, mw,
+                       wt, rows, cols);
+    if ((rc = check_launch(what))) return rc;
+  }
   // any input pixel a stride phase leaves without taps gets zero deltas (k < stride)
   const int nph = (int)(g->stride * g->stride);
   bool holes = false;
@@ -196,7 +201,7 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
   bwd_phase0(g, &R0, &K0);
   GemmArgs a{};
   a.a = conv_operand(dmz, dSz, g, R0, K0);
-  a.b = conv_operand(wt, nullptr, g, g->C, K0);
+  a.b = conv_operand(in_place ? mw : wt, nullptr, g, g->C, K0);
   a.epi = Epi{};
   a.epi.kind = 2;
   a.epi.om = dma;
@@ -231,6 +236,7 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
   const int64_t gx = (int64_t)p.tiles_m * p.tiles_n;  // phase 0 is the largest
   const bool va = g->Cout % 4 == 0 && al16(dmz) && al16(dSz);
   const bool vb = g->C % 4 == 0;
+  if (va && in_place) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4>(a, nph, p, part, part_bytes, s, what, gx);
   if (va && vb) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B4>(a, nph, p, part, part_bytes, s, what, gx);
   if (va) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B_S>(a, nph, p, part, part_bytes, s, what, gx);
   return run_gemm<PROD_SHARED_B, LD_CBWD_A_S, LD_CBWD_B_S>(a, nph, p, part, part_bytes, s, what, gx);

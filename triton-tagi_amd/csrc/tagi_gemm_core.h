@@ -47,6 +47,8 @@ enum {
   LD_CWG_A4 = 11,     // conv weight delta patches: mn = (kh,kw,c) [+ ones row], k = out pixel m
   LD_CWG_A_S = 12,    //   scalar version
   LD_CFWD_B_S = 13,   // conv fwd weights, scalar (any Cout)
+  LD_CBWD_BK4 = 14,   // input-delta weights read in place, w[((c*kk + kh)*kk + kw)*Cout + co]:
+                      //   mn = c, k = (ikh,ikw,co), float4 along co (Cout % 4 == 0)
 };
 
 template <int KIND>
@@ -55,7 +57,7 @@ struct KindTraits {
                                    KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CWG_A4 ||
                                    KIND == LD_CWG_A_S || KIND == LD_CFWD_B_S);
   static constexpr bool vec4 = (KIND == LD_STR_MN4 || KIND == LD_STR_K4 || KIND == LD_CFWD_A4 || KIND == LD_CFWD_B4 ||
-                                KIND == LD_CBWD_A4 || KIND == LD_CBWD_B4 || KIND == LD_CWG_A4);
+                                KIND == LD_CBWD_A4 || KIND == LD_CBWD_B4 || KIND == LD_CWG_A4 || KIND == LD_CBWD_BK4);
 };
 
 // Exact division by an invariant d >= 1 for dividends 0 <= n < 2^31 (Granlund and
@@ -190,8 +192,8 @@ struct Loader {
   using Vt = typename std::conditional<V4, float4, float>::type;
   static constexpr bool CONV_ROWS = (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S || KIND == LD_CBWD_A4 ||
                                      KIND == LD_CBWD_A_S);
-  static constexpr bool CONV_R = CONV_ROWS || KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CWG_A4 ||
-                                 KIND == LD_CWG_A_S;
+  static constexpr bool CONV_R = CONV_ROWS || KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CBWD_BK4 ||
+                                 KIND == LD_CWG_A4 || KIND == LD_CWG_A_S;
   static constexpr int NRB = CONV_ROWS ? NC : 1;  // per-chunk row bases only where rows differ
   static constexpr int NR = CONV_R ? NC : 1;
 
@@ -221,7 +223,8 @@ struct Loader {
     map(tid);
     mnmax = o.MN;
     kmax = o.K;
-    if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S || KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S) {
+    if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S || KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S ||
+                  KIND == LD_CBWD_BK4) {
       const Phase ph = make_phase(o.g, z);
       kmax = ph.nkh * ph.nkw * o.g.Cout;
       dnkw = make_fastdiv(ph.nkw > 0 ? ph.nkw : 1);
@@ -266,7 +269,7 @@ struct Loader {
         }
         r2[i] = ph.nkw;
       }
-    } else if constexpr (KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S) {
+    } else if constexpr (KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CBWD_BK4) {
       // tap offsets of this phase
       const Phase ph = make_phase(o.g, z);
 #pragma unroll
@@ -343,6 +346,15 @@ struct Loader {
         const int kw = r1[i] + ikw * o.g.stride;
         ok = k < kmax && mn < mnmax;
         off = ((kh * o.g.kk + kw) * o.g.Cout + co) * o.g.C + mn;
+      } else if constexpr (KIND == LD_CBWD_BK4) {
+        // the same (kh, kw, co) as LD_CBWD_B4, read from the weights in their own layout: the
+        // chunk's 4 reduction indices are 4 consecutive co of one tap
+        const int kidx = fdiv(k, o.g.dCout), co = k - kidx * o.g.Cout;
+        const int ikh = fdiv(kidx, dnkw), ikw = kidx - ikh * r2[i];
+        const int kh = r0[i] + ikh * o.g.stride;
+        const int kw = r1[i] + ikw * o.g.stride;
+        ok = k < kmax && mn < mnmax;
+        off = ((int64_t)(mn * o.g.kk + kh) * o.g.kk + kw) * o.g.Cout + co;
       } else if constexpr (KIND == LD_CWG_A4 || KIND == LD_CWG_A_S) {
         // k = (n*Ho + oh)*Wo + ow
         const int n = fdiv(k, o.g.dHW), pix = k - n * (o.g.Ho * o.g.Wo);
