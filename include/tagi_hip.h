@@ -300,6 +300,33 @@ int tagi_bn_relu_bwd(const float* dma, const float* dSa, const float* mhat, cons
                      float* dSz, float* dmg, float* dSg, float* dmb, float* dSb, int64_t N, int64_t C,
                      int64_t HW, float eps, float* ws, int64_t ws_bytes, tagi_stream_t stream);
 
+/* tagi_bn_relu_bwd without the parameter-delta pass: dmz/dSz are written and the
+ * per-channel partial sums are left in ws (size from tagi_bn_bwd_ws_bytes), which must
+ * stay untouched until tagi_bn_bwd_finalize_multi has consumed them. Together the two
+ * replace batchnorm2d.py:465-513 + relu.py:152-169 for a whole network's BatchNorm2D
+ * layers with one parameter-delta launch. */
+int tagi_bn_relu_bwd_partials(const float* dma, const float* dSa, const float* mhat,
+                              const float* J, const float* var, const float* mg, float* dmz,
+                              float* dSz, int64_t N, int64_t C, int64_t HW, float eps, float* ws,
+                              int64_t ws_bytes, tagi_stream_t stream);
+
+/* One layer left pending by tagi_bn_relu_bwd_partials: its partial sums (ws) and sizes,
+ * the gamma/beta variances and the four parameter-delta outputs of length C. */
+typedef struct {
+  const float* ws;
+  const float* Sg;
+  const float* Sb;
+  float* dmg;
+  float* dSg;
+  float* dmb;
+  float* dSb;
+  int64_t N, C, HW;
+} tagi_bn_bwd_pending;
+
+/* The parameter deltas of count pending layers, in one launch per 32 layers:
+ *   dmg = Sg * sum(dmu mhat), dSg = Sg^2 * sum(dS mhat^2), dmb = Sb * sum(dmu), dSb = Sb^2 * sum(dS). */
+int tagi_bn_bwd_finalize_multi(const tagi_bn_bwd_pending* items, int64_t count, tagi_stream_t stream);
+
 /* -------------------------------------------------- RMSNorm / Embedding / PE ---- */
 /* RMSNorm forward over rows of length D (rms_norm.py:93-110); inv_rms (rows) is cached. */
 int tagi_rmsnorm_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw,

@@ -334,6 +334,38 @@ __global__ void __launch_bounds__(256) bn_bwd_finalize_kernel(const float* __res
   dSb[c] = b * b * s3;
 }
 
+// The BatchNorm2D parameter-delta pass of several layers in one launch: block b finalizes
+// channel b - start[t] of layer t (the same fixed-order sums as bn_bwd_finalize_kernel).
+constexpr int kBnMulti = 32;
+struct BnFinalizeMulti {
+  const float* ws[kBnMulti];
+  const float* Sg[kBnMulti];
+  const float* Sb[kBnMulti];
+  float* dmg[kBnMulti];
+  float* dSg[kBnMulti];
+  float* dmb[kBnMulti];
+  float* dSb[kBnMulti];
+  int C[kBnMulti];
+  int nblk[kBnMulti];
+  int start[kBnMulti + 1];
+  int count;
+};
+
+__global__ void __launch_bounds__(256) bn_bwd_finalize_multi_kernel(BnFinalizeMulti a) {
+  const int b = blockIdx.x;
+  int t = 0;
+  while (t + 1 < a.count && a.start[t + 1] <= b) ++t;
+  const int c = b - a.start[t];
+  float sums[4];
+  channel_sums<4>(a.ws[t], a.C[t], c, a.nblk[t], sums);
+  if (threadIdx.x != 0) return;
+  const float g = a.Sg[t][c], bb = a.Sb[t][c];
+  a.dmg[t][c] = g * sums[0];
+  a.dSg[t][c] = g * g * sums[1];
+  a.dmb[t][c] = bb * sums[2];
+  a.dSb[t][c] = bb * bb * sums[3];
+}
+
 // --------------------------------------------------------------------- RMSNorm
 // One wavefront per row (rms_norm.py:99-110).
 template <int EPT>
@@ -723,9 +755,9 @@ extern "C" int64_t tagi_bn_bwd_ws_bytes(int64_t N, int64_t C, int64_t HW) {
 static int bn_bwd_impl(const char* what, const float* dma, const float* dSa, const float* mhat, const float* J,
                        const float* var, const float* mg, const float* Sg, const float* Sb, float* dmz, float* dSz,
                        float* dmg, float* dSg, float* dmb, float* dSb, int64_t N, int64_t C, int64_t HW, float eps,
-                       float* ws, int64_t ws_bytes, tagi_stream_t stream, bool jac) {
-  TAGI_REQUIRE(dma && dSa && mhat && var && mg && Sg && Sb && dmz && dSz && dmg && dSg && dmb && dSb && ws &&
-                   (!jac || J),
+                       float* ws, int64_t ws_bytes, tagi_stream_t stream, bool jac, bool finalize = true) {
+  TAGI_REQUIRE(dma && dSa && mhat && var && mg && dmz && dSz && ws && (!jac || J) &&
+                   (!finalize || (Sg && Sb && dmg && dSg && dmb && dSb)),
                "%s: null pointer", what);
   TAGI_REQUIRE(N > 0 && C > 0 && HW > 0, "%s: bad sizes", what);
   TAGI_REQUIRE(ws_bytes >= tagi_bn_bwd_ws_bytes(N, C, HW), "%s: workspace too small", what);
@@ -752,7 +784,7 @@ static int bn_bwd_impl(const char* what, const float* dma, const float* dSa, con
                          nblk, var, mg, dmz, dSz, eps);
   }
   int rc = check_launch(what);
-  if (rc) return rc;
+  if (rc || !finalize) return rc;
   hipLaunchKernelGGL(bn_bwd_finalize_kernel, dim3((unsigned)C), dim3(256), 0, s, (const float*)ws, Sg, Sb,
                      dmg, dSg, dmb, dSb, (int)C, nblk);
   return check_launch(what);
@@ -772,6 +804,53 @@ extern "C" int tagi_bn_relu_bwd(const float* dma, const float* dSa, const float*
                                 int64_t HW, float eps, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
   return bn_bwd_impl("tagi_bn_relu_bwd", dma, dSa, mhat, J, var, mg, Sg, Sb, dmz, dSz, dmg, dSg, dmb, dSb, N, C, HW,
                      eps, ws, ws_bytes, stream, true);
+}
+
+extern "C" int tagi_bn_relu_bwd_partials(const float* dma, const float* dSa, const float* mhat, const float* J,
+                                         const float* var, const float* mg, float* dmz, float* dSz, int64_t N,
+                                         int64_t C, int64_t HW, float eps, float* ws, int64_t ws_bytes,
+                                         tagi_stream_t stream) {
+  return bn_bwd_impl("tagi_bn_relu_bwd_partials", dma, dSa, mhat, J, var, mg, nullptr, nullptr, dmz, dSz, nullptr,
+                     nullptr, nullptr, nullptr, N, C, HW, eps, ws, ws_bytes, stream, true, false);
+}
+
+extern "C" int tagi_bn_bwd_finalize_multi(const tagi_bn_bwd_pending* items, int64_t count, tagi_stream_t stream) {
+  const char* what = "tagi_bn_bwd_finalize_multi";
+  TAGI_REQUIRE(count >= 0 && (count == 0 || items), "%s: bad table", what);
+  hipStream_t s = as_stream(stream);
+  int64_t bytes = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const tagi_bn_bwd_pending& p = items[i];
+    TAGI_REQUIRE(p.ws && p.Sg && p.Sb && p.dmg && p.dSg && p.dmb && p.dSb, "%s: null pointer at %lld", what,
+                 (long long)i);
+    TAGI_REQUIRE(p.N > 0 && p.C > 0 && p.HW > 0 && p.C < (1 << 24), "%s: bad sizes at %lld", what, (long long)i);
+    bytes += (int64_t)red_rows(p.N * p.HW) * p.C * 16 + 24 * p.C;
+  }
+  ProfScope ps(FAM_BN_BWD, s, 0.0, (double)bytes);
+  for (int64_t t0 = 0; t0 < count; t0 += kBnMulti) {
+    BnFinalizeMulti a{};
+    int c = 0, blocks = 0;
+    for (int64_t t = t0; t < count && c < kBnMulti; ++t, ++c) {
+      const tagi_bn_bwd_pending& p = items[t];
+      a.ws[c] = p.ws;
+      a.Sg[c] = p.Sg;
+      a.Sb[c] = p.Sb;
+      a.dmg[c] = p.dmg;
+      a.dSg[c] = p.dSg;
+      a.dmb[c] = p.dmb;
+      a.dSb[c] = p.dSb;
+      a.C[c] = (int)p.C;
+      a.nblk[c] = red_rows(p.N * p.HW);
+      a.start[c] = blocks;
+      blocks += (int)p.C;
+    }
+    a.start[c] = blocks;
+    a.count = c;
+    hipLaunchKernelGGL(bn_bwd_finalize_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    int rc = check_launch(what);
+    if (rc) return rc;
+  }
+  return TAGI_OK;
 }
 
 extern "C" int tagi_rmsnorm_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw, float* mz,

@@ -45,8 +45,17 @@ class ConvGeom(ctypes.Structure):
 P = c_void_p
 I64 = c_int64
 F = c_float
+class BnPending(ctypes.Structure):
+    """tagi_bn_bwd_pending: one BatchNorm2D layer whose parameter deltas are still to form."""
+
+    _fields_ = [(n, c_void_p) for n in ("ws", "Sg", "Sb", "dmg", "dSg", "dmb", "dSb")] + [
+        (n, c_int64) for n in ("N", "C", "HW")
+    ]
+
+
 VP = POINTER(TagiView)
 GP = POINTER(ConvGeom)
+BP = POINTER(BnPending)
 
 # name -> (restype, argtypes)
 _SIGS = {
@@ -89,6 +98,8 @@ _SIGS = {
     "tagi_relu_bn_stats": (c_int, [P, P, P, P, P, P, P, P, I64, I64, I64, F, F, c_int, c_int, P, I64, P]),
     "tagi_relu_bn_fwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P]),
     "tagi_bn_relu_bwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P, I64, P]),
+    "tagi_bn_relu_bwd_partials": (c_int, [P, P, P, P, P, P, P, P, I64, I64, I64, F, P, I64, P]),
+    "tagi_bn_bwd_finalize_multi": (c_int, [BP, I64, P]),
     "tagi_rmsnorm_fwd": (c_int, [P, P, P, P, P, P, P, I64, I64, F, P]),
     "tagi_rmsnorm_bwd": (c_int, [P, P, P, P, P, P, P, P, P, P, I64, I64, P, I64, P]),
     "tagi_rmsnorm_bwd_ws_bytes": (I64, [I64, I64]),

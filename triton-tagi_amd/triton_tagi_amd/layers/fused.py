@@ -21,6 +21,8 @@ working after a fused pass.
 
 from __future__ import annotations
 
+import threading
+
 import torch
 from torch import Tensor
 
@@ -28,6 +30,37 @@ from .. import _lib
 from .batchnorm2d import BatchNorm2D
 from .conv2d import Conv2D
 from .relu import ReLU
+
+
+_scope = threading.local()
+
+
+class defer_bn_parameter_deltas:
+    """Within this context the fused BatchNorm2D -> ReLU backward passes leave their
+    per-channel partial sums pending; leaving it forms the parameter deltas of all of them
+    in one launch (``Sequential.step`` wraps its backward pass in it). The layers'
+    ``delta_*`` tensors are complete once the context has exited."""
+
+    def __enter__(self):
+        self.items = []
+        self._keep = []
+        self._outer = getattr(_scope, "ctx", None)
+        _scope.ctx = self
+        return self
+
+    def add(self, bn: BatchNorm2D, ws: Tensor, N: int, C: int, HW: int) -> None:
+        self._keep.append(ws)  # the partial sums must outlive the launch below
+        self.items.append(_lib.BnPending(ws.data_ptr(), bn.Sw.data_ptr(), bn.Sb.data_ptr(), bn.delta_mw.data_ptr(),
+                                         bn.delta_Sw.data_ptr(), bn.delta_mb.data_ptr(), bn.delta_Sb.data_ptr(),
+                                         N, C, HW))
+        self._stream = _lib.stream_of(ws)
+
+    def __exit__(self, exc_type, exc, tb):
+        _scope.ctx = self._outer
+        if exc_type is None and self.items:
+            arr = (_lib.BnPending * len(self.items))(*self.items)
+            _lib.call("tagi_bn_bwd_finalize_multi", arr, len(self.items), self._stream)
+        return False
 
 
 def _add_in_place(src_m: Tensor, src_S: Tensor, dst_m: Tensor, dst_S: Tensor) -> None:
@@ -97,6 +130,13 @@ def bn_relu_backward(bn: BatchNorm2D, relu: ReLU, delta_ma: Tensor, delta_Sa: Te
     bn.delta_Sb = torch.empty_like(bn.delta_mw)
     ws = _lib.workspace(_lib.query("tagi_bn_bwd_ws_bytes", N, C, HW), dev)
     wp, wb = _lib.ws_args(ws)
+    ctx = getattr(_scope, "ctx", None)
+    if ctx is not None:
+        _lib.call("tagi_bn_relu_bwd_partials", dma.data_ptr(), dSa.data_ptr(), bn.m_hat.data_ptr(), J.data_ptr(),
+                  bn._norm_var.data_ptr(), bn.mw.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), N, C, HW,
+                  float(bn.eps), wp, wb, _lib.stream_of(dma))
+        ctx.add(bn, ws, N, C, HW)
+        return dmz, dSz
     _lib.call("tagi_bn_relu_bwd", dma.data_ptr(), dSa.data_ptr(), bn.m_hat.data_ptr(), J.data_ptr(),
               bn._norm_var.data_ptr(), bn.mw.data_ptr(), bn.Sw.data_ptr(), bn.Sb.data_ptr(), dmz.data_ptr(),
               dSz.data_ptr(), bn.delta_mw.data_ptr(), bn.delta_Sw.data_ptr(), bn.delta_mb.data_ptr(),

@@ -14,7 +14,7 @@ from torch import Tensor
 
 from .base import Layer, LearnableLayer
 from .layers.conv2d import Conv2D
-from .layers.fused import backward_chain, forward_chain
+from .layers.fused import backward_chain, defer_bn_parameter_deltas, forward_chain
 from .layers.multihead_attention import MultiheadAttentionV2
 from .layers.resblock import ResBlock
 from .update.observation import compute_innovation
@@ -101,7 +101,8 @@ class Sequential:
         batch_size = x_batch.shape[0]
         y_pred_mu, y_pred_var = self.forward(x_batch)
         delta_mu, delta_var = compute_innovation(y_batch, y_pred_mu, y_pred_var, sigma_v)
-        backward_chain(self.layers, delta_mu, delta_var, first_params_only=True)
+        with defer_bn_parameter_deltas():  # one launch forms every BatchNorm2D's parameter deltas
+            backward_chain(self.layers, delta_mu, delta_var, first_params_only=True)
         self.update(get_cap_factor(batch_size))
         return y_pred_mu, y_pred_var
 
