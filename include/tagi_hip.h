@@ -166,6 +166,21 @@ int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw, const flo
                     const tagi_conv_geom* g, float* ws, int64_t ws_bytes, tagi_stream_t stream);
 int64_t tagi_conv2d_fwd_ws_bytes(const tagi_conv_geom* g);
 
+/* tagi_conv2d_fwd followed by the first pass of ReLU -> BatchNorm2D on its output
+ * (conv2d.py:254-309, relu.py:135-140, batchnorm2d.py:307-355): mz, Sz as tagi_conv2d_fwd,
+ * then J, the batch statistics and the running-stat / gamma bookkeeping as
+ * tagi_relu_bn_stats on (mz, Sz). Where the GEMM runs unsplit its epilogue forms J and
+ * the per-tile channel sums, so the output is not read back. ws: 16-byte aligned, size
+ * from tagi_conv2d_fwd_relu_bn_stats_ws_bytes. */
+int tagi_conv2d_fwd_relu_bn_stats(const float* ma, const float* Sa, const float* mw, const float* Sw,
+                                  const float* mb, const float* Sb, float* mz, float* Sz,
+                                  const tagi_conv_geom* g, float* J, float* batch_mean,
+                                  float* batch_var, float* running_mean, float* running_var,
+                                  float* mg, float momentum, float eps, int first_call,
+                                  int preserve_var, float* ws, int64_t ws_bytes,
+                                  tagi_stream_t stream);
+int64_t tagi_conv2d_fwd_relu_bn_stats_ws_bytes(const tagi_conv_geom* g);
+
 /* Transposed implicit GEMM for the input deltas (no patch matrix, no col2im):
  *   dma = fold(dmz_rows @ mw^T), dSa = fold(dSz_rows @ (mw^2)^T), channels-last (N,C,H,W).
  * Split by stride phase: each phase multiplies only the kernel taps that reach it.

@@ -1,8 +1,8 @@
 """Fused multi-layer passes against the float64 oracle and against the unfused layers.
 
-The fused passes (ReLU -> BatchNorm2D forward with an optional residual add, BatchNorm2D
--> ReLU backward, conv input deltas with the shortcut deltas added in the epilogue) must
-give the reference's results: checked against the oracle's layer-by-layer chain at the
+The fused passes (Conv2D -> ReLU -> BatchNorm2D and ReLU -> BatchNorm2D forward with an
+optional residual add, BatchNorm2D -> ReLU backward, conv input deltas with the shortcut
+deltas added in the epilogue) must give the reference's results: checked against the oracle's layer-by-layer chain at the
 engine's bar (|gpu - oracle| <= 1e-6 + 1e-4 * scale), and against the engine's own
 unfused kernels (same fp32 formulas, so they agree to a few ulps).
 """
@@ -121,6 +121,63 @@ def test_relu_bn_fused(dev, shape, first, preserve, add):
     close_unfused(om, vm, "bwd mean")
     close_unfused(oS, vS, "bwd var")
     close_unfused(bn.delta_mw, bn_u.delta_mw, "delta gamma")
+
+
+CONV_BN_CASES = [
+    # N, C, H, W, Cout, k, stride, padding, padding_type, first call, preserve_var, residual add
+    (16, 16, 16, 16, 64, 3, 1, 1, 1, True, True, True),
+    (4, 3, 32, 32, 64, 3, 1, 1, 1, True, True, False),     # stem: 3 input channels
+    (8, 64, 16, 16, 128, 3, 2, 1, 2, False, False, True),  # stride 2, right/bottom padding
+    (3, 5, 7, 9, 6, 3, 2, 1, 2, True, False, True),        # 6 channels, rows not a tile multiple
+    (32, 512, 4, 4, 512, 3, 1, 1, 1, False, False, True),  # long reduction: split-K launch
+    (16, 256, 8, 8, 512, 2, 2, 0, 1, True, False, False),  # 2x2 projection
+]
+
+
+@pytest.mark.parametrize("case", CONV_BN_CASES, ids=[str(c) for c in CONV_BN_CASES])
+def test_conv_relu_bn_fused(dev, case):
+    """Conv2D -> ReLU -> BatchNorm2D with the statistics formed in the conv epilogue."""
+    from triton_tagi_amd.layers.conv2d import Conv2D
+    from triton_tagi_amd.layers.fused import conv_relu_bn_forward, relu_bn_forward
+    from triton_tagi_amd.layers.relu import ReLU
+
+    N, C, H, W, Cout, k, s, p, pt, first, preserve, add = case
+    seed = N * 13 + C + Cout
+    torch.manual_seed(seed)
+    conv = Conv2D(C, Cout, k, stride=s, padding=p, padding_type=pt, device="cpu")
+    rconv = O.mirror(conv)
+    for a in ("mw", "Sw", "mb", "Sb"):
+        setattr(conv, a, getattr(conv, a).to(dev))
+    conv_u = copy.deepcopy(conv)
+    bn, rbn = make_bn(Cout, first, preserve, seed, dev)
+    bn_u = copy.deepcopy(bn)
+    relu, relu_u, rrelu = ReLU(), ReLU(), O.OReLU()
+    r = g(seed + 1)
+    ma, Sa = torch.randn(N, C, H, W, generator=r), 0.1 * torch.rand(N, C, H, W, generator=r)
+    qz, qSz = rconv.forward(d64(ma), d64(Sa))
+    am, aS = torch.randn(qz.shape, generator=r), torch.rand(qz.shape, generator=r)
+    addend = (am.to(dev), aS.to(dev)) if add else None
+
+    om, oS = conv_relu_bn_forward(conv, relu, bn, ma.to(dev), Sa.to(dev), addend)
+    qa, qS = rrelu.forward(qz, qSz)
+    rm, rS = rbn.forward(qa, qS)
+    if add:
+        rm, rS = rm + d64(am), rS + d64(aS)
+    assert_scaled_close(om, rm, rm.abs() + 1.0, RTOL, ATOL, "mean")
+    assert_scaled_close(oS, rS, None, RTOL, ATOL, "var")
+    assert_scaled_close(relu.J, rrelu.J, None, RTOL, ATOL, "ReLU Jacobian")
+    assert_scaled_close(bn.running_mean, rbn.running_mean, rbn.running_mean.abs() + 1.0, RTOL, ATOL, "running mean")
+    assert_scaled_close(bn.running_var, rbn.running_var, None, RTOL, ATOL, "running var")
+    assert_scaled_close(bn.mw, rbn.mw, None, RTOL, ATOL, "gamma")
+    assert conv.ma_in.shape == (N, C, H, W) and conv.spatial == tuple(qz.shape[2:])
+
+    # the engine's separate passes: conv forward, then the ReLU -> BatchNorm2D statistics pass
+    uz, uSz = conv_u.forward(ma.to(dev), Sa.to(dev))
+    um, uS = relu_bn_forward(relu_u, bn_u, uz, uSz, addend)
+    close_unfused(om, um, "mean vs separate passes")
+    close_unfused(oS, uS, "var vs separate passes")
+    close_unfused(relu.J, relu_u.J, "Jacobian vs separate passes")
+    close_unfused(bn.running_var, bn_u.running_var, "running var vs separate passes")
 
 
 ADD_CASES = [

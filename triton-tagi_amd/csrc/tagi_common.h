@@ -72,6 +72,13 @@ struct ProfScope {
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// BatchNorm2D batch statistics from per-row-range partial sums of (mu, S, mu^2),
+// ws[(q * C + c) * nblk + b], with the running-stat / gamma bookkeeping of tagi_bn_stats
+// (defined with the BatchNorm kernels; launched on s, returns a TAGI status).
+int bn_stats_finalize(const char* what, const float* ws, int nblk, int64_t rows, int64_t C, float* batch_mean,
+                      float* batch_var, float* running_mean, float* running_var, float* mg, float momentum, float eps,
+                      int first_call, int preserve_var, hipStream_t s);
+
 // Grid size for a grid-stride elementwise kernel: enough blocks to fill 256 CUs several
 // times over, never more than needed.
 inline unsigned ew_blocks(int64_t n_items, int threads) {

@@ -125,6 +125,33 @@ extern "C" int64_t tagi_conv2d_fwd_ws_bytes(const tagi_conv_geom* g) {
   return plan_ws_bytes(conv_fwd_plan(g), g->N * g->Ho * g->Wo, g->Cout, 1);
 }
 
+// Forward GEMM; with st_J/st_ws set (and no split-K) the epilogue also forms the ReLU
+// Jacobian and the per-tile column sums of the rectified moments.
+static int conv_fwd_impl(const char* what, const float* ma, const float* Sa, const float* mw, const float* Sw,
+                         const float* mb, const float* Sb, float* mz, float* Sz, const tagi_conv_geom* g,
+                         const Plan& p, float* st_J, float* st_ws, float* ws, int64_t ws_bytes, hipStream_t s) {
+  const int64_t R = g->N * g->Ho * g->Wo, C = g->Cout, K = g->C * g->k * g->k;
+  ProfScope ps(FAM_CONV_FWD, s, 2.0 * 3 * R * C * K, 4.0 * (2 * g->N * g->C * g->H * g->W + 2 * K * C + 2 * R * C));
+  GemmArgs a{};
+  a.a = conv_operand(ma, Sa, g, R, K);
+  a.b = conv_operand(mw, Sw, g, C, K);
+  a.epi = epi_store(mz, Sz, mb, Sb, 0, 1, 1.f, 1.f, 1, 0, 0, C, 1);
+  if (st_ws) {
+    TAGI_REQUIRE(p.splits == 1 && st_J, "%s: internal: statistics epilogue needs an unsplit launch", what);
+    a.epi.st_J = st_J;
+    a.epi.st_ws = st_ws;
+    a.epi.st_nblk = p.tiles_m;
+  }
+  a.R = (int)R;
+  a.C = (int)C;
+  a.Kred = (int)K;
+  const bool va = g->C % 4 == 0 && al16(ma) && al16(Sa);
+  const bool vb = g->Cout % 4 == 0 && al16(mw) && al16(Sw);
+  if (va && vb) return run_gemm<PROD_FWD, LD_CFWD_A4, LD_CFWD_B4>(a, 1, p, ws, ws_bytes, s, what);
+  if (vb) return run_gemm<PROD_FWD, LD_CFWD_A_S, LD_CFWD_B4>(a, 1, p, ws, ws_bytes, s, what);
+  return run_gemm<PROD_FWD, LD_CFWD_A_S, LD_CFWD_B_S>(a, 1, p, ws, ws_bytes, s, what);
+}
+
 extern "C" int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw, const float* mb,
                                const float* Sb, float* mz, float* Sz, const tagi_conv_geom* g, float* ws,
                                int64_t ws_bytes, tagi_stream_t stream) {
@@ -132,23 +159,58 @@ extern "C" int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw
   int rc = check_geom(g, what);
   if (rc) return rc;
   TAGI_REQUIRE(ma && Sa && mw && Sw && mz && Sz, "%s: null pointer", what);
-  hipStream_t s = as_stream(stream);
   const int64_t R = g->N * g->Ho * g->Wo, C = g->Cout, K = g->C * g->k * g->k;
-  ProfScope ps(FAM_CONV_FWD, s, 2.0 * 3 * R * C * K, 4.0 * (2 * g->N * g->C * g->H * g->W + 2 * K * C + 2 * R * C));
-  GemmArgs a{};
-  a.a = conv_operand(ma, Sa, g, R, K);
-  a.b = conv_operand(mw, Sw, g, C, K);
-  a.epi = epi_store(mz, Sz, mb, Sb, 0, 1, 1.f, 1.f, 1, 0, 0, C, 1);
-  a.R = (int)R;
-  a.C = (int)C;
-  a.Kred = (int)K;
   Plan p = conv_fwd_plan(g);
   if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, R, C, 1))) p = choose_plan(R, C, K, 1, 3, false, 1);
-  const bool va = g->C % 4 == 0 && al16(ma) && al16(Sa);
-  const bool vb = g->Cout % 4 == 0 && al16(mw) && al16(Sw);
-  if (va && vb) return run_gemm<PROD_FWD, LD_CFWD_A4, LD_CFWD_B4>(a, 1, p, ws, ws_bytes, s, what);
-  if (vb) return run_gemm<PROD_FWD, LD_CFWD_A_S, LD_CFWD_B4>(a, 1, p, ws, ws_bytes, s, what);
-  return run_gemm<PROD_FWD, LD_CFWD_A_S, LD_CFWD_B_S>(a, 1, p, ws, ws_bytes, s, what);
+  return conv_fwd_impl(what, ma, Sa, mw, Sw, mb, Sb, mz, Sz, g, p, nullptr, nullptr, ws, ws_bytes,
+                       as_stream(stream));
+}
+
+// Statistics partials of the fused form: one row per M tile of an unsplit launch; a
+// split launch runs the separate statistics pass over the stored output instead.
+static int64_t fwd_stats_floats(const tagi_conv_geom* g, const Plan& p) {
+  const int64_t C = g->Cout;
+  if (p.splits > 1) return (tagi_bn_stats_ws_bytes(g->N, C, g->Ho * g->Wo) + 3) / 4;
+  return (int64_t)p.tiles_m * C * 3;
+}
+
+extern "C" int64_t tagi_conv2d_fwd_relu_bn_stats_ws_bytes(const tagi_conv_geom* g) {
+  if (!g || g->N <= 0 || g->Cout <= 0 || g->Ho <= 0 || g->Wo <= 0 || g->C <= 0 || g->k <= 0) return 0;
+  const Plan p = conv_fwd_plan(g);
+  const int64_t conv = plan_ws_bytes(p, g->N * g->Ho * g->Wo, g->Cout, 1);
+  return (conv + 255) / 256 * 256 + fwd_stats_floats(g, p) * (int64_t)sizeof(float);
+}
+
+extern "C" int tagi_conv2d_fwd_relu_bn_stats(const float* ma, const float* Sa, const float* mw, const float* Sw,
+                                             const float* mb, const float* Sb, float* mz, float* Sz,
+                                             const tagi_conv_geom* g, float* J, float* batch_mean, float* batch_var,
+                                             float* running_mean, float* running_var, float* mg, float momentum,
+                                             float eps, int first_call, int preserve_var, float* ws,
+                                             int64_t ws_bytes, tagi_stream_t stream) {
+  const char* what = "tagi_conv2d_fwd_relu_bn_stats";
+  int rc = check_geom(g, what);
+  if (rc) return rc;
+  TAGI_REQUIRE(ma && Sa && mw && Sw && mz && Sz && J && batch_mean && batch_var, "%s: null pointer", what);
+  const int64_t R = g->N * g->Ho * g->Wo, C = g->Cout;
+  TAGI_REQUIRE(R > 1, "%s: BatchNorm2D needs more than one value per channel", what);
+  TAGI_REQUIRE(ws && ws_bytes >= tagi_conv2d_fwd_relu_bn_stats_ws_bytes(g) && al16(ws),
+               "%s: workspace of %lld bytes (16-byte aligned) needed", what,
+               (long long)tagi_conv2d_fwd_relu_bn_stats_ws_bytes(g));
+  hipStream_t s = as_stream(stream);
+  const Plan p = conv_fwd_plan(g);
+  const int64_t conv = (plan_ws_bytes(p, R, C, 1) + 255) / 256 * 256;
+  float* sws = ws + conv / (int64_t)sizeof(float);
+  const int64_t sbytes = ws_bytes - conv;
+  if (p.splits > 1) {
+    rc = conv_fwd_impl(what, ma, Sa, mw, Sw, mb, Sb, mz, Sz, g, p, nullptr, nullptr, ws, conv, s);
+    if (rc) return rc;
+    return tagi_relu_bn_stats(mz, Sz, J, batch_mean, batch_var, running_mean, running_var, mg, g->N, C,
+                              g->Ho * g->Wo, momentum, eps, first_call, preserve_var, sws, sbytes, stream);
+  }
+  rc = conv_fwd_impl(what, ma, Sa, mw, Sw, mb, Sb, mz, Sz, g, p, J, sws, ws, conv, s);
+  if (rc) return rc;
+  return bn_stats_finalize(what, sws, p.tiles_m, R, C, batch_mean, batch_var, running_mean, running_var, mg, momentum,
+                           eps, first_call, preserve_var, s);
 }
 
 // ================================================================== input delta

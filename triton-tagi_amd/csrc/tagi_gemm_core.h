@@ -23,6 +23,7 @@
 #include <type_traits>
 
 #include "tagi_common.h"
+#include "tagi_moments.h"
 
 namespace tagi {
 
@@ -143,6 +144,12 @@ struct Epi {
   // kind 0: optional multiplier laid out like the output (mean * j, variance * j^2: the
   // Jacobian of an elementwise layer applied to the product's deltas)
   const float* jm;
+  // kind 0, plain store only: statistics of ReLU(output) for a BatchNorm2D after it.
+  // st_J receives the ReLU Jacobian (laid out like the output) and st_ws the per-tile
+  // column sums of mu_a, S_a and mu_a^2, st_ws[(q * C + col) * st_nblk + tile row].
+  float* st_J;
+  float* st_ws;
+  int st_nblk;
 };
 
 struct GemmArgs {
@@ -724,6 +731,8 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   } else if (e.kind == 0 && e.b_sr == 0) {
     // plain store with an optional per-column bias (Linear, Conv2D forward, bmm)
     const int64_t zoff = (z / e.zdiv) * e.sz1 + (z % e.zdiv) * e.sz2;
+    const bool st = e.st_ws != nullptr;
+    float* red = smem;  // [BM / WM][3][BN] column sums per wave row (LDS is free here)
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int col = n0 + wn * WN + j * 32 + rl;
@@ -731,6 +740,7 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
       const float bmj = (e.bm && cok) ? e.bm[(int64_t)col * e.b_sc] : 0.f;
       const float bvj = (e.bv && cok) ? e.bv[(int64_t)col * e.b_sc] : 0.f;
       const int64_t coff = zoff + (int64_t)col * e.scol;
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -750,8 +760,43 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
             }
             if (e.om) e.om[off] = m;
             e.ov[off] = vv;
+            if (st) {
+              float ra, rS, rJ;
+              relu_moments(m, vv, ra, rS, rJ);
+              e.st_J[off] = rJ;
+              s0 += ra;
+              s1 += rS;
+              s2 += ra * ra;
+            }
           }
         }
+      if (st) {
+        // lanes l and l + 32 hold the same column
+        s0 += __shfl_xor(s0, 32, 64);
+        s1 += __shfl_xor(s1, 32, 64);
+        s2 += __shfl_xor(s2, 32, 64);
+        if (hl == 0) {
+          const int cl = wn * WN + j * 32 + rl;
+          red[(wm * 3 + 0) * BN + cl] = s0;
+          red[(wm * 3 + 1) * BN + cl] = s1;
+          red[(wm * 3 + 2) * BN + cl] = s2;
+        }
+      }
+    }
+    if (st) {
+      __syncthreads();
+      for (int cl = tid; cl < BN; cl += NTH) {
+        const int col = n0 + cl;
+        if (col < g.C) {
+#pragma unroll
+          for (int q = 0; q < 3; ++q) {
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < BM / WM; ++w) sum += red[(w * 3 + q) * BN + cl];
+            e.st_ws[((int64_t)q * g.C + col) * e.st_nblk + tmi] = sum;
+          }
+        }
+      }
     }
   } else if (e.kind == 2) {
     // conv input delta: row q of stride phase z is input pixel (n, hh*s + a, ww*s + b)

@@ -634,6 +634,15 @@ extern "C" int64_t tagi_bn_stats_ws_bytes(int64_t N, int64_t C, int64_t HW) {
 
 static inline bool al16p(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+int tagi::bn_stats_finalize(const char* what, const float* ws, int nblk, int64_t rows, int64_t C, float* batch_mean,
+                            float* batch_var, float* running_mean, float* running_var, float* mg, float momentum,
+                            float eps, int first_call, int preserve_var, hipStream_t s) {
+  hipLaunchKernelGGL(bn_stats_finalize_kernel, dim3((unsigned)C), dim3(256), 0, s, ws, batch_mean, batch_var,
+                     running_mean, running_var, mg, (int)C, nblk, (double)rows, momentum, eps, first_call,
+                     preserve_var);
+  return check_launch(what);
+}
+
 // Statistics pass (MODE 0 or 1) + finalize: batch mean/var and running-stat bookkeeping.
 static int bn_stats_impl(const char* what, bool relu, const float* mz, const float* Sz, float* J, float* batch_mean,
                          float* batch_var, float* running_mean, float* running_var, float* mg, int64_t N, int64_t C,
@@ -666,10 +675,8 @@ static int bn_stats_impl(const char* what, bool relu, const float* mz, const flo
   }
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(bn_stats_finalize_kernel, dim3((unsigned)C), dim3(256), 0, s, (const float*)ws,
-                     batch_mean, batch_var, running_mean, running_var, mg, (int)C, nblk, (double)rows, momentum, eps,
-                     first_call, preserve_var);
-  return check_launch(what);
+  return bn_stats_finalize(what, ws, nblk, rows, C, batch_mean, batch_var, running_mean, running_var, mg, momentum,
+                           eps, first_call, preserve_var, s);
 }
 
 extern "C" int tagi_bn_stats(const float* mz, const float* Sz, float* batch_mean, float* batch_var,

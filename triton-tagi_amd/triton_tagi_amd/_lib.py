@@ -76,6 +76,9 @@ _SIGS = {
     "tagi_bmm_shared_jacobian": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),
     "tagi_conv2d_fwd": (c_int, [P, P, P, P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_fwd_ws_bytes": (I64, [GP]),
+    "tagi_conv2d_fwd_relu_bn_stats": (c_int, [P, P, P, P, P, P, P, P, GP, P, P, P, P, P, P, F, F, c_int, c_int, P,
+                                              I64, P]),
+    "tagi_conv2d_fwd_relu_bn_stats_ws_bytes": (I64, [GP]),
     "tagi_conv2d_bwd_delta": (c_int, [P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_bwd_delta_ws_bytes": (I64, [GP]),
     "tagi_conv2d_bwd_delta_add": (c_int, [P, P, P, P, P, P, P, GP, P, I64, P]),

@@ -55,10 +55,25 @@ class Conv2D(LearnableLayer):
         return _lib.ConvGeom(N, C, H, W, self.C_out, k, s, pt, pt, Ho, Wo)
 
     def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
+        ma, Sa, mz, Sz, g = self._forward_prepare(ma, Sa)
+        ws = _lib.workspace(_lib.query("tagi_conv2d_fwd_ws_bytes", g), mz.device)
+        wp, wb = _lib.ws_args(ws)
+        _lib.call("tagi_conv2d_fwd", ma.data_ptr(), Sa.data_ptr(), self.mw.data_ptr(), self.Sw.data_ptr(),
+                  self.mb.data_ptr(), self.Sb.data_ptr(), mz.data_ptr(), Sz.data_ptr(), g, wp, wb,
+                  _lib.stream_of(mz))
+        return mz, Sz
+
+    def _forward_prepare(self, ma: Tensor, Sa: Tensor):
+        """Checks the input, records what backward needs and allocates the output moments.
+
+        Returns (ma, Sa, mz, Sz, geometry) with the inputs channels-last; the caller
+        launches the forward."""
         if ma.dim() != 4 or ma.shape[1] != self.C_in:
             raise ValueError(f"Conv2D: expected (N, {self.C_in}, H, W), got {tuple(ma.shape)}")
         ma = _lib.check(_lib.channels_last(ma), "ma")
         Sa = _lib.check(_lib.channels_last(Sa), "Sa")
+        if Sa.shape != ma.shape:
+            raise ValueError(f"Conv2D: Sa {tuple(Sa.shape)} does not match ma {tuple(ma.shape)}")
         N, C, H, W = ma.shape
         self.input_shape = (N, C, H, W)
         g = self._geom(N, C, H, W)
@@ -66,12 +81,7 @@ class Conv2D(LearnableLayer):
         self.ma_in = ma
         mz = _lib.empty_cl(N, self.C_out, g.Ho, g.Wo, ma.device)
         Sz = _lib.empty_cl(N, self.C_out, g.Ho, g.Wo, ma.device)
-        ws = _lib.workspace(_lib.query("tagi_conv2d_fwd_ws_bytes", g), ma.device)
-        wp, wb = _lib.ws_args(ws)
-        _lib.call("tagi_conv2d_fwd", ma.data_ptr(), Sa.data_ptr(), self.mw.data_ptr(), self.Sw.data_ptr(),
-                  self.mb.data_ptr(), self.Sb.data_ptr(), mz.data_ptr(), Sz.data_ptr(), g, wp, wb,
-                  _lib.stream_of(ma))
-        return mz, Sz
+        return ma, Sa, mz, Sz, g
 
     def backward(self, delta_mz: Tensor, delta_Sz: Tensor) -> tuple[Tensor, Tensor]:
         return self._backward(delta_mz, delta_Sz, True)

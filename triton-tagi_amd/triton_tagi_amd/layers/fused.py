@@ -8,6 +8,8 @@ in how often activations cross HBM:
   runs as two passes over the ReLU input: the first forms the batch statistics of the
   rectified moments (and the ReLU Jacobian), the second recomputes the rectified moments
   and normalises them. The ReLU output is never written.
+* When a Conv2D produces that ReLU input, the first pass is the convolution's own GEMM
+  epilogue (conv2d.py:254-309): the output moments are not read back for the statistics.
 * The residual add that closes a block (resblock.py:380) is folded into that second pass.
 * Backward through BatchNorm2D and the ReLU in front of it (batchnorm2d.py:465-513,
   relu.py:152-169) is one pass.
@@ -69,31 +71,63 @@ def _add_in_place(src_m: Tensor, src_S: Tensor, dst_m: Tensor, dst_S: Tensor) ->
     add_shortcut(src_m, src_S, dst_m, dst_S)
 
 
+def _stats_args(bn: BatchNorm2D, C: int, dev) -> tuple[Tensor, Tensor, tuple]:
+    """Batch-statistic outputs and the running-stat arguments shared by the first passes."""
+    if not bn.training:
+        raise ValueError("relu_bn_forward: the BatchNorm2D must be in training mode")
+    if C != bn.num_features:
+        raise ValueError(f"BatchNorm2D: expected {bn.num_features} channels, got {C}")
+    bmean = torch.empty(C, device=dev, dtype=torch.float32)
+    bvar = torch.empty(C, device=dev, dtype=torch.float32)
+    tail = (_lib.check(bn.running_mean, "running_mean").data_ptr(),
+            _lib.check(bn.running_var, "running_var").data_ptr(), _lib.check(bn.mw, "mw").data_ptr())
+    return bmean, bvar, tail
+
+
 def relu_bn_forward(relu: ReLU, bn: BatchNorm2D, mz: Tensor, Sz: Tensor,
                     add: tuple[Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor]:
     """BatchNorm2D(ReLU(mz, Sz)) in training mode, plus ``add`` when given."""
-    if not bn.training:
-        raise ValueError("relu_bn_forward: the BatchNorm2D must be in training mode")
     mz = _lib.check(_lib.channels_last(mz), "mz")
     Sz = _lib.check(_lib.channels_last(Sz), "Sz")
     if mz.dim() != 4 or Sz.shape != mz.shape:
         raise ValueError(f"relu_bn_forward: expected matching (N, C, H, W) moments, got {tuple(mz.shape)}")
     N, C, H, W = mz.shape
-    if C != bn.num_features:
-        raise ValueError(f"BatchNorm2D: expected {bn.num_features} channels, got {C}")
-    HW = H * W
     dev = mz.device
-    st = _lib.stream_of(mz)
+    bmean, bvar, tail = _stats_args(bn, C, dev)
     J = torch.empty_like(mz)
-    bmean = torch.empty(C, device=dev, dtype=torch.float32)
-    bvar = torch.empty(C, device=dev, dtype=torch.float32)
     first = not bn._is_initialized
-    ws = _lib.workspace(_lib.query("tagi_bn_stats_ws_bytes", N, C, HW), dev)
+    ws = _lib.workspace(_lib.query("tagi_bn_stats_ws_bytes", N, C, H * W), dev)
     wp, wb = _lib.ws_args(ws)
     _lib.call("tagi_relu_bn_stats", mz.data_ptr(), Sz.data_ptr(), J.data_ptr(), bmean.data_ptr(), bvar.data_ptr(),
-              _lib.check(bn.running_mean, "running_mean").data_ptr(),
-              _lib.check(bn.running_var, "running_var").data_ptr(), _lib.check(bn.mw, "mw").data_ptr(),
-              N, C, HW, float(bn.momentum), float(bn.eps), int(first), int(bn.preserve_var), wp, wb, st)
+              *tail, N, C, H * W, float(bn.momentum), float(bn.eps), int(first), int(bn.preserve_var), wp, wb,
+              _lib.stream_of(mz))
+    return _relu_bn_apply(relu, bn, mz, Sz, J, bmean, bvar, add)
+
+
+def conv_relu_bn_forward(conv: Conv2D, relu: ReLU, bn: BatchNorm2D, ma: Tensor, Sa: Tensor,
+                         add: tuple[Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor]:
+    """BatchNorm2D(ReLU(Conv2D(ma, Sa))) in training mode, plus ``add`` when given."""
+    ma, Sa, mz, Sz, geom = conv._forward_prepare(ma, Sa)
+    N, C, H, W = mz.shape
+    dev = mz.device
+    bmean, bvar, tail = _stats_args(bn, C, dev)
+    J = torch.empty_like(mz)
+    first = not bn._is_initialized
+    ws = _lib.workspace(_lib.query("tagi_conv2d_fwd_relu_bn_stats_ws_bytes", geom), dev)
+    wp, wb = _lib.ws_args(ws)
+    _lib.call("tagi_conv2d_fwd_relu_bn_stats", ma.data_ptr(), Sa.data_ptr(), conv.mw.data_ptr(),
+              conv.Sw.data_ptr(), conv.mb.data_ptr(), conv.Sb.data_ptr(), mz.data_ptr(), Sz.data_ptr(), geom,
+              J.data_ptr(), bmean.data_ptr(), bvar.data_ptr(), *tail, float(bn.momentum), float(bn.eps), int(first),
+              int(bn.preserve_var), wp, wb, _lib.stream_of(mz))
+    return _relu_bn_apply(relu, bn, mz, Sz, J, bmean, bvar, add)
+
+
+def _relu_bn_apply(relu: ReLU, bn: BatchNorm2D, mz: Tensor, Sz: Tensor, J: Tensor, bmean: Tensor, bvar: Tensor,
+                   add: tuple[Tensor, Tensor] | None) -> tuple[Tensor, Tensor]:
+    """Second pass: normalise the rectified moments (batch statistics already formed)."""
+    N, C, H, W = mz.shape
+    HW = H * W
+    st = _lib.stream_of(mz)
     bn._is_initialized = True
     relu.J = J
     am = aS = None
@@ -148,6 +182,11 @@ def _fusable_forward(layer, nxt, mu: Tensor) -> bool:
     return isinstance(layer, ReLU) and isinstance(nxt, BatchNorm2D) and nxt.training and mu.dim() == 4
 
 
+def _fusable_conv_forward(layers, i: int, mu: Tensor) -> bool:
+    return (i + 2 < len(layers) and isinstance(layers[i], Conv2D) and mu.dim() == 4
+            and _fusable_forward(layers[i + 1], layers[i + 2], mu))
+
+
 def _fusable_backward(layer, prev) -> bool:
     return (isinstance(layer, BatchNorm2D) and isinstance(prev, ReLU) and prev.J is not None
             and layer.m_hat is not None and tuple(prev.J.shape) == tuple(layer.m_hat.shape))
@@ -160,7 +199,13 @@ def forward_chain(layers, mu: Tensor, var: Tensor,
     while i < n:
         layer = layers[i]
         nxt = layers[i + 1] if i + 1 < n else None
-        if _fusable_forward(layer, nxt, mu):
+        if _fusable_conv_forward(layers, i, mu):
+            last = i + 3 == n
+            mu, var = conv_relu_bn_forward(layer, nxt, layers[i + 2], mu, var, add if last else None)
+            if last:
+                add = None
+            i += 3
+        elif _fusable_forward(layer, nxt, mu):
             last = i + 2 == n
             mu, var = relu_bn_forward(layer, nxt, mu, var, add if last else None)
             if last:
