@@ -51,7 +51,7 @@ enum {
   TAGI_FAM_BN_STATS = 10, TAGI_FAM_BN_FWD = 11, TAGI_FAM_BN_BWD = 12, TAGI_FAM_UPDATE = 13,
   TAGI_FAM_INNOVATION = 14, TAGI_FAM_ADD = 15, TAGI_FAM_AVGPOOL = 16, TAGI_FAM_JACOBIAN = 17,
   TAGI_FAM_RMSNORM = 18, TAGI_FAM_EMBEDDING = 19, TAGI_FAM_PE = 20, TAGI_FAM_SPLITK_REDUCE = 21,
-  TAGI_FAM_COUNT = 22
+  TAGI_FAM_MAXPOOL = 22, TAGI_FAM_LAYERNORM = 23, TAGI_FAM_SOFTPLUS = 24, TAGI_FAM_COUNT = 25
 };
 
 /* Ceiling probe (no counterpart in the reference; measurement only): `blocks` blocks of
@@ -370,6 +370,65 @@ int64_t tagi_embedding_bwd_ws_bytes(int64_t n_tokens, int64_t V, int64_t D);
 /* Sinusoidal positional encoding add (positional_encoding.py:62): out = ma + pe[:S]. */
 int tagi_pe_add(const float* ma, const float* pe, float* out, int64_t B, int64_t S, int64_t E,
                 tagi_stream_t stream);
+
+/* ------------------------------------------------- output heads and further layers */
+/* Sparse (hierarchical-softmax) innovation. Replaces compute_innovation_with_indices
+ * (observation.py:171-224). ma, Sa, dm, dS: (rows, n_out); y_obs, var_obs: (rows, n_obs)
+ * fp32; idx: (rows, n_obs) int32, 1-indexed nodes. dm/dS are overwritten: zero except at
+ * the selected nodes, where (y - ma)/(Sa + v) and -1/(Sa + v) are added per bit (a node
+ * selected twice receives both). Indices outside [1, n_out] select nothing. */
+int tagi_innovation_indexed(const float* ma, const float* Sa, const float* y_obs, const float* var_obs,
+                            const int32_t* idx, float* dm, float* dS, int64_t rows, int64_t n_out,
+                            int64_t n_obs, tagi_stream_t stream);
+/* The same from integer class labels: row b uses the class tables obs/idx (n_classes, n_obs)
+ * at labels[b] and the noise variance sigma_v2. Replaces labels_to_hrc + full_like +
+ * compute_innovation_with_indices inside Sequential.step_hrc (network.py:157-224,
+ * hrc_softmax.py:131-150). A label outside [0, n_classes) makes its row of dm/dS NaN. */
+int tagi_hrc_innovation(const float* ma, const float* Sa, const int64_t* labels, const float* obs,
+                        const int32_t* idx, float sigma_v2, float* dm, float* dS, int64_t rows,
+                        int64_t n_out, int64_t n_obs, int64_t n_classes, tagi_stream_t stream);
+/* Class probabilities of a hierarchical-softmax output (hrc_softmax.py:164-208):
+ * probs[b, r] = prod_c (obs[r,c] > 0 ? P : 1 - P), P = Phi(ma/sqrt(1/alpha^2 + Sa)) at node
+ * idx[r,c]-1 of row b. probs: (rows, n_classes). pred (optional, may be NULL): int64 (rows,)
+ * first index of the largest probability (get_predicted_labels, hrc_softmax.py:211-231). */
+int tagi_hrc_class_probs(const float* ma, const float* Sa, const float* obs, const int32_t* idx,
+                         float alpha, float* probs, int64_t* pred, int64_t rows, int64_t n_out,
+                         int64_t n_obs, int64_t n_classes, tagi_stream_t stream);
+/* Heteroscedastic (TAGI-V) innovation: y has n elements; mu/var/dm/dS have 2n, interleaved
+ * (mean, noise-variance) pairs. Replaces _output_innovation_kernel_heteros
+ * (observation.py:49-111) and the 2x-wide dispatch of compute_innovation (:137). */
+int tagi_innovation_heteros(const float* y, const float* mu, const float* var, float* dm,
+                            float* dS, int64_t n, tagi_stream_t stream);
+/* EvenSoftplus forward (even_softplus.py:38-124): softplus moments at odd flat positions,
+ * identity at even ones; J = sigmoid(mu) or 1. The backward pass is tagi_jacobian_bwd. */
+int tagi_even_softplus_fwd(const float* mz, const float* Sz, float* ma, float* Sa, float* J,
+                           int64_t n, tagi_stream_t stream);
+/* MaxPool2D, hard argmax of the means (maxpool2d.py:62-126). Tensors (N, C, H, W), all
+ * NCHW or all channels-last (channels_last != 0); output (N, C, Ho, Wo), Ho = (H + 2 pad -
+ * k)/stride + 1; pool_idx int32 (output layout) holds h*W + w of each pick. Needs
+ * 0 <= pad <= k/2. */
+int tagi_maxpool2d_fwd(const float* ma, const float* Sa, float* mz, float* Sz, int32_t* pool_idx,
+                       int64_t N, int64_t C, int64_t H, int64_t W, int64_t k, int64_t stride,
+                       int64_t pad, int channels_last, tagi_stream_t stream);
+/* MaxPool2D deltas: each input position receives the sum of the output deltas whose window
+ * picked it (scatter_add at maxpool2d.py:100-126); dma/dSa (N, C, H, W) are overwritten. */
+int tagi_maxpool2d_bwd(const float* dmz, const float* dSz, const int32_t* pool_idx, float* dma,
+                       float* dSa, int64_t N, int64_t C, int64_t H, int64_t W, int64_t k,
+                       int64_t stride, int64_t pad, int channels_last, tagi_stream_t stream);
+/* LayerNorm forward over the last dimension (layernorm.py:101-135): rows x D; writes the
+ * per-row mean mu_ra and Bessel-corrected variance var_ra (rows,) used by the backward. */
+int tagi_layernorm_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw,
+                       const float* mb, const float* Sb, float* mz, float* Sz, float* mu_ra,
+                       float* var_ra, int64_t rows, int64_t D, float eps, tagi_stream_t stream);
+/* LayerNorm deltas (layernorm.py:140-175): dma = J dmz, dSa = J^2 dSz with J = mw/sqrt(var_ra +
+ * eps); dmw/dSw/dmb/dSb (D,) overwritten with the parameter deltas. ws from
+ * tagi_layernorm_bwd_ws_bytes (deterministic two-stage column sums). */
+int tagi_layernorm_bwd(const float* dmz, const float* dSz, const float* ma, const float* mu_ra,
+                       const float* var_ra, const float* mw, const float* Sw, const float* Sb,
+                       float* dma, float* dSa, float* dmw, float* dSw, float* dmb, float* dSb,
+                       int64_t rows, int64_t D, float eps, float* ws, int64_t ws_bytes,
+                       tagi_stream_t stream);
+int64_t tagi_layernorm_bwd_ws_bytes(int64_t rows, int64_t D);
 
 #ifdef __cplusplus
 }

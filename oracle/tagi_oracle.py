@@ -571,6 +571,237 @@ class ONet:
                 layer.update(cap)
         return mu, var
 
+    def step_hrc(self, x, labels, n_classes, sigma_v):
+        """network.py:157-224: sparse innovation on each label's tree path."""
+        mu, var = self.forward(x)
+        obs, idx, L, _ = hrc_tree(n_classes)
+        width = mu.shape[-1]
+        lab = labels.reshape(-1).long()
+        y_obs, y_idx = obs[lab], idx[lab]
+        dm, dS = innovation_indexed(mu.reshape(-1, width), var.reshape(-1, width), y_obs,
+                                    torch.full_like(y_obs, sigma_v**2), y_idx)
+        dm, dS = dm.reshape(mu.shape), dS.reshape(mu.shape)
+        for layer in reversed(self.layers):
+            dm, dS = layer.backward(dm, dS)
+        cap = get_cap_factor(x.shape[0])
+        for layer in self.layers:
+            if layer.learnable:
+                layer.update(cap)
+        return mu, var
+
+    def step_heteros(self, x, y):
+        """network.py:119-152 with the heteroscedastic innovation (observation.py:137)."""
+        mu, var = self.forward(x)
+        dm, dS = heteros_innovation(y, mu, var)
+        for layer in reversed(self.layers):
+            dm, dS = layer.backward(dm, dS)
+        cap = get_cap_factor(x.shape[0])
+        for layer in self.layers:
+            if layer.learnable:
+                layer.update(cap)
+        return mu, var
+
+
+# ================================================================ output heads (HRC)
+def hrc_tree(n_classes):
+    """hrc_softmax.py:73-128 (cuTAGI class_to_obs): (obs, idx, n_obs, len).
+
+    Bits of class r are its binary code, MSB first; bit c is observed as (-1)^bit at the
+    node numbered 1 + (nodes on the levels above) + (value of the c leading bits).
+    """
+    L = math.ceil(math.log2(n_classes))
+    per_level = [n_classes]
+    for _ in range(L):
+        per_level.insert(0, math.ceil(per_level[0] / 2))
+    offset = [1]
+    for d in range(1, L):
+        offset.append(offset[-1] + per_level[d - 1])
+    obs = [[0.0] * L for _ in range(n_classes)]
+    idx = [[0] * L for _ in range(n_classes)]
+    for r in range(n_classes):
+        code = format(r, f"0{L}b")
+        for c in range(L):
+            obs[r][c] = 1.0 if code[c] == "0" else -1.0
+            idx[r][c] = offset[c] + (int(code[:c], 2) if c else 0)
+    return torch.tensor(obs, dtype=DT), torch.tensor(idx, dtype=torch.int64), L, max(max(row) for row in idx)
+
+
+def innovation_indexed(ma, Sa, y_obs, var_obs, idx):
+    """update/observation.py:171-224: dense rule at node idx-1 of each row, zeros elsewhere
+    (index_add, so a node selected twice receives both terms)."""
+    dm, dS = torch.zeros_like(ma), torch.zeros_like(Sa)
+    for b in range(ma.shape[0]):
+        for c in range(idx.shape[1]):
+            j = int(idx[b, c]) - 1
+            if j < 0 or j >= ma.shape[1]:
+                continue
+            den = Sa[b, j] + var_obs[b, c]
+            dm[b, j] += (y_obs[b, c] - ma[b, j]) / den
+            dS[b, j] += -1.0 / den
+    return dm, dS
+
+
+def hrc_class_probs(ma, Sa, obs, idx, alpha=3.0):
+    """hrc_softmax.py:164-208: product along each class path of Phi(mu/sqrt(1/alpha^2+S))
+    (bit +1) or its complement (bit -1)."""
+    P = torch.special.ndtr(ma / torch.sqrt((1.0 / alpha) ** 2 + Sa))
+    node = P[:, idx - 1]  # (B, n_classes, L)
+    f = torch.where(obs > 0, node, 1.0 - node)
+    return f.prod(dim=2)
+
+
+# ===================================================== heteroscedastic output (TAGI-V)
+def hetero_noise_prior(mu_v2b, var_v2b):
+    """observation.py:82-86: moments of V^2 for V ~ N(0, V2b), V2b ~ N(mu, var):
+    E[V^2] = mu, Var[V^2] = 3 var + 2 mu^2."""
+    return mu_v2b, 3.0 * var_v2b + 2.0 * mu_v2b * mu_v2b
+
+
+def hetero_v_posterior(y, mu_a, var_a, mu_v2):
+    """observation.py:88-98: Y = A + V, A ~ N(mu_a, var_a), V ~ N(0, mu_v2); moments of
+    V | Y = y (and the innovation of the mean output)."""
+    var_sum = var_a + mu_v2
+    m = mu_v2 / var_sum * (y - mu_a)
+    v = mu_v2 - mu_v2 / var_sum * mu_v2
+    return m, v
+
+
+def gaussian_square_moments(m, v):
+    """observation.py:100-102: E[X^2], Var[X^2] of X ~ N(m, v)."""
+    return m * m + v, 2.0 * v * v + 4.0 * v * m * m
+
+
+def rts_update(mu_x, var_x, cov_xw, mu_w, var_w, mu_w_post, var_w_post):
+    """observation.py:104-107: move X by the change of the linked W (gain cov/var_w)."""
+    k = cov_xw / var_w
+    return mu_x + k * (mu_w_post - mu_w), var_x + k * k * (var_w_post - var_w)
+
+
+def heteros_innovation(y, mu, var):
+    """observation.py:49-111: interleaved (mean, noise) output pairs; returns deltas
+    shaped like mu."""
+    mu_a, mu_v2b = mu[..., 0::2], mu[..., 1::2]
+    var_a, var_v2b = var[..., 0::2], var[..., 1::2]
+    mu_v2, var_v2 = hetero_noise_prior(mu_v2b, var_v2b)
+    var_sum = var_a + mu_v2
+    d_mu, d_var = (y - mu_a) / var_sum, -1.0 / var_sum
+    mv, vv = hetero_v_posterior(y, mu_a, var_a, mu_v2)
+    m2, v2 = gaussian_square_moments(mv, vv)
+    mb_post, vb_post = rts_update(mu_v2b, var_v2b, var_v2b, mu_v2, var_v2, m2, v2)
+    dm, dS = torch.empty_like(mu), torch.empty_like(var)
+    dm[..., 0::2], dS[..., 0::2] = d_mu, d_var
+    dm[..., 1::2], dS[..., 1::2] = mb_post - mu_v2b, vb_post - var_v2b
+    return dm, dS
+
+
+def even_softplus(mz, Sz):
+    """layers/even_softplus.py:38-90: second-order softplus moments at odd flat positions."""
+    m, S = mz.reshape(-1), Sz.reshape(-1)
+    sig = torch.sigmoid(m)
+    sp = F.softplus(m)
+    mu = torch.clamp(sp + 0.5 * S * sig * (1.0 - sig), min=1e-9)
+    var = torch.clamp(sig * sig * S, min=1e-9)
+    odd = (torch.arange(m.numel()) % 2) == 1
+    ma = torch.where(odd, mu, m)
+    Sa = torch.where(odd, var, S)
+    J = torch.where(odd, sig, torch.ones_like(m))
+    return ma.reshape(mz.shape), Sa.reshape(mz.shape), J.reshape(mz.shape)
+
+
+class OEvenSoftplus(OLayer):
+    """layers/even_softplus.py:157-190."""
+
+    def forward(self, mz, Sz):
+        ma, Sa, self.J = even_softplus(mz, Sz)
+        return ma, Sa
+
+    def backward(self, dm, dS):
+        return dm * self.J, dS * self.J * self.J
+
+
+class OMaxPool2D(OLayer):
+    """layers/maxpool2d.py:62-126: window loops; first largest mean wins, a NaN replaces
+    the pick; backward adds each delta at its pick."""
+
+    def __init__(self, k, stride, padding):
+        self.k, self.s, self.p = k, stride, padding
+
+    def forward(self, ma, Sa):
+        N, C, H, W = ma.shape
+        k, s, p = self.k, self.s, self.p
+        Ho, Wo = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+        self.shape = (N, C, H, W)
+        flat_m, flat_S = ma.reshape(N, C, H * W), Sa.reshape(N, C, H * W)
+        idx = torch.empty(N, C, Ho, Wo, dtype=torch.int64)
+        for ho in range(Ho):
+            for wo in range(Wo):
+                h0, w0 = ho * s - p, wo * s - p
+                cand = [(h, w) for h in range(max(h0, 0), min(h0 + k, H)) for w in range(max(w0, 0), min(w0 + k, W))]
+                best = torch.full((N, C), -math.inf, dtype=ma.dtype)
+                pick = torch.full((N, C), cand[0][0] * W + cand[0][1], dtype=torch.int64)
+                for h, w in cand:
+                    v = ma[:, :, h, w]
+                    take = (v > best) | torch.isnan(v)
+                    best = torch.where(take, v, best)
+                    pick = torch.where(take, torch.full_like(pick, h * W + w), pick)
+                idx[:, :, ho, wo] = pick
+        self.idx = idx
+        g = idx.reshape(N, C, -1)
+        return flat_m.gather(2, g).reshape(N, C, Ho, Wo), flat_S.gather(2, g).reshape(N, C, Ho, Wo)
+
+    def backward(self, dm, dS):
+        N, C, H, W = self.shape
+        g = self.idx.reshape(N, C, -1)
+        om = torch.zeros(N, C, H * W, dtype=dm.dtype).scatter_add_(2, g, dm.reshape(N, C, -1))
+        oS = torch.zeros(N, C, H * W, dtype=dS.dtype).scatter_add_(2, g, dS.reshape(N, C, -1))
+        return om.reshape(N, C, H, W), oS.reshape(N, C, H, W)
+
+
+def layernorm_stats(ma, Sa):
+    """layers/layernorm.py:117-121: per-row mean, (sum of squared deviations + sum S)/(D-1)."""
+    D = ma.shape[-1]
+    mu = ma.mean(dim=-1, keepdim=True)
+    var = (((ma - mu) ** 2).sum(dim=-1, keepdim=True) + Sa.sum(dim=-1, keepdim=True)) / (D - 1)
+    return mu, var
+
+
+class OLayerNorm(OLayer):
+    """layers/layernorm.py:101-175."""
+
+    learnable = True
+
+    def __init__(self, mw, Sw, mb, Sb, eps, has_bias=True):
+        self.mw, self.Sw, self.mb, self.Sb, self.eps, self.has_bias = mw, Sw, mb, Sb, eps, has_bias
+
+    def forward(self, ma, Sa):
+        D = self.mw.shape[0]
+        self.shape = ma.shape
+        m, S = ma.reshape(-1, D), Sa.reshape(-1, D)
+        self.mu_ra, self.var_ra = layernorm_stats(m, S)
+        inv = 1.0 / torch.sqrt(self.var_ra + self.eps)
+        d = m - self.mu_ra
+        self.m_in, self.inv = m, inv
+        mz = inv * d * self.mw + self.mb
+        Sz = inv * inv * (S * (self.mw * self.mw + self.Sw) + self.Sw * d * d) + self.Sb
+        return mz.reshape(self.shape), Sz.reshape(self.shape)
+
+    def backward(self, dmz, dSz):
+        D = self.mw.shape[0]
+        dm, dS = dmz.reshape(-1, D), dSz.reshape(-1, D)
+        J = self.inv * self.mw
+        h = self.inv * (self.m_in - self.mu_ra)
+        self.delta_mw = self.Sw * (h * dm).sum(0)
+        self.delta_Sw = self.Sw * self.Sw * (h * h * dS).sum(0)
+        self.delta_mb = self.Sb * dm.sum(0)
+        self.delta_Sb = self.Sb * self.Sb * dS.sum(0)
+        return (J * dm).reshape(dmz.shape), (J * J * dS).reshape(dSz.shape)
+
+    def param_groups(self):
+        g = [(self, "mw", "Sw", "delta_mw", "delta_Sw")]
+        if self.has_bias:
+            g.append((self, "mb", "Sb", "delta_mb", "delta_Sb"))
+        return g
+
 
 # ========================================================================== mirror
 def mirror(layer, dtype=DT):
@@ -605,6 +836,12 @@ def mirror(layer, dtype=DT):
         return OEmbedding(c(layer.mw), c(layer.Sw), layer.padding_idx)
     if name == "PositionalEncoding":
         return OPositionalEncoding(c(layer.pe_cache))
+    if name == "MaxPool2D":
+        return OMaxPool2D(layer.kernel_size, layer.stride, layer.padding)
+    if name == "LayerNorm":
+        return OLayerNorm(c(layer.mw), c(layer.Sw), c(layer.mb), c(layer.Sb), layer.eps, layer.has_bias)
+    if name == "EvenSoftplus":
+        return OEvenSoftplus()
     raise TypeError(f"no oracle for layer type {name}")
 
 

@@ -53,7 +53,10 @@ enum Family {
   FAM_EMBEDDING = 19,
   FAM_PE = 20,
   FAM_SPLITK_REDUCE = 21,
-  FAM_COUNT = 22
+  FAM_MAXPOOL = 22,
+  FAM_LAYERNORM = 23,
+  FAM_SOFTPLUS = 24,
+  FAM_COUNT = 25
 };
 
 // Record a start event for `fam` on `s` if the timer is on for that family.

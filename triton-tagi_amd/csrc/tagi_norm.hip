@@ -493,6 +493,199 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_finalize_kernel(const float* 
   dSw[c] = sums[1] * sw * sw;
 }
 
+// --------------------------------------------------------------------- LayerNorm
+// Per-row statistics over the features (layernorm.py:101-135):
+//   mu = mean(m),  var = (sum (m - mu)^2 + sum S) / (D - 1),  inv = 1/sqrt(var + eps)
+//   mz = inv (m - mu) g + b,   Sz = inv^2 (S (g^2 + Sg) + Sg (m - mu)^2) + Sb
+// The mean is formed first and the squared deviations are summed from it, as written.
+// One wavefront per row with the row in registers for D <= 1024; one block per row,
+// re-reading the row, above that.
+template <int EPT>
+__global__ void __launch_bounds__(256) layernorm_fwd_kernel(
+    const float* __restrict__ ma, const float* __restrict__ Sa, const float* __restrict__ mw,
+    const float* __restrict__ Sw, const float* __restrict__ mb, const float* __restrict__ Sb, float* __restrict__ mz,
+    float* __restrict__ Sz, float* __restrict__ mu_ra, float* __restrict__ var_ra, int64_t rows, int D, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* pm = ma + row * D;
+  const float* ps = Sa + row * D;
+  float m[EPT], s[EPT];
+  float sm = 0.f, ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int c = lane + 64 * e;
+    m[e] = c < D ? pm[c] : 0.f;
+    s[e] = c < D ? ps[c] : 0.f;
+    sm += m[e];
+    ss += s[e];
+  }
+  const float mu = wave_reduce(sm) / (float)D;
+  float sq = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const float d = m[e] - mu;
+    if (lane + 64 * e < D) sq += d * d;
+  }
+  const float var = (wave_reduce(sq) + wave_reduce(ss)) / (float)(D - 1);
+  const float inv = 1.0f / sqrtf(var + eps);
+  if (lane == 0) {
+    mu_ra[row] = mu;
+    var_ra[row] = var;
+  }
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int c = lane + 64 * e;
+    if (c >= D) continue;
+    const float g = mw[c], sg = Sw[c], d = m[e] - mu;
+    mz[row * D + c] = inv * d * g + mb[c];
+    Sz[row * D + c] = (inv * inv) * (s[e] * (g * g + sg) + sg * d * d) + Sb[c];
+  }
+}
+
+__device__ __forceinline__ float block_sum256(float v, float* sh) {
+  v = wave_reduce(v);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  __syncthreads();
+  return r;
+}
+
+__global__ void __launch_bounds__(256) layernorm_fwd_row_kernel(
+    const float* __restrict__ ma, const float* __restrict__ Sa, const float* __restrict__ mw,
+    const float* __restrict__ Sw, const float* __restrict__ mb, const float* __restrict__ Sb, float* __restrict__ mz,
+    float* __restrict__ Sz, float* __restrict__ mu_ra, float* __restrict__ var_ra, int D, float eps) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const float* pm = ma + row * D;
+  const float* ps = Sa + row * D;
+  float sm = 0.f, ss = 0.f;
+  for (int c = threadIdx.x; c < D; c += 256) {
+    sm += pm[c];
+    ss += ps[c];
+  }
+  const float mu = block_sum256(sm, sh) / (float)D;
+  float sq = 0.f;
+  for (int c = threadIdx.x; c < D; c += 256) {
+    const float d = pm[c] - mu;
+    sq += d * d;
+  }
+  const float var = (block_sum256(sq, sh) + block_sum256(ss, sh)) / (float)(D - 1);
+  const float inv = 1.0f / sqrtf(var + eps);
+  if (threadIdx.x == 0) {
+    mu_ra[row] = mu;
+    var_ra[row] = var;
+  }
+  for (int c = threadIdx.x; c < D; c += 256) {
+    const float g = mw[c], sg = Sw[c], d = pm[c] - mu;
+    mz[row * D + c] = inv * d * g + mb[c];
+    Sz[row * D + c] = (inv * inv) * (ps[c] * (g * g + sg) + sg * d * d) + Sb[c];
+  }
+}
+
+// Backward (layernorm.py:140-175), diagonal Jacobian J = inv g per element:
+//   delta_m = J delta_mz, delta_S = J^2 delta_Sz, and four per-column sums with
+//   h = inv (m - mu): sum h delta_mz, sum h^2 delta_Sz, sum delta_mz, sum delta_Sz,
+// scaled by Sg, Sg^2, Sb, Sb^2 in the finalize kernel. Partials as for RMSNorm.
+__global__ void __launch_bounds__(256) layernorm_bwd_partial_vec_kernel(
+    const float* __restrict__ dmz, const float* __restrict__ dSz, const float* __restrict__ ma,
+    const float* __restrict__ mu_ra, const float* __restrict__ var_ra, const float* __restrict__ mw,
+    float* __restrict__ dma, float* __restrict__ dSa, float* __restrict__ ws, int64_t rows, int D, int nblk,
+    float eps) {
+  __shared__ float red[256 * 4 * 4];
+  const int64_t r0 = rows * blockIdx.x / nblk, r1 = rows * (blockIdx.x + 1) / nblk;
+  const int W = D / (int)gridDim.y, c0 = (int)blockIdx.y * W;  // this block's column chunk
+  const int cq = W >> 2, rpi = 256 / cq;
+  const int t = threadIdx.x, c4 = t % cq, rr = t / cq;
+  const float4 w4 = *reinterpret_cast<const float4*>(mw + c0 + 4 * c4);
+  const float w[4] = {w4.x, w4.y, w4.z, w4.w};
+  float acc[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[j][q] = 0.f;
+#pragma unroll 2
+  for (int64_t row = r0 + rr; row < r1; row += rpi) {
+    const float mu = mu_ra[row];
+    const float inv = 1.0f / sqrtf(var_ra[row] + eps);
+    const int64_t off = row * D + c0 + 4 * c4;
+    const float4 d4 = *reinterpret_cast<const float4*>(dmz + off);
+    const float4 s4 = *reinterpret_cast<const float4*>(dSz + off);
+    const float4 m4 = *reinterpret_cast<const float4*>(ma + off);
+    const float dm[4] = {d4.x, d4.y, d4.z, d4.w}, ds[4] = {s4.x, s4.y, s4.z, s4.w}, m[4] = {m4.x, m4.y, m4.z, m4.w};
+    float o0[4], o1[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float k = inv * w[j];
+      const float h = inv * (m[j] - mu);
+      o0[j] = k * dm[j];
+      o1[j] = k * k * ds[j];
+      acc[j][0] += h * dm[j];
+      acc[j][1] += h * h * ds[j];
+      acc[j][2] += dm[j];
+      acc[j][3] += ds[j];
+    }
+    *reinterpret_cast<float4*>(dma + off) = make_float4(o0[0], o0[1], o0[2], o0[3]);
+    *reinterpret_cast<float4*>(dSa + off) = make_float4(o1[0], o1[1], o1[2], o1[3]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[(t * 4 + j) * 4 + q] = acc[j][q];
+  __syncthreads();
+  for (int cl = t; cl < W; cl += 256) {
+    const int g4 = cl >> 2, j = cl & 3;
+    for (int q = 0; q < 4; ++q) {
+      float sum = 0.f;
+      for (int r = 0; r < rpi; ++r) sum += red[((r * cq + g4) * 4 + j) * 4 + q];
+      ws[((int64_t)q * D + c0 + cl) * nblk + blockIdx.x] = sum;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) layernorm_bwd_partial_kernel(
+    const float* __restrict__ dmz, const float* __restrict__ dSz, const float* __restrict__ ma,
+    const float* __restrict__ mu_ra, const float* __restrict__ var_ra, const float* __restrict__ mw,
+    float* __restrict__ dma, float* __restrict__ dSa, float* __restrict__ ws, int64_t rows, int D, int nblk,
+    float eps) {
+  const int64_t r0 = rows * blockIdx.x / nblk, r1 = rows * (blockIdx.x + 1) / nblk;
+  for (int c = threadIdx.x; c < D; c += blockDim.x) {
+    const float w = mw[c];
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t r = r0; r < r1; ++r) {
+      const float inv = 1.0f / sqrtf(var_ra[r] + eps);
+      const int64_t i = r * D + c;
+      const float dm = dmz[i], ds = dSz[i], h = inv * (ma[i] - mu_ra[r]);
+      const float k = inv * w;
+      dma[i] = k * dm;
+      dSa[i] = k * k * ds;
+      acc[0] += h * dm;
+      acc[1] += h * h * ds;
+      acc[2] += dm;
+      acc[3] += ds;
+    }
+    for (int q = 0; q < 4; ++q) ws[((int64_t)q * D + c) * nblk + blockIdx.x] = acc[q];
+  }
+}
+
+__global__ void __launch_bounds__(256) layernorm_bwd_finalize_kernel(const float* __restrict__ ws,
+                                                                     const float* __restrict__ Sw,
+                                                                     const float* __restrict__ Sb,
+                                                                     float* __restrict__ dmw, float* __restrict__ dSw,
+                                                                     float* __restrict__ dmb, float* __restrict__ dSb,
+                                                                     int D, int nblk) {
+  const int c = blockIdx.x;
+  float sums[4];
+  channel_sums<4>(ws, D, c, nblk, sums);
+  if (threadIdx.x != 0) return;
+  const float sw = Sw[c], sb = Sb[c];
+  dmw[c] = sw * sums[0];
+  dSw[c] = sw * sw * sums[1];
+  dmb[c] = sb * sums[2];
+  dSb[c] = sb * sb * sums[3];
+}
+
 // ------------------------------------------------------------------- Embedding
 __device__ __forceinline__ int64_t token_id(float t) { return (int64_t)t; }  // truncation, as .long()
 
@@ -909,6 +1102,64 @@ extern "C" int tagi_rmsnorm_bwd(const float* dmz, const float* dSz, const float*
   if (rc) return rc;
   hipLaunchKernelGGL(rmsnorm_bwd_finalize_kernel, dim3((unsigned)D), dim3(256), 0, s, (const float*)ws, Sw, dmw, dSw,
                      (int)D, nblk);
+  return check_launch(what);
+}
+
+extern "C" int tagi_layernorm_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw, const float* mb,
+                                  const float* Sb, float* mz, float* Sz, float* mu_ra, float* var_ra, int64_t rows,
+                                  int64_t D, float eps, tagi_stream_t stream) {
+  const char* what = "tagi_layernorm_fwd";
+  TAGI_REQUIRE(rows >= 0 && D > 0 && D < (1ll << 31), "%s: bad sizes", what);
+  if (rows == 0) return TAGI_OK;
+  TAGI_REQUIRE(ma && Sa && mw && Sw && mb && Sb && mz && Sz && mu_ra && var_ra, "%s: null pointer", what);
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_LAYERNORM, s, 0.0, 16.0 * rows * D + 8.0 * rows);
+  const unsigned blocks = (unsigned)cdiv(rows, 4);
+  if (D <= 64)
+    hipLaunchKernelGGL(layernorm_fwd_kernel<1>, dim3(blocks), dim3(256), 0, s, ma, Sa, mw, Sw, mb, Sb, mz, Sz, mu_ra,
+                       var_ra, rows, (int)D, eps);
+  else if (D <= 256)
+    hipLaunchKernelGGL(layernorm_fwd_kernel<4>, dim3(blocks), dim3(256), 0, s, ma, Sa, mw, Sw, mb, Sb, mz, Sz, mu_ra,
+                       var_ra, rows, (int)D, eps);
+  else if (D <= 1024)
+    hipLaunchKernelGGL(layernorm_fwd_kernel<16>, dim3(blocks), dim3(256), 0, s, ma, Sa, mw, Sw, mb, Sb, mz, Sz,
+                       mu_ra, var_ra, rows, (int)D, eps);
+  else {
+    TAGI_REQUIRE(rows < (1ll << 31), "%s: more than 2^31 rows", what);
+    hipLaunchKernelGGL(layernorm_fwd_row_kernel, dim3((unsigned)rows), dim3(256), 0, s, ma, Sa, mw, Sw, mb, Sb, mz, Sz,
+                       mu_ra, var_ra, (int)D, eps);
+  }
+  return check_launch(what);
+}
+
+extern "C" int64_t tagi_layernorm_bwd_ws_bytes(int64_t rows, int64_t D) {
+  if (rows <= 0 || D <= 0) return 0;
+  return (int64_t)red_rows(rows) * 4 * D * (int64_t)sizeof(float);
+}
+
+extern "C" int tagi_layernorm_bwd(const float* dmz, const float* dSz, const float* ma, const float* mu_ra,
+                                  const float* var_ra, const float* mw, const float* Sw, const float* Sb, float* dma,
+                                  float* dSa, float* dmw, float* dSw, float* dmb, float* dSb, int64_t rows, int64_t D,
+                                  float eps, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+  const char* what = "tagi_layernorm_bwd";
+  TAGI_REQUIRE(dmz && dSz && ma && mu_ra && var_ra && mw && Sw && Sb && dma && dSa && dmw && dSw && dmb && dSb && ws,
+               "%s: null pointer", what);
+  TAGI_REQUIRE(rows > 0 && D > 0 && D < (1ll << 31), "%s: bad sizes", what);
+  TAGI_REQUIRE(ws_bytes >= tagi_layernorm_bwd_ws_bytes(rows, D), "%s: workspace too small", what);
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_LAYERNORM, s, 0.0, 20.0 * rows * D + 8.0 * rows);
+  const int nblk = red_rows(rows);
+  const bool vec = bn_vec(D) && al16p(dmz) && al16p(dSz) && al16p(ma) && al16p(mw) && al16p(dma) && al16p(dSa);
+  if (vec)
+    hipLaunchKernelGGL(layernorm_bwd_partial_vec_kernel, dim3((unsigned)nblk, red_chunks(nblk, D, true)), dim3(256),
+                       0, s, dmz, dSz, ma, mu_ra, var_ra, mw, dma, dSa, ws, rows, (int)D, nblk, eps);
+  else
+    hipLaunchKernelGGL(layernorm_bwd_partial_kernel, dim3((unsigned)nblk), dim3(256), 0, s, dmz, dSz, ma, mu_ra,
+                       var_ra, mw, dma, dSa, ws, rows, (int)D, nblk, eps);
+  int rc = check_launch(what);
+  if (rc) return rc;
+  hipLaunchKernelGGL(layernorm_bwd_finalize_kernel, dim3((unsigned)D), dim3(256), 0, s, (const float*)ws, Sw, Sb, dmw,
+                     dSw, dmb, dSb, (int)D, nblk);
   return check_launch(what);
 }
 

@@ -22,7 +22,7 @@ FAMILIES = [
     "conv_fwd", "conv_bwd_delta", "conv_wgrad", "linear_fwd", "linear_bwd_delta",
     "linear_wgrad", "bmm_fwd", "bmm_shared", "relu", "remax", "bn_stats", "bn_fwd",
     "bn_bwd", "update", "innovation", "add", "avgpool", "jacobian", "rmsnorm",
-    "embedding", "pe", "splitk_reduce",
+    "embedding", "pe", "splitk_reduce", "maxpool", "layernorm", "softplus",
 ]
 FAM_COUNT = len(FAMILIES)
 
@@ -110,6 +110,16 @@ _SIGS = {
     "tagi_embedding_bwd": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, P, I64, P]),
     "tagi_embedding_bwd_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_pe_add": (c_int, [P, P, P, I64, I64, I64, P]),
+    "tagi_innovation_indexed": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, P]),
+    "tagi_hrc_innovation": (c_int, [P, P, P, P, P, F, P, P, I64, I64, I64, I64, P]),
+    "tagi_hrc_class_probs": (c_int, [P, P, P, P, F, P, P, I64, I64, I64, I64, P]),
+    "tagi_innovation_heteros": (c_int, [P, P, P, P, P, I64, P]),
+    "tagi_even_softplus_fwd": (c_int, [P, P, P, P, P, I64, P]),
+    "tagi_maxpool2d_fwd": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, c_int, P]),
+    "tagi_maxpool2d_bwd": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, c_int, P]),
+    "tagi_layernorm_fwd": (c_int, [P, P, P, P, P, P, P, P, P, P, I64, I64, F, P]),
+    "tagi_layernorm_bwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, F, P, I64, P]),
+    "tagi_layernorm_bwd_ws_bytes": (I64, [I64, I64]),
 }
 
 EXPORTED = tuple(_SIGS)

@@ -17,7 +17,7 @@ from .layers.conv2d import Conv2D
 from .layers.fused import backward_chain, defer_bn_parameter_deltas, forward_chain
 from .layers.multihead_attention import MultiheadAttentionV2
 from .layers.resblock import ResBlock
-from .update.observation import compute_innovation
+from .update.observation import compute_innovation, hrc_innovation
 from .update.parameters import get_cap_factor, update_parameters_multi
 
 
@@ -103,6 +103,23 @@ class Sequential:
         delta_mu, delta_var = compute_innovation(y_batch, y_pred_mu, y_pred_var, sigma_v)
         with defer_bn_parameter_deltas():  # one launch forms every BatchNorm2D's parameter deltas
             backward_chain(self.layers, delta_mu, delta_var, first_params_only=True)
+        self.update(get_cap_factor(batch_size))
+        return y_pred_mu, y_pred_var
+
+    def step_hrc(self, x_batch: Tensor, labels: Tensor, hrc, sigma_v: float) -> tuple[Tensor, Tensor]:
+        """forward -> sparse HRC innovation -> backward -> capped update (network.py:157-224).
+
+        The output layer is ``hrc.len`` wide; only the ``hrc.n_obs`` tree nodes on each
+        label's path receive innovation. Sequence outputs (B, S, len) take B*S labels.
+        """
+        batch_size = x_batch.shape[0]
+        y_pred_mu, y_pred_var = self.forward(x_batch)
+        shape = y_pred_mu.shape
+        width = shape[-1]
+        delta_mu, delta_var = hrc_innovation(y_pred_mu.reshape(-1, width), y_pred_var.reshape(-1, width), labels,
+                                             hrc, sigma_v)
+        with defer_bn_parameter_deltas():
+            backward_chain(self.layers, delta_mu.reshape(shape), delta_var.reshape(shape), first_params_only=True)
         self.update(get_cap_factor(batch_size))
         return y_pred_mu, y_pred_var
 
