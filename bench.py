@@ -42,6 +42,9 @@ WORKLOAD_DESC = {
     "mlp": "TAGI MLP 784-256-128-10 ReLU + Remax, batch 256",
     "transformer": "TAGI transformer block (Embedding 64x256 + PE + MHA-V2 8 heads + RMSNorm + Linear 256-64), "
                    "batch 64, seq 256",
+    "mlp_hrc": "TAGI MLP 784-128-11 with a hierarchical-softmax head (10 classes), step_hrc, batch 512",
+    "resnet18_hrc": "TAGI ResNet-18 (as resnet18) with the head Linear 512-11 and a hierarchical-softmax "
+                    "output (10 classes), step_hrc, batch 128",
     "linear": "TAGI Linear layer microbench, (batch, in, out) = (4096,4096,4096), (8192,1024,4096), "
               "(256,4096,11008): forward moments + backward deltas + capped update",
 }
@@ -64,12 +67,23 @@ def cpu_baseline(workload: str, sample_batch: int, min_steps: int = 3, budget_s:
     torch.set_num_threads(max(cores, 1))
     w = workloads.build(workload, device="cpu", batch=sample_batch)
     onet = O.mirror_net(w.net, dtype=torch.float32)
-    x, y = w.x.float(), w.y.float()
-    onet.step(x, y, w.sigma_v)  # warm-up
+    x = w.x.float()
+    if w.hrc is not None:
+        n_classes = w.hrc.obs.shape[0]
+
+        def step():
+            onet.step_hrc(x, w.y, n_classes, w.sigma_v)
+    else:
+        y = w.y.float()
+
+        def step():
+            onet.step(x, y, w.sigma_v)
+
+    step()  # warm-up
     times = []
     while len(times) < min_steps or sum(times) < budget_s:
         t0 = time.perf_counter()
-        onet.step(x, y, w.sigma_v)
+        step()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     steps = len(times)
@@ -257,7 +271,7 @@ def main():
         if i == 1 or (i == 0 and args.warmup == 1):
             torch.cuda.synchronize()
             _lib.prof_begin()
-        net.step(x, y, sv)
+        w.step()
         prof_steps += i >= 1 or args.warmup == 1
     torch.cuda.synchronize()
     if prof_steps:
@@ -269,6 +283,9 @@ def main():
     # event record holds the queue for a few microseconds, so it runs on the last few
     # timed steps only (same shapes every step) instead of inflating all of them.
     timer_steps = min(args.steps, TIMER_STEPS)
+    if args.graph and w.hrc is not None:
+        print("bench.py: --graph records Sequential.step; HRC workloads are timed eagerly", file=sys.stderr)
+        sys.exit(2)
     if args.graph:
         log("[bench] recording the step into a HIP graph (one more eager step)")
         graph = net.capture_step(x, y, sv)
@@ -289,7 +306,7 @@ def main():
         for i in range(args.steps):
             if dom and i == args.steps - timer_steps:
                 _lib.prof_begin([dom])
-            net.step(x, y, sv)
+            w.step()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         timed = _lib.prof_end() if dom else {}
@@ -358,7 +375,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (seeded N(0,1) inputs, one-hot targets, random-init priors of the architecture)",
+        "data": "synthetic (seeded inputs, one-hot targets or class labels, random-init priors of the architecture)",
         "config": {"workload": WORKLOAD_DESC[args.workload], "global_batch": w.batch, "parallelism": "single GPU",
                    "launch": "hip graph replay" if args.graph else "eager"},
         "roofline": roofline,

@@ -326,3 +326,17 @@ def test_checkpoint_round_trip_on_gpu(dev, tmp_path):
     b, _ = other.step(x, y, 0.1)
     torch.cuda.synchronize()
     assert torch.equal(a.cpu(), b.cpu())
+
+
+def test_resnet18_hrc_workload_step(dev):
+    from triton_tagi_amd import workloads
+
+    w = workloads.build("resnet18_hrc", device=dev, batch=4)
+    onet = O.mirror_net(w.net)
+    mu, var = w.step()
+    rmu, rvar = onet.step_hrc(d64(w.x), w.y.cpu(), 10, w.sigma_v)
+    torch.cuda.synchronize()
+    assert mu.shape == (4, 11)
+    assert_scaled_close(mu, rmu, mscale(rmu), RTOL, ATOL, "mu")
+    assert_scaled_close(var, rvar, None, RTOL, ATOL, "var")
+    compare_params(w.net, onet)

@@ -13,6 +13,10 @@ any device holds the same priors; inputs use a generator seeded ``seed + 1`` and
                  gain 0.1, batch 128, x ~ N(0,1) 3x32x32
     transformer  Embedding(64, 256) + PE + MHA-V2 (8 heads) + RMSNorm + Linear 256-64,
                  batch 64, sequence 256, target = one-hot of the reversed sequence
+    mlp_hrc      784-128-11 with a hierarchical-softmax head (10 classes), batch 512,
+                 trained with step_hrc (tests/validation/test_mnist_hrc_10epochs.py)
+    resnet18_hrc resnet18 with the head Linear 512-11 and step_hrc
+                 (examples/cifar10_resnet18_hrc.py), batch 128
 and the Linear microbenchmark shapes (batch, in, out).
 """
 
@@ -21,6 +25,8 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 import torch
+
+from .hrc_softmax import HierarchicalSoftmax, class_to_obs
 
 from .layers import (
     AvgPool2D,
@@ -46,9 +52,16 @@ class Workload:
     name: str
     net: Sequential
     x: torch.Tensor
-    y: torch.Tensor
+    y: torch.Tensor  # one-hot targets, or integer labels for an HRC head
     sigma_v: float
     batch: int
+    hrc: HierarchicalSoftmax | None = None
+
+    def step(self):
+        """One training step of the workload (step_hrc for an HRC head)."""
+        if self.hrc is not None:
+            return self.net.step_hrc(self.x, self.y, self.hrc, self.sigma_v)
+        return self.net.step(self.x, self.y, self.sigma_v)
 
 
 def _onehot(labels: torch.Tensor, classes: int) -> torch.Tensor:
@@ -72,7 +85,11 @@ def cnn_layers():
     ]
 
 
-def resnet18_layers(gain: float = 0.1, width: int = 64):
+def mlp_hrc_layers(hrc_len: int = 11):
+    return [Linear(784, 128, device="cpu"), ReLU(), Linear(128, hrc_len, device="cpu")]
+
+
+def resnet18_layers(gain: float = 0.1, width: int = 64, hrc_len: int | None = None):
     kw = dict(device="cpu", gain_w=gain, gain_b=gain)
     w = width
     return [
@@ -81,7 +98,8 @@ def resnet18_layers(gain: float = 0.1, width: int = 64):
         ResBlock(w, 2 * w, 2, **kw), ResBlock(2 * w, 2 * w, 1, **kw),
         ResBlock(2 * w, 4 * w, 2, **kw), ResBlock(4 * w, 4 * w, 1, **kw),
         ResBlock(4 * w, 8 * w, 2, **kw), ResBlock(8 * w, 8 * w, 1, **kw),
-        AvgPool2D(4), Flatten(), Linear(8 * w, 10, **kw), Remax(),
+        AvgPool2D(4), Flatten(),
+        *([Linear(8 * w, 10, **kw), Remax()] if hrc_len is None else [Linear(8 * w, hrc_len, **kw)]),
     ]
 
 
@@ -101,7 +119,22 @@ def build(name: str, device: str = "cuda", seed: int = 0, batch: int | None = No
     torch.manual_seed(seed)
     gx = torch.Generator().manual_seed(seed + 1)
     gy = torch.Generator().manual_seed(seed + 2)
-    if name == "mlp":
+    hrc = None
+    if name == "mlp_hrc":
+        B = batch or 512
+        hrc = class_to_obs(10)
+        layers = mlp_hrc_layers(hrc.len)
+        x = torch.rand(B, 784, generator=gx)
+        y = torch.randint(0, 10, (B,), generator=gy)
+        sv = 0.05
+    elif name == "resnet18_hrc":
+        B = batch or 128
+        hrc = class_to_obs(10)
+        layers = resnet18_layers(hrc_len=hrc.len, **kw)
+        x = torch.randn(B, 3, 32, 32, generator=gx)
+        y = torch.randint(0, 10, (B,), generator=gy)
+        sv = 0.05
+    elif name == "mlp":
         B = batch or 256
         layers = mlp_layers()
         x = torch.rand(B, 784, generator=gx)
@@ -131,7 +164,7 @@ def build(name: str, device: str = "cuda", seed: int = 0, batch: int | None = No
     else:
         raise ValueError(f"unknown workload {name!r}")
     net = Sequential(layers, device=device)
-    return Workload(name, net, x.to(device), y.to(device), sv, B)
+    return Workload(name, net, x.to(device), y.to(device), sv, B, hrc)
 
 
 def linear_microbench(batch: int, fan_in: int, fan_out: int, device: str = "cuda", seed: int = 0):
