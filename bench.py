@@ -45,6 +45,8 @@ WORKLOAD_DESC = {
     "mlp_hrc": "TAGI MLP 784-128-11 with a hierarchical-softmax head (10 classes), step_hrc, batch 512",
     "resnet18_hrc": "TAGI ResNet-18 (as resnet18) with the head Linear 512-11 and a hierarchical-softmax "
                     "output (10 classes), step_hrc, batch 128",
+    "heads": "bandwidth of the HRC, heteroscedastic, EvenSoftplus, MaxPool2D and LayerNorm kernels at "
+             "HBM-bound sizes (one case per kernel, listed in cases)",
     "linear": "TAGI Linear layer microbench, (batch, in, out) = (4096,4096,4096), (8192,1024,4096), "
               "(256,4096,11008): forward moments + backward deltas + capped update",
 }
@@ -190,6 +192,75 @@ def linear_bench(args) -> dict:
     return {"tflops": total_flops / total_s / 1e12, "ms": total_s * 1e3, "shapes": shapes}
 
 
+def heads_bench(args) -> dict:
+    """Bandwidth of the output-head and extra-layer kernels at sizes where HBM bounds them.
+    Each case: W warm-up then K timed calls on the live HIP-event timer; algorithmic bytes
+    per call (each tensor read or written once) over the measured kernel time."""
+    import torch
+
+    import triton_tagi_amd as tt
+    from triton_tagi_amd import _lib
+    from triton_tagi_amd.update.observation import compute_innovation, hrc_innovation
+
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rnd(*shape, lo=None):
+        t = torch.randn(*shape, device=dev, generator=g)
+        return t.abs() + lo if lo is not None else t
+
+    cases = []
+    # MaxPool2D 3x3 s2 p1 over a ResNet-stem-sized activation, channels-last
+    x = rnd(128, 64, 64, 64).contiguous(memory_format=torch.channels_last)
+    xs = rnd(128, 64, 64, 64, lo=0.01).contiguous(memory_format=torch.channels_last)
+    mp = tt.MaxPool2D(3, 2, 1)
+    out, _ = mp.forward(x, xs)
+    dmo, dso = torch.randn_like(out), -torch.rand_like(out)
+    cases.append(("maxpool", "MaxPool2D 3x3/2 pad 1 fwd+bwd, (128,64,64,64) channels-last",
+                  lambda: (mp.forward(x, xs), mp.backward(dmo, dso))))
+    # LayerNorm fwd+bwd over 16384 x 1024 rows
+    ln = tt.LayerNorm(1024, device=dev)
+    la, ls = rnd(16384, 1024), rnd(16384, 1024, lo=0.01)
+    ldm, lds = torch.randn_like(la), -torch.rand_like(la)
+    ln.forward(la, ls)
+    cases.append(("layernorm", "LayerNorm(1024) fwd+bwd, 16384 rows", lambda: (ln.forward(la, ls), ln.backward(ldm, lds))))
+    # EvenSoftplus forward, 32 M elements
+    es = tt.EvenSoftplus(1 << 24)
+    em, eS = rnd(1 << 25), rnd(1 << 25, lo=0.01)
+    cases.append(("softplus", "EvenSoftplus fwd, 2^25 elements", lambda: es.forward(em, eS)))
+    # heteroscedastic innovation, 16 M observations (32 M outputs)
+    hy = rnd(1 << 24)
+    hm, hv = rnd(1 << 25), rnd(1 << 25, lo=0.05)
+    hm[1::2] = hm[1::2].abs() + 0.1
+    cases.append(("innovation", "heteroscedastic innovation, 2^24 observations",
+                  lambda: compute_innovation(hy, hm, hv, 0.0)))
+    # HRC sparse innovation, 2^20 rows of an 11-node tree (10 classes)
+    hrc = tt.class_to_obs(10)
+    rm, rS = rnd(1 << 20, hrc.len), rnd(1 << 20, hrc.len, lo=0.01)
+    lab = torch.randint(0, 10, (1 << 20,), device=dev, generator=g)
+    cases.append(("innovation", "HRC sparse innovation (labels), 2^20 rows x 11 nodes",
+                  lambda: hrc_innovation(rm, rS, lab, hrc, 0.05)))
+    cases.append(("innovation", "HRC class probabilities + predicted labels, 2^20 rows x 10 classes",
+                  lambda: tt.get_predicted_labels(rm, rS, hrc)))
+    res = []
+    for fam, desc, fn in cases:
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        _lib.prof_begin([fam])
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        d = _lib.prof_end()[fam]
+        gbs = d["bytes"] / (d["ms"] / 1e3) / 1e9
+        res.append({"kernel": desc, "family": fam, "us_per_call": round(1e3 * d["ms"] / args.steps, 2),
+                    "alg_bytes_per_call": round(d["bytes"] / args.steps), "gbs": round(gbs, 1),
+                    "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)})
+        log(f"[bench] {desc}: {res[-1]['us_per_call']} us, {res[-1]['gbs']} GB/s")
+    return {"cases": res, "bytes": sum(r["alg_bytes_per_call"] for r in res),
+            "us": sum(r["us_per_call"] for r in res)}
+
+
 def load_traffic(workload: str, family: str):
     p = ROOT / "profiles" / "traffic.json"
     if not p.exists():
@@ -250,6 +321,21 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None},
             "cpu_baseline": None, "shapes": r["shapes"]}), flush=True)
+        return
+    if args.workload == "heads":
+        log("[bench] output-head and extra-layer kernels")
+        r = heads_bench(args)
+        agg = r["bytes"] / (r["us"] / 1e6) / 1e9
+        top = max(r["cases"], key=lambda c: c["us_per_call"])
+        print(json.dumps({
+            "metric": "TAGI output-head / extra-layer kernels, aggregate algorithmic GB/s",
+            "value": round(agg, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(r["us"] / 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp32", "data": "synthetic (seeded moments, labels)",
+            "config": {"workload": WORKLOAD_DESC["heads"], "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "kernel": top["kernel"], "achieved": top["gbs"], "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": top["hbm_frac"], "traffic": None},
+            "cpu_baseline": None, "cases": r["cases"]}), flush=True)
         return
     log(f"[bench] building {args.workload} on {dev}")
     w = workloads.build(args.workload, device=dev, batch=args.batch)

@@ -18,7 +18,7 @@ namespace tagi {
 // LABELS: the bits come from class tables, obs/idx[label[b] * n_obs + c], with the
 // scalar noise v = sigma_v^2 (labels_to_hrc + torch.full_like at network.py:205-209
 // folded in); a label outside [0, n_classes) makes its row NaN.
-template <bool LABELS>
+template <bool LABELS, typename IT>
 __global__ void __launch_bounds__(256) hrc_innovation_kernel(const float* __restrict__ ma,
                                                              const float* __restrict__ Sa,
                                                              const float* __restrict__ y_obs,
@@ -31,7 +31,8 @@ __global__ void __launch_bounds__(256) hrc_innovation_kernel(const float* __rest
   const int64_t total = rows * (int64_t)n_out;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-    const int64_t b = e / n_out;
+    // IT = uint32_t when every flat index fits: 32-bit division is a short sequence
+    const int64_t b = (int64_t)((IT)e / (IT)n_out);
     const int j = (int)(e - b * n_out);
     const int32_t* ib;
     const float* yb;
@@ -87,6 +88,44 @@ __device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi)
   if (vn != bn) return vn;
   if (!vn && v != bv) return v > bv;
   return i < bi;
+}
+
+// Trees of at most 64 nodes and 64 classes: one wavefront per row, four rows per block.
+// Lane j holds the probability of node j; class r (lane r) multiplies the probabilities
+// of its path's nodes, fetched from the lanes that hold them by cross-lane permutes.
+__global__ void __launch_bounds__(256) hrc_class_probs_wave_kernel(const float* __restrict__ ma,
+                                                                   const float* __restrict__ Sa,
+                                                                   const float* __restrict__ obs,
+                                                                   const int32_t* __restrict__ idx, float inv_a2,
+                                                                   float* __restrict__ probs,
+                                                                   int64_t* __restrict__ pred, int64_t rows,
+                                                                   int n_out, int n_obs, int n_classes) {
+  const int lane = threadIdx.x & 63;
+  const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= rows) return;  // whole wavefronts leave together
+  const float pz = lane < n_out ? node_prob(ma[b * n_out + lane], Sa[b * n_out + lane], inv_a2) : 0.f;
+  const bool mine = lane < n_classes;
+  float p = 1.0f;
+  for (int c = 0; c < n_obs; ++c) {
+    int node = mine ? idx[lane * n_obs + c] - 1 : 0;
+    const bool ok = node >= 0 && node < n_out;
+    const float q = __shfl(pz, ok ? node : 0, 64);
+    if (mine) p *= obs[lane * n_obs + c] > 0.f ? (ok ? q : 0.f) : 1.0f - (ok ? q : 0.f);
+  }
+  if (mine) probs[b * n_classes + lane] = p;
+  if (pred == nullptr) return;
+  float bv = mine ? p : -__builtin_inff();
+  int64_t bi = mine ? lane : 0x7fffffffffffffffll;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int64_t oi = __shfl_xor(bi, off, 64);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) pred[b] = bi;
 }
 
 __global__ void __launch_bounds__(256) hrc_class_probs_kernel(const float* __restrict__ ma,
@@ -263,9 +302,14 @@ extern "C" int tagi_innovation_indexed(const float* ma, const float* Sa, const f
   TAGI_REQUIRE(ma && Sa && dm && dS && (n_obs == 0 || (y_obs && var_obs && idx)), "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_INNOVATION, s, 0.0, 8.0 * rows * n_out + 12.0 * rows * n_obs + 8.0 * rows * n_out);
-  hipLaunchKernelGGL(hrc_innovation_kernel<false>, dim3(ew_blocks(rows * n_out, 256)), dim3(256), 0, s, ma, Sa,
-                     y_obs, var_obs, idx, (const int64_t*)nullptr, (int64_t)0, 0.0f, dm, dS, rows, (int)n_out,
-                     (int)n_obs);
+  if (rows * n_out < (1ll << 32))
+    hipLaunchKernelGGL((hrc_innovation_kernel<false, uint32_t>), dim3(ew_blocks(rows * n_out, 256)), dim3(256), 0, s,
+                       ma, Sa, y_obs, var_obs, idx, (const int64_t*)nullptr, (int64_t)0, 0.0f, dm, dS, rows,
+                       (int)n_out, (int)n_obs);
+  else
+    hipLaunchKernelGGL((hrc_innovation_kernel<false, int64_t>), dim3(ew_blocks(rows * n_out, 256)), dim3(256), 0, s,
+                       ma, Sa, y_obs, var_obs, idx, (const int64_t*)nullptr, (int64_t)0, 0.0f, dm, dS, rows,
+                       (int)n_out, (int)n_obs);
   return check_launch(what);
 }
 
@@ -279,8 +323,14 @@ extern "C" int tagi_hrc_innovation(const float* ma, const float* Sa, const int64
   TAGI_REQUIRE(ma && Sa && labels && obs && idx && dm && dS, "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_INNOVATION, s, 0.0, 16.0 * rows * n_out + 8.0 * rows);
-  hipLaunchKernelGGL(hrc_innovation_kernel<true>, dim3(ew_blocks(rows * n_out, 256)), dim3(256), 0, s, ma, Sa, obs,
-                     (const float*)nullptr, idx, labels, n_classes, sigma_v2, dm, dS, rows, (int)n_out, (int)n_obs);
+  if (rows * n_out < (1ll << 32))
+    hipLaunchKernelGGL((hrc_innovation_kernel<true, uint32_t>), dim3(ew_blocks(rows * n_out, 256)), dim3(256), 0, s,
+                       ma, Sa, obs, (const float*)nullptr, idx, labels, n_classes, sigma_v2, dm, dS, rows, (int)n_out,
+                       (int)n_obs);
+  else
+    hipLaunchKernelGGL((hrc_innovation_kernel<true, int64_t>), dim3(ew_blocks(rows * n_out, 256)), dim3(256), 0, s,
+                       ma, Sa, obs, (const float*)nullptr, idx, labels, n_classes, sigma_v2, dm, dS, rows, (int)n_out,
+                       (int)n_obs);
   return check_launch(what);
 }
 
@@ -296,8 +346,12 @@ extern "C" int tagi_hrc_class_probs(const float* ma, const float* Sa, const floa
   TAGI_REQUIRE(ma && Sa && obs && idx && probs, "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_INNOVATION, s, 0.0, 8.0 * rows * n_out + 4.0 * rows * n_classes);
-  hipLaunchKernelGGL(hrc_class_probs_kernel, dim3((unsigned)rows), dim3(256), 0, s, ma, Sa, obs, idx,
-                     1.0f / (alpha * alpha), probs, pred, (int)n_out, (int)n_obs, (int)n_classes);
+  if (n_out <= 64 && n_classes <= 64)
+    hipLaunchKernelGGL(hrc_class_probs_wave_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, ma, Sa, obs, idx,
+                       1.0f / (alpha * alpha), probs, pred, rows, (int)n_out, (int)n_obs, (int)n_classes);
+  else
+    hipLaunchKernelGGL(hrc_class_probs_kernel, dim3((unsigned)rows), dim3(256), 0, s, ma, Sa, obs, idx,
+                       1.0f / (alpha * alpha), probs, pred, (int)n_out, (int)n_obs, (int)n_classes);
   return check_launch(what);
 }
 

@@ -23,28 +23,32 @@ __device__ __forceinline__ int64_t in_off(const PoolGeom& g, int64_t n, int c, i
 __device__ __forceinline__ int64_t out_off(const PoolGeom& g, int64_t n, int c, int h, int w) {
   return g.cl ? ((n * g.Ho + h) * g.Wo + w) * g.C + c : ((n * g.C + c) * g.Ho + h) * (int64_t)g.Wo + w;
 }
-// (n, c, h, w) of flat storage position e of a tensor with spatial size (h_n, w_n)
-__device__ __forceinline__ void decode(const PoolGeom& g, int64_t e, int h_n, int w_n, int64_t& n, int& c, int& h,
+// (n, c, h, w) of flat storage position e of a tensor with spatial size (h_n, w_n).
+// IT is uint32_t when every flat index fits (32-bit division is a short sequence;
+// 64-bit division is a long software routine), int64_t otherwise.
+template <typename IT>
+__device__ __forceinline__ void decode(const PoolGeom& g, IT e, int h_n, int w_n, int64_t& n, int& c, int& h,
                                        int& w) {
   if (g.cl) {
-    c = (int)(e % g.C);
-    e /= g.C;
-    w = (int)(e % w_n);
-    e /= w_n;
-    h = (int)(e % h_n);
-    n = e / h_n;
+    c = (int)(e % (IT)g.C);
+    e /= (IT)g.C;
+    w = (int)(e % (IT)w_n);
+    e /= (IT)w_n;
+    h = (int)(e % (IT)h_n);
+    n = (int64_t)(e / (IT)h_n);
   } else {
-    w = (int)(e % w_n);
-    e /= w_n;
-    h = (int)(e % h_n);
-    e /= h_n;
-    c = (int)(e % g.C);
-    n = e / g.C;
+    w = (int)(e % (IT)w_n);
+    e /= (IT)w_n;
+    h = (int)(e % (IT)h_n);
+    e /= (IT)h_n;
+    c = (int)(e % (IT)g.C);
+    n = (int64_t)(e / (IT)g.C);
   }
 }
 
 // The first in-window position starts as the pick with value -inf; a later position
 // replaces it when its mean is larger or NaN (torch's max_pool2d selection rule).
+template <typename IT>
 __global__ void __launch_bounds__(256) maxpool_fwd_kernel(PoolGeom g, const float* __restrict__ ma,
                                                           const float* __restrict__ Sa, float* __restrict__ mz,
                                                           float* __restrict__ Sz, int32_t* __restrict__ pool_idx) {
@@ -53,7 +57,7 @@ __global__ void __launch_bounds__(256) maxpool_fwd_kernel(PoolGeom g, const floa
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
     int64_t n;
     int c, ho, wo;
-    decode(g, e, g.Ho, g.Wo, n, c, ho, wo);
+    decode<IT>(g, (IT)e, g.Ho, g.Wo, n, c, ho, wo);
     const int h0 = ho * g.s - g.p, w0 = wo * g.s - g.p;
     const int ha = max(h0, 0), hb = min(h0 + g.k, g.H), wa = max(w0, 0), wb = min(w0 + g.k, g.W);
     float best = -__builtin_inff();
@@ -74,6 +78,7 @@ __global__ void __launch_bounds__(256) maxpool_fwd_kernel(PoolGeom g, const floa
   }
 }
 
+template <typename IT>
 __global__ void __launch_bounds__(256) maxpool_bwd_kernel(PoolGeom g, const float* __restrict__ dmz,
                                                           const float* __restrict__ dSz,
                                                           const int32_t* __restrict__ pool_idx,
@@ -83,7 +88,7 @@ __global__ void __launch_bounds__(256) maxpool_bwd_kernel(PoolGeom g, const floa
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
     int64_t n;
     int c, h, w;
-    decode(g, e, g.H, g.W, n, c, h, w);
+    decode<IT>(g, (IT)e, g.H, g.W, n, c, h, w);
     // windows ho with ho*s - p <= h <= ho*s - p + k - 1
     const int hp = h + g.p, wp = w + g.p;
     const int ho_a = hp - g.k + 1 <= 0 ? 0 : (hp - g.k + 1 + g.s - 1) / g.s;
@@ -135,7 +140,12 @@ extern "C" int tagi_maxpool2d_fwd(const float* ma, const float* Sa, float* mz, f
   hipStream_t s = as_stream(stream);
   const int64_t out = N * C * (int64_t)g.Ho * g.Wo;
   ProfScope ps(FAM_MAXPOOL, s, 0.0, 4.0 * N * C * H * W + 12.0 * out);
-  hipLaunchKernelGGL(maxpool_fwd_kernel, dim3(ew_blocks(out, 256)), dim3(256), 0, s, g, ma, Sa, mz, Sz, pool_idx);
+  if (out < (1ll << 32))
+    hipLaunchKernelGGL(maxpool_fwd_kernel<uint32_t>, dim3(ew_blocks(out, 256)), dim3(256), 0, s, g, ma, Sa, mz, Sz,
+                       pool_idx);
+  else
+    hipLaunchKernelGGL(maxpool_fwd_kernel<int64_t>, dim3(ew_blocks(out, 256)), dim3(256), 0, s, g, ma, Sa, mz, Sz,
+                       pool_idx);
   return check_launch(what);
 }
 
@@ -151,7 +161,11 @@ extern "C" int tagi_maxpool2d_bwd(const float* dmz, const float* dSz, const int3
   hipStream_t s = as_stream(stream);
   const int64_t total = N * C * H * W;
   ProfScope ps(FAM_MAXPOOL, s, 0.0, 12.0 * N * C * (int64_t)g.Ho * g.Wo + 8.0 * total);
-  hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(ew_blocks(total, 256)), dim3(256), 0, s, g, dmz, dSz, pool_idx, dma,
-                     dSa);
+  if (total < (1ll << 32))
+    hipLaunchKernelGGL(maxpool_bwd_kernel<uint32_t>, dim3(ew_blocks(total, 256)), dim3(256), 0, s, g, dmz, dSz,
+                       pool_idx, dma, dSa);
+  else
+    hipLaunchKernelGGL(maxpool_bwd_kernel<int64_t>, dim3(ew_blocks(total, 256)), dim3(256), 0, s, g, dmz, dSz,
+                       pool_idx, dma, dSa);
   return check_launch(what);
 }
