@@ -340,3 +340,58 @@ def test_resnet18_hrc_workload_step(dev):
     assert_scaled_close(mu, rmu, mscale(rmu), RTOL, ATOL, "mu")
     assert_scaled_close(var, rvar, None, RTOL, ATOL, "var")
     compare_params(w.net, onet)
+
+
+# ------------------------------------------------------------ eval-mode forward
+def test_eval_forward_uses_running_statistics(dev):
+    """Inference after training (batchnorm2d.py:393-395): BatchNorm2D normalises with its
+    running statistics, the fused ReLU->BatchNorm2D passes step aside, and train() restores
+    the batch-statistics path."""
+    from triton_tagi_amd import workloads
+
+    w = workloads.build("resnet18", device=dev, batch=8)
+    for _ in range(2):
+        w.step()
+    w.net.eval()
+    r = g(77)
+    x = torch.randn(8, 3, 32, 32, generator=r)
+    mu, var = w.net.forward(x.to(dev))
+    onet = O.mirror_net(w.net)
+    rmu, rvar = onet.forward(d64(x))
+    torch.cuda.synchronize()
+    assert_scaled_close(mu, rmu, mscale(rmu), RTOL, ATOL, "eval mu")
+    assert_scaled_close(var, rvar, None, RTOL, ATOL, "eval var")
+    assert torch.equal(mu.cpu().argmax(1), rmu.argmax(1))
+    # the prediction of one sample does not depend on the rest of the batch in eval mode
+    mu1, _ = w.net.forward(x[:1].to(dev))
+    assert_scaled_close(mu1, rmu[:1], mscale(rmu[:1]), RTOL, ATOL, "eval mu, batch of one")
+    w.net.train()
+    mu_t, _ = w.net.forward(x.to(dev))
+    assert not torch.allclose(mu_t.cpu(), mu.cpu())
+
+
+def test_eval_hrc_predicted_labels(dev):
+    import triton_tagi_amd as tt
+
+    torch.manual_seed(4)
+    h = tt.class_to_obs(10)
+    net = tt.Sequential([
+        tt.Conv2D(3, 16, 3, padding=1, device="cpu"), tt.ReLU(), tt.BatchNorm2D(16, device="cpu"),
+        tt.AvgPool2D(2), tt.Flatten(), tt.Linear(16 * 8 * 8, 64, device="cpu"), tt.ReLU(),
+        tt.Linear(64, h.len, device="cpu"),
+    ], device=dev)
+    r = g(8)
+    for _ in range(3):
+        x = torch.randn(64, 3, 16, 16, generator=r)
+        net.step_hrc(x.to(dev), torch.randint(0, 10, (64,), generator=r).to(dev), h, 0.05)
+    net.eval()
+    x = torch.randn(32, 3, 16, 16, generator=r)
+    mu, var = net.forward(x.to(dev))
+    pred = tt.get_predicted_labels(mu, var, h)
+    onet = O.mirror_net(net)
+    rmu, rvar = onet.forward(d64(x))
+    R = O.hrc_class_probs(rmu, rvar, d64(h.obs), h.idx.long())
+    top2 = R.topk(2, dim=1).values
+    clear = (top2[:, 0] - top2[:, 1]) > 1e-3 * top2[:, 0]
+    assert clear.sum() >= 16
+    assert torch.equal(pred.cpu()[clear], R.argmax(1)[clear])
