@@ -369,12 +369,9 @@ def main():
     # event record holds the queue for a few microseconds, so it runs on the last few
     # timed steps only (same shapes every step) instead of inflating all of them.
     timer_steps = min(args.steps, TIMER_STEPS)
-    if args.graph and w.hrc is not None:
-        print("bench.py: --graph records Sequential.step; HRC workloads are timed eagerly", file=sys.stderr)
-        sys.exit(2)
     if args.graph:
         log("[bench] recording the step into a HIP graph (one more eager step)")
-        graph = net.capture_step(x, y, sv)
+        graph = net.capture_step_hrc(x, y, w.hrc, sv) if w.hrc is not None else net.capture_step(x, y, sv)
         torch.cuda.synchronize()
         log(f"[bench] timing {args.steps} graph replays")
         t0 = time.perf_counter()

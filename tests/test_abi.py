@@ -63,3 +63,41 @@ def test_product_path_refuses_cpu_tensors():
     t = torch.zeros(4)
     with pytest.raises(ValueError, match="GPU only"):
         update_parameters(t, t.clone(), t.clone(), t.clone(), 2.0)
+
+
+def test_new_entry_points_validate_arguments_without_a_gpu():
+    from triton_tagi_amd import _lib
+
+    lib = _lib.load()
+    # MaxPool2D: padding above half the window
+    rc = lib.tagi_maxpool2d_fwd(None, None, None, None, None, 1, 1, 4, 4, 2, 2, 2, 0, None)
+    assert rc == 1 and "pad" in _lib.last_error()
+    # HRC class probabilities: alpha must be positive
+    rc = lib.tagi_hrc_class_probs(None, None, None, None, 0.0, None, None, 1, 11, 4, 10, None)
+    assert rc == 1 and "alpha" in _lib.last_error()
+    # LayerNorm backward: workspace too small
+    rc = lib.tagi_layernorm_bwd(*([1] * 14), 64, 256, 1e-5, 1, 0, None)
+    assert rc == 1 and "workspace" in _lib.last_error()
+    assert lib.tagi_layernorm_bwd_ws_bytes(64, 256) == 2 * 4 * 256 * 4
+    # empty inputs are no-ops
+    assert lib.tagi_innovation_heteros(None, None, None, None, None, 0, None) == 0
+    assert lib.tagi_even_softplus_fwd(None, None, None, None, None, 0, None) == 0
+    assert lib.tagi_innovation_indexed(None, None, None, None, None, None, None, 0, 11, 4, None) == 0
+    rc = lib.tagi_hrc_innovation(None, None, None, None, None, 0.1, None, None, 3, 11, 4, 10, None)
+    assert rc == 1 and "null pointer" in _lib.last_error()
+
+
+def test_heads_refuse_cpu_tensors():
+    import torch
+
+    import triton_tagi_amd as tt
+    from triton_tagi_amd.update.observation import compute_innovation_with_indices
+
+    h = tt.class_to_obs(10)
+    t = torch.zeros(2, h.len)
+    with pytest.raises(ValueError, match="GPU only"):
+        tt.obs_to_class_probs(t, t, h)
+    with pytest.raises(ValueError, match="GPU only"):
+        compute_innovation_with_indices(t, t, torch.zeros(2, 4), torch.zeros(2, 4), torch.ones(2, 4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="GPU only"):
+        tt.MaxPool2D(2).forward(torch.zeros(1, 1, 4, 4), torch.zeros(1, 1, 4, 4))

@@ -47,3 +47,27 @@ def test_graph_replays_match_eager_steps(dev, name, batch):
         # eager work on the same stream between replays
         torch.cuda.synchronize()
     assert bool(torch.isfinite(mu).all())
+
+
+@pytest.mark.parametrize("name,batch", [("mlp_hrc", 512), ("resnet18_hrc", 16)])
+def test_graph_replays_match_eager_hrc_steps(dev, name, batch):
+    from triton_tagi_amd import workloads
+
+    eager = workloads.build(name, device="cuda:0", batch=batch)
+    graphed = workloads.build(name, device="cuda:0", batch=batch)
+    g = graphed.net.capture_step_hrc(graphed.x, graphed.y, graphed.hrc, graphed.sigma_v)
+    eager.step()
+    torch.cuda.synchronize()
+    gen = torch.Generator().manual_seed(11)
+    for r in range(3):
+        mu, var = g.replay()
+        emu, evar = eager.step()
+        torch.cuda.synchronize()
+        assert torch.equal(mu, emu) and torch.equal(var, evar), f"replay {r}: predictions differ"
+        for i, (a, b) in enumerate(zip(_params(eager.net), _params(graphed.net))):
+            assert torch.equal(a, b), f"replay {r}: parameter tensor {i} differs"
+        # new labels copied in place are seen by the next replay and the next eager step
+        new = torch.randint(0, 10, (batch,), generator=gen).to(dev)
+        graphed.y.copy_(new)
+        eager.y.copy_(new)
+        torch.cuda.synchronize()

@@ -135,11 +135,21 @@ class Sequential:
         """
         if not x_batch.is_cuda:
             raise ValueError("capture_step: the batch must be on a GPU")
-        self.step(x_batch, y_batch, sigma_v)
-        torch.cuda.synchronize(x_batch.device)
+        return self._capture(lambda: self.step(x_batch, y_batch, sigma_v), x_batch.device)
+
+    def capture_step_hrc(self, x_batch: Tensor, labels: Tensor, hrc, sigma_v: float) -> "StepGraph":
+        """``capture_step`` for ``step_hrc``: replays read ``x_batch`` and ``labels`` in place
+        (both must be on the GPU; copy the next batch and labels into them before a replay)."""
+        if not x_batch.is_cuda or not labels.is_cuda or labels.device != x_batch.device:
+            raise ValueError("capture_step_hrc: the batch and the labels must be on the same GPU")
+        return self._capture(lambda: self.step_hrc(x_batch, labels, hrc, sigma_v), x_batch.device)
+
+    def _capture(self, step, device) -> "StepGraph":
+        step()
+        torch.cuda.synchronize(device)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            mu, var = self.step(x_batch, y_batch, sigma_v)
+            mu, var = step()
         return StepGraph(graph, mu, var)
 
     def train(self) -> None:
