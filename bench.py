@@ -284,6 +284,8 @@ def main():
     ap.add_argument("--graph", action="store_true",
                     help="time replays of a HIP graph of the step (Sequential.capture_step) instead of eager "
                          "steps; the roofline then comes from the warm-up steps' live timer")
+    ap.add_argument("--no-overlap", action="store_true",
+                    help="queue the Conv2D parameter-delta GEMMs on the step's own stream instead of a side stream")
     ap.add_argument("--ceilings", action="store_true",
                     help="print measured MFMA / copy / vendor-GEMM ceilings as one JSON line and exit")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -340,6 +342,8 @@ def main():
     log(f"[bench] building {args.workload} on {dev}")
     w = workloads.build(args.workload, device=dev, batch=args.batch)
     net, x, y, sv = w.net, w.x, w.y, w.sigma_v
+    if args.no_overlap:
+        net.overlap_param_deltas = False
 
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
@@ -460,7 +464,8 @@ def main():
         "dtype": "fp32",
         "data": "synthetic (seeded inputs, one-hot targets or class labels, random-init priors of the architecture)",
         "config": {"workload": WORKLOAD_DESC[args.workload], "global_batch": w.batch, "parallelism": "single GPU",
-                   "launch": "hip graph replay" if args.graph else "eager"},
+                   "launch": "hip graph replay" if args.graph else "eager",
+                   "param_deltas": "side stream" if net.overlap_param_deltas else "step stream"},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernel_ms_per_step_warmup": round(gpu_ms / nps, 4),

@@ -13,10 +13,12 @@ padding_type 1 pads p on every side; padding_type 2 pads p on the right/bottom o
 
 from __future__ import annotations
 
+import contextlib
+
 import torch
 from torch import Tensor
 
-from .. import _lib
+from .. import _lib, _overlap
 from ..base import LearnableLayer
 from ..param_init import init_weight_bias_conv2d
 from ..update.parameters import update_parameters
@@ -101,16 +103,19 @@ class Conv2D(LearnableLayer):
             raise ValueError(f"Conv2D.backward: delta shape {tuple(dmz.shape)} != output shape")
         dev = dmz.device
         K = self.C_in * self.kH * self.kW
-        self.delta_mw = torch.empty(K, self.C_out, device=dev, dtype=torch.float32)
-        self.delta_Sw = torch.empty_like(self.delta_mw)
-        self.delta_mb = torch.empty(1, self.C_out, device=dev, dtype=torch.float32)
-        self.delta_Sb = torch.empty_like(self.delta_mb)
-        ws = _lib.workspace(_lib.query("tagi_conv2d_wgrad_ws_bytes", g), dev)
-        wp, wb = _lib.ws_args(ws)
+        ctx = _overlap.active()
+        side = ctx.fork(dev, self.ma_in, dmz, dSz) if ctx is not None else None
+        with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
+            self.delta_mw = torch.empty(K, self.C_out, device=dev, dtype=torch.float32)
+            self.delta_Sw = torch.empty_like(self.delta_mw)
+            self.delta_mb = torch.empty(1, self.C_out, device=dev, dtype=torch.float32)
+            self.delta_Sb = torch.empty_like(self.delta_mb)
+            ws = _lib.workspace(_lib.query("tagi_conv2d_wgrad_ws_bytes", g), dev)
+            wp, wb = _lib.ws_args(ws)
+            _lib.call("tagi_conv2d_wgrad", self.ma_in.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), self.Sw.data_ptr(),
+                      self.Sb.data_ptr(), self.delta_mw.data_ptr(), self.delta_Sw.data_ptr(),
+                      self.delta_mb.data_ptr(), self.delta_Sb.data_ptr(), g, wp, wb, _lib.stream_of(dmz))
         st = _lib.stream_of(dmz)
-        _lib.call("tagi_conv2d_wgrad", self.ma_in.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), self.Sw.data_ptr(),
-                  self.Sb.data_ptr(), self.delta_mw.data_ptr(), self.delta_Sw.data_ptr(), self.delta_mb.data_ptr(),
-                  self.delta_Sb.data_ptr(), g, wp, wb, st)
         if not input_deltas:
             return None
         d_ma = _lib.empty_cl(N, C, H, W, dev)

@@ -9,9 +9,12 @@ ReLU -> BatchNorm2D pairs run as fused passes (same results as the layers one by
 
 from __future__ import annotations
 
+import contextlib
+
 import torch
 from torch import Tensor
 
+from . import _overlap
 from .base import Layer, LearnableLayer
 from .layers.conv2d import Conv2D
 from .layers.fused import backward_chain, defer_bn_parameter_deltas, forward_chain
@@ -22,6 +25,8 @@ from .update.parameters import get_cap_factor, update_parameters_multi
 
 
 class Sequential:
+    overlap_param_deltas = True  # Conv2D parameter-delta GEMMs on a side stream within step()
+
     def __init__(self, layers: list, device: str = "cuda") -> None:
         self.device = torch.device(device)
         self.layers = layers
@@ -101,10 +106,20 @@ class Sequential:
         batch_size = x_batch.shape[0]
         y_pred_mu, y_pred_var = self.forward(x_batch)
         delta_mu, delta_var = compute_innovation(y_batch, y_pred_mu, y_pred_var, sigma_v)
-        with defer_bn_parameter_deltas():  # one launch forms every BatchNorm2D's parameter deltas
+        with self._backward_scope():
             backward_chain(self.layers, delta_mu, delta_var, first_params_only=True)
         self.update(get_cap_factor(batch_size))
         return y_pred_mu, y_pred_var
+
+    def _backward_scope(self):
+        """One launch forms every BatchNorm2D's parameter deltas at the end of the backward
+        pass; with ``overlap_param_deltas`` the Conv2D parameter-delta GEMMs run on a side
+        stream beside the input-delta chain (joined before the update)."""
+        stack = contextlib.ExitStack()
+        if self.overlap_param_deltas:
+            stack.enter_context(_overlap.overlap_param_deltas())
+        stack.enter_context(defer_bn_parameter_deltas())
+        return stack
 
     def step_hrc(self, x_batch: Tensor, labels: Tensor, hrc, sigma_v: float) -> tuple[Tensor, Tensor]:
         """forward -> sparse HRC innovation -> backward -> capped update (network.py:157-224).
@@ -118,7 +133,7 @@ class Sequential:
         width = shape[-1]
         delta_mu, delta_var = hrc_innovation(y_pred_mu.reshape(-1, width), y_pred_var.reshape(-1, width), labels,
                                              hrc, sigma_v)
-        with defer_bn_parameter_deltas():
+        with self._backward_scope():
             backward_chain(self.layers, delta_mu.reshape(shape), delta_var.reshape(shape), first_params_only=True)
         self.update(get_cap_factor(batch_size))
         return y_pred_mu, y_pred_var
