@@ -104,7 +104,8 @@ class Conv2D(LearnableLayer):
         dev = dmz.device
         K = self.C_in * self.kH * self.kW
         ctx = _overlap.active()
-        side = ctx.fork(dev, self.ma_in, dmz, dSz) if ctx is not None else None
+        big = N * g.Ho * g.Wo * K * self.C_out >= _overlap.MIN_MACS_CONV
+        side = ctx.fork(dev, self.ma_in, dmz, dSz) if ctx is not None and big else None
         with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
             self.delta_mw = torch.empty(K, self.C_out, device=dev, dtype=torch.float32)
             self.delta_Sw = torch.empty_like(self.delta_mw)

@@ -11,9 +11,12 @@ Backward (deltas stored, applied by ``update``):
 
 from __future__ import annotations
 
+import contextlib
+
 import torch
 from torch import Tensor
 
+from .. import _overlap
 from ..base import LearnableLayer
 from ..kernels.common import fused_backward_delta, linear_forward, linear_param_deltas
 from ..param_init import init_weight_bias_linear
@@ -58,7 +61,12 @@ class Linear(LearnableLayer):
         and ``add`` is returned."""
         dmz = delta_mz.reshape(-1, self.out_features).contiguous()
         dSz = delta_Sz.reshape(-1, self.out_features).contiguous()
-        dmw, dSw, dmb, dSb = linear_param_deltas(self.ma_in, dmz, dSz, self.Sw, self.Sb if self.has_bias else None)
+        ctx = _overlap.active()
+        big = dmz.shape[0] * self.in_features * self.out_features >= _overlap.MIN_MACS_LINEAR
+        side = ctx.fork(dmz.device, self.ma_in, dmz, dSz) if ctx is not None and big else None
+        with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
+            dmw, dSw, dmb, dSb = linear_param_deltas(self.ma_in, dmz, dSz, self.Sw,
+                                                     self.Sb if self.has_bias else None)
         self.delta_mw, self.delta_Sw = dmw, dSw
         if self.has_bias:
             self.delta_mb, self.delta_Sb = dmb, dSb
