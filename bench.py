@@ -285,7 +285,7 @@ def main():
                     help="time replays of a HIP graph of the step (Sequential.capture_step) instead of eager "
                          "steps; the roofline then comes from the warm-up steps' live timer")
     ap.add_argument("--no-overlap", action="store_true",
-                    help="queue the Conv2D parameter-delta GEMMs on the step's own stream instead of a side stream")
+                    help="queue the parameter-delta GEMMs on the step's own stream instead of a side stream")
     ap.add_argument("--ceilings", action="store_true",
                     help="print measured MFMA / copy / vendor-GEMM ceilings as one JSON line and exit")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,

@@ -60,8 +60,11 @@ class defer_bn_parameter_deltas:
     def __exit__(self, exc_type, exc, tb):
         _scope.ctx = self._outer
         if exc_type is None and self.items:
+            # on the stream current at exit (every pending layer's partial sums are ordered
+            # before it: side-stream work has been joined by then)
             arr = (_lib.BnPending * len(self.items))(*self.items)
-            _lib.call("tagi_bn_bwd_finalize_multi", arr, len(self.items), self._stream)
+            _lib.call("tagi_bn_bwd_finalize_multi", arr, len(self.items),
+                      torch.cuda.current_stream(self._keep[0].device).cuda_stream)
         return False
 
 

@@ -116,9 +116,9 @@ class Sequential:
         pass; with ``overlap_param_deltas`` the Conv2D parameter-delta GEMMs run on a side
         stream beside the input-delta chain (joined before the update)."""
         stack = contextlib.ExitStack()
-        if self.overlap_param_deltas:
-            stack.enter_context(_overlap.overlap_param_deltas())
         stack.enter_context(defer_bn_parameter_deltas())
+        if self.overlap_param_deltas:  # exits first: the side stream is joined before the BN finalize
+            stack.enter_context(_overlap.overlap_param_deltas())
         return stack
 
     def step_hrc(self, x_batch: Tensor, labels: Tensor, hrc, sigma_v: float) -> tuple[Tensor, Tensor]:
