@@ -7,8 +7,9 @@ capped update, ResNet-18 at batch 128 on 3x32x32 synthetic inputs (fp32).
 Prints one JSON line. ``value`` is samples/s over the K timed steps (inputs already in
 HBM). The engine's HIP-event timer (events recorded on the launch stream around each
 kernel-family entry point) runs in two modes: over the warm-up steps it brackets every
-family (the per-family breakdown, and the choice of the dominant MFMA family); over the
-timed steps it brackets only that dominant family, whose algorithmic FLOPs divided by
+family (the per-family breakdown, and the choice of the dominant MFMA family: the one with
+the most algorithmic work); over the timed steps it brackets only that family, whose
+algorithmic FLOPs divided by
 its measured time give ``roofline.achieved`` (timing every family would add ~500 event
 records per step to the timed region). ``cpu_baseline`` times the float32 CPU oracle
 (the reference's moment equations in torch CPU ops) on a bounded sample of the same
@@ -367,7 +368,10 @@ def main():
     if prof_steps:
         fams = _lib.prof_end()
     mfma = {f: v for f, v in fams.items() if f in MFMA_FAMILIES}
-    dom = max(mfma, key=lambda f: mfma[f]["ms"]) if mfma else None
+    # the dominant kernel: the family with the most algorithmic MFMA work per step (its
+    # measured time can include a side stream's kernels sharing the GPU; the forward
+    # families, which carry the most work, run alone)
+    dom = max(mfma, key=lambda f: mfma[f]["flops"]) if mfma else None
 
     # The live timer brackets each launch of the dominant family with two HIP events; an
     # event record holds the queue for a few microseconds, so it runs on the last few
