@@ -395,3 +395,24 @@ def test_eval_hrc_predicted_labels(dev):
     clear = (top2[:, 0] - top2[:, 1]) > 1e-3 * top2[:, 0]
     assert clear.sum() >= 16
     assert torch.equal(pred.cpu()[clear], R.argmax(1)[clear])
+
+
+def test_layernorm_sequence_input_and_no_bias(dev):
+    """(B, S, D) input (rows = B*S) and bias=False (zero beta that is never updated)."""
+    import triton_tagi_amd as tt
+
+    torch.manual_seed(6)
+    layer = tt.LayerNorm(48, bias=False, device="cpu")
+    net = tt.Sequential([tt.Linear(16, 48, device="cpu"), tt.ReLU(), layer, tt.Linear(48, 8, device="cpu")],
+                        device=dev)
+    onet = O.mirror_net(net)
+    r = g(12)
+    x, y = torch.randn(4, 9, 16, generator=r), torch.randn(4, 9, 8, generator=r)
+    mu, var = net.step(x.to(dev), y.to(dev), 0.3)
+    rmu, rvar = onet.step(d64(x), d64(y), 0.3)
+    torch.cuda.synchronize()
+    assert mu.shape == (4, 9, 8) and layer.mu_ra.shape == (36, 1)
+    assert_scaled_close(mu, rmu, mscale(rmu), RTOL, ATOL, "mu")
+    assert_scaled_close(var, rvar, None, RTOL, ATOL, "var")
+    compare_params(net, onet)
+    assert torch.all(layer.mb == 0) and torch.all(layer.Sb == 0) and layer.num_parameters == 2 * 48
