@@ -146,14 +146,15 @@ POOLS = [(2, 2, 0), (3, 2, 1), (3, 1, 1), (2, 1, 0), (4, 4, 2), (3, 3, 0)]
 
 
 @pytest.mark.parametrize("k,s,p", POOLS)
-@pytest.mark.parametrize("channels_last", [False, True])
-def test_maxpool(dev, k, s, p, channels_last):
+@pytest.mark.parametrize("channels_last,C", [(False, 5), (True, 5), (True, 8)])
+def test_maxpool(dev, k, s, p, channels_last, C):
+    """C = 8 channels-last takes the float4 path, C = 5 the per-element one."""
     import torch.nn.functional as F
 
     from triton_tagi_amd.layers.maxpool2d import MaxPool2D
 
-    r = g(k * 100 + s * 10 + p + int(channels_last))
-    N, C, H, W = 3, 5, 11, 9
+    r = g(k * 100 + s * 10 + p + int(channels_last) + C)
+    N, H, W = 3, 11, 9
     ma = torch.randn(N, C, H, W, generator=r)
     ma[0, 0, :2, :2] = 1.5  # ties inside one window
     Sa = torch.rand(N, C, H, W, generator=r)

@@ -110,6 +110,96 @@ __global__ void __launch_bounds__(256) maxpool_bwd_kernel(PoolGeom g, const floa
   }
 }
 
+// Channels-last with C % 4 == 0 and 16-byte aligned tensors: one thread per four
+// consecutive channels of one output (forward) or input (backward) pixel, float4 loads
+// and stores along the channels; the same selection and summation order per channel.
+template <typename IT>
+__global__ void __launch_bounds__(256) maxpool_fwd_cl4_kernel(PoolGeom g, const float* __restrict__ ma,
+                                                              const float* __restrict__ Sa, float* __restrict__ mz,
+                                                              float* __restrict__ Sz, int32_t* __restrict__ pool_idx) {
+  const int C4 = g.C >> 2;
+  const int64_t total = g.N * g.Ho * (int64_t)g.Wo * C4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+    IT q = (IT)e;
+    const int c = (int)(q % (IT)C4) * 4;
+    q /= (IT)C4;
+    const int wo = (int)(q % (IT)g.Wo);
+    q /= (IT)g.Wo;
+    const int ho = (int)(q % (IT)g.Ho);
+    const int64_t n = (int64_t)(q / (IT)g.Ho);
+    const int h0 = ho * g.s - g.p, w0 = wo * g.s - g.p;
+    const int ha = max(h0, 0), hb = min(h0 + g.k, g.H), wa = max(w0, 0), wb = min(w0 + g.k, g.W);
+    float best[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+    int pick[4] = {ha * g.W + wa, ha * g.W + wa, ha * g.W + wa, ha * g.W + wa};
+    const int64_t img = n * g.H * (int64_t)g.W;
+    for (int h = ha; h < hb; ++h)
+      for (int w = wa; w < wb; ++w) {
+        const float4 v4 = *reinterpret_cast<const float4*>(ma + (img + (int64_t)h * g.W + w) * g.C + c);
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (v[j] > best[j] || v[j] != v[j]) {
+            best[j] = v[j];
+            pick[j] = h * g.W + w;
+          }
+      }
+    float sv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sv[j] = Sa[(img + pick[j]) * g.C + c + j];
+    const int64_t o = e * 4;  // output (n, ho, wo, c) in channels-last order
+    *reinterpret_cast<float4*>(mz + o) = make_float4(best[0], best[1], best[2], best[3]);
+    *reinterpret_cast<float4*>(Sz + o) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    *reinterpret_cast<int4*>(pool_idx + o) = make_int4(pick[0], pick[1], pick[2], pick[3]);
+  }
+}
+
+template <typename IT>
+__global__ void __launch_bounds__(256) maxpool_bwd_cl4_kernel(PoolGeom g, const float* __restrict__ dmz,
+                                                              const float* __restrict__ dSz,
+                                                              const int32_t* __restrict__ pool_idx,
+                                                              float* __restrict__ dma, float* __restrict__ dSa) {
+  const int C4 = g.C >> 2;
+  const int64_t total = g.N * g.H * (int64_t)g.W * C4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+    IT q = (IT)e;
+    const int c = (int)(q % (IT)C4) * 4;
+    q /= (IT)C4;
+    const int w = (int)(q % (IT)g.W);
+    q /= (IT)g.W;
+    const int h = (int)(q % (IT)g.H);
+    const int64_t n = (int64_t)(q / (IT)g.H);
+    const int hp = h + g.p, wp = w + g.p;
+    const int ho_a = hp - g.k + 1 <= 0 ? 0 : (hp - g.k + 1 + g.s - 1) / g.s;
+    const int ho_b = min(hp / g.s, g.Ho - 1);
+    const int wo_a = wp - g.k + 1 <= 0 ? 0 : (wp - g.k + 1 + g.s - 1) / g.s;
+    const int wo_b = min(wp / g.s, g.Wo - 1);
+    const int32_t me = h * g.W + w;
+    float am[4] = {0.f, 0.f, 0.f, 0.f}, aS[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int ho = ho_a; ho <= ho_b; ++ho)
+      for (int wo = wo_a; wo <= wo_b; ++wo) {
+        const int64_t o = ((n * g.Ho + ho) * g.Wo + wo) * g.C + c;
+        const int4 p4 = *reinterpret_cast<const int4*>(pool_idx + o);
+        const int p[4] = {p4.x, p4.y, p4.z, p4.w};
+        if (p[0] != me && p[1] != me && p[2] != me && p[3] != me) continue;
+        const float4 m4 = *reinterpret_cast<const float4*>(dmz + o);
+        const float4 s4 = *reinterpret_cast<const float4*>(dSz + o);
+        const float m[4] = {m4.x, m4.y, m4.z, m4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (p[j] == me) {
+            am[j] += m[j];
+            aS[j] += sv[j];
+          }
+      }
+    *reinterpret_cast<float4*>(dma + e * 4) = make_float4(am[0], am[1], am[2], am[3]);
+    *reinterpret_cast<float4*>(dSa + e * 4) = make_float4(aS[0], aS[1], aS[2], aS[3]);
+  }
+}
+
+static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
 }  // namespace tagi
 
 using namespace tagi;
@@ -140,7 +230,15 @@ extern "C" int tagi_maxpool2d_fwd(const float* ma, const float* Sa, float* mz, f
   hipStream_t s = as_stream(stream);
   const int64_t out = N * C * (int64_t)g.Ho * g.Wo;
   ProfScope ps(FAM_MAXPOOL, s, 0.0, 4.0 * N * C * H * W + 12.0 * out);
-  if (out < (1ll << 32))
+  if (g.cl && C % 4 == 0 && al16(ma) && al16(Sa) && al16(mz) && al16(Sz) && al16(pool_idx)) {
+    const int64_t items = out / 4;
+    if (items < (1ll << 32))
+      hipLaunchKernelGGL(maxpool_fwd_cl4_kernel<uint32_t>, dim3(ew_blocks(items, 256)), dim3(256), 0, s, g, ma, Sa,
+                         mz, Sz, pool_idx);
+    else
+      hipLaunchKernelGGL(maxpool_fwd_cl4_kernel<int64_t>, dim3(ew_blocks(items, 256)), dim3(256), 0, s, g, ma, Sa,
+                         mz, Sz, pool_idx);
+  } else if (out < (1ll << 32))
     hipLaunchKernelGGL(maxpool_fwd_kernel<uint32_t>, dim3(ew_blocks(out, 256)), dim3(256), 0, s, g, ma, Sa, mz, Sz,
                        pool_idx);
   else
@@ -161,7 +259,15 @@ extern "C" int tagi_maxpool2d_bwd(const float* dmz, const float* dSz, const int3
   hipStream_t s = as_stream(stream);
   const int64_t total = N * C * H * W;
   ProfScope ps(FAM_MAXPOOL, s, 0.0, 12.0 * N * C * (int64_t)g.Ho * g.Wo + 8.0 * total);
-  if (total < (1ll << 32))
+  if (g.cl && C % 4 == 0 && al16(dmz) && al16(dSz) && al16(pool_idx) && al16(dma) && al16(dSa)) {
+    const int64_t items = total / 4;
+    if (items < (1ll << 32))
+      hipLaunchKernelGGL(maxpool_bwd_cl4_kernel<uint32_t>, dim3(ew_blocks(items, 256)), dim3(256), 0, s, g, dmz, dSz,
+                         pool_idx, dma, dSa);
+    else
+      hipLaunchKernelGGL(maxpool_bwd_cl4_kernel<int64_t>, dim3(ew_blocks(items, 256)), dim3(256), 0, s, g, dmz, dSz,
+                         pool_idx, dma, dSa);
+  } else if (total < (1ll << 32))
     hipLaunchKernelGGL(maxpool_bwd_kernel<uint32_t>, dim3(ew_blocks(total, 256)), dim3(256), 0, s, g, dmz, dSz,
                        pool_idx, dma, dSa);
   else
