@@ -543,8 +543,38 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   const int hl = lane >> 5;
   const int rl = lane & 31;
 
-  const int zq = blockIdx.y / g.splits;
-  const int split = blockIdx.y - zq * g.splits;
+  // Split-K launches with at least 8 split groups: every tile of one split group (the
+  // tiles that read the same stretch of the reduction) goes to one XCD. Workgroups are
+  // dealt round-robin over the 8 XCDs in linear-id order, so the linear id L is read as
+  // (XCD x = L mod 8, k-th block of that XCD) and group 8*(k / nt) + x, tile k mod nt
+  // are assigned; groups past the last multiple of 8 keep the plain order. Without this,
+  // the tiles of a group land on different XCDs and each XCD's L2 fetches the shared
+  // operand panels again (the parameter-delta GEMMs' 9 tap tiles share one pixel range).
+  int zq, split, bid;
+  bool xcd_tiles = true;
+  if (!g.phased && g.splits > 1 && gridDim.y >= 8 && (uint64_t)gridDim.x * gridDim.y < (1ull << 31)) {
+    const int nt0 = g.tiles_m * g.tiles_n;
+    const int L = blockIdx.x + blockIdx.y * gridDim.x;
+    const int g8 = (int)(gridDim.y & ~7u);
+    int grp, tile;
+    if (L < g8 * nt0) {
+      const int k = L >> 3, q = k / nt0;
+      grp = q * 8 + (L & 7);
+      tile = k - q * nt0;
+    } else {
+      const int L2 = L - g8 * nt0, q = L2 / nt0;
+      grp = g8 + q;
+      tile = L2 - q * nt0;
+    }
+    zq = grp / g.splits;
+    split = grp - zq * g.splits;
+    bid = tile;
+    xcd_tiles = false;
+  } else {
+    zq = blockIdx.y / g.splits;
+    split = blockIdx.y - zq * g.splits;
+    bid = blockIdx.x;
+  }
   const int z = g.phased ? (int)g.phase_order[zq] : zq;
   const int zz = z * g.splits + split;  // partial-sum slot
   const int R = rows_of(g, z);
@@ -555,10 +585,9 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   // consecutive block ids of one XCD onto consecutive tiles (shared operand panels stay
   // in that XCD's L2).
   const int nt = tiles_m * g.tiles_n;
-  const int bid = blockIdx.x;
   if (bid >= nt) return;  // phased launches size the grid for the largest phase
   const int per = nt >> 3;
-  const int t = (bid < (per << 3)) ? ((bid & 7) * per + (bid >> 3)) : bid;
+  const int t = (xcd_tiles && bid < (per << 3)) ? ((bid & 7) * per + (bid >> 3)) : bid;
   const int tmi = t / g.tiles_n;
   const int tni = t - tmi * g.tiles_n;
   const int m0 = tmi * BM;
