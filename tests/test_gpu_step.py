@@ -104,8 +104,11 @@ def _check_step(w, names, assert_scaled_close):
     assert torch.equal(pred, rpred), f"{w.name}: argmax differs on {(pred != rpred).sum().item()} rows"
 
 
-@pytest.mark.parametrize("name,batch", [("mlp", None), ("cnn", None), ("resnet18", 16), ("transformer", None)])
+@pytest.mark.parametrize("name,batch", [("mlp", None), ("cnn", None), ("resnet18", 16), ("transformer", None),
+                                        ("mlp", 1), ("mlp", 257), ("cnn", 3), ("transformer", 1)])
 def test_step_matches_oracle(dev, name, batch):
+    """Full-size workloads, plus edge batches: 1 (cap factor 0.1, one-row GEMMs), 257 (the
+    first batch with cap factor 3.0, ragged tiles), 3 (ragged conv tiles)."""
     from triton_tagi_amd import workloads
 
     w = workloads.build(name, device="cuda:0", batch=batch)
