@@ -327,20 +327,22 @@ def test_rmsnorm_embedding_pe(dev):
     assert_scaled_close(rms.delta_mw, ref.delta_mw, sc, RTOL, ATOL, "rms delta gamma")
     assert_scaled_close(rms.delta_Sw, ref.delta_Sw, None, RTOL, ATOL, "rms delta Sgamma")
 
-    for pad in (-1, 3):
-        emb = Embedding(17, 40, scale=0.25, padding_idx=pad, device="cpu")
+    # V = 17, D = 40: the per-category one-hot loader; V = 64, D = 256: four categories per
+    # chunk (the transformer block's table); V = 300: a vocabulary above 256 rows
+    for V, D, pad in ((17, 40, -1), (17, 40, 3), (64, 256, -1), (64, 256, 5), (300, 24, 7)):
+        emb = Embedding(V, D, scale=0.25, padding_idx=pad, device="cpu")
         eref = O.mirror(emb)
         emb.mw, emb.Sw = emb.mw.to(dev), emb.Sw.to(dev)
-        tok = torch.randint(0, 17, (6, 300), generator=r).to(torch.float32)
+        tok = torch.randint(0, V, (6, 300), generator=r).to(torch.float32)
         mz, Sz = emb.forward(tok.to(dev), torch.zeros_like(tok).to(dev))
         rm, rS = eref.forward(d64(tok), d64(tok) * 0)
         assert torch.equal(mz.cpu().double(), rm) and torch.equal(Sz.cpu().double(), rS)
-        dm, dS = torch.randn(6, 300, 40, generator=r), -torch.rand(6, 300, 40, generator=r)
+        dm, dS = torch.randn(6, 300, D, generator=r), -torch.rand(6, 300, D, generator=r)
         zm, zS = emb.backward(dm.to(dev), dS.to(dev))
         eref.backward(d64(dm), d64(dS))
         assert float(zm.abs().sum()) == 0.0 and tuple(zm.shape) == (6, 300)
-        sc = torch.zeros(17, 40, dtype=torch.float64).index_add_(
-            0, tok.long().reshape(-1), (d64(dm).reshape(-1, 40) * eref.Sw[tok.long().reshape(-1)]).abs())
+        sc = torch.zeros(V, D, dtype=torch.float64).index_add_(
+            0, tok.long().reshape(-1), (d64(dm).reshape(-1, D) * eref.Sw[tok.long().reshape(-1)]).abs())
         assert_scaled_close(emb.delta_mw, eref.delta_mw, sc, RTOL, ATOL, "emb delta mw")
         assert_scaled_close(emb.delta_Sw, eref.delta_Sw, None, RTOL, ATOL, "emb delta Sw")
 

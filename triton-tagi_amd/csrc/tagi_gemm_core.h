@@ -50,15 +50,20 @@ enum {
   LD_CFWD_B_S = 13,   // conv fwd weights, scalar (any Cout)
   LD_CBWD_BK4 = 14,   // input-delta weights read in place, w[((c*kk + kh)*kk + kw)*Cout + co]:
                       //   mn = c, k = (ikh,ikw,co), float4 along co (Cout % 4 == 0)
+  LD_ONEHOT4 = 15,    // embedding deltas: mn = category, k = token; 1.0 where token k (a float
+                      //   id, cast toward zero) is category mn, else 0; four categories per chunk
+  LD_ONEHOT_S = 16,   //   one category per chunk
 };
 
 template <int KIND>
 struct KindTraits {
   static constexpr bool mn_fast = (KIND == LD_STR_MN4 || KIND == LD_STR_MN_S || KIND == LD_CFWD_B4 ||
                                    KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CWG_A4 ||
-                                   KIND == LD_CWG_A_S || KIND == LD_CFWD_B_S);
+                                   KIND == LD_CWG_A_S || KIND == LD_CFWD_B_S || KIND == LD_ONEHOT4 ||
+                                   KIND == LD_ONEHOT_S);
   static constexpr bool vec4 = (KIND == LD_STR_MN4 || KIND == LD_STR_K4 || KIND == LD_CFWD_A4 || KIND == LD_CFWD_B4 ||
-                                KIND == LD_CBWD_A4 || KIND == LD_CBWD_B4 || KIND == LD_CWG_A4 || KIND == LD_CBWD_BK4);
+                                KIND == LD_CBWD_A4 || KIND == LD_CBWD_B4 || KIND == LD_CWG_A4 || KIND == LD_CBWD_BK4 ||
+                                KIND == LD_ONEHOT4);
 };
 
 // Exact division by an invariant d >= 1 for dividends 0 <= n < 2^31 (Granlund and
@@ -114,6 +119,7 @@ struct Operand {
   int64_t s_mn, s_k;       // strided kinds
   int MN, K;               // extents along the tile dim and the reduction
   int ones_row;            // tile index that reads as 1.0 for valid k (bias row), -1 = none
+  int64_t pad;             // one-hot kinds: category that reads as all zeros (-1 = none)
   ConvG g;                 // conv kinds
 };
 
@@ -316,6 +322,18 @@ struct Loader {
     for (int i = 0; i < NC; ++i) {
       const int mn = mn0 + cmn[i];
       const int k = k0 + ck[i];
+      if constexpr (KIND == LD_ONEHOT4 || KIND == LD_ONEHOT_S) {
+        // row r of the chunk is 1.0 when token k's category is mn + r (a valid, unpadded one)
+        int r = -1;
+        if (k < o.K) {
+          const int64_t cat = (int64_t)o.p0[k];
+          if (cat >= 0 && cat < o.MN && cat != o.pad) r = (int)(cat - mn);
+        }
+        if constexpr (V4) v[ST][0][i] = make_float4(r == 0 ? 1.f : 0.f, r == 1 ? 1.f : 0.f, r == 2 ? 1.f : 0.f,
+                                                     r == 3 ? 1.f : 0.f);
+        else v[ST][0][i] = r == 0 ? 1.f : 0.f;
+        continue;
+      }
       bool ok = false, one = false;
       int64_t off = 0;
       if constexpr (KIND == LD_STR_MN4 || KIND == LD_STR_MN_S || KIND == LD_STR_K_S) {

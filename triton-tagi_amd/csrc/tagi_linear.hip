@@ -115,3 +115,47 @@ extern "C" int tagi_linear_wgrad(const float* ma, const float* dmz, const float*
   if (v4) return run_gemm<PROD_SHARED_A, LD_STR_MN4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
   return run_gemm<PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
 }
+
+// ------------------------------------------------------------------- Embedding
+// Backward (embedding.py:111-145): delta_mw[cat, d] = sum over the category's tokens of
+// dmz[t, d] Sw[cat, d], and delta_Sw with dSz and Sw^2. Sw[cat, d] is the same for every
+// token of a category, so the raw sums are formed first and weighted once in the epilogue
+// (equal in exact arithmetic). The raw sums are the product of the tokens' one-hot matrix
+// with the deltas, O^T dmz and (O^2)^T dSz (O^2 = O): a parameter-delta product whose A
+// operand is generated from the token ids in the loader, run on the MFMA engine with a
+// deterministic split-K over the tokens. (A non-finite delta would reach the other
+// categories of its token's row through 0 * inf; deltas of a running step are finite.)
+static Plan embedding_bwd_plan(int64_t n_tokens, int64_t V, int64_t D) {
+  return choose_plan(V, D, n_tokens, 1, 2, true, 512);
+}
+
+extern "C" int64_t tagi_embedding_bwd_ws_bytes(int64_t n_tokens, int64_t V, int64_t D) {
+  if (n_tokens <= 0 || V <= 0 || D <= 0) return 0;
+  return plan_ws_bytes(embedding_bwd_plan(n_tokens, V, D), V, D, 1);
+}
+
+extern "C" int tagi_embedding_bwd(const float* tokens, const float* dmz, const float* dSz, const float* Sw, float* dmw,
+                                  float* dSw, int64_t n_tokens, int64_t V, int64_t D, int64_t padding_idx, float* ws,
+                                  int64_t ws_bytes, tagi_stream_t stream) {
+  const char* what = "tagi_embedding_bwd";
+  TAGI_REQUIRE(tokens && dmz && dSz && Sw && dmw && dSw, "%s: null pointer", what);
+  TAGI_REQUIRE(n_tokens > 0 && V > 0 && D > 0, "%s: bad sizes", what);
+  TAGI_REQUIRE(fits_i32(n_tokens * D) && fits_i32(V * D), "%s: too large for 32-bit tiles", what);
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_EMBEDDING, s, 0.0, 4.0 * n_tokens + 8.0 * n_tokens * D + 12.0 * V * D);
+  GemmArgs g{};
+  g.a = strided_operand(tokens, nullptr, 1, 0, 0, 1, 1, V, n_tokens);
+  g.a.pad = padding_idx;
+  g.b = strided_operand(dmz, dSz, 1, 0, 0, 1, D, D, n_tokens);
+  g.epi = epi_wgrad(dmw, dSw, nullptr, nullptr, Sw, nullptr, V, D);
+  g.R = (int)V;
+  g.C = (int)D;
+  g.Kred = (int)n_tokens;
+  Plan p = embedding_bwd_plan(n_tokens, V, D);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, V, D, 1))) p = choose_plan(V, D, n_tokens, 1, 2, false, 1);
+  const bool v4 = V % 4 == 0 && D % 4 == 0 && al16(dmz) && al16(dSz);
+  if (v4) return run_gemm<PROD_SHARED_A, LD_ONEHOT4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
+  if (D % 4 == 0 && al16(dmz) && al16(dSz))
+    return run_gemm<PROD_SHARED_A, LD_ONEHOT_S, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
+  return run_gemm<PROD_SHARED_A, LD_ONEHOT_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
+}

@@ -723,80 +723,6 @@ __global__ void __launch_bounds__(256) embedding_fwd_vec_kernel(const float* __r
   *reinterpret_cast<float4*>(Sz + t * D + d) = v;
 }
 
-// Backward (embedding.py:111-145): delta_mw[cat, d] = sum over the category's tokens of
-// dmz[t, d] Sw[cat, d], and delta_Sw with dSz and Sw^2. Sw[cat, d] is the same for every
-// token of a category, so the raw sums are formed first and weighted once at the end
-// (equal in exact arithmetic). grid (slabs of columns, chunks of tokens): a thread owns
-// column d of the slab and adds the chunk's deltas into an LDS table [2][V][slab], eight
-// tokens' loads in flight at a time; tokens outside [0, V) and the padding index add
-// nothing.
-__global__ void embedding_bwd_partial_kernel(const float* __restrict__ tokens, const float* __restrict__ dmz,
-                                             const float* __restrict__ dSz, float* __restrict__ ws, int64_t n_tokens,
-                                             int V, int D, int64_t padding_idx, int slab, int chunk) {
-  extern __shared__ float tab[];  // [2][V][slab]
-  const int d = blockIdx.x * slab + threadIdx.x;
-  const int64_t t0 = (int64_t)blockIdx.y * chunk;
-  const int n = (int)(min(n_tokens, t0 + chunk) - t0);
-  for (int i = threadIdx.x; i < 2 * V * slab; i += blockDim.x) tab[i] = 0.f;
-  __syncthreads();
-  if (threadIdx.x < slab && d < D) {
-    float* tm = tab + threadIdx.x;
-    float* ts = tab + V * slab + threadIdx.x;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-      float dm[8], ds[8];
-      int c[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int64_t t = t0 + i + u;
-        const int64_t cat = token_id(tokens[t]);
-        c[u] = (cat < 0 || cat >= V || cat == padding_idx) ? -1 : (int)cat;
-        dm[u] = dmz[t * D + d];
-        ds[u] = dSz[t * D + d];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (c[u] >= 0) {
-          tm[c[u] * slab] += dm[u];
-          ts[c[u] * slab] += ds[u];
-        }
-      }
-    }
-    for (; i < n; ++i) {
-      const int64_t t = t0 + i;
-      const int64_t cat = token_id(tokens[t]);
-      if (cat < 0 || cat >= V || cat == padding_idx) continue;
-      tm[cat * slab] += dmz[t * D + d];
-      ts[cat * slab] += dSz[t * D + d];
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x < slab && d < D) {
-    for (int v = 0; v < V; ++v) {
-      ws[(((int64_t)blockIdx.y * 2) * V + v) * D + d] = tab[v * slab + threadIdx.x];
-      ws[(((int64_t)blockIdx.y * 2 + 1) * V + v) * D + d] = tab[(V + v) * slab + threadIdx.x];
-    }
-  }
-}
-
-// Adds the chunk partials in chunk order and applies the Sw, Sw^2 weights.
-__global__ void embedding_bwd_finalize_kernel(const float* __restrict__ ws, const float* __restrict__ Sw,
-                                              float* __restrict__ dmw, float* __restrict__ dSw, int V, int D,
-                                              int nchunks) {
-  const int64_t total = (int64_t)V * D;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    float a = 0.f, b = 0.f;
-#pragma unroll 8
-    for (int k = 0; k < nchunks; ++k) {
-      a += ws[((int64_t)k * 2) * total + i];
-      b += ws[((int64_t)k * 2 + 1) * total + i];
-    }
-    const float sw = Sw[i];
-    dmw[i] = a * sw;
-    dSw[i] = b * (sw * sw);
-  }
-}
-
 // -------------------------------------------------------------------------- PE
 __global__ void pe_add_kernel(const float* __restrict__ ma, const float* __restrict__ pe, float* __restrict__ out,
                               int64_t total, int64_t SE) {
@@ -804,15 +730,6 @@ __global__ void pe_add_kernel(const float* __restrict__ ma, const float* __restr
     out[i] = ma[i] + pe[i % SE];
 }
 
-static inline void emb_plan(int64_t n_tokens, int64_t V, int64_t D, int* slab, int* chunk, int* nchunks) {
-  int s = (int)(65536 / (8 * V));
-  s = (s / 32) * 32;
-  if (s > 256) s = 256;
-  if (s > D) s = (int)(((D + 31) / 32) * 32);
-  *slab = s;
-  *chunk = 128;
-  *nchunks = (int)cdiv(n_tokens, 128);
-}
 
 }  // namespace tagi
 
@@ -1178,35 +1095,6 @@ extern "C" int tagi_embedding_fwd(const float* tokens, const float* mw, const fl
   else
     hipLaunchKernelGGL(embedding_fwd_kernel, dim3(ew_blocks(n_tokens * D, 256)), dim3(256), 0, s, tokens, mw, Sw, mz,
                        Sz, n_tokens, V, (int)D, padding_idx);
-  return check_launch(what);
-}
-
-extern "C" int64_t tagi_embedding_bwd_ws_bytes(int64_t n_tokens, int64_t V, int64_t D) {
-  if (n_tokens <= 0 || V <= 0 || D <= 0) return 0;
-  int slab, chunk, nch;
-  emb_plan(n_tokens, V, D, &slab, &chunk, &nch);
-  return (int64_t)nch * 2 * V * D * (int64_t)sizeof(float);
-}
-
-extern "C" int tagi_embedding_bwd(const float* tokens, const float* dmz, const float* dSz, const float* Sw, float* dmw,
-                                  float* dSw, int64_t n_tokens, int64_t V, int64_t D, int64_t padding_idx, float* ws,
-                                  int64_t ws_bytes, tagi_stream_t stream) {
-  const char* what = "tagi_embedding_bwd";
-  TAGI_REQUIRE(tokens && dmz && dSz && Sw && dmw && dSw, "%s: null pointer", what);
-  TAGI_REQUIRE(n_tokens > 0 && V > 0 && D > 0, "%s: bad sizes", what);
-  if (V > 256) return fail(TAGI_ERR_UNSUPPORTED, "%s: vocabularies above 256 rows", what);
-  TAGI_REQUIRE(ws && ws_bytes >= tagi_embedding_bwd_ws_bytes(n_tokens, V, D), "%s: workspace too small", what);
-  hipStream_t s = as_stream(stream);
-  ProfScope ps(FAM_EMBEDDING, s, 0.0, 4.0 * n_tokens + 8.0 * n_tokens * D + 8.0 * V * D);
-  int slab, chunk, nch;
-  emb_plan(n_tokens, V, D, &slab, &chunk, &nch);
-  const size_t lds = (size_t)2 * V * slab * sizeof(float);
-  hipLaunchKernelGGL(embedding_bwd_partial_kernel, dim3((unsigned)cdiv(D, slab), (unsigned)nch), dim3(slab), lds, s,
-                     tokens, dmz, dSz, ws, n_tokens, (int)V, (int)D, padding_idx, slab, chunk);
-  int rc = check_launch(what);
-  if (rc) return rc;
-  hipLaunchKernelGGL(embedding_bwd_finalize_kernel, dim3(ew_blocks(V * D, 256)), dim3(256), 0, s, (const float*)ws, Sw,
-                     dmw, dSw, (int)V, (int)D, nch);
   return check_launch(what);
 }
 
