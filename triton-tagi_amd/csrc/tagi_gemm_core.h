@@ -789,7 +789,25 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
       const int64_t coff = zoff + (int64_t)col * e.scol;
       float s0 = 0.f, s1 = 0.f, s2 = 0.f;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i) {
+        // Multiplier and addend of the lane's 16 outputs are loaded before any store: the
+        // addend may alias the output, so loads issued after a store could not be moved
+        // ahead of it and every element would wait for the previous one's store.
+        // (linear and batched products only: in the conv kernels the extra registers cost
+        // more occupancy than the loads gain)
+        constexpr bool PRE = KA <= LD_STR_K_S;
+        float jv[16], av0[16], av1[16];
+        if (PRE && (e.jm || e.am)) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+            const bool ok = row < R && cok;
+            const int64_t off = coff + (int64_t)row * e.srow;
+            jv[v] = (e.jm && ok) ? e.jm[off] : 1.f;
+            av0[v] = (e.am && ok) ? e.am[off] : 0.f;
+            av1[v] = (e.am && ok) ? e.av[off] : 0.f;
+          }
+        }
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
@@ -797,13 +815,13 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
             const int64_t off = coff + (int64_t)row * e.srow;
             float m = accM[i][j][v] * e.sm + bmj, vv = accV[i][j][v] * e.sv + bvj;
             if (e.jm) {
-              const float jj = e.jm[off];
+              const float jj = PRE ? jv[v] : e.jm[off];
               m *= jj;
               vv *= jj * jj;
             }
             if (e.am) {
-              m += e.am[off];
-              vv += e.av[off];
+              m += PRE ? av0[v] : e.am[off];
+              vv += PRE ? av1[v] : e.av[off];
             }
             if (e.om) e.om[off] = m;
             e.ov[off] = vv;
@@ -817,6 +835,7 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
             }
           }
         }
+      }
       if (st) {
         // lanes l and l + 32 hold the same column
         s0 += __shfl_xor(s0, 32, 64);
