@@ -198,8 +198,12 @@ struct Loader {
   static constexpr bool V4 = KindTraits<KIND>::vec4;
   static constexpr bool MNF = KindTraits<KIND>::mn_fast;
   static constexpr int W = V4 ? 4 : 1;  // elements per chunk
-  static constexpr int NC = BMN * BK / (W * NTH);
-  static_assert(NC * W * NTH == BMN * BK, "tile does not split evenly over threads");
+  static constexpr int NCH = BMN * BK / W;  // chunks in the tile
+  // fewer chunks than threads (a 32-wide operand of a 4-wave block): threads past NCH idle
+  static constexpr bool PART = NCH < NTH;
+  static constexpr int NC = PART ? 1 : NCH / NTH;
+  static_assert(PART ? (NCH * W == BMN * BK && NTH % NCH == 0) : (NC * W * NTH == BMN * BK),
+                "tile does not split evenly over threads");
   static constexpr int LD = BMN + 4;
 
   using Vt = typename std::conditional<V4, float4, float>::type;
@@ -214,10 +218,12 @@ struct Loader {
   FastDiv dnkw;              // divider for the phase's taps per row (conv input delta)
   int mnmax, kmax;           // extents checked by fetch (per phase for the conv input delta)
   int cmn[NC], ck[NC];       // chunk origin within the tile
+  bool active;               // this thread loads a chunk (always, unless PART)
   int64_t rowbase[NRB];      // batch offset (strided kinds) or per-chunk image base (conv rows)
   int r0[NR], r1[NR], r2[NR];
 
   __device__ __forceinline__ void map(int tid) {
+    active = !PART || tid < NCH;
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const int c = tid + i * NTH;
@@ -318,6 +324,9 @@ struct Loader {
   // multiply-high divisions; chunks outside the operand or in the zero padding read as 0.
   template <int ST = 0>
   __device__ __forceinline__ void fetch(const Operand& o, int z, int mn0, int k0) {
+    if constexpr (PART) {
+      if (!active) return;
+    }
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const int mn = mn0 + cmn[i];
@@ -407,6 +416,9 @@ struct Loader {
 
   template <int ST = 0>
   __device__ __forceinline__ void store(float* s) const {
+    if constexpr (PART) {
+      if (!active) return;
+    }
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
 #pragma unroll
@@ -1015,12 +1027,13 @@ using C128x64 = Cfg<128, 64, 64, 32>;    // 4 waves
 using C64x128 = Cfg<64, 128, 32, 64>;    // 4 waves
 using C64x64 = Cfg<64, 64, 32, 32>;      // 4 waves
 using C32x32 = Cfg<32, 32, 32, 32>;      // 1 wave
+using C128x32 = Cfg<128, 32, 32, 32>;    // 4 waves stacked along M (products with 32 columns)
 
 struct CfgDesc {
   int BM, BN;
 };
-static const CfgDesc kCfg[] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}, {32, 32}};
-static const int kNumCfg = 5;
+static const CfgDesc kCfg[] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}, {32, 32}, {128, 32}};
+static const int kNumCfg = 6;
 
 struct Plan {
   int cfg;
@@ -1046,11 +1059,11 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
                                         bool allow_split, int64_t max_splits, const int64_t* phase_k) {
   // resident blocks per CU (LDS / register limited), waves per block and sustained
   // fraction of peak, per config
-  static const int kBpc[] = {2, 3, 3, 4, 8};
-  static const int kWaves[] = {8, 4, 4, 4, 1};
-  static const double kEff[] = {0.65, 0.58, 0.61, 0.61, 0.33};
+  static const int kBpc[] = {2, 3, 3, 4, 8, 3};
+  static const int kWaves[] = {8, 4, 4, 4, 1, 4};
+  static const double kEff[] = {0.65, 0.58, 0.61, 0.61, 0.33, 0.50};
   const double kSplitSecPerByte = 9.65e-14, kSplitLaunch = 8.9e-6;
-  Plan best{kNumCfg - 1, 1, (int)Kred, 1, 1};
+  Plan best{4, 1, (int)Kred, 1, 1};
   double best_t = DBL_MAX;
   const double peak_cu = 157.3e12 / 256.0;
   const int64_t max_sp = allow_split ? (max_splits < 512 ? max_splits : 512) : 1;
@@ -1159,6 +1172,7 @@ static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, 
     case 1: launch_cfg<PROD, C128x64, KA, KB>(g, gx, gy, s); break;
     case 2: launch_cfg<PROD, C64x128, KA, KB>(g, gx, gy, s); break;
     case 3: launch_cfg<PROD, C64x64, KA, KB>(g, gx, gy, s); break;
+    case 5: launch_cfg<PROD, C128x32, KA, KB>(g, gx, gy, s); break;
     default: launch_cfg<PROD, C32x32, KA, KB>(g, gx, gy, s); break;
   }
   int rc = check_launch(what);
