@@ -79,11 +79,15 @@ def test_innovation_indexed_repeated_and_out_of_range_nodes(dev):
     assert torch.isnan(lm[1]).all() and torch.isnan(lS[1]).all() and not torch.isnan(lm[0]).any()
 
 
-@pytest.mark.parametrize("n_classes,B", [(2, 4), (10, 128), (100, 16), (1000, 8), (10000, 3)])
+# (10, 600) and (30, 300): several 256-row blocks of the row-per-thread kernel, the last
+# partial; 40 classes: the one-wavefront-per-row kernel; 100 and more: one block per row;
+# 10000 classes: a tree wider than that kernel's LDS table
+@pytest.mark.parametrize("n_classes,B", [(2, 4), (10, 128), (10, 600), (30, 300), (40, 70), (100, 16), (1000, 8),
+                                         (10000, 3)])
 def test_class_probs_and_predicted_labels(dev, n_classes, B):
     from triton_tagi_amd.hrc_softmax import class_to_obs, get_predicted_labels, obs_to_class_probs
 
-    h = class_to_obs(n_classes)  # 10000 classes: a tree wider than the kernel's LDS table
+    h = class_to_obs(n_classes)
     r = g(n_classes * 7 + B)
     ma = 0.8 * torch.randn(B, h.len, generator=r)
     Sa = 0.2 * torch.rand(B, h.len, generator=r)
@@ -97,6 +101,12 @@ def test_class_probs_and_predicted_labels(dev, n_classes, B):
     assert torch.equal(pred.cpu()[clear], R.argmax(1)[clear])
     # strongly positive nodes: class 0 (all bits 0) wins
     assert get_predicted_labels(torch.full((1, h.len), 10.0, device=dev), torch.zeros(1, h.len, device=dev), h).item() == 0
+    # a NaN node moment: the classes whose path uses it are NaN, and NaN is the largest
+    # value for the argmax, as in torch.argmax
+    ma[B // 2, h.len - 1] = float("nan")
+    P = obs_to_class_probs(ma.to(dev), Sa.to(dev), h).cpu()
+    assert P[B // 2].isnan().any() and not P[:B // 2].isnan().any()
+    assert torch.equal(get_predicted_labels(ma.to(dev), Sa.to(dev), h).cpu(), P.argmax(1))
 
 
 # ---------------------------------------------------------- heteroscedastic head

@@ -13,7 +13,9 @@ namespace tagi {
 // (y - mu)/(S + v) and -1/(S + v) at node idx[b, c] - 1, and zeros elsewhere
 // (observation.py:171-224). One thread per output element gathers the bits that select
 // it, in bit order: nodes selected twice add up as scatter_add does, and no memset or
-// atomic is needed. Node indices outside [1, n_out] select nothing.
+// atomic is needed. Node indices outside [1, n_out] select nothing. The grid covers one
+// element per thread up to 2^28 elements, so the dependent loads (label, class table,
+// moments) of many elements are in flight at once.
 //
 // LABELS: the bits come from class tables, obs/idx[label[b] * n_obs + c], with the
 // scalar noise v = sigma_v^2 (labels_to_hrc + torch.full_like at network.py:205-209
@@ -34,6 +36,8 @@ __global__ void __launch_bounds__(256) hrc_innovation_kernel(const float* __rest
     // IT = uint32_t when every flat index fits: 32-bit division is a short sequence
     const int64_t b = (int64_t)((IT)e / (IT)n_out);
     const int j = (int)(e - b * n_out);
+    // the moments are loaded up front so their latency overlaps the table lookups
+    const float mu = ma[e], S = Sa[e];
     const int32_t* ib;
     const float* yb;
     if constexpr (LABELS) {
@@ -50,15 +54,8 @@ __global__ void __launch_bounds__(256) hrc_innovation_kernel(const float* __rest
       yb = y_obs + b * n_obs;
     }
     float am = 0.f, aS = 0.f;
-    bool hit = false;
-    float mu = 0.f, S = 0.f;
     for (int c = 0; c < n_obs; ++c) {
       if (ib[c] - 1 != j) continue;
-      if (!hit) {
-        mu = ma[e];
-        S = Sa[e];
-        hit = true;
-      }
       const float v = LABELS ? var_scalar : var_obs[b * n_obs + c];
       const float den = S + v;
       am += (yb[c] - mu) / den;
@@ -72,9 +69,9 @@ __global__ void __launch_bounds__(256) hrc_innovation_kernel(const float* __rest
 // ------------------------------------------------------------ HRC class probabilities
 // P_z[i] = Phi(mu[i] / sqrt(1/alpha^2 + S[i])) per tree node, then for each class the
 // product along its path of P_z (bit +1) or 1 - P_z (bit -1) (hrc_softmax.py:164-208).
-// One block per sample row: node probabilities are formed once into LDS (up to
-// kHrcLds nodes; larger trees evaluate them per use), then threads take classes. With
-// `pred`, the block also writes the first index of the largest probability (a NaN
+// Large trees: one block per sample row; node probabilities are formed once into LDS (up
+// to kHrcLds nodes; larger trees evaluate them per use), then threads take classes. With
+// `pred`, each kernel also writes the first index of the largest probability (a NaN
 // counts as the largest, as torch's argmax treats it).
 constexpr int kHrcLds = 8192;
 
@@ -88,6 +85,65 @@ __device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi)
   if (vn != bn) return vn;
   if (!vn && v != bv) return v > bv;
   return i < bi;
+}
+
+// Small trees (padded node and class widths summing to at most kHrcRowLds / kHrcRows): one
+// thread per sample row, kHrcRows rows per block. The block reads its rows' node moments
+// with coalesced loads, forms each node probability once into LDS (row stride odd, so the
+// per-thread row reads do not conflict), and every thread walks the classes in order:
+// the table entries are the same for all lanes. Class probabilities go back through LDS so
+// the stores are coalesced too.
+constexpr int kHrcRows = 256;
+constexpr int kHrcRowLds = 64 * kHrcRows;  // floats of dynamic LDS at most (64 KiB)
+
+__host__ __device__ inline int odd_stride(int n) { return n | 1; }
+
+__global__ void __launch_bounds__(kHrcRows) hrc_class_probs_rows_kernel(const float* __restrict__ ma,
+                                                                        const float* __restrict__ Sa,
+                                                                        const float* __restrict__ obs,
+                                                                        const int32_t* __restrict__ idx,
+                                                                        float inv_a2, float* __restrict__ probs,
+                                                                        int64_t* __restrict__ pred, int64_t rows,
+                                                                        int n_out, int n_obs, int n_classes) {
+  extern __shared__ float lds[];
+  const int ldz = odd_stride(n_out), ldp = odd_stride(n_classes);
+  float* pz = lds;                      // [kHrcRows][ldz]
+  float* pc = lds + kHrcRows * ldz;     // [kHrcRows][ldp]
+  const int64_t b0 = (int64_t)blockIdx.x * kHrcRows;
+  const int nr = (int)min((int64_t)kHrcRows, rows - b0);
+  const int64_t base = b0 * n_out;
+  for (int e = threadIdx.x; e < nr * n_out; e += kHrcRows) {
+    const int r = e / n_out, j = e - r * n_out;
+    pz[r * ldz + j] = node_prob(ma[base + e], Sa[base + e], inv_a2);
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < nr) {
+    const float* z = pz + t * ldz;
+    float* out = pc + t * ldp;
+    float best_v = -__builtin_inff();
+    int64_t best_i = 0x7fffffffffffffffll;
+    for (int r = 0; r < n_classes; ++r) {
+      float p = 1.0f;
+      for (int c = 0; c < n_obs; ++c) {
+        const int node = idx[r * n_obs + c] - 1;
+        const float q = (node >= 0 && node < n_out) ? z[node] : 0.f;
+        p *= obs[r * n_obs + c] > 0.f ? q : 1.0f - q;
+      }
+      out[r] = p;
+      if (better(p, r, best_v, best_i)) {
+        best_v = p;
+        best_i = r;
+      }
+    }
+    if (pred != nullptr) pred[b0 + t] = best_i;
+  }
+  __syncthreads();
+  const int64_t obase = b0 * n_classes;
+  for (int e = threadIdx.x; e < nr * n_classes; e += kHrcRows) {
+    const int r = e / n_classes, k = e - r * n_classes;
+    probs[obase + e] = pc[r * ldp + k];
+  }
 }
 
 // Trees of at most 64 nodes and 64 classes: one wavefront per row, four rows per block.
@@ -292,6 +348,8 @@ using namespace tagi;
 
 static inline hipStream_t as_stream(tagi_stream_t s) { return (hipStream_t)s; }
 
+static unsigned hrc_blocks(int64_t total) { return (unsigned)std::min<int64_t>(cdiv(total, 256), 1ll << 20); }
+
 extern "C" int tagi_innovation_indexed(const float* ma, const float* Sa, const float* y_obs, const float* var_obs,
                                        const int32_t* idx, float* dm, float* dS, int64_t rows, int64_t n_out,
                                        int64_t n_obs, tagi_stream_t stream) {
@@ -303,11 +361,11 @@ extern "C" int tagi_innovation_indexed(const float* ma, const float* Sa, const f
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_INNOVATION, s, 0.0, 8.0 * rows * n_out + 12.0 * rows * n_obs + 8.0 * rows * n_out);
   if (rows * n_out < (1ll << 32))
-    hipLaunchKernelGGL((hrc_innovation_kernel<false, uint32_t>), dim3(ew_blocks(rows * n_out, 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL((hrc_innovation_kernel<false, uint32_t>), dim3(hrc_blocks(rows * n_out)), dim3(256), 0, s,
                        ma, Sa, y_obs, var_obs, idx, (const int64_t*)nullptr, (int64_t)0, 0.0f, dm, dS, rows,
                        (int)n_out, (int)n_obs);
   else
-    hipLaunchKernelGGL((hrc_innovation_kernel<false, int64_t>), dim3(ew_blocks(rows * n_out, 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL((hrc_innovation_kernel<false, int64_t>), dim3(hrc_blocks(rows * n_out)), dim3(256), 0, s,
                        ma, Sa, y_obs, var_obs, idx, (const int64_t*)nullptr, (int64_t)0, 0.0f, dm, dS, rows,
                        (int)n_out, (int)n_obs);
   return check_launch(what);
@@ -324,11 +382,11 @@ extern "C" int tagi_hrc_innovation(const float* ma, const float* Sa, const int64
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_INNOVATION, s, 0.0, 16.0 * rows * n_out + 8.0 * rows);
   if (rows * n_out < (1ll << 32))
-    hipLaunchKernelGGL((hrc_innovation_kernel<true, uint32_t>), dim3(ew_blocks(rows * n_out, 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL((hrc_innovation_kernel<true, uint32_t>), dim3(hrc_blocks(rows * n_out)), dim3(256), 0, s,
                        ma, Sa, obs, (const float*)nullptr, idx, labels, n_classes, sigma_v2, dm, dS, rows, (int)n_out,
                        (int)n_obs);
   else
-    hipLaunchKernelGGL((hrc_innovation_kernel<true, int64_t>), dim3(ew_blocks(rows * n_out, 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL((hrc_innovation_kernel<true, int64_t>), dim3(hrc_blocks(rows * n_out)), dim3(256), 0, s,
                        ma, Sa, obs, (const float*)nullptr, idx, labels, n_classes, sigma_v2, dm, dS, rows, (int)n_out,
                        (int)n_obs);
   return check_launch(what);
@@ -345,8 +403,13 @@ extern "C" int tagi_hrc_class_probs(const float* ma, const float* Sa, const floa
   TAGI_REQUIRE(rows < (1ll << 31), "%s: more than 2^31 rows", what);
   TAGI_REQUIRE(ma && Sa && obs && idx && probs, "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
-  ProfScope ps(FAM_INNOVATION, s, 0.0, 8.0 * rows * n_out + 4.0 * rows * n_classes);
-  if (n_out <= 64 && n_classes <= 64)
+  ProfScope ps(FAM_INNOVATION, s, 0.0, 8.0 * rows * n_out + 4.0 * rows * n_classes + (pred ? 8.0 * rows : 0.0));
+  const int64_t lds_floats = (int64_t)kHrcRows * (odd_stride((int)n_out) + odd_stride((int)n_classes));
+  if (lds_floats <= kHrcRowLds && (int64_t)n_classes * n_obs < (1ll << 31))
+    hipLaunchKernelGGL(hrc_class_probs_rows_kernel, dim3((unsigned)cdiv(rows, kHrcRows)), dim3(kHrcRows),
+                       (size_t)lds_floats * sizeof(float), s, ma, Sa, obs, idx, 1.0f / (alpha * alpha), probs, pred,
+                       rows, (int)n_out, (int)n_obs, (int)n_classes);
+  else if (n_out <= 64 && n_classes <= 64)
     hipLaunchKernelGGL(hrc_class_probs_wave_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, ma, Sa, obs, idx,
                        1.0f / (alpha * alpha), probs, pred, rows, (int)n_out, (int)n_obs, (int)n_classes);
   else
