@@ -198,12 +198,15 @@ def test_innovation_update_add_jacobian(dev):
     assert_scaled_close(oS, d64(b[:333]) * d64(J) ** 2, None, RTOL, ATOL, "jacobian var")
 
 
-@pytest.mark.parametrize("k,sc", [(2, False), (4, False), (2, True), (3, False)])
-def test_avgpool(dev, k, sc):
+# C = 8: float4 along the channels; 13 x 13 with k = 2 or 3: a partial last window row
+# and column, whose input positions receive zero deltas
+@pytest.mark.parametrize("k,sc,C,HW", [(2, False, 5, 12), (4, False, 5, 12), (2, True, 5, 12), (3, False, 5, 12),
+                                       (2, False, 8, 12), (2, True, 8, 13), (3, False, 8, 13), (3, False, 5, 13)])
+def test_avgpool(dev, k, sc, C, HW):
     from triton_tagi_amd.layers.avgpool2d import AvgPool2D
 
-    r = g(k)
-    ma, Sa = torch.randn(3, 5, 12, 12, generator=r), torch.rand(3, 5, 12, 12, generator=r)
+    r = g(k + C + HW)
+    ma, Sa = torch.randn(3, C, HW, HW, generator=r), torch.rand(3, C, HW, HW, generator=r)
     layer, ref = AvgPool2D(k, sc), O.OAvgPool2D(k, sc)
     mo, So = layer.forward(ma.to(dev), Sa.to(dev))
     rm, rS = ref.forward(d64(ma), d64(Sa))

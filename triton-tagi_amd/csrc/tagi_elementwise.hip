@@ -207,53 +207,86 @@ __global__ void add_kernel(const float* __restrict__ ms, const float* __restrict
 }
 
 // -------------------------------------------------------------------- AvgPool2D
-// Channels-last: one lane per (output pixel, channel); consecutive lanes walk channels,
-// so every window read is a coalesced row of C floats.
-__global__ void avgpool_fwd_kernel(const float* __restrict__ ma, const float* __restrict__ Sa,
-                                   float* __restrict__ mo, float* __restrict__ So, int64_t N, int H, int W, int C,
-                                   int k, float inv_k2, float var_scale) {
-  const int Ho = H / k, Wo = W / k;
-  const int64_t total = N * Ho * Wo * C;
-  for_each_vec(total, [&](int64_t i) {
-    const int c = (int)(i % C);
-    const int64_t pix = i / C;
-    const int64_t n = pix / (Ho * Wo);
-    const int r = (int)(pix - n * (Ho * Wo));
-    const int oh = r / Wo, ow = r - (r / Wo) * Wo;
-    const int64_t base = ((n * H + (int64_t)oh * k) * W + (int64_t)ow * k) * C + c;
-    float sm = 0.f, ss = 0.f;
-    for (int a = 0; a < k; ++a)
-      for (int b = 0; b < k; ++b) {
-        const int64_t off = base + ((int64_t)a * W + b) * C;
-        sm += ma[off];
-        ss += Sa[off];
+// Channels-last: one lane per (output pixel, group of V channels); consecutive lanes walk
+// channels, so every window read is a coalesced row of C floats. V = 4 moves float4 when
+// C % 4 == 0 and the pointers are 16-byte aligned; IT = uint32_t when every flat index of
+// the input fits in 31 bits (the index decode is then 32-bit division). Each component
+// sums its window in the same (row, column) order for every V, so the results do not
+// depend on the vector width.
+template <int V>
+struct vec_of;
+template <>
+struct vec_of<1> {
+  using T = float;
+  static __device__ __forceinline__ T zero() { return 0.f; }
+  static __device__ __forceinline__ void add(T& a, T b) { a += b; }
+  static __device__ __forceinline__ T scale(T a, float s) { return a * s; }
+};
+template <>
+struct vec_of<4> {
+  using T = float4;
+  static __device__ __forceinline__ T zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+  static __device__ __forceinline__ void add(T& a, T b) {
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+  }
+  static __device__ __forceinline__ T scale(T a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
+};
+
+template <typename IT, int V>
+__global__ void __launch_bounds__(256) avgpool_fwd_kernel(const float* __restrict__ ma, const float* __restrict__ Sa,
+                                                          float* __restrict__ mo, float* __restrict__ So, IT N, IT H,
+                                                          IT W, IT C, IT k, float inv_k2, float var_scale) {
+  using VO = vec_of<V>;
+  using T = typename VO::T;
+  const T* m = reinterpret_cast<const T*>(ma);
+  const T* S = reinterpret_cast<const T*>(Sa);
+  const IT Ho = H / k, Wo = W / k, Cv = C / V;
+  const IT total = N * Ho * Wo * Cv;
+  const IT stride = (IT)gridDim.x * blockDim.x;
+  for (IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const IT c = i % Cv, pix = i / Cv;
+    const IT ow = pix % Wo, t = pix / Wo;
+    const IT oh = t % Ho, n = t / Ho;
+    const IT base = ((n * H + oh * k) * W + ow * k) * Cv + c;
+    T sm = VO::zero(), ss = VO::zero();
+    for (IT a = 0; a < k; ++a)
+      for (IT b = 0; b < k; ++b) {
+        const IT off = base + (a * W + b) * Cv;
+        VO::add(sm, m[off]);
+        VO::add(ss, S[off]);
       }
-    mo[i] = sm * inv_k2;
-    So[i] = ss * var_scale;
-  });
+    reinterpret_cast<T*>(mo)[i] = VO::scale(sm, inv_k2);
+    reinterpret_cast<T*>(So)[i] = VO::scale(ss, var_scale);
+  }
 }
 
-__global__ void avgpool_bwd_kernel(const float* __restrict__ dm, const float* __restrict__ dS,
-                                   float* __restrict__ om, float* __restrict__ oS, int64_t N, int H, int W, int C,
-                                   int k, float inv_k2, float var_scale) {
-  const int Ho = H / k, Wo = W / k;
-  const int64_t total = N * H * W * C;
-  for_each_vec(total, [&](int64_t i) {
-    const int c = (int)(i % C);
-    const int64_t pix = i / C;
-    const int64_t n = pix / (H * W);
-    const int r = (int)(pix - n * (H * W));
-    const int h = r / W, w = r - (r / W) * W;
-    const int oh = h / k, ow = w / k;
+// Input positions past the last whole window (H % k rows, W % k columns) receive zeros.
+template <typename IT, int V>
+__global__ void __launch_bounds__(256) avgpool_bwd_kernel(const float* __restrict__ dm, const float* __restrict__ dS,
+                                                          float* __restrict__ om, float* __restrict__ oS, IT N, IT H,
+                                                          IT W, IT C, IT k, float inv_k2, float var_scale) {
+  using VO = vec_of<V>;
+  using T = typename VO::T;
+  const IT Ho = H / k, Wo = W / k, Cv = C / V;
+  const IT total = N * H * W * Cv;
+  const IT stride = (IT)gridDim.x * blockDim.x;
+  for (IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const IT c = i % Cv, pix = i / Cv;
+    const IT w = pix % W, t = pix / W;
+    const IT h = t % H, n = t / H;
+    const IT oh = h / k, ow = w / k;
+    T a = VO::zero(), b = VO::zero();
     if (oh < Ho && ow < Wo) {
-      const int64_t j = ((n * Ho + oh) * Wo + ow) * C + c;
-      om[i] = dm[j] * inv_k2;
-      oS[i] = dS[j] * var_scale;
-    } else {
-      om[i] = 0.f;
-      oS[i] = 0.f;
+      const IT j = ((n * Ho + oh) * Wo + ow) * Cv + c;
+      a = VO::scale(reinterpret_cast<const T*>(dm)[j], inv_k2);
+      b = VO::scale(reinterpret_cast<const T*>(dS)[j], var_scale);
     }
-  });
+    reinterpret_cast<T*>(om)[i] = a;
+    reinterpret_cast<T*>(oS)[i] = b;
+  }
 }
 
 // ------------------------------------------------------------------------ Remax
@@ -471,6 +504,36 @@ extern "C" int tagi_add_inplace(const float* mu_s, const float* var_s, float* mu
   return check_launch("tagi_add_inplace");
 }
 
+template <bool FWD, typename IT, int V>
+static void launch_avgpool_as(const float* a, const float* b, float* c, float* d, IT N, IT C, IT H, IT W, IT k,
+                              float var_scale, unsigned blocks, hipStream_t s) {
+  const float inv_k2 = 1.0f / (float)(k * k);
+  if constexpr (FWD)
+    hipLaunchKernelGGL((avgpool_fwd_kernel<IT, V>), dim3(blocks), dim3(256), 0, s, a, b, c, d, N, H, W, C, k, inv_k2,
+                       var_scale);
+  else
+    hipLaunchKernelGGL((avgpool_bwd_kernel<IT, V>), dim3(blocks), dim3(256), 0, s, a, b, c, d, N, H, W, C, k, inv_k2,
+                       var_scale);
+}
+
+template <bool FWD>
+static void launch_avgpool(const float* a, const float* b, float* c, float* d, int64_t N, int64_t C, int64_t H,
+                           int64_t W, int64_t k, float var_scale, int64_t items, hipStream_t s) {
+  const bool v4 = C % 4 == 0 && aligned16(a) && aligned16(b) && aligned16(c) && aligned16(d);
+  const bool small = N * C * H * W < (1ll << 31);
+  const unsigned blocks = ew_blocks(v4 ? items / 4 : items, 256);
+  if (small && v4)
+    launch_avgpool_as<FWD, uint32_t, 4>(a, b, c, d, (uint32_t)N, (uint32_t)C, (uint32_t)H, (uint32_t)W, (uint32_t)k,
+                                        var_scale, blocks, s);
+  else if (small)
+    launch_avgpool_as<FWD, uint32_t, 1>(a, b, c, d, (uint32_t)N, (uint32_t)C, (uint32_t)H, (uint32_t)W, (uint32_t)k,
+                                        var_scale, blocks, s);
+  else if (v4)
+    launch_avgpool_as<FWD, int64_t, 4>(a, b, c, d, N, C, H, W, k, var_scale, blocks, s);
+  else
+    launch_avgpool_as<FWD, int64_t, 1>(a, b, c, d, N, C, H, W, k, var_scale, blocks, s);
+}
+
 extern "C" int tagi_avgpool2d_fwd(const float* ma, const float* Sa, float* ma_out, float* Sa_out, int64_t N,
                                   int64_t C, int64_t H, int64_t W, int64_t k, float var_scale, tagi_stream_t stream) {
   TAGI_REQUIRE(ma && Sa && ma_out && Sa_out, "tagi_avgpool2d_fwd: null pointer");
@@ -478,8 +541,7 @@ extern "C" int tagi_avgpool2d_fwd(const float* ma, const float* Sa, float* ma_ou
   hipStream_t s = as_stream(stream);
   const int64_t out = N * C * (H / k) * (W / k);
   ProfScope ps(FAM_AVGPOOL, s, 0.0, 8.0 * (N * C * H * W + out));
-  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(ew_blocks(out, 256)), dim3(256), 0, s, ma, Sa, ma_out, Sa_out, N, (int)H,
-                     (int)W, (int)C, (int)k, 1.0f / (float)(k * k), var_scale);
+  launch_avgpool<true>(ma, Sa, ma_out, Sa_out, N, C, H, W, k, var_scale, out, s);
   return check_launch("tagi_avgpool2d_fwd");
 }
 
@@ -490,8 +552,7 @@ extern "C" int tagi_avgpool2d_bwd(const float* dm, const float* dS, float* dm_ou
   hipStream_t s = as_stream(stream);
   const int64_t total = N * C * H * W;
   ProfScope ps(FAM_AVGPOOL, s, 0.0, 8.0 * (total + N * C * (H / k) * (W / k)));
-  hipLaunchKernelGGL(avgpool_bwd_kernel, dim3(ew_blocks(total, 256)), dim3(256), 0, s, dm, dS, dm_out, dS_out, N,
-                     (int)H, (int)W, (int)C, (int)k, 1.0f / (float)(k * k), var_scale);
+  launch_avgpool<false>(dm, dS, dm_out, dS_out, N, C, H, W, k, var_scale, total, s);
   return check_launch("tagi_avgpool2d_bwd");
 }
 
