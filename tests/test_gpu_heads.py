@@ -36,7 +36,9 @@ def mscale(ref):
 
 
 # -------------------------------------------------------------------- HRC kernels
-@pytest.mark.parametrize("n_classes,B", [(2, 5), (10, 256), (100, 33), (1000, 64)])
+# fewer than 32 outputs: one thread per row in 256-row blocks ((28, 700): 31 outputs, three
+# blocks, the last partial); wider outputs: one thread per output element
+@pytest.mark.parametrize("n_classes,B", [(2, 5), (10, 256), (28, 700), (100, 33), (1000, 64)])
 def test_innovation_indexed_and_labels(dev, n_classes, B):
     from triton_tagi_amd.hrc_softmax import class_to_obs, labels_to_hrc
     from triton_tagi_amd.update.observation import compute_innovation_with_indices, hrc_innovation

@@ -66,6 +66,77 @@ __global__ void __launch_bounds__(256) hrc_innovation_kernel(const float* __rest
   }
 }
 
+// Small trees (fewer than 32 nodes): one thread per sample row, kHrcRows rows per
+// block. Each thread adds its row's bits, in bit order, into the row's slots in LDS (the
+// same sums as the kernel above, in the same order), then the block writes its rows with
+// coalesced stores.
+constexpr int kHrcRows = 256;
+constexpr int kHrcRowLds = 64 * kHrcRows;  // floats of dynamic LDS at most (64 KiB)
+
+__host__ __device__ inline int odd_stride(int n) { return n | 1; }
+
+template <bool LABELS>
+__global__ void __launch_bounds__(kHrcRows) hrc_innovation_rows_kernel(const float* __restrict__ ma,
+                                                                       const float* __restrict__ Sa,
+                                                                       const float* __restrict__ y_obs,
+                                                                       const float* __restrict__ var_obs,
+                                                                       const int32_t* __restrict__ idx,
+                                                                       const int64_t* __restrict__ labels,
+                                                                       int64_t n_classes, float var_scalar,
+                                                                       float* __restrict__ dm, float* __restrict__ dS,
+                                                                       int64_t rows, int n_out, int n_obs) {
+  extern __shared__ float lds[];
+  const int ldz = odd_stride(n_out);
+  float* om = lds;                   // [kHrcRows][ldz]
+  float* oS = lds + kHrcRows * ldz;  // [kHrcRows][ldz]
+  const int64_t b0 = (int64_t)blockIdx.x * kHrcRows;
+  const int nr = (int)min((int64_t)kHrcRows, rows - b0);
+  for (int e = threadIdx.x; e < kHrcRows * ldz; e += kHrcRows) {
+    om[e] = 0.f;
+    oS[e] = 0.f;
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < nr) {
+    const int64_t b = b0 + t;
+    float* rm = om + t * ldz;
+    float* rS = oS + t * ldz;
+    int64_t tab = b;  // the row of the bit tables
+    bool bad = false;
+    if constexpr (LABELS) {
+      const int64_t lab = labels[b];
+      bad = lab < 0 || lab >= n_classes;
+      tab = bad ? 0 : lab;
+    }
+    const int32_t* ib = idx + tab * n_obs;
+    const float* yb = y_obs + tab * n_obs;
+    if (bad) {
+      for (int j = 0; j < n_out; ++j) {
+        rm[j] = __builtin_nanf("");
+        rS[j] = __builtin_nanf("");
+      }
+    } else {
+      const float* mb = ma + b * n_out;
+      const float* sb = Sa + b * n_out;
+      for (int c = 0; c < n_obs; ++c) {
+        const int node = ib[c] - 1;
+        if (node < 0 || node >= n_out) continue;
+        const float v = LABELS ? var_scalar : var_obs[b * n_obs + c];
+        const float den = sb[node] + v;
+        rm[node] += (yb[c] - mb[node]) / den;
+        rS[node] += -1.0f / den;
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t base = b0 * n_out;
+  for (int e = threadIdx.x; e < nr * n_out; e += kHrcRows) {
+    const int r = e / n_out, j = e - r * n_out;
+    dm[base + e] = om[r * ldz + j];
+    dS[base + e] = oS[r * ldz + j];
+  }
+}
+
 // ------------------------------------------------------------ HRC class probabilities
 // P_z[i] = Phi(mu[i] / sqrt(1/alpha^2 + S[i])) per tree node, then for each class the
 // product along its path of P_z (bit +1) or 1 - P_z (bit -1) (hrc_softmax.py:164-208).
@@ -87,17 +158,12 @@ __device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi)
   return i < bi;
 }
 
-// Small trees (padded node and class widths summing to at most kHrcRowLds / kHrcRows): one
-// thread per sample row, kHrcRows rows per block. The block reads its rows' node moments
+// Small trees (odd-padded node and class widths summing to at most 64): one thread per
+// sample row, kHrcRows rows per block. The block reads its rows' node moments
 // with coalesced loads, forms each node probability once into LDS (row stride odd, so the
 // per-thread row reads do not conflict), and every thread walks the classes in order:
 // the table entries are the same for all lanes. Class probabilities go back through LDS so
 // the stores are coalesced too.
-constexpr int kHrcRows = 256;
-constexpr int kHrcRowLds = 64 * kHrcRows;  // floats of dynamic LDS at most (64 KiB)
-
-__host__ __device__ inline int odd_stride(int n) { return n | 1; }
-
 __global__ void __launch_bounds__(kHrcRows) hrc_class_probs_rows_kernel(const float* __restrict__ ma,
                                                                         const float* __restrict__ Sa,
                                                                         const float* __restrict__ obs,
@@ -350,6 +416,21 @@ static inline hipStream_t as_stream(tagi_stream_t s) { return (hipStream_t)s; }
 
 static unsigned hrc_blocks(int64_t total) { return (unsigned)std::min<int64_t>(cdiv(total, 256), 1ll << 20); }
 
+// The row-per-thread innovation kernel holds two (256 x odd-padded width) float tables in LDS.
+static bool hrc_rows_fit(int64_t rows, int64_t n_out) {
+  return rows < (1ll << 31) && n_out < 32 && 2ll * kHrcRows * odd_stride((int)n_out) <= kHrcRowLds;
+}
+
+template <bool LABELS>
+static void launch_hrc_rows(const float* ma, const float* Sa, const float* y_obs, const float* var_obs,
+                            const int32_t* idx, const int64_t* labels, int64_t n_classes, float var_scalar, float* dm,
+                            float* dS, int64_t rows, int64_t n_out, int64_t n_obs, hipStream_t s) {
+  const size_t lds = 2ull * kHrcRows * odd_stride((int)n_out) * sizeof(float);
+  hipLaunchKernelGGL((hrc_innovation_rows_kernel<LABELS>), dim3((unsigned)cdiv(rows, kHrcRows)), dim3(kHrcRows), lds,
+                     s, ma, Sa, y_obs, var_obs, idx, labels, n_classes, var_scalar, dm, dS, rows, (int)n_out,
+                     (int)n_obs);
+}
+
 extern "C" int tagi_innovation_indexed(const float* ma, const float* Sa, const float* y_obs, const float* var_obs,
                                        const int32_t* idx, float* dm, float* dS, int64_t rows, int64_t n_out,
                                        int64_t n_obs, tagi_stream_t stream) {
@@ -360,7 +441,9 @@ extern "C" int tagi_innovation_indexed(const float* ma, const float* Sa, const f
   TAGI_REQUIRE(ma && Sa && dm && dS && (n_obs == 0 || (y_obs && var_obs && idx)), "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_INNOVATION, s, 0.0, 8.0 * rows * n_out + 12.0 * rows * n_obs + 8.0 * rows * n_out);
-  if (rows * n_out < (1ll << 32))
+  if (hrc_rows_fit(rows, n_out))
+    launch_hrc_rows<false>(ma, Sa, y_obs, var_obs, idx, nullptr, 0, 0.0f, dm, dS, rows, n_out, n_obs, s);
+  else if (rows * n_out < (1ll << 32))
     hipLaunchKernelGGL((hrc_innovation_kernel<false, uint32_t>), dim3(hrc_blocks(rows * n_out)), dim3(256), 0, s,
                        ma, Sa, y_obs, var_obs, idx, (const int64_t*)nullptr, (int64_t)0, 0.0f, dm, dS, rows,
                        (int)n_out, (int)n_obs);
@@ -381,7 +464,9 @@ extern "C" int tagi_hrc_innovation(const float* ma, const float* Sa, const int64
   TAGI_REQUIRE(ma && Sa && labels && obs && idx && dm && dS, "%s: null pointer", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_INNOVATION, s, 0.0, 16.0 * rows * n_out + 8.0 * rows);
-  if (rows * n_out < (1ll << 32))
+  if (hrc_rows_fit(rows, n_out))
+    launch_hrc_rows<true>(ma, Sa, obs, nullptr, idx, labels, n_classes, sigma_v2, dm, dS, rows, n_out, n_obs, s);
+  else if (rows * n_out < (1ll << 32))
     hipLaunchKernelGGL((hrc_innovation_kernel<true, uint32_t>), dim3(hrc_blocks(rows * n_out)), dim3(256), 0, s,
                        ma, Sa, obs, (const float*)nullptr, idx, labels, n_classes, sigma_v2, dm, dS, rows, (int)n_out,
                        (int)n_obs);
