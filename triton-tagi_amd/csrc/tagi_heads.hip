@@ -118,13 +118,29 @@ __global__ void __launch_bounds__(kHrcRows) hrc_innovation_rows_kernel(const flo
     } else {
       const float* mb = ma + b * n_out;
       const float* sb = Sa + b * n_out;
-      for (int c = 0; c < n_obs; ++c) {
-        const int node = ib[c] - 1;
-        if (node < 0 || node >= n_out) continue;
-        const float v = LABELS ? var_scalar : var_obs[b * n_obs + c];
-        const float den = sb[node] + v;
-        rm[node] += (yb[c] - mb[node]) / den;
-        rS[node] += -1.0f / den;
+      // up to kU bits at a time: their loads are issued together, then the sums are added
+      // in bit order
+      constexpr int kU = 8;
+      for (int c0 = 0; c0 < n_obs; c0 += kU) {
+        int node[kU];
+        float mu[kU], S[kU], y[kU], v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          const int c = c0 + u;
+          node[u] = c < n_obs ? ib[c] - 1 : -1;
+          const bool ok = node[u] >= 0 && node[u] < n_out;
+          mu[u] = ok ? mb[node[u]] : 0.f;
+          S[u] = ok ? sb[node[u]] : 0.f;
+          y[u] = ok ? yb[c] : 0.f;
+          v[u] = ok ? (LABELS ? var_scalar : var_obs[b * n_obs + c]) : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          if (node[u] < 0 || node[u] >= n_out) continue;
+          const float den = S[u] + v[u];
+          rm[node[u]] += (y[u] - mu[u]) / den;
+          rS[node[u]] += -1.0f / den;
+        }
       }
     }
   }
