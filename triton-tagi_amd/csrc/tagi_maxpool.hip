@@ -177,6 +177,43 @@ __global__ void __launch_bounds__(256) maxpool_bwd_cl4_kernel(PoolGeom g, const 
     const int wo_b = min(wp / g.s, g.Wo - 1);
     const int32_t me = h * g.W + w;
     float am[4] = {0.f, 0.f, 0.f, 0.f}, aS[4] = {0.f, 0.f, 0.f, 0.f};
+    if (g.k <= 2 * g.s) {
+      // at most 2 x 2 windows cover a position: the indices and deltas of all of them are
+      // loaded at once, then the matching ones are added in the (ho, wo) order of the loop
+      // below
+      int4 p4[2][2];
+      float4 m4[2][2], s4[2][2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          p4[i][j] = make_int4(-1, -1, -1, -1);
+          m4[i][j] = s4[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (ho_a + i <= ho_b && wo_a + j <= wo_b) {
+            const int64_t o = ((n * g.Ho + ho_a + i) * g.Wo + wo_a + j) * g.C + c;
+            p4[i][j] = *reinterpret_cast<const int4*>(pool_idx + o);
+            m4[i][j] = *reinterpret_cast<const float4*>(dmz + o);
+            s4[i][j] = *reinterpret_cast<const float4*>(dSz + o);
+          }
+        }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int p[4] = {p4[i][j].x, p4[i][j].y, p4[i][j].z, p4[i][j].w};
+          const float m[4] = {m4[i][j].x, m4[i][j].y, m4[i][j].z, m4[i][j].w};
+          const float sv[4] = {s4[i][j].x, s4[i][j].y, s4[i][j].z, s4[i][j].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (p[q] == me) {
+              am[q] += m[q];
+              aS[q] += sv[q];
+            }
+        }
+      *reinterpret_cast<float4*>(dma + e * 4) = make_float4(am[0], am[1], am[2], am[3]);
+      *reinterpret_cast<float4*>(dSa + e * 4) = make_float4(aS[0], aS[1], aS[2], aS[3]);
+      continue;
+    }
     for (int ho = ho_a; ho <= ho_b; ++ho)
       for (int wo = wo_a; wo <= wo_b; ++wo) {
         const int64_t o = ((n * g.Ho + ho) * g.Wo + wo) * g.C + c;
@@ -199,6 +236,10 @@ __global__ void __launch_bounds__(256) maxpool_bwd_cl4_kernel(PoolGeom g, const 
 }
 
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// one float4 group per thread up to 2^28 groups, so the gathers of many positions are in
+// flight at once
+static inline unsigned bwd_blocks(int64_t items) { return (unsigned)std::min<int64_t>(cdiv(items, 256), 1ll << 20); }
 
 }  // namespace tagi
 
@@ -262,10 +303,10 @@ extern "C" int tagi_maxpool2d_bwd(const float* dmz, const float* dSz, const int3
   if (g.cl && C % 4 == 0 && al16(dmz) && al16(dSz) && al16(pool_idx) && al16(dma) && al16(dSa)) {
     const int64_t items = total / 4;
     if (items < (1ll << 32))
-      hipLaunchKernelGGL(maxpool_bwd_cl4_kernel<uint32_t>, dim3(ew_blocks(items, 256)), dim3(256), 0, s, g, dmz, dSz,
+      hipLaunchKernelGGL(maxpool_bwd_cl4_kernel<uint32_t>, dim3(bwd_blocks(items)), dim3(256), 0, s, g, dmz, dSz,
                          pool_idx, dma, dSa);
     else
-      hipLaunchKernelGGL(maxpool_bwd_cl4_kernel<int64_t>, dim3(ew_blocks(items, 256)), dim3(256), 0, s, g, dmz, dSz,
+      hipLaunchKernelGGL(maxpool_bwd_cl4_kernel<int64_t>, dim3(bwd_blocks(items)), dim3(256), 0, s, g, dmz, dSz,
                          pool_idx, dma, dSa);
   } else if (total < (1ll << 32))
     hipLaunchKernelGGL(maxpool_bwd_kernel<uint32_t>, dim3(ew_blocks(total, 256)), dim3(256), 0, s, g, dmz, dSz,
