@@ -93,7 +93,7 @@ def test_relu(dev):
     ma, Sa, J = bayesian_relu(mz.to(dev), Sz.to(dev))
     rm, rS, rJ = O.relu_moments(d64(mz), d64(Sz))
     assert_scaled_close(ma, rm, None, RTOL, ATOL, "relu mean")
-    assert_scaled_close(Sa, rS, rS.abs() + d64(mz) ** 2 * 1e-3, RTOL, ATOL, "relu var")
+    assert_scaled_close(Sa, rS, None, RTOL, ATOL, "relu var")
     assert_scaled_close(J, rJ, None, RTOL, ATOL, "relu J")
 
 
@@ -147,7 +147,35 @@ def test_remax_on_reference_golden_inputs(dev):
             assert_scaled_close(gt, rt, None, RTOL, ATOL, f"remax {n} {key} vs oracle")
             stored = torch.tensor(d[f"{n}_{key}"], dtype=torch.float64)
             rel = ((gt.cpu().double() - stored).norm() / stored.norm()).item()
-            assert rel < (2e-3 if key == "mu_a" else 3e-2), f"remax {n} {key}: {rel:.2e} from the reference output"
+            # the oracle itself sits 1.2e-6 (mean) and 2.4e-4 / 3.0e-4 (variance, J) from these
+            # outputs in the 2-norm (the reference's fp32 rounding)
+            assert rel < (1e-5 if key == "mu_a" else 1e-3), f"remax {n} {key}: {rel:.2e} from the reference output"
+
+
+def update_multi_many_groups_with_empty_ones(dev, r):
+    """The C entry point directly (the Python wrapper drops empty groups): 50 groups, more
+    than one launch holds, with empty groups first and in between. Every non-empty group
+    must be updated exactly once (a second application would move it twice)."""
+    import ctypes
+
+    from triton_tagi_amd import _lib
+
+    sizes = [0] + [int(n) for n in torch.randint(1, 9000, (49,), generator=r)]
+    sizes[7] = sizes[30] = 0
+    groups, refs = [], []
+    for n in sizes:
+        m, S = torch.randn(n, generator=r), 1e-3 + torch.rand(n, generator=r) * 1e-2
+        ddm, ddS = torch.randn(n, generator=r) * 0.05, torch.randn(n, generator=r) * 1e-2
+        groups.append(tuple(t.to(dev) for t in (m, S, ddm, ddS)))
+        refs.append(O.capped_update(d64(m), d64(S), d64(ddm), d64(ddS), 2.0))
+    k = len(groups)
+    tab = [(ctypes.c_void_p * k)(*[grp[j].data_ptr() for grp in groups]) for j in range(4)]
+    pn = (ctypes.c_int64 * k)(*sizes)
+    _lib.call("tagi_capped_update_multi", *(ctypes.addressof(t) for t in tab), ctypes.addressof(pn), k, 2.0,
+              torch.cuda.current_stream(dev).cuda_stream)
+    for j, ((mg, Sg, _, _), (rm, rS)) in enumerate(zip(groups, refs)):
+        assert_scaled_close(mg, rm, None, RTOL, ATOL, f"50-group update m, group {j} (n={sizes[j]})")
+        assert_scaled_close(Sg, rS, None, RTOL, ATOL, f"50-group update S, group {j} (n={sizes[j]})")
 
 
 def test_innovation_update_add_jacobian(dev):
@@ -186,6 +214,8 @@ def test_innovation_update_add_jacobian(dev):
     for (mg, Sg, _, _), (rm, rS) in zip(groups, refs):
         assert_scaled_close(mg, rm, None, RTOL, ATOL, "multi update m")
         assert_scaled_close(Sg, rS, None, RTOL, ATOL, "multi update S")
+
+    update_multi_many_groups_with_empty_ones(dev, r)
 
     a, b, c, d = (torch.randn(1001, generator=r) for _ in range(4))
     ag, bg = a.to(dev), b.to(dev)

@@ -213,8 +213,9 @@ def golden_cases():
 
 # The reference's own fp32 evaluation of these formulas carries up to ~3% rounding error on
 # individual variance/Jacobian elements (log-normal cancellations), so the golden pin is
-# norm-wise: mean within 2e-3, variance and Jacobian within 3e-2 relative in the 2-norm.
-REMAX_TOL = {"mu_a": 2e-3, "var_a": 3e-2, "J": 3e-2}
+# norm-wise, about four times the oracle's measured distance from the stored outputs
+# (1.2e-6 for the mean, 2.4e-4 / 3.0e-4 for the variance and the Jacobian in the 2-norm).
+REMAX_TOL = {"mu_a": 1e-5, "var_a": 1e-3, "J": 1e-3}
 
 
 def remax_golden_errors(fn=None):

@@ -461,12 +461,15 @@ extern "C" int tagi_capped_update_multi(float* const* m, float* const* S, const 
     total += n[t];
   }
   ProfScope ps(FAM_UPDATE, s, 0.0, 24.0 * total);
-  for (int64_t t0 = 0; t0 < count; t0 += kMultiMax) {
+  // one cursor over the table: each launch takes the next (up to) kMultiMax non-empty
+  // groups, so every group is updated exactly once whatever the empty groups between them
+  int64_t t = 0;
+  while (t < count) {
     MultiUpdateArgs a{};
     a.cap = cap_factor;
     int c = 0;
     int64_t blocks = 0;
-    for (int64_t t = t0; t < count && c < kMultiMax; ++t) {
+    for (; t < count && c < kMultiMax; ++t) {
       if (n[t] == 0) continue;
       a.m[c] = m[t];
       a.S[c] = S[t];
