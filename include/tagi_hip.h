@@ -73,6 +73,22 @@ int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw, const flo
                     tagi_stream_t stream);
 int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N);
 
+/* Bytes of the fixed device scratch behind tagi_linear_fwd_noalloc, per GPU. */
+#define TAGI_LINEAR_FWD_NOALLOC_SCRATCH_BYTES (128ll << 20)
+
+/* tagi_linear_fwd with no workspace argument that allocates nothing. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The split-K
+ * partial sums go to a fixed device array of TAGI_LINEAR_FWD_NOALLOC_SCRATCH_BYTES that
+ * each GPU holds from the first call on it until the process ends. Same plan and kernels
+ * as tagi_linear_fwd given its full workspace, so the same results bit for bit; a shape
+ * whose partials exceed the scratch returns TAGI_ERR_ARG before launching anything. The
+ * stream's device must be the current device. Calls that overlap on one GPU (several
+ * streams or host threads) share the scratch and race: serialise them. */
+int tagi_linear_fwd_noalloc(const float* ma, const float* Sa, const float* mw, const float* Sw,
+                            const float* mb, const float* Sb, float* mz, float* Sz,
+                            int64_t M, int64_t K, int64_t N, tagi_stream_t stream);
+
 /* Backward delta propagation:  dma = dmz @ mw^T ;  dSa = dSz @ (mw^2)^T.
  * dmz, dSz (M,N); mw (K,N); dma, dSa (M,K). ws: split-K partials (size from the query).
  * Replaces triton_fused_backward_delta (common.py:287). */

@@ -1,4 +1,6 @@
 // Linear layer entry points (forward moments, backward deltas, parameter deltas).
+#include <mutex>
+
 #include "tagi_gemm_core.h"
 
 using namespace tagi;
@@ -14,15 +16,19 @@ extern "C" int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N) {
   return plan_ws_bytes(linear_fwd_plan(M, K, N), M, N, 1);
 }
 
-extern "C" int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw, const float* mb,
-                               const float* Sb, float* mz, float* Sz, int64_t M, int64_t K, int64_t N, float* ws,
-                               int64_t ws_bytes, tagi_stream_t stream) {
-  const char* what = "tagi_linear_fwd";
+static int linear_fwd_check(const char* what, const float* ma, const float* Sa, const float* mw, const float* Sw,
+                            const float* Sz, int64_t M, int64_t K, int64_t N) {
   TAGI_REQUIRE(ma && Sa && mw && Sw && Sz, "%s: null pointer", what);
   TAGI_REQUIRE(M > 0 && K > 0 && N > 0, "%s: sizes must be positive (M=%lld K=%lld N=%lld)", what, (long long)M,
                (long long)K, (long long)N);
   TAGI_REQUIRE(fits_i32(M * K) && fits_i32(K * N) && fits_i32(M * N), "%s: too large for 32-bit tiles", what);
-  hipStream_t s = as_stream(stream);
+  return TAGI_OK;
+}
+
+// Launch of the forward product with plan p (split-K partials in ws when p splits).
+static int linear_fwd_run(const char* what, const float* ma, const float* Sa, const float* mw, const float* Sw,
+                          const float* mb, const float* Sb, float* mz, float* Sz, int64_t M, int64_t K, int64_t N,
+                          const Plan& p, float* ws, int64_t ws_bytes, hipStream_t s) {
   ProfScope ps(FAM_LINEAR_FWD, s, 2.0 * 3 * M * K * N, 4.0 * (2 * M * K + 2 * K * N + 2 * M * N));
   GemmArgs g{};
   g.a = strided_operand(ma, Sa, 1, 0, 0, K, 1, M, K);
@@ -31,11 +37,85 @@ extern "C" int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw
   g.R = (int)M;
   g.C = (int)N;
   g.Kred = (int)K;
-  Plan p = linear_fwd_plan(M, K, N);
-  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, N, 1))) p = choose_plan(M, N, K, 1, 3, false, 1);
   const bool v4 = K % 4 == 0 && N % 4 == 0 && al16(ma) && al16(Sa) && al16(mw) && al16(Sw);
   if (v4) return run_gemm<PROD_FWD, LD_STR_K4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
   return run_gemm<PROD_FWD, LD_STR_K_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
+}
+
+extern "C" int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw, const float* mb,
+                               const float* Sb, float* mz, float* Sz, int64_t M, int64_t K, int64_t N, float* ws,
+                               int64_t ws_bytes, tagi_stream_t stream) {
+  const char* what = "tagi_linear_fwd";
+  int rc = linear_fwd_check(what, ma, Sa, mw, Sw, Sz, M, K, N);
+  if (rc != TAGI_OK) return rc;
+  Plan p = linear_fwd_plan(M, K, N);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, N, 1))) p = choose_plan(M, N, K, 1, 3, false, 1);
+  return linear_fwd_run(what, ma, Sa, mw, Sw, mb, Sb, mz, Sz, M, K, N, p, ws, ws_bytes, as_stream(stream));
+}
+
+// --------------------------------------------------- forward without allocation
+// tagi_linear_fwd_noalloc keeps the split-K partial sums of a call in this file-scope
+// device array instead of a caller workspace. Each GPU holds its own copy, at its own
+// address, from the first call on that GPU until the process ends. In host code the
+// array's name is not a device address: the address is taken once per device with
+// hipGetSymbolAddress (that device current) and only that pointer is handed to kernels.
+// Every split writes all of its partial plane before the reduction reads it, so nothing
+// in the array has to start at zero; the array keeps the last call's partials. Calls
+// that overlap on one GPU (two streams, or two host threads) share the array and race.
+static __device__ __align__(256) float scratch[TAGI_LINEAR_FWD_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// The calling thread's current device's copy of `scratch` (its address resolved on the
+// first call for that device).
+static int scratch_of_current_device(const char* what, hipStream_t s, float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TAGI_ERR_LAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  TAGI_REQUIRE(dev >= 0 && dev < kMaxDevices, "%s: device index %d out of range", what, dev);
+  if (s != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(s, &sdev);
+    if (e != hipSuccess) return fail(TAGI_ERR_LAUNCH, "%s: hipStreamGetDevice failed: %s", what, hipGetErrorString(e));
+    TAGI_REQUIRE((int)sdev == dev, "%s: the stream belongs to device %d but device %d is current", what, (int)sdev,
+                 dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(TAGI_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return TAGI_OK;
+}
+
+extern "C" int tagi_linear_fwd_noalloc(const float* ma, const float* Sa, const float* mw, const float* Sw,
+                                       const float* mb, const float* Sb, float* mz, float* Sz, int64_t M, int64_t K,
+                                       int64_t N, tagi_stream_t stream) {
+  const char* what = "tagi_linear_fwd_noalloc";
+  int rc = linear_fwd_check(what, ma, Sa, mw, Sw, Sz, M, K, N);
+  if (rc != TAGI_OK) return rc;
+  // the plan tagi_linear_fwd runs with its full workspace, so results are the same bits
+  const Plan p = linear_fwd_plan(M, K, N);
+  const int64_t need = plan_ws_bytes(p, M, N, 1);
+  TAGI_REQUIRE(need <= (int64_t)TAGI_LINEAR_FWD_NOALLOC_SCRATCH_BYTES,
+               "%s: M=%lld K=%lld N=%lld needs %lld bytes of split-K scratch, above the fixed %lld; use "
+               "tagi_linear_fwd with a workspace",
+               what, (long long)M, (long long)K, (long long)N, (long long)need,
+               (long long)TAGI_LINEAR_FWD_NOALLOC_SCRATCH_BYTES);
+  hipStream_t s = as_stream(stream);
+  float* ws = nullptr;
+  rc = scratch_of_current_device(what, s, &ws);
+  if (rc != TAGI_OK) return rc;
+  return linear_fwd_run(what, ma, Sa, mw, Sw, mb, Sb, mz, Sz, M, K, N, p, ws, need, s);
 }
 
 extern "C" int64_t tagi_linear_bwd_delta_ws_bytes(int64_t M, int64_t K, int64_t N) {
