@@ -1,7 +1,7 @@
 """Build libtagi_hip.so for gfx950 from csrc/*.hip with hipcc.
 
-Each translation unit compiles in its own hipcc process (in parallel), then one hipcc
-link produces ``triton_tagi_amd/libtagi_hip.so`` in-tree, next to the Python package
+Each translation unit compiles in its own hipcc process (in parallel; the GEMM kernel
+instantiations are split over 18 units), then one hipcc link produces ``triton_tagi_amd/libtagi_hip.so`` in-tree, next to the Python package
 that loads it.
 
     python triton-tagi_amd/build.py            # build
@@ -51,25 +51,50 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{proc.stdout}")
 
 
+# tagi_gemm_inst.hip holds the GEMM kernels; it is compiled once per tile config (0..5)
+# and product (0..2), each into its own object.
+INST = "tagi_gemm_inst.hip"
+N_CFG, N_PROD = 6, 3
+
+
+def compile_units() -> list[tuple[Path, Path, list[str]]]:
+    """(source, object, extra defines) for every translation unit."""
+    units = []
+    for src in sorted(CSRC.glob("*.hip")):
+        if src.name == INST:
+            for c in range(N_CFG):
+                for p in range(N_PROD):
+                    units.append((src, OUT_DIR / f"{src.stem}_c{c}_p{p}.o",
+                                  [f"-DTAGI_INST_CFG={c}", f"-DTAGI_INST_PROD={p}"]))
+        else:
+            units.append((src, OUT_DIR / (src.stem + ".o"), []))
+    return units
+
+
 def build(jobs: int | None = None, verbose: bool = True) -> Path:
     hipcc = _hipcc()
     OUT_DIR.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
-    if not sources:
+    units = compile_units()
+    if not units:
         raise RuntimeError(f"no sources in {CSRC}")
-    objs = [OUT_DIR / (s.stem + ".o") for s in sources]
-    jobs = jobs or min(len(sources), max(1, os.cpu_count() or 1))
+    objs = [obj for _, obj, _ in units]
+    jobs = jobs or min(len(units), max(1, os.cpu_count() or 1))
 
-    def compile_one(pair):
-        src, obj = pair
+    def compile_one(unit):
+        src, obj, defs = unit
         if verbose:
-            print(f"[build] hipcc {src.name}", flush=True)
-        _run([hipcc, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
+            print(f"[build] hipcc {src.name} {' '.join(defs)}".rstrip(), flush=True)
+        _run([hipcc, *HIP_FLAGS, *defs, "-c", str(src), "-o", str(obj)])
 
+    # the instantiation units are the slowest: start them first
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        list(ex.map(compile_one, zip(sources, objs)))
+        list(ex.map(compile_one, sorted(units, key=lambda u: not u[2])))
+    for stale in OUT_DIR.glob("*.o"):
+        if stale not in objs:
+            stale.unlink()
     tmp = LIB.with_suffix(".so.tmp")
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    # -z defs: a kernel combination missing from the instantiation lists fails here
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, LIB)
     if verbose:
         print(f"[build] wrote {LIB}", flush=True)

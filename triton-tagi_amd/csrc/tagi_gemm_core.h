@@ -205,6 +205,20 @@ struct Loader {
   static_assert(PART ? (NCH * W == BMN * BK && NTH % NCH == 0) : (NC * W * NTH == BMN * BK),
                 "tile does not split evenly over threads");
   static constexpr int LD = BMN + 4;
+  // LDS tile of one tensor. Reduction-major [BK][LD] (rows of the tile dim padded by 4),
+  // except for float4 loaders that walk the reduction ("K4" kinds): those keep the tile
+  // row-major, [BMN][BK], so a fetched chunk (4 consecutive k of one row) is stored with
+  // one 16-byte write instead of four scattered ones, and a lane reads the 8 k values of
+  // its fragments with two 16-byte reads. The 4 chunks of a row are XOR-swizzled by
+  // ((row >> 1) ^ (row >> 2)) & 3 so that 8 (or 16) lanes of one 16-byte access hit
+  // distinct bank groups with 32 (or 64) banks, for the stores (4 lanes per row) and for
+  // the fragment reads (one row per lane).
+  static constexpr bool KMAJ = V4 && !MNF;
+  static constexpr int TILE = KMAJ ? BMN * BK : BK * LD;
+  static_assert(!KMAJ || BK == 16, "the row-major tile swizzle assumes 4 chunks per row");
+  __device__ static __forceinline__ int kmaj_off(int row, int k) {
+    return row * BK + ((((k >> 2) ^ (row >> 1) ^ (row >> 2)) & 3) << 2);
+  }
 
   using Vt = typename std::conditional<V4, float4, float>::type;
   static constexpr bool CONV_ROWS = (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S || KIND == LD_CBWD_A4 ||
@@ -423,17 +437,14 @@ struct Loader {
     for (int i = 0; i < NC; ++i) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        float* st = s + t * BK * LD;
+        float* st = s + t * TILE;
         const Vt x = v[ST][t][i];
         if constexpr (!V4) {
           st[ck[i] * LD + cmn[i]] = x;
         } else if constexpr (MNF) {
           *reinterpret_cast<float4*>(st + ck[i] * LD + cmn[i]) = x;
         } else {
-          st[(ck[i] + 0) * LD + cmn[i]] = x.x;
-          st[(ck[i] + 1) * LD + cmn[i]] = x.y;
-          st[(ck[i] + 2) * LD + cmn[i]] = x.z;
-          st[(ck[i] + 3) * LD + cmn[i]] = x.w;
+          *reinterpret_cast<float4*>(st + kmaj_off(cmn[i], ck[i])) = x;
         }
       }
     }
@@ -559,9 +570,15 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   constexpr int BM = CFG::BM, BN = CFG::BN, BK = CFG::BK, WM = CFG::WM, WN = CFG::WN, NTH = CFG::NTH;
   constexpr int NA = (PROD == PROD_SHARED_A) ? 1 : 2;
   constexpr int NB = (PROD == PROD_SHARED_B) ? 1 : 2;
-  constexpr int LDA = BM + 4, LDB = BN + 4;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int SA = NA * BK * LDA, SB = NB * BK * LDB;
+  // register stages of operand prefetch: k-tiles are fetched two tiles ahead, except in
+  // the forward product's 8-wave tiles, where a second stage would cost the tile its
+  // second resident block per CU
+  constexpr int PF = (PROD != PROD_FWD || NTH <= 256) ? 2 : 1;
+  using LA = Loader<KA, NA, BM, BK, NTH, PF>;
+  using LB = Loader<KB, NB, BN, BK, NTH, PF>;
+  constexpr int LDA = LA::LD, LDB = LB::LD;
+  constexpr int SA = NA * LA::TILE, SB = NB * LB::TILE;
 
   __shared__ __attribute__((aligned(16))) float smem[2 * (SA + SB)];
 
@@ -625,12 +642,8 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   const int kbeg = split * g.k_chunk;
   const int kend = min(Kred, kbeg + g.k_chunk);
 
-  // register stages of operand prefetch: k-tiles are fetched two tiles ahead, except in
-  // the forward product's 8-wave tiles, where a second stage would cost the tile its
-  // second resident block per CU
-  constexpr int PF = (PROD != PROD_FWD || NTH <= 256) ? 2 : 1;
-  Loader<KA, NA, BM, BK, NTH, PF> la;
-  Loader<KB, NB, BN, BK, NTH, PF> lb;
+  LA la;
+  LB lb;
   la.init(g.a, z, m0, tid);
   lb.init(g.b, z, n0, tid);
 
@@ -668,26 +681,77 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   auto compute_tile = [&](const float* sA) {
     const float* sB = sA + SA;
     {
-      // Fragments of k-step s+2 are read from LDS while the MFMAs of k-step s run; the
-      // scheduling barriers keep the compiler from sinking the reads next to their use.
+      // MFMA k-step s takes reduction indices s (lanes 0-31) and NS + s (lanes 32-63) of
+      // the tile, the same assignment for both operands. Row-major (K4) tiles give a lane
+      // its 8 values with two 16-byte reads at the start of the tile; for the others the
+      // fragments of k-step s+2 are read while the MFMAs of k-step s run (the scheduling
+      // barriers keep the compiler from sinking the reads next to their use).
       constexpr int NS = BK / 2;
       constexpr int PD = 2;
       float fa0[NS][TM], fa1[NS][TM], fb0[NS][TN], fb1[NS][TN];
       auto load = [&](int s) {
-        const int kr = 2 * s + hl;
+        const int kr = hl * NS + s;
+        if constexpr (!LA::KMAJ) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const int c = kr * LDA + wm * WM + i * 32 + rl;
-          fa0[s][i] = sA[c];
-          if constexpr (NA == 2) fa1[s][i] = sA[BK * LDA + c];
+          for (int i = 0; i < TM; ++i) {
+            const int c = kr * LDA + wm * WM + i * 32 + rl;
+            fa0[s][i] = sA[c];
+            if constexpr (NA == 2) fa1[s][i] = sA[LA::TILE + c];
+          }
         }
+        if constexpr (!LB::KMAJ) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int c = kr * LDB + wn * WN + j * 32 + rl;
-          fb0[s][j] = sB[c];
-          if constexpr (NB == 2) fb1[s][j] = sB[BK * LDB + c];
+          for (int j = 0; j < TN; ++j) {
+            const int c = kr * LDB + wn * WN + j * 32 + rl;
+            fb0[s][j] = sB[c];
+            if constexpr (NB == 2) fb1[s][j] = sB[LB::TILE + c];
+          }
         }
       };
+      if constexpr (LA::KMAJ) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int row = wm * WM + i * 32 + rl;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int o = LA::kmaj_off(row, hl * NS + 4 * h);
+            const float4 x = *reinterpret_cast<const float4*>(sA + o);
+            fa0[4 * h + 0][i] = x.x;
+            fa0[4 * h + 1][i] = x.y;
+            fa0[4 * h + 2][i] = x.z;
+            fa0[4 * h + 3][i] = x.w;
+            if constexpr (NA == 2) {
+              const float4 y = *reinterpret_cast<const float4*>(sA + LA::TILE + o);
+              fa1[4 * h + 0][i] = y.x;
+              fa1[4 * h + 1][i] = y.y;
+              fa1[4 * h + 2][i] = y.z;
+              fa1[4 * h + 3][i] = y.w;
+            }
+          }
+        }
+      }
+      if constexpr (LB::KMAJ) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int row = wn * WN + j * 32 + rl;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int o = LB::kmaj_off(row, hl * NS + 4 * h);
+            const float4 x = *reinterpret_cast<const float4*>(sB + o);
+            fb0[4 * h + 0][j] = x.x;
+            fb0[4 * h + 1][j] = x.y;
+            fb0[4 * h + 2][j] = x.z;
+            fb0[4 * h + 3][j] = x.w;
+            if constexpr (NB == 2) {
+              const float4 y = *reinterpret_cast<const float4*>(sB + LB::TILE + o);
+              fb1[4 * h + 0][j] = y.x;
+              fb1[4 * h + 1][j] = y.y;
+              fb1[4 * h + 2][j] = y.z;
+              fb1[4 * h + 3][j] = y.w;
+            }
+          }
+        }
+      }
       auto mma = [&](int s) {
         float* a0 = fa0[s];
         float* a1 = fa1[s];
@@ -1141,11 +1205,40 @@ static inline int64_t plan_ws_bytes(const Plan& p, int64_t R, int64_t C, int64_t
   return p.splits > 1 ? (int64_t)p.splits * 2 * R * C * batch * (int64_t)sizeof(float) : 0;
 }
 
+// The (product, tile config, loader) combinations the entry points launch. Each
+// combination's kernel is compiled once, in tagi_gemm_inst.hip (built once per tile
+// config and product, so the kernels compile in parallel translation units); the entry
+// points' translation units see launch_cfg's declaration only.
+#define TAGI_GEMM_COMBOS_FWD(X)                                                          \
+  X(PROD_FWD, LD_CFWD_A4, LD_CFWD_B4) X(PROD_FWD, LD_CFWD_A_S, LD_CFWD_B4)               \
+  X(PROD_FWD, LD_CFWD_A_S, LD_CFWD_B_S) X(PROD_FWD, LD_STR_K4, LD_STR_MN4)               \
+  X(PROD_FWD, LD_STR_K_S, LD_STR_MN_S) X(PROD_FWD, LD_STR_MN_S, LD_STR_MN_S)             \
+  X(PROD_FWD, LD_STR_K4, LD_STR_K4) X(PROD_FWD, LD_STR_MN4, LD_STR_K4)                   \
+  X(PROD_FWD, LD_STR_MN4, LD_STR_MN4)
+#define TAGI_GEMM_COMBOS_SHARED_B(X)                                                     \
+  X(PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B4) X(PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4)     \
+  X(PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B_S) X(PROD_SHARED_B, LD_CBWD_A_S, LD_CBWD_B_S)   \
+  X(PROD_SHARED_B, LD_STR_K4, LD_STR_K4) X(PROD_SHARED_B, LD_STR_K_S, LD_STR_K_S)        \
+  X(PROD_SHARED_B, LD_STR_MN_S, LD_STR_MN_S) X(PROD_SHARED_B, LD_STR_K4, LD_STR_MN4)     \
+  X(PROD_SHARED_B, LD_STR_MN4, LD_STR_K4) X(PROD_SHARED_B, LD_STR_MN4, LD_STR_MN4)
+#define TAGI_GEMM_COMBOS_SHARED_A(X)                                                     \
+  X(PROD_SHARED_A, LD_CWG_A4, LD_STR_MN4) X(PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN4)       \
+  X(PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN_S) X(PROD_SHARED_A, LD_ONEHOT4, LD_STR_MN4)     \
+  X(PROD_SHARED_A, LD_ONEHOT_S, LD_STR_MN4) X(PROD_SHARED_A, LD_ONEHOT_S, LD_STR_MN_S)   \
+  X(PROD_SHARED_A, LD_STR_MN4, LD_STR_MN4) X(PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S)    \
+  X(PROD_SHARED_A, LD_STR_K4, LD_STR_K4) X(PROD_SHARED_A, LD_STR_K4, LD_STR_MN4)         \
+  X(PROD_SHARED_A, LD_STR_MN4, LD_STR_K4)
+
 template <int PROD, class CFG, int KA, int KB>
-static inline void launch_cfg(const GemmArgs& g, int64_t grid_x, int64_t grid_y, hipStream_t s) {
+void launch_cfg(const GemmArgs& g, int64_t grid_x, int64_t grid_y, hipStream_t s)
+#ifdef TAGI_GEMM_DEFINE_LAUNCH
+{
   hipLaunchKernelGGL((gemm_kernel<PROD, CFG, KA, KB>), dim3((unsigned)grid_x, (unsigned)grid_y), dim3(CFG::NTH), 0, s,
                      g);
 }
+#else
+    ;
+#endif
 
 // Launch with plan p. For phased (conv input-delta) launches grid_x covers the largest
 // phase and blocks past a phase's tiles exit at once.

@@ -1,0 +1,37 @@
+// Kernel instantiations of the moment GEMM engine: the launch_cfg<product, tile config,
+// loaders> combinations listed in tagi_gemm_core.h for one tile config and one product.
+// build.py compiles this file once per (TAGI_INST_CFG, TAGI_INST_PROD) pair, so the
+// ~200 kernels compile in parallel translation units.
+#define TAGI_GEMM_DEFINE_LAUNCH
+#include "tagi_gemm_core.h"
+
+#ifndef TAGI_INST_CFG
+#error "compile with -DTAGI_INST_CFG=<0..5> -DTAGI_INST_PROD=<0..2>"
+#endif
+
+namespace tagi {
+
+#if TAGI_INST_CFG == 0
+using InstCfg = C128x128;
+#elif TAGI_INST_CFG == 1
+using InstCfg = C128x64;
+#elif TAGI_INST_CFG == 2
+using InstCfg = C64x128;
+#elif TAGI_INST_CFG == 3
+using InstCfg = C64x64;
+#elif TAGI_INST_CFG == 4
+using InstCfg = C32x32;
+#else
+using InstCfg = C128x32;
+#endif
+
+#define TAGI_INST(P, KA, KB) template void launch_cfg<P, InstCfg, KA, KB>(const GemmArgs&, int64_t, int64_t, hipStream_t);
+#if TAGI_INST_PROD == 0
+TAGI_GEMM_COMBOS_FWD(TAGI_INST)
+#elif TAGI_INST_PROD == 1
+TAGI_GEMM_COMBOS_SHARED_B(TAGI_INST)
+#else
+TAGI_GEMM_COMBOS_SHARED_A(TAGI_INST)
+#endif
+
+}  // namespace tagi
