@@ -63,7 +63,7 @@ extern "C" int tagi_bmm_tagi(const float* mu_a, const float* var_a, const float*
   g.R = (int)M;
   g.C = (int)L;
   g.Kred = (int)K;
-  Plan p = choose_plan(M, L, K, batch, 3, false, 1);
+  Plan p = choose_plan(M, L, K, batch, PROD_FWD, false, 1);
   int ka = view_kind(mu_a, va->zdiv, va->sz1, va->sz2, va->si, va->sj, M, K);
   if (!al16(var_a)) ka = LD_STR_MN_S;
   int kb = view_kind(mu_b, vb->zdiv, vb->sz1, vb->sz2, vb->sj, vb->si, L, K);
@@ -92,7 +92,7 @@ static int bmm_shared_impl(const char* what, const float* p0, const float* p1, c
   g.R = (int)M;
   g.C = (int)L;
   g.Kred = (int)K;
-  Plan p = choose_plan(M, L, K, batch, 2, false, 1);
+  Plan p = choose_plan(M, L, K, batch, shared_left ? PROD_SHARED_A : PROD_SHARED_B, false, 1);
   const float* a0 = shared_left ? p2 : p0;
   const float* a1 = shared_left ? nullptr : p1;
   const float* b0 = shared_left ? p0 : p2;

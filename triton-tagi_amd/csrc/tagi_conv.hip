@@ -57,7 +57,7 @@ static int check_geom(const tagi_conv_geom* g, const char* what) {
 }
 
 static Plan conv_fwd_plan(const tagi_conv_geom* g) {
-  return choose_plan(g->N * g->Ho * g->Wo, g->Cout, g->C * g->k * g->k, 1, 3, true, 16);
+  return choose_plan(g->N * g->Ho * g->Wo, g->Cout, g->C * g->k * g->k, 1, PROD_FWD, true, 16);
 }
 
 // Largest row count (phase 0) and largest reduction over the stride phases of the
@@ -82,16 +82,16 @@ static Plan conv_bwd_plan(const tagi_conv_geom* g) {
   const ConvG cg = to_g(g);
   const int nph = cg.stride * cg.stride;
   int64_t pk[64];
-  if (nph > 64) return choose_plan(R, g->C, K, nph, 2, true, 16);
+  if (nph > 64) return choose_plan(R, g->C, K, nph, PROD_SHARED_B, true, 16);
   for (int ph = 0; ph < nph; ++ph) {
     const Phase p = make_phase(cg, ph);
     pk[ph] = (int64_t)p.nkh * p.nkw * g->Cout;
   }
-  return choose_plan(R, g->C, K, nph, 2, true, 16, pk);
+  return choose_plan(R, g->C, K, nph, PROD_SHARED_B, true, 16, pk);
 }
 
 static Plan conv_wgrad_plan(const tagi_conv_geom* g) {
-  return choose_plan(g->C * g->k * g->k + 1, g->Cout, g->N * g->Ho * g->Wo, 1, 2, true, 512);
+  return choose_plan(g->C * g->k * g->k + 1, g->Cout, g->N * g->Ho * g->Wo, 1, PROD_SHARED_A, true, 512);
 }
 
 static int64_t wt_floats(const tagi_conv_geom* g) { return ((g->C * g->k * g->k * g->Cout) + 3) / 4 * 4; }
@@ -161,7 +161,7 @@ extern "C" int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw
   TAGI_REQUIRE(ma && Sa && mw && Sw && mz && Sz, "%s: null pointer", what);
   const int64_t R = g->N * g->Ho * g->Wo, C = g->Cout, K = g->C * g->k * g->k;
   Plan p = conv_fwd_plan(g);
-  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, R, C, 1))) p = choose_plan(R, C, K, 1, 3, false, 1);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, R, C, 1))) p = choose_plan(R, C, K, 1, PROD_FWD, false, 1);
   return conv_fwd_impl(what, ma, Sa, mw, Sw, mb, Sb, mz, Sz, g, p, nullptr, nullptr, ws, ws_bytes,
                        as_stream(stream));
 }
@@ -294,7 +294,7 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
   Plan p = conv_bwd_plan(g);
   float* part = ws + wt_floats(g);
   const int64_t part_bytes = ws_bytes - wt_floats(g) * (int64_t)sizeof(float);
-  if (p.splits > 1 && part_bytes < plan_ws_bytes(p, R0, g->C, nph)) p = choose_plan(R0, g->C, K0, nph, 2, false, 1);
+  if (p.splits > 1 && part_bytes < plan_ws_bytes(p, R0, g->C, nph)) p = choose_plan(R0, g->C, K0, nph, PROD_SHARED_B, false, 1);
   const int64_t gx = (int64_t)p.tiles_m * p.tiles_n;  // phase 0 is the largest
   const bool va = g->Cout % 4 == 0 && al16(dmz) && al16(dSz);
   const bool vb = g->C % 4 == 0;
@@ -348,7 +348,7 @@ extern "C" int tagi_conv2d_wgrad(const float* ma, const float* dmz, const float*
   a.Kred = (int)M;
   Plan p = conv_wgrad_plan(g);
   if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, K + 1, N, 1)))
-    p = choose_plan(K + 1, N, M, 1, 2, false, 1);
+    p = choose_plan(K + 1, N, M, 1, PROD_SHARED_A, false, 1);
   p.tiles_m = (int)cdiv(a.R, kCfg[p.cfg].BM);
   const bool va = g->C % 4 == 0 && al16(ma);
   const bool vb = g->Cout % 4 == 0 && al16(dmz) && al16(dSz);

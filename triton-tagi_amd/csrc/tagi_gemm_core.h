@@ -1110,32 +1110,42 @@ struct Plan {
 //   * blocks run in rounds of 256 CUs x (resident blocks per CU); a partial last round
 //     runs at the occupancy of the blocks it holds (a lone block per CU leaves the MFMA
 //     pipes half idle);
-//   * each tile shape sustains a fraction of the fp32 MFMA peak (operand loads, LDS
-//     traffic and epilogue per flop), and fewer than ~3 waves per SIMD expose latency;
+//   * each tile shape and product sustains a fraction of the fp32 MFMA peak (operand
+//     loads, LDS traffic and epilogue per flop), and fewer than ~3 waves per SIMD expose
+//     latency;
 //   * split-K adds the partial sums' round trip (8 bytes per element and split, written
 //     and read back, mostly through the last-level cache) plus the reduction launch.
-// The constants were fitted to measured conv/linear GEMM timings on MI355X. Every
-// split count up to max_splits is tried (not only powers of two).
+// Resident blocks per CU are what the built kernels' register and LDS use allow (the
+// 8-wave 128x128 kernels need more than 128 VGPRs, so one block per CU). The sustained
+// fractions, the occupancy factors and the split costs were fitted to a sweep of every
+// tile shape and split count over the ResNet-18, CNN, transformer and Linear
+// microbenchmark GEMMs on MI355X (mean loss against the best measured plan 1.0%). The
+// split counts tried are the swept ones.
 //
 // phase_k (optional, batch entries): per-GEMM reduction lengths when they differ (stride
 // phases of the conv input delta); splits past a GEMM's own length launch no work.
-static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int64_t batch, int products,
-                                        bool allow_split, int64_t max_splits, const int64_t* phase_k) {
-  // resident blocks per CU (LDS / register limited), waves per block and sustained
-  // fraction of peak, per config
-  static const int kBpc[] = {2, 3, 3, 4, 8, 3};
+static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int64_t batch, int prod, bool allow_split,
+                                        int64_t max_splits, const int64_t* phase_k) {
+  // [tile config][product: forward, shared B, shared A]
+  static const int kBpc[6][3] = {{1, 1, 1}, {2, 3, 3}, {2, 3, 3}, {4, 5, 5}, {8, 10, 10}, {3, 4, 4}};
+  static const double kEff[6][3] = {{0.761, 0.645, 0.492}, {0.611, 0.615, 0.319}, {0.499, 0.624, 0.628},
+                                    {0.685, 0.585, 0.620}, {0.300, 0.303, 0.454}, {0.535, 0.450, 0.589}};
   static const int kWaves[] = {8, 4, 4, 4, 1, 4};
-  static const double kEff[] = {0.65, 0.58, 0.61, 0.61, 0.33, 0.50};
-  const double kSplitSecPerByte = 9.65e-14, kSplitLaunch = 8.9e-6;
-  Plan best{4, 1, (int)Kred, 1, 1};
+  static const int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 20, 24, 32, 40, 48, 64, 80, 96, 128, 160, 192, 256};
+  const double kOcc2 = 0.909, kOcc1 = 0.588, kOcc0 = 0.35;
+  const double kSplitSecPerByte = 1.68e-13, kSplitLaunch = 3.33e-6;
+  const int products = prod == PROD_FWD ? 3 : 2;
+  Plan best{3, 1, (int)Kred, 1, 1};
   double best_t = DBL_MAX;
   const double peak_cu = 157.3e12 / 256.0;
-  const int64_t max_sp = allow_split ? (max_splits < 512 ? max_splits : 512) : 1;
+  const int64_t max_sp = allow_split ? (max_splits < 256 ? max_splits : 256) : 1;
   for (int ci = 0; ci < kNumCfg; ++ci) {
     const int BM = kCfg[ci].BM, BN = kCfg[ci].BN;
     const int64_t tm = cdiv(R, BM), tn = cdiv(C, BN);
+    const int bpc = kBpc[ci][prod];
     int64_t prev_actual = -1;
-    for (int64_t sp = 1; sp <= max_sp; ++sp) {
+    for (int si = 0; si < (int)(sizeof(kSplits) / sizeof(kSplits[0])) && kSplits[si] <= max_sp; ++si) {
+      const int64_t sp = kSplits[si];
       int64_t kc = cdiv(cdiv(Kred, sp), 16) * 16;
       if (kc < 16) kc = 16;
       const int64_t actual = cdiv(Kred, kc);
@@ -1150,16 +1160,16 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
         for (int64_t z = 0; z < batch; ++z) eq += (double)(tm * tn) * (phase_k[z] > 0 ? (double)phase_k[z] / kc : 0.1);
         blocks = (int64_t)ceil(eq);
       }
-      const double block_s = (2.0 * BM * BN * kc * products) / (peak_cu * kEff[ci]);
+      const double block_s = (2.0 * BM * BN * kc * products) / (peak_cu * kEff[ci][prod]);
       // time for one CU to finish r co-resident blocks
       auto round_s = [&](int64_t r) {
         const double wps = (double)r * kWaves[ci] / 4.0;  // waves per SIMD
-        const double occ = wps >= 3.0 ? 1.0 : (wps >= 2.0 ? 0.93 : (wps >= 1.0 ? 0.55 : 0.35));
+        const double occ = wps >= 3.0 ? 1.0 : (wps >= 2.0 ? kOcc2 : (wps >= 1.0 ? kOcc1 : kOcc0));
         return (double)r * block_s / occ;
       };
-      const int64_t slots = 256 * (int64_t)kBpc[ci];
+      const int64_t slots = 256 * (int64_t)bpc;
       const int64_t full = blocks / slots, rem = blocks - full * slots;
-      double t = (double)full * round_s(kBpc[ci]) + (rem > 0 ? round_s(cdiv(rem, 256)) : 0.0);
+      double t = (double)full * round_s(bpc) + (rem > 0 ? round_s(cdiv(rem, 256)) : 0.0);
       if (actual > 1) t += (double)actual * 16.0 * R * C * batch * kSplitSecPerByte + kSplitLaunch;
       if (t < best_t * 0.999) {
         best_t = t;
@@ -1172,11 +1182,11 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
 
 // Plans are pure functions of the problem shape; memoise them per host thread (the
 // search above costs a few microseconds and the same shapes recur every step).
-static inline Plan choose_plan(int64_t R, int64_t C, int64_t Kred, int64_t batch, int products, bool allow_split,
+static inline Plan choose_plan(int64_t R, int64_t C, int64_t Kred, int64_t batch, int prod, bool allow_split,
                                int64_t max_splits, const int64_t* phase_k = nullptr) {
   struct Key {
     int64_t R, C, K, batch, max_splits, salt;
-    int products, allow;
+    int prod, allow;
   };
   int64_t salt = 0;
   if (phase_k)
@@ -1187,14 +1197,14 @@ static inline Plan choose_plan(int64_t R, int64_t C, int64_t Kred, int64_t batch
   };
   static thread_local Entry cache[64];
   static thread_local int used = 0, next = 0;
-  const Key key{R, C, Kred, batch, max_splits, salt, products, allow_split ? 1 : 0};
+  const Key key{R, C, Kred, batch, max_splits, salt, prod, allow_split ? 1 : 0};
   for (int i = 0; i < used; ++i) {
     const Key& k = cache[i].k;
     if (k.R == R && k.C == C && k.K == Kred && k.batch == batch && k.max_splits == max_splits && k.salt == salt &&
-        k.products == products && k.allow == key.allow)
+        k.prod == prod && k.allow == key.allow)
       return cache[i].p;
   }
-  const Plan p = choose_plan_uncached(R, C, Kred, batch, products, allow_split, max_splits, phase_k);
+  const Plan p = choose_plan_uncached(R, C, Kred, batch, prod, allow_split, max_splits, phase_k);
   cache[next] = Entry{key, p};
   next = (next + 1) % 64;
   if (used < 64) ++used;

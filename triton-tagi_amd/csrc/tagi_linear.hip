@@ -7,9 +7,9 @@ using namespace tagi;
 
 static inline hipStream_t as_stream(tagi_stream_t s) { return (hipStream_t)s; }
 
-static Plan linear_fwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, N, K, 1, 3, true, 16); }
-static Plan linear_bwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, K, N, 1, 2, true, 16); }
-static Plan linear_wgrad_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(K + 1, N, M, 1, 2, true, 512); }
+static Plan linear_fwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, N, K, 1, PROD_FWD, true, 16); }
+static Plan linear_bwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, K, N, 1, PROD_SHARED_B, true, 16); }
+static Plan linear_wgrad_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(K + 1, N, M, 1, PROD_SHARED_A, true, 512); }
 
 extern "C" int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N) {
   if (M <= 0 || K <= 0 || N <= 0) return 0;
@@ -49,7 +49,7 @@ extern "C" int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw
   int rc = linear_fwd_check(what, ma, Sa, mw, Sw, Sz, M, K, N);
   if (rc != TAGI_OK) return rc;
   Plan p = linear_fwd_plan(M, K, N);
-  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, N, 1))) p = choose_plan(M, N, K, 1, 3, false, 1);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, N, 1))) p = choose_plan(M, N, K, 1, PROD_FWD, false, 1);
   return linear_fwd_run(what, ma, Sa, mw, Sw, mb, Sb, mz, Sz, M, K, N, p, ws, ws_bytes, as_stream(stream));
 }
 
@@ -143,7 +143,7 @@ static int linear_bwd_delta_impl(const char* what, const float* dmz, const float
   g.C = (int)K;
   g.Kred = (int)N;
   Plan p = linear_bwd_plan(M, K, N);
-  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, K, 1))) p = choose_plan(M, K, N, 1, 2, false, 1);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, K, 1))) p = choose_plan(M, K, N, 1, PROD_SHARED_B, false, 1);
   const bool v4 = N % 4 == 0 && al16(dmz) && al16(dSz) && al16(mw);
   if (v4) return run_gemm<PROD_SHARED_B, LD_STR_K4, LD_STR_K4>(g, 1, p, ws, ws_bytes, s, what);
   return run_gemm<PROD_SHARED_B, LD_STR_K_S, LD_STR_K_S>(g, 1, p, ws, ws_bytes, s, what);
@@ -189,7 +189,7 @@ extern "C" int tagi_linear_wgrad(const float* ma, const float* dmz, const float*
   g.Kred = (int)M;
   Plan p = linear_wgrad_plan(M, K, N);
   if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, K + 1, N, 1)))
-    p = choose_plan(K + 1, N, M, 1, 2, false, 1);
+    p = choose_plan(K + 1, N, M, 1, PROD_SHARED_A, false, 1);
   p.tiles_m = (int)cdiv(g.R, kCfg[p.cfg].BM);
   const bool v4 = K % 4 == 0 && N % 4 == 0 && al16(ma) && al16(dmz) && al16(dSz);
   if (v4) return run_gemm<PROD_SHARED_A, LD_STR_MN4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
@@ -206,7 +206,7 @@ extern "C" int tagi_linear_wgrad(const float* ma, const float* dmz, const float*
 // deterministic split-K over the tokens. (A non-finite delta would reach the other
 // categories of its token's row through 0 * inf; deltas of a running step are finite.)
 static Plan embedding_bwd_plan(int64_t n_tokens, int64_t V, int64_t D) {
-  return choose_plan(V, D, n_tokens, 1, 2, true, 512);
+  return choose_plan(V, D, n_tokens, 1, PROD_SHARED_A, true, 512);
 }
 
 extern "C" int64_t tagi_embedding_bwd_ws_bytes(int64_t n_tokens, int64_t V, int64_t D) {
@@ -232,7 +232,7 @@ extern "C" int tagi_embedding_bwd(const float* tokens, const float* dmz, const f
   g.C = (int)D;
   g.Kred = (int)n_tokens;
   Plan p = embedding_bwd_plan(n_tokens, V, D);
-  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, V, D, 1))) p = choose_plan(V, D, n_tokens, 1, 2, false, 1);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, V, D, 1))) p = choose_plan(V, D, n_tokens, 1, PROD_SHARED_A, false, 1);
   const bool v4 = V % 4 == 0 && D % 4 == 0 && al16(dmz) && al16(dSz);
   if (v4) return run_gemm<PROD_SHARED_A, LD_ONEHOT4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
   if (D % 4 == 0 && al16(dmz) && al16(dSz))
