@@ -57,18 +57,18 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(workload: str, sample_batch: int, min_steps: int = 3, budget_s: float = 12.0):
-    """Float32 CPU oracle steps on a bounded sample: at least ``min_steps`` steps and
-    about ``budget_s`` seconds of CPU work; samples/s from the median step time."""
+def cpu_baseline(workload: str, batch: int, timed_steps: int = 3):
+    """Float32 CPU oracle on the same workload as the GPU run (same architecture, batch,
+    seeded priors and inputs), on all the host cores this process may run on: 1 warm-up
+    step, then the median of ``timed_steps`` steps; samples/s from the median."""
     import torch
 
     from oracle import tagi_oracle as O
     from triton_tagi_amd import workloads
 
-    # the host's share of cores for one GPU (OMP_NUM_THREADS where the job sets it)
-    cores = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
+    cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(max(cores, 1))
-    w = workloads.build(workload, device="cpu", batch=sample_batch)
+    w = workloads.build(workload, device="cpu", batch=batch)
     onet = O.mirror_net(w.net, dtype=torch.float32)
     x = w.x.float()
     if w.hrc is not None:
@@ -84,12 +84,12 @@ def cpu_baseline(workload: str, sample_batch: int, min_steps: int = 3, budget_s:
 
     step()  # warm-up
     times = []
-    while len(times) < min_steps or sum(times) < budget_s:
+    for _ in range(timed_steps):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
+        log(f"[bench] cpu step {len(times)}: {times[-1]:.2f} s")
     med = statistics.median(times)
-    steps = len(times)
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -99,13 +99,13 @@ def cpu_baseline(workload: str, sample_batch: int, min_steps: int = 3, budget_s:
     except OSError:
         pass
     return {
-        "value": sample_batch / med,
+        "value": w.batch / med,
         "unit": "samples/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{workload} step at batch {sample_batch} (same architecture, priors and input distribution), "
-                  f"fp32 torch CPU ops, 1 warm-up + median of {steps} steps ({med:.2f} s/step, "
-                  f"{sum(times):.1f} s measured); cpu: {cpu_model}",
+        "sample": f"{workload} step at batch {w.batch} (the GPU run's workload: same architecture, priors and "
+                  f"inputs), fp32 torch CPU ops on {cores} threads (sched_getaffinity), 1 warm-up + median of "
+                  f"{timed_steps} steps ({med:.2f} s/step); cpu: {cpu_model}",
     }
 
 
@@ -149,7 +149,20 @@ def measure_ceilings(dev: str) -> dict:
     dst = torch.empty_like(src)
     s = timed(lambda: dst.copy_(src), 10)
     out["copy_1gib_gbs_read_plus_write"] = round(2 * (1 << 30) / s / 1e9, 1)
-    del src, dst
+    # the engine's own streaming kernels (float4, 4 loads in flight per lane), over a sweep
+    # of grid sizes: copy (read + write) and read-only
+    part = torch.empty(cus * 64 * 256, device=dev)
+    for mode, name, nbytes in ((0, "stream_copy_1gib_gbs_read_plus_write", 2 * (1 << 30)),
+                               (1, "stream_read_1gib_gbs", 1 << 30)):
+        best = {}
+        for per_cu in (2, 4, 8, 16, 32, 64):
+            blocks = cus * per_cu
+            d = dst if mode == 0 else part
+            s = timed(lambda: _lib.call("tagi_probe_stream", src.data_ptr(), d.data_ptr(), n, blocks, mode, st), 10)
+            best[per_cu] = round(nbytes / s / 1e9, 1)
+        out[name] = max(best.values())
+        out[name + "_by_blocks_per_cu"] = best
+    del src, dst, part
     torch.backends.cuda.matmul.allow_tf32 = False
     a = torch.randn(8192, 8192, device=dev)
     b = torch.randn(8192, 8192, device=dev)
@@ -280,7 +293,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="resnet18", choices=sorted(WORKLOAD_DESC))
     ap.add_argument("--batch", type=int, default=None)
-    ap.add_argument("--cpu-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true",
                     help="time replays of a HIP graph of the step (Sequential.capture_step) instead of eager "
@@ -450,8 +462,8 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log(f"[bench] cpu baseline (oracle fp32, batch {args.cpu_batch})")
-        cpu = cpu_baseline(args.workload, args.cpu_batch)
+        log(f"[bench] cpu baseline (oracle fp32, batch {w.batch})")
+        cpu = cpu_baseline(args.workload, w.batch)
 
     out = {
         "metric": METRIC if args.workload == "resnet18" else

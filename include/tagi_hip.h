@@ -60,6 +60,13 @@ enum {
  * blocks*256 floats. blocks = 256*w on a 256-CU GPU gives w waves per SIMD. */
 int tagi_probe_mfma_loop(float* out, int64_t blocks, int64_t iters, tagi_stream_t stream);
 
+/* HBM ceiling probe (no counterpart in the reference; measurement only): mode 0 copies n
+ * floats src -> dst with float4 loads and stores, mode 1 reads n floats and writes one
+ * partial sum per thread (dst holds blocks*256 floats). Grid-stride over `blocks` blocks
+ * of 256 threads, 4 float4 loads in flight per thread. n % 4 == 0, 16-byte aligned. */
+int tagi_probe_stream(const float* src, float* dst, int64_t n, int64_t blocks, int mode,
+                      tagi_stream_t stream);
+
 /* ------------------------------------------------------------------ Linear ---- */
 /* Fused Linear forward moments, one MFMA pass sharing the A/B tiles:
  *   mz = ma @ mw + mb

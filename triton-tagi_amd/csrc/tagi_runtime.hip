@@ -145,7 +145,61 @@ __global__ void __launch_bounds__(256) mfma_loop_kernel(float* __restrict__ out,
     for (int v = 0; v < 16; ++v) s += acc[i][v];
   out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
+// HBM streaming probes. Each thread moves U float4 per grid-stride step with all U loads
+// issued before any store or add, so U * 16 bytes per lane are in flight.
+constexpr int kStreamU = 4;
+
+__global__ void __launch_bounds__(256) stream_copy_kernel(const float4* __restrict__ src, float4* __restrict__ dst,
+                                                          int64_t n4) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x * kStreamU;
+  for (int64_t base = (int64_t)blockIdx.x * blockDim.x * kStreamU + threadIdx.x; base < n4; base += stride) {
+    float4 v[kStreamU];
+#pragma unroll
+    for (int u = 0; u < kStreamU; ++u) {
+      const int64_t i = base + (int64_t)u * blockDim.x;
+      if (i < n4) v[u] = src[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kStreamU; ++u) {
+      const int64_t i = base + (int64_t)u * blockDim.x;
+      if (i < n4) dst[i] = v[u];
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) stream_read_kernel(const float4* __restrict__ src, float* __restrict__ out,
+                                                          int64_t n4) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x * kStreamU;
+  float acc = 0.f;
+  for (int64_t base = (int64_t)blockIdx.x * blockDim.x * kStreamU + threadIdx.x; base < n4; base += stride) {
+    float4 v[kStreamU];
+#pragma unroll
+    for (int u = 0; u < kStreamU; ++u) {
+      const int64_t i = base + (int64_t)u * blockDim.x;
+      v[u] = i < n4 ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < kStreamU; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+  }
+  out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;  // keeps the loads live
+}
 }  // namespace
+
+extern "C" int tagi_probe_stream(const float* src, float* dst, int64_t n, int64_t blocks, int mode,
+                                 tagi_stream_t stream) {
+  const char* what = "tagi_probe_stream";
+  TAGI_REQUIRE(src != nullptr && dst != nullptr && n > 0 && n % 4 == 0 && blocks > 0 && blocks <= (1 << 20) &&
+                   (mode == 0 || mode == 1) && (((uintptr_t)src | (uintptr_t)dst) & 15u) == 0,
+               "%s: bad arguments (n must be a positive multiple of 4, buffers 16-byte aligned, mode 0 or 1)", what);
+  hipStream_t s = (hipStream_t)stream;
+  if (mode == 0)
+    hipLaunchKernelGGL(stream_copy_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                       reinterpret_cast<const float4*>(src), reinterpret_cast<float4*>(dst), n / 4);
+  else
+    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                       reinterpret_cast<const float4*>(src), dst, n / 4);
+  return check_launch(what);
+}
 
 extern "C" int tagi_probe_mfma_loop(float* out, int64_t blocks, int64_t iters, tagi_stream_t stream) {
   const char* what = "tagi_probe_mfma_loop";
