@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define TAGI_ABI_VERSION 1
+#define TAGI_ABI_VERSION 2
 
 enum {
   TAGI_OK = 0,
@@ -348,8 +348,20 @@ int tagi_bn_relu_bwd_partials(const float* dma, const float* dSa, const float* m
                               float* dSz, int64_t N, int64_t C, int64_t HW, float eps, float* ws,
                               int64_t ws_bytes, tagi_stream_t stream);
 
-/* One layer left pending by tagi_bn_relu_bwd_partials: its partial sums (ws) and sizes,
- * the gamma/beta variances and the four parameter-delta outputs of length C. */
+/* tagi_bn_relu_bwd_partials that also leaves the per-channel sums of its outputs dmz and
+ * dSz in ws: the bias sums of the Conv2D whose output feeds the ReLU (conv2d.py:341-354,
+ * the column sums of its output deltas), so that Conv2D's parameter-delta GEMM needs no
+ * bias row. ws: size from tagi_bn_relu_bwd_bias_ws_bytes (six sums per channel). */
+int tagi_bn_relu_bwd_partials_bias(const float* dma, const float* dSa, const float* mhat,
+                                   const float* J, const float* var, const float* mg, float* dmz,
+                                   float* dSz, int64_t N, int64_t C, int64_t HW, float eps, float* ws,
+                                   int64_t ws_bytes, tagi_stream_t stream);
+int64_t tagi_bn_relu_bwd_bias_ws_bytes(int64_t N, int64_t C, int64_t HW);
+
+/* One layer left pending by tagi_bn_relu_bwd_partials(_bias): its partial sums (ws) and
+ * sizes, the gamma/beta variances and the four parameter-delta outputs of length C; for
+ * a layer left by the _bias variant also the conv's bias variances cSb and its two bias
+ * delta outputs (all three NULL otherwise). */
 typedef struct {
   const float* ws;
   const float* Sg;
@@ -359,10 +371,14 @@ typedef struct {
   float* dmb;
   float* dSb;
   int64_t N, C, HW;
+  const float* cSb;
+  float* cdmb;
+  float* cdSb;
 } tagi_bn_bwd_pending;
 
 /* The parameter deltas of count pending layers, in one launch per 32 layers:
- *   dmg = Sg * sum(dmu mhat), dSg = Sg^2 * sum(dS mhat^2), dmb = Sb * sum(dmu), dSb = Sb^2 * sum(dS). */
+ *   dmg = Sg * sum(dmu mhat), dSg = Sg^2 * sum(dS mhat^2), dmb = Sb * sum(dmu), dSb = Sb^2 * sum(dS);
+ * with conv bias outputs also cdmb = cSb * sum(dmz), cdSb = cSb^2 * sum(dSz). */
 int tagi_bn_bwd_finalize_multi(const tagi_bn_bwd_pending* items, int64_t count, tagi_stream_t stream);
 
 /* -------------------------------------------------- RMSNorm / Embedding / PE ---- */

@@ -227,8 +227,8 @@ def _install(monkeypatch, rec):
 
     orig_brb = fused.bn_relu_backward
 
-    def brb(bn, relu, dma, dSa):
-        out = orig_brb(bn, relu, dma, dSa)
+    def brb(bn, relu, dma, dSa, conv=None):
+        out = orig_brb(bn, relu, dma, dSa, conv)
         rec.append(dict(kind="brb", bn=bn, dma=cl(dma), dSa=cl(dSa), out=(cl(out[0]), cl(out[1]))))
         return out
 

@@ -90,8 +90,9 @@ static Plan conv_bwd_plan(const tagi_conv_geom* g) {
   return choose_plan(R, g->C, K, nph, PROD_SHARED_B, true, 16, pk);
 }
 
-static Plan conv_wgrad_plan(const tagi_conv_geom* g) {
-  return choose_plan(g->C * g->k * g->k + 1, g->Cout, g->N * g->Ho * g->Wo, 1, PROD_SHARED_A, true, 512);
+// rows: the weight rows (c, kh, kw), plus the ones row of the bias sums when the GEMM forms them
+static Plan conv_wgrad_plan(const tagi_conv_geom* g, bool bias) {
+  return choose_plan(g->C * g->k * g->k + (bias ? 1 : 0), g->Cout, g->N * g->Ho * g->Wo, 1, PROD_SHARED_A, true, 512);
 }
 
 static int64_t wt_floats(const tagi_conv_geom* g) { return ((g->C * g->k * g->k * g->Cout) + 3) / 4 * 4; }
@@ -320,7 +321,11 @@ extern "C" int tagi_conv2d_bwd_delta_add(const float* dmz, const float* dSz, con
 // ============================================================== parameter deltas
 extern "C" int64_t tagi_conv2d_wgrad_ws_bytes(const tagi_conv_geom* g) {
   if (!g || g->N <= 0 || g->Cout <= 0 || g->Ho <= 0 || g->Wo <= 0 || g->C <= 0 || g->k <= 0) return 0;
-  return plan_ws_bytes(conv_wgrad_plan(g), g->C * g->k * g->k + 1, g->Cout, 1);
+  // enough for either form (with or without the bias row)
+  const int64_t K = g->C * g->k * g->k;
+  const int64_t a = plan_ws_bytes(conv_wgrad_plan(g, true), K + 1, g->Cout, 1);
+  const int64_t b = plan_ws_bytes(conv_wgrad_plan(g, false), K, g->Cout, 1);
+  return a > b ? a : b;
 }
 
 extern "C" int tagi_conv2d_wgrad(const float* ma, const float* dmz, const float* dSz, const float* Sw, const float* Sb,
@@ -346,9 +351,9 @@ extern "C" int tagi_conv2d_wgrad(const float* ma, const float* dmz, const float*
   a.R = (int)(K + (bias ? 1 : 0));
   a.C = (int)N;
   a.Kred = (int)M;
-  Plan p = conv_wgrad_plan(g);
-  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, K + 1, N, 1)))
-    p = choose_plan(K + 1, N, M, 1, PROD_SHARED_A, false, 1);
+  Plan p = conv_wgrad_plan(g, bias);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, a.R, N, 1)))
+    p = choose_plan(a.R, N, M, 1, PROD_SHARED_A, false, 1);
   p.tiles_m = (int)cdiv(a.R, kCfg[p.cfg].BM);
   const bool va = g->C % 4 == 0 && al16(ma);
   const bool vb = g->Cout % 4 == 0 && al16(dmz) && al16(dSz);

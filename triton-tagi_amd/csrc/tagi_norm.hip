@@ -40,9 +40,11 @@ static inline int red_chunks(int nbr, int64_t C, bool vec) {
 //           y1 = dS g^2/(var+eps); sums dmu mhat, dS mhat^2, dmu, dS
 //   MODE 3  MODE 2 followed by the Jacobian of the ReLU in front of the BN (x3 = J):
 //           y0 = (dmu g/sqrt(var+eps)) J, y1 = (dS g^2/(var+eps)) J^2; same sums
+//   MODE 4  MODE 3, plus the sums of y0 and y1 (the bias sums of the convolution in
+//           front of the ReLU, whose output deltas y0, y1 are)
 template <int MODE>
 struct BnRed {
-  static constexpr int NQ = MODE >= 2 ? 4 : 3;
+  static constexpr int NQ = MODE == 4 ? 6 : (MODE >= 2 ? 4 : 3);
   __device__ __forceinline__ static void elem(float a, float b, float h, float j, float km, float kS, float* acc,
                                               float& o0, float& o1) {
     if constexpr (MODE == 0) {
@@ -63,9 +65,13 @@ struct BnRed {
       acc[3] += b;
       o0 = a * km;
       o1 = b * kS;
-      if constexpr (MODE == 3) {
+      if constexpr (MODE >= 3) {
         o0 = o0 * j;
         o1 = o1 * j * j;
+      }
+      if constexpr (MODE == 4) {
+        acc[4] += o0;
+        acc[5] += o1;
       }
     }
   }
@@ -79,7 +85,11 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
                                                         float* __restrict__ y0, float* __restrict__ y1, float eps) {
   using R = BnRed<MODE>;
   constexpr int NQ = R::NQ;
-  __shared__ float red[256 * 4 * NQ];
+  // per-thread partials, quantity-major with the thread index fastest (one bank per lane
+  // on the stores); the combine reads them with the channel's 4 lanes of a float4 group
+  // spread over the rows
+  constexpr int RP = 256 + 4;
+  __shared__ float red[4 * NQ * RP];
   const int64_t r0 = rows * blockIdx.x / nblk, r1 = rows * (blockIdx.x + 1) / nblk;
   const int t = threadIdx.x;
   if constexpr (VEC) {
@@ -108,7 +118,7 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
       const float4 b = *reinterpret_cast<const float4*>(x1 + off);
       float4 h = make_float4(0.f, 0.f, 0.f, 0.f), jj = h;
       if constexpr (MODE >= 2) h = *reinterpret_cast<const float4*>(x2 + off);
-      if constexpr (MODE == 3) jj = *reinterpret_cast<const float4*>(x3 + off);
+      if constexpr (MODE >= 3) jj = *reinterpret_cast<const float4*>(x3 + off);
       const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
       const float hv[4] = {h.x, h.y, h.z, h.w}, jv[4] = {jj.x, jj.y, jj.z, jj.w};
       float o0[4], o1[4];
@@ -120,13 +130,16 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) red[(t * 4 + j) * NQ + q] = acc[j][q];
+      for (int q = 0; q < NQ; ++q) red[(q * 4 + j) * RP + t] = acc[j][q];
     __syncthreads();
-    for (int cl = t; cl < W; cl += 256) {
-      const int g4 = cl >> 2, j = cl & 3;
+    // thread u combines channel 4 * g4 + j of the chunk, u = j * cq + g4 (lanes of one j
+    // read consecutive words)
+    for (int u = t; u < W; u += 256) {
+      const int j = u / cq, g4 = u - j * cq;
+      const int cl = 4 * g4 + j;
       for (int q = 0; q < NQ; ++q) {
         float sum = 0.f;
-        for (int r = 0; r < rpi; ++r) sum += red[((r * cq + g4) * 4 + j) * NQ + q];
+        for (int r = 0; r < rpi; ++r) sum += red[(q * 4 + j) * RP + r * cq + g4];
         ws[((int64_t)q * C + c0 + cl) * nblk + blockIdx.x] = sum;
       }
     }
@@ -144,7 +157,7 @@ __global__ void __launch_bounds__(256) bn_reduce_kernel(const float* __restrict_
       for (int64_t row = r0; row < r1; ++row) {
         const int64_t off = row * C + c;
         const float h = MODE >= 2 ? x2[off] : 0.f;
-        const float j = MODE == 3 ? x3[off] : 0.f;
+        const float j = MODE >= 3 ? x3[off] : 0.f;
         float o0 = 0.f, o1 = 0.f;
         R::elem(x0[off], x1[off], h, j, kmc, kSc, acc, o0, o1);
         if constexpr (MODE >= 1) y0[off] = o0;
@@ -345,6 +358,9 @@ struct BnFinalizeMulti {
   float* dSg[kBnMulti];
   float* dmb[kBnMulti];
   float* dSb[kBnMulti];
+  const float* cSb[kBnMulti];  // bias variances of the conv in front (six-sum layers), else null
+  float* cdmb[kBnMulti];
+  float* cdSb[kBnMulti];
   int C[kBnMulti];
   int nblk[kBnMulti];
   int start[kBnMulti + 1];
@@ -356,14 +372,23 @@ __global__ void __launch_bounds__(256) bn_bwd_finalize_multi_kernel(BnFinalizeMu
   int t = 0;
   while (t + 1 < a.count && a.start[t + 1] <= b) ++t;
   const int c = b - a.start[t];
-  float sums[4];
-  channel_sums<4>(a.ws[t], a.C[t], c, a.nblk[t], sums);
+  float sums[6];
+  const bool conv_bias = a.cdmb[t] != nullptr;
+  if (conv_bias)
+    channel_sums<6>(a.ws[t], a.C[t], c, a.nblk[t], sums);
+  else
+    channel_sums<4>(a.ws[t], a.C[t], c, a.nblk[t], sums);
   if (threadIdx.x != 0) return;
   const float g = a.Sg[t][c], bb = a.Sb[t][c];
   a.dmg[t][c] = g * sums[0];
   a.dSg[t][c] = g * g * sums[1];
   a.dmb[t][c] = bb * sums[2];
   a.dSb[t][c] = bb * bb * sums[3];
+  if (conv_bias) {
+    const float cb = a.cSb[t][c];
+    a.cdmb[t][c] = cb * sums[4];
+    a.cdSb[t][c] = cb * cb * sums[5];
+  }
 }
 
 // --------------------------------------------------------------------- RMSNorm
@@ -869,15 +894,22 @@ extern "C" int64_t tagi_bn_bwd_ws_bytes(int64_t N, int64_t C, int64_t HW) {
   return (int64_t)red_rows(N * HW) * C * 4 * (int64_t)sizeof(float);
 }
 
+extern "C" int64_t tagi_bn_relu_bwd_bias_ws_bytes(int64_t N, int64_t C, int64_t HW) {
+  if (N <= 0 || C <= 0 || HW <= 0) return 0;
+  return (int64_t)red_rows(N * HW) * C * 6 * (int64_t)sizeof(float);
+}
+
 static int bn_bwd_impl(const char* what, const float* dma, const float* dSa, const float* mhat, const float* J,
                        const float* var, const float* mg, const float* Sg, const float* Sb, float* dmz, float* dSz,
                        float* dmg, float* dSg, float* dmb, float* dSb, int64_t N, int64_t C, int64_t HW, float eps,
-                       float* ws, int64_t ws_bytes, tagi_stream_t stream, bool jac, bool finalize = true) {
+                       float* ws, int64_t ws_bytes, tagi_stream_t stream, bool jac, bool finalize = true,
+                       bool bias_sums = false) {
   TAGI_REQUIRE(dma && dSa && mhat && var && mg && dmz && dSz && ws && (!jac || J) &&
                    (!finalize || (Sg && Sb && dmg && dSg && dmb && dSb)),
                "%s: null pointer", what);
   TAGI_REQUIRE(N > 0 && C > 0 && HW > 0, "%s: bad sizes", what);
-  TAGI_REQUIRE(ws_bytes >= tagi_bn_bwd_ws_bytes(N, C, HW), "%s: workspace too small", what);
+  TAGI_REQUIRE(ws_bytes >= (bias_sums ? tagi_bn_relu_bwd_bias_ws_bytes(N, C, HW) : tagi_bn_bwd_ws_bytes(N, C, HW)),
+               "%s: workspace too small", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_BN_BWD, s, 0.0, (jac ? 24.0 : 20.0) * N * C * HW);
   const int64_t rows = N * HW;
@@ -885,7 +917,14 @@ static int bn_bwd_impl(const char* what, const float* dma, const float* dSa, con
   const bool vec = bn_vec(C) && al16p(dma) && al16p(dSa) && al16p(mhat) && al16p(dmz) && al16p(dSz) &&
                    (!jac || al16p(J));
   const dim3 grid(nblk, red_chunks(nblk, C, vec)), blk(256);
-  if (jac) {
+  if (bias_sums) {
+    if (vec)
+      hipLaunchKernelGGL((bn_reduce_kernel<4, true>), grid, blk, 0, s, dma, dSa, mhat, J, ws, rows, (int)C, nblk, var,
+                         mg, dmz, dSz, eps);
+    else
+      hipLaunchKernelGGL((bn_reduce_kernel<4, false>), grid, blk, 0, s, dma, dSa, mhat, J, ws, rows, (int)C, nblk,
+                         var, mg, dmz, dSz, eps);
+  } else if (jac) {
     if (vec)
       hipLaunchKernelGGL((bn_reduce_kernel<3, true>), grid, blk, 0, s, dma, dSa, mhat, J, ws, rows, (int)C, nblk, var,
                          mg, dmz, dSz, eps);
@@ -931,6 +970,14 @@ extern "C" int tagi_bn_relu_bwd_partials(const float* dma, const float* dSa, con
                      nullptr, nullptr, nullptr, N, C, HW, eps, ws, ws_bytes, stream, true, false);
 }
 
+extern "C" int tagi_bn_relu_bwd_partials_bias(const float* dma, const float* dSa, const float* mhat, const float* J,
+                                              const float* var, const float* mg, float* dmz, float* dSz, int64_t N,
+                                              int64_t C, int64_t HW, float eps, float* ws, int64_t ws_bytes,
+                                              tagi_stream_t stream) {
+  return bn_bwd_impl("tagi_bn_relu_bwd_partials_bias", dma, dSa, mhat, J, var, mg, nullptr, nullptr, dmz, dSz, nullptr,
+                     nullptr, nullptr, nullptr, N, C, HW, eps, ws, ws_bytes, stream, true, false, true);
+}
+
 extern "C" int tagi_bn_bwd_finalize_multi(const tagi_bn_bwd_pending* items, int64_t count, tagi_stream_t stream) {
   const char* what = "tagi_bn_bwd_finalize_multi";
   TAGI_REQUIRE(count >= 0 && (count == 0 || items), "%s: bad table", what);
@@ -941,7 +988,10 @@ extern "C" int tagi_bn_bwd_finalize_multi(const tagi_bn_bwd_pending* items, int6
     TAGI_REQUIRE(p.ws && p.Sg && p.Sb && p.dmg && p.dSg && p.dmb && p.dSb, "%s: null pointer at %lld", what,
                  (long long)i);
     TAGI_REQUIRE(p.N > 0 && p.C > 0 && p.HW > 0 && p.C < (1 << 24), "%s: bad sizes at %lld", what, (long long)i);
-    bytes += (int64_t)red_rows(p.N * p.HW) * p.C * 16 + 24 * p.C;
+    TAGI_REQUIRE((p.cdmb == nullptr) == (p.cdSb == nullptr) && (p.cdmb == nullptr || p.cSb != nullptr),
+                 "%s: conv bias outputs at %lld must be all given or all NULL", what, (long long)i);
+    const bool cb = p.cdmb != nullptr;
+    bytes += (int64_t)red_rows(p.N * p.HW) * p.C * (cb ? 24 : 16) + (cb ? 36 : 24) * p.C;
   }
   ProfScope ps(FAM_BN_BWD, s, 0.0, (double)bytes);
   for (int64_t t0 = 0; t0 < count; t0 += kBnMulti) {
@@ -956,6 +1006,9 @@ extern "C" int tagi_bn_bwd_finalize_multi(const tagi_bn_bwd_pending* items, int6
       a.dSg[c] = p.dSg;
       a.dmb[c] = p.dmb;
       a.dSb[c] = p.dSb;
+      a.cSb[c] = p.cSb;
+      a.cdmb[c] = p.cdmb;
+      a.cdSb[c] = p.cdSb;
       a.C[c] = (int)p.C;
       a.nblk[c] = red_rows(p.N * p.HW);
       a.start[c] = blocks;

@@ -50,7 +50,7 @@ class BnPending(ctypes.Structure):
 
     _fields_ = [(n, c_void_p) for n in ("ws", "Sg", "Sb", "dmg", "dSg", "dmb", "dSb")] + [
         (n, c_int64) for n in ("N", "C", "HW")
-    ]
+    ] + [(n, c_void_p) for n in ("cSb", "cdmb", "cdSb")]
 
 
 VP = POINTER(TagiView)
@@ -104,6 +104,8 @@ _SIGS = {
     "tagi_relu_bn_fwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P]),
     "tagi_bn_relu_bwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P, I64, P]),
     "tagi_bn_relu_bwd_partials": (c_int, [P, P, P, P, P, P, P, P, I64, I64, I64, F, P, I64, P]),
+    "tagi_bn_relu_bwd_partials_bias": (c_int, [P, P, P, P, P, P, P, P, I64, I64, I64, F, P, I64, P]),
+    "tagi_bn_relu_bwd_bias_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_bn_bwd_finalize_multi": (c_int, [BP, I64, P]),
     "tagi_rmsnorm_fwd": (c_int, [P, P, P, P, P, P, P, I64, I64, F, P]),
     "tagi_rmsnorm_bwd": (c_int, [P, P, P, P, P, P, P, P, P, P, I64, I64, P, I64, P]),

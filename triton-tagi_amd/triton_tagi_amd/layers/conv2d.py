@@ -45,6 +45,8 @@ class Conv2D(LearnableLayer):
         self.input_shape = None
         self.spatial = None
         self.delta_mw = self.delta_Sw = self.delta_mb = self.delta_Sb = None
+        # set by a fused BatchNorm2D -> ReLU backward pass that forms this layer's bias deltas
+        self._bias_deltas_pending = False
 
     def _geom(self, N, C, H, W) -> _lib.ConvGeom:
         k, s, p = self.kH, self.stride, self.padding
@@ -105,17 +107,23 @@ class Conv2D(LearnableLayer):
         K = self.C_in * self.kH * self.kW
         ctx = _overlap.active()
         big = N * g.Ho * g.Wo * K * self.C_out >= _overlap.MIN_MACS_CONV
+        # bias deltas already formed by the fused BatchNorm2D -> ReLU pass that produced these
+        # deltas (finalized with the BatchNorm parameter deltas): no bias row in the GEMM
+        bias_done = self._bias_deltas_pending
+        self._bias_deltas_pending = False
         side = ctx.fork(dev, self.ma_in, dmz, dSz) if ctx is not None and big else None
         with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
             self.delta_mw = torch.empty(K, self.C_out, device=dev, dtype=torch.float32)
             self.delta_Sw = torch.empty_like(self.delta_mw)
-            self.delta_mb = torch.empty(1, self.C_out, device=dev, dtype=torch.float32)
-            self.delta_Sb = torch.empty_like(self.delta_mb)
+            if not bias_done:
+                self.delta_mb = torch.empty(1, self.C_out, device=dev, dtype=torch.float32)
+                self.delta_Sb = torch.empty_like(self.delta_mb)
             ws = _lib.workspace(_lib.query("tagi_conv2d_wgrad_ws_bytes", g), dev)
             wp, wb = _lib.ws_args(ws)
             _lib.call("tagi_conv2d_wgrad", self.ma_in.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), self.Sw.data_ptr(),
                       self.Sb.data_ptr(), self.delta_mw.data_ptr(), self.delta_Sw.data_ptr(),
-                      self.delta_mb.data_ptr(), self.delta_Sb.data_ptr(), g, wp, wb, _lib.stream_of(dmz))
+                      None if bias_done else self.delta_mb.data_ptr(),
+                      None if bias_done else self.delta_Sb.data_ptr(), g, wp, wb, _lib.stream_of(dmz))
         st = _lib.stream_of(dmz)
         if not input_deltas:
             return None

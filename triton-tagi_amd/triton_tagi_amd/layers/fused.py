@@ -50,11 +50,14 @@ class defer_bn_parameter_deltas:
         _scope.ctx = self
         return self
 
-    def add(self, bn: BatchNorm2D, ws: Tensor, N: int, C: int, HW: int) -> None:
+    def add(self, bn: BatchNorm2D, ws: Tensor, N: int, C: int, HW: int, conv: Conv2D | None = None) -> None:
+        """``conv``: the Conv2D in front of the ReLU, whose bias sums ``ws`` also holds."""
         self._keep.append(ws)  # the partial sums must outlive the launch below
+        cb = (None, None, None) if conv is None else (conv.Sb.data_ptr(), conv.delta_mb.data_ptr(),
+                                                      conv.delta_Sb.data_ptr())
         self.items.append(_lib.BnPending(ws.data_ptr(), bn.Sw.data_ptr(), bn.Sb.data_ptr(), bn.delta_mw.data_ptr(),
                                          bn.delta_Sw.data_ptr(), bn.delta_mb.data_ptr(), bn.delta_Sb.data_ptr(),
-                                         N, C, HW))
+                                         N, C, HW, *cb))
         self._stream = _lib.stream_of(ws)
 
     def __exit__(self, exc_type, exc, tb):
@@ -150,8 +153,14 @@ def _relu_bn_apply(relu: ReLU, bn: BatchNorm2D, mz: Tensor, Sz: Tensor, J: Tenso
     return ma, Sa
 
 
-def bn_relu_backward(bn: BatchNorm2D, relu: ReLU, delta_ma: Tensor, delta_Sa: Tensor) -> tuple[Tensor, Tensor]:
-    """relu.backward(*bn.backward(delta_ma, delta_Sa)) in one pass; stores the BN deltas."""
+def bn_relu_backward(bn: BatchNorm2D, relu: ReLU, delta_ma: Tensor, delta_Sa: Tensor,
+                     conv: Conv2D | None = None) -> tuple[Tensor, Tensor]:
+    """relu.backward(*bn.backward(delta_ma, delta_Sa)) in one pass; stores the BN deltas.
+
+    Within ``defer_bn_parameter_deltas``, ``conv`` (the Conv2D whose output the ReLU
+    takes) gets its bias deltas from the same pass: the column sums of the returned
+    deltas are formed with the BN sums (conv2d.py:341-354), and the conv's parameter-delta
+    GEMM then runs without its bias row."""
     dma = _lib.check(_lib.channels_last(delta_ma.reshape(bn.input_shape)), "delta_ma")
     dSa = _lib.check(_lib.channels_last(delta_Sa.reshape(bn.input_shape)), "delta_Sa")
     J = _lib.check(_lib.like(relu.J, dma), "J")
@@ -168,6 +177,17 @@ def bn_relu_backward(bn: BatchNorm2D, relu: ReLU, delta_ma: Tensor, delta_Sa: Te
     ws = _lib.workspace(_lib.query("tagi_bn_bwd_ws_bytes", N, C, HW), dev)
     wp, wb = _lib.ws_args(ws)
     ctx = getattr(_scope, "ctx", None)
+    if ctx is not None and conv is not None and conv.C_out == C and conv.mb is not None:
+        conv.delta_mb = torch.empty(1, C, device=dev, dtype=torch.float32)
+        conv.delta_Sb = torch.empty_like(conv.delta_mb)
+        ws = _lib.workspace(_lib.query("tagi_bn_relu_bwd_bias_ws_bytes", N, C, HW), dev)
+        wp, wb = _lib.ws_args(ws)
+        _lib.call("tagi_bn_relu_bwd_partials_bias", dma.data_ptr(), dSa.data_ptr(), bn.m_hat.data_ptr(),
+                  J.data_ptr(), bn._norm_var.data_ptr(), bn.mw.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), N, C, HW,
+                  float(bn.eps), wp, wb, _lib.stream_of(dma))
+        ctx.add(bn, ws, N, C, HW, conv=conv)
+        conv._bias_deltas_pending = True
+        return dmz, dSz
     if ctx is not None:
         _lib.call("tagi_bn_relu_bwd_partials", dma.data_ptr(), dSa.data_ptr(), bn.m_hat.data_ptr(), J.data_ptr(),
                   bn._norm_var.data_ptr(), bn.mw.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), N, C, HW,
@@ -234,7 +254,8 @@ def backward_chain(layers, delta_mu: Tensor, delta_var: Tensor, add: tuple[Tenso
         layer = layers[i]
         prev = layers[i - 1] if i >= 1 else None
         if _fusable_backward(layer, prev):
-            delta_mu, delta_var = bn_relu_backward(layer, prev, delta_mu, delta_var)
+            conv = layers[i - 2] if i >= 2 and isinstance(layers[i - 2], Conv2D) else None
+            delta_mu, delta_var = bn_relu_backward(layer, prev, delta_mu, delta_var, conv)
             i -= 2
             continue
         if i == 0:
