@@ -174,13 +174,19 @@ def bmm_shared_left(a, b_mean, b_var, scale=1.0):
 
 
 def sinusoidal_table(max_seq_len, embed_dim):
-    """layers/positional_encoding.py:45-52 (frequency exponent d/E with d as a float)."""
-    d = torch.arange(embed_dim, dtype=DT)
-    pos = torch.arange(max_seq_len, dtype=DT)
-    freq = 1.0 / torch.pow(torch.tensor(10000.0, dtype=DT), d / embed_dim)
+    """layers/positional_encoding.py:45-52 (frequency exponent d/E with d as a float).
+
+    The table is a constant of the layer that the reference builds in float32 (angle =
+    t * freq rounded to float32 before sin/cos); it is built the same way here and then
+    widened, so it holds the reference's values rather than the float64 ones (they differ
+    by the float32 rounding of the angle, up to ~1e-4 at t = 2047)."""
+    f32 = torch.float32
+    d = torch.arange(embed_dim, dtype=f32)
+    pos = torch.arange(max_seq_len, dtype=f32)
+    freq = 1.0 / torch.pow(10000.0, d / embed_dim)
     angle = pos.unsqueeze(1) * freq.unsqueeze(0)
     even = (torch.arange(embed_dim) % 2 == 0).unsqueeze(0)
-    return torch.where(even, torch.sin(angle), torch.cos(angle))
+    return torch.where(even, torch.sin(angle), torch.cos(angle)).to(DT)
 
 
 # =========================================================================== layers

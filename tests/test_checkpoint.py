@@ -103,6 +103,48 @@ def test_reference_written_file_loads(tmp_path):
     assert torch.all(got.layers[4].mw == 0.5) and torch.equal(got.layers[7].running_mean, torch.arange(4.0))
 
 
+def golden_net():
+    """The topology of tests/golden/checkpoint_golden.pt (written by the reference's
+    RunDir.save_checkpoint, tests/golden/make_pe_checkpoint_golden.py)."""
+    torch.manual_seed(0)
+    return tt.Sequential([tt.Conv2D(3, 4, 3, padding=1, device="cpu"), tt.ReLU(), tt.BatchNorm2D(4, device="cpu"),
+                          tt.ResBlock(4, 8, 2, device="cpu"), tt.AvgPool2D(2), tt.Flatten(),
+                          tt.Linear(8 * 2 * 2, 5, device="cpu")], device="cpu")
+
+
+def test_file_written_by_the_reference_loads_and_resaves_identically(tmp_path):
+    from pathlib import Path
+
+    golden = Path(__file__).resolve().parent / "golden" / "checkpoint_golden.pt"
+    ref = torch.load(golden, weights_only=True)  # executes nothing from the file
+    net, cfg, ep = tt.load_model(golden, lambda c: golden_net(), device="cpu")
+    assert ep == 12 and cfg == {"arch": "smallcnn", "batch": 4, "sigma_v": 0.05}
+    # every tensor the reference saved is now in the engine's layer, at the same index
+    ls = net.layers
+    targets = {0: ls[0], 2: ls[2], 3: ls[3]._learnable, 6: ls[6]}
+    n = 0
+    for i, st in ref["net_state"].items():
+        layers = targets[i] if isinstance(st, list) else [targets[i]]
+        sts = st if isinstance(st, list) else [st]
+        assert len(layers) == len(sts)
+        for layer, d in zip(layers, sts):
+            for a, t in d.items():
+                assert torch.equal(getattr(layer, a), t), (i, type(layer).__name__, a)
+                n += 1
+    assert n == 4 + 6 + 3 * 4 + 3 * 6 + 4
+    # and the engine writes the same layout back: keys, nesting, shapes, values
+    run = tt.RunDir("synthetic", "smallcnn", "tagi", base=str(tmp_path))
+    mine = torch.load(run.save_checkpoint(net, 12, cfg), weights_only=True)
+    assert mine["epoch"] == ref["epoch"] and mine["config"] == ref["config"]
+    assert set(mine["net_state"]) == set(ref["net_state"])
+    for i, st in ref["net_state"].items():
+        got = mine["net_state"][i]
+        assert type(got) is type(st)
+        for dg, dr in zip(got if isinstance(got, list) else [got], st if isinstance(st, list) else [st]):
+            assert set(dg) == set(dr)
+            assert all(torch.equal(dg[a], dr[a]) for a in dr)
+
+
 def test_shape_mismatch_and_unsafe_files_are_refused(tmp_path):
     net = build()
     p = tmp_path / "bad.pt"

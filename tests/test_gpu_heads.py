@@ -111,6 +111,39 @@ def test_class_probs_and_predicted_labels(dev, n_classes, B):
     assert torch.equal(get_predicted_labels(ma.to(dev), Sa.to(dev), h).cpu(), P.argmax(1))
 
 
+def test_class_probs_in_the_far_tails(dev):
+    """Node moments with |mu| / sqrt(1/alpha^2 + S) from 6 to 40: the node probability
+    Phi is formed as Q(-x) = erfc(-x/sqrt 2)/2 here, so the far-tail class probabilities
+    are the tiny positive values of exact arithmetic (the float64 oracle, torch's ndtr),
+    held to the 1e-4 bar; the reference's float32 0.5*(1+erf(x/sqrt 2)) rounds them to
+    exactly 0 below x ~ -5.9 (hrc_softmax.py:164-208). Either way they are far below the
+    absolute tolerance and the predicted labels are the oracle's."""
+    from triton_tagi_amd.hrc_softmax import class_to_obs, get_predicted_labels, obs_to_class_probs
+
+    h = class_to_obs(10)
+    r = g(77)
+    B = 64
+    sign = torch.where(torch.rand(B, h.len, generator=r) < 0.5, -1.0, 1.0)
+    ma = sign * (6.0 + 34.0 * torch.rand(B, h.len, generator=r)) * (1.0 / 3.0)
+    Sa = torch.zeros(B, h.len)
+    P = obs_to_class_probs(ma.to(dev), Sa.to(dev), h)
+    R = O.hrc_class_probs(d64(ma), d64(Sa), d64(h.obs), h.idx.long(), 3.0)
+    assert_scaled_close(P, R, None, RTOL, ATOL, "far-tail class probabilities")
+    # the reference's float32 form of the same products (zeros in the far tails) sits within
+    # the same tolerance of the oracle
+    x = ma / torch.sqrt(torch.tensor(1.0 / 9.0) + Sa)
+    node = (0.5 * (1.0 + torch.erf(x * 0.7071067811865476)))[:, h.idx.long() - 1]
+    ref32 = torch.where(h.obs > 0, node, 1.0 - node).prod(dim=2)
+    assert_scaled_close(ref32, R, None, RTOL, ATOL, "reference float32 form")
+    # labels where some class keeps a probability float32 can hold; in rows where every
+    # class path crosses a node far in its tail all products are below 1e-30 and the label
+    # is decided by rounding in every implementation
+    pred = get_predicted_labels(ma.to(dev), Sa.to(dev), h).cpu()
+    ok = R.max(1).values > 1e-30
+    assert ok.sum() > B // 2
+    assert torch.equal(pred[ok], R.argmax(1)[ok])
+
+
 # ---------------------------------------------------------- heteroscedastic head
 @pytest.mark.parametrize("shape,offset", [((4, 10), 0), ((128, 1), 0), ((3, 7), 1), ((64, 256, 8), 0)])
 def test_heteros_innovation(dev, shape, offset):

@@ -385,7 +385,21 @@ def test_rmsnorm_embedding_pe(dev):
     ma = torch.randn(3, 200, 64, generator=r)
     out, _ = pe.forward(ma.to(dev), ma.to(dev))
     ro, _ = pref.forward(d64(ma), d64(ma))
-    assert_scaled_close(out, ro, ro.abs() + 1, RTOL, ATOL, "pe add")
+    assert_scaled_close(out, ro, d64(ma).abs() + pref.pe[:200].abs(), RTOL, ATOL, "pe add")
+
+    # the transformer block's table, built on the GPU, against the table the reference wrote
+    from pathlib import Path
+
+    import numpy as np
+
+    gold = np.load(Path(__file__).resolve().parent / "golden" / "pe_golden.npz")
+    pe_dev = PositionalEncoding(256, max_seq_len=2048, device=dev)
+    rows = torch.tensor(gold["e256_rows"])
+    assert_scaled_close(pe_dev.pe_cache[rows.to(dev)], torch.tensor(gold["e256"], dtype=torch.float64), None,
+                        RTOL, ATOL, "PE table (GPU) vs the reference's")
+    z = torch.zeros(2, 256, 256, device=dev)
+    out, _ = pe_dev.forward(z, z)
+    assert torch.equal(out[1].cpu(), pe_dev.pe_cache[:256].cpu())
 
 
 @pytest.mark.parametrize("B,S,E,H", [(2, 16, 32, 2), (3, 40, 64, 8), (2, 256, 256, 8)])

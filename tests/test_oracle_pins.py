@@ -481,12 +481,35 @@ def test_embedding_gather_scatter_by_loops():
         torch.testing.assert_close(e.delta_Sw, eS)
 
 
-def test_positional_encoding_table():
-    pe = O.sinusoidal_table(7, 6)
-    for t in range(7):
-        for d in range(6):
-            a = t / (10000.0 ** (d / 6))
-            assert abs(pe[t, d].item() - (math.sin(a) if d % 2 == 0 else math.cos(a))) < 1e-12
+def test_positional_encoding_table_against_reference_golden():
+    """The oracle's table and the engine's table builder against the tables the reference
+    wrote (tests/golden/make_pe_checkpoint_golden.py): equal. Against exact arithmetic the
+    reference's float32 angles put its entries within |fl(a) - a| <= a * 2^-24 (+ the
+    float32 sin/cos rounding) of sin/cos of the exact angle, which the golden table must
+    meet; a pair-rounded exponent 2*(d//2)/E or swapped sin/cos is far off."""
+    from triton_tagi_amd.layers.positional_encoding import sinusoidal_table
+
+    d = np.load(Path(__file__).resolve().parent / "golden" / "pe_golden.npz")
+    rows = torch.tensor(d["e256_rows"])
+    ref_big, ref_small = torch.tensor(d["e256"], dtype=D), torch.tensor(d["e6_s7"], dtype=D)
+    assert torch.equal(O.sinusoidal_table(2048, 256)[rows], ref_big)
+    assert torch.equal(O.sinusoidal_table(7, 6), ref_small)
+    assert torch.equal(sinusoidal_table(2048, 256).double()[rows], ref_big)
+    assert torch.equal(sinusoidal_table(7, 6).double(), ref_small)
+
+    def exact(pos, E, pair=False):
+        dd = torch.arange(E, dtype=D)
+        e = 2 * (dd // 2) if pair else dd
+        ang = pos.to(D).unsqueeze(1) / torch.pow(torch.tensor(10000.0, dtype=D), e / E).unsqueeze(0)
+        even = (torch.arange(E) % 2 == 0).unsqueeze(0)
+        return torch.where(even, torch.sin(ang), torch.cos(ang)), ang
+
+    ex, ang = exact(rows, 256)
+    assert ((ref_big - ex).abs() <= ang * 2.0**-23 + 2e-7).all()
+    ex_s, ang_s = exact(torch.arange(7), 6)
+    assert ((ref_small - ex_s).abs() <= ang_s * 2.0**-23 + 2e-7).all()
+    assert (exact(rows, 256, pair=True)[0] - ref_big).abs().max() > 0.1
+    assert (ref_small[:, [1, 0, 3, 2, 5, 4]] - ex_s).abs().max() > 0.1
 
 
 # -------------------------------------------------------- update / innovation / priors

@@ -27,7 +27,10 @@ class PositionalEncoding(Layer):
         self.embed_dim = embed_dim
         self.max_seq_len = max_seq_len
         self.device = torch.device(device)
-        self.pe_cache = sinusoidal_table(max_seq_len, embed_dim, device=self.device)
+        # built on the CPU whatever the device: the float32 angles t * freq reach ~2000 rad, so
+        # a one-ulp difference between two devices' pow() moves an entry by up to ~1e-4; the
+        # CPU table is the same on every machine (and equal to the reference's CPU table)
+        self.pe_cache = sinusoidal_table(max_seq_len, embed_dim, device="cpu").to(self.device)
 
     def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
         S, E = ma.shape[-2], ma.shape[-1]
