@@ -30,8 +30,11 @@ static ConvG to_g(const tagi_conv_geom* g) {
   return c;
 }
 
-static Operand conv_operand(const float* p0, const float* p1, const tagi_conv_geom* g, int64_t MN, int64_t K) {
+// elems: the tensor's element count (its reach from p0)
+static Operand conv_operand(const float* p0, const float* p1, const tagi_conv_geom* g, int64_t MN, int64_t K,
+                            int64_t elems) {
   Operand o{};
+  o.nbytes = 4 * elems;
   o.p0 = p0;
   o.p1 = p1;
   o.zdiv = 1;
@@ -134,8 +137,8 @@ static int conv_fwd_impl(const char* what, const float* ma, const float* Sa, con
   const int64_t R = g->N * g->Ho * g->Wo, C = g->Cout, K = g->C * g->k * g->k;
   ProfScope ps(FAM_CONV_FWD, s, 2.0 * 3 * R * C * K, 4.0 * (2 * g->N * g->C * g->H * g->W + 2 * K * C + 2 * R * C));
   GemmArgs a{};
-  a.a = conv_operand(ma, Sa, g, R, K);
-  a.b = conv_operand(mw, Sw, g, C, K);
+  a.a = conv_operand(ma, Sa, g, R, K, g->N * g->C * g->H * g->W);
+  a.b = conv_operand(mw, Sw, g, C, K, K * g->Cout);
   a.epi = epi_store(mz, Sz, mb, Sb, 0, 1, 1.f, 1.f, 1, 0, 0, C, 1);
   if (st_ws) {
     TAGI_REQUIRE(p.splits == 1 && st_J, "%s: internal: statistics epilogue needs an unsplit launch", what);
@@ -263,8 +266,8 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
   int64_t R0, K0;
   bwd_phase0(g, &R0, &K0);
   GemmArgs a{};
-  a.a = conv_operand(dmz, dSz, g, R0, K0);
-  a.b = conv_operand(in_place ? mw : wt, nullptr, g, g->C, K0);
+  a.a = conv_operand(dmz, dSz, g, R0, K0, g->N * g->Cout * g->Ho * g->Wo);
+  a.b = conv_operand(in_place ? mw : wt, nullptr, g, g->C, K0, g->C * g->k * g->k * g->Cout);
   a.epi = Epi{};
   a.epi.kind = 2;
   a.epi.om = dma;
@@ -341,7 +344,7 @@ extern "C" int tagi_conv2d_wgrad(const float* ma, const float* dmz, const float*
   const bool bias = dmb != nullptr;
   ProfScope ps(FAM_CONV_WGRAD, s, 2.0 * 2 * M * K * N, 4.0 * (g->N * g->C * g->H * g->W + 2 * M * N + 3 * K * N));
   GemmArgs a{};
-  a.a = conv_operand(ma, nullptr, g, K, M);
+  a.a = conv_operand(ma, nullptr, g, K, M, g->N * g->C * g->H * g->W);
   if (bias) a.a.ones_row = (int)K;
   a.b = strided_operand(dmz, dSz, 1, 0, 0, 1, N, N, M);
   a.epi = epi_wgrad(dmw, dSw, dmb, dSb, Sw, Sb, K, N);

@@ -67,24 +67,25 @@ struct KindTraits {
 };
 
 // Exact division by an invariant d >= 1 for dividends 0 <= n < 2^31 (Granlund and
-// Montgomery, "Division by invariant integers using multiplication", 1994): with
-// l = ceil(log2 d), p = 31 + l and m = ceil(2^p / d) (which fits 32 bits),
-// floor(n / d) = (n * m) >> p, because 0 <= m d - 2^p < d <= 2^(p - 31).
+// Montgomery, "Division by invariant integers using multiplication", 1994, the
+// round-up multiplier with the add-back step): with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1 (which fits 32 bits), floor(n / d) =
+// (umulhi(n, m) + n) >> l. The sum stays below 2^32 because umulhi(n, m) <= n < 2^31.
+// Three full-rate 32-bit instructions (multiply-high, add, shift).
 struct FastDiv {
   uint32_t m;
-  int p;
+  int l;
 };
 
 __host__ __device__ inline FastDiv make_fastdiv(int d) {
   int l = 0;
   while ((1ll << l) < (long long)d) ++l;
-  const int p = 31 + l;
-  const uint64_t two_p = 1ull << p;
-  return FastDiv{(uint32_t)((two_p + (uint64_t)d - 1) / (uint64_t)d), p};
+  const uint64_t num = ((1ull << l) - (uint64_t)d) << 32;
+  return FastDiv{(uint32_t)(num / (uint64_t)d + 1), l};
 }
 
 __device__ __forceinline__ int fdiv(int n, FastDiv f) {
-  return (int)(((uint64_t)(uint32_t)n * f.m) >> f.p);
+  return (int)((__umulhi((uint32_t)n, f.m) + (uint32_t)n) >> f.l);
 }
 
 struct ConvG {
@@ -121,7 +122,34 @@ struct Operand {
   int ones_row;            // tile index that reads as 1.0 for valid k (bias row), -1 = none
   int64_t pad;             // one-hot kinds: category that reads as all zeros (-1 = none)
   ConvG g;                 // conv kinds
+  int64_t nbytes;          // bytes reachable from the operand's (per-batch) base; < 2^31
 };
+
+// Buffer loads (MUBUF, raw, offset in a VGPR): the operand tensors are read through a
+// buffer resource held in scalar registers, so the per-lane address is a 32-bit byte
+// offset (no 64-bit address arithmetic) and a chunk outside the operand or in the conv
+// zero padding is given an offset past the resource's range, for which the hardware
+// returns zeros (no exec-mask branch and no select per element).
+typedef int tagi_i32x4 __attribute__((ext_vector_type(4)));
+typedef float tagi_f32x4 __attribute__((ext_vector_type(4)));
+__device__ tagi_f32x4 tagi_raw_buffer_load_f32x4(tagi_i32x4 rsrc, int voffset, int soffset,
+                                                 int aux) __asm("llvm.amdgcn.raw.buffer.load.v4f32");
+__device__ float tagi_raw_buffer_load_f32(tagi_i32x4 rsrc, int voffset, int soffset,
+                                          int aux) __asm("llvm.amdgcn.raw.buffer.load.f32");
+
+constexpr uint32_t kBufOutOfRange = 0x80000000u;  // byte offset past every operand's range
+
+// Resource of `nbytes` bytes at `base`: 48-bit base address, stride 0, the range in bytes,
+// and the gfx9 raw-buffer format word.
+__device__ __forceinline__ tagi_i32x4 make_buffer_rsrc(const float* base, int64_t nbytes) {
+  const uint64_t a = (uint64_t)base;
+  tagi_i32x4 r;
+  r.x = (int)(uint32_t)a;
+  r.y = (int)((a >> 32) & 0xffffu);
+  r.z = (int)nbytes;
+  r.w = 0x00020000;
+  return r;
+}
 
 struct Epi {
   int kind;  // 0: strided store (+bias, scale); 1: weight deltas (+bias row); 2: conv input-delta rows
@@ -229,12 +257,19 @@ struct Loader {
   static constexpr int NR = CONV_R ? NC : 1;
 
   Vt v[PF][NT][NC];  // PF register stages of fetched chunks
+  // kinds with a ones row (the bias sums of a parameter-delta product): the chunk holds
+  // that row, whose first element is written as 1.0 when the chunk is stored to LDS (a
+  // select on the loaded value at fetch time would wait for the load right there)
+  static constexpr bool ONES = (KIND == LD_STR_MN4 || KIND == LD_STR_MN_S || KIND == LD_STR_K_S ||
+                                KIND == LD_CWG_A4 || KIND == LD_CWG_A_S);
+  bool onef[ONES ? PF : 1][ONES ? NC : 1];
   FastDiv dnkw;              // divider for the phase's taps per row (conv input delta)
   int mnmax, kmax;           // extents checked by fetch (per phase for the conv input delta)
   int cmn[NC], ck[NC];       // chunk origin within the tile
   bool active;               // this thread loads a chunk (always, unless PART)
-  int64_t rowbase[NRB];      // batch offset (strided kinds) or per-chunk image base (conv rows)
+  int rowbase[NRB];          // per-chunk image base (conv rows), elements from the operand base
   int r0[NR], r1[NR], r2[NR];
+  tagi_i32x4 rs0, rs1;       // buffer resources of the operand's tensors (block-uniform)
 
   __device__ __forceinline__ void map(int tid) {
     active = !PART || tid < NCH;
@@ -272,7 +307,7 @@ struct Loader {
         if (m < o.MN) {
           const int n = m / howo, p = m - n * howo;
           const int oh = p / o.g.Wo, ow = p - oh * o.g.Wo;
-          rowbase[i] = (int64_t)n * o.g.H * o.g.W * o.g.C;
+          rowbase[i] = n * o.g.H * o.g.W * o.g.C;
           r0[i] = oh * o.g.stride - o.g.pt;
           r1[i] = ow * o.g.stride - o.g.pl;
         } else {
@@ -292,7 +327,7 @@ struct Loader {
           const int n = q / hq, rr = q - n * hq;
           const int hh = rr / ph.Wq, ww = rr - hh * ph.Wq;
           const int h = hh * o.g.stride + ph.a, w = ww * o.g.stride + ph.b;
-          rowbase[i] = (int64_t)n * o.g.Ho * o.g.Wo * o.g.Cout;
+          rowbase[i] = n * o.g.Ho * o.g.Wo * o.g.Cout;
           r0[i] = (h + o.g.pt - ph.kh0) / o.g.stride;
           r1[i] = (w + o.g.pl - ph.kw0) / o.g.stride;
         } else {
@@ -323,15 +358,18 @@ struct Loader {
         r1[i] = kidx - kh * o.g.kk;
         r2[i] = c;
       }
-    } else {
-      rowbase[0] = (z / o.zdiv) * o.sz1 + (z % o.zdiv) * o.sz2;
     }
-  }
-
-  template <bool VV>
-  __device__ __forceinline__ static float4 ldv(const float* p, int64_t off) {
-    if constexpr (VV) return *reinterpret_cast<const float4*>(p + off);
-    else return make_float4(p[off], 0.f, 0.f, 0.f);
+    if constexpr (KIND == LD_ONEHOT4 || KIND == LD_ONEHOT_S) {
+      rs0 = rs1 = tagi_i32x4{0, 0, 0, 0};  // token ids are read directly
+    } else if constexpr (CONV_R || KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
+      rs0 = make_buffer_rsrc(o.p0, o.nbytes);
+      rs1 = make_buffer_rsrc(NT == 2 ? o.p1 : o.p0, o.nbytes);
+    } else {
+      // strided kinds: the batch offset goes into the resources' base
+      const int64_t zb = (z / o.zdiv) * o.sz1 + (z % o.zdiv) * o.sz2;
+      rs0 = make_buffer_rsrc(o.p0 + zb, o.nbytes);
+      rs1 = make_buffer_rsrc((NT == 2 ? o.p1 : o.p0) + zb, o.nbytes);
+    }
   }
 
   // Gather of one k tile: each chunk's reduction index is decoded with exact
@@ -358,42 +396,44 @@ struct Loader {
         continue;
       }
       bool ok = false, one = false;
-      int64_t off = 0;
+      // element offset from the resource base (< 2^29 when ok, checked on the host); formed
+      // in unsigned arithmetic because chunks that are not ok may compute anything
+      uint32_t off = 0;
+      using U = uint32_t;
       if constexpr (KIND == LD_STR_MN4 || KIND == LD_STR_MN_S || KIND == LD_STR_K_S) {
         ok = k < o.K && mn < o.MN;
         one = k < o.K && mn == o.ones_row;
-        if constexpr (KIND == LD_STR_MN4) off = rowbase[0] + mn + (int64_t)k * o.s_k;
-        else off = rowbase[0] + (int64_t)mn * o.s_mn + (int64_t)k * o.s_k;
+        if constexpr (KIND == LD_STR_MN4) off = U(mn) + U(k) * U(o.s_k);
+        else off = U(mn) * U(o.s_mn) + U(k) * U(o.s_k);
       } else if constexpr (KIND == LD_STR_K4) {
         ok = mn < o.MN && k < o.K;
-        off = rowbase[0] + (int64_t)mn * o.s_mn + k;
+        off = U(mn) * U(o.s_mn) + U(k);
       } else if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
         // k = (kh*kk + kw)*C + c
         const int kidx = fdiv(k, o.g.dC), c = k - kidx * o.g.C;
         const int kh = fdiv(kidx, o.g.dkk), kw = kidx - kh * o.g.kk;
         const int ih = r0[i] + kh, iw = r1[i] + kw;
         ok = k < o.K && ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W;
-        // in-image offset fits int32 (checked on the host)
-        off = rowbase[i] + ((ih * o.g.W + iw) * o.g.C + c);
+        off = U(rowbase[i]) + (U(ih) * U(o.g.W) + U(iw)) * U(o.g.C) + U(c);
       } else if constexpr (KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
         // k = kidx*C + c; weight row (c, kh, kw)
         const int kidx = fdiv(k, o.g.dC), c = k - kidx * o.g.C;
         ok = k < o.K && mn < o.MN;
-        off = (c * (o.g.kk * o.g.kk) + kidx) * o.g.Cout + mn;
+        off = (U(c) * U(o.g.kk * o.g.kk) + U(kidx)) * U(o.g.Cout) + U(mn);
       } else if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S) {
         // k = (ikh*nkw + ikw)*Cout + co over the phase's taps
         const int kidx = fdiv(k, o.g.dCout), co = k - kidx * o.g.Cout;
         const int ikh = fdiv(kidx, dnkw), ikw = kidx - ikh * r2[i];
         const int oh = r0[i] - ikh, ow = r1[i] - ikw;
         ok = k < kmax && oh >= 0 && oh < o.g.Ho && ow >= 0 && ow < o.g.Wo;
-        off = rowbase[i] + ((oh * o.g.Wo + ow) * o.g.Cout + co);
+        off = U(rowbase[i]) + (U(oh) * U(o.g.Wo) + U(ow)) * U(o.g.Cout) + U(co);
       } else if constexpr (KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S) {
         const int kidx = fdiv(k, o.g.dCout), co = k - kidx * o.g.Cout;
         const int ikh = fdiv(kidx, dnkw), ikw = kidx - ikh * r2[i];
         const int kh = r0[i] + ikh * o.g.stride;
         const int kw = r1[i] + ikw * o.g.stride;
         ok = k < kmax && mn < mnmax;
-        off = ((kh * o.g.kk + kw) * o.g.Cout + co) * o.g.C + mn;
+        off = ((U(kh) * U(o.g.kk) + U(kw)) * U(o.g.Cout) + U(co)) * U(o.g.C) + U(mn);
       } else if constexpr (KIND == LD_CBWD_BK4) {
         // the same (kh, kw, co) as LD_CBWD_B4, read from the weights in their own layout: the
         // chunk's 4 reduction indices are 4 consecutive co of one tap
@@ -402,7 +442,7 @@ struct Loader {
         const int kh = r0[i] + ikh * o.g.stride;
         const int kw = r1[i] + ikw * o.g.stride;
         ok = k < kmax && mn < mnmax;
-        off = ((int64_t)(mn * o.g.kk + kh) * o.g.kk + kw) * o.g.Cout + co;
+        off = ((U(mn) * U(o.g.kk) + U(kh)) * U(o.g.kk) + U(kw)) * U(o.g.Cout) + U(co);
       } else if constexpr (KIND == LD_CWG_A4 || KIND == LD_CWG_A_S) {
         // k = (n*Ho + oh)*Wo + ow
         const int n = fdiv(k, o.g.dHW), pix = k - n * (o.g.Ho * o.g.Wo);
@@ -411,19 +451,21 @@ struct Loader {
         const int iw = ow * o.g.stride - o.g.pl + r1[i];
         ok = k < o.K && mn < o.MN && ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W;
         one = k < o.K && mn == o.ones_row;
-        off = (int64_t)n * (o.g.H * o.g.W * o.g.C) + ((ih * o.g.W + iw) * o.g.C + r2[i]);
+        off = U(n) * U(o.g.H * o.g.W * o.g.C) + (U(ih) * U(o.g.W) + U(iw)) * U(o.g.C) + U(r2[i]);
       }
-      const int64_t so = ok ? off : 0;
-      float4 a = ldv<V4>(o.p0, so), b = make_float4(0.f, 0.f, 0.f, 0.f);
-      if constexpr (NT == 2) b = ldv<V4>(o.p1, so);
-      a = make_float4(ok ? a.x : (one ? 1.f : 0.f), ok ? a.y : 0.f, ok ? a.z : 0.f, ok ? a.w : 0.f);
-      b = make_float4(ok ? b.x : 0.f, ok ? b.y : 0.f, ok ? b.z : 0.f, ok ? b.w : 0.f);
+      const int vo = (int)(ok ? off * 4u : kBufOutOfRange);
+      if constexpr (ONES) onef[ST][i] = one;
+      (void)one;
       if constexpr (V4) {
-        v[ST][0][i] = a;
-        if constexpr (NT == 2) v[ST][1][i] = b;
+        const tagi_f32x4 a = tagi_raw_buffer_load_f32x4(rs0, vo, 0, 0);
+        v[ST][0][i] = make_float4(a.x, a.y, a.z, a.w);
+        if constexpr (NT == 2) {
+          const tagi_f32x4 b = tagi_raw_buffer_load_f32x4(rs1, vo, 0, 0);
+          v[ST][1][i] = make_float4(b.x, b.y, b.z, b.w);
+        }
       } else {
-        v[ST][0][i] = a.x;
-        if constexpr (NT == 2) v[ST][1][i] = b.x;
+        v[ST][0][i] = tagi_raw_buffer_load_f32(rs0, vo, 0, 0);
+        if constexpr (NT == 2) v[ST][1][i] = tagi_raw_buffer_load_f32(rs1, vo, 0, 0);
       }
     }
   }
@@ -438,7 +480,14 @@ struct Loader {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         float* st = s + t * TILE;
-        const Vt x = v[ST][t][i];
+        Vt x = v[ST][t][i];
+        if constexpr (ONES) {
+          // ones-row chunks are out of range (loaded as zeros): their first element is 1
+          if (t == 0 && onef[ST][i]) {
+            if constexpr (V4) x.x = 1.f;
+            else x = 1.f;
+          }
+        }
         if constexpr (!V4) {
           st[ck[i] * LD + cmn[i]] = x;
         } else if constexpr (MNF) {
@@ -1255,6 +1304,11 @@ void launch_cfg(const GemmArgs& g, int64_t grid_x, int64_t grid_y, hipStream_t s
 template <int PROD, int KA, int KB>
 static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, int64_t ws_bytes, hipStream_t s,
                            const char* what, int64_t grid_x_override = 0) {
+  // operand byte offsets are 32-bit with the out-of-range sentinel above them
+  TAGI_REQUIRE(g.a.nbytes >= 0 && g.a.nbytes < (int64_t)kBufOutOfRange && g.b.nbytes >= 0 &&
+                   g.b.nbytes < (int64_t)kBufOutOfRange,
+               "%s: an operand spans %lld / %lld bytes; at most 2 GiB per operand", what, (long long)g.a.nbytes,
+               (long long)g.b.nbytes);
   g.tiles_m = p.tiles_m;
   g.tiles_n = p.tiles_n;
   g.splits = p.splits;
@@ -1303,6 +1357,8 @@ static inline Operand strided_operand(const float* p0, const float* p1, int64_t 
   o.MN = (int)MN;
   o.K = (int)K;
   o.ones_row = -1;
+  // reach of one batch entry (strides are non-negative)
+  o.nbytes = (MN > 0 && K > 0) ? 4 * ((MN - 1) * s_mn + (K - 1) * s_k + 1) : 0;
   return o;
 }
 
