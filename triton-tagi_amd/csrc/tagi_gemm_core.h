@@ -287,7 +287,9 @@ struct Loader {
   }
 
   // per-block / per-thread invariants
-  __device__ __forceinline__ void init(const Operand& o, int z, int mn0, int tid) {
+  // klim: end of the block's stretch of the reduction (its split-K chunk); tiles past it
+  // read as zeros
+  __device__ __forceinline__ void init(const Operand& o, int z, int mn0, int tid, int klim) {
     map(tid);
     mnmax = o.MN;
     kmax = o.K;
@@ -298,6 +300,7 @@ struct Loader {
       dnkw = make_fastdiv(ph.nkw > 0 ? ph.nkw : 1);
       if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S) mnmax = o.g.N * ph.Hq * ph.Wq;
     }
+    kmax = min(kmax, klim);
     if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
       // rows are output pixels: base of image n and the top-left input corner
       const int howo = o.g.Ho * o.g.Wo;
@@ -386,7 +389,7 @@ struct Loader {
       if constexpr (KIND == LD_ONEHOT4 || KIND == LD_ONEHOT_S) {
         // row r of the chunk is 1.0 when token k's category is mn + r (a valid, unpadded one)
         int r = -1;
-        if (k < o.K) {
+        if (k < kmax) {
           const int64_t cat = (int64_t)o.p0[k];
           if (cat >= 0 && cat < o.MN && cat != o.pad) r = (int)(cat - mn);
         }
@@ -401,24 +404,24 @@ struct Loader {
       uint32_t off = 0;
       using U = uint32_t;
       if constexpr (KIND == LD_STR_MN4 || KIND == LD_STR_MN_S || KIND == LD_STR_K_S) {
-        ok = k < o.K && mn < o.MN;
-        one = k < o.K && mn == o.ones_row;
+        ok = k < kmax && mn < o.MN;
+        one = k < kmax && mn == o.ones_row;
         if constexpr (KIND == LD_STR_MN4) off = U(mn) + U(k) * U(o.s_k);
         else off = U(mn) * U(o.s_mn) + U(k) * U(o.s_k);
       } else if constexpr (KIND == LD_STR_K4) {
-        ok = mn < o.MN && k < o.K;
+        ok = mn < o.MN && k < kmax;
         off = U(mn) * U(o.s_mn) + U(k);
       } else if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
         // k = (kh*kk + kw)*C + c
         const int kidx = fdiv(k, o.g.dC), c = k - kidx * o.g.C;
         const int kh = fdiv(kidx, o.g.dkk), kw = kidx - kh * o.g.kk;
         const int ih = r0[i] + kh, iw = r1[i] + kw;
-        ok = k < o.K && ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W;
+        ok = k < kmax && ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W;
         off = U(rowbase[i]) + (U(ih) * U(o.g.W) + U(iw)) * U(o.g.C) + U(c);
       } else if constexpr (KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
         // k = kidx*C + c; weight row (c, kh, kw)
         const int kidx = fdiv(k, o.g.dC), c = k - kidx * o.g.C;
-        ok = k < o.K && mn < o.MN;
+        ok = k < kmax && mn < o.MN;
         off = (U(c) * U(o.g.kk * o.g.kk) + U(kidx)) * U(o.g.Cout) + U(mn);
       } else if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S) {
         // k = (ikh*nkw + ikw)*Cout + co over the phase's taps
@@ -449,8 +452,8 @@ struct Loader {
         const int oh = fdiv(pix, o.g.dWo), ow = pix - oh * o.g.Wo;
         const int ih = oh * o.g.stride - o.g.pt + r0[i];
         const int iw = ow * o.g.stride - o.g.pl + r1[i];
-        ok = k < o.K && mn < o.MN && ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W;
-        one = k < o.K && mn == o.ones_row;
+        ok = k < kmax && mn < o.MN && ih >= 0 && ih < o.g.H && iw >= 0 && iw < o.g.W;
+        one = k < kmax && mn == o.ones_row;
         off = U(n) * U(o.g.H * o.g.W * o.g.C) + (U(ih) * U(o.g.W) + U(iw)) * U(o.g.C) + U(r2[i]);
       }
       const int vo = (int)(ok ? off * 4u : kBufOutOfRange);
@@ -693,8 +696,8 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
 
   LA la;
   LB lb;
-  la.init(g.a, z, m0, tid);
-  lb.init(g.b, z, n0, tid);
+  la.init(g.a, z, m0, tid, kend);
+  lb.init(g.b, z, n0, tid, kend);
 
   floatx16 accM[TM][TN], accV[TM][TN];
 #pragma unroll
@@ -710,20 +713,23 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   const int nk = kbeg < kend ? (kend - kbeg + BK - 1) / BK : 0;
   // a split past this phase's reduction contributes nothing; the reduction skips it
   if (g.phased && g.partial && nk == 0) return;
+  // The k-loop below runs a whole number of its periods and issues every fetch and LDS
+  // store without a condition: tiles past the block's reduction (the padding tile of an
+  // odd count, the prefetches past the end) read as zeros and add nothing. With no
+  // conditional loads, the compiler can count the loads still in flight exactly and waits
+  // only for the stage it stores, keeping the next tiles' loads in flight.
   if (nk > 0) {
     la.fetch(g.a, z, m0, kbeg);
     lb.fetch(g.b, z, n0, kbeg);
     la.store(smem);
     lb.store(smem + SA);
-  }
-  // tiles 1 .. PF-1 go to register stages 1 .. PF-1
-  static_for<1, PF>([&](auto U) {
-    constexpr int u = decltype(U)::value;
-    if (u < nk) {
+    // tiles 1 .. PF-1 go to register stages 1 .. PF-1
+    static_for<1, PF>([&](auto U) {
+      constexpr int u = decltype(U)::value;
       la.template fetch<u>(g.a, z, m0, kbeg + u * BK);
       lb.template fetch<u>(g.b, z, n0, kbeg + u * BK);
-    }
-  });
+    });
+  }
   __syncthreads();
 
   // one k-tile of MFMAs on LDS buffer sA
@@ -864,19 +870,13 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
     static_for<0, PERIOD>([&](auto U) {
       constexpr int u = decltype(U)::value;
       const int t = kt + u;
-      if (t < nk) {
-        if (t + PF < nk) {
-          la.template fetch<u % PF>(g.a, z, m0, kbeg + (t + PF) * BK);
-          lb.template fetch<u % PF>(g.b, z, n0, kbeg + (t + PF) * BK);
-        }
-        compute_tile(smem + (u & 1) * (SA + SB));
-        if (t + 1 < nk) {
-          float* nA = smem + ((u + 1) & 1) * (SA + SB);
-          la.template store<(u + 1) % PF>(nA);
-          lb.template store<(u + 1) % PF>(nA + SA);
-        }
-        __syncthreads();
-      }
+      la.template fetch<u % PF>(g.a, z, m0, kbeg + (t + PF) * BK);
+      lb.template fetch<u % PF>(g.b, z, n0, kbeg + (t + PF) * BK);
+      compute_tile(smem + (u & 1) * (SA + SB));
+      float* nA = smem + ((u + 1) & 1) * (SA + SB);
+      la.template store<(u + 1) % PF>(nA);
+      lb.template store<(u + 1) % PF>(nA + SA);
+      __syncthreads();
     });
   }
 
