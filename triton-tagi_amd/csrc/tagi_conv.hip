@@ -151,6 +151,9 @@ static int conv_fwd_impl(const char* what, const float* ma, const float* Sa, con
   a.Kred = (int)K;
   const bool va = g->C % 4 == 0 && al16(ma) && al16(Sa);
   const bool vb = g->Cout % 4 == 0 && al16(mw) && al16(Sw);
+  // 16 channels per k tile and at most 25 taps: the tile-aligned loaders
+  if (va && vb && g->C % 16 == 0 && g->k <= 5)
+    return run_gemm<PROD_FWD, LD_CFWD_A4T, LD_CFWD_B4T>(a, 1, p, ws, ws_bytes, s, what);
   if (va && vb) return run_gemm<PROD_FWD, LD_CFWD_A4, LD_CFWD_B4>(a, 1, p, ws, ws_bytes, s, what);
   if (vb) return run_gemm<PROD_FWD, LD_CFWD_A_S, LD_CFWD_B4>(a, 1, p, ws, ws_bytes, s, what);
   return run_gemm<PROD_FWD, LD_CFWD_A_S, LD_CFWD_B_S>(a, 1, p, ws, ws_bytes, s, what);
@@ -302,6 +305,8 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
   const int64_t gx = (int64_t)p.tiles_m * p.tiles_n;  // phase 0 is the largest
   const bool va = g->Cout % 4 == 0 && al16(dmz) && al16(dSz);
   const bool vb = g->C % 4 == 0;
+  if (va && in_place && g->Cout % 16 == 0 && g->k <= 5)
+    return run_gemm<PROD_SHARED_B, LD_CBWD_A4T, LD_CBWD_BK4T>(a, nph, p, part, part_bytes, s, what, gx);
   if (va && in_place) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4>(a, nph, p, part, part_bytes, s, what, gx);
   if (va && vb) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B4>(a, nph, p, part, part_bytes, s, what, gx);
   if (va) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B_S>(a, nph, p, part, part_bytes, s, what, gx);
@@ -360,6 +365,10 @@ extern "C" int tagi_conv2d_wgrad(const float* ma, const float* dmz, const float*
   p.tiles_m = (int)cdiv(a.R, kCfg[p.cfg].BM);
   const bool va = g->C % 4 == 0 && al16(ma);
   const bool vb = g->Cout % 4 == 0 && al16(dmz) && al16(dSz);
+  // every 16-pixel run of the reduction inside one image, in whole rows or within one row
+  const int64_t howo = g->Ho * g->Wo;
+  if (va && vb && howo % 16 == 0 && (g->Wo % 16 == 0 || 16 % g->Wo == 0))
+    return run_gemm<PROD_SHARED_A, LD_CWG_A4T, LD_STR_MN4>(a, 1, p, ws, ws_bytes, s, what);
   if (va && vb) return run_gemm<PROD_SHARED_A, LD_CWG_A4, LD_STR_MN4>(a, 1, p, ws, ws_bytes, s, what);
   if (vb) return run_gemm<PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN4>(a, 1, p, ws, ws_bytes, s, what);
   return run_gemm<PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN_S>(a, 1, p, ws, ws_bytes, s, what);

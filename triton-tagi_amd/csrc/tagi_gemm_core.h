@@ -10,8 +10,9 @@
 //
 // Matrix core: v_mfma_f32_32x32x2f32 (64 lanes; lane l supplies A[l%32][l/32] and
 // B[l/32][l%32]; accumulator register v of lane l is D[8(v/4)+4(l/32)+v%4][l%32]).
-// LDS tiles are reduction-major ([k][row], [k][col]) and double-buffered: the global loads
-// of k-tile t+1 are in flight while the MFMAs consume tile t, one barrier per k-tile.
+// LDS tiles are double-buffered and the global loads run two k-tiles ahead: while the
+// MFMAs consume tile t, tile t+2 is in flight and tile t+1 is stored to the other LDS
+// buffer; one barrier per k-tile.
 //
 // Operand loaders read the caller's tensors in place -- strided views (Linear, attention
 // heads, transposes) or the NHWC convolution index maps (patches, transposed patches,
@@ -53,6 +54,18 @@ enum {
   LD_ONEHOT4 = 15,    // embedding deltas: mn = category, k = token; 1.0 where token k (a float
                       //   id, cast toward zero) is category mn, else 0; four categories per chunk
   LD_ONEHOT_S = 16,   //   one category per chunk
+  // Tile-aligned conv kinds: the same index maps as LD_CFWD_A4 / LD_CFWD_B4 / LD_CBWD_A4 /
+  // LD_CBWD_BK4 / LD_CWG_A4 for geometries where a 16-wide k tile never straddles a kernel
+  // tap (C % 16 == 0, or Cout % 16 == 0 for the input delta) or an image (the weight
+  // delta: Ho*Wo % 16 == 0 and Wo a multiple or a divisor of 16). The tile's tap (or
+  // image and output position) is then the same for every lane, so it is decoded once in
+  // scalar registers and each lane adds a constant formed at block start; a lane's
+  // padding test is one bit of a per-lane mask over the taps (kk <= 5).
+  LD_CFWD_A4T = 17,
+  LD_CFWD_B4T = 18,
+  LD_CBWD_A4T = 19,
+  LD_CBWD_BK4T = 20,
+  LD_CWG_A4T = 21,
 };
 
 template <int KIND>
@@ -60,10 +73,11 @@ struct KindTraits {
   static constexpr bool mn_fast = (KIND == LD_STR_MN4 || KIND == LD_STR_MN_S || KIND == LD_CFWD_B4 ||
                                    KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CWG_A4 ||
                                    KIND == LD_CWG_A_S || KIND == LD_CFWD_B_S || KIND == LD_ONEHOT4 ||
-                                   KIND == LD_ONEHOT_S);
+                                   KIND == LD_ONEHOT_S || KIND == LD_CFWD_B4T || KIND == LD_CWG_A4T);
   static constexpr bool vec4 = (KIND == LD_STR_MN4 || KIND == LD_STR_K4 || KIND == LD_CFWD_A4 || KIND == LD_CFWD_B4 ||
                                 KIND == LD_CBWD_A4 || KIND == LD_CBWD_B4 || KIND == LD_CWG_A4 || KIND == LD_CBWD_BK4 ||
-                                KIND == LD_ONEHOT4);
+                                KIND == LD_ONEHOT4 || KIND >= LD_CFWD_A4T);
+  static constexpr bool tiled = KIND >= LD_CFWD_A4T;
 };
 
 // Exact division by an invariant d >= 1 for dividends 0 <= n < 2^31 (Granlund and
@@ -261,7 +275,8 @@ struct Loader {
   // that row, whose first element is written as 1.0 when the chunk is stored to LDS (a
   // select on the loaded value at fetch time would wait for the load right there)
   static constexpr bool ONES = (KIND == LD_STR_MN4 || KIND == LD_STR_MN_S || KIND == LD_STR_K_S ||
-                                KIND == LD_CWG_A4 || KIND == LD_CWG_A_S);
+                                KIND == LD_CWG_A4 || KIND == LD_CWG_A_S || KIND == LD_CWG_A4T);
+  static constexpr bool TILED = KindTraits<KIND>::tiled;
   bool onef[ONES ? PF : 1][ONES ? NC : 1];
   FastDiv dnkw;              // divider for the phase's taps per row (conv input delta)
   int mnmax, kmax;           // extents checked by fetch (per phase for the conv input delta)
@@ -270,6 +285,14 @@ struct Loader {
   int rowbase[NRB];          // per-chunk image base (conv rows), elements from the operand base
   int r0[NR], r1[NR], r2[NR];
   tagi_i32x4 rs0, rs1;       // buffer resources of the operand's tensors (block-uniform)
+  // tile-aligned kinds: per-chunk byte offset of the chunk at the tile's origin (modulo
+  // 2^32; the tile's scalar part is added per fetch), tap masks, and the weight delta's
+  // input-row / input-column offsets of the chunk's pixel and kernel tap
+  uint32_t lb[TILED ? NC : 1], tapm[TILED ? NC : 1];
+  int lih[TILED ? NC : 1], liw[TILED ? NC : 1];
+  bool okl[TILED ? NC : 1], onel[TILED ? NC : 1];
+  int tkh0, tkw0, tnkw;      // input delta: the phase's first tap and taps per row
+  uint32_t oobv;             // kBufOutOfRange, held in a register
 
   __device__ __forceinline__ void map(int tid) {
     active = !PART || tid < NCH;
@@ -294,13 +317,19 @@ struct Loader {
     mnmax = o.MN;
     kmax = o.K;
     if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S || KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S ||
-                  KIND == LD_CBWD_BK4) {
+                  KIND == LD_CBWD_BK4 || KIND == LD_CBWD_A4T || KIND == LD_CBWD_BK4T) {
       const Phase ph = make_phase(o.g, z);
       kmax = ph.nkh * ph.nkw * o.g.Cout;
       dnkw = make_fastdiv(ph.nkw > 0 ? ph.nkw : 1);
-      if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S) mnmax = o.g.N * ph.Hq * ph.Wq;
+      if constexpr (KIND == LD_CBWD_A4 || KIND == LD_CBWD_A_S || KIND == LD_CBWD_A4T) mnmax = o.g.N * ph.Hq * ph.Wq;
+      tkh0 = ph.kh0;
+      tkw0 = ph.kw0;
+      tnkw = ph.nkw;
     }
     kmax = min(kmax, klim);
+    oobv = kBufOutOfRange;
+    asm volatile("" : "+v"(oobv));  // one register for every chunk's out-of-range offset
+    if constexpr (TILED) init_tiled(o, z, mn0);
     if constexpr (KIND == LD_CFWD_A4 || KIND == LD_CFWD_A_S) {
       // rows are output pixels: base of image n and the top-left input corner
       const int howo = o.g.Ho * o.g.Wo;
@@ -364,7 +393,7 @@ struct Loader {
     }
     if constexpr (KIND == LD_ONEHOT4 || KIND == LD_ONEHOT_S) {
       rs0 = rs1 = tagi_i32x4{0, 0, 0, 0};  // token ids are read directly
-    } else if constexpr (CONV_R || KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
+    } else if constexpr (CONV_R || TILED || KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
       rs0 = make_buffer_rsrc(o.p0, o.nbytes);
       rs1 = make_buffer_rsrc(NT == 2 ? o.p1 : o.p0, o.nbytes);
     } else {
@@ -375,12 +404,159 @@ struct Loader {
     }
   }
 
+  // bits j of [0, n) with lo <= j < hi (n <= 25)
+  __device__ static __forceinline__ uint32_t range_bits(int lo, int hi, int n) {
+    lo = max(lo, 0);
+    hi = min(hi, n);
+    return hi > lo ? ((1u << hi) - 1u) & ~((1u << lo) - 1u) : 0u;
+  }
+  // tap mask over (i, j) in [0, nh) x [0, nw), bit i*nw + j: row bit i and column bit j
+  __device__ static __forceinline__ uint32_t spread_bits(uint32_t hm, uint32_t wm, int nh, int nw) {
+    uint32_t m = 0;
+    for (int i = 0; i < nh; ++i)
+      if ((hm >> i) & 1u) m |= wm << (i * nw);
+    return m;
+  }
+
+  __device__ __forceinline__ void init_tiled(const Operand& o, int z, int mn0) {
+    using U = uint32_t;
+    const ConvG& g = o.g;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int mn = mn0 + cmn[i];
+      if constexpr (KIND == LD_CFWD_A4T) {
+        // row = output pixel (n, oh, ow); chunk = 4 channels at k offset ck of tap (kh, kw)
+        uint32_t base = 0, msk = 0;
+        if (mn < o.MN) {
+          const int howo = g.Ho * g.Wo;
+          const int n = mn / howo, p = mn - n * howo;
+          const int oh = p / g.Wo, ow = p - oh * g.Wo;
+          const int ih0 = oh * g.stride - g.pt, iw0 = ow * g.stride - g.pl;
+          base = ((U(n) * U(g.H) + U(ih0)) * U(g.W) + U(iw0)) * U(g.C) + U(ck[i]);
+          msk = spread_bits(range_bits(-ih0, g.H - ih0, g.kk), range_bits(-iw0, g.W - iw0, g.kk), g.kk, g.kk);
+        }
+        lb[i] = base * 4u;
+        tapm[i] = msk;
+      } else if constexpr (KIND == LD_CFWD_B4T) {
+        // weights w[(c*kk2 + kidx)*Cout + co]: chunk = 4 co at reduction offset ck (channel c0 + ck)
+        lb[i] = (U(ck[i]) * U(g.kk * g.kk) * U(g.Cout) + U(mn)) * 4u;
+        okl[i] = mn < o.MN;
+      } else if constexpr (KIND == LD_CBWD_A4T) {
+        // row = input pixel of stride phase z; (r0, r1) = output pixel of tap (kh0, kw0)
+        const Phase ph = make_phase(g, z);
+        const int hq = ph.Hq * ph.Wq;
+        uint32_t base = 0, msk = 0;
+        if (mn < mnmax && hq > 0) {
+          const int n = mn / hq, rr = mn - n * hq;
+          const int hh = rr / ph.Wq, ww = rr - hh * ph.Wq;
+          const int h = hh * g.stride + ph.a, w = ww * g.stride + ph.b;
+          const int r0 = (h + g.pt - ph.kh0) / g.stride, r1 = (w + g.pl - ph.kw0) / g.stride;
+          base = ((U(n) * U(g.Ho) + U(r0)) * U(g.Wo) + U(r1)) * U(g.Cout) + U(ck[i]);
+          // output row r0 - ikh in [0, Ho) and column r1 - ikw in [0, Wo)
+          msk = spread_bits(range_bits(r0 - g.Ho + 1, r0 + 1, ph.nkh), range_bits(r1 - g.Wo + 1, r1 + 1, ph.nkw),
+                            ph.nkh, ph.nkw);
+        }
+        lb[i] = base * 4u;
+        tapm[i] = msk;
+      } else if constexpr (KIND == LD_CBWD_BK4T) {
+        // weights w[((c*kk + kh)*kk + kw)*Cout + co] in place: row c, chunk = 4 co at offset ck
+        lb[i] = (U(mn) * U(g.kk * g.kk) * U(g.Cout) + U(ck[i])) * 4u;
+        okl[i] = mn < mnmax;
+      } else if constexpr (KIND == LD_CWG_A4T) {
+        // row = weight row (kh, kw, c) (+ the ones row); the chunk's pixel is at offset ck
+        // of a 16-pixel run inside one image, (dh, dw) rows/columns past the run's start
+        const int kidx = mn / g.C, c = mn - kidx * g.C;
+        const int kh = kidx / g.kk, kw = kidx - kh * g.kk;
+        const int dh = g.Wo >= 16 ? 0 : ck[i] / g.Wo, dw = ck[i] - dh * g.Wo;
+        int ih = dh * g.stride - g.pt + kh;
+        const int iw = dw * g.stride - g.pl + kw;
+        if (mn >= o.MN) ih = -(1 << 28);  // past the weight rows: reads zeros
+        lih[i] = ih;
+        liw[i] = iw;
+        lb[i] = ((U(ih) * U(g.W) + U(iw)) * U(g.C) + U(c)) * 4u;
+        onel[i] = mn == o.ones_row;
+      }
+    }
+  }
+
+  template <int ST>
+  __device__ __forceinline__ void load_chunk(int i, uint32_t vo) {
+    if constexpr (V4) {
+      const tagi_f32x4 a = tagi_raw_buffer_load_f32x4(rs0, (int)vo, 0, 0);
+      v[ST][0][i] = make_float4(a.x, a.y, a.z, a.w);
+      if constexpr (NT == 2) {
+        const tagi_f32x4 b = tagi_raw_buffer_load_f32x4(rs1, (int)vo, 0, 0);
+        v[ST][1][i] = make_float4(b.x, b.y, b.z, b.w);
+      }
+    } else {
+      v[ST][0][i] = tagi_raw_buffer_load_f32(rs0, (int)vo, 0, 0);
+      if constexpr (NT == 2) v[ST][1][i] = tagi_raw_buffer_load_f32(rs1, (int)vo, 0, 0);
+    }
+  }
+
+  // Tile-aligned kinds: the tile's tap / pixel run is decoded in scalar registers
+  // (k0 is the same for every lane), then one add and a mask bit per chunk.
+  template <int ST>
+  __device__ __forceinline__ void fetch_tiled(const Operand& o, int k0) {
+    using U = uint32_t;
+    const ConvG& g = o.g;
+    const bool kin = k0 < kmax;  // whole tile in range (the reduction length is a multiple of 16)
+    if constexpr (KIND == LD_CFWD_A4T || KIND == LD_CFWD_B4T) {
+      const int kidx = fdiv(k0, g.dC), c0 = k0 - kidx * g.C;
+      if constexpr (KIND == LD_CFWD_A4T) {
+        const int kh = fdiv(kidx, g.dkk), kw = kidx - kh * g.kk;
+        const uint32_t s4 = ((U(kh) * U(g.W) + U(kw)) * U(g.C) + U(c0)) * 4u;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+          const bool ok = kin && ((tapm[i] >> (kidx & 31)) & 1u);
+          load_chunk<ST>(i, ok ? lb[i] + s4 : oobv);
+        }
+      } else {
+        const uint32_t s4 = (U(c0) * U(g.kk * g.kk) + U(kidx)) * U(g.Cout) * 4u;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) load_chunk<ST>(i, (kin && okl[i]) ? lb[i] + s4 : oobv);
+      }
+    } else if constexpr (KIND == LD_CBWD_A4T || KIND == LD_CBWD_BK4T) {
+      const int kidx = fdiv(k0, g.dCout), co0 = k0 - kidx * g.Cout;
+      const int ikh = fdiv(kidx, dnkw), ikw = kidx - ikh * tnkw;
+      if constexpr (KIND == LD_CBWD_A4T) {
+        const uint32_t s4 = ((U(ikh) * U(g.Wo) + U(ikw)) * U(g.Cout) - U(co0)) * 4u;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+          const bool ok = kin && ((tapm[i] >> (kidx & 31)) & 1u);
+          load_chunk<ST>(i, ok ? lb[i] - s4 : oobv);
+        }
+      } else {
+        const int kh = tkh0 + ikh * g.stride, kw = tkw0 + ikw * g.stride;
+        const uint32_t s4 = ((U(kh) * U(g.kk) + U(kw)) * U(g.Cout) + U(co0)) * 4u;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) load_chunk<ST>(i, (kin && okl[i]) ? lb[i] + s4 : oobv);
+      }
+    } else if constexpr (KIND == LD_CWG_A4T) {
+      const int n = fdiv(k0, g.dHW), p0 = k0 - n * (g.Ho * g.Wo);
+      const int oh0 = fdiv(p0, g.dWo), ow0 = p0 - oh0 * g.Wo;
+      const int sih = oh0 * g.stride, siw = ow0 * g.stride;
+      const uint32_t s4 = ((U(n) * U(g.H) + U(sih)) * U(g.W) + U(siw)) * U(g.C) * 4u;
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int ih = sih + lih[i], iw = siw + liw[i];
+        const bool ok = kin && U(ih) < U(g.H) && U(iw) < U(g.W);
+        onef[ST][i] = kin && onel[i];
+        load_chunk<ST>(i, ok ? lb[i] + s4 : oobv);
+      }
+    }
+  }
+
   // Gather of one k tile: each chunk's reduction index is decoded with exact
   // multiply-high divisions; chunks outside the operand or in the zero padding read as 0.
   template <int ST = 0>
   __device__ __forceinline__ void fetch(const Operand& o, int z, int mn0, int k0) {
     if constexpr (PART) {
       if (!active) return;
+    }
+    if constexpr (TILED) {
+      fetch_tiled<ST>(o, k0);
+      return;
     }
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
@@ -456,20 +632,9 @@ struct Loader {
         one = k < kmax && mn == o.ones_row;
         off = U(n) * U(o.g.H * o.g.W * o.g.C) + (U(ih) * U(o.g.W) + U(iw)) * U(o.g.C) + U(r2[i]);
       }
-      const int vo = (int)(ok ? off * 4u : kBufOutOfRange);
       if constexpr (ONES) onef[ST][i] = one;
       (void)one;
-      if constexpr (V4) {
-        const tagi_f32x4 a = tagi_raw_buffer_load_f32x4(rs0, vo, 0, 0);
-        v[ST][0][i] = make_float4(a.x, a.y, a.z, a.w);
-        if constexpr (NT == 2) {
-          const tagi_f32x4 b = tagi_raw_buffer_load_f32x4(rs1, vo, 0, 0);
-          v[ST][1][i] = make_float4(b.x, b.y, b.z, b.w);
-        }
-      } else {
-        v[ST][0][i] = tagi_raw_buffer_load_f32(rs0, vo, 0, 0);
-        if constexpr (NT == 2) v[ST][1][i] = tagi_raw_buffer_load_f32(rs1, vo, 0, 0);
-      }
+      load_chunk<ST>(i, ok ? off * 4u : oobv);
     }
   }
 
@@ -480,23 +645,25 @@ struct Loader {
     }
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
+      Vt x[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) x[t] = v[ST][t][i];
+      if constexpr (ONES) {
+        // ones-row chunks are out of range (loaded as zeros): their first element is 1
+        if (onef[ST][i]) {
+          if constexpr (V4) x[0].x = 1.f;
+          else x[0] = 1.f;
+        }
+      }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         float* st = s + t * TILE;
-        Vt x = v[ST][t][i];
-        if constexpr (ONES) {
-          // ones-row chunks are out of range (loaded as zeros): their first element is 1
-          if (t == 0 && onef[ST][i]) {
-            if constexpr (V4) x.x = 1.f;
-            else x = 1.f;
-          }
-        }
         if constexpr (!V4) {
-          st[ck[i] * LD + cmn[i]] = x;
+          st[ck[i] * LD + cmn[i]] = x[t];
         } else if constexpr (MNF) {
-          *reinterpret_cast<float4*>(st + ck[i] * LD + cmn[i]) = x;
+          *reinterpret_cast<float4*>(st + ck[i] * LD + cmn[i]) = x[t];
         } else {
-          *reinterpret_cast<float4*>(st + kmaj_off(cmn[i], ck[i])) = x;
+          *reinterpret_cast<float4*>(st + kmaj_off(cmn[i], ck[i])) = x[t];
         }
       }
     }
@@ -626,7 +793,11 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   // register stages of operand prefetch: k-tiles are fetched two tiles ahead, except in
   // the forward product's 8-wave tiles, where a second stage would cost the tile its
   // second resident block per CU
-  constexpr int PF = (PROD != PROD_FWD || NTH <= 256) ? 2 : 1;
+  // register stages of operand prefetch: k-tile t+2 is fetched while tile t is consumed,
+  // and tile t+1 (fetched one step earlier) is stored to the other LDS buffer halfway
+  // through tile t's MFMAs, so the LDS stores overlap the matrix work instead of
+  // bunching up before the barrier
+  constexpr int PF = 2;
   using LA = Loader<KA, NA, BM, BK, NTH, PF>;
   using LB = Loader<KB, NB, BN, BK, NTH, PF>;
   constexpr int LDA = LA::LD, LDB = LB::LD;
@@ -733,7 +904,7 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   __syncthreads();
 
   // one k-tile of MFMAs on LDS buffer sA
-  auto compute_tile = [&](const float* sA) {
+  auto compute_tile = [&](const float* sA, auto&& mid) {
     const float* sB = sA + SA;
     {
       // MFMA k-step s takes reduction indices s (lanes 0-31) and NS + s (lanes 32-63) of
@@ -743,23 +914,24 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
       // barriers keep the compiler from sinking the reads next to their use).
       constexpr int NS = BK / 2;
       constexpr int PD = 2;
-      float fa0[NS][TM], fa1[NS][TM], fb0[NS][TN], fb1[NS][TN];
+      // fa[t] / fb[t]: fragments of the operand's tensor t (mean, then variance)
+      float fa[NA][NS][TM], fb[NB][NS][TN];
       auto load = [&](int s) {
         const int kr = hl * NS + s;
         if constexpr (!LA::KMAJ) {
 #pragma unroll
           for (int i = 0; i < TM; ++i) {
             const int c = kr * LDA + wm * WM + i * 32 + rl;
-            fa0[s][i] = sA[c];
-            if constexpr (NA == 2) fa1[s][i] = sA[LA::TILE + c];
+#pragma unroll
+            for (int t = 0; t < NA; ++t) fa[t][s][i] = sA[t * LA::TILE + c];
           }
         }
         if constexpr (!LB::KMAJ) {
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
             const int c = kr * LDB + wn * WN + j * 32 + rl;
-            fb0[s][j] = sB[c];
-            if constexpr (NB == 2) fb1[s][j] = sB[LB::TILE + c];
+#pragma unroll
+            for (int t = 0; t < NB; ++t) fb[t][s][j] = sB[t * LB::TILE + c];
           }
         }
       };
@@ -770,17 +942,13 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const int o = LA::kmaj_off(row, hl * NS + 4 * h);
-            const float4 x = *reinterpret_cast<const float4*>(sA + o);
-            fa0[4 * h + 0][i] = x.x;
-            fa0[4 * h + 1][i] = x.y;
-            fa0[4 * h + 2][i] = x.z;
-            fa0[4 * h + 3][i] = x.w;
-            if constexpr (NA == 2) {
-              const float4 y = *reinterpret_cast<const float4*>(sA + LA::TILE + o);
-              fa1[4 * h + 0][i] = y.x;
-              fa1[4 * h + 1][i] = y.y;
-              fa1[4 * h + 2][i] = y.z;
-              fa1[4 * h + 3][i] = y.w;
+#pragma unroll
+            for (int t = 0; t < NA; ++t) {
+              const float4 x = *reinterpret_cast<const float4*>(sA + t * LA::TILE + o);
+              fa[t][4 * h + 0][i] = x.x;
+              fa[t][4 * h + 1][i] = x.y;
+              fa[t][4 * h + 2][i] = x.z;
+              fa[t][4 * h + 3][i] = x.w;
             }
           }
         }
@@ -792,27 +960,23 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const int o = LB::kmaj_off(row, hl * NS + 4 * h);
-            const float4 x = *reinterpret_cast<const float4*>(sB + o);
-            fb0[4 * h + 0][j] = x.x;
-            fb0[4 * h + 1][j] = x.y;
-            fb0[4 * h + 2][j] = x.z;
-            fb0[4 * h + 3][j] = x.w;
-            if constexpr (NB == 2) {
-              const float4 y = *reinterpret_cast<const float4*>(sB + LB::TILE + o);
-              fb1[4 * h + 0][j] = y.x;
-              fb1[4 * h + 1][j] = y.y;
-              fb1[4 * h + 2][j] = y.z;
-              fb1[4 * h + 3][j] = y.w;
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+              const float4 x = *reinterpret_cast<const float4*>(sB + t * LB::TILE + o);
+              fb[t][4 * h + 0][j] = x.x;
+              fb[t][4 * h + 1][j] = x.y;
+              fb[t][4 * h + 2][j] = x.z;
+              fb[t][4 * h + 3][j] = x.w;
             }
           }
         }
       }
       auto mma = [&](int s) {
-        float* a0 = fa0[s];
-        float* a1 = fa1[s];
-        float* b0 = fb0[s];
-        float* b1 = fb1[s];
+        const float* a0 = fa[0][s];
+        const float* b0 = fb[0][s];
         if constexpr (PROD == PROD_FWD) {
+          const float* a1 = fa[1][s];
+          const float* b1 = fb[1][s];
           float asq[TM], bvar[TN];
 #pragma unroll
           for (int i = 0; i < TM; ++i) asq[i] = a0[i] * a0[i];
@@ -827,6 +991,7 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
               accV[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[i], bvar[j], accV[i][j], 0, 0, 0);
             }
         } else if constexpr (PROD == PROD_SHARED_B) {
+          const float* a1 = fa[1][s];
           float bsq[TN];
 #pragma unroll
           for (int j = 0; j < TN; ++j) bsq[j] = b0[j] * b0[j];
@@ -838,6 +1003,7 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
               accV[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[i], bsq[j], accV[i][j], 0, 0, 0);
             }
         } else {
+          const float* b1 = fb[1][s];
           float asq[TM];
 #pragma unroll
           for (int i = 0; i < TM; ++i) asq[i] = a0[i] * a0[i];
@@ -858,24 +1024,30 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
         __builtin_amdgcn_sched_barrier(0);
         mma(s);
         __builtin_amdgcn_sched_barrier(0);
+        if (s == NS / 2 - 1) {
+          mid();
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
   };
-  // Tile t is in LDS buffer t & 1 while tiles t+1 .. t+PF-1 sit in register stages
-  // (t+1) % PF ..; the stage that held tile t (stored at the end of step t-1) takes the
-  // fetch of tile t+PF. The loop runs in periods of lcm(2, PF) steps so that every
-  // buffer and stage index is a compile-time constant.
-  constexpr int PERIOD = PF % 2 == 0 ? PF : 2 * PF;
+  // Tile t is in LDS buffer t & 1 and tile t+1 in register stage (t+1) % 2. Step t
+  // fetches tile t+2 into stage t % 2 (whose tile went to LDS during step t-1), runs tile
+  // t's MFMAs and, halfway through them, stores tile t+1 to buffer (t+1) & 1, which no
+  // wave reads after the barrier that ended step t-1. The loop runs in periods of two
+  // steps so that every buffer and stage index is a compile-time constant.
+  constexpr int PERIOD = 2;
   for (int kt = 0; kt < nk; kt += PERIOD) {
     static_for<0, PERIOD>([&](auto U) {
       constexpr int u = decltype(U)::value;
       const int t = kt + u;
       la.template fetch<u % PF>(g.a, z, m0, kbeg + (t + PF) * BK);
       lb.template fetch<u % PF>(g.b, z, n0, kbeg + (t + PF) * BK);
-      compute_tile(smem + (u & 1) * (SA + SB));
       float* nA = smem + ((u + 1) & 1) * (SA + SB);
-      la.template store<(u + 1) % PF>(nA);
-      lb.template store<(u + 1) % PF>(nA + SA);
+      compute_tile(smem + (u & 1) * (SA + SB), [&] {
+        la.template store<(u + 1) % PF>(nA);
+        lb.template store<(u + 1) % PF>(nA + SA);
+      });
       __syncthreads();
     });
   }
@@ -1168,15 +1340,18 @@ struct Plan {
 // 8-wave 128x128 kernels need more than 128 VGPRs, so one block per CU). The sustained
 // fractions, the occupancy factors and the split costs were fitted to a sweep of every
 // tile shape and split count over the ResNet-18, CNN, transformer and Linear
-// microbenchmark GEMMs on MI355X (mean loss against the best measured plan 1.0%). The
-// split counts tried are the swept ones.
+// microbenchmark GEMMs on MI355X (mean loss against the best measured plan 1.0%). A
+// refit to the same sweep of the tile-aligned kernels lowers that loss to 0.9% but slows
+// the whole ResNet-18 step by 3% (its picks favour isolated launches over the two-stream
+// step), so the earlier fit is kept; the resident-block counts are the current kernels'.
+// The split counts tried are the swept ones.
 //
 // phase_k (optional, batch entries): per-GEMM reduction lengths when they differ (stride
 // phases of the conv input delta); splits past a GEMM's own length launch no work.
 static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int64_t batch, int prod, bool allow_split,
                                         int64_t max_splits, const int64_t* phase_k) {
   // [tile config][product: forward, shared B, shared A]
-  static const int kBpc[6][3] = {{1, 1, 1}, {2, 3, 3}, {2, 3, 3}, {4, 5, 5}, {8, 10, 10}, {3, 4, 4}};
+  static const int kBpc[6][3] = {{1, 1, 1}, {2, 3, 3}, {2, 3, 2}, {4, 4, 4}, {8, 10, 10}, {3, 4, 4}};
   static const double kEff[6][3] = {{0.761, 0.645, 0.492}, {0.611, 0.615, 0.319}, {0.499, 0.624, 0.628},
                                     {0.685, 0.585, 0.620}, {0.300, 0.303, 0.454}, {0.535, 0.450, 0.589}};
   static const int kWaves[] = {8, 4, 4, 4, 1, 4};
@@ -1269,18 +1444,21 @@ static inline int64_t plan_ws_bytes(const Plan& p, int64_t R, int64_t C, int64_t
 // config and product, so the kernels compile in parallel translation units); the entry
 // points' translation units see launch_cfg's declaration only.
 #define TAGI_GEMM_COMBOS_FWD(X)                                                          \
+  X(PROD_FWD, LD_CFWD_A4T, LD_CFWD_B4T)                                                  \
   X(PROD_FWD, LD_CFWD_A4, LD_CFWD_B4) X(PROD_FWD, LD_CFWD_A_S, LD_CFWD_B4)               \
   X(PROD_FWD, LD_CFWD_A_S, LD_CFWD_B_S) X(PROD_FWD, LD_STR_K4, LD_STR_MN4)               \
   X(PROD_FWD, LD_STR_K_S, LD_STR_MN_S) X(PROD_FWD, LD_STR_MN_S, LD_STR_MN_S)             \
   X(PROD_FWD, LD_STR_K4, LD_STR_K4) X(PROD_FWD, LD_STR_MN4, LD_STR_K4)                   \
   X(PROD_FWD, LD_STR_MN4, LD_STR_MN4)
 #define TAGI_GEMM_COMBOS_SHARED_B(X)                                                     \
+  X(PROD_SHARED_B, LD_CBWD_A4T, LD_CBWD_BK4T)                                            \
   X(PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B4) X(PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4)     \
   X(PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_B_S) X(PROD_SHARED_B, LD_CBWD_A_S, LD_CBWD_B_S)   \
   X(PROD_SHARED_B, LD_STR_K4, LD_STR_K4) X(PROD_SHARED_B, LD_STR_K_S, LD_STR_K_S)        \
   X(PROD_SHARED_B, LD_STR_MN_S, LD_STR_MN_S) X(PROD_SHARED_B, LD_STR_K4, LD_STR_MN4)     \
   X(PROD_SHARED_B, LD_STR_MN4, LD_STR_K4) X(PROD_SHARED_B, LD_STR_MN4, LD_STR_MN4)
 #define TAGI_GEMM_COMBOS_SHARED_A(X)                                                     \
+  X(PROD_SHARED_A, LD_CWG_A4T, LD_STR_MN4)                                               \
   X(PROD_SHARED_A, LD_CWG_A4, LD_STR_MN4) X(PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN4)       \
   X(PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN_S) X(PROD_SHARED_A, LD_ONEHOT4, LD_STR_MN4)     \
   X(PROD_SHARED_A, LD_ONEHOT_S, LD_STR_MN4) X(PROD_SHARED_A, LD_ONEHOT_S, LD_STR_MN_S)   \
