@@ -1339,12 +1339,10 @@ struct Plan {
 // Resident blocks per CU are what the built kernels' register and LDS use allow (the
 // 8-wave 128x128 kernels need more than 128 VGPRs, so one block per CU). The sustained
 // fractions, the occupancy factors and the split costs were fitted to a sweep of every
-// tile shape and split count over the ResNet-18, CNN, transformer and Linear
-// microbenchmark GEMMs on MI355X (mean loss against the best measured plan 1.0%). A
-// refit to the same sweep of the tile-aligned kernels lowers that loss to 0.9% but slows
-// the whole ResNet-18 step by 3% (its picks favour isolated launches over the two-stream
-// step), so the earlier fit is kept; the resident-block counts are the current kernels'.
-// The split counts tried are the swept ones.
+// tile shape and split count (each plan forced in turn and timed alone) over the
+// ResNet-18, CNN, transformer (including its batched attention products) and Linear
+// microbenchmark GEMMs on MI355X: mean loss against the best measured plan 1.5%. The
+// split counts tried are the swept ones.
 //
 // phase_k (optional, batch entries): per-GEMM reduction lengths when they differ (stride
 // phases of the conv input delta); splits past a GEMM's own length launch no work.
@@ -1352,12 +1350,12 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
                                         int64_t max_splits, const int64_t* phase_k) {
   // [tile config][product: forward, shared B, shared A]
   static const int kBpc[6][3] = {{1, 1, 1}, {2, 3, 3}, {2, 3, 2}, {4, 4, 4}, {8, 10, 10}, {3, 4, 4}};
-  static const double kEff[6][3] = {{0.761, 0.645, 0.492}, {0.611, 0.615, 0.319}, {0.499, 0.624, 0.628},
-                                    {0.685, 0.585, 0.620}, {0.300, 0.303, 0.454}, {0.535, 0.450, 0.589}};
+  static const double kEff[6][3] = {{0.624, 0.353, 0.483}, {0.595, 0.632, 0.608}, {0.465, 0.519, 0.492},
+                                    {0.655, 0.639, 0.687}, {0.300, 0.398, 0.442}, {0.655, 0.374, 0.427}};
   static const int kWaves[] = {8, 4, 4, 4, 1, 4};
   static const int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 20, 24, 32, 40, 48, 64, 80, 96, 128, 160, 192, 256};
-  const double kOcc2 = 0.909, kOcc1 = 0.588, kOcc0 = 0.35;
-  const double kSplitSecPerByte = 1.68e-13, kSplitLaunch = 3.33e-6;
+  const double kOcc2 = 0.924, kOcc1 = 0.667, kOcc0 = 0.35;
+  const double kSplitSecPerByte = 1.82e-13, kSplitLaunch = 5.95e-6;
   const int products = prod == PROD_FWD ? 3 : 2;
   Plan best{3, 1, (int)Kred, 1, 1};
   double best_t = DBL_MAX;
