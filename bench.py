@@ -111,7 +111,8 @@ def cpu_baseline(workload: str, batch: int, timed_steps: int = 3):
 
 def measure_ceilings(dev: str) -> dict:
     """Measured ceilings of this GPU: the fp32 MFMA issue loop at 1, 2 and 4 waves per
-    SIMD (the engine's probe kernel), a 1 GiB device-to-device copy (the HIP runtime's copy
+    SIMD (the engine's probe kernel), the same loop with 1-8 VALU or LDS instructions per
+    MFMA, a 1 GiB device-to-device copy (the HIP runtime's copy
     kernel) and an fp32 GEMM through torch.matmul (hipBLASLt) for comparison."""
     import torch
 
@@ -144,6 +145,15 @@ def measure_ceilings(dev: str) -> dict:
         s = timed(lambda: _lib.call("tagi_probe_mfma_loop", buf.data_ptr(), blocks, iters, st), 20)
         flops = blocks * 4 * iters * 4 * (32 * 32 * 2 * 2)
         out[f"mfma_fp32_loop_tflops_{w}_waves_per_simd"] = round(flops / s / 1e12, 1)
+    # the same loop with v_fma_f32 (kind 0) or LDS reads (kind 1) after every MFMA, at 2
+    # waves per SIMD: the drop shows whether the instruction issues beside the matrix core
+    for kind, name in ((0, "valu"), (1, "lds_read")):
+        res = {}
+        for per in (1, 2, 4, 8):
+            blocks = cus * 2
+            s = timed(lambda: _lib.call("tagi_probe_mfma_mix", buf.data_ptr(), blocks, iters, kind, per, st), 20)
+            res[per] = round(blocks * 4 * iters * 4 * (32 * 32 * 2 * 2) / s / 1e12, 1)
+        out[f"mfma_fp32_tflops_with_{name}_per_mfma"] = res
     n = (1 << 30) // 4
     src = torch.ones(n, device=dev)
     dst = torch.empty_like(src)

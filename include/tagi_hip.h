@@ -60,6 +60,12 @@ enum {
  * blocks*256 floats. blocks = 256*w on a 256-CU GPU gives w waves per SIMD. */
 int tagi_probe_mfma_loop(float* out, int64_t blocks, int64_t iters, tagi_stream_t stream);
 
+/* Co-issue probe (no counterpart in the reference; measurement only): the loop of
+ * tagi_probe_mfma_loop with `per_mfma` (1, 2, 4 or 8) further instructions after every
+ * MFMA, independent v_fma_f32 chains (kind 0) or LDS reads (kind 1); the drop in MFMA
+ * rate against tagi_probe_mfma_loop is what each such instruction costs the matrix core. */
+int tagi_probe_mfma_mix(float* out, int64_t blocks, int64_t iters, int kind, int per_mfma, tagi_stream_t stream);
+
 /* HBM ceiling probe (no counterpart in the reference; measurement only): mode 0 copies n
  * floats src -> dst with float4 loads and stores, mode 1 reads n floats and writes one
  * partial sum per thread (dst holds blocks*256 floats). Grid-stride over `blocks` blocks

@@ -145,6 +145,48 @@ __global__ void __launch_bounds__(256) mfma_loop_kernel(float* __restrict__ out,
     for (int v = 0; v < 16; ++v) s += acc[i][v];
   out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
+// The same loop with `V` other instructions after each MFMA: independent v_fma_f32
+// chains (KIND 0) or LDS reads (KIND 1, waited for once per round). Written as inline
+// assembly so that the compiler issues exactly V of them per MFMA. How much each costs
+// the MFMA rate tells whether that kind of instruction issues beside the matrix core.
+template <int KIND, int V>
+__global__ void __launch_bounds__(256) mfma_mix_kernel(float* __restrict__ out, int iters) {
+  __shared__ float lds[256];
+  lds[threadIdx.x] = threadIdx.x * 1e-3f;
+  __syncthreads();
+  probe_floatx16 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
+  const float x = 1.0f + threadIdx.x * 1e-6f, y = 1.0f;
+  float f[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = threadIdx.x * 1e-3f + j;
+  const float c0 = 0.999f, c1 = 0.5f;
+  float r = 0.f;
+  const unsigned addr = (unsigned)(threadIdx.x * 4);
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc[i], 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if constexpr (KIND == 0) asm volatile("v_fma_f32 %0, %0, %1, %2" : "+v"(f[v & 7]) : "v"(c0), "v"(c1));
+        else asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
+      }
+    }
+    if constexpr (KIND == 1) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+  float s = r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += f[j];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s += acc[i][v];
+  out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
 // HBM streaming probes. Each thread moves U float4 per grid-stride step with all U loads
 // issued before any store or add, so U * 16 bytes per lane are in flight.
 constexpr int kStreamU = 4;
@@ -198,6 +240,31 @@ extern "C" int tagi_probe_stream(const float* src, float* dst, int64_t n, int64_
   else
     hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
                        reinterpret_cast<const float4*>(src), dst, n / 4);
+  return check_launch(what);
+}
+
+extern "C" int tagi_probe_mfma_mix(float* out, int64_t blocks, int64_t iters, int kind, int per_mfma,
+                                   tagi_stream_t stream) {
+  const char* what = "tagi_probe_mfma_mix";
+  TAGI_REQUIRE(out != nullptr && blocks > 0 && blocks <= (1 << 20) && iters > 0 && iters < (1ll << 31),
+               "%s: bad arguments", what);
+  TAGI_REQUIRE((kind == 0 || kind == 1) && (per_mfma == 1 || per_mfma == 2 || per_mfma == 4 || per_mfma == 8),
+               "%s: kind must be 0 (VALU) or 1 (LDS) and per_mfma 1, 2, 4 or 8", what);
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)blocks), blk(256);
+#define TAGI_MIX(K, V) hipLaunchKernelGGL((mfma_mix_kernel<K, V>), grid, blk, 0, s, out, (int)iters)
+  if (kind == 0) {
+    if (per_mfma == 1) TAGI_MIX(0, 1);
+    else if (per_mfma == 2) TAGI_MIX(0, 2);
+    else if (per_mfma == 4) TAGI_MIX(0, 4);
+    else TAGI_MIX(0, 8);
+  } else {
+    if (per_mfma == 1) TAGI_MIX(1, 1);
+    else if (per_mfma == 2) TAGI_MIX(1, 2);
+    else if (per_mfma == 4) TAGI_MIX(1, 4);
+    else TAGI_MIX(1, 8);
+  }
+#undef TAGI_MIX
   return check_launch(what);
 }
 
