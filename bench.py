@@ -35,7 +35,7 @@ PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 TIMER_STEPS = 5  # timed steps (the last ones) that carry the live per-launch timer
 MFMA_FAMILIES = ("conv_fwd", "conv_bwd_delta", "conv_wgrad", "linear_fwd", "linear_bwd_delta", "linear_wgrad",
-                 "bmm_fwd", "bmm_shared")
+                 "bmm_fwd", "bmm_shared", "attn_scores")
 WORKLOAD_DESC = {
     "resnet18": "TAGI ResNet-18 (BasicBlock 64/128/256/512, BatchNorm2D, Add, AvgPool4, Linear 512-10, Remax), "
                 "batch 128, 3x32x32 ~ N(0,1), gain 0.1, sigma_v 0.05, full fwd+bwd+update step",

@@ -173,6 +173,17 @@ int tagi_bmm_shared_jacobian(const float* p0, const float* p1, const float* p2, 
                              const tagi_view* vo, float scale, float scale_sq, int shared_left,
                              tagi_stream_t stream);
 
+/* The attention scores' moments passed through the Remax in one kernel
+ * (multihead_attention.py:174-190: Q K^T by bmm_tagi_var and the scaled mean matmul, then
+ * triton_remax over each score row). q/k: (B, S, H*D) projection outputs, head h at columns
+ * h*D .. h*D+D-1, 16-byte aligned; outputs mu_a, var_a, J: (B, H, S, S) contiguous. The
+ * scores are the ones tagi_bmm_tagi forms (scale, scale_sq applied) and the outputs those
+ * of tagi_remax_fwd on them, bit for bit, but the scores never reach memory. Needs
+ * S <= 256 and D in {16, 32, 64} (else TAGI_ERR_UNSUPPORTED: use the two calls). */
+int tagi_attn_scores_remax(const float* mu_q, const float* var_q, const float* mu_k, const float* var_k,
+                           float* mu_a, float* var_a, float* J, int64_t B, int64_t H, int64_t S, int64_t D,
+                           float scale, float scale_sq, tagi_stream_t stream);
+
 /* ------------------------------------------------------------------ Conv2D ---- */
 /* 4-D activations and deltas of the conv path (Conv2D, BatchNorm2D, AvgPool2D) are
  * channels-last: element (n, c, h, w) of an (N, C, H, W) tensor sits at ((n*H + h)*W + w)*C + c

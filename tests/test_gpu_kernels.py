@@ -434,6 +434,34 @@ def test_attention_layer(dev, B, S, E, H):
                             f"{name} delta Sw")
 
 
+@pytest.mark.parametrize("B,H,S,D", [(2, 8, 256, 32), (1, 2, 40, 16), (2, 2, 100, 64), (1, 3, 1, 32)])
+def test_attention_scores_remax_fused_equals_two_calls(dev, B, H, S, D):
+    """tagi_attn_scores_remax (scores and Remax in one kernel) gives the outputs of
+    tagi_bmm_tagi followed by tagi_remax_fwd bit for bit (same product order, same row
+    math); the oracle comparison of both paths is test_attention_layer's."""
+    import math
+
+    from triton_tagi_amd import _lib
+    from triton_tagi_amd.layers.remax import remax
+
+    r = g(B * S + D)
+    E = H * D
+    mq, mk = (torch.randn(B, S, E, generator=r).to(dev) for _ in range(2))
+    vq, vk = (0.1 * torch.rand(B, S, E, generator=r).to(dev) for _ in range(2))
+    sc = 1.0 / math.sqrt(D)
+    st = _lib.stream_of(mq)
+    mu_qk, var_qk = torch.empty(B, H, S, S, device=dev), torch.empty(B, H, S, S, device=dev)
+    _lib.call("tagi_bmm_tagi", mq.data_ptr(), vq.data_ptr(), mk.data_ptr(), vk.data_ptr(), mu_qk.data_ptr(),
+              var_qk.data_ptr(), B * H, S, D, S, _lib.view(H, S * E, D, E, 1), _lib.view(H, S * E, D, 1, E),
+              _lib.view(1, S * S, 0, S, 1), sc, sc * sc, st)
+    ra, rv, rj = remax(mu_qk.view(-1, S), var_qk.view(-1, S))
+    fa, fv, fj = (torch.empty(B, H, S, S, device=dev) for _ in range(3))
+    _lib.call("tagi_attn_scores_remax", mq.data_ptr(), vq.data_ptr(), mk.data_ptr(), vk.data_ptr(), fa.data_ptr(),
+              fv.data_ptr(), fj.data_ptr(), B, H, S, D, sc, sc * sc, st)
+    for name, got, ref in (("mu_a", fa, ra), ("var_a", fv, rv), ("J", fj, rj)):
+        assert torch.equal(got.view(-1, S), ref), f"{name}: fused differs from the two calls"
+
+
 @pytest.mark.parametrize("transpose_a,transpose_b", [(False, False), (True, False), (False, True), (True, True)])
 def test_bmm_wrappers_strided(dev, transpose_a, transpose_b):
     from triton_tagi_amd.kernels.attention import bmm_shared_left, bmm_shared_right, bmm_tagi, bmm_tagi_var

@@ -124,3 +124,144 @@ extern "C" int tagi_bmm_shared_jacobian(const float* p0, const float* p1, const 
   return bmm_shared_impl(what, p0, p1, p2, J, mean, var, batch, M, K, L, va, vb, vo, scale, scale_sq, shared_left,
                          stream);
 }
+
+// =================================================== attention scores + Remax, fused
+// multihead_attention.py:174-190: the scores' moments Q K^T for one head and 32 query rows
+// (the TAGI product of tagi_bmm_tagi, with its reduction order: k-tile t of 16, k-step s,
+// lane half hl taking k = 16t + 8hl + s, so the scores are bit-identical to that path's),
+// held in LDS and passed through the Remax row by row (the row math of tagi_remax_fwd).
+// The raw scores never reach HBM: per head, 2 S x S tensors are neither written nor read
+// back. Eight waves (two blocks per CU fit the 64 KB tile, 4 waves per SIMD to hide the
+// Remax's dependent VALU chains): wave w forms column tile w (S <= 256), then applies the
+// Remax to rows 4w .. 4w + 3 of the block.
+namespace {
+constexpr int kScoreLd = 257;  // padded LDS row (S <= 256): conflict-free row reads
+
+template <int HD>
+__global__ void __launch_bounds__(512) attn_scores_remax_kernel(const float* __restrict__ mq,
+                                                                const float* __restrict__ vq,
+                                                                const float* __restrict__ mk,
+                                                                const float* __restrict__ vk, float* __restrict__ ma,
+                                                                float* __restrict__ Sa, float* __restrict__ Jo, int H,
+                                                                int S, int E, float scale, float scale_sq) {
+  constexpr int NKT = HD / 16;
+  __shared__ float sm[2 * 32 * kScoreLd];
+  const int z = blockIdx.y;
+  const int b = z / H, h = z - b * H;
+  const int r0 = blockIdx.x * 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, rl = lane & 31;
+  const int64_t hbase = (int64_t)b * S * E + (int64_t)h * HD + 8 * hl;
+
+  // query row r0 + rl: the lane's 8 reduction indices of each k-tile
+  float aq[NKT][8], av[NKT][8];
+  {
+    const int qi = r0 + rl;
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+        if (qi < S) {
+          const int64_t o = hbase + (int64_t)qi * E + 16 * t + 4 * u;
+          x = *reinterpret_cast<const float4*>(mq + o);
+          y = *reinterpret_cast<const float4*>(vq + o);
+        }
+        aq[t][4 * u + 0] = x.x, aq[t][4 * u + 1] = x.y, aq[t][4 * u + 2] = x.z, aq[t][4 * u + 3] = x.w;
+        av[t][4 * u + 0] = y.x, av[t][4 * u + 1] = y.y, av[t][4 * u + 2] = y.z, av[t][4 * u + 3] = y.w;
+      }
+  }
+  if (wave * 32 < S) {  // column tiles past S are neither formed nor read
+    const int j = wave;
+    const int kn = j * 32 + rl;  // key row
+    float bm[NKT][8], bv[NKT][8];
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+        if (kn < S) {
+          const int64_t o = hbase + (int64_t)kn * E + 16 * t + 4 * u;
+          x = *reinterpret_cast<const float4*>(mk + o);
+          y = *reinterpret_cast<const float4*>(vk + o);
+        }
+        bm[t][4 * u + 0] = x.x, bm[t][4 * u + 1] = x.y, bm[t][4 * u + 2] = x.z, bm[t][4 * u + 3] = x.w;
+        bv[t][4 * u + 0] = y.x, bv[t][4 * u + 1] = y.y, bv[t][4 * u + 2] = y.z, bv[t][4 * u + 3] = y.w;
+      }
+    floatx16 accM, accV;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) accM[v] = accV[v] = 0.f;
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float a0 = aq[t][s], a1 = av[t][s], b0 = bm[t][s], b1 = bv[t][s];
+        const float asq = a0 * a0, bvar = b0 * b0 + b1;
+        accM = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, accM, 0, 0, 0);
+        accV = __builtin_amdgcn_mfma_f32_32x32x2f32(asq, b1, accV, 0, 0, 0);
+        accV = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, bvar, accV, 0, 0, 0);
+      }
+    // accumulator v of lane l: row 8(v/4) + 4hl + v%4, column j*32 + rl (scaled as the
+    // batched product's epilogue does)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int row = 8 * (v >> 2) + 4 * hl + (v & 3);
+      sm[row * kScoreLd + kn] = accM[v] * scale + 0.f;
+      sm[32 * kScoreLd + row * kScoreLd + kn] = accV[v] * scale_sq + 0.f;
+    }
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int rr = 0; rr < 4; ++rr) {
+    const int row = wave * 4 + rr;
+    const int i = r0 + row;
+    if (i >= S) break;
+    float m[4], v[4], oa[4], os[4], oj[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = lane + 64 * e;
+      const bool ok = c < S;
+      m[e] = ok ? sm[row * kScoreLd + c] : 0.f;
+      v[e] = ok ? sm[32 * kScoreLd + row * kScoreLd + c] : 1.f;
+    }
+    remax_row<4>(m, v, lane, S, oa, os, oj);
+    const int64_t ob = ((int64_t)z * S + i) * S;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = lane + 64 * e;
+      if (c < S) {
+        ma[ob + c] = oa[e];
+        Sa[ob + c] = os[e];
+        Jo[ob + c] = oj[e];
+      }
+    }
+  }
+}
+}  // namespace
+
+extern "C" int tagi_attn_scores_remax(const float* mu_q, const float* var_q, const float* mu_k, const float* var_k,
+                                      float* mu_a, float* var_a, float* J, int64_t B, int64_t H, int64_t S, int64_t D,
+                                      float scale, float scale_sq, tagi_stream_t stream) {
+  const char* what = "tagi_attn_scores_remax";
+  TAGI_REQUIRE(mu_q && var_q && mu_k && var_k && mu_a && var_a && J, "%s: null pointer", what);
+  TAGI_REQUIRE(B > 0 && H > 0 && S > 0 && D > 0, "%s: bad sizes", what);
+  if (S > 256 || !(D == 16 || D == 32 || D == 64))
+    return fail(TAGI_ERR_UNSUPPORTED, "%s: needs S <= 256 and head_dim 16, 32 or 64 (S=%lld, D=%lld)", what,
+                (long long)S, (long long)D);
+  TAGI_REQUIRE(al16(mu_q) && al16(var_q) && al16(mu_k) && al16(var_k), "%s: q/k must be 16-byte aligned", what);
+  TAGI_REQUIRE(B * H < 65536 && fits_i32(B * S * H * D) && B * H * S * S < (1ll << 40), "%s: too large", what);
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_ATTN_SCORES, s, 2.0 * 3 * B * H * S * S * D, 4.0 * (4 * B * S * H * D + 3 * B * H * S * S));
+  const dim3 grid((unsigned)cdiv(S, 32), (unsigned)(B * H));
+  const int E = (int)(H * D);
+  if (D == 16)
+    hipLaunchKernelGGL(attn_scores_remax_kernel<16>, grid, dim3(512), 0, s, mu_q, var_q, mu_k, var_k, mu_a, var_a, J,
+                       (int)H, (int)S, E, scale, scale_sq);
+  else if (D == 32)
+    hipLaunchKernelGGL(attn_scores_remax_kernel<32>, grid, dim3(512), 0, s, mu_q, var_q, mu_k, var_k, mu_a, var_a, J,
+                       (int)H, (int)S, E, scale, scale_sq);
+  else
+    hipLaunchKernelGGL(attn_scores_remax_kernel<64>, grid, dim3(512), 0, s, mu_q, var_q, mu_k, var_k, mu_a, var_a, J,
+                       (int)H, (int)S, E, scale, scale_sq);
+  return check_launch(what);
+}

@@ -56,7 +56,8 @@ enum Family {
   FAM_MAXPOOL = 22,
   FAM_LAYERNORM = 23,
   FAM_SOFTPLUS = 24,
-  FAM_COUNT = 25
+  FAM_ATTN_SCORES = 25,
+  FAM_COUNT = 26
 };
 
 // Record a start event for `fam` on `s` if the timer is on for that family.

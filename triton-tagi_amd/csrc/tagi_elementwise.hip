@@ -290,92 +290,32 @@ __global__ void __launch_bounds__(256) avgpool_bwd_kernel(const float* __restric
 }
 
 // ------------------------------------------------------------------------ Remax
-// remax.py:33-114. One wavefront per row; each lane keeps EPT classes in registers.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
+// remax.py:33-114. One wavefront per row (the row math is remax_row in tagi_moments.h).
 template <int EPT>
 __global__ void __launch_bounds__(256) remax_kernel(const float* __restrict__ mz, const float* __restrict__ Sz,
                                                     float* __restrict__ ma, float* __restrict__ Sa,
                                                     float* __restrict__ Jo, int64_t rows, int K) {
-  const float EPS = 1e-6f;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= rows) return;
   const float* pm = mz + row * K;
   const float* ps = Sz + row * K;
-  float var_z[EPT], mu_m[EPT], var_m[EPT], jcb[EPT];
-  float s_mu = 0.f, s_var = 0.f;
+  float m[EPT], v[EPT], mua[EPT], vara[EPT], jo[EPT];
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const int c = lane + 64 * e;
     const bool ok = c < K;
-    const float m = ok ? pm[c] : 0.f;
-    const float v = ok ? ps[c] : 1.f;
-    const float rs = fast_rsqrt(v);
-    const float sd = v * rs;
-    const float al = m * rs;
-    const float pdf = INV_SQRT_2PI * fast_exp(-0.5f * al * al);
-    float cdf, ccdf;
-    normal_cdf_pair(al, cdf, ccdf);
-    const float mraw = m * cdf + sd * pdf;
-    const float mm = fmaxf(mraw, EPS);
-    // same variance as -mm^2 + 2 mm m - m sd pdf + (v - m^2) cdf while the mean floor is
-    // inactive (see rect_var); the floored case keeps the reference's expression
-    const float vraw = (mraw >= EPS) ? rect_var(v, al, pdf, cdf, ccdf)
-                                     : -mm * mm + 2.0f * mm * m - m * sd * pdf + (v - m * m) * cdf;
-    const float vm = fmaxf(vraw, EPS);
-    var_z[e] = v;
-    mu_m[e] = mm;
-    var_m[e] = vm;
-    jcb[e] = cdf;
-    if (ok) {
-      s_mu += mm;
-      s_var += vm;
-    }
+    m[e] = ok ? pm[c] : 0.f;
+    v[e] = ok ? ps[c] : 1.f;
   }
-  const float mu_mt = fmaxf(wave_sum(s_mu), EPS);
-  const float var_mt = fmaxf(wave_sum(s_var), EPS);
-  const float inv_mt = fast_rcp(mu_mt);
-  // log1p/expm1 below are the reference's log(1 + x) / exp(x) - 1 without fp32 cancellation
-  const float var_log_mt = log1p_pos(var_mt * inv_mt * inv_mt);
-  const float mu_log_mt = fast_log(mu_mt) - 0.5f * var_log_mt;
-  float var_log_m[EPT], cov_m_mt[EPT], mu_a_raw[EPT], var_log_a[EPT];
-  float s_a = 0.f;
-#pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    const int c = lane + 64 * e;
-    const float rm = fast_rcp(mu_m[e]);
-    const float vlm = log1p_pos(var_m[e] * rm * rm);
-    const float mlm = fast_log(mu_m[e]) - 0.5f * vlm;
-    const float cov = log1p_pos(var_m[e] * rm * inv_mt);
-    const float mla = mlm - mu_log_mt;
-    const float vla = fmaxf(vlm + var_log_mt - 2.0f * cov, 0.0f);
-    const float mar = fmaxf(fast_exp(mla + 0.5f * vla), EPS);
-    var_log_m[e] = vlm;
-    cov_m_mt[e] = cov;
-    var_log_a[e] = vla;
-    mu_a_raw[e] = mar;
-    if (c < K) s_a += mar;
-  }
-  const float inv_sum_a = fast_rcp(fmaxf(wave_sum(s_a), EPS));
+  remax_row<EPT>(m, v, lane, K, mua, vara, jo);
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const int c = lane + 64 * e;
     if (c >= K) continue;
-    const float mua = mu_a_raw[e] * inv_sum_a;
-    const float vara = expm1_pos(var_log_a[e]) * mua * mua;
-    // log-space covariance of a and m: vlm - cov >= 0 up to rounding, since mu_m <= mu_mt
-    const float cov_la_lm = fmaxf(var_log_m[e] - cov_m_mt[e], 0.0f);
-    const float cov_am = expm1_pos(cov_la_lm) * mua * mu_m[e];
-    const float cs = __builtin_amdgcn_sqrtf(vara * var_z[e]);
-    const float cov_az = fminf(cs, cov_am * fast_rcp(fmaxf(jcb[e], EPS)));
-    ma[row * K + c] = mua;
-    Sa[row * K + c] = vara;
-    Jo[row * K + c] = cov_az * fast_rcp(var_z[e]);
+    ma[row * K + c] = mua[e];
+    Sa[row * K + c] = vara[e];
+    Jo[row * K + c] = jo[e];
   }
 }
 

@@ -113,4 +113,86 @@ __device__ __forceinline__ void relu_moments(float mz, float Sz, float& ma, floa
   J = cdf;
 }
 
+// Sum over a 64-lane wavefront (butterfly; every lane gets the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Remax of one row of K <= 64*EPT classes held by a wavefront (remax.py:33-114): lane
+// holds classes lane + 64e. In: the row's moments (any values past K). Out: mu_a, S_a and
+// the Jacobian J = cov(a, z) / S_z, valid for the lane's classes below K.
+template <int EPT>
+__device__ __forceinline__ void remax_row(const float (&mz)[EPT], const float (&Sz)[EPT], int lane, int K,
+                                          float (&ma)[EPT], float (&Sa)[EPT], float (&Jo)[EPT]) {
+  const float EPS = 1e-6f;
+  float var_z[EPT], mu_m[EPT], var_m[EPT], jcb[EPT];
+  float s_mu = 0.f, s_var = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const bool ok = lane + 64 * e < K;
+    const float m = mz[e];
+    const float v = Sz[e];
+    const float rs = fast_rsqrt(v);
+    const float sd = v * rs;
+    const float al = m * rs;
+    const float pdf = INV_SQRT_2PI * fast_exp(-0.5f * al * al);
+    float cdf, ccdf;
+    normal_cdf_pair(al, cdf, ccdf);
+    const float mraw = m * cdf + sd * pdf;
+    const float mm = fmaxf(mraw, EPS);
+    // same variance as -mm^2 + 2 mm m - m sd pdf + (v - m^2) cdf while the mean floor is
+    // inactive (see rect_var); the floored case keeps the reference's expression
+    const float vraw = (mraw >= EPS) ? rect_var(v, al, pdf, cdf, ccdf)
+                                     : -mm * mm + 2.0f * mm * m - m * sd * pdf + (v - m * m) * cdf;
+    const float vm = fmaxf(vraw, EPS);
+    var_z[e] = v;
+    mu_m[e] = mm;
+    var_m[e] = vm;
+    jcb[e] = cdf;
+    if (ok) {
+      s_mu += mm;
+      s_var += vm;
+    }
+  }
+  const float mu_mt = fmaxf(wave_sum(s_mu), EPS);
+  const float var_mt = fmaxf(wave_sum(s_var), EPS);
+  const float inv_mt = fast_rcp(mu_mt);
+  // log1p/expm1 below are the reference's log(1 + x) / exp(x) - 1 without fp32 cancellation
+  const float var_log_mt = log1p_pos(var_mt * inv_mt * inv_mt);
+  const float mu_log_mt = fast_log(mu_mt) - 0.5f * var_log_mt;
+  float var_log_m[EPT], cov_m_mt[EPT], mu_a_raw[EPT], var_log_a[EPT];
+  float s_a = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const float rm = fast_rcp(mu_m[e]);
+    const float vlm = log1p_pos(var_m[e] * rm * rm);
+    const float mlm = fast_log(mu_m[e]) - 0.5f * vlm;
+    const float cov = log1p_pos(var_m[e] * rm * inv_mt);
+    const float mla = mlm - mu_log_mt;
+    const float vla = fmaxf(vlm + var_log_mt - 2.0f * cov, 0.0f);
+    const float mar = fmaxf(fast_exp(mla + 0.5f * vla), EPS);
+    var_log_m[e] = vlm;
+    cov_m_mt[e] = cov;
+    var_log_a[e] = vla;
+    mu_a_raw[e] = mar;
+    if (lane + 64 * e < K) s_a += mar;
+  }
+  const float inv_sum_a = fast_rcp(fmaxf(wave_sum(s_a), EPS));
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const float mua = mu_a_raw[e] * inv_sum_a;
+    const float vara = expm1_pos(var_log_a[e]) * mua * mua;
+    // log-space covariance of a and m: vlm - cov >= 0 up to rounding, since mu_m <= mu_mt
+    const float cov_la_lm = fmaxf(var_log_m[e] - cov_m_mt[e], 0.0f);
+    const float cov_am = expm1_pos(cov_la_lm) * mua * mu_m[e];
+    const float cs = __builtin_amdgcn_sqrtf(vara * var_z[e]);
+    const float cov_az = fminf(cs, cov_am * fast_rcp(fmaxf(jcb[e], EPS)));
+    ma[e] = mua;
+    Sa[e] = vara;
+    Jo[e] = cov_az * fast_rcp(var_z[e]);
+  }
+}
+
 }  // namespace tagi

@@ -22,7 +22,7 @@ FAMILIES = [
     "conv_fwd", "conv_bwd_delta", "conv_wgrad", "linear_fwd", "linear_bwd_delta",
     "linear_wgrad", "bmm_fwd", "bmm_shared", "relu", "remax", "bn_stats", "bn_fwd",
     "bn_bwd", "update", "innovation", "add", "avgpool", "jacobian", "rmsnorm",
-    "embedding", "pe", "splitk_reduce", "maxpool", "layernorm", "softplus",
+    "embedding", "pe", "splitk_reduce", "maxpool", "layernorm", "softplus", "attn_scores",
 ]
 FAM_COUNT = len(FAMILIES)
 
@@ -75,6 +75,7 @@ _SIGS = {
     "tagi_linear_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
     "tagi_linear_wgrad_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_bmm_tagi": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, P]),
+    "tagi_attn_scores_remax": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, F, F, P]),
     "tagi_bmm_shared": (c_int, [P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),
     "tagi_bmm_shared_jacobian": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),
     "tagi_conv2d_fwd": (c_int, [P, P, P, P, P, P, P, P, GP, P, I64, P]),

@@ -81,15 +81,23 @@ class MultiheadAttentionV2(LearnableLayer):
         dev = ma.device
         st = _lib.stream_of(mu_q)
         s = self._scale
-        mu_qk = torch.empty(B, H, S, S, device=dev, dtype=torch.float32)
-        var_qk = torch.empty_like(mu_qk)
-        _lib.call("tagi_bmm_tagi", mu_q.data_ptr(), var_q.data_ptr(), mu_k.data_ptr(), var_k.data_ptr(),
-                  mu_qk.data_ptr(), var_qk.data_ptr(), B * H, S, D, S, self._head_view(S),
-                  self._head_view(S, transpose=True), self._score_view(S), s, s * s, st)
-        mu_score, var_score, jcb = remax(mu_qk.view(B * H * S, S), var_qk.view(B * H * S, S))
-        mu_score = mu_score.view(B, H, S, S)
-        var_score = var_score.view(B, H, S, S)
-        jcb = jcb.view(B, H, S, S)
+        if S <= 256 and D in (16, 32, 64) and all(t.data_ptr() % 16 == 0 for t in (mu_q, var_q, mu_k, var_k)):
+            # scores and Remax in one kernel; the same values as the two calls below
+            mu_score = torch.empty(B, H, S, S, device=dev, dtype=torch.float32)
+            var_score, jcb = torch.empty_like(mu_score), torch.empty_like(mu_score)
+            _lib.call("tagi_attn_scores_remax", mu_q.data_ptr(), var_q.data_ptr(), mu_k.data_ptr(),
+                      var_k.data_ptr(), mu_score.data_ptr(), var_score.data_ptr(), jcb.data_ptr(), B, H, S, D,
+                      s, s * s, st)
+        else:
+            mu_qk = torch.empty(B, H, S, S, device=dev, dtype=torch.float32)
+            var_qk = torch.empty_like(mu_qk)
+            _lib.call("tagi_bmm_tagi", mu_q.data_ptr(), var_q.data_ptr(), mu_k.data_ptr(), var_k.data_ptr(),
+                      mu_qk.data_ptr(), var_qk.data_ptr(), B * H, S, D, S, self._head_view(S),
+                      self._head_view(S, transpose=True), self._score_view(S), s, s * s, st)
+            mu_score, var_score, jcb = remax(mu_qk.view(B * H * S, S), var_qk.view(B * H * S, S))
+            mu_score = mu_score.view(B, H, S, S)
+            var_score = var_score.view(B, H, S, S)
+            jcb = jcb.view(B, H, S, S)
         mu_out = torch.empty(B, S, E, device=dev, dtype=torch.float32)
         var_out = torch.empty_like(mu_out)
         _lib.call("tagi_bmm_tagi", mu_score.data_ptr(), var_score.data_ptr(), mu_v.data_ptr(), var_v.data_ptr(),
