@@ -184,6 +184,19 @@ int tagi_attn_scores_remax(const float* mu_q, const float* var_q, const float* m
                            float* mu_a, float* var_a, float* J, int64_t B, int64_t H, int64_t S, int64_t D,
                            float scale, float scale_sq, tagi_stream_t stream);
 
+/* The attention's query or key deltas from the output deltas in one kernel
+ * (multihead_attention.py:238-251): with scaled = (d_out @ mu_v^T) x J (mean; the variance
+ * is (d_var @ (mu_v^2)^T) x J^2, as tagi_bmm_shared_jacobian forms it),
+ *   transpose == 0:  out = scale * scaled @ mu_x,   out_var = scale_sq * scaled_var @ mu_x^2  (dQ, mu_x = mu_k)
+ *   transpose == 1:  out = scale * scaled^T @ mu_x, ...                                      (dK, mu_x = mu_q)
+ * d_mu, d_var, mu_v, mu_x, out: (B, S, H*D), head h at columns h*D ..; J: (B, H, S, S). The
+ * scaled deltas are formed per block in LDS and never reach memory. Needs S <= 256,
+ * D in {16, 32} and 16-byte aligned d_mu, d_var, mu_v (else TAGI_ERR_UNSUPPORTED: use
+ * tagi_bmm_shared_jacobian and tagi_bmm_shared). */
+int tagi_attn_score_deltas_qk(const float* d_mu, const float* d_var, const float* mu_v, const float* J,
+                              const float* mu_x, float* out_mu, float* out_var, int64_t B, int64_t H, int64_t S,
+                              int64_t D, float scale, float scale_sq, int transpose, tagi_stream_t stream);
+
 /* ------------------------------------------------------------------ Conv2D ---- */
 /* 4-D activations and deltas of the conv path (Conv2D, BatchNorm2D, AvgPool2D) are
  * channels-last: element (n, c, h, w) of an (N, C, H, W) tensor sits at ((n*H + h)*W + w)*C + c

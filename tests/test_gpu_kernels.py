@@ -462,6 +462,47 @@ def test_attention_scores_remax_fused_equals_two_calls(dev, B, H, S, D):
         assert torch.equal(got.view(-1, S), ref), f"{name}: fused differs from the two calls"
 
 
+@pytest.mark.parametrize("B,H,S,D", [(2, 8, 256, 32), (1, 2, 40, 16), (2, 2, 100, 32), (1, 3, 1, 32)])
+def test_attention_score_deltas_qk_fused(dev, B, H, S, D):
+    """tagi_attn_score_deltas_qk (the Jacobian-scaled score deltas formed per block in LDS,
+    then the dQ / dK product) against tagi_bmm_shared_jacobian followed by tagi_bmm_shared
+    on the materialised scaled deltas: the same terms summed in a different grouping (the
+    reduction over the S scores is split over 8 waves), so each output is held to 1e-5 of
+    the sum of its terms' magnitudes."""
+    import math
+
+    from triton_tagi_amd import _lib
+
+    r = g(7 * S + D + H)
+    E = H * D
+    dmu, mv, mq, mk = (torch.randn(B, S, E, generator=r).to(dev) for _ in range(4))
+    dvar = -torch.rand(B, S, E, generator=r).to(dev)
+    J = torch.rand(B, H, S, S, generator=r).to(dev)
+    sc = 1.0 / math.sqrt(D)
+    st = _lib.stream_of(dmu)
+    hv, hvt = _lib.view(H, S * E, D, E, 1), _lib.view(H, S * E, D, 1, E)
+    sv, svt = _lib.view(1, S * S, 0, S, 1), _lib.view(1, S * S, 0, 1, S)
+    smu, svar = torch.empty(B, H, S, S, device=dev), torch.empty(B, H, S, S, device=dev)
+    _lib.call("tagi_bmm_shared_jacobian", dmu.data_ptr(), dvar.data_ptr(), mv.data_ptr(), J.data_ptr(),
+              smu.data_ptr(), svar.data_ptr(), B * H, S, D, S, hv, hvt, sv, 1.0, 1.0, 0, st)
+    for x, view, tr, name in ((mk, sv, 0, "dQ"), (mq, svt, 1, "dK")):
+        rm, rS = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
+        _lib.call("tagi_bmm_shared", smu.data_ptr(), svar.data_ptr(), x.data_ptr(), rm.data_ptr(), rS.data_ptr(),
+                  B * H, S, S, D, view, hv, hv, sc, sc * sc, 0, st)
+        fm, fS = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
+        _lib.call("tagi_attn_score_deltas_qk", dmu.data_ptr(), dvar.data_ptr(), mv.data_ptr(), J.data_ptr(),
+                  x.data_ptr(), fm.data_ptr(), fS.data_ptr(), B, H, S, D, sc, sc * sc, tr, st)
+        # term magnitudes: |scaled| @ |x| per head (the scaled deltas as the two-call path holds them)
+        a_m, a_S = smu.abs(), svar.abs()
+        if tr:
+            a_m, a_S = a_m.transpose(-1, -2), a_S.transpose(-1, -2)
+        xh = x.view(B, S, H, D).permute(0, 2, 1, 3).contiguous()
+        tm = sc * torch.matmul(a_m.contiguous(), xh.abs()).permute(0, 2, 1, 3).reshape(B, S, E)
+        tS = sc * sc * torch.matmul(a_S.contiguous(), xh * xh).permute(0, 2, 1, 3).reshape(B, S, E)
+        assert_scaled_close(fm, rm, tm, 1e-5, 1e-7, f"{name} mean")
+        assert_scaled_close(fS, rS, tS, 1e-5, 1e-7, f"{name} var")
+
+
 @pytest.mark.parametrize("transpose_a,transpose_b", [(False, False), (True, False), (False, True), (True, True)])
 def test_bmm_wrappers_strided(dev, transpose_a, transpose_b):
     from triton_tagi_amd.kernels.attention import bmm_shared_left, bmm_shared_right, bmm_tagi, bmm_tagi_var

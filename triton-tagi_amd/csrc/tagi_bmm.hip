@@ -265,3 +265,167 @@ extern "C" int tagi_attn_scores_remax(const float* mu_q, const float* var_q, con
                        (int)H, (int)S, E, scale, scale_sq);
   return check_launch(what);
 }
+
+// ================================== attention score deltas -> dQ / dK products, fused
+// multihead_attention.py:238-251: the score deltas d_out @ mu_v^T, scaled by the Remax
+// Jacobian J (mean x J, variance x J^2), feed dQ = s * scaled @ mu_k and
+// dK = s * scaled^T @ mu_q. Each block rebuilds in LDS the part of the scaled deltas its
+// output needs -- 32 query rows for dQ, 32 key columns for dK (TRANS) -- with the
+// score-delta product and Jacobian of tagi_bmm_shared_jacobian (same MFMA order and
+// epilogue, so the same values), then runs the second product from LDS: the (B, H, S, S)
+// scaled deltas are never written or read back. The second product's reduction over the
+// S scores is split over the 8 waves (32 scores each); the 8 partial tiles are added in
+// wave order, so results are deterministic and within rounding of the one-pass sum.
+namespace {
+// (at most 128 registers, so that two blocks -- four waves per SIMD -- fit beside the LDS)
+template <int HD, bool TRANS>
+__global__ void __launch_bounds__(512, 4) attn_dqk_kernel(const float* __restrict__ dmu, const float* __restrict__ dvar,
+                                                       const float* __restrict__ mv, const float* __restrict__ Jg,
+                                                       const float* __restrict__ mx, float* __restrict__ omu,
+                                                       float* __restrict__ ovar, int H, int S, int E, float scale,
+                                                       float scale_sq) {
+  constexpr int NKT = HD / 16;
+  // phase 1-2: [moment][output row][score index]; phase 3: 8 waves x 2 moments x 32 x 32 partials
+  __shared__ float sm[2 * 32 * kScoreLd];
+  static_assert(8 * 2 * 32 * 32 <= 2 * 32 * kScoreLd, "partials must fit the score tile");
+  const int z = blockIdx.y;
+  const int b = z / H, h = z - b * H;
+  const int o0 = blockIdx.x * 32;  // first output row: query (dQ) or key (dK)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, rl = lane & 31;
+  const int64_t hbase = (int64_t)b * S * E + (int64_t)h * HD;
+  const int64_t jz = (int64_t)z * S * S;
+  const bool active = wave * 32 < S;  // this wave's 32 score indices exist
+
+  // the Jacobian tile is loaded first, so its latency overlaps phase 1's loads and MFMAs
+  float jr[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int tr = 8 * (q >> 2) + 4 * hl + (q & 3);
+    const int qi = TRANS ? 32 * wave + tr : o0 + tr;
+    const int kj = TRANS ? o0 + rl : 32 * wave + rl;
+    jr[q] = (active && qi < S && kj < S) ? Jg[jz + (int64_t)qi * S + kj] : 0.f;
+  }
+  // phase 1: scaled score deltas of query rows x key columns, one 32 x 32 tile per wave
+  if (active) {
+    const int ai = TRANS ? 32 * wave + rl : o0 + rl;  // query row (A = output deltas)
+    const int bj = TRANS ? o0 + rl : 32 * wave + rl;  // key row (B = mu_v, shared)
+    float am[NKT][8], av[NKT][8], bm[NKT][8];
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x, w = x;
+        const int64_t ko = hbase + 8 * hl + 16 * t + 4 * u;
+        if (ai < S) {
+          x = *reinterpret_cast<const float4*>(dmu + ko + (int64_t)ai * E);
+          y = *reinterpret_cast<const float4*>(dvar + ko + (int64_t)ai * E);
+        }
+        if (bj < S) w = *reinterpret_cast<const float4*>(mv + ko + (int64_t)bj * E);
+        am[t][4 * u + 0] = x.x, am[t][4 * u + 1] = x.y, am[t][4 * u + 2] = x.z, am[t][4 * u + 3] = x.w;
+        av[t][4 * u + 0] = y.x, av[t][4 * u + 1] = y.y, av[t][4 * u + 2] = y.z, av[t][4 * u + 3] = y.w;
+        bm[t][4 * u + 0] = w.x, bm[t][4 * u + 1] = w.y, bm[t][4 * u + 2] = w.z, bm[t][4 * u + 3] = w.w;
+      }
+    floatx16 accM, accV;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) accM[v] = accV[v] = 0.f;
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float b0 = bm[t][s], bsq = b0 * b0;
+        accM = __builtin_amdgcn_mfma_f32_32x32x2f32(am[t][s], b0, accM, 0, 0, 0);
+        accV = __builtin_amdgcn_mfma_f32_32x32x2f32(av[t][s], bsq, accV, 0, 0, 0);
+      }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int tr = 8 * (v >> 2) + 4 * hl + (v & 3);  // tile row (query side of A)
+      const float jj = jr[v];
+      float m = accM[v] * 1.f + 0.f, vv = accV[v] * 1.f + 0.f;
+      m *= jj;
+      vv *= jj * jj;
+      const int orow = TRANS ? rl : tr;
+      const int ocol = TRANS ? 32 * wave + tr : 32 * wave + rl;
+      sm[orow * kScoreLd + ocol] = m;
+      sm[32 * kScoreLd + orow * kScoreLd + ocol] = vv;
+    }
+  }
+  __syncthreads();
+
+  // phase 2: the output rows times mu_x over this wave's 32 score indices
+  floatx16 pM, pV;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) pM[v] = pV[v] = 0.f;
+  if (active) {
+    float xr[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int k = 32 * wave + 16 * (q >> 3) + 8 * hl + (q & 7);
+      xr[q] = (k < S && rl < HD) ? mx[hbase + (int64_t)k * E + rl] : 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int k = 32 * wave + 16 * t + 8 * hl + s;  // score index
+        const float a0 = sm[rl * kScoreLd + k], a1 = sm[32 * kScoreLd + rl * kScoreLd + k];
+        const float x = xr[8 * t + s];
+        const float xsq = x * x;
+        pM = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, x, pM, 0, 0, 0);
+        pV = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, xsq, pV, 0, 0, 0);
+      }
+  }
+  __syncthreads();
+  // phase 3: partials (output row, column d) in wave order, then the fixed-order sum
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int tr = 8 * (v >> 2) + 4 * hl + (v & 3);
+    sm[(wave * 2 + 0) * 1024 + tr * 32 + rl] = pM[v];
+    sm[(wave * 2 + 1) * 1024 + tr * 32 + rl] = pV[v];
+  }
+  __syncthreads();
+  const int nw = (S + 31) / 32;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int idx = threadIdx.x + 512 * q;  // 2 moments x 32 rows x 32 columns
+    const int mom = idx >> 10, row = (idx >> 5) & 31, d = idx & 31;
+    float acc = 0.f;
+    for (int w = 0; w < nw; ++w) acc += sm[(w * 2 + mom) * 1024 + row * 32 + d];
+    if (o0 + row < S && d < HD) {
+      const int64_t o = hbase + (int64_t)(o0 + row) * E + d;
+      if (mom == 0) omu[o] = acc * scale + 0.f;
+      else ovar[o] = acc * scale_sq + 0.f;
+    }
+  }
+}
+}  // namespace
+
+extern "C" int tagi_attn_score_deltas_qk(const float* d_mu, const float* d_var, const float* mu_v, const float* J,
+                                         const float* mu_x, float* out_mu, float* out_var, int64_t B, int64_t H,
+                                         int64_t S, int64_t D, float scale, float scale_sq, int transpose,
+                                         tagi_stream_t stream) {
+  const char* what = "tagi_attn_score_deltas_qk";
+  TAGI_REQUIRE(d_mu && d_var && mu_v && J && mu_x && out_mu && out_var, "%s: null pointer", what);
+  TAGI_REQUIRE(B > 0 && H > 0 && S > 0 && D > 0, "%s: bad sizes", what);
+  if (S > 256 || !(D == 16 || D == 32))
+    return fail(TAGI_ERR_UNSUPPORTED, "%s: needs S <= 256 and head_dim 16 or 32 (S=%lld, D=%lld)", what,
+                (long long)S, (long long)D);
+  TAGI_REQUIRE(al16(d_mu) && al16(d_var) && al16(mu_v), "%s: d_mu, d_var and mu_v must be 16-byte aligned", what);
+  TAGI_REQUIRE(B * H < 65536 && fits_i32(B * S * H * D) && B * H * S * S < (1ll << 40), "%s: too large", what);
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_BMM_SHARED, s, 2.0 * 4 * B * H * S * S * D, 4.0 * (B * H * S * S + 6 * B * S * H * D));
+  const dim3 grid((unsigned)cdiv(S, 32), (unsigned)(B * H));
+  const int E = (int)(H * D);
+#define TAGI_DQK(HD_, T_)                                                                                      \
+  hipLaunchKernelGGL((attn_dqk_kernel<HD_, T_>), grid, dim3(512), 0, s, d_mu, d_var, mu_v, J, mu_x, out_mu, out_var, \
+                     (int)H, (int)S, E, scale, scale_sq)
+  if (D == 16) {
+    if (transpose) TAGI_DQK(16, true);
+    else TAGI_DQK(16, false);
+  } else {
+    if (transpose) TAGI_DQK(32, true);
+    else TAGI_DQK(32, false);
+  }
+#undef TAGI_DQK
+  return check_launch(what);
+}

@@ -122,23 +122,30 @@ class MultiheadAttentionV2(LearnableLayer):
         dv, dSv = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
         _lib.call("tagi_bmm_shared", d_mu.data_ptr(), d_var.data_ptr(), c["mu_score"].data_ptr(), dv.data_ptr(),
                   dSv.data_ptr(), B * H, S, S, D, svt, hv, hv, 1.0, 1.0, 1, st)
-        # dscore = d_out @ mu_v^T (mu_v shared on the right), times the Remax Jacobian in the
-        # product's epilogue (multihead_attention.py:239-243)
+        # dscore = d_out @ mu_v^T (mu_v shared on the right), times the Remax Jacobian
+        # (multihead_attention.py:239-243); dQ = s scaled @ mu_k ; dK = s scaled^T @ mu_q
         jcb = _lib.check(c["jcb"], "jcb")
         if tuple(jcb.shape) != (B, H, S, S):
             raise ValueError(f"MultiheadAttentionV2: stored Remax Jacobian {tuple(jcb.shape)} vs {(B, H, S, S)}")
-        scaled_mu = torch.empty(B, H, S, S, device=dev)
-        scaled_var = torch.empty_like(scaled_mu)
-        _lib.call("tagi_bmm_shared_jacobian", d_mu.data_ptr(), d_var.data_ptr(), c["mu_v"].data_ptr(),
-                  jcb.data_ptr(), scaled_mu.data_ptr(), scaled_var.data_ptr(), B * H, S, D, S, hv, hvt, sv, 1.0, 1.0,
-                  0, st)
-        # dQ = s scaled @ mu_k ; dK = s scaled^T @ mu_q
         dq, dSq = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
-        _lib.call("tagi_bmm_shared", scaled_mu.data_ptr(), scaled_var.data_ptr(), c["mu_k"].data_ptr(),
-                  dq.data_ptr(), dSq.data_ptr(), B * H, S, S, D, sv, hv, hv, s, s * s, 0, st)
         dk, dSk = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
-        _lib.call("tagi_bmm_shared", scaled_mu.data_ptr(), scaled_var.data_ptr(), c["mu_q"].data_ptr(),
-                  dk.data_ptr(), dSk.data_ptr(), B * H, S, S, D, svt, hv, hv, s, s * s, 0, st)
+        mu_v = c["mu_v"]
+        if S <= 256 and D in (16, 32) and all(t.data_ptr() % 16 == 0 for t in (d_mu, d_var, mu_v)):
+            # the scaled score deltas are formed per block in LDS, never in memory
+            for x, om, oS, tr in ((c["mu_k"], dq, dSq, 0), (c["mu_q"], dk, dSk, 1)):
+                _lib.call("tagi_attn_score_deltas_qk", d_mu.data_ptr(), d_var.data_ptr(), mu_v.data_ptr(),
+                          jcb.data_ptr(), _lib.check(x, "mu_x").data_ptr(), om.data_ptr(), oS.data_ptr(), B, H, S, D,
+                          s, s * s, tr, st)
+        else:
+            scaled_mu = torch.empty(B, H, S, S, device=dev)
+            scaled_var = torch.empty_like(scaled_mu)
+            _lib.call("tagi_bmm_shared_jacobian", d_mu.data_ptr(), d_var.data_ptr(), mu_v.data_ptr(),
+                      jcb.data_ptr(), scaled_mu.data_ptr(), scaled_var.data_ptr(), B * H, S, D, S, hv, hvt, sv, 1.0,
+                      1.0, 0, st)
+            _lib.call("tagi_bmm_shared", scaled_mu.data_ptr(), scaled_var.data_ptr(), c["mu_k"].data_ptr(),
+                      dq.data_ptr(), dSq.data_ptr(), B * H, S, S, D, sv, hv, hv, s, s * s, 0, st)
+            _lib.call("tagi_bmm_shared", scaled_mu.data_ptr(), scaled_var.data_ptr(), c["mu_q"].data_ptr(),
+                      dk.data_ptr(), dSk.data_ptr(), B * H, S, S, D, svt, hv, hv, s, s * s, 0, st)
         # the projections' input deltas summed in the GEMM epilogues: (q + k) + v
         d_ma_q, d_Sa_q = self.q_proj.backward(dq, dSq)
         self.k_proj._backward(dk, dSk, True, add=(d_ma_q, d_Sa_q))
