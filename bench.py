@@ -495,6 +495,9 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernel_ms_per_step_warmup": round(gpu_ms / nps, 4),
+        # the family with the most GPU time per step (with the side stream, the parameter-
+        # delta families' time includes sharing the GPU with the input-delta chain)
+        "top_family_by_time": next(iter(breakdown), None),
         "families_warmup": breakdown,
     }
     print(json.dumps(out), flush=True)

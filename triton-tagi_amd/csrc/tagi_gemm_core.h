@@ -752,6 +752,30 @@ __device__ __forceinline__ bool epi_apply4(const Epi& e, int z, int row, int col
     *reinterpret_cast<float4*>(e.ov + off) = ov4;
     return true;
   }
+  if (e.kind == 1) {
+    // parameter deltas: 4 consecutive columns of one weight row (or of the bias row)
+    const bool wrow = row < e.wrows;
+    int64_t idx = col;
+    if (wrow) {
+      int wr = row;
+      if (e.perm_C > 0) {
+        const int kidx = fdiv(row, e.dperm);
+        wr = (row - kidx * e.perm_C) * e.perm_kk2 + kidx;
+      }
+      idx = (int64_t)wr * e.ldw + col;
+    }
+    const float* sp = wrow ? e.Sw : e.Sb;
+    float* om = wrow ? e.om : e.dmb;
+    float* ov = wrow ? e.ov : e.dSb;
+    uintptr_t al = (uintptr_t)(om + idx) | (uintptr_t)(ov + idx);
+    if (sp) al |= (uintptr_t)(sp + idx);
+    if (al & 15u) return false;
+    const float4 s4 = sp ? *reinterpret_cast<const float4*>(sp + idx) : make_float4(1.f, 1.f, 1.f, 1.f);
+    *reinterpret_cast<float4*>(om + idx) = make_float4(s4.x * m[0], s4.y * m[1], s4.z * m[2], s4.w * m[3]);
+    *reinterpret_cast<float4*>(ov + idx) =
+        make_float4((s4.x * s4.x) * v[0], (s4.y * s4.y) * v[1], (s4.z * s4.z) * v[2], (s4.w * s4.w) * v[3]);
+    return true;
+  }
   if (e.kind == 0 && e.scol == 1 && !e.jm && !e.am) {
     const int64_t off = (z / e.zdiv) * e.sz1 + (z % e.zdiv) * e.sz2 + (int64_t)row * e.srow + col;
     uintptr_t al = (uintptr_t)(e.ov + off);
@@ -1186,6 +1210,51 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
             }
             e.om[off] = m;
             e.ov[off] = vv;
+          }
+        }
+      }
+  } else if (e.kind == 1) {
+    // parameter deltas (unsplit): the Sw (Sb) factors of a lane's 16 outputs are loaded
+    // before any of them is stored -- the stores may alias them as far as the compiler
+    // knows, so a load issued after a store would wait for it, element by element
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + rl;
+        float sf[16];
+        int64_t widx[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+          sf[v] = 1.f;
+          widx[v] = -1;
+          if (row < R && col < g.C) {
+            if (row < e.wrows) {
+              int wr = row;
+              if (e.perm_C > 0) {
+                const int kidx = fdiv(row, e.dperm);
+                wr = (row - kidx * e.perm_C) * e.perm_kk2 + kidx;
+              }
+              widx[v] = (int64_t)wr * e.ldw + col;
+              if (e.Sw) sf[v] = e.Sw[widx[v]];
+            } else if (e.Sb) {
+              sf[v] = e.Sb[col];
+            }
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+          if (row < R && col < g.C) {
+            const float sv = sf[v];
+            if (row < e.wrows) {
+              e.om[widx[v]] = sv * accM[i][j][v];
+              e.ov[widx[v]] = (sv * sv) * accV[i][j][v];
+            } else {
+              e.dmb[col] = sv * accM[i][j][v];
+              e.dSb[col] = (sv * sv) * accV[i][j][v];
+            }
           }
         }
       }
