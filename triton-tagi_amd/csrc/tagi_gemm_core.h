@@ -1190,29 +1190,46 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
     const Phase ph = make_phase(e.g, z);
     const int hq = ph.Hq * ph.Wq;
     const FastDiv dhq = make_fastdiv(hq > 0 ? hq : 1), dwq = make_fastdiv(ph.Wq > 0 ? ph.Wq : 1);
+    // With an addend (the shortcut deltas, possibly the output itself), a lane's 16 addends
+    // of a column are loaded before any of its outputs is stored: a load issued after a
+    // store to a possibly aliasing address would wait for it, element by element.
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
+      int64_t pixc[16];  // pixel offset * C, or -1 past the phase's rows
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
         const int n = fdiv(row, dhq), rr = row - n * hq;
         const int hh = fdiv(rr, dwq), ww = rr - hh * ph.Wq;
         const int64_t pix = ((int64_t)n * e.g.H + (hh * e.g.stride + ph.a)) * e.g.W + (ww * e.g.stride + ph.b);
+        pixc[v] = row < R ? pix * e.g.C : -1;
+      }
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int col = n0 + wn * WN + j * 32 + rl;
-          if (row < R && col < g.C) {
-            const int64_t off = pix * e.g.C + col;
-            float m = accM[i][j][v], vv = accV[i][j][v];
-            if (e.am) {
-              m = m + e.am[off];
-              vv = vv + e.av[off];
-            }
-            e.om[off] = m;
-            e.ov[off] = vv;
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + rl;
+        if (col >= g.C) continue;
+        float addm[16], addv[16];
+        if (e.am) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            addm[v] = pixc[v] >= 0 ? e.am[pixc[v] + col] : 0.f;
+            addv[v] = pixc[v] >= 0 ? e.av[pixc[v] + col] : 0.f;
           }
         }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          if (pixc[v] < 0) continue;
+          const int64_t off = pixc[v] + col;
+          float m = accM[i][j][v], vv = accV[i][j][v];
+          if (e.am) {
+            m = m + addm[v];
+            vv = vv + addv[v];
+          }
+          e.om[off] = m;
+          e.ov[off] = vv;
+        }
       }
+    }
   } else if (e.kind == 1) {
     // parameter deltas (unsplit): the Sw (Sb) factors of a lane's 16 outputs are loaded
     // before any of them is stored -- the stores may alias them as far as the compiler
