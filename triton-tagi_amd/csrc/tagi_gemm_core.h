@@ -1046,11 +1046,11 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         if (s + PD < NS) load(s + PD);
-        // the forward product keeps its fragment reads ahead of the MFMAs; the two-product
-        // kernels run 1-3% faster with the compiler's own interleaving
+        // the forward product keeps its fragment reads ahead of the MFMAs (a barrier after
+        // them as well is 0.4% slower); the two-product kernels run 1-3% faster with the
+        // compiler's own interleaving
         if constexpr (PROD == PROD_FWD) __builtin_amdgcn_sched_barrier(0);
         mma(s);
-        if constexpr (PROD == PROD_FWD) __builtin_amdgcn_sched_barrier(0);
         if (s == NS / 2 - 1) {
           mid();
           __builtin_amdgcn_sched_barrier(0);
