@@ -413,7 +413,9 @@ extern "C" int tagi_attn_score_deltas_qk(const float* d_mu, const float* d_var, 
   TAGI_REQUIRE(al16(d_mu) && al16(d_var) && al16(mu_v), "%s: d_mu, d_var and mu_v must be 16-byte aligned", what);
   TAGI_REQUIRE(B * H < 65536 && fits_i32(B * S * H * D) && B * H * S * S < (1ll << 40), "%s: too large", what);
   hipStream_t s = as_stream(stream);
-  ProfScope ps(FAM_BMM_SHARED, s, 2.0 * 4 * B * H * S * S * D, 4.0 * (B * H * S * S + 6 * B * S * H * D));
+  // algorithmic work: this product (2 moments) plus half of the score-delta product (2
+  // moments), which the dQ and dK kernels each form again for their own blocks
+  ProfScope ps(FAM_BMM_SHARED, s, 2.0 * 3 * B * H * S * S * D, 4.0 * (B * H * S * S + 6 * B * S * H * D));
   const dim3 grid((unsigned)cdiv(S, 32), (unsigned)(B * H));
   const int E = (int)(H * D);
 #define TAGI_DQK(HD_, T_)                                                                                      \
