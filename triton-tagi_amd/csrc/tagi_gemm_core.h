@@ -1430,8 +1430,10 @@ struct Plan {
 // fractions, the occupancy factors and the split costs were fitted to a sweep of every
 // tile shape and split count (each plan forced in turn and timed alone) over the
 // ResNet-18, CNN, transformer (including its batched attention products) and Linear
-// microbenchmark GEMMs on MI355X: mean loss against the best measured plan 1.5%. The
-// split counts tried are the swept ones.
+// microbenchmark GEMMs on MI355X: mean loss against the best measured plan 1.5%. (Twice
+// the cost per partial-sum byte, for reductions that share the GPU with the other
+// stream's GEMMs, gives ResNet-18 +0.5% but the CNN's input deltas -20%.) The split
+// counts tried are the swept ones.
 //
 // phase_k (optional, batch entries): per-GEMM reduction lengths when they differ (stride
 // phases of the conv input delta); splits past a GEMM's own length launch no work.
