@@ -81,7 +81,8 @@ class MultiheadAttentionV2(LearnableLayer):
         dev = ma.device
         st = _lib.stream_of(mu_q)
         s = self._scale
-        if S <= 256 and D in (16, 32, 64) and all(t.data_ptr() % 16 == 0 for t in (mu_q, var_q, mu_k, var_k)):
+        if S <= 256 and D in (16, 32, 64) and B * H < 65536 and all(
+                t.data_ptr() % 16 == 0 for t in (mu_q, var_q, mu_k, var_k)):
             # scores and Remax in one kernel; the same values as the two calls below
             mu_score = torch.empty(B, H, S, S, device=dev, dtype=torch.float32)
             var_score, jcb = torch.empty_like(mu_score), torch.empty_like(mu_score)
@@ -130,7 +131,7 @@ class MultiheadAttentionV2(LearnableLayer):
         dq, dSq = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
         dk, dSk = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
         mu_v = c["mu_v"]
-        if S <= 256 and D in (16, 32) and all(t.data_ptr() % 16 == 0 for t in (d_mu, d_var, mu_v)):
+        if S <= 256 and D in (16, 32) and B * H < 65536 and all(t.data_ptr() % 16 == 0 for t in (d_mu, d_var, mu_v)):
             # the scaled score deltas are formed per block in LDS, never in memory
             for x, om, oS, tr in ((c["mu_k"], dq, dSq, 0), (c["mu_q"], dk, dSk, 1)):
                 _lib.call("tagi_attn_score_deltas_qk", d_mu.data_ptr(), d_var.data_ptr(), mu_v.data_ptr(),
