@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define TAGI_ABI_VERSION 2
+#define TAGI_ABI_VERSION 3
 
 enum {
   TAGI_OK = 0,
@@ -175,27 +175,31 @@ int tagi_bmm_shared_jacobian(const float* p0, const float* p1, const float* p2, 
 
 /* The attention scores' moments passed through the Remax in one kernel
  * (multihead_attention.py:174-190: Q K^T by bmm_tagi_var and the scaled mean matmul, then
- * triton_remax over each score row). q/k: (B, S, H*D) projection outputs, head h at columns
- * h*D .. h*D+D-1, 16-byte aligned; outputs mu_a, var_a, J: (B, H, S, S) contiguous. The
- * scores are the ones tagi_bmm_tagi forms (scale, scale_sq applied) and the outputs those
- * of tagi_remax_fwd on them, bit for bit, but the scores never reach memory. Needs
- * S <= 256 and D in {16, 32, 64} (else TAGI_ERR_UNSUPPORTED: use the two calls). */
+ * triton_remax over each score row). q/k: rows of ld_qk floats (batch b, position s at row
+ * b*S + s), head h at columns h*D .. h*D+D-1 from the given pointers (so the Q, K and V
+ * projections may share one (B*S, 3*H*D) buffer), 16-byte aligned, ld_qk % 4 == 0;
+ * outputs mu_a, var_a, J: (B, H, S, S) contiguous. The scores are the ones
+ * tagi_bmm_tagi forms (scale, scale_sq applied) and the outputs those of
+ * tagi_remax_fwd on them, bit for bit, but the scores never reach memory. Needs S <= 256
+ * and D in {16, 32, 64} (else TAGI_ERR_UNSUPPORTED: use the two calls). */
 int tagi_attn_scores_remax(const float* mu_q, const float* var_q, const float* mu_k, const float* var_k,
-                           float* mu_a, float* var_a, float* J, int64_t B, int64_t H, int64_t S, int64_t D,
-                           float scale, float scale_sq, tagi_stream_t stream);
+                           int64_t ld_qk, float* mu_a, float* var_a, float* J, int64_t B, int64_t H, int64_t S,
+                           int64_t D, float scale, float scale_sq, tagi_stream_t stream);
 
 /* The attention's query or key deltas from the output deltas in one kernel
  * (multihead_attention.py:238-251): with scaled = (d_out @ mu_v^T) x J (mean; the variance
  * is (d_var @ (mu_v^2)^T) x J^2, as tagi_bmm_shared_jacobian forms it),
  *   transpose == 0:  out = scale * scaled @ mu_x,   out_var = scale_sq * scaled_var @ mu_x^2  (dQ, mu_x = mu_k)
  *   transpose == 1:  out = scale * scaled^T @ mu_x, ...                                      (dK, mu_x = mu_q)
- * d_mu, d_var, mu_v, mu_x, out: (B, S, H*D), head h at columns h*D ..; J: (B, H, S, S). The
- * scaled deltas are formed per block in LDS and never reach memory. Needs S <= 256,
- * D in {16, 32} and 16-byte aligned d_mu, d_var, mu_v (else TAGI_ERR_UNSUPPORTED: use
- * tagi_bmm_shared_jacobian and tagi_bmm_shared). */
-int tagi_attn_score_deltas_qk(const float* d_mu, const float* d_var, const float* mu_v, const float* J,
-                              const float* mu_x, float* out_mu, float* out_var, int64_t B, int64_t H, int64_t S,
-                              int64_t D, float scale, float scale_sq, int transpose, tagi_stream_t stream);
+ * Rows as in tagi_attn_scores_remax: d_mu, d_var with row stride ld_d, mu_v and mu_x ld_x,
+ * out ld_out (head h at columns h*D ..); J: (B, H, S, S). The scaled deltas are formed
+ * per block in LDS and never reach memory. Needs S <= 256, D in {16, 32}, 16-byte
+ * aligned d_mu, d_var, mu_v and ld_d, ld_x multiples of 4 (else TAGI_ERR_UNSUPPORTED /
+ * TAGI_ERR_ARG: use tagi_bmm_shared_jacobian and tagi_bmm_shared). */
+int tagi_attn_score_deltas_qk(const float* d_mu, const float* d_var, int64_t ld_d, const float* mu_v,
+                              const float* mu_x, int64_t ld_x, const float* J, float* out_mu, float* out_var,
+                              int64_t ld_out, int64_t B, int64_t H, int64_t S, int64_t D, float scale,
+                              float scale_sq, int transpose, tagi_stream_t stream);
 
 /* ------------------------------------------------------------------ Conv2D ---- */
 /* 4-D activations and deltas of the conv path (Conv2D, BatchNorm2D, AvgPool2D) are

@@ -456,8 +456,8 @@ def test_attention_scores_remax_fused_equals_two_calls(dev, B, H, S, D):
               _lib.view(1, S * S, 0, S, 1), sc, sc * sc, st)
     ra, rv, rj = remax(mu_qk.view(-1, S), var_qk.view(-1, S))
     fa, fv, fj = (torch.empty(B, H, S, S, device=dev) for _ in range(3))
-    _lib.call("tagi_attn_scores_remax", mq.data_ptr(), vq.data_ptr(), mk.data_ptr(), vk.data_ptr(), fa.data_ptr(),
-              fv.data_ptr(), fj.data_ptr(), B, H, S, D, sc, sc * sc, st)
+    _lib.call("tagi_attn_scores_remax", mq.data_ptr(), vq.data_ptr(), mk.data_ptr(), vk.data_ptr(), E,
+              fa.data_ptr(), fv.data_ptr(), fj.data_ptr(), B, H, S, D, sc, sc * sc, st)
     for name, got, ref in (("mu_a", fa, ra), ("var_a", fv, rv), ("J", fj, rj)):
         assert torch.equal(got.view(-1, S), ref), f"{name}: fused differs from the two calls"
 
@@ -490,8 +490,8 @@ def test_attention_score_deltas_qk_fused(dev, B, H, S, D):
         _lib.call("tagi_bmm_shared", smu.data_ptr(), svar.data_ptr(), x.data_ptr(), rm.data_ptr(), rS.data_ptr(),
                   B * H, S, S, D, view, hv, hv, sc, sc * sc, 0, st)
         fm, fS = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
-        _lib.call("tagi_attn_score_deltas_qk", dmu.data_ptr(), dvar.data_ptr(), mv.data_ptr(), J.data_ptr(),
-                  x.data_ptr(), fm.data_ptr(), fS.data_ptr(), B, H, S, D, sc, sc * sc, tr, st)
+        _lib.call("tagi_attn_score_deltas_qk", dmu.data_ptr(), dvar.data_ptr(), E, mv.data_ptr(), x.data_ptr(), E,
+                  J.data_ptr(), fm.data_ptr(), fS.data_ptr(), E, B, H, S, D, sc, sc * sc, tr, st)
         # term magnitudes: |scaled| @ |x| per head (the scaled deltas as the two-call path holds them)
         a_m, a_S = smu.abs(), svar.abs()
         if tr:

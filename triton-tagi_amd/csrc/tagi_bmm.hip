@@ -144,6 +144,7 @@ __global__ void __launch_bounds__(512) attn_scores_remax_kernel(const float* __r
                                                                 const float* __restrict__ vk, float* __restrict__ ma,
                                                                 float* __restrict__ Sa, float* __restrict__ Jo, int H,
                                                                 int S, int E, float scale, float scale_sq) {
+  // E: row stride of q and k (their rows hold the heads side by side, head h at h*HD)
   constexpr int NKT = HD / 16;
   __shared__ float sm[2 * 32 * kScoreLd];
   const int z = blockIdx.y;
@@ -240,20 +241,22 @@ __global__ void __launch_bounds__(512) attn_scores_remax_kernel(const float* __r
 }  // namespace
 
 extern "C" int tagi_attn_scores_remax(const float* mu_q, const float* var_q, const float* mu_k, const float* var_k,
-                                      float* mu_a, float* var_a, float* J, int64_t B, int64_t H, int64_t S, int64_t D,
-                                      float scale, float scale_sq, tagi_stream_t stream) {
+                                      int64_t ld_qk, float* mu_a, float* var_a, float* J, int64_t B, int64_t H,
+                                      int64_t S, int64_t D, float scale, float scale_sq, tagi_stream_t stream) {
   const char* what = "tagi_attn_scores_remax";
   TAGI_REQUIRE(mu_q && var_q && mu_k && var_k && mu_a && var_a && J, "%s: null pointer", what);
   TAGI_REQUIRE(B > 0 && H > 0 && S > 0 && D > 0, "%s: bad sizes", what);
   if (S > 256 || !(D == 16 || D == 32 || D == 64))
     return fail(TAGI_ERR_UNSUPPORTED, "%s: needs S <= 256 and head_dim 16, 32 or 64 (S=%lld, D=%lld)", what,
                 (long long)S, (long long)D);
+  TAGI_REQUIRE(ld_qk >= H * D && ld_qk % 4 == 0, "%s: row stride %lld below H*D or not a multiple of 4", what,
+               (long long)ld_qk);
   TAGI_REQUIRE(al16(mu_q) && al16(var_q) && al16(mu_k) && al16(var_k), "%s: q/k must be 16-byte aligned", what);
-  TAGI_REQUIRE(B * H < 65536 && fits_i32(B * S * H * D) && B * H * S * S < (1ll << 40), "%s: too large", what);
+  TAGI_REQUIRE(B * H < 65536 && fits_i32(B * S * ld_qk) && B * H * S * S < (1ll << 40), "%s: too large", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_ATTN_SCORES, s, 2.0 * 3 * B * H * S * S * D, 4.0 * (4 * B * S * H * D + 3 * B * H * S * S));
   const dim3 grid((unsigned)cdiv(S, 32), (unsigned)(B * H));
-  const int E = (int)(H * D);
+  const int E = (int)ld_qk;
   if (D == 16)
     hipLaunchKernelGGL(attn_scores_remax_kernel<16>, grid, dim3(512), 0, s, mu_q, var_q, mu_k, var_k, mu_a, var_a, J,
                        (int)H, (int)S, E, scale, scale_sq);
@@ -282,8 +285,8 @@ template <int HD, bool TRANS>
 __global__ void __launch_bounds__(512, 4) attn_dqk_kernel(const float* __restrict__ dmu, const float* __restrict__ dvar,
                                                        const float* __restrict__ mv, const float* __restrict__ Jg,
                                                        const float* __restrict__ mx, float* __restrict__ omu,
-                                                       float* __restrict__ ovar, int H, int S, int E, float scale,
-                                                       float scale_sq) {
+                                                       float* __restrict__ ovar, int H, int S, int ld_d, int ld_x,
+                                                       int ld_o, float scale, float scale_sq) {
   constexpr int NKT = HD / 16;
   // phase 1-2: [moment][output row][score index]; phase 3: 8 waves x 2 moments x 32 x 32 partials
   __shared__ float sm[2 * 32 * kScoreLd];
@@ -293,7 +296,10 @@ __global__ void __launch_bounds__(512, 4) attn_dqk_kernel(const float* __restric
   const int o0 = blockIdx.x * 32;  // first output row: query (dQ) or key (dK)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hl = lane >> 5, rl = lane & 31;
-  const int64_t hbase = (int64_t)b * S * E + (int64_t)h * HD;
+  // head h of batch b in the output deltas (row stride ld_d), mu_v / mu_x (ld_x), out (ld_o)
+  const int64_t bd = (int64_t)b * S * ld_d + (int64_t)h * HD;
+  const int64_t bx = (int64_t)b * S * ld_x + (int64_t)h * HD;
+  const int64_t bo = (int64_t)b * S * ld_o + (int64_t)h * HD;
   const int64_t jz = (int64_t)z * S * S;
   const bool active = wave * 32 < S;  // this wave's 32 score indices exist
 
@@ -316,12 +322,12 @@ __global__ void __launch_bounds__(512, 4) attn_dqk_kernel(const float* __restric
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x, w = x;
-        const int64_t ko = hbase + 8 * hl + 16 * t + 4 * u;
+        const int ko = 8 * hl + 16 * t + 4 * u;
         if (ai < S) {
-          x = *reinterpret_cast<const float4*>(dmu + ko + (int64_t)ai * E);
-          y = *reinterpret_cast<const float4*>(dvar + ko + (int64_t)ai * E);
+          x = *reinterpret_cast<const float4*>(dmu + bd + ko + (int64_t)ai * ld_d);
+          y = *reinterpret_cast<const float4*>(dvar + bd + ko + (int64_t)ai * ld_d);
         }
-        if (bj < S) w = *reinterpret_cast<const float4*>(mv + ko + (int64_t)bj * E);
+        if (bj < S) w = *reinterpret_cast<const float4*>(mv + bx + ko + (int64_t)bj * ld_x);
         am[t][4 * u + 0] = x.x, am[t][4 * u + 1] = x.y, am[t][4 * u + 2] = x.z, am[t][4 * u + 3] = x.w;
         av[t][4 * u + 0] = y.x, av[t][4 * u + 1] = y.y, av[t][4 * u + 2] = y.z, av[t][4 * u + 3] = y.w;
         bm[t][4 * u + 0] = w.x, bm[t][4 * u + 1] = w.y, bm[t][4 * u + 2] = w.z, bm[t][4 * u + 3] = w.w;
@@ -361,7 +367,7 @@ __global__ void __launch_bounds__(512, 4) attn_dqk_kernel(const float* __restric
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       const int k = 32 * wave + 16 * (q >> 3) + 8 * hl + (q & 7);
-      xr[q] = (k < S && rl < HD) ? mx[hbase + (int64_t)k * E + rl] : 0.f;
+      xr[q] = (k < S && rl < HD) ? mx[bx + (int64_t)k * ld_x + rl] : 0.f;
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -392,7 +398,7 @@ __global__ void __launch_bounds__(512, 4) attn_dqk_kernel(const float* __restric
     float acc = 0.f;
     for (int w = 0; w < nw; ++w) acc += sm[(w * 2 + mom) * 1024 + row * 32 + d];
     if (o0 + row < S && d < HD) {
-      const int64_t o = hbase + (int64_t)(o0 + row) * E + d;
+      const int64_t o = bo + (int64_t)(o0 + row) * ld_o + d;
       if (mom == 0) omu[o] = acc * scale + 0.f;
       else ovar[o] = acc * scale_sq + 0.f;
     }
@@ -400,27 +406,30 @@ __global__ void __launch_bounds__(512, 4) attn_dqk_kernel(const float* __restric
 }
 }  // namespace
 
-extern "C" int tagi_attn_score_deltas_qk(const float* d_mu, const float* d_var, const float* mu_v, const float* J,
-                                         const float* mu_x, float* out_mu, float* out_var, int64_t B, int64_t H,
-                                         int64_t S, int64_t D, float scale, float scale_sq, int transpose,
-                                         tagi_stream_t stream) {
+extern "C" int tagi_attn_score_deltas_qk(const float* d_mu, const float* d_var, int64_t ld_d, const float* mu_v,
+                                         const float* mu_x, int64_t ld_x, const float* J, float* out_mu,
+                                         float* out_var, int64_t ld_out, int64_t B, int64_t H, int64_t S, int64_t D,
+                                         float scale, float scale_sq, int transpose, tagi_stream_t stream) {
   const char* what = "tagi_attn_score_deltas_qk";
   TAGI_REQUIRE(d_mu && d_var && mu_v && J && mu_x && out_mu && out_var, "%s: null pointer", what);
   TAGI_REQUIRE(B > 0 && H > 0 && S > 0 && D > 0, "%s: bad sizes", what);
   if (S > 256 || !(D == 16 || D == 32))
     return fail(TAGI_ERR_UNSUPPORTED, "%s: needs S <= 256 and head_dim 16 or 32 (S=%lld, D=%lld)", what,
                 (long long)S, (long long)D);
+  TAGI_REQUIRE(ld_d >= H * D && ld_x >= H * D && ld_out >= H * D && ld_d % 4 == 0 && ld_x % 4 == 0,
+               "%s: row strides below H*D (or d/x strides not multiples of 4)", what);
   TAGI_REQUIRE(al16(d_mu) && al16(d_var) && al16(mu_v), "%s: d_mu, d_var and mu_v must be 16-byte aligned", what);
-  TAGI_REQUIRE(B * H < 65536 && fits_i32(B * S * H * D) && B * H * S * S < (1ll << 40), "%s: too large", what);
+  TAGI_REQUIRE(B * H < 65536 && fits_i32(B * S * ld_d) && fits_i32(B * S * ld_x) && fits_i32(B * S * ld_out) &&
+                   B * H * S * S < (1ll << 40),
+               "%s: too large", what);
   hipStream_t s = as_stream(stream);
   // algorithmic work: this product (2 moments) plus half of the score-delta product (2
   // moments), which the dQ and dK kernels each form again for their own blocks
   ProfScope ps(FAM_BMM_SHARED, s, 2.0 * 3 * B * H * S * S * D, 4.0 * (B * H * S * S + 6 * B * S * H * D));
   const dim3 grid((unsigned)cdiv(S, 32), (unsigned)(B * H));
-  const int E = (int)(H * D);
 #define TAGI_DQK(HD_, T_)                                                                                      \
   hipLaunchKernelGGL((attn_dqk_kernel<HD_, T_>), grid, dim3(512), 0, s, d_mu, d_var, mu_v, J, mu_x, out_mu, out_var, \
-                     (int)H, (int)S, E, scale, scale_sq)
+                     (int)H, (int)S, (int)ld_d, (int)ld_x, (int)ld_out, scale, scale_sq)
   if (D == 16) {
     if (transpose) TAGI_DQK(16, true);
     else TAGI_DQK(16, false);

@@ -1,7 +1,9 @@
 """Bayesian multi-head self-attention V2 (mirrors triton_tagi/layers/multihead_attention.py:64-294).
 
-Separate Q/K/V Linear projections; heads are read in place from the (B, S, E)
-projection outputs through strided views (no head transposes are materialised):
+Separate Q/K/V Linear projections (three Linear layers holding the parameters), run as
+one product with their weights side by side: the (B*S, 3E) output holds Q, K and V, and
+heads are read in place from it through strided views (no head transposes are
+materialised):
     mu_qk  = s mu_q mu_k^T,  var_qk = s^2 sum (S_q (mu_k^2 + S_k) + mu_q^2 S_k),  s = 1/sqrt(D)
     scores = Remax over the last dim of (mu_qk, var_qk)       -> mu_score, var_score, J
     out    = TAGI product score @ V, written straight into (B, S, E)
@@ -9,18 +11,22 @@ Backward (deterministic operand shared per product):
     dV     = score^T @ d_out          (var: score^2)
     dscore = d_out @ mu_v^T           (var: mu_v^2), then * J and * J^2
     dQ     = s dscore @ mu_k,  dK = s dscore^T @ mu_q   (var: s^2, squared operand)
-and the three projection backwards are summed.
+and the three projection backwards are summed: one input-delta product over the (B*S, 3E)
+deltas of Q, K and V, one parameter-delta product whose (E, 3E) result is split into the
+three layers' deltas.
 """
 
 from __future__ import annotations
 
+import contextlib
 import math
 
 import torch
 from torch import Tensor
 
-from .. import _lib
+from .. import _lib, _overlap
 from ..base import LearnableLayer
+from ..kernels.common import fused_backward_delta, linear_forward, linear_param_deltas
 from .linear import Linear
 from .remax import remax
 
@@ -61,50 +67,68 @@ class MultiheadAttentionV2(LearnableLayer):
         self._attn_mu: Tensor | None = None
         self._attn_var: Tensor | None = None
 
-    # views of a (B, S, E) tensor as (B*H, S, D) heads, and of (B, H, S, S) scores
-    def _head_view(self, S: int, transpose: bool = False):
-        E, D, H = self.embed_dim, self.head_dim, self.num_heads
-        return _lib.view(H, S * E, D, 1, E) if transpose else _lib.view(H, S * E, D, E, 1)
+    # views of a (B, S, ld) tensor as (B*H, S, D) heads (row stride ld; the Q/K/V
+    # projections live side by side in one (B*S, 3E) buffer), and of (B, H, S, S) scores
+    def _head_view(self, S: int, transpose: bool = False, ld: int | None = None):
+        D, H = self.head_dim, self.num_heads
+        ld = self.embed_dim if ld is None else ld
+        return _lib.view(H, S * ld, D, 1, ld) if transpose else _lib.view(H, S * ld, D, ld, 1)
 
     @staticmethod
     def _score_view(S: int, transpose: bool = False):
         return _lib.view(1, S * S, 0, 1, S) if transpose else _lib.view(1, S * S, 0, S, 1)
+
+    def _projections(self):
+        return (self.q_proj, self.k_proj, self.v_proj)
 
     def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
         B, S, E = ma.shape
         if E != self.embed_dim:
             raise ValueError(f"Expected last dim {self.embed_dim}, got {E}")
         H, D = self.num_heads, self.head_dim
-        mu_q, var_q = self.q_proj.forward(ma, Sa)
-        mu_k, var_k = self.k_proj.forward(ma, Sa)
-        mu_v, var_v = self.v_proj.forward(ma, Sa)
+        # Q, K and V (multihead_attention.py:160-172) as one product with the three weight
+        # matrices side by side: the same values as three projections, one pass over the input
+        ma_flat = ma.reshape(-1, E).contiguous()
+        Sa_flat = Sa.reshape(-1, E).contiguous()
+        projs = self._projections()
+        w_m = torch.cat([p.mw for p in projs], 1)
+        w_S = torch.cat([p.Sw for p in projs], 1)
+        b_m = torch.cat([p.mb for p in projs], 1) if self.has_bias else None
+        b_S = torch.cat([p.Sb for p in projs], 1) if self.has_bias else None
+        qkv_m, qkv_S = linear_forward(ma_flat, Sa_flat, w_m, w_S, b_m, b_S)
+        for p in projs:
+            p.ma_in, p._input_shape = ma_flat, ma.shape
+        L = 3 * E
+        f4 = 4  # bytes per float
+        q_m, q_S = qkv_m.data_ptr(), qkv_S.data_ptr()
+        k_m, k_S = q_m + E * f4, q_S + E * f4
+        v_m, v_S = q_m + 2 * E * f4, q_S + 2 * E * f4
         dev = ma.device
-        st = _lib.stream_of(mu_q)
+        st = _lib.stream_of(qkv_m)
         s = self._scale
-        if S <= 256 and D in (16, 32, 64) and B * H < 65536 and all(
-                t.data_ptr() % 16 == 0 for t in (mu_q, var_q, mu_k, var_k)):
+        if S <= 256 and D in (16, 32, 64) and B * H < 65536 and L % 4 == 0 and q_m % 16 == 0 and q_S % 16 == 0:
             # scores and Remax in one kernel; the same values as the two calls below
             mu_score = torch.empty(B, H, S, S, device=dev, dtype=torch.float32)
             var_score, jcb = torch.empty_like(mu_score), torch.empty_like(mu_score)
-            _lib.call("tagi_attn_scores_remax", mu_q.data_ptr(), var_q.data_ptr(), mu_k.data_ptr(),
-                      var_k.data_ptr(), mu_score.data_ptr(), var_score.data_ptr(), jcb.data_ptr(), B, H, S, D,
-                      s, s * s, st)
+            _lib.call("tagi_attn_scores_remax", q_m, q_S, k_m, k_S, L, mu_score.data_ptr(), var_score.data_ptr(),
+                      jcb.data_ptr(), B, H, S, D, s, s * s, st)
         else:
             mu_qk = torch.empty(B, H, S, S, device=dev, dtype=torch.float32)
             var_qk = torch.empty_like(mu_qk)
-            _lib.call("tagi_bmm_tagi", mu_q.data_ptr(), var_q.data_ptr(), mu_k.data_ptr(), var_k.data_ptr(),
-                      mu_qk.data_ptr(), var_qk.data_ptr(), B * H, S, D, S, self._head_view(S),
-                      self._head_view(S, transpose=True), self._score_view(S), s, s * s, st)
+            _lib.call("tagi_bmm_tagi", q_m, q_S, k_m, k_S, mu_qk.data_ptr(), var_qk.data_ptr(), B * H, S, D, S,
+                      self._head_view(S, ld=L), self._head_view(S, transpose=True, ld=L), self._score_view(S), s,
+                      s * s, st)
             mu_score, var_score, jcb = remax(mu_qk.view(B * H * S, S), var_qk.view(B * H * S, S))
             mu_score = mu_score.view(B, H, S, S)
             var_score = var_score.view(B, H, S, S)
             jcb = jcb.view(B, H, S, S)
         mu_out = torch.empty(B, S, E, device=dev, dtype=torch.float32)
         var_out = torch.empty_like(mu_out)
-        _lib.call("tagi_bmm_tagi", mu_score.data_ptr(), var_score.data_ptr(), mu_v.data_ptr(), var_v.data_ptr(),
-                  mu_out.data_ptr(), var_out.data_ptr(), B * H, S, S, D, self._score_view(S), self._head_view(S),
+        _lib.call("tagi_bmm_tagi", mu_score.data_ptr(), var_score.data_ptr(), v_m, v_S, mu_out.data_ptr(),
+                  var_out.data_ptr(), B * H, S, S, D, self._score_view(S), self._head_view(S, ld=L),
                   self._head_view(S), 1.0, 1.0, st)
-        self._cache = dict(B=B, S=S, H=H, D=D, mu_q=mu_q, mu_k=mu_k, mu_v=mu_v, mu_score=mu_score, jcb=jcb)
+        self._cache = dict(B=B, S=S, H=H, D=D, qkv_m=qkv_m, ma_in=ma_flat, w_m=w_m, w_S=w_S, b_S=b_S,
+                           mu_score=mu_score, jcb=jcb)
         self._attn_mu = mu_score
         self._attn_var = var_score
         return mu_out, var_out
@@ -113,45 +137,64 @@ class MultiheadAttentionV2(LearnableLayer):
         c = self._cache
         B, S, H, D = c["B"], c["S"], c["H"], c["D"]
         E = self.embed_dim
+        L = 3 * E
+        f4 = 4
         s = self._scale
         d_mu = _lib.check(delta_mz.reshape(B, S, E).contiguous(), "delta_mz")
         d_var = _lib.check(delta_Sz.reshape(B, S, E).contiguous(), "delta_Sz")
         dev = d_mu.device
         st = _lib.stream_of(d_mu)
-        hv, hvt, sv, svt = self._head_view(S), self._head_view(S, True), self._score_view(S), self._score_view(S, True)
+        hv, sv, svt = self._head_view(S), self._score_view(S), self._score_view(S, True)
+        hL, hLt = self._head_view(S, ld=L), self._head_view(S, True, ld=L)
+        qkv = c["qkv_m"]
+        q_m, k_m, v_m = qkv.data_ptr(), qkv.data_ptr() + E * f4, qkv.data_ptr() + 2 * E * f4
+        # the deltas of Q, K and V side by side, (B*S, 3E), for one projection backward
+        dqkv_m = torch.empty(B * S, L, device=dev)
+        dqkv_S = torch.empty(B * S, L, device=dev)
+        dq_m, dq_S = dqkv_m.data_ptr(), dqkv_S.data_ptr()
+        dk_m, dk_S = dq_m + E * f4, dq_S + E * f4
+        dv_m, dv_S = dq_m + 2 * E * f4, dq_S + 2 * E * f4
         # dV = score^T @ d_out (score shared on the left)
-        dv, dSv = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
-        _lib.call("tagi_bmm_shared", d_mu.data_ptr(), d_var.data_ptr(), c["mu_score"].data_ptr(), dv.data_ptr(),
-                  dSv.data_ptr(), B * H, S, S, D, svt, hv, hv, 1.0, 1.0, 1, st)
+        _lib.call("tagi_bmm_shared", d_mu.data_ptr(), d_var.data_ptr(), c["mu_score"].data_ptr(), dv_m, dv_S,
+                  B * H, S, S, D, svt, hv, hL, 1.0, 1.0, 1, st)
         # dscore = d_out @ mu_v^T (mu_v shared on the right), times the Remax Jacobian
         # (multihead_attention.py:239-243); dQ = s scaled @ mu_k ; dK = s scaled^T @ mu_q
         jcb = _lib.check(c["jcb"], "jcb")
         if tuple(jcb.shape) != (B, H, S, S):
             raise ValueError(f"MultiheadAttentionV2: stored Remax Jacobian {tuple(jcb.shape)} vs {(B, H, S, S)}")
-        dq, dSq = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
-        dk, dSk = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
-        mu_v = c["mu_v"]
-        if S <= 256 and D in (16, 32) and B * H < 65536 and all(t.data_ptr() % 16 == 0 for t in (d_mu, d_var, mu_v)):
+        if S <= 256 and D in (16, 32) and B * H < 65536 and all(
+                t.data_ptr() % 16 == 0 for t in (d_mu, d_var, qkv)):
             # the scaled score deltas are formed per block in LDS, never in memory
-            for x, om, oS, tr in ((c["mu_k"], dq, dSq, 0), (c["mu_q"], dk, dSk, 1)):
-                _lib.call("tagi_attn_score_deltas_qk", d_mu.data_ptr(), d_var.data_ptr(), mu_v.data_ptr(),
-                          jcb.data_ptr(), _lib.check(x, "mu_x").data_ptr(), om.data_ptr(), oS.data_ptr(), B, H, S, D,
-                          s, s * s, tr, st)
+            for x, om, oS, tr in ((k_m, dq_m, dq_S, 0), (q_m, dk_m, dk_S, 1)):
+                _lib.call("tagi_attn_score_deltas_qk", d_mu.data_ptr(), d_var.data_ptr(), E, v_m, x, L,
+                          jcb.data_ptr(), om, oS, L, B, H, S, D, s, s * s, tr, st)
         else:
             scaled_mu = torch.empty(B, H, S, S, device=dev)
             scaled_var = torch.empty_like(scaled_mu)
-            _lib.call("tagi_bmm_shared_jacobian", d_mu.data_ptr(), d_var.data_ptr(), mu_v.data_ptr(),
-                      jcb.data_ptr(), scaled_mu.data_ptr(), scaled_var.data_ptr(), B * H, S, D, S, hv, hvt, sv, 1.0,
-                      1.0, 0, st)
-            _lib.call("tagi_bmm_shared", scaled_mu.data_ptr(), scaled_var.data_ptr(), c["mu_k"].data_ptr(),
-                      dq.data_ptr(), dSq.data_ptr(), B * H, S, S, D, sv, hv, hv, s, s * s, 0, st)
-            _lib.call("tagi_bmm_shared", scaled_mu.data_ptr(), scaled_var.data_ptr(), c["mu_q"].data_ptr(),
-                      dk.data_ptr(), dSk.data_ptr(), B * H, S, S, D, svt, hv, hv, s, s * s, 0, st)
-        # the projections' input deltas summed in the GEMM epilogues: (q + k) + v
-        d_ma_q, d_Sa_q = self.q_proj.backward(dq, dSq)
-        self.k_proj._backward(dk, dSk, True, add=(d_ma_q, d_Sa_q))
-        self.v_proj._backward(dv, dSv, True, add=(d_ma_q, d_Sa_q))
-        return d_ma_q, d_Sa_q
+            _lib.call("tagi_bmm_shared_jacobian", d_mu.data_ptr(), d_var.data_ptr(), v_m, jcb.data_ptr(),
+                      scaled_mu.data_ptr(), scaled_var.data_ptr(), B * H, S, D, S, hv, hLt, sv, 1.0, 1.0, 0, st)
+            _lib.call("tagi_bmm_shared", scaled_mu.data_ptr(), scaled_var.data_ptr(), k_m, dq_m, dq_S, B * H, S, S,
+                      D, sv, hL, hL, s, s * s, 0, st)
+            _lib.call("tagi_bmm_shared", scaled_mu.data_ptr(), scaled_var.data_ptr(), q_m, dk_m, dk_S, B * H, S, S,
+                      D, svt, hL, hL, s, s * s, 0, st)
+        # the three projections' parameter deltas in one product (on the side stream within
+        # a step when large), their input deltas in one product over the 3E deltas
+        # (the sum of the three projections' input deltas, multihead_attention.py:262-267)
+        projs = self._projections()
+        ma_in = c["ma_in"]
+        ctx = _overlap.active()
+        big = ma_in.shape[0] * E * L >= _overlap.MIN_MACS_LINEAR
+        side = ctx.fork(dev, ma_in, dqkv_m, dqkv_S, c["w_S"], c["b_S"]) if ctx is not None and big else None
+        with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
+            dmw, dSw, dmb, dSb = linear_param_deltas(ma_in, dqkv_m, dqkv_S, c["w_S"], c["b_S"])
+            for i, p in enumerate(projs):
+                p.delta_mw = dmw[:, i * E:(i + 1) * E].contiguous()
+                p.delta_Sw = dSw[:, i * E:(i + 1) * E].contiguous()
+                if self.has_bias:
+                    p.delta_mb = dmb[:, i * E:(i + 1) * E].contiguous()
+                    p.delta_Sb = dSb[:, i * E:(i + 1) * E].contiguous()
+        dma, dSa = fused_backward_delta(dqkv_m, dqkv_S, c["w_m"])
+        return dma.reshape(B, S, E), dSa.reshape(B, S, E)
 
     def _update_items(self):
         return self.q_proj._update_items() + self.k_proj._update_items() + self.v_proj._update_items()
