@@ -186,6 +186,22 @@ int tagi_attn_scores_remax(const float* mu_q, const float* var_q, const float* m
                            int64_t ld_qk, float* mu_a, float* var_a, float* J, int64_t B, int64_t H, int64_t S,
                            int64_t D, float scale, float scale_sq, tagi_stream_t stream);
 
+/* The attention forward of one layer in one kernel (multihead_attention.py:174-193): the
+ * scores and their Remax as tagi_attn_scores_remax forms them (bit for bit), then
+ *   out = mu_a @ mu_v,   out_var = mu_a^2 @ var_v + var_a @ (mu_v^2 + var_v)
+ * (the score @ V TAGI product of tagi_bmm_tagi with scale 1), written into out_m / out_S:
+ * rows of ld_out floats (batch b, position s at row b*S + s), head h at columns h*D ...
+ * q/k/v as in tagi_attn_scores_remax (row stride ld_qkv; v needs no alignment). mu_a and J
+ * (B, H, S, S) are written for the backward pass; var_a may be NULL (then the score
+ * variances never reach memory; tagi_attn_scores_remax rebuilds them). Needs S <= 256
+ * and D in {16, 32} (else TAGI_ERR_UNSUPPORTED: use tagi_attn_scores_remax and
+ * tagi_bmm_tagi). The score @ V sums run in another order than tagi_bmm_tagi's (per
+ * 32-key stretch, then over the stretches), so out / out_var agree with it to rounding. */
+int tagi_attn_fwd(const float* mu_q, const float* var_q, const float* mu_k, const float* var_k, const float* mu_v,
+                  const float* var_v, int64_t ld_qkv, float* mu_a, float* var_a, float* J, float* out_m,
+                  float* out_S, int64_t ld_out, int64_t B, int64_t H, int64_t S, int64_t D, float scale,
+                  float scale_sq, tagi_stream_t stream);
+
 /* The attention's query or key deltas from the output deltas in one kernel
  * (multihead_attention.py:238-251): with scaled = (d_out @ mu_v^T) x J (mean; the variance
  * is (d_var @ (mu_v^2)^T) x J^2, as tagi_bmm_shared_jacobian forms it),

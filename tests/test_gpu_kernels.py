@@ -462,6 +462,54 @@ def test_attention_scores_remax_fused_equals_two_calls(dev, B, H, S, D):
         assert torch.equal(got.view(-1, S), ref), f"{name}: fused differs from the two calls"
 
 
+@pytest.mark.parametrize("B,H,S,D", [(2, 8, 256, 32), (1, 2, 40, 16), (2, 2, 100, 32), (1, 3, 1, 32),
+                                     (1, 4, 250, 16)])
+def test_attention_fwd_fused(dev, B, H, S, D):
+    """tagi_attn_fwd (scores, Remax and score @ V in one kernel) on Q/K/V read from one
+    (B*S, 3E) buffer: mu_a, var_a and J equal tagi_attn_scores_remax's bit for bit, with or
+    without var_a requested; the output equals tagi_bmm_tagi's score @ V on those scores to
+    1e-5 of the sum of its terms' magnitudes (the sum over keys runs per 32-key stretch, then
+    over the stretches)."""
+    import math
+
+    from triton_tagi_amd import _lib
+
+    r = g(11 * S + D + H)
+    E = H * D
+    L = 3 * E
+    qkv_m = torch.randn(B * S, L, generator=r).to(dev)
+    qkv_S = (0.1 * torch.rand(B * S, L, generator=r) + 0.01).to(dev)
+    q_m, q_S = qkv_m.data_ptr(), qkv_S.data_ptr()
+    k_m, k_S, v_m, v_S = q_m + 4 * E, q_S + 4 * E, q_m + 8 * E, q_S + 8 * E
+    sc = 1.0 / math.sqrt(D)
+    st = _lib.stream_of(qkv_m)
+    ra, rv, rj = (torch.empty(B, H, S, S, device=dev) for _ in range(3))
+    _lib.call("tagi_attn_scores_remax", q_m, q_S, k_m, k_S, L, ra.data_ptr(), rv.data_ptr(), rj.data_ptr(), B, H, S,
+              D, sc, sc * sc, st)
+    rm, rS = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
+    hL = _lib.view(H, S * L, D, L, 1)
+    _lib.call("tagi_bmm_tagi", ra.data_ptr(), rv.data_ptr(), v_m, v_S, rm.data_ptr(), rS.data_ptr(), B * H, S, S, D,
+              _lib.view(1, S * S, 0, S, 1), hL, _lib.view(H, S * E, D, E, 1), 1.0, 1.0, st)
+    outs = []
+    for keep_var in (True, False):
+        fa, fv, fj = (torch.full((B, H, S, S), 7.0, device=dev) for _ in range(3))
+        fm, fS = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
+        _lib.call("tagi_attn_fwd", q_m, q_S, k_m, k_S, v_m, v_S, L, fa.data_ptr(), fv.data_ptr() if keep_var else None,
+                  fj.data_ptr(), fm.data_ptr(), fS.data_ptr(), E, B, H, S, D, sc, sc * sc, st)
+        assert torch.equal(fa, ra) and torch.equal(fj, rj), "mu_a / J differ from tagi_attn_scores_remax"
+        if keep_var:
+            assert torch.equal(fv, rv), "var_a differs from tagi_attn_scores_remax"
+        else:
+            assert bool((fv == 7.0).all()), "var_a written although not requested"
+        outs.append((fm, fS))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    fm, fS = outs[0]
+    vm = qkv_m[:, 2 * E:].reshape(B, S, H, D).permute(0, 2, 1, 3).contiguous()
+    tm = torch.matmul(ra.abs(), vm.abs()).permute(0, 2, 1, 3).reshape(B, S, E)
+    assert_scaled_close(fm, rm, tm, 1e-5, 1e-7, "out mean")
+    assert_scaled_close(fS, rS, rS, 1e-5, 1e-7, "out var")
+
+
 @pytest.mark.parametrize("B,H,S,D", [(2, 8, 256, 32), (1, 2, 40, 16), (2, 2, 100, 32), (1, 3, 1, 32)])
 def test_attention_score_deltas_qk_fused(dev, B, H, S, D):
     """tagi_attn_score_deltas_qk (the Jacobian-scaled score deltas formed per block in LDS,

@@ -136,24 +136,17 @@ extern "C" int tagi_bmm_shared_jacobian(const float* p0, const float* p1, const 
 // Remax to rows 4w .. 4w + 3 of the block.
 namespace {
 constexpr int kScoreLd = 257;  // padded LDS row (S <= 256): conflict-free row reads
+constexpr int kScorePlane = 32 * kScoreLd;
 
+// Scores of query rows r0 .. r0+31 of head (b, h) against all S keys into sm: means in
+// rows 0..31, variances in rows 32..63 (row stride kScoreLd). hbase: offset of the head's
+// first element plus the lane half's 8 reduction indices; E: row stride of q and k.
 template <int HD>
-__global__ void __launch_bounds__(512) attn_scores_remax_kernel(const float* __restrict__ mq,
-                                                                const float* __restrict__ vq,
-                                                                const float* __restrict__ mk,
-                                                                const float* __restrict__ vk, float* __restrict__ ma,
-                                                                float* __restrict__ Sa, float* __restrict__ Jo, int H,
-                                                                int S, int E, float scale, float scale_sq) {
-  // E: row stride of q and k (their rows hold the heads side by side, head h at h*HD)
+__device__ __forceinline__ void attn_scores_to_lds(const float* __restrict__ mq, const float* __restrict__ vq,
+                                                   const float* __restrict__ mk, const float* __restrict__ vk,
+                                                   float* sm, int64_t hbase, int r0, int S, int E, float scale,
+                                                   float scale_sq, int wave, int hl, int rl) {
   constexpr int NKT = HD / 16;
-  __shared__ float sm[2 * 32 * kScoreLd];
-  const int z = blockIdx.y;
-  const int b = z / H, h = z - b * H;
-  const int r0 = blockIdx.x * 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int hl = lane >> 5, rl = lane & 31;
-  const int64_t hbase = (int64_t)b * S * E + (int64_t)h * HD + 8 * hl;
-
   // query row r0 + rl: the lane's 8 reduction indices of each k-tile
   float aq[NKT][8], av[NKT][8];
   {
@@ -172,46 +165,51 @@ __global__ void __launch_bounds__(512) attn_scores_remax_kernel(const float* __r
         av[t][4 * u + 0] = y.x, av[t][4 * u + 1] = y.y, av[t][4 * u + 2] = y.z, av[t][4 * u + 3] = y.w;
       }
   }
-  if (wave * 32 < S) {  // column tiles past S are neither formed nor read
-    const int j = wave;
-    const int kn = j * 32 + rl;  // key row
-    float bm[NKT][8], bv[NKT][8];
+  if (wave * 32 >= S) return;  // column tiles past S are neither formed nor read
+  const int kn = wave * 32 + rl;  // key row
+  float bm[NKT][8], bv[NKT][8];
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
+  for (int t = 0; t < NKT; ++t)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
-        if (kn < S) {
-          const int64_t o = hbase + (int64_t)kn * E + 16 * t + 4 * u;
-          x = *reinterpret_cast<const float4*>(mk + o);
-          y = *reinterpret_cast<const float4*>(vk + o);
-        }
-        bm[t][4 * u + 0] = x.x, bm[t][4 * u + 1] = x.y, bm[t][4 * u + 2] = x.z, bm[t][4 * u + 3] = x.w;
-        bv[t][4 * u + 0] = y.x, bv[t][4 * u + 1] = y.y, bv[t][4 * u + 2] = y.z, bv[t][4 * u + 3] = y.w;
+    for (int u = 0; u < 2; ++u) {
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+      if (kn < S) {
+        const int64_t o = hbase + (int64_t)kn * E + 16 * t + 4 * u;
+        x = *reinterpret_cast<const float4*>(mk + o);
+        y = *reinterpret_cast<const float4*>(vk + o);
       }
-    floatx16 accM, accV;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) accM[v] = accV[v] = 0.f;
-#pragma unroll
-    for (int t = 0; t < NKT; ++t)
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const float a0 = aq[t][s], a1 = av[t][s], b0 = bm[t][s], b1 = bv[t][s];
-        const float asq = a0 * a0, bvar = b0 * b0 + b1;
-        accM = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, accM, 0, 0, 0);
-        accV = __builtin_amdgcn_mfma_f32_32x32x2f32(asq, b1, accV, 0, 0, 0);
-        accV = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, bvar, accV, 0, 0, 0);
-      }
-    // accumulator v of lane l: row 8(v/4) + 4hl + v%4, column j*32 + rl (scaled as the
-    // batched product's epilogue does)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int row = 8 * (v >> 2) + 4 * hl + (v & 3);
-      sm[row * kScoreLd + kn] = accM[v] * scale + 0.f;
-      sm[32 * kScoreLd + row * kScoreLd + kn] = accV[v] * scale_sq + 0.f;
+      bm[t][4 * u + 0] = x.x, bm[t][4 * u + 1] = x.y, bm[t][4 * u + 2] = x.z, bm[t][4 * u + 3] = x.w;
+      bv[t][4 * u + 0] = y.x, bv[t][4 * u + 1] = y.y, bv[t][4 * u + 2] = y.z, bv[t][4 * u + 3] = y.w;
     }
+  floatx16 accM, accV;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) accM[v] = accV[v] = 0.f;
+#pragma unroll
+  for (int t = 0; t < NKT; ++t)
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const float a0 = aq[t][s], a1 = av[t][s], b0 = bm[t][s], b1 = bv[t][s];
+      const float asq = a0 * a0, bvar = b0 * b0 + b1;
+      accM = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, accM, 0, 0, 0);
+      accV = __builtin_amdgcn_mfma_f32_32x32x2f32(asq, b1, accV, 0, 0, 0);
+      accV = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, bvar, accV, 0, 0, 0);
+    }
+  // accumulator v of lane l: row 8(v/4) + 4hl + v%4, column j*32 + rl (scaled as the
+  // batched product's epilogue does); columns kn >= S hold zeros
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int row = 8 * (v >> 2) + 4 * hl + (v & 3);
+    sm[row * kScoreLd + kn] = accM[v] * scale + 0.f;
+    sm[kScorePlane + row * kScoreLd + kn] = accV[v] * scale_sq + 0.f;
   }
-  __syncthreads();
+}
+
+// The Remax of rows 4w .. 4w+3 of the block (wave w), written to mu_a / J (and var_a
+// when non-null) at (z, r0 + row); with BACK, mu_a and var_a also replace the scores in LDS.
+template <bool BACK>
+__device__ __forceinline__ void attn_remax_rows(float* sm, float* __restrict__ ma, float* __restrict__ Sa,
+                                                float* __restrict__ Jo, int64_t z, int r0, int S, int wave,
+                                                int lane) {
 #pragma unroll 1
   for (int rr = 0; rr < 4; ++rr) {
     const int row = wave * 4 + rr;
@@ -223,18 +221,127 @@ __global__ void __launch_bounds__(512) attn_scores_remax_kernel(const float* __r
       const int c = lane + 64 * e;
       const bool ok = c < S;
       m[e] = ok ? sm[row * kScoreLd + c] : 0.f;
-      v[e] = ok ? sm[32 * kScoreLd + row * kScoreLd + c] : 1.f;
+      v[e] = ok ? sm[kScorePlane + row * kScoreLd + c] : 1.f;
     }
     remax_row<4>(m, v, lane, S, oa, os, oj);
-    const int64_t ob = ((int64_t)z * S + i) * S;
+    const int64_t ob = (z * S + i) * S;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int c = lane + 64 * e;
       if (c < S) {
         ma[ob + c] = oa[e];
-        Sa[ob + c] = os[e];
+        if (Sa) Sa[ob + c] = os[e];
         Jo[ob + c] = oj[e];
+        if constexpr (BACK) {
+          sm[row * kScoreLd + c] = oa[e];
+          sm[kScorePlane + row * kScoreLd + c] = os[e];
+        }
       }
+    }
+  }
+}
+
+template <int HD>
+__global__ void __launch_bounds__(512) attn_scores_remax_kernel(const float* __restrict__ mq,
+                                                                const float* __restrict__ vq,
+                                                                const float* __restrict__ mk,
+                                                                const float* __restrict__ vk, float* __restrict__ ma,
+                                                                float* __restrict__ Sa, float* __restrict__ Jo, int H,
+                                                                int S, int E, float scale, float scale_sq) {
+  // E: row stride of q and k (their rows hold the heads side by side, head h at h*HD)
+  __shared__ float sm[2 * kScorePlane];
+  const int z = blockIdx.y;
+  const int b = z / H, h = z - b * H;
+  const int r0 = blockIdx.x * 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, rl = lane & 31;
+  const int64_t hbase = (int64_t)b * S * E + (int64_t)h * HD + 8 * hl;
+  attn_scores_to_lds<HD>(mq, vq, mk, vk, sm, hbase, r0, S, E, scale, scale_sq, wave, hl, rl);
+  __syncthreads();
+  attn_remax_rows<false>(sm, ma, Sa, Jo, z, r0, S, wave, lane);
+}
+
+// Scores, Remax and the score @ V product (multihead_attention.py:174-193) in one kernel
+// for head dimensions up to 32: after the Remax, mu_a and var_a of the block's 32 rows sit
+// in LDS and each wave multiplies its 32 keys' stretch of them by V (the TAGI product:
+// mean mu_a mu_v, variance mu_a^2 S_v + S_a (mu_v^2 + S_v), MFMA k-step s taking key
+// 32w + 2s + hl); the 8 partial 32 x 32 tiles are summed through LDS in wave order and
+// written into the (B, S, ld_out) output at column h*HD. mu_a and J are written for the
+// backward pass, var_a only when requested (the raw scores and var_a otherwise never
+// reach HBM, and score @ V reads nothing of the S x S tensors back).
+template <int HD>
+__global__ void __launch_bounds__(512) attn_fwd_kernel(const float* __restrict__ mq, const float* __restrict__ vq,
+                                                       const float* __restrict__ mk, const float* __restrict__ vk,
+                                                       const float* __restrict__ mv, const float* __restrict__ vv,
+                                                       float* __restrict__ ma, float* __restrict__ Sa,
+                                                       float* __restrict__ Jo, float* __restrict__ om,
+                                                       float* __restrict__ oS, int H, int S, int E, int ldo,
+                                                       float scale, float scale_sq) {
+  static_assert(HD <= 32, "one 32-column MFMA tile per head");
+  __shared__ float sm[2 * kScorePlane];
+  const int z = blockIdx.y;
+  const int b = z / H, h = z - b * H;
+  const int r0 = blockIdx.x * 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, rl = lane & 31;
+  const int64_t hbase = (int64_t)b * S * E + (int64_t)h * HD + 8 * hl;
+  attn_scores_to_lds<HD>(mq, vq, mk, vk, sm, hbase, r0, S, E, scale, scale_sq, wave, hl, rl);
+  __syncthreads();
+  attn_remax_rows<true>(sm, ma, Sa, Jo, z, r0, S, wave, lane);
+  __syncthreads();
+  // score @ V over keys kb .. kb+31; LDS columns kb .. 32*ceil(S/32)-1 past S hold zeros
+  // (scores formed from zero keys, left untouched by the Remax) and V reads as zero there
+  const int kb = 32 * wave;
+  floatx16 accM, accV;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) accM[v] = accV[v] = 0.f;
+  if (kb < S) {
+    const int64_t vbase = (int64_t)b * S * E + (int64_t)h * HD + rl;
+    float bm[16], bv[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int key = kb + 2 * s + hl;
+      const bool ok = key < S && rl < HD;
+      bm[s] = ok ? mv[vbase + (int64_t)key * E] : 0.f;
+      bv[s] = ok ? vv[vbase + (int64_t)key * E] : 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int key = kb + 2 * s + hl;
+      const float a0 = sm[rl * kScoreLd + key], a1 = sm[kScorePlane + rl * kScoreLd + key];
+      const float b0 = bm[s], b1 = bv[s];
+      const float asq = a0 * a0, bvar = b0 * b0 + b1;
+      accM = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, accM, 0, 0, 0);
+      accV = __builtin_amdgcn_mfma_f32_32x32x2f32(asq, b1, accV, 0, 0, 0);
+      accV = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, bvar, accV, 0, 0, 0);
+    }
+  }
+  __syncthreads();  // every wave is done reading the scores
+  float* red = sm;  // [wave][mean, variance][32 x 32]
+  if (kb < S) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int o = (8 * (v >> 2) + 4 * hl + (v & 3)) * 32 + rl;
+      red[wave * 2048 + o] = accM[v];
+      red[wave * 2048 + 1024 + o] = accV[v];
+    }
+  }
+  __syncthreads();
+  const int nw = min(8, (S + 31) / 32);
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int o = threadIdx.x + 512 * q;
+    const int row = o >> 5, col = o & 31;
+    float m = 0.f, v = 0.f;
+    for (int w = 0; w < nw; ++w) {
+      m += red[w * 2048 + o];
+      v += red[w * 2048 + 1024 + o];
+    }
+    const int i = r0 + row;
+    if (i < S && col < HD) {
+      const int64_t off = ((int64_t)b * S + i) * ldo + (int64_t)h * HD + col;
+      om[off] = m;
+      oS[off] = v;
     }
   }
 }
@@ -266,6 +373,36 @@ extern "C" int tagi_attn_scores_remax(const float* mu_q, const float* var_q, con
   else
     hipLaunchKernelGGL(attn_scores_remax_kernel<64>, grid, dim3(512), 0, s, mu_q, var_q, mu_k, var_k, mu_a, var_a, J,
                        (int)H, (int)S, E, scale, scale_sq);
+  return check_launch(what);
+}
+
+extern "C" int tagi_attn_fwd(const float* mu_q, const float* var_q, const float* mu_k, const float* var_k,
+                             const float* mu_v, const float* var_v, int64_t ld_qkv, float* mu_a, float* var_a,
+                             float* J, float* out_m, float* out_S, int64_t ld_out, int64_t B, int64_t H, int64_t S,
+                             int64_t D, float scale, float scale_sq, tagi_stream_t stream) {
+  const char* what = "tagi_attn_fwd";
+  TAGI_REQUIRE(mu_q && var_q && mu_k && var_k && mu_v && var_v && mu_a && J && out_m && out_S, "%s: null pointer",
+               what);
+  TAGI_REQUIRE(B > 0 && H > 0 && S > 0 && D > 0, "%s: bad sizes", what);
+  if (S > 256 || !(D == 16 || D == 32))
+    return fail(TAGI_ERR_UNSUPPORTED, "%s: needs S <= 256 and head_dim 16 or 32 (S=%lld, D=%lld)", what, (long long)S,
+                (long long)D);
+  TAGI_REQUIRE(ld_qkv >= H * D && ld_qkv % 4 == 0 && ld_out >= H * D, "%s: row strides %lld / %lld below H*D (or q/k "
+               "stride not a multiple of 4)", what, (long long)ld_qkv, (long long)ld_out);
+  TAGI_REQUIRE(al16(mu_q) && al16(var_q) && al16(mu_k) && al16(var_k), "%s: q/k must be 16-byte aligned", what);
+  TAGI_REQUIRE(B * H < 65536 && fits_i32(B * S * ld_qkv) && fits_i32(ld_out) && B * H * S * S < (1ll << 40),
+               "%s: too large", what);
+  hipStream_t s = as_stream(stream);
+  ProfScope ps(FAM_ATTN_SCORES, s, 2.0 * 6 * B * H * S * S * D,
+               4.0 * (8 * B * S * H * D + (var_a ? 3 : 2) * B * H * S * S));
+  const dim3 grid((unsigned)cdiv(S, 32), (unsigned)(B * H));
+  const int E = (int)ld_qkv, LO = (int)ld_out;
+  if (D == 16)
+    hipLaunchKernelGGL(attn_fwd_kernel<16>, grid, dim3(512), 0, s, mu_q, var_q, mu_k, var_k, mu_v, var_v, mu_a,
+                       var_a, J, out_m, out_S, (int)H, (int)S, E, LO, scale, scale_sq);
+  else
+    hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, dim3(512), 0, s, mu_q, var_q, mu_k, var_k, mu_v, var_v, mu_a,
+                       var_a, J, out_m, out_S, (int)H, (int)S, E, LO, scale, scale_sq);
   return check_launch(what);
 }
 

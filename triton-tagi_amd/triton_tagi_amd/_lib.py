@@ -76,6 +76,7 @@ _SIGS = {
     "tagi_linear_wgrad_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_bmm_tagi": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, P]),
     "tagi_attn_scores_remax": (c_int, [P, P, P, P, I64, P, P, P, I64, I64, I64, I64, F, F, P]),
+    "tagi_attn_fwd": (c_int, [P, P, P, P, P, P, I64, P, P, P, P, P, I64, I64, I64, I64, I64, F, F, P]),
     "tagi_attn_score_deltas_qk": (c_int, [P, P, I64, P, P, I64, P, P, P, I64, I64, I64, I64, I64, F, F, c_int, P]),
     "tagi_bmm_shared": (c_int, [P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),
     "tagi_bmm_shared_jacobian": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),

@@ -66,6 +66,7 @@ class MultiheadAttentionV2(LearnableLayer):
         self._cache: dict | None = None
         self._attn_mu: Tensor | None = None
         self._attn_var: Tensor | None = None
+        self._attn_src: tuple | None = None  # (qkv_m, qkv_S, B, S) when the variances were not kept
 
     # views of a (B, S, ld) tensor as (B*H, S, D) heads (row stride ld; the Q/K/V
     # projections live side by side in one (B*S, 3E) buffer), and of (B, H, S, S) scores
@@ -106,7 +107,24 @@ class MultiheadAttentionV2(LearnableLayer):
         dev = ma.device
         st = _lib.stream_of(qkv_m)
         s = self._scale
-        if S <= 256 and D in (16, 32, 64) and B * H < 65536 and L % 4 == 0 and q_m % 16 == 0 and q_S % 16 == 0:
+        aligned = B * H < 65536 and L % 4 == 0 and q_m % 16 == 0 and q_S % 16 == 0
+        self._attn_src = None
+        if S <= 256 and D in (16, 32) and aligned:
+            # scores, Remax and score @ V in one kernel (the scores and Remax are the values
+            # of the calls below, bit for bit); the score variances are not kept: the
+            # backward does not read them and get_attention_scores rebuilds them on request
+            mu_score = torch.empty(B, H, S, S, device=dev, dtype=torch.float32)
+            jcb = torch.empty_like(mu_score)
+            mu_out = torch.empty(B, S, E, device=dev, dtype=torch.float32)
+            var_out = torch.empty_like(mu_out)
+            _lib.call("tagi_attn_fwd", q_m, q_S, k_m, k_S, v_m, v_S, L, mu_score.data_ptr(), None, jcb.data_ptr(),
+                      mu_out.data_ptr(), var_out.data_ptr(), E, B, H, S, D, s, s * s, st)
+            self._cache = dict(B=B, S=S, H=H, D=D, qkv_m=qkv_m, ma_in=ma_flat, w_m=w_m, w_S=w_S, b_S=b_S,
+                               mu_score=mu_score, jcb=jcb)
+            self._attn_mu, self._attn_var = mu_score, None
+            self._attn_src = (qkv_m, qkv_S, B, S)
+            return mu_out, var_out
+        if S <= 256 and D in (16, 32, 64) and aligned:
             # scores and Remax in one kernel; the same values as the two calls below
             mu_score = torch.empty(B, H, S, S, device=dev, dtype=torch.float32)
             var_score, jcb = torch.empty_like(mu_score), torch.empty_like(mu_score)
@@ -211,6 +229,17 @@ class MultiheadAttentionV2(LearnableLayer):
     def get_attention_scores(self) -> tuple[Tensor, Tensor]:
         if self._attn_mu is None:
             raise RuntimeError("No attention scores yet; call forward first.")
+        if self._attn_var is None and self._attn_src is not None:
+            # the fused forward kept only the means: form the scores and their Remax again
+            # from the stored projections (the same kernel math, so the same values)
+            qkv_m, qkv_S, B, S = self._attn_src
+            E, H, D, s = self.embed_dim, self.num_heads, self.head_dim, self._scale
+            mu = torch.empty_like(self._attn_mu)
+            var, jcb = torch.empty_like(mu), torch.empty_like(mu)
+            q_m, q_S = qkv_m.data_ptr(), qkv_S.data_ptr()
+            _lib.call("tagi_attn_scores_remax", q_m, q_S, q_m + 4 * E, q_S + 4 * E, 3 * E, mu.data_ptr(),
+                      var.data_ptr(), jcb.data_ptr(), B, H, S, D, s, s * s, _lib.stream_of(qkv_m))
+            self._attn_var = var
         return self._attn_mu, self._attn_var
 
     def __repr__(self) -> str:
