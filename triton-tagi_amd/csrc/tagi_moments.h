@@ -113,11 +113,27 @@ __device__ __forceinline__ void relu_moments(float mz, float Sz, float& ma, floa
   J = cdf;
 }
 
-// Sum over a 64-lane wavefront (butterfly; every lane gets the total).
+// Sum over a 64-lane wavefront; every lane gets the same total. Pairs of lanes are added
+// in registers, without the LDS crossbar that __shfl_xor goes through: DPP quad
+// permutations (lane ^ 1, lane ^ 2), the 8-lane and 16-lane mirrors (lane i with 7 - i,
+// then with 15 - i, within each 16-lane row), then v_permlane16_swap (rows 0 <-> 1,
+// 2 <-> 3) and v_permlane32_swap (lanes 0-31 <-> 32-63). Each step adds two partial sums
+// that cover disjoint lane sets, and fp32 addition commutes, so all lanes hold the
+// bit-identical total.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  int x;
+  x = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  v += __int_as_float(x);
+  x = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  v += __int_as_float(x);
+  x = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false);  // row_half_mirror
+  v += __int_as_float(x);
+  x = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false);  // row_mirror
+  v += __int_as_float(x);
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
 // Remax of one row of K <= 64*EPT classes held by a wavefront (remax.py:33-114): lane
