@@ -360,9 +360,11 @@ def test_rmsnorm_embedding_pe(dev):
     assert_scaled_close(rms.delta_mw, ref.delta_mw, sc, RTOL, ATOL, "rms delta gamma")
     assert_scaled_close(rms.delta_Sw, ref.delta_Sw, None, RTOL, ATOL, "rms delta Sgamma")
 
-    # V = 17, D = 40: the per-category one-hot loader; V = 64, D = 256: four categories per
-    # chunk (the transformer block's table); V = 300: a vocabulary above 256 rows
-    for V, D, pad in ((17, 40, -1), (17, 40, 3), (64, 256, -1), (64, 256, 5), (300, 24, 7)):
+    # 1800 tokens: V = 17 / 64 / 300 sum over 8 / 8 / 4 token slices (64, 256: the transformer
+    # block's table); V = 1100: one slice, written directly; D = 30: the scalar loads;
+    # D = 300: two 256-column groups
+    for V, D, pad in ((17, 40, -1), (17, 40, 3), (64, 256, -1), (64, 256, 5), (300, 24, 7), (1100, 30, -1),
+                      (5, 300, 2)):
         emb = Embedding(V, D, scale=0.25, padding_idx=pad, device="cpu")
         eref = O.mirror(emb)
         emb.mw, emb.Sw = emb.mw.to(dev), emb.Sw.to(dev)

@@ -51,9 +51,6 @@ enum {
   LD_CFWD_B_S = 13,   // conv fwd weights, scalar (any Cout)
   LD_CBWD_BK4 = 14,   // input-delta weights read in place, w[((c*kk + kh)*kk + kw)*Cout + co]:
                       //   mn = c, k = (ikh,ikw,co), float4 along co (Cout % 4 == 0)
-  LD_ONEHOT4 = 15,    // embedding deltas: mn = category, k = token; 1.0 where token k (a float
-                      //   id, cast toward zero) is category mn, else 0; four categories per chunk
-  LD_ONEHOT_S = 16,   //   one category per chunk
   // Tile-aligned conv kinds: the same index maps as LD_CFWD_A4 / LD_CFWD_B4 / LD_CBWD_A4 /
   // LD_CBWD_BK4 / LD_CWG_A4 for geometries where a 16-wide k tile never straddles a kernel
   // tap (C % 16 == 0, or Cout % 16 == 0 for the input delta) or an image (the weight
@@ -72,11 +69,11 @@ template <int KIND>
 struct KindTraits {
   static constexpr bool mn_fast = (KIND == LD_STR_MN4 || KIND == LD_STR_MN_S || KIND == LD_CFWD_B4 ||
                                    KIND == LD_CBWD_B4 || KIND == LD_CBWD_B_S || KIND == LD_CWG_A4 ||
-                                   KIND == LD_CWG_A_S || KIND == LD_CFWD_B_S || KIND == LD_ONEHOT4 ||
-                                   KIND == LD_ONEHOT_S || KIND == LD_CFWD_B4T || KIND == LD_CWG_A4T);
+                                   KIND == LD_CWG_A_S || KIND == LD_CFWD_B_S || KIND == LD_CFWD_B4T ||
+                                   KIND == LD_CWG_A4T);
   static constexpr bool vec4 = (KIND == LD_STR_MN4 || KIND == LD_STR_K4 || KIND == LD_CFWD_A4 || KIND == LD_CFWD_B4 ||
                                 KIND == LD_CBWD_A4 || KIND == LD_CBWD_B4 || KIND == LD_CWG_A4 || KIND == LD_CBWD_BK4 ||
-                                KIND == LD_ONEHOT4 || KIND >= LD_CFWD_A4T);
+                                KIND >= LD_CFWD_A4T);
   static constexpr bool tiled = KIND >= LD_CFWD_A4T;
 };
 
@@ -134,7 +131,6 @@ struct Operand {
   int64_t s_mn, s_k;       // strided kinds
   int MN, K;               // extents along the tile dim and the reduction
   int ones_row;            // tile index that reads as 1.0 for valid k (bias row), -1 = none
-  int64_t pad;             // one-hot kinds: category that reads as all zeros (-1 = none)
   ConvG g;                 // conv kinds
   int64_t nbytes;          // bytes reachable from the operand's (per-batch) base; < 2^31
 };
@@ -391,9 +387,7 @@ struct Loader {
         r2[i] = c;
       }
     }
-    if constexpr (KIND == LD_ONEHOT4 || KIND == LD_ONEHOT_S) {
-      rs0 = rs1 = tagi_i32x4{0, 0, 0, 0};  // token ids are read directly
-    } else if constexpr (CONV_R || TILED || KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
+    if constexpr (CONV_R || TILED || KIND == LD_CFWD_B4 || KIND == LD_CFWD_B_S) {
       rs0 = make_buffer_rsrc(o.p0, o.nbytes);
       rs1 = make_buffer_rsrc(NT == 2 ? o.p1 : o.p0, o.nbytes);
     } else {
@@ -562,18 +556,6 @@ struct Loader {
     for (int i = 0; i < NC; ++i) {
       const int mn = mn0 + cmn[i];
       const int k = k0 + ck[i];
-      if constexpr (KIND == LD_ONEHOT4 || KIND == LD_ONEHOT_S) {
-        // row r of the chunk is 1.0 when token k's category is mn + r (a valid, unpadded one)
-        int r = -1;
-        if (k < kmax) {
-          const int64_t cat = (int64_t)o.p0[k];
-          if (cat >= 0 && cat < o.MN && cat != o.pad) r = (int)(cat - mn);
-        }
-        if constexpr (V4) v[ST][0][i] = make_float4(r == 0 ? 1.f : 0.f, r == 1 ? 1.f : 0.f, r == 2 ? 1.f : 0.f,
-                                                     r == 3 ? 1.f : 0.f);
-        else v[ST][0][i] = r == 0 ? 1.f : 0.f;
-        continue;
-      }
       bool ok = false, one = false;
       // element offset from the resource base (< 2^29 when ok, checked on the host); formed
       // in unsigned arithmetic because chunks that are not ok may compute anything
@@ -1549,8 +1531,7 @@ static inline int64_t plan_ws_bytes(const Plan& p, int64_t R, int64_t C, int64_t
 #define TAGI_GEMM_COMBOS_SHARED_A(X)                                                     \
   X(PROD_SHARED_A, LD_CWG_A4T, LD_STR_MN4)                                               \
   X(PROD_SHARED_A, LD_CWG_A4, LD_STR_MN4) X(PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN4)       \
-  X(PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN_S) X(PROD_SHARED_A, LD_ONEHOT4, LD_STR_MN4)     \
-  X(PROD_SHARED_A, LD_ONEHOT_S, LD_STR_MN4) X(PROD_SHARED_A, LD_ONEHOT_S, LD_STR_MN_S)   \
+  X(PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN_S)                                              \
   X(PROD_SHARED_A, LD_STR_MN4, LD_STR_MN4) X(PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S)    \
   X(PROD_SHARED_A, LD_STR_K4, LD_STR_K4) X(PROD_SHARED_A, LD_STR_K4, LD_STR_MN4)         \
   X(PROD_SHARED_A, LD_STR_MN4, LD_STR_K4)

@@ -199,19 +199,154 @@ extern "C" int tagi_linear_wgrad(const float* ma, const float* dmz, const float*
 // ------------------------------------------------------------------- Embedding
 // Backward (embedding.py:111-145): delta_mw[cat, d] = sum over the category's tokens of
 // dmz[t, d] Sw[cat, d], and delta_Sw with dSz and Sw^2. Sw[cat, d] is the same for every
-// token of a category, so the raw sums are formed first and weighted once in the epilogue
-// (equal in exact arithmetic). The raw sums are the product of the tokens' one-hot matrix
-// with the deltas, O^T dmz and (O^2)^T dSz (O^2 = O): a parameter-delta product whose A
-// operand is generated from the token ids in the loader, run on the MFMA engine with a
-// deterministic split-K over the tokens. (A non-finite delta would reach the other
-// categories of its token's row through 0 * inf; deltas of a running step are finite.)
-static Plan embedding_bwd_plan(int64_t n_tokens, int64_t V, int64_t D) {
-  return choose_plan(V, D, n_tokens, 1, PROD_SHARED_A, true, 512);
+// token of a category, so the raw sums are formed first and weighted once (equal in exact
+// arithmetic). Block (c, slice) sums category c's rows of one slice of the tokens: each of
+// its 4 waves scans a quarter of the slice in 64-token chunks, takes the chunk's tokens of
+// category c from a ballot of their ids and adds their delta rows in token order (up to 4
+// rows' loads in flight), each lane holding 4 columns of a 256-column group. The waves'
+// sums are added in wave order through LDS. With one slice the block weights its sums and
+// writes the output; otherwise the slice sums go to the workspace and a second kernel adds
+// the slices in order. Deterministic; every delta row is read once, the ids (4 bytes per
+// token, cache-resident) once per category. Tokens of padding_idx or outside [0, V) add
+// nothing, and a delta row only reaches its own category.
+namespace {
+constexpr int kEmbWaves = 4;
+
+__device__ __forceinline__ int64_t emb_token_id(float t) { return (int64_t)t; }  // truncation, as .long()
+
+template <bool V4>
+__global__ void __launch_bounds__(256) embedding_bwd_kernel(const float* __restrict__ tokens,
+                                                            const float* __restrict__ dmz,
+                                                            const float* __restrict__ dSz,
+                                                            const float* __restrict__ Sw, float* __restrict__ dmw,
+                                                            float* __restrict__ dSw, float* __restrict__ part,
+                                                            int64_t n, int64_t V, int D, int64_t padding_idx,
+                                                            int64_t tps) {
+  __shared__ float red[kEmbWaves][2][256];
+  const int64_t cat = blockIdx.x;
+  const int slice = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t tpw = tps / kEmbWaves;
+  const int64_t t0 = (int64_t)slice * tps + wave * tpw;
+  const int64_t t1 = min(n, t0 + tpw);
+  const bool skip = cat == padding_idx;
+  for (int g0 = 0; g0 < D; g0 += 256) {
+    float am[4] = {0.f, 0.f, 0.f, 0.f}, as[4] = {0.f, 0.f, 0.f, 0.f};
+    const int col = g0 + 4 * lane;
+    for (int64_t c0 = t0; c0 < t1 && !skip; c0 += 64) {
+      const int64_t t = c0 + lane;
+      const bool hit = t < t1 && emb_token_id(tokens[t]) == cat;
+      uint64_t m = __ballot(hit);
+      while (m) {
+        int64_t tt[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          tt[u] = -1;
+          if (m) {
+            tt[u] = c0 + __builtin_ctzll(m);
+            m &= m - 1;
+          }
+        }
+        float xm[4][4], xs[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if constexpr (V4) {
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+            if (tt[u] >= 0 && col < D) {
+              a = *reinterpret_cast<const float4*>(dmz + tt[u] * D + col);
+              b = *reinterpret_cast<const float4*>(dSz + tt[u] * D + col);
+            }
+            xm[u][0] = a.x, xm[u][1] = a.y, xm[u][2] = a.z, xm[u][3] = a.w;
+            xs[u][0] = b.x, xs[u][1] = b.y, xs[u][2] = b.z, xs[u][3] = b.w;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const bool ok = tt[u] >= 0 && col + e < D;
+              xm[u][e] = ok ? dmz[tt[u] * D + col + e] : 0.f;
+              xs[u][e] = ok ? dSz[tt[u] * D + col + e] : 0.f;
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (tt[u] >= 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              am[e] += xm[u][e];
+              as[e] += xs[u][e];
+            }
+          }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      red[wave][0][4 * lane + e] = am[e];
+      red[wave][1][4 * lane + e] = as[e];
+    }
+    __syncthreads();
+    const int d = g0 + (int)threadIdx.x;
+    if (d < D) {
+      float sm = red[0][0][threadIdx.x], ss = red[0][1][threadIdx.x];
+#pragma unroll
+      for (int w = 1; w < kEmbWaves; ++w) {
+        sm += red[w][0][threadIdx.x];
+        ss += red[w][1][threadIdx.x];
+      }
+      if (part) {
+        float* o = part + ((int64_t)slice * V + cat) * 2 * D;
+        o[d] = sm;
+        o[D + d] = ss;
+      } else {
+        const float sw = Sw[cat * D + d];
+        dmw[cat * D + d] = sm * sw;
+        dSw[cat * D + d] = ss * (sw * sw);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// The slices' sums (part[slice][cat][moment][d]) added in slice order, then weighted.
+__global__ void embedding_bwd_finalize_kernel(const float* __restrict__ part, const float* __restrict__ Sw,
+                                              float* __restrict__ dmw, float* __restrict__ dSw, int64_t V, int D,
+                                              int nslices) {
+  const int64_t total = V * D;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t cat = i / D;
+    const int d = (int)(i - cat * D);
+    float sm = 0.f, ss = 0.f;
+    for (int sl = 0; sl < nslices; ++sl) {
+      const float* o = part + ((int64_t)sl * V + cat) * 2 * D;
+      sm += o[d];
+      ss += o[D + d];
+    }
+    const float sw = Sw[i];
+    dmw[i] = sm * sw;
+    dSw[i] = ss * (sw * sw);
+  }
+}
+}  // namespace
+
+struct EmbSlices {
+  int nslices;
+  int64_t tps;  // tokens per slice, a multiple of 64 x the waves per block
+};
+
+// About 1024 blocks (categories x slices), at most 64 slices, at least 256 tokens a slice.
+static EmbSlices embedding_bwd_slices(int64_t n_tokens, int64_t V) {
+  int64_t ns = cdiv(1024, V);
+  ns = std::min<int64_t>(ns, 64);
+  ns = std::min<int64_t>(ns, cdiv(n_tokens, 256));
+  ns = std::max<int64_t>(ns, 1);
+  const int64_t unit = 64 * kEmbWaves;
+  const int64_t tps = cdiv(cdiv(n_tokens, ns), unit) * unit;
+  return EmbSlices{(int)cdiv(n_tokens, tps), tps};
 }
 
 extern "C" int64_t tagi_embedding_bwd_ws_bytes(int64_t n_tokens, int64_t V, int64_t D) {
   if (n_tokens <= 0 || V <= 0 || D <= 0) return 0;
-  return plan_ws_bytes(embedding_bwd_plan(n_tokens, V, D), V, D, 1);
+  const EmbSlices sl = embedding_bwd_slices(n_tokens, V);
+  return sl.nslices > 1 ? (int64_t)sl.nslices * V * D * 2 * (int64_t)sizeof(float) : 0;
 }
 
 extern "C" int tagi_embedding_bwd(const float* tokens, const float* dmz, const float* dSz, const float* Sw, float* dmw,
@@ -220,22 +355,24 @@ extern "C" int tagi_embedding_bwd(const float* tokens, const float* dmz, const f
   const char* what = "tagi_embedding_bwd";
   TAGI_REQUIRE(tokens && dmz && dSz && Sw && dmw && dSw, "%s: null pointer", what);
   TAGI_REQUIRE(n_tokens > 0 && V > 0 && D > 0, "%s: bad sizes", what);
-  TAGI_REQUIRE(fits_i32(n_tokens * D) && fits_i32(V * D), "%s: too large for 32-bit tiles", what);
+  TAGI_REQUIRE(V < (1ll << 31) && D < (1 << 30) && n_tokens * D < (1ll << 40), "%s: too large", what);
+  const EmbSlices sl = embedding_bwd_slices(n_tokens, V);
+  const int64_t need = tagi_embedding_bwd_ws_bytes(n_tokens, V, D);
+  TAGI_REQUIRE(need == 0 || (ws != nullptr && ws_bytes >= need), "%s: workspace of %lld bytes needed (got %lld)",
+               what, (long long)need, (long long)ws_bytes);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_EMBEDDING, s, 0.0, 4.0 * n_tokens + 8.0 * n_tokens * D + 12.0 * V * D);
-  GemmArgs g{};
-  g.a = strided_operand(tokens, nullptr, 1, 0, 0, 1, 1, V, n_tokens);
-  g.a.pad = padding_idx;
-  g.b = strided_operand(dmz, dSz, 1, 0, 0, 1, D, D, n_tokens);
-  g.epi = epi_wgrad(dmw, dSw, nullptr, nullptr, Sw, nullptr, V, D);
-  g.R = (int)V;
-  g.C = (int)D;
-  g.Kred = (int)n_tokens;
-  Plan p = embedding_bwd_plan(n_tokens, V, D);
-  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, V, D, 1))) p = choose_plan(V, D, n_tokens, 1, PROD_SHARED_A, false, 1);
-  const bool v4 = V % 4 == 0 && D % 4 == 0 && al16(dmz) && al16(dSz);
-  if (v4) return run_gemm<PROD_SHARED_A, LD_ONEHOT4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
-  if (D % 4 == 0 && al16(dmz) && al16(dSz))
-    return run_gemm<PROD_SHARED_A, LD_ONEHOT_S, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
-  return run_gemm<PROD_SHARED_A, LD_ONEHOT_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
+  float* part = sl.nslices > 1 ? ws : nullptr;
+  const dim3 grid((unsigned)V, (unsigned)sl.nslices);
+  const bool v4 = D % 4 == 0 && al16(dmz) && al16(dSz);
+  if (v4)
+    hipLaunchKernelGGL(embedding_bwd_kernel<true>, grid, dim3(256), 0, s, tokens, dmz, dSz, Sw, dmw, dSw, part,
+                       n_tokens, V, (int)D, padding_idx, sl.tps);
+  else
+    hipLaunchKernelGGL(embedding_bwd_kernel<false>, grid, dim3(256), 0, s, tokens, dmz, dSz, Sw, dmw, dSw, part,
+                       n_tokens, V, (int)D, padding_idx, sl.tps);
+  if (part)
+    hipLaunchKernelGGL(embedding_bwd_finalize_kernel, dim3(ew_blocks(V * D, 256)), dim3(256), 0, s, part, Sw, dmw, dSw,
+                       V, (int)D, sl.nslices);
+  return check_launch(what);
 }

@@ -205,9 +205,11 @@ class MultiheadAttentionV2(LearnableLayer):
         side = ctx.fork(dev, ma_in, dqkv_m, dqkv_S, c["w_S"], c["b_S"]) if ctx is not None and big else None
         with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
             dmw, dSw, dmb, dSb = linear_param_deltas(ma_in, dqkv_m, dqkv_S, c["w_S"], c["b_S"])
+            # the (E, 3E) deltas as three contiguous (E, E) blocks: one copy per moment
+            blk_m = dmw.view(E, 3, E).transpose(0, 1).contiguous()
+            blk_S = dSw.view(E, 3, E).transpose(0, 1).contiguous()
             for i, p in enumerate(projs):
-                p.delta_mw = dmw[:, i * E:(i + 1) * E].contiguous()
-                p.delta_Sw = dSw[:, i * E:(i + 1) * E].contiguous()
+                p.delta_mw, p.delta_Sw = blk_m[i], blk_S[i]
                 if self.has_bias:
                     p.delta_mb = dmb[:, i * E:(i + 1) * E].contiguous()
                     p.delta_Sb = dSb[:, i * E:(i + 1) * E].contiguous()
