@@ -449,9 +449,10 @@ int tagi_embedding_fwd(const float* tokens, const float* mw, const float* Sw, fl
                        float* Sz, int64_t n_tokens, int64_t V, int64_t D, int64_t padding_idx,
                        tagi_stream_t stream);
 /* Embedding deltas (embedding.py:111-150): dmw[cat] = sum dm Sw[cat], dSw[cat] = sum dS Sw[cat]^2
- * over the tokens of each category; dmw/dSw (V,D) are overwritten. Each category's delta
- * rows are summed in token order per slice of the tokens, the slices in order through ws
- * (size from tagi_embedding_bwd_ws_bytes, 0 when one slice suffices): deterministic. */
+ * over the tokens of each category; dmw/dSw (V,D) are overwritten. One block per category
+ * finds its tokens from ballots of the ids and sums their delta rows in an order fixed by
+ * the ids (deterministic). ws is not used (tagi_embedding_bwd_ws_bytes returns 0; kept so
+ * that callers sizing a workspace keep working). */
 int tagi_embedding_bwd(const float* tokens, const float* dmz, const float* dSz, const float* Sw,
                        float* dmw, float* dSw, int64_t n_tokens, int64_t V, int64_t D,
                        int64_t padding_idx, float* ws, int64_t ws_bytes, tagi_stream_t stream);

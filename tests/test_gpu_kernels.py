@@ -360,22 +360,22 @@ def test_rmsnorm_embedding_pe(dev):
     assert_scaled_close(rms.delta_mw, ref.delta_mw, sc, RTOL, ATOL, "rms delta gamma")
     assert_scaled_close(rms.delta_Sw, ref.delta_Sw, None, RTOL, ATOL, "rms delta Sgamma")
 
-    # 1800 tokens: V = 17 / 64 / 300 sum over 8 / 8 / 4 token slices (64, 256: the transformer
-    # block's table); V = 1100: one slice, written directly; D = 30: the scalar loads;
-    # D = 300: two 256-column groups
-    for V, D, pad in ((17, 40, -1), (17, 40, 3), (64, 256, -1), (64, 256, 5), (300, 24, 7), (1100, 30, -1),
-                      (5, 300, 2)):
+    # (6, 300) tokens: one 16384-token window; (3, 6000): two windows; V = 64, D = 256: the
+    # transformer block's table; D = 30: the scalar loads; D = 300: two 256-column groups
+    for V, D, pad, T in ((17, 40, -1, (6, 300)), (17, 40, 3, (6, 300)), (64, 256, -1, (6, 300)),
+                         (64, 256, 5, (6, 300)), (300, 24, 7, (6, 300)), (1100, 30, -1, (6, 300)),
+                         (5, 300, 2, (6, 300)), (40, 64, 1, (3, 6000))):
         emb = Embedding(V, D, scale=0.25, padding_idx=pad, device="cpu")
         eref = O.mirror(emb)
         emb.mw, emb.Sw = emb.mw.to(dev), emb.Sw.to(dev)
-        tok = torch.randint(0, V, (6, 300), generator=r).to(torch.float32)
+        tok = torch.randint(0, V, T, generator=r).to(torch.float32)
         mz, Sz = emb.forward(tok.to(dev), torch.zeros_like(tok).to(dev))
         rm, rS = eref.forward(d64(tok), d64(tok) * 0)
         assert torch.equal(mz.cpu().double(), rm) and torch.equal(Sz.cpu().double(), rS)
-        dm, dS = torch.randn(6, 300, D, generator=r), -torch.rand(6, 300, D, generator=r)
+        dm, dS = torch.randn(*T, D, generator=r), -torch.rand(*T, D, generator=r)
         zm, zS = emb.backward(dm.to(dev), dS.to(dev))
         eref.backward(d64(dm), d64(dS))
-        assert float(zm.abs().sum()) == 0.0 and tuple(zm.shape) == (6, 300)
+        assert float(zm.abs().sum()) == 0.0 and tuple(zm.shape) == T
         sc = torch.zeros(V, D, dtype=torch.float64).index_add_(
             0, tok.long().reshape(-1), (d64(dm).reshape(-1, D) * eref.Sw[tok.long().reshape(-1)]).abs())
         assert_scaled_close(emb.delta_mw, eref.delta_mw, sc, RTOL, ATOL, "emb delta mw")

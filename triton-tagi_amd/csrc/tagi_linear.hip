@@ -200,51 +200,77 @@ extern "C" int tagi_linear_wgrad(const float* ma, const float* dmz, const float*
 // Backward (embedding.py:111-145): delta_mw[cat, d] = sum over the category's tokens of
 // dmz[t, d] Sw[cat, d], and delta_Sw with dSz and Sw^2. Sw[cat, d] is the same for every
 // token of a category, so the raw sums are formed first and weighted once (equal in exact
-// arithmetic). Block (c, slice) sums category c's rows of one slice of the tokens: each of
-// its 4 waves scans a quarter of the slice in 64-token chunks, takes the chunk's tokens of
-// category c from a ballot of their ids and adds their delta rows in token order (up to 4
-// rows' loads in flight), each lane holding 4 columns of a 256-column group. The waves'
-// sums are added in wave order through LDS. With one slice the block weights its sums and
-// writes the output; otherwise the slice sums go to the workspace and a second kernel adds
-// the slices in order. Deterministic; every delta row is read once, the ids (4 bytes per
-// token, cache-resident) once per category. Tokens of padding_idx or outside [0, V) add
-// nothing, and a delta row only reaches its own category.
+// arithmetic). One block per category, 16 waves, over windows of 16384 tokens:
+//   * each wave takes a 1024-token stretch of the window (ids loaded up front), finds the
+//     category's tokens by a ballot per 64-token chunk and appends them to its own LDS list
+//     in token order -- the window's matches are the wave lists one after the other;
+//   * match j of that sequence is added by wave j % 16 (up to 4 rows' loads in flight per
+//     wave, each lane holding 4 columns of a 256-column group);
+//   * the 16 waves' sums are added in wave order through LDS.
+// The sum order is fixed by the token ids alone: deterministic. Every delta row is read
+// once; the ids are read once per category (cache-resident, 4 bytes per token). Tokens of
+// padding_idx or outside [0, V) add nothing, and a delta row reaches only its category.
 namespace {
-constexpr int kEmbWaves = 4;
+constexpr int kEmbWaves = 16;
+constexpr int kEmbPerWave = 1024;                    // tokens a wave scans per window
+constexpr int kEmbWin = kEmbWaves * kEmbPerWave;     // tokens per window
 
 __device__ __forceinline__ int64_t emb_token_id(float t) { return (int64_t)t; }  // truncation, as .long()
 
 template <bool V4>
-__global__ void __launch_bounds__(256) embedding_bwd_kernel(const float* __restrict__ tokens,
-                                                            const float* __restrict__ dmz,
-                                                            const float* __restrict__ dSz,
-                                                            const float* __restrict__ Sw, float* __restrict__ dmw,
-                                                            float* __restrict__ dSw, float* __restrict__ part,
-                                                            int64_t n, int64_t V, int D, int64_t padding_idx,
-                                                            int64_t tps) {
-  __shared__ float red[kEmbWaves][2][256];
+__global__ void __launch_bounds__(1024) embedding_bwd_kernel(const float* __restrict__ tokens,
+                                                             const float* __restrict__ dmz,
+                                                             const float* __restrict__ dSz,
+                                                             const float* __restrict__ Sw, float* __restrict__ dmw,
+                                                             float* __restrict__ dSw, int64_t n, int D,
+                                                             int64_t padding_idx) {
+  // the match lists (window-relative token indices), then the waves' sums (float
+  // [wave][moment][256]) in the same 32 KB
+  __shared__ __attribute__((aligned(16))) unsigned char buf[kEmbWin * sizeof(unsigned short)];
+  __shared__ int wcnt[kEmbWaves];
+  static_assert(kEmbWaves * 2 * 256 * sizeof(float) <= sizeof(buf), "sums must fit the list space");
+  unsigned short* list = reinterpret_cast<unsigned short*>(buf);
+  float* red = reinterpret_cast<float*>(buf);
   const int64_t cat = blockIdx.x;
-  const int slice = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t tpw = tps / kEmbWaves;
-  const int64_t t0 = (int64_t)slice * tps + wave * tpw;
-  const int64_t t1 = min(n, t0 + tpw);
   const bool skip = cat == padding_idx;
   for (int g0 = 0; g0 < D; g0 += 256) {
     float am[4] = {0.f, 0.f, 0.f, 0.f}, as[4] = {0.f, 0.f, 0.f, 0.f};
     const int col = g0 + 4 * lane;
-    for (int64_t c0 = t0; c0 < t1 && !skip; c0 += 64) {
-      const int64_t t = c0 + lane;
-      const bool hit = t < t1 && emb_token_id(tokens[t]) == cat;
-      uint64_t m = __ballot(hit);
-      while (m) {
+    for (int64_t w0 = 0; w0 < n && !skip; w0 += kEmbWin) {
+      // scan: this wave's stretch of the window, matches appended in token order
+      const int64_t s0 = w0 + (int64_t)wave * kEmbPerWave;
+      constexpr int NCH = kEmbPerWave / 64;
+      bool hit[NCH];
+#pragma unroll
+      for (int q = 0; q < NCH; ++q) {
+        const int64_t t = s0 + 64 * q + lane;
+        hit[q] = t < n && emb_token_id(tokens[t]) == cat;
+      }
+      int cnt = 0;
+      unsigned short* mylist = list + wave * kEmbPerWave;
+#pragma unroll
+      for (int q = 0; q < NCH; ++q) {
+        const uint64_t m = __ballot(hit[q]);
+        if (hit[q]) mylist[cnt + __popcll(m & ((1ull << lane) - 1))] = (unsigned short)(wave * kEmbPerWave + 64 * q + lane);
+        cnt += __popcll(m);
+      }
+      if (lane == 0) wcnt[wave] = cnt;
+      __syncthreads();
+      // sum: match j (in wave-list order) goes to wave j % kEmbWaves
+      int total = 0;
+      for (int w = 0; w < kEmbWaves; ++w) total += wcnt[w];
+      for (int j0 = wave; j0 < total; j0 += 4 * kEmbWaves) {
         int64_t tt[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
+          const int j = j0 + u * kEmbWaves;
           tt[u] = -1;
-          if (m) {
-            tt[u] = c0 + __builtin_ctzll(m);
-            m &= m - 1;
+          if (j < total) {
+            // locate match j: wave list w holds matches [sum of earlier counts, + wcnt[w])
+            int w = 0, base = 0;
+            while (j >= base + wcnt[w]) base += wcnt[w++];
+            tt[u] = w0 + list[w * kEmbPerWave + (j - base)];
           }
         }
         float xm[4][4], xs[4][4];
@@ -277,26 +303,23 @@ __global__ void __launch_bounds__(256) embedding_bwd_kernel(const float* __restr
             }
           }
       }
+      __syncthreads();  // the lists and counts are rewritten by the next window
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      red[wave][0][4 * lane + e] = am[e];
-      red[wave][1][4 * lane + e] = as[e];
+      red[(wave * 2 + 0) * 256 + 4 * lane + e] = am[e];
+      red[(wave * 2 + 1) * 256 + 4 * lane + e] = as[e];
     }
     __syncthreads();
-    const int d = g0 + (int)threadIdx.x;
-    if (d < D) {
-      float sm = red[0][0][threadIdx.x], ss = red[0][1][threadIdx.x];
+    if (threadIdx.x < 256) {
+      const int d = g0 + (int)threadIdx.x;
+      float sm = red[threadIdx.x], ss = red[256 + threadIdx.x];
 #pragma unroll
       for (int w = 1; w < kEmbWaves; ++w) {
-        sm += red[w][0][threadIdx.x];
-        ss += red[w][1][threadIdx.x];
+        sm += red[(w * 2 + 0) * 256 + threadIdx.x];
+        ss += red[(w * 2 + 1) * 256 + threadIdx.x];
       }
-      if (part) {
-        float* o = part + ((int64_t)slice * V + cat) * 2 * D;
-        o[d] = sm;
-        o[D + d] = ss;
-      } else {
+      if (d < D) {
         const float sw = Sw[cat * D + d];
         dmw[cat * D + d] = sm * sw;
         dSw[cat * D + d] = ss * (sw * sw);
@@ -305,74 +328,29 @@ __global__ void __launch_bounds__(256) embedding_bwd_kernel(const float* __restr
     __syncthreads();
   }
 }
-
-// The slices' sums (part[slice][cat][moment][d]) added in slice order, then weighted.
-__global__ void embedding_bwd_finalize_kernel(const float* __restrict__ part, const float* __restrict__ Sw,
-                                              float* __restrict__ dmw, float* __restrict__ dSw, int64_t V, int D,
-                                              int nslices) {
-  const int64_t total = V * D;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t cat = i / D;
-    const int d = (int)(i - cat * D);
-    float sm = 0.f, ss = 0.f;
-    for (int sl = 0; sl < nslices; ++sl) {
-      const float* o = part + ((int64_t)sl * V + cat) * 2 * D;
-      sm += o[d];
-      ss += o[D + d];
-    }
-    const float sw = Sw[i];
-    dmw[i] = sm * sw;
-    dSw[i] = ss * (sw * sw);
-  }
-}
 }  // namespace
 
-struct EmbSlices {
-  int nslices;
-  int64_t tps;  // tokens per slice, a multiple of 64 x the waves per block
-};
-
-// About 1024 blocks (categories x slices), at most 64 slices, at least 256 tokens a slice.
-static EmbSlices embedding_bwd_slices(int64_t n_tokens, int64_t V) {
-  int64_t ns = cdiv(1024, V);
-  ns = std::min<int64_t>(ns, 64);
-  ns = std::min<int64_t>(ns, cdiv(n_tokens, 256));
-  ns = std::max<int64_t>(ns, 1);
-  const int64_t unit = 64 * kEmbWaves;
-  const int64_t tps = cdiv(cdiv(n_tokens, ns), unit) * unit;
-  return EmbSlices{(int)cdiv(n_tokens, tps), tps};
-}
-
 extern "C" int64_t tagi_embedding_bwd_ws_bytes(int64_t n_tokens, int64_t V, int64_t D) {
-  if (n_tokens <= 0 || V <= 0 || D <= 0) return 0;
-  const EmbSlices sl = embedding_bwd_slices(n_tokens, V);
-  return sl.nslices > 1 ? (int64_t)sl.nslices * V * D * 2 * (int64_t)sizeof(float) : 0;
+  (void)n_tokens, (void)V, (void)D;
+  return 0;
 }
 
 extern "C" int tagi_embedding_bwd(const float* tokens, const float* dmz, const float* dSz, const float* Sw, float* dmw,
                                   float* dSw, int64_t n_tokens, int64_t V, int64_t D, int64_t padding_idx, float* ws,
                                   int64_t ws_bytes, tagi_stream_t stream) {
   const char* what = "tagi_embedding_bwd";
+  (void)ws, (void)ws_bytes;
   TAGI_REQUIRE(tokens && dmz && dSz && Sw && dmw && dSw, "%s: null pointer", what);
   TAGI_REQUIRE(n_tokens > 0 && V > 0 && D > 0, "%s: bad sizes", what);
   TAGI_REQUIRE(V < (1ll << 31) && D < (1 << 30) && n_tokens * D < (1ll << 40), "%s: too large", what);
-  const EmbSlices sl = embedding_bwd_slices(n_tokens, V);
-  const int64_t need = tagi_embedding_bwd_ws_bytes(n_tokens, V, D);
-  TAGI_REQUIRE(need == 0 || (ws != nullptr && ws_bytes >= need), "%s: workspace of %lld bytes needed (got %lld)",
-               what, (long long)need, (long long)ws_bytes);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_EMBEDDING, s, 0.0, 4.0 * n_tokens + 8.0 * n_tokens * D + 12.0 * V * D);
-  float* part = sl.nslices > 1 ? ws : nullptr;
-  const dim3 grid((unsigned)V, (unsigned)sl.nslices);
   const bool v4 = D % 4 == 0 && al16(dmz) && al16(dSz);
   if (v4)
-    hipLaunchKernelGGL(embedding_bwd_kernel<true>, grid, dim3(256), 0, s, tokens, dmz, dSz, Sw, dmw, dSw, part,
-                       n_tokens, V, (int)D, padding_idx, sl.tps);
+    hipLaunchKernelGGL(embedding_bwd_kernel<true>, dim3((unsigned)V), dim3(1024), 0, s, tokens, dmz, dSz, Sw, dmw, dSw,
+                       n_tokens, (int)D, padding_idx);
   else
-    hipLaunchKernelGGL(embedding_bwd_kernel<false>, grid, dim3(256), 0, s, tokens, dmz, dSz, Sw, dmw, dSw, part,
-                       n_tokens, V, (int)D, padding_idx, sl.tps);
-  if (part)
-    hipLaunchKernelGGL(embedding_bwd_finalize_kernel, dim3(ew_blocks(V * D, 256)), dim3(256), 0, s, part, Sw, dmw, dSw,
-                       V, (int)D, sl.nslices);
+    hipLaunchKernelGGL(embedding_bwd_kernel<false>, dim3((unsigned)V), dim3(1024), 0, s, tokens, dmz, dSz, Sw, dmw,
+                       dSw, n_tokens, (int)D, padding_idx);
   return check_launch(what);
 }
