@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define TAGI_ABI_VERSION 3
+#define TAGI_ABI_VERSION 4
 
 enum {
   TAGI_OK = 0,
@@ -272,6 +272,23 @@ int64_t tagi_conv2d_bwd_delta_ws_bytes(const tagi_conv_geom* g);
 int tagi_conv2d_bwd_delta_add(const float* dmz, const float* dSz, const float* mw, const float* add_m,
                               const float* add_S, float* dma, float* dSa, const tagi_conv_geom* g,
                               float* ws, int64_t ws_bytes, tagi_stream_t stream);
+/* tagi_conv2d_bwd_delta followed by the backward of the BatchNorm2D and the ReLU in front
+ * of the convolution (the layer order conv_prev -> ReLU -> BatchNorm2D -> this conv), in the
+ * GEMM's epilogue: the products (deltas at the BatchNorm2D output) never reach memory.
+ * dma/dSa receive the deltas at the ReLU input, the values tagi_bn_relu_bwd_partials_bias
+ * writes for them (batchnorm2d.py:465-513, relu.py:152-169); part receives per-tile sums of
+ * the six quantities that call's ws holds, for tagi_bn_bwd_finalize_multi (with nblk =
+ * part_bytes / (24 C) and the conv_prev bias fields). mhat, J: the BatchNorm2D's saved
+ * normalised input and the ReLU's Jacobian, laid out like dma; var, mg: the normalisation
+ * variance and gamma means (C). Needs stride 1 and an unsplit plan:
+ * tagi_conv2d_bwd_delta_bn_relu_part_bytes returns the partial-sum bytes, 0 when the fold
+ * does not apply (then TAGI_ERR_UNSUPPORTED: use the two calls). ws as for
+ * tagi_conv2d_bwd_delta. */
+int tagi_conv2d_bwd_delta_bn_relu(const float* dmz, const float* dSz, const float* mw, const float* mhat,
+                                  const float* J, const float* var, const float* mg, float eps, float* dma,
+                                  float* dSa, float* part, int64_t part_bytes, const tagi_conv_geom* g, float* ws,
+                                  int64_t ws_bytes, tagi_stream_t stream);
+int64_t tagi_conv2d_bwd_delta_bn_relu_part_bytes(const tagi_conv_geom* g);
 
 /* Parameter deltas of a Conv2D layer (reduction over N*Ho*Wo patches, split-K):
  *   dmw = Sw * P^T @ dmz, dSw = Sw^2 * (P^2)^T @ dSz, dmb = Sb * sum dmz, dSb = Sb^2 * sum dSz.
@@ -408,10 +425,12 @@ int tagi_bn_relu_bwd_partials_bias(const float* dma, const float* dSa, const flo
                                    int64_t ws_bytes, tagi_stream_t stream);
 int64_t tagi_bn_relu_bwd_bias_ws_bytes(int64_t N, int64_t C, int64_t HW);
 
-/* One layer left pending by tagi_bn_relu_bwd_partials(_bias): its partial sums (ws) and
- * sizes, the gamma/beta variances and the four parameter-delta outputs of length C; for
- * a layer left by the _bias variant also the conv's bias variances cSb and its two bias
- * delta outputs (all three NULL otherwise). */
+/* One layer left pending by tagi_bn_relu_bwd_partials(_bias) or
+ * tagi_conv2d_bwd_delta_bn_relu: its partial sums (ws) and sizes, the gamma/beta variances
+ * and the four parameter-delta outputs of length C; for a layer left by the _bias variant
+ * or the conv fold also the conv's bias variances cSb and its two bias delta outputs (all
+ * three NULL otherwise); nblk: partial sums per channel and quantity (0: the count
+ * tagi_bn_relu_bwd_partials uses for N*HW rows; the conv fold's is its part_bytes / (24 C)). */
 typedef struct {
   const float* ws;
   const float* Sg;
@@ -424,6 +443,7 @@ typedef struct {
   const float* cSb;
   float* cdmb;
   float* cdSb;
+  int64_t nblk;
 } tagi_bn_bwd_pending;
 
 /* The parameter deltas of count pending layers, in one launch per 32 layers:

@@ -10,6 +10,7 @@ unfused kernels (same fp32 formulas, so they agree to a few ulps).
 from __future__ import annotations
 
 import copy
+import ctypes
 
 import pytest
 import torch
@@ -214,6 +215,88 @@ def test_conv_bwd_delta_with_addend(dev, case):
     um, uS = layer.backward(dm.to(dev), dS.to(dev))
     close_unfused(om, um + am.to(dev), "dma")
     close_unfused(oS, uS + aS.to(dev), "dSa")
+
+
+FOLD_CASES = [
+    # N, C_in (the BatchNorm2D channels), H, W, C_out, k: shapes whose input-delta plan
+    # is unsplit with one tile per wave (the fold's condition)
+    (16, 64, 32, 32, 64, 3),  # ResNet-18 stage 1 at batch 16
+    (16, 6, 16, 16, 8, 3),    # C_in off the float4 path
+    (8, 12, 12, 10, 16, 3),   # C_out below the tile-aligned loaders' 16
+    (8, 32, 8, 8, 16, 1),
+]
+
+
+@pytest.mark.parametrize("case", FOLD_CASES, ids=[str(c) for c in FOLD_CASES])
+def test_conv_bwd_delta_bn_relu_fold(dev, case):
+    """tagi_conv2d_bwd_delta_bn_relu (the BatchNorm2D -> ReLU backward in the input-delta
+    GEMM's epilogue) against tagi_conv2d_bwd_delta followed by
+    tagi_bn_relu_bwd_partials_bias: the propagated deltas bit for bit (same fp32 operations
+    on the same products), the parameter and bias deltas after tagi_bn_bwd_finalize_multi
+    to 1e-5 (the per-channel sums are grouped by GEMM tile instead of by row block)."""
+    from triton_tagi_amd import _lib
+    from triton_tagi_amd.layers.conv2d import Conv2D
+
+    N, C, H, W, Cout, k = case
+    torch.manual_seed(sum(case))
+    conv = Conv2D(C, Cout, k, stride=1, padding=k // 2, device="cpu")
+    for a in ("mw", "Sw", "mb", "Sb"):
+        setattr(conv, a, getattr(conv, a).to(dev))
+    r = g(sum(case) + 11)
+    cl = lambda t: t.to(dev).contiguous(memory_format=torch.channels_last)
+    dmz, dSz = cl(torch.randn(N, Cout, H, W, generator=r)), cl(-torch.rand(N, Cout, H, W, generator=r))
+    mhat, J = cl(torch.randn(N, C, H, W, generator=r)), cl(torch.rand(N, C, H, W, generator=r))
+    var = (torch.rand(C, generator=r) + 0.5).to(dev)
+    mg = (1 + 0.1 * torch.randn(C, generator=r)).to(dev)
+    Sg, Sb, cSb = ((torch.rand(C, generator=r) * 0.1 + 0.01).to(dev) for _ in range(3))
+    eps = 1e-5
+    conv.input_shape = (N, C, H, W)
+    geo = conv._geom(N, C, H, W)
+    st = _lib.stream_of(dmz)
+    ws = _lib.workspace(_lib.query("tagi_conv2d_bwd_delta_ws_bytes", geo), dev)
+    wp, wb = _lib.ws_args(ws)
+    part_bytes = _lib.query("tagi_conv2d_bwd_delta_bn_relu_part_bytes", geo)
+    assert part_bytes > 0
+    part = _lib.workspace(part_bytes, dev)
+    fm, fS = _lib.empty_cl(N, C, H, W, dev), _lib.empty_cl(N, C, H, W, dev)
+    _lib.call("tagi_conv2d_bwd_delta_bn_relu", dmz.data_ptr(), dSz.data_ptr(), conv.mw.data_ptr(), mhat.data_ptr(),
+              J.data_ptr(), var.data_ptr(), mg.data_ptr(), eps, fm.data_ptr(), fS.data_ptr(), part.data_ptr(),
+              part_bytes, geo, wp, wb, st)
+    # the two calls
+    dma, dSa = _lib.empty_cl(N, C, H, W, dev), _lib.empty_cl(N, C, H, W, dev)
+    _lib.call("tagi_conv2d_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), conv.mw.data_ptr(), dma.data_ptr(),
+              dSa.data_ptr(), geo, wp, wb, st)
+    um, uS = _lib.empty_cl(N, C, H, W, dev), _lib.empty_cl(N, C, H, W, dev)
+    ws2 = _lib.workspace(_lib.query("tagi_bn_relu_bwd_bias_ws_bytes", N, C, H * W), dev)
+    w2p, w2b = _lib.ws_args(ws2)
+    _lib.call("tagi_bn_relu_bwd_partials_bias", dma.data_ptr(), dSa.data_ptr(), mhat.data_ptr(), J.data_ptr(),
+              var.data_ptr(), mg.data_ptr(), um.data_ptr(), uS.data_ptr(), N, C, H * W, eps, w2p, w2b, st)
+    assert torch.equal(fm, um) and torch.equal(fS, uS), "folded deltas differ from the two calls"
+    outs = []
+    for wsx, nblk in ((part, part_bytes // (24 * C)), (ws2, 0)):
+        o = [torch.empty(C, device=dev) for _ in range(6)]
+        item = _lib.BnPending(wsx.data_ptr(), Sg.data_ptr(), Sb.data_ptr(), *(t.data_ptr() for t in o[:4]), N, C,
+                              H * W, cSb.data_ptr(), o[4].data_ptr(), o[5].data_ptr(), nblk)
+        _lib.call("tagi_bn_bwd_finalize_multi", ctypes.byref(item), 1, st)
+        outs.append(o)
+    names = ("delta gamma", "delta Sgamma", "delta beta", "delta Sbeta", "conv bias delta", "conv bias Sdelta")
+    for name, a, b in zip(names, *outs):
+        close_unfused_rel(a, b, 1e-5, name)
+
+
+def test_conv_bwd_delta_bn_relu_fold_refuses_stride2(dev):
+    from triton_tagi_amd import _lib
+    from triton_tagi_amd.layers.conv2d import Conv2D
+
+    conv = Conv2D(16, 16, 3, stride=2, padding=1, device="cpu")
+    assert _lib.query("tagi_conv2d_bwd_delta_bn_relu_part_bytes", conv._geom(2, 16, 8, 8)) == 0
+
+
+def close_unfused_rel(a, b, rtol, what):
+    a, b = a.detach().cpu().double(), b.detach().cpu().double()
+    err = (a - b).abs().max().item()
+    lim = rtol * (b.abs().max().item() + 1e-30) + 1e-12
+    assert err <= lim, f"{what}: folded vs two-call max err {err:.3e} > {lim:.3e}"
 
 
 def test_fused_step_matches_oracle(dev):

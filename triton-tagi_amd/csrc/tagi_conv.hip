@@ -228,9 +228,28 @@ extern "C" int64_t tagi_conv2d_bwd_delta_ws_bytes(const tagi_conv_geom* g) {
   return wt_floats(g) * (int64_t)sizeof(float) + plan_ws_bytes(conv_bwd_plan(g), R, g->C, g->stride * g->stride);
 }
 
+// The BatchNorm2D -> ReLU backward folded into the input-delta GEMM's epilogue: the pair's
+// saved state and the per-tile partial sums' destination.
+struct BnBwdFuse {
+  const float* mhat;
+  const float* J;
+  const float* var;
+  const float* mg;
+  float eps;
+  float* part;
+};
+
+// Tiles along the rows of the fused launch (the partial sums per channel), or 0 when the
+// fold does not apply: stride 1 (one phase) and an unsplit plan.
+static int64_t bn_fuse_tiles(const tagi_conv_geom* g) {
+  if (!g || g->N <= 0 || g->Cout <= 0 || g->C <= 0 || g->k <= 0 || g->stride != 1 || g->Cout % 4 != 0) return 0;
+  const Plan p = conv_bwd_plan(g);
+  return p.splits == 1 && bnf_cfg(p.cfg) ? p.tiles_m : 0;
+}
+
 static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* dSz, const float* mw,
                                const float* add_m, const float* add_S, float* dma, float* dSa, const tagi_conv_geom* g,
-                               float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+                               float* ws, int64_t ws_bytes, tagi_stream_t stream, const BnBwdFuse* bnf = nullptr) {
   TAGI_REQUIRE((add_m == nullptr) == (add_S == nullptr), "%s: add_m and add_S must both be given or both be NULL",
                what);
   int rc = check_geom(g, what);
@@ -279,6 +298,14 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
   a.epi.g = to_g(g);
   a.epi.am = add_m;
   a.epi.av = add_S;
+  if (bnf) {
+    a.epi.bn_mhat = bnf->mhat;
+    a.epi.bn_J = bnf->J;
+    a.epi.bn_var = bnf->var;
+    a.epi.bn_g = bnf->mg;
+    a.epi.bn_eps = bnf->eps;
+    a.epi.st_ws = bnf->part;
+  }
   a.R = (int)R0;
   a.C = (int)g->C;
   a.Kred = (int)K0;
@@ -302,9 +329,21 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
   float* part = ws + wt_floats(g);
   const int64_t part_bytes = ws_bytes - wt_floats(g) * (int64_t)sizeof(float);
   if (p.splits > 1 && part_bytes < plan_ws_bytes(p, R0, g->C, nph)) p = choose_plan(R0, g->C, K0, nph, PROD_SHARED_B, false, 1);
+  if (bnf) {
+    TAGI_REQUIRE(nph == 1 && p.splits == 1 && bnf_cfg(p.cfg),
+                 "%s: the folded BatchNorm2D backward needs stride 1 and an unsplit one-tile-per-wave plan", what);
+    a.epi.st_nblk = p.tiles_m;
+  }
   const int64_t gx = (int64_t)p.tiles_m * p.tiles_n;  // phase 0 is the largest
   const bool va = g->Cout % 4 == 0 && al16(dmz) && al16(dSz);
   const bool vb = g->C % 4 == 0;
+  if (bnf) {
+    TAGI_REQUIRE(va && in_place, "%s: the folded BatchNorm2D backward needs Cout %% 4 == 0 and 16-byte aligned "
+                 "deltas and weights", what);
+    if (g->Cout % 16 == 0 && g->k <= 5)
+      return run_gemm<PROD_SHARED_B, LD_CBWD_A4T, LD_CBWD_BK4T, 1>(a, nph, p, part, part_bytes, s, what, gx);
+    return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4, 1>(a, nph, p, part, part_bytes, s, what, gx);
+  }
   if (va && in_place && g->Cout % 16 == 0 && g->k <= 5)
     return run_gemm<PROD_SHARED_B, LD_CBWD_A4T, LD_CBWD_BK4T>(a, nph, p, part, part_bytes, s, what, gx);
   if (va && in_place) return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4>(a, nph, p, part, part_bytes, s, what, gx);
@@ -324,6 +363,27 @@ extern "C" int tagi_conv2d_bwd_delta_add(const float* dmz, const float* dSz, con
                                          float* ws, int64_t ws_bytes, tagi_stream_t stream) {
   return conv_bwd_delta_impl("tagi_conv2d_bwd_delta_add", dmz, dSz, mw, add_m, add_S, dma, dSa, g, ws, ws_bytes,
                              stream);
+}
+
+extern "C" int64_t tagi_conv2d_bwd_delta_bn_relu_part_bytes(const tagi_conv_geom* g) {
+  return bn_fuse_tiles(g) * 6 * (g ? g->C : 0) * (int64_t)sizeof(float);
+}
+
+extern "C" int tagi_conv2d_bwd_delta_bn_relu(const float* dmz, const float* dSz, const float* mw, const float* mhat,
+                                             const float* J, const float* var, const float* mg, float eps,
+                                             float* dma, float* dSa, float* part, int64_t part_bytes,
+                                             const tagi_conv_geom* g, float* ws, int64_t ws_bytes,
+                                             tagi_stream_t stream) {
+  const char* what = "tagi_conv2d_bwd_delta_bn_relu";
+  TAGI_REQUIRE(mhat && J && var && mg && part, "%s: null pointer", what);
+  const int64_t need = tagi_conv2d_bwd_delta_bn_relu_part_bytes(g);
+  if (need == 0)
+    return fail(TAGI_ERR_UNSUPPORTED, "%s: needs stride 1 and an unsplit input-delta plan (use "
+                "tagi_conv2d_bwd_delta and tagi_bn_relu_bwd_partials_bias)", what);
+  TAGI_REQUIRE(part_bytes >= need, "%s: partial sums need %lld bytes (got %lld)", what, (long long)need,
+               (long long)part_bytes);
+  const BnBwdFuse f{mhat, J, var, mg, eps, part};
+  return conv_bwd_delta_impl(what, dmz, dSz, mw, nullptr, nullptr, dma, dSa, g, ws, ws_bytes, stream, &f);
 }
 
 // ============================================================== parameter deltas

@@ -194,6 +194,16 @@ struct Epi {
   float* st_J;
   float* st_ws;
   int st_nblk;
+  // kind 2, unsplit single-phase launches: the backward of a BatchNorm2D and the ReLU in
+  // front of it applied to the product (the deltas at the BatchNorm2D output), whose
+  // outputs are then the deltas at the ReLU input: m mg/sqrt(var+eps) J and
+  // v mg^2/(var+eps) J^2; st_ws receives the per-tile column sums of m mhat, v mhat^2, m,
+  // v and of the two outputs, st_ws[(q * C + col) * st_nblk + tile row]
+  const float* bn_mhat;
+  const float* bn_J;
+  const float* bn_var;
+  const float* bn_g;
+  float bn_eps;
 };
 
 struct GemmArgs {
@@ -790,7 +800,9 @@ __device__ __forceinline__ int kred_of(const GemmArgs& g, int z) {
   return ph.nkh * ph.nkw * g.a.g.Cout;
 }
 
-template <int PROD, class CFG, int KA, int KB>
+// EPI 1: the kind-2 epilogue with the BatchNorm2D -> ReLU backward folded in (a separate
+// instantiation: its extra registers would otherwise cost every kernel occupancy)
+template <int PROD, class CFG, int KA, int KB, int EPI = 0>
 __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   constexpr int BM = CFG::BM, BN = CFG::BN, BK = CFG::BK, WM = CFG::WM, WN = CFG::WN, NTH = CFG::NTH;
   constexpr int NA = (PROD == PROD_SHARED_A) ? 1 : 2;
@@ -1178,6 +1190,14 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
     // With an addend (the shortcut deltas, possibly the output itself), a lane's 16 addends
     // of a column are loaded before any of its outputs is stored: a load issued after a
     // store to a possibly aliasing address would wait for it, element by element.
+    constexpr bool bn = EPI == 1;
+    float* red = smem;  // BatchNorm sums: [BM / WM][6][BN] column sums per wave row
+    static_assert((BM / WM) * 6 * BN <= 2 * (SA + SB), "BatchNorm sums must fit the LDS tiles");
+    float bsum[TN][6];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 6; ++q) bsum[j][q] = 0.f;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       int64_t pixc[16];  // pixel offset * C, or -1 past the phase's rows
@@ -1193,6 +1213,37 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
       for (int j = 0; j < TN; ++j) {
         const int col = n0 + wn * WN + j * 32 + rl;
         if (col >= g.C) continue;
+        if constexpr (bn) {
+          // the same operations, in the same order, as the separate BatchNorm2D -> ReLU
+          // backward pass (bn_reduce_kernel MODE 4), so the outputs are identical
+          const float rv = e.bn_var[col] + e.bn_eps;
+          const float km = e.bn_g[col] * (1.0f / sqrtf(rv));
+          const float kS = e.bn_g[col] * e.bn_g[col] * (1.0f / rv);
+          float hv[16], jv[16];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            hv[v] = pixc[v] >= 0 ? e.bn_mhat[pixc[v] + col] : 0.f;
+            jv[v] = pixc[v] >= 0 ? e.bn_J[pixc[v] + col] : 0.f;
+          }
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            if (pixc[v] < 0) continue;
+            const int64_t off = pixc[v] + col;
+            const float a = accM[i][j][v], b = accV[i][j][v], h = hv[v], jj = jv[v];
+            bsum[j][0] += a * h;
+            bsum[j][1] += b * h * h;
+            bsum[j][2] += a;
+            bsum[j][3] += b;
+            float o0 = a * km, o1 = b * kS;
+            o0 = o0 * jj;
+            o1 = o1 * jj * jj;
+            bsum[j][4] += o0;
+            bsum[j][5] += o1;
+            e.om[off] = o0;
+            e.ov[off] = o1;
+          }
+          continue;
+        }
         float addm[16], addv[16];
         if (e.am) {
 #pragma unroll
@@ -1212,6 +1263,32 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
           }
           e.om[off] = m;
           e.ov[off] = vv;
+        }
+      }
+    }
+    if constexpr (bn) {
+      // lanes l and l + 32 hold the same column; then the tile's wave rows in order
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+#pragma unroll
+        for (int q = 0; q < 6; ++q) bsum[j][q] += __shfl_xor(bsum[j][q], 32, 64);
+        if (hl == 0) {
+          const int cl = wn * WN + j * 32 + rl;
+#pragma unroll
+          for (int q = 0; q < 6; ++q) red[(wm * 6 + q) * BN + cl] = bsum[j][q];
+        }
+      }
+      __syncthreads();
+      for (int cl = tid; cl < BN; cl += NTH) {
+        const int col = n0 + cl;
+        if (col < g.C) {
+#pragma unroll
+          for (int q = 0; q < 6; ++q) {
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < BM / WM; ++w) sum += red[(w * 6 + q) * BN + cl];
+            e.st_ws[((int64_t)q * g.C + col) * e.st_nblk + tmi] = sum;
+          }
         }
       }
     }
@@ -1536,12 +1613,18 @@ static inline int64_t plan_ws_bytes(const Plan& p, int64_t R, int64_t C, int64_t
   X(PROD_SHARED_A, LD_STR_K4, LD_STR_K4) X(PROD_SHARED_A, LD_STR_K4, LD_STR_MN4)         \
   X(PROD_SHARED_A, LD_STR_MN4, LD_STR_K4)
 
-template <int PROD, class CFG, int KA, int KB>
+// The input-delta loader pairs that also get the folded BatchNorm2D epilogue (EPI 1), in
+// the tile configs with one 32 x 32 tile per wave (64 x 64, 32 x 32, 128 x 32)
+#define TAGI_GEMM_COMBOS_SHARED_B_BNF(X)                                                 \
+  X(PROD_SHARED_B, LD_CBWD_A4T, LD_CBWD_BK4T) X(PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4)
+static inline bool bnf_cfg(int cfg) { return cfg == 3 || cfg == 4 || cfg == 5; }
+
+template <int PROD, class CFG, int KA, int KB, int EPI = 0>
 void launch_cfg(const GemmArgs& g, int64_t grid_x, int64_t grid_y, hipStream_t s)
 #ifdef TAGI_GEMM_DEFINE_LAUNCH
 {
-  hipLaunchKernelGGL((gemm_kernel<PROD, CFG, KA, KB>), dim3((unsigned)grid_x, (unsigned)grid_y), dim3(CFG::NTH), 0, s,
-                     g);
+  hipLaunchKernelGGL((gemm_kernel<PROD, CFG, KA, KB, EPI>), dim3((unsigned)grid_x, (unsigned)grid_y), dim3(CFG::NTH),
+                     0, s, g);
 }
 #else
     ;
@@ -1549,9 +1632,12 @@ void launch_cfg(const GemmArgs& g, int64_t grid_x, int64_t grid_y, hipStream_t s
 
 // Launch with plan p. For phased (conv input-delta) launches grid_x covers the largest
 // phase and blocks past a phase's tiles exit at once.
-template <int PROD, int KA, int KB>
+template <int PROD, int KA, int KB, int EPI = 0>
 static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, int64_t ws_bytes, hipStream_t s,
                            const char* what, int64_t grid_x_override = 0) {
+  if constexpr (EPI == 1)
+    TAGI_REQUIRE(bnf_cfg(p.cfg) && p.splits == 1, "%s: folded epilogue needs an unsplit one-tile-per-wave plan",
+                 what);
   // operand byte offsets are 32-bit with the out-of-range sentinel above them
   TAGI_REQUIRE(g.a.nbytes >= 0 && g.a.nbytes < (int64_t)kBufOutOfRange && g.b.nbytes >= 0 &&
                    g.b.nbytes < (int64_t)kBufOutOfRange,
@@ -1572,13 +1658,21 @@ static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, 
   const int64_t gy = batch * p.splits;
   TAGI_REQUIRE(gx > 0 && gx < (1ll << 31) && gy < 65536, "%s: grid out of range (%lld x %lld)", what, (long long)gx,
                (long long)gy);
-  switch (p.cfg) {
-    case 0: launch_cfg<PROD, C128x128, KA, KB>(g, gx, gy, s); break;
-    case 1: launch_cfg<PROD, C128x64, KA, KB>(g, gx, gy, s); break;
-    case 2: launch_cfg<PROD, C64x128, KA, KB>(g, gx, gy, s); break;
-    case 3: launch_cfg<PROD, C64x64, KA, KB>(g, gx, gy, s); break;
-    case 5: launch_cfg<PROD, C128x32, KA, KB>(g, gx, gy, s); break;
-    default: launch_cfg<PROD, C32x32, KA, KB>(g, gx, gy, s); break;
+  if constexpr (EPI == 1) {
+    switch (p.cfg) {
+      case 3: launch_cfg<PROD, C64x64, KA, KB, 1>(g, gx, gy, s); break;
+      case 5: launch_cfg<PROD, C128x32, KA, KB, 1>(g, gx, gy, s); break;
+      default: launch_cfg<PROD, C32x32, KA, KB, 1>(g, gx, gy, s); break;
+    }
+  } else {
+    switch (p.cfg) {
+      case 0: launch_cfg<PROD, C128x128, KA, KB>(g, gx, gy, s); break;
+      case 1: launch_cfg<PROD, C128x64, KA, KB>(g, gx, gy, s); break;
+      case 2: launch_cfg<PROD, C64x128, KA, KB>(g, gx, gy, s); break;
+      case 3: launch_cfg<PROD, C64x64, KA, KB>(g, gx, gy, s); break;
+      case 5: launch_cfg<PROD, C128x32, KA, KB>(g, gx, gy, s); break;
+      default: launch_cfg<PROD, C32x32, KA, KB>(g, gx, gy, s); break;
+    }
   }
   int rc = check_launch(what);
   if (rc != TAGI_OK) return rc;

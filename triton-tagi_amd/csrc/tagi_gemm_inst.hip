@@ -30,6 +30,11 @@ using InstCfg = C128x32;
 TAGI_GEMM_COMBOS_FWD(TAGI_INST)
 #elif TAGI_INST_PROD == 1
 TAGI_GEMM_COMBOS_SHARED_B(TAGI_INST)
+#if TAGI_INST_CFG >= 3
+#define TAGI_INST_BNF(P, KA, KB) \
+  template void launch_cfg<P, InstCfg, KA, KB, 1>(const GemmArgs&, int64_t, int64_t, hipStream_t);
+TAGI_GEMM_COMBOS_SHARED_B_BNF(TAGI_INST_BNF)
+#endif
 #else
 TAGI_GEMM_COMBOS_SHARED_A(TAGI_INST)
 #endif

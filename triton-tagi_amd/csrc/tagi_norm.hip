@@ -991,7 +991,8 @@ extern "C" int tagi_bn_bwd_finalize_multi(const tagi_bn_bwd_pending* items, int6
     TAGI_REQUIRE((p.cdmb == nullptr) == (p.cdSb == nullptr) && (p.cdmb == nullptr || p.cSb != nullptr),
                  "%s: conv bias outputs at %lld must be all given or all NULL", what, (long long)i);
     const bool cb = p.cdmb != nullptr;
-    bytes += (int64_t)red_rows(p.N * p.HW) * p.C * (cb ? 24 : 16) + (cb ? 36 : 24) * p.C;
+    TAGI_REQUIRE(p.nblk >= 0 && p.nblk < (1ll << 31), "%s: bad nblk at %lld", what, (long long)i);
+    bytes += (p.nblk > 0 ? p.nblk : (int64_t)red_rows(p.N * p.HW)) * p.C * (cb ? 24 : 16) + (cb ? 36 : 24) * p.C;
   }
   ProfScope ps(FAM_BN_BWD, s, 0.0, (double)bytes);
   for (int64_t t0 = 0; t0 < count; t0 += kBnMulti) {
@@ -1010,7 +1011,7 @@ extern "C" int tagi_bn_bwd_finalize_multi(const tagi_bn_bwd_pending* items, int6
       a.cdmb[c] = p.cdmb;
       a.cdSb[c] = p.cdSb;
       a.C[c] = (int)p.C;
-      a.nblk[c] = red_rows(p.N * p.HW);
+      a.nblk[c] = p.nblk > 0 ? (int)p.nblk : red_rows(p.N * p.HW);
       a.start[c] = blocks;
       blocks += (int)p.C;
     }

@@ -50,7 +50,7 @@ class BnPending(ctypes.Structure):
 
     _fields_ = [(n, c_void_p) for n in ("ws", "Sg", "Sb", "dmg", "dSg", "dmb", "dSb")] + [
         (n, c_int64) for n in ("N", "C", "HW")
-    ] + [(n, c_void_p) for n in ("cSb", "cdmb", "cdSb")]
+    ] + [(n, c_void_p) for n in ("cSb", "cdmb", "cdSb")] + [("nblk", c_int64)]
 
 
 VP = POINTER(TagiView)
@@ -88,6 +88,8 @@ _SIGS = {
     "tagi_conv2d_bwd_delta": (c_int, [P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_bwd_delta_ws_bytes": (I64, [GP]),
     "tagi_conv2d_bwd_delta_add": (c_int, [P, P, P, P, P, P, P, GP, P, I64, P]),
+    "tagi_conv2d_bwd_delta_bn_relu": (c_int, [P, P, P, P, P, P, P, F, P, P, P, I64, GP, P, I64, P]),
+    "tagi_conv2d_bwd_delta_bn_relu_part_bytes": (I64, [GP]),
     "tagi_conv2d_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_wgrad_ws_bytes": (I64, [GP]),
     "tagi_relu_fwd": (c_int, [P, P, P, P, P, I64, P]),

@@ -94,15 +94,44 @@ class Conv2D(LearnableLayer):
         """The parameter deltas of ``backward`` without forming the input deltas."""
         self._backward(delta_mz, delta_Sz, False)
 
-    def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool,
-                  add: tuple[Tensor, Tensor] | None = None):
-        """Parameter deltas, then (if asked) the input deltas, plus ``add`` when given."""
+    def _output_deltas(self, delta_mz: Tensor, delta_Sz: Tensor):
+        """The geometry and the output deltas as channels-last (N, C_out, Ho, Wo) tensors."""
         N, C, H, W = self.input_shape
         g = self._geom(N, C, H, W)
         dmz = _lib.check(_lib.channels_last(delta_mz.reshape(N, self.C_out, g.Ho, g.Wo)), "delta_mz")
         dSz = _lib.check(_lib.channels_last(delta_Sz.reshape(N, self.C_out, g.Ho, g.Wo)), "delta_Sz")
         if tuple(dmz.shape) != (N, self.C_out, g.Ho, g.Wo):
             raise ValueError(f"Conv2D.backward: delta shape {tuple(dmz.shape)} != output shape")
+        return g, dmz, dSz
+
+    def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool,
+                  add: tuple[Tensor, Tensor] | None = None):
+        """Parameter deltas, then (if asked) the input deltas, plus ``add`` when given."""
+        N, C, H, W = self.input_shape
+        g, dmz, dSz = self._output_deltas(delta_mz, delta_Sz)
+        self._param_deltas(g, dmz, dSz)
+        if not input_deltas:
+            return None
+        dev = dmz.device
+        st = _lib.stream_of(dmz)
+        d_ma = _lib.empty_cl(N, C, H, W, dev)
+        d_Sa = _lib.empty_cl(N, C, H, W, dev)
+        ws = _lib.workspace(_lib.query("tagi_conv2d_bwd_delta_ws_bytes", g), dev)
+        wp, wb = _lib.ws_args(ws)
+        if add is None:
+            _lib.call("tagi_conv2d_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), self.mw.data_ptr(), d_ma.data_ptr(),
+                      d_Sa.data_ptr(), g, wp, wb, st)
+        else:
+            am = _lib.check(_lib.like(add[0].reshape(N, C, H, W), d_ma), "add_m")
+            aS = _lib.check(_lib.like(add[1].reshape(N, C, H, W), d_ma), "add_S")
+            _lib.call("tagi_conv2d_bwd_delta_add", dmz.data_ptr(), dSz.data_ptr(), self.mw.data_ptr(),
+                      am.data_ptr(), aS.data_ptr(), d_ma.data_ptr(), d_Sa.data_ptr(), g, wp, wb, st)
+        return d_ma, d_Sa
+
+    def _param_deltas(self, g, dmz: Tensor, dSz: Tensor) -> None:
+        """delta_mw / delta_Sw (and the bias deltas unless a fused pass formed them), on the
+        side stream of an overlapped step when the product is large."""
+        N = self.input_shape[0]
         dev = dmz.device
         K = self.C_in * self.kH * self.kW
         ctx = _overlap.active()
@@ -124,22 +153,6 @@ class Conv2D(LearnableLayer):
                       self.Sb.data_ptr(), self.delta_mw.data_ptr(), self.delta_Sw.data_ptr(),
                       None if bias_done else self.delta_mb.data_ptr(),
                       None if bias_done else self.delta_Sb.data_ptr(), g, wp, wb, _lib.stream_of(dmz))
-        st = _lib.stream_of(dmz)
-        if not input_deltas:
-            return None
-        d_ma = _lib.empty_cl(N, C, H, W, dev)
-        d_Sa = _lib.empty_cl(N, C, H, W, dev)
-        ws = _lib.workspace(_lib.query("tagi_conv2d_bwd_delta_ws_bytes", g), dev)
-        wp, wb = _lib.ws_args(ws)
-        if add is None:
-            _lib.call("tagi_conv2d_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), self.mw.data_ptr(), d_ma.data_ptr(),
-                      d_Sa.data_ptr(), g, wp, wb, st)
-        else:
-            am = _lib.check(_lib.like(add[0].reshape(N, C, H, W), d_ma), "add_m")
-            aS = _lib.check(_lib.like(add[1].reshape(N, C, H, W), d_ma), "add_S")
-            _lib.call("tagi_conv2d_bwd_delta_add", dmz.data_ptr(), dSz.data_ptr(), self.mw.data_ptr(),
-                      am.data_ptr(), aS.data_ptr(), d_ma.data_ptr(), d_Sa.data_ptr(), g, wp, wb, st)
-        return d_ma, d_Sa
 
     def _update_items(self):
         return [(self.mw, self.Sw, self.delta_mw, self.delta_Sw), (self.mb, self.Sb, self.delta_mb, self.delta_Sb)]

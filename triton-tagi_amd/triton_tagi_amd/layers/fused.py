@@ -12,7 +12,8 @@ in how often activations cross HBM:
   epilogue (conv2d.py:254-309): the output moments are not read back for the statistics.
 * The residual add that closes a block (resblock.py:380) is folded into that second pass.
 * Backward through BatchNorm2D and the ReLU in front of it (batchnorm2d.py:465-513,
-  relu.py:152-169) is one pass.
+  relu.py:152-169) is one pass; within ``Sequential.step``, where a stride-1 Conv2D
+  follows the pair, that pass is the epilogue of the Conv2D's input-delta GEMM.
 * The merge of the shortcut deltas into the main branch (resblock.py:421-423) is folded
   into the input-delta GEMM of the block's first convolution.
 
@@ -50,14 +51,16 @@ class defer_bn_parameter_deltas:
         _scope.ctx = self
         return self
 
-    def add(self, bn: BatchNorm2D, ws: Tensor, N: int, C: int, HW: int, conv: Conv2D | None = None) -> None:
-        """``conv``: the Conv2D in front of the ReLU, whose bias sums ``ws`` also holds."""
+    def add(self, bn: BatchNorm2D, ws: Tensor, N: int, C: int, HW: int, conv: Conv2D | None = None,
+            nblk: int = 0) -> None:
+        """``conv``: the Conv2D in front of the ReLU, whose bias sums ``ws`` also holds;
+        ``nblk``: partial sums per channel and quantity (0: the BatchNorm pass's own count)."""
         self._keep.append(ws)  # the partial sums must outlive the launch below
         cb = (None, None, None) if conv is None else (conv.Sb.data_ptr(), conv.delta_mb.data_ptr(),
                                                       conv.delta_Sb.data_ptr())
         self.items.append(_lib.BnPending(ws.data_ptr(), bn.Sw.data_ptr(), bn.Sb.data_ptr(), bn.delta_mw.data_ptr(),
                                          bn.delta_Sw.data_ptr(), bn.delta_mb.data_ptr(), bn.delta_Sb.data_ptr(),
-                                         N, C, HW, *cb))
+                                         N, C, HW, *cb, nblk))
         self._stream = _lib.stream_of(ws)
 
     def __exit__(self, exc_type, exc, tb):
@@ -201,6 +204,50 @@ def bn_relu_backward(bn: BatchNorm2D, relu: ReLU, delta_ma: Tensor, delta_Sa: Te
     return dmz, dSz
 
 
+def conv_bn_relu_backward(conv: Conv2D, bn: BatchNorm2D, relu: ReLU, conv_prev: Conv2D, delta_ma: Tensor,
+                          delta_Sa: Tensor) -> tuple[Tensor, Tensor] | None:
+    """``conv.backward`` followed by ``bn_relu_backward(bn, relu, ..., conv_prev)`` for the
+    layer order conv_prev -> relu -> bn -> conv, with the BatchNorm2D -> ReLU backward
+    folded into the epilogue of conv's input-delta GEMM: the deltas at the BatchNorm2D
+    output are never written. Within ``defer_bn_parameter_deltas`` only (the pass leaves
+    its partial sums pending, conv_prev's bias sums among them); returns None, having done
+    nothing, where the fold does not apply (then the caller runs the two steps)."""
+    ctx = getattr(_scope, "ctx", None)
+    if ctx is None or conv_prev.mb is None or bn.m_hat is None or relu.J is None:
+        return None
+    N, C, H, W = conv.input_shape
+    if (conv_prev.C_out != C or tuple(bn.input_shape) != (N, C, H, W) or tuple(bn.m_hat.shape) != (N, C, H, W)
+            or tuple(relu.J.shape) != (N, C, H, W)):
+        return None
+    g = conv._geom(N, C, H, W)
+    part_bytes = _lib.query("tagi_conv2d_bwd_delta_bn_relu_part_bytes", g)
+    if part_bytes <= 0:
+        return None
+    g, dmz, dSz = conv._output_deltas(delta_ma, delta_Sa)
+    conv._param_deltas(g, dmz, dSz)
+    dev = dmz.device
+    d_ma = _lib.empty_cl(N, C, H, W, dev)
+    d_Sa = _lib.empty_cl(N, C, H, W, dev)
+    mhat = _lib.check(_lib.like(bn.m_hat, d_ma), "m_hat")
+    J = _lib.check(_lib.like(relu.J, d_ma), "J")
+    bn.delta_mw = torch.empty(C, device=dev, dtype=torch.float32)
+    bn.delta_Sw = torch.empty_like(bn.delta_mw)
+    bn.delta_mb = torch.empty_like(bn.delta_mw)
+    bn.delta_Sb = torch.empty_like(bn.delta_mw)
+    conv_prev.delta_mb = torch.empty(1, C, device=dev, dtype=torch.float32)
+    conv_prev.delta_Sb = torch.empty_like(conv_prev.delta_mb)
+    part = _lib.workspace(part_bytes, dev)
+    ws = _lib.workspace(_lib.query("tagi_conv2d_bwd_delta_ws_bytes", g), dev)
+    wp, wb = _lib.ws_args(ws)
+    _lib.call("tagi_conv2d_bwd_delta_bn_relu", dmz.data_ptr(), dSz.data_ptr(), conv.mw.data_ptr(), mhat.data_ptr(),
+              J.data_ptr(), _lib.check(bn._norm_var, "norm_var").data_ptr(), _lib.check(bn.mw, "mw").data_ptr(),
+              float(bn.eps), d_ma.data_ptr(), d_Sa.data_ptr(), part.data_ptr(), part_bytes, g, wp, wb,
+              _lib.stream_of(dmz))
+    ctx.add(bn, part, N, C, H * W, conv=conv_prev, nblk=part_bytes // (24 * C))
+    conv_prev._bias_deltas_pending = True
+    return d_ma, d_Sa
+
+
 def _fusable_forward(layer, nxt, mu: Tensor) -> bool:
     return isinstance(layer, ReLU) and isinstance(nxt, BatchNorm2D) and nxt.training and mu.dim() == 4
 
@@ -253,6 +300,13 @@ def backward_chain(layers, delta_mu: Tensor, delta_var: Tensor, add: tuple[Tenso
     while i >= 0:
         layer = layers[i]
         prev = layers[i - 1] if i >= 1 else None
+        if (isinstance(layer, Conv2D) and i >= 3 and _fusable_backward(prev, layers[i - 2])
+                and isinstance(layers[i - 3], Conv2D)):
+            out = conv_bn_relu_backward(layer, prev, layers[i - 2], layers[i - 3], delta_mu, delta_var)
+            if out is not None:
+                delta_mu, delta_var = out
+                i -= 3
+                continue
         if _fusable_backward(layer, prev):
             conv = layers[i - 2] if i >= 2 and isinstance(layers[i - 2], Conv2D) else None
             delta_mu, delta_var = bn_relu_backward(layer, prev, delta_mu, delta_var, conv)
