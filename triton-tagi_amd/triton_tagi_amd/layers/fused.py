@@ -224,6 +224,8 @@ def conv_bn_relu_backward(conv: Conv2D, bn: BatchNorm2D, relu: ReLU, conv_prev: 
     if part_bytes <= 0:
         return None
     g, dmz, dSz = conv._output_deltas(delta_ma, delta_Sa)
+    if any(t.data_ptr() % 16 for t in (dmz, dSz, conv.mw)):
+        return None  # the fold reads the deltas and weights as float4
     conv._param_deltas(g, dmz, dSz)
     dev = dmz.device
     d_ma = _lib.empty_cl(N, C, H, W, dev)
