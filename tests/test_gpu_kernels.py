@@ -512,6 +512,33 @@ def test_attention_fwd_fused(dev, B, H, S, D):
     assert_scaled_close(fS, rS, rS, 1e-5, 1e-7, "out var")
 
 
+def test_attention_scores_rebuilt_after_fused_forward(dev):
+    """The fused attention forward keeps only the score means; get_attention_scores rebuilds
+    the variances with tagi_attn_scores_remax from the kept projections. Both halves must be
+    the values that kernel forms from those projections, bit for bit."""
+    import math
+
+    from triton_tagi_amd import _lib
+    from triton_tagi_amd.layers import MultiheadAttentionV2
+
+    torch.manual_seed(3)
+    B, S, E, H = 2, 256, 256, 8
+    att = MultiheadAttentionV2(E, H, S, device=dev)
+    r = g(3)
+    ma, Sa = torch.randn(B, S, E, generator=r).to(dev), (0.1 * torch.rand(B, S, E, generator=r)).to(dev)
+    att.forward(ma, Sa)
+    qkv_m, qkv_S, _, _ = att._attn_src
+    msc, vsc = att.get_attention_scores()
+    D = E // H
+    sc = 1.0 / math.sqrt(D)
+    rm, rv, rj = (torch.empty(B, H, S, S, device=dev) for _ in range(3))
+    q_m, q_S = qkv_m.data_ptr(), qkv_S.data_ptr()
+    _lib.call("tagi_attn_scores_remax", q_m, q_S, q_m + 4 * E, q_S + 4 * E, 3 * E, rm.data_ptr(), rv.data_ptr(),
+              rj.data_ptr(), B, H, S, D, sc, sc * sc, _lib.stream_of(qkv_m))
+    assert torch.equal(msc, rm) and torch.equal(vsc, rv)
+    assert torch.equal(att._cache["jcb"], rj)
+
+
 @pytest.mark.parametrize("B,H,S,D", [(2, 8, 256, 32), (1, 2, 40, 16), (2, 2, 100, 32), (1, 3, 1, 32)])
 def test_attention_score_deltas_qk_fused(dev, B, H, S, D):
     """tagi_attn_score_deltas_qk (the Jacobian-scaled score deltas formed per block in LDS,
