@@ -299,6 +299,28 @@ def close_unfused_rel(a, b, rtol, what):
     assert err <= lim, f"{what}: folded vs two-call max err {err:.3e} > {lim:.3e}"
 
 
+def test_bn_fold_taken_in_step(dev, monkeypatch):
+    """Within Sequential.step on ResNet-18 (batch 16) the BatchNorm2D -> ReLU backward of
+    each stage-1 block's first BatchNorm2D runs inside the second conv's input-delta GEMM
+    (the fold applies there: stride 1, unsplit plan), so the step exercises that path."""
+    from triton_tagi_amd import workloads
+    from triton_tagi_amd.layers import fused
+
+    taken = []
+    orig = fused.conv_bn_relu_backward
+
+    def counting(*a, **k):
+        out = orig(*a, **k)
+        taken.append(out is not None)
+        return out
+
+    monkeypatch.setattr(fused, "conv_bn_relu_backward", counting)
+    w = workloads.build("resnet18", device="cuda:0", batch=16)
+    w.net.step(w.x, w.y, w.sigma_v)
+    torch.cuda.synchronize()
+    assert len(taken) == 8 and sum(taken) >= 2, taken
+
+
 def test_fused_step_matches_oracle(dev):
     """Sequential.step (fused passes) on ResNet-18 at batch 16 against the oracle's step:
     predictions, every updated parameter and the BN running statistics."""
