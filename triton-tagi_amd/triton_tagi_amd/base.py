@@ -23,6 +23,11 @@ class Layer(ABC):
     def backward(self, delta_ma: Tensor, delta_Sa: Tensor) -> tuple[Tensor, Tensor]:
         """Propagate innovation deltas backward; return the deltas for the previous layer."""
 
+    def sublayers(self) -> tuple:
+        """Layers held inside this one (a residual block's branches, an attention layer's
+        projections); containers walk them to place or visit every parameter tensor."""
+        return ()
+
 
 class LearnableLayer(Layer):
     """Base class for layers with parameters updated by the capped TAGI rule."""

@@ -22,6 +22,7 @@ from .. import _lib, _overlap
 from ..base import LearnableLayer
 from ..param_init import init_weight_bias_conv2d
 from ..update.parameters import update_parameters
+from ._bn_pending import bias_deltas_formed
 
 
 class Conv2D(LearnableLayer):
@@ -45,8 +46,6 @@ class Conv2D(LearnableLayer):
         self.input_shape = None
         self.spatial = None
         self.delta_mw = self.delta_Sw = self.delta_mb = self.delta_Sb = None
-        # set by a fused BatchNorm2D -> ReLU backward pass that forms this layer's bias deltas
-        self._bias_deltas_pending = False
 
     def _geom(self, N, C, H, W) -> _lib.ConvGeom:
         k, s, p = self.kH, self.stride, self.padding
@@ -138,8 +137,7 @@ class Conv2D(LearnableLayer):
         big = N * g.Ho * g.Wo * K * self.C_out >= _overlap.MIN_MACS_CONV
         # bias deltas already formed by the fused BatchNorm2D -> ReLU pass that produced these
         # deltas (finalized with the BatchNorm parameter deltas): no bias row in the GEMM
-        bias_done = self._bias_deltas_pending
-        self._bias_deltas_pending = False
+        bias_done = bias_deltas_formed(self)
         side = ctx.fork(dev, self.ma_in, dmz, dSz) if ctx is not None and big else None
         with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
             self.delta_mw = torch.empty(K, self.C_out, device=dev, dtype=torch.float32)

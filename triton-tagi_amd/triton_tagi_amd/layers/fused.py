@@ -24,54 +24,15 @@ working after a fused pass.
 
 from __future__ import annotations
 
-import threading
-
 import torch
 from torch import Tensor
 
 from .. import _lib
+from ._bn_pending import active as _active_defer
+from ._bn_pending import defer_bn_parameter_deltas  # noqa: F401  (re-exported)
 from .batchnorm2d import BatchNorm2D
 from .conv2d import Conv2D
 from .relu import ReLU
-
-
-_scope = threading.local()
-
-
-class defer_bn_parameter_deltas:
-    """Within this context the fused BatchNorm2D -> ReLU backward passes leave their
-    per-channel partial sums pending; leaving it forms the parameter deltas of all of them
-    in one launch (``Sequential.step`` wraps its backward pass in it). The layers'
-    ``delta_*`` tensors are complete once the context has exited."""
-
-    def __enter__(self):
-        self.items = []
-        self._keep = []
-        self._outer = getattr(_scope, "ctx", None)
-        _scope.ctx = self
-        return self
-
-    def add(self, bn: BatchNorm2D, ws: Tensor, N: int, C: int, HW: int, conv: Conv2D | None = None,
-            nblk: int = 0) -> None:
-        """``conv``: the Conv2D in front of the ReLU, whose bias sums ``ws`` also holds;
-        ``nblk``: partial sums per channel and quantity (0: the BatchNorm pass's own count)."""
-        self._keep.append(ws)  # the partial sums must outlive the launch below
-        cb = (None, None, None) if conv is None else (conv.Sb.data_ptr(), conv.delta_mb.data_ptr(),
-                                                      conv.delta_Sb.data_ptr())
-        self.items.append(_lib.BnPending(ws.data_ptr(), bn.Sw.data_ptr(), bn.Sb.data_ptr(), bn.delta_mw.data_ptr(),
-                                         bn.delta_Sw.data_ptr(), bn.delta_mb.data_ptr(), bn.delta_Sb.data_ptr(),
-                                         N, C, HW, *cb, nblk))
-        self._stream = _lib.stream_of(ws)
-
-    def __exit__(self, exc_type, exc, tb):
-        _scope.ctx = self._outer
-        if exc_type is None and self.items:
-            # on the stream current at exit (every pending layer's partial sums are ordered
-            # before it: side-stream work has been joined by then)
-            arr = (_lib.BnPending * len(self.items))(*self.items)
-            _lib.call("tagi_bn_bwd_finalize_multi", arr, len(self.items),
-                      torch.cuda.current_stream(self._keep[0].device).cuda_stream)
-        return False
 
 
 def _add_in_place(src_m: Tensor, src_S: Tensor, dst_m: Tensor, dst_S: Tensor) -> None:
@@ -179,7 +140,7 @@ def bn_relu_backward(bn: BatchNorm2D, relu: ReLU, delta_ma: Tensor, delta_Sa: Te
     bn.delta_Sb = torch.empty_like(bn.delta_mw)
     ws = _lib.workspace(_lib.query("tagi_bn_bwd_ws_bytes", N, C, HW), dev)
     wp, wb = _lib.ws_args(ws)
-    ctx = getattr(_scope, "ctx", None)
+    ctx = _active_defer()
     if ctx is not None and conv is not None and conv.C_out == C and conv.mb is not None:
         conv.delta_mb = torch.empty(1, C, device=dev, dtype=torch.float32)
         conv.delta_Sb = torch.empty_like(conv.delta_mb)
@@ -189,7 +150,6 @@ def bn_relu_backward(bn: BatchNorm2D, relu: ReLU, delta_ma: Tensor, delta_Sa: Te
                   J.data_ptr(), bn._norm_var.data_ptr(), bn.mw.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), N, C, HW,
                   float(bn.eps), wp, wb, _lib.stream_of(dma))
         ctx.add(bn, ws, N, C, HW, conv=conv)
-        conv._bias_deltas_pending = True
         return dmz, dSz
     if ctx is not None:
         _lib.call("tagi_bn_relu_bwd_partials", dma.data_ptr(), dSa.data_ptr(), bn.m_hat.data_ptr(), J.data_ptr(),
@@ -212,7 +172,7 @@ def conv_bn_relu_backward(conv: Conv2D, bn: BatchNorm2D, relu: ReLU, conv_prev: 
     output are never written. Within ``defer_bn_parameter_deltas`` only (the pass leaves
     its partial sums pending, conv_prev's bias sums among them); returns None, having done
     nothing, where the fold does not apply (then the caller runs the two steps)."""
-    ctx = getattr(_scope, "ctx", None)
+    ctx = _active_defer()
     if ctx is None or conv_prev.mb is None or bn.m_hat is None or relu.J is None:
         return None
     N, C, H, W = conv.input_shape
@@ -246,7 +206,6 @@ def conv_bn_relu_backward(conv: Conv2D, bn: BatchNorm2D, relu: ReLU, conv_prev: 
               float(bn.eps), d_ma.data_ptr(), d_Sa.data_ptr(), part.data_ptr(), part_bytes, g, wp, wb,
               _lib.stream_of(dmz))
     ctx.add(bn, part, N, C, H * W, conv=conv_prev, nblk=part_bytes // (24 * C))
-    conv_prev._bias_deltas_pending = True
     return d_ma, d_Sa
 
 

@@ -82,6 +82,9 @@ class MultiheadAttentionV2(LearnableLayer):
     def _projections(self):
         return (self.q_proj, self.k_proj, self.v_proj)
 
+    def sublayers(self) -> tuple:
+        return self._projections()
+
     def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
         B, S, E = ma.shape
         if E != self.embed_dim:

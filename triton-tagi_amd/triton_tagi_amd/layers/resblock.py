@@ -89,6 +89,9 @@ class ResBlock(LearnableLayer):
         if self.use_projection:
             self._learnable.extend([self.proj_conv, self.proj_bn])
 
+    def sublayers(self) -> tuple:
+        return tuple(self._main_layers + self._proj_layers)
+
     def train(self) -> None:
         self.training = True
         for layer in self._learnable:

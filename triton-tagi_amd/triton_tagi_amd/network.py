@@ -19,50 +19,42 @@ from .base import Layer, LearnableLayer
 from .layers.conv2d import Conv2D
 from .layers.fused import backward_chain, defer_bn_parameter_deltas, forward_chain
 from .layers.multihead_attention import MultiheadAttentionV2
-from .layers.resblock import ResBlock
 from .update.observation import compute_innovation, hrc_innovation
 from .update.parameters import get_cap_factor, update_parameters_multi
+
+
+# Per-layer state that lives on the network's device: parameters, BatchNorm running
+# statistics, the positional-encoding table. Anything else a layer holds is formed on
+# the device of the tensors it is given.
+_PLACED_STATE = ("mw", "Sw", "mb", "Sb", "running_mean", "running_var", "pe_cache")
+
+
+def _all_layers(layers):
+    """Every layer of the list, each followed by the layers nested inside it."""
+    for layer in layers:
+        yield layer
+        nested = getattr(layer, "sublayers", None)
+        if nested is not None:
+            yield from _all_layers(nested())
 
 
 class Sequential:
     overlap_param_deltas = True  # Conv2D parameter-delta GEMMs on a side stream within step()
 
     def __init__(self, layers: list, device: str = "cuda") -> None:
+        """Holds ``layers`` in order and places every state tensor they (and the layers
+        nested in them) hold on ``device``; layers that record a device are told it."""
         self.device = torch.device(device)
         self.layers = layers
-        for layer in self.layers:
-            if isinstance(layer, ResBlock):
+        for layer in _all_layers(layers):
+            if hasattr(layer, "device"):
                 layer.device = self.device
-                for sub in layer._learnable:
-                    self._move_layer_to_device(sub)
-            elif isinstance(layer, LearnableLayer):
-                self._move_layer_to_device(layer)
-            if hasattr(layer, "running_mean"):
-                layer.running_mean = layer.running_mean.to(self.device)
-                layer.running_var = layer.running_var.to(self.device)
-            if getattr(layer, "pe_cache", None) is not None:
-                layer.pe_cache = layer.pe_cache.to(self.device)
-                layer.device = self.device
-
-    def _move_layer_to_device(self, layer):
-        if isinstance(layer, MultiheadAttentionV2):
-            layer.device = self.device
-            for sub in (layer.q_proj, layer.k_proj, layer.v_proj):
-                self._move_layer_to_device(sub)
-            return
-        if not hasattr(layer, "mw") or layer.mw is None:
-            return
-        layer.device = self.device
-        layer.mw = layer.mw.to(self.device)
-        if getattr(layer, "Sw", None) is not None:
-            layer.Sw = layer.Sw.to(self.device)
-        if getattr(layer, "mb", None) is not None:
-            layer.mb = layer.mb.to(self.device)
-            if getattr(layer, "Sb", None) is not None:
-                layer.Sb = layer.Sb.to(self.device)
-        if getattr(layer, "running_mean", None) is not None:
-            layer.running_mean = layer.running_mean.to(self.device)
-            layer.running_var = layer.running_var.to(self.device)
+            if isinstance(layer, Layer) and layer.sublayers():
+                continue  # a container's parameters are its nested layers' (ResBlock only aliases them)
+            for name in _PLACED_STATE:
+                t = getattr(layer, name, None)
+                if isinstance(t, torch.Tensor):
+                    setattr(layer, name, t.to(self.device))
 
     def forward(self, x: Tensor) -> tuple[Tensor, Tensor]:
         """Layer-by-layer moment propagation from a deterministic input (S_a = 0)."""
