@@ -92,8 +92,11 @@ int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N);
 /* tagi_linear_fwd with no workspace argument that allocates nothing. No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). The split-K
- * partial sums go to a fixed device array of TAGI_LINEAR_FWD_NOALLOC_SCRATCH_BYTES that
- * each GPU holds from the first call on it until the process ends. Same plan and kernels
+ * partial sums go to a fixed device array of TAGI_LINEAR_FWD_NOALLOC_SCRATCH_BYTES, alone
+ * in a code object of its own: the HIP runtime allocates it on a GPU when it loads that
+ * code object there, which with its default deferred loading is this entry point's first
+ * call on that GPU (with HIP_ENABLE_DEFERRED_LOADING=0, when the library is loaded), and
+ * the GPU keeps it until the process ends. Same plan and kernels
  * as tagi_linear_fwd given its full workspace, so the same results bit for bit; a shape
  * whose partials exceed the scratch returns TAGI_ERR_ARG before launching anything. The
  * stream's device must be the current device. Calls that overlap on one GPU (several

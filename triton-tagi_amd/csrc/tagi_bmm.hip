@@ -131,12 +131,15 @@ extern "C" int tagi_bmm_shared_jacobian(const float* p0, const float* p1, const 
 // lane half hl taking k = 16t + 8hl + s, so the scores are bit-identical to that path's),
 // held in LDS and passed through the Remax row by row (the row math of tagi_remax_fwd).
 // The raw scores never reach HBM: per head, 2 S x S tensors are neither written nor read
-// back. Eight waves (two blocks per CU fit the 64 KB tile, 4 waves per SIMD to hide the
-// Remax's dependent VALU chains): wave w forms column tile w (S <= 256), then applies the
-// Remax to rows 4w .. 4w + 3 of the block.
+// back. Eight waves (4 waves per SIMD at two blocks per CU, to hide the Remax's dependent
+// VALU chains): wave w forms column tile w (S <= 256), then applies the Remax to rows
+// 4w .. 4w + 3 of the block. The LDS tile is 2 x 32 x 257 floats = 65,792 bytes, more than
+// the 64 KiB a workgroup may use on earlier CDNA parts: these kernels rely on gfx950's
+// 160 KiB of LDS per CU (two blocks per CU), and the library is built for gfx950 only.
 namespace {
 constexpr int kScoreLd = 257;  // padded LDS row (S <= 256): conflict-free row reads
 constexpr int kScorePlane = 32 * kScoreLd;
+static_assert(2 * 2 * kScorePlane * sizeof(float) <= 160 * 1024, "two score tiles must fit one CU's LDS");
 
 // Scores of query rows r0 .. r0+31 of head (b, h) against all S keys into sm: means in
 // rows 0..31, variances in rows 32..63 (row stride kScoreLd). hbase: offset of the head's
