@@ -8,6 +8,12 @@ namespace tagi {
 #define INV_SQRT_2 0.7071067811865476f
 
 // ------------------------------------------------------------------------ fast fp32 math
+// The moment helpers below turn off the compiler's implicit contraction of a * b + c into
+// fused multiply-adds (#pragma clang fp contract(off)) and write every fused multiply-add
+// they use as fmaf: whether an implicit contraction happens depends on the code around
+// the inlined helper, and kernels that share the row math (the fused attention forward
+// and the two-call Remax, the conv epilogue's ReLU statistics and the ReLU/BatchNorm
+// pass) must round the same way to give the same bits.
 // The hardware transcendental instructions (v_rcp_f32, v_rsq_f32, v_exp_f32, v_log_f32)
 // are accurate to about 1 ulp on normal operands. The library forms add range reduction,
 // denormal scaling and correct rounding that the moment formulas below do not need: their
@@ -21,10 +27,11 @@ __device__ __forceinline__ float fast_div(float a, float b) { return a * __built
 // result: 2^(p + e) = 2^p (1 + e ln 2) to second order in e. Relative error about 2 ulp
 // for results above 2^-126; smaller results (x < -87.3) flush to 0.
 __device__ __forceinline__ float fast_exp(float x) {
+#pragma clang fp contract(off)
   const float L2E = 1.44269502162933349609375f;   // log2(e) rounded to fp32
   const float L2E_LO = 1.925963033500011e-8f;     // log2(e) - L2E
   const float p = x * L2E;
-  const float e = fmaf(x, L2E, -p) + x * L2E_LO;
+  const float e = fmaf(x, L2E_LO, fmaf(x, L2E, -p));
   return __builtin_amdgcn_exp2f(p) * fmaf(e, 0.6931471805599453f, 1.0f);
 }
 
@@ -92,10 +99,107 @@ __device__ __forceinline__ void normal_cdf_pair(float alpha, float& cdf, float& 
 // The identity holds for any Phi value (it only uses mu = sigma phi + mz Phi), so it also
 // covers the asymptotic branch; the second form has no O(alpha^2) cancellation in fp32.
 __device__ __forceinline__ float rect_var(float S, float alpha, float pdf, float cdf, float Q) {
+#pragma clang fp contract(off)
   return S * (cdf + alpha * alpha * cdf * Q + alpha * pdf * (Q - cdf) - pdf * pdf);
 }
 
+// 1 - x R(x) and (1 + x^2) R(x) - x for x >= 2, where R = Q / phi is the Mills ratio.
+// They are about 1/x^2 and 2/x^3, differences of terms near 1 and x: formed from R they
+// would carry R's relative rounding multiplied by about x^2 and x^4 / 2 (1e-4 of the
+// variance near x = 4). They are evaluated from their own fits instead, g1 = x^2 u1 and
+// g2 = x^3 u2 / 2 (both tend to 1 as x grows) as polynomials in t = 1 / (1 + x / (2 sqrt 2)),
+// the variable of the erfc fit, t in (0, 0.586] for x >= 2: least squares on Chebyshev
+// nodes of values computed at 90 digits (gen_mills_fit.py next to this file), relative
+// error 6e-8 / 9e-8 in exact arithmetic and below 2e-7 / 4e-7 in fp32 Horner evaluation.
+// No cancellation at any x: t = 0 (x = inf) gives u1 = u2 = 0.
+__device__ __forceinline__ void mills_differences(float a, float t, float& u1, float& u2) {
+#pragma clang fp contract(off)
+  float g1 = 4.963217913e-02f;
+  g1 = fmaf(g1, t, -3.676841643e+00f);
+  g1 = fmaf(g1, t, 7.277117302e+00f);
+  g1 = fmaf(g1, t, -2.912598560e+00f);
+  g1 = fmaf(g1, t, 3.630294165e-01f);
+  g1 = fmaf(g1, t, -1.046916153e+00f);
+  g1 = fmaf(g1, t, -7.352366037e-01f);
+  g1 = fmaf(g1, t, -3.756972988e-01f);
+  g1 = fmaf(g1, t, 1.265216389e-05f);
+  g1 = fmaf(g1, t, 9.999999624e-01f);
+  float g2 = 1.280788407e+01f;
+  g2 = fmaf(g2, t, -2.014247635e+01f);
+  g2 = fmaf(g2, t, -3.991492743e+00f);
+  g2 = fmaf(g2, t, 1.672760442e+01f);
+  g2 = fmaf(g2, t, -3.405939506e+00f);
+  g2 = fmaf(g2, t, 1.312790107e+00f);
+  g2 = fmaf(g2, t, -1.765867478e+00f);
+  g2 = fmaf(g2, t, -1.482223791e+00f);
+  g2 = fmaf(g2, t, -7.507189017e-01f);
+  g2 = fmaf(g2, t, 1.112854611e-05f);
+  g2 = fmaf(g2, t, 9.999999719e-01f);
+  const float r = fast_rcp(a);
+  const float r2 = r * r;
+  u1 = g1 * r2;
+  u2 = 2.0f * g2 * r2 * r;
+}
+
+// Moments of max(z, 0) for z ~ N(mz, S), sd = sqrt(S), alpha = mz / sd, without the
+// fp32 cancellation of their two terms for alpha < 0 (layers/remax.py:60-75 in exact
+// arithmetic). Out: mean, variance and Phi(alpha) (the density pdf is returned too).
+// With a = |alpha|, the Chebyshev fit of normal_tail writes Q(a) = 0.5 t exp(-a^2/2 + P(t));
+// its part without the Gaussian factor is the Mills ratio R(a) = Q(a) / phi(a) =
+// sqrt(pi/2) t exp(P(t)), so the tail is phi(a) R(a), one exp(-a^2/2) shared by the density
+// and the tail. For alpha = -x < 0, with Phi = phi R:
+//   mean     = mz Phi + sd phi                         = sd phi (1 - x R)
+//   variance = S [Phi + alpha^2 Phi Q + alpha phi (Q - Phi) - phi^2]
+//            = S phi [((1 + x^2) R - x) - phi (1 - x R)^2]
+// 1 - x R (about 1/x^2) and (1 + x^2) R - x (about 2/x^3) cancel by about x^2 and x^4 / 2.
+// Below x = 2 (at most 8-fold) they are formed from R with exact products (fma), so the
+// cancellation meets only R's own rounding (a few 1e-7) and not the independent roundings
+// of two exponentials; from x = 2 on they come from fits of their own
+// (mills_differences), without cancellation. Either way the variance near alpha = -4,
+// which sits just above the Remax's 1e-6 floor there and sets its Jacobian, keeps the
+// relative accuracy of its terms (the density and the tail formed independently gave
+// 1e-4 of it). For alpha >= 0 the terms do not cancel and the forms are the reference's
+// (mean) and rect_var's (variance).
+__device__ __forceinline__ void rect_moments(float mz, float S, float sd, float alpha, float& mean, float& var,
+                                             float& cdf, float& pdf) {
+#pragma clang fp contract(off)
+  const float a = fabsf(alpha);
+  const float z = a * INV_SQRT_2;
+  const float t = fast_rcp(fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = fmaf(p, t, -0.82215223f);
+  p = fmaf(p, t, 1.48851587f);
+  p = fmaf(p, t, -1.13520398f);
+  p = fmaf(p, t, 0.27886807f);
+  p = fmaf(p, t, -0.18628806f);
+  p = fmaf(p, t, 0.09678418f);
+  p = fmaf(p, t, 0.37409196f);
+  p = fmaf(p, t, 1.00002368f);
+  p = fmaf(p, t, -1.26551223f);
+  const float SQRT_PI_2 = 1.2533141373155003f;  // sqrt(pi / 2)
+  const float mills = SQRT_PI_2 * t * fast_exp(p);
+  pdf = INV_SQRT_2PI * fast_exp(-0.5f * a * a);
+  const float tail = pdf * mills;
+  if (alpha >= 0.0f) {
+    cdf = 1.0f - tail;
+    mean = fmaf(mz, cdf, sd * pdf);
+    var = rect_var(S, alpha, pdf, cdf, tail);
+  } else {
+    float u1, u2;
+    if (a >= 2.0f) {
+      mills_differences(a, t, u1, u2);
+    } else {
+      u1 = fmaf(-a, mills, 1.0f);                 // 1 - x R
+      u2 = fmaf(fmaf(a, a, 1.0f), mills, -a);      // (1 + x^2) R - x
+    }
+    cdf = tail;
+    mean = sd * pdf * u1;
+    var = S * pdf * fmaf(-pdf * u1, u1, u2);
+  }
+}
+
 __device__ __forceinline__ void relu_moments(float mz, float Sz, float& ma, float& Sa, float& J) {
+#pragma clang fp contract(off)
   const float Ss = fmaxf(Sz, 1e-30f);
   const float rs = fast_rsqrt(Ss);
   const float sig = Ss * rs;
@@ -108,7 +212,7 @@ __device__ __forceinline__ void relu_moments(float mz, float Sz, float& ma, floa
   normal_cdf_pair(alpha, cdf_e, Q_e);
   const float cdf = asym ? fast_div(pdf, -alpha) : cdf_e;
   const float Q = asym ? 1.0f - cdf : Q_e;
-  ma = sig * pdf + mz * cdf;
+  ma = fmaf(mz, cdf, sig * pdf);
   Sa = fmaxf(rect_var(Ss, alpha, pdf, cdf, Q), 0.0f);
   J = cdf;
 }
@@ -142,6 +246,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <int EPT>
 __device__ __forceinline__ void remax_row(const float (&mz)[EPT], const float (&Sz)[EPT], int lane, int K,
                                           float (&ma)[EPT], float (&Sa)[EPT], float (&Jo)[EPT]) {
+#pragma clang fp contract(off)
   const float EPS = 1e-6f;
   float var_z[EPT], mu_m[EPT], var_m[EPT], jcb[EPT];
   float s_mu = 0.f, s_var = 0.f;
@@ -153,15 +258,12 @@ __device__ __forceinline__ void remax_row(const float (&mz)[EPT], const float (&
     const float rs = fast_rsqrt(v);
     const float sd = v * rs;
     const float al = m * rs;
-    const float pdf = INV_SQRT_2PI * fast_exp(-0.5f * al * al);
-    float cdf, ccdf;
-    normal_cdf_pair(al, cdf, ccdf);
-    const float mraw = m * cdf + sd * pdf;
+    float mraw, vrect, cdf, pdf;
+    rect_moments(m, v, sd, al, mraw, vrect, cdf, pdf);
     const float mm = fmaxf(mraw, EPS);
     // same variance as -mm^2 + 2 mm m - m sd pdf + (v - m^2) cdf while the mean floor is
-    // inactive (see rect_var); the floored case keeps the reference's expression
-    const float vraw = (mraw >= EPS) ? rect_var(v, al, pdf, cdf, ccdf)
-                                     : -mm * mm + 2.0f * mm * m - m * sd * pdf + (v - m * m) * cdf;
+    // inactive (see rect_moments); the floored case keeps the reference's expression
+    const float vraw = (mraw >= EPS) ? vrect : -mm * mm + 2.0f * mm * m - m * sd * pdf + (v - m * m) * cdf;
     const float vm = fmaxf(vraw, EPS);
     var_z[e] = v;
     mu_m[e] = mm;
@@ -177,18 +279,18 @@ __device__ __forceinline__ void remax_row(const float (&mz)[EPT], const float (&
   const float inv_mt = fast_rcp(mu_mt);
   // log1p/expm1 below are the reference's log(1 + x) / exp(x) - 1 without fp32 cancellation
   const float var_log_mt = log1p_pos(var_mt * inv_mt * inv_mt);
-  const float mu_log_mt = fast_log(mu_mt) - 0.5f * var_log_mt;
+  const float mu_log_mt = fmaf(-0.5f, var_log_mt, fast_log(mu_mt));
   float var_log_m[EPT], cov_m_mt[EPT], mu_a_raw[EPT], var_log_a[EPT];
   float s_a = 0.f;
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const float rm = fast_rcp(mu_m[e]);
     const float vlm = log1p_pos(var_m[e] * rm * rm);
-    const float mlm = fast_log(mu_m[e]) - 0.5f * vlm;
+    const float mlm = fmaf(-0.5f, vlm, fast_log(mu_m[e]));
     const float cov = log1p_pos(var_m[e] * rm * inv_mt);
     const float mla = mlm - mu_log_mt;
-    const float vla = fmaxf(vlm + var_log_mt - 2.0f * cov, 0.0f);
-    const float mar = fmaxf(fast_exp(mla + 0.5f * vla), EPS);
+    const float vla = fmaxf(fmaf(-2.0f, cov, vlm + var_log_mt), 0.0f);
+    const float mar = fmaxf(fast_exp(fmaf(0.5f, vla, mla)), EPS);
     var_log_m[e] = vlm;
     cov_m_mt[e] = cov;
     var_log_a[e] = vla;
