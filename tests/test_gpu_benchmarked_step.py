@@ -11,8 +11,10 @@
 2. Teacher-forced oracle comparison of ResNet-18 at batch 128 through ``Sequential.step``
    with the side stream on (network.py:119-152, resblock.py:354-438). Every pass of the
    step is recorded as it runs (the fused conv -> ReLU -> BatchNorm2D passes, the
-   BatchNorm2D -> ReLU backward passes, each Conv2D backward, the head layers, the
-   innovation); the float64 oracle then recomputes each pass from the GPU's own input to
+   BatchNorm2D -> ReLU backward passes, each Conv2D backward, the conv input-delta
+   products that carry the BatchNorm2D -> ReLU backward in their epilogue, the head
+   layers, the innovation) and counted by kind, so a pass that goes unrecorded fails the
+   test; the float64 oracle then recomputes each pass from the GPU's own input to
    that pass, so no error is carried from one layer to the next, and the result is held
    elementwise to |gpu - oracle| <= 1e-6 + 1e-4 * scale, where scale is the sum of the
    absolute values of the terms the oracle adds for that element:
@@ -24,29 +26,25 @@
        variance delta is <= 0) and elementwise maps: |oracle|.
    Conv forward and input-delta passes are checked on three whole images of the batch
    (each output depends only on its own image); BatchNorm2D, ReLU, pooling, the head and
-   the innovation on the full batch; Conv2D parameter deltas over the full batch for up to
+   the innovation on the full batch (the folded passes too: their BatchNorm parameter
+   deltas sum over every image, so the oracle forms the transposed product of the whole
+   batch); Conv2D parameter deltas over the full batch for up to
    96 sampled weight rows (all columns); the capped update of every parameter tensor in
    full. The worst err/bound of every pass is printed.
 """
 
 from __future__ import annotations
 
-import math
-
 import pytest
 import torch
 
 from oracle import tagi_oracle as O
+from teacher_forcing import ATOL, RTOL, Report, check_attention, d64  # noqa: F401
 
 pytestmark = pytest.mark.gpu
 
-RTOL, ATOL = 1e-4, 1e-6
 IMAGES = [0, 63, 127]
 MAX_ROWS = 96
-
-
-def d64(t):
-    return t.detach().to("cpu", torch.float64).contiguous()
 
 
 # ---------------------------------------------------------------------------- part 1
@@ -124,33 +122,6 @@ def test_transformer_step_equals_layer_by_layer_path(dev):
 
 
 # ---------------------------------------------------------------------------- part 2
-class Report:
-    def __init__(self):
-        self.rows = []
-
-    def check(self, tag, got, ref, scale=None):
-        got = d64(got)
-        ref = ref.to(torch.float64)
-        assert got.shape == ref.shape, f"{tag}: shape {tuple(got.shape)} vs {tuple(ref.shape)}"
-        sc = ref.abs() if scale is None else scale.abs()
-        bound = ATOL + RTOL * sc
-        r = ((got - ref).abs() / bound).reshape(-1)
-        r = torch.nan_to_num(r, nan=math.inf)
-        i = int(torch.argmax(r))
-        self.rows.append((tag, float(r[i]), int((r > 1).sum()), r.numel(), float(got.reshape(-1)[i]),
-                          float(ref.reshape(-1)[i]), float(sc.reshape(-1)[i])))
-
-    def finish(self):
-        w = max(len(t[0]) for t in self.rows)
-        print(f"\n{'pass':<{w}}  worst err/bound   over  elements")
-        for tag, worst, over, n, *_ in self.rows:
-            print(f"{tag:<{w}}  {worst:15.3e}  {over:5d}  {n:9d}")
-        bad = [t for t in self.rows if t[1] > 1.0]
-        assert not bad, "out of tolerance:\n" + "\n".join(
-            f"{t[0]}: {t[2]}/{t[3]} elements, worst err/bound {t[1]:.3g} (got {t[4]:.9g} ref {t[5]:.9g} "
-            f"scale {t[6]:.3g})" for t in bad)
-
-
 def _pads(conv, H, W):
     return O.conv_pads(H, W, conv.kH, conv.stride, conv.padding, conv.padding_type)
 
@@ -234,6 +205,17 @@ def _install(monkeypatch, rec):
 
     monkeypatch.setattr(fused, "bn_relu_backward", brb)
 
+    orig_fold = fused.conv_bn_relu_backward
+
+    def fold(conv, bn, relu, conv_prev, dma, dSa):
+        out = orig_fold(conv, bn, relu, conv_prev, dma, dSa)
+        if out is not None:  # None: the fold declined and the two-step path (recorded above) runs
+            rec.append(dict(kind="fold", conv=conv, bn=bn, conv_prev=conv_prev, dmz=cl(dma), dSz=cl(dSa),
+                            out=(cl(out[0]), cl(out[1]))))
+        return out
+
+    monkeypatch.setattr(fused, "conv_bn_relu_backward", fold)
+
     orig_cb = Conv2D._backward
 
     def cb(self, dmz, dSz, input_deltas, add=None):
@@ -264,6 +246,33 @@ def _install(monkeypatch, rec):
         return out
 
     monkeypatch.setattr(network, "compute_innovation", inn)
+
+
+def _transposed_product(conv, d, w):
+    """The input deltas sum_co d[n, co, oh, ow] * w[(c, kh, kw), co] folded back onto the
+    input pixels, over the whole batch: the transposed convolution of ``d`` (NCHW) with the
+    weights read as (C_out, C_in, k, k). Stride-1 padding-type-1 convolutions only."""
+    assert conv.stride == 1 and conv.padding_type == 1
+    k = conv.kH
+    wt = w.T.reshape(conv.C_out, conv.C_in, k, k).contiguous()
+    return torch.nn.functional.conv_transpose2d(d, wt, stride=1, padding=conv.padding)
+
+
+def _check_conv_param_deltas(rep, tag, conv, oc, x, dm, dS):
+    """delta_mw / delta_Sw on up to MAX_ROWS sampled weight rows (every column) and the bias
+    deltas, from the recorded input ``x`` and output deltas (full batch, float64)."""
+    Cout = conv.C_out
+    K = oc.mw.shape[0]
+    gr = torch.Generator().manual_seed(K * 7 + Cout)
+    rows = torch.arange(K) if K <= MAX_ROWS else torch.randperm(K, generator=gr)[:MAX_ROWS].sort().values
+    Pc = _patch_columns(conv, x, rows)
+    dmr, dSr = _nchw_rows(dm), _nchw_rows(dS)
+    Sw = oc.Sw[rows]
+    rep.check(f"{tag} delta_mw", d64(conv.delta_mw)[rows], Sw * (Pc.T @ dmr), Sw * (Pc.abs().T @ dmr.abs()))
+    rep.check(f"{tag} delta_Sw", d64(conv.delta_Sw)[rows], Sw * Sw * ((Pc * Pc).T @ dSr))
+    rep.check(f"{tag} delta_mb", conv.delta_mb, oc.Sb * dmr.sum(0, keepdim=True),
+              oc.Sb * dmr.abs().sum(0, keepdim=True))
+    rep.check(f"{tag} delta_Sb", conv.delta_Sb, oc.Sb ** 2 * dSr.sum(0, keepdim=True))
 
 
 def _oracle_map(net, onet):
@@ -298,6 +307,7 @@ def test_resnet18_b128_step_teacher_forced(dev, monkeypatch):
     conv_in = {}  # id(conv) -> recorded input mean (float64, NCHW)
     learn = []  # (tag, engine layer) in order, for the update check
     nconv = nbn = 0
+    n_indelta = n_param = n_bnbwd = n_fold = 0  # backward passes by kind
     for r in rec:
         if r["kind"] == "crb":
             conv, bn = r["conv"], r["bn"]
@@ -367,13 +377,13 @@ def test_resnet18_b128_step_teacher_forced(dev, monkeypatch):
                       ob.Sw ** 2 * (dSa.abs() * st["mag"] ** 2).sum(dims))
             rep.check(f"{btag} delta_beta", bn.delta_mb, ob.Sb * dma.sum(dims), ob.Sb * dma.abs().sum(dims))
             rep.check(f"{btag} delta_S_beta", bn.delta_Sb, ob.Sb ** 2 * dSa.sum(dims))
+            n_bnbwd += 1
         elif r["kind"] == "conv_bwd":
             conv = r["conv"]
             oc = omap[id(conv)]
             tag = [t for t, lay in learn if lay is conv][0]
             x = conv_in[id(conv)]
             dm, dS = d64(r["dmz"]), d64(r["dSz"])
-            Cout = conv.C_out
             if r["out"] is not None:
                 a = _conv_args(conv, x[IMAGES])
                 dmi, dSi = _nchw_rows(dm[IMAGES]), _nchw_rows(dS[IMAGES])
@@ -386,17 +396,45 @@ def test_resnet18_b128_step_teacher_forced(dev, monkeypatch):
                 sfx = " +shortcut" if r["add"] is not None else ""
                 rep.check(f"{tag} bwd delta_mu{sfx}", d64(r["out"][0])[IMAGES], qm, sm)
                 rep.check(f"{tag} bwd delta_S{sfx}", d64(r["out"][1])[IMAGES], qS)
-            K = oc.mw.shape[0]
-            gr = torch.Generator().manual_seed(K * 7 + Cout)
-            rows = torch.arange(K) if K <= MAX_ROWS else torch.randperm(K, generator=gr)[:MAX_ROWS].sort().values
-            Pc = _patch_columns(conv, x, rows)
-            dmr, dSr = _nchw_rows(dm), _nchw_rows(dS)
-            Sw = oc.Sw[rows]
-            rep.check(f"{tag} delta_mw", d64(conv.delta_mw)[rows], Sw * (Pc.T @ dmr), Sw * (Pc.abs().T @ dmr.abs()))
-            rep.check(f"{tag} delta_Sw", d64(conv.delta_Sw)[rows], Sw * Sw * ((Pc * Pc).T @ dSr))
-            rep.check(f"{tag} delta_mb", conv.delta_mb, oc.Sb * dmr.sum(0, keepdim=True),
-                      oc.Sb * dmr.abs().sum(0, keepdim=True))
-            rep.check(f"{tag} delta_Sb", conv.delta_Sb, oc.Sb ** 2 * dSr.sum(0, keepdim=True))
+            _check_conv_param_deltas(rep, tag, conv, oc, x, dm, dS)
+            n_param += 1
+            n_indelta += r["out"] is not None
+        elif r["kind"] == "fold":
+            # conv's input-delta product with the BatchNorm2D -> ReLU backward of the pair in
+            # front of it in the epilogue: the deltas at the BatchNorm output exist only in
+            # registers, so the oracle forms them from the GPU's deltas at conv's output, over
+            # the whole batch (the BatchNorm parameter deltas sum over every image)
+            conv, bn = r["conv"], r["bn"]
+            oc = omap[id(conv)]
+            tag = [t for t, lay in learn if lay is conv][0]
+            btag = [t for t, lay in learn if lay is bn][0]
+            st = bn_state[id(bn)]
+            x = conv_in[id(conv)]
+            dm, dS = d64(r["dmz"]), d64(r["dSz"])
+            q = _transposed_product(conv, dm, oc.mw)
+            qS = _transposed_product(conv, dS, oc.mw * oc.mw)
+            sq = _transposed_product(conv, dm.abs(), oc.mw.abs())
+            # the transposed convolution is the oracle's patch product folded back (col2im)
+            a = _conv_args(conv, x[IMAGES])
+            ref_i = O.col2im(_nchw_rows(dm[IMAGES]) @ oc.mw.T, *a)
+            assert torch.allclose(q[IMAGES], ref_i, rtol=1e-12, atol=1e-15), "transposed product != col2im"
+            v = lambda t: t.view(1, -1, 1, 1)  # noqa: E731
+            g = v(st["gamma"])
+            fm, fS = g / st["sig"] * st["J"], (g / st["sig"]) ** 2 * st["J"] ** 2
+            rep.check(f"{tag}+{btag} folded bwd delta_mu", r["out"][0], q * fm, sq * fm.abs())
+            rep.check(f"{tag}+{btag} folded bwd delta_S", r["out"][1], qS * fS)
+            ob, mh, dims = st["ob"], st["mhat"], (0, 2, 3)
+            rep.check(f"{btag} (folded) delta_gamma", bn.delta_mw, ob.Sw * (q * mh).sum(dims),
+                      ob.Sw * (sq * st["mag"]).sum(dims))
+            rep.check(f"{btag} (folded) delta_S_gamma", bn.delta_Sw, ob.Sw ** 2 * (qS * mh * mh).sum(dims),
+                      ob.Sw ** 2 * (qS.abs() * st["mag"] ** 2).sum(dims))
+            rep.check(f"{btag} (folded) delta_beta", bn.delta_mb, ob.Sb * q.sum(dims), ob.Sb * sq.sum(dims))
+            rep.check(f"{btag} (folded) delta_S_beta", bn.delta_Sb, ob.Sb ** 2 * qS.sum(dims))
+            _check_conv_param_deltas(rep, f"{tag} (folded)", conv, oc, x, dm, dS)
+            n_fold += 1
+            n_param += 1
+            n_indelta += 1
+            n_bnbwd += 1
         elif r["kind"] in ("forward", "backward"):
             layer = r["layer"]
             name = type(layer).__name__
@@ -452,7 +490,15 @@ def test_resnet18_b128_step_teacher_forced(dev, monkeypatch):
             qm, qS = O.innovation(y, mu, var, r["sv"])
             rep.check("innovation delta_mu", r["out"][0], qm, (y.abs() + mu.abs()) / (var + r["sv"] ** 2))
             rep.check("innovation delta_S", r["out"][1], qS)
+    # every pass of the step was recorded and checked: 20 convolutions and 20 BatchNorm2D
+    # layers forward; backward, every conv's parameter deltas, the input deltas of all but
+    # the stem (the first layer forms none), every BatchNorm2D backward (two-step or folded)
+    print(f"\npasses: {nconv} conv forward, {nbn} BatchNorm2D forward, {n_param} conv parameter-delta, "
+          f"{n_indelta} conv input-delta ({n_fold} with the BatchNorm2D -> ReLU backward folded in), "
+          f"{n_bnbwd} BatchNorm2D backward")
     assert nconv == 20 and nbn == 20
+    assert n_param == 20 and n_indelta == 19 and n_bnbwd == 20
+    assert n_fold > 0, "the folded BatchNorm2D backward never ran: the test would not cover it"
 
     # capped update of every parameter tensor from its pre-step value and the GPU's deltas
     for tag, layer in learn:
@@ -468,4 +514,187 @@ def test_resnet18_b128_step_teacher_forced(dev, monkeypatch):
             rep.check(f"{tag} updated {mname}", getattr(layer, mname), um, m0.abs() + (um - m0).abs())
             rep.check(f"{tag} updated {Sname}", getattr(layer, Sname), uS, S0.abs() + (uS - S0).abs())
     assert isinstance(w.net.layers[0], Conv2D) and isinstance(w.net.layers[-2], Linear)
+    rep.finish()
+
+
+# ---------------------------------------------------------------------------- part 3
+def _install_transformer(monkeypatch, rec):
+    from triton_tagi_amd import network
+    from triton_tagi_amd.layers import Embedding, Linear, MultiheadAttentionV2, PositionalEncoding, RMSNorm
+    from triton_tagi_amd.layers import multihead_attention as mha_mod
+
+    cl = lambda t: None if t is None else t.detach().clone()  # noqa: E731
+    for cls in (Embedding, PositionalEncoding, RMSNorm, Linear):
+        for meth in ("forward", "backward"):
+            orig = getattr(cls, meth)
+
+            def wrap(self, a, b, _orig=orig, _meth=meth):
+                out = _orig(self, a, b)
+                rec.append(dict(kind=_meth, layer=self, a=cl(a), b=cl(b), out=(cl(out[0]), cl(out[1]))))
+                return out
+
+            monkeypatch.setattr(cls, meth, wrap)
+
+    orig_f = MultiheadAttentionV2.forward
+
+    def mha_forward(self, ma, Sa):
+        out = orig_f(self, ma, Sa)
+        src = self._attn_src
+        assert src is not None, "the fused attention forward did not run at the benchmarked shape"
+        rec.append(dict(kind="mha_forward", layer=self, ma=cl(ma), Sa=cl(Sa), qkv_m=cl(src[0]), qkv_S=cl(src[1]),
+                        mu_a=cl(self._cache["mu_score"]), J=cl(self._cache["jcb"]), out=(cl(out[0]), cl(out[1]))))
+        return out
+
+    monkeypatch.setattr(MultiheadAttentionV2, "forward", mha_forward)
+
+    seen = {}
+    orig_delta = mha_mod.fused_backward_delta
+
+    def delta(dmz, dSz, mw, add=None):  # the summed input deltas of the three projections
+        seen["dqkv"] = (cl(dmz), cl(dSz))
+        return orig_delta(dmz, dSz, mw, add)
+
+    monkeypatch.setattr(mha_mod, "fused_backward_delta", delta)
+    orig_b = MultiheadAttentionV2.backward
+
+    def mha_backward(self, dm, dS):
+        seen.clear()
+        out = orig_b(self, dm, dS)
+        rec.append(dict(kind="mha_backward", layer=self, d_m=cl(dm), d_S=cl(dS), dqkv=seen["dqkv"],
+                        out=(cl(out[0]), cl(out[1]))))
+        return out
+
+    monkeypatch.setattr(MultiheadAttentionV2, "backward", mha_backward)
+
+    orig_inn = network.compute_innovation
+
+    def inn(y, mu, var, sv):
+        out = orig_inn(y, mu, var, sv)
+        rec.append(dict(kind="innovation", y=cl(y), mu=cl(mu), var=cl(var), sv=sv, out=(cl(out[0]), cl(out[1]))))
+        return out
+
+    monkeypatch.setattr(network, "compute_innovation", inn)
+
+
+@pytest.mark.timeout(900)
+def test_transformer_b64_s256_step_teacher_forced(dev, monkeypatch):
+    """The transformer block (Embedding -> PositionalEncoding -> MultiheadAttentionV2 ->
+    RMSNorm -> Linear) at batch 64 x sequence 256 through ``Sequential.step`` with the side
+    stream on, teacher forced: every pass recorded, recomputed by the float64 oracle from
+    the GPU's own input to it and held to the per-element bar (teacher_forcing.py)."""
+    from triton_tagi_amd import _overlap, workloads
+    from triton_tagi_amd.layers import Embedding, Linear, MultiheadAttentionV2, PositionalEncoding, RMSNorm
+
+    w = workloads.build("transformer", device="cuda:0")
+    assert w.batch == 64 and w.net.overlap_param_deltas
+    emb, pe, att, rms, head = w.net.layers
+    assert (isinstance(emb, Embedding) and isinstance(pe, PositionalEncoding) and isinstance(att, MultiheadAttentionV2)
+            and isinstance(rms, RMSNorm) and isinstance(head, Linear))
+    onet = O.mirror_net(w.net)
+    oemb, ope, oatt, orms, ohead = onet.layers
+    rec = []
+    forks = [0]
+    orig_fork = _overlap.overlap_param_deltas.fork
+
+    def counting_fork(self, *a):
+        forks[0] += 1
+        return orig_fork(self, *a)
+
+    _install_transformer(monkeypatch, rec)
+    monkeypatch.setattr(_overlap.overlap_param_deltas, "fork", counting_fork)
+    w.net.step(w.x, w.y, w.sigma_v)
+    torch.cuda.synchronize()
+    monkeypatch.undo()
+    assert forks[0] > 0, "the side stream was never used: the test would not cover the overlapped step"
+    var_a = att.get_attention_scores()[1]  # rebuilt from the recorded projections (the fused kernel's values)
+    torch.cuda.synchronize()
+
+    rep = Report()
+    kinds = [(r["kind"], type(r.get("layer")).__name__) for r in rec]
+    expect = [("forward", "Embedding"), ("forward", "PositionalEncoding"), ("mha_forward", "MultiheadAttentionV2"),
+              ("forward", "RMSNorm"), ("forward", "Linear"), ("innovation", "NoneType"), ("backward", "Linear"),
+              ("backward", "RMSNorm"), ("mha_backward", "MultiheadAttentionV2"), ("backward", "PositionalEncoding"),
+              ("backward", "Embedding")]
+    assert kinds == expect, f"passes of the step: {kinds}"
+    f_emb, f_pe, f_att, f_rms, f_head, r_inn, b_head, b_rms, b_att, b_pe, b_emb = rec
+    D = emb.embedding_dim
+
+    # Embedding forward: a gather (embedding.py:88-106)
+    cat = d64(f_emb["a"]).long()
+    assert torch.equal(d64(f_emb["out"][0]), oemb.mw[cat]) and torch.equal(d64(f_emb["out"][1]), oemb.Sw[cat])
+    # PositionalEncoding forward (positional_encoding.py:59-63)
+    a = d64(f_pe["a"])
+    pe_rows = ope.pe[: a.shape[-2]]
+    rep.check("PositionalEncoding fwd mu", f_pe["out"][0], a + pe_rows, a.abs() + pe_rows.abs())
+    assert torch.equal(f_pe["out"][1], f_pe["b"])
+    # attention, stage by stage
+    projs = (oatt.q, oatt.k, oatt.v)
+    check_attention(rep, "attention", dict(
+        H=att.num_heads, ma=f_att["ma"], Sa=f_att["Sa"], w_m=torch.cat([p.mw for p in projs], 1),
+        w_S=torch.cat([p.Sw for p in projs], 1), qkv_m=f_att["qkv_m"], qkv_S=f_att["qkv_S"], mu_a=f_att["mu_a"],
+        var_a=var_a, J=f_att["J"], out_m=f_att["out"][0], out_S=f_att["out"][1], d_m=b_att["d_m"], d_S=b_att["d_S"],
+        dqkv_m=b_att["dqkv"][0], dqkv_S=b_att["dqkv"][1], dma=b_att["out"][0], dSa=b_att["out"][1],
+        pd=[(p.delta_mw, p.delta_Sw) for p in (att.q_proj, att.k_proj, att.v_proj)], Sw_qkv=[p.Sw for p in projs]))
+    # RMSNorm forward (rms_norm.py:93-110): products of same-sign factors, no cancellation
+    a, b = d64(f_rms["a"]).reshape(-1, D), d64(f_rms["b"]).reshape(-1, D)
+    inv = 1.0 / torch.sqrt((a * a + b).mean(1, keepdim=True) + orms.eps)
+    g, Sg = orms.mw, orms.Sw
+    rep.check("RMSNorm fwd mu", f_rms["out"][0].reshape(-1, D), inv * a * g)
+    rep.check("RMSNorm fwd S", f_rms["out"][1].reshape(-1, D), inv * inv * (b * (g * g + Sg) + Sg * a * a))
+    # head Linear forward (linear.py:83-103)
+    a, b = d64(f_head["a"]).reshape(-1, D), d64(f_head["b"]).reshape(-1, D)
+    rm, rS = O.linear_moments(a, b, ohead.mw, ohead.Sw, ohead.mb, ohead.Sb)
+    rep.check("head Linear fwd mu", f_head["out"][0].reshape(rm.shape), rm, a.abs() @ ohead.mw.abs() + ohead.mb.abs())
+    rep.check("head Linear fwd S", f_head["out"][1].reshape(rS.shape), rS)
+    x_head = a
+    # innovation (observation.py:24-46)
+    y, mu, var = d64(r_inn["y"]), d64(r_inn["mu"]), d64(r_inn["var"])
+    qm, qS = O.innovation(y, mu, var, r_inn["sv"])
+    rep.check("innovation delta_mu", r_inn["out"][0], qm, (y.abs() + mu.abs()) / (var + r_inn["sv"] ** 2))
+    rep.check("innovation delta_S", r_inn["out"][1], qS)
+    # head Linear backward (linear.py:108-156)
+    N = ohead.mw.shape[1]
+    dm, dS = d64(b_head["a"]).reshape(-1, N), d64(b_head["b"]).reshape(-1, N)
+    qm, qS = O.linear_backward_delta(dm, dS, ohead.mw)
+    rep.check("head Linear bwd delta_mu", b_head["out"][0].reshape(qm.shape), qm, dm.abs() @ ohead.mw.abs().T)
+    rep.check("head Linear bwd delta_S", b_head["out"][1].reshape(qS.shape), qS)
+    rep.check("head delta_mw", head.delta_mw, ohead.Sw * (x_head.T @ dm), ohead.Sw * (x_head.abs().T @ dm.abs()))
+    rep.check("head delta_Sw", head.delta_Sw, ohead.Sw ** 2 * ((x_head * x_head).T @ dS))
+    rep.check("head delta_mb", head.delta_mb, ohead.Sb * dm.sum(0, keepdim=True),
+              ohead.Sb * dm.abs().sum(0, keepdim=True))
+    rep.check("head delta_Sb", head.delta_Sb, ohead.Sb ** 2 * dS.sum(0, keepdim=True))
+    # RMSNorm backward (rms_norm.py:112-140), from the forward's input
+    a = d64(f_rms["a"]).reshape(-1, D)
+    dm, dS = d64(b_rms["a"]).reshape(-1, D), d64(b_rms["b"]).reshape(-1, D)
+    t = inv * g
+    rep.check("RMSNorm bwd delta_mu", b_rms["out"][0].reshape(-1, D), t * dm)
+    rep.check("RMSNorm bwd delta_S", b_rms["out"][1].reshape(-1, D), t * t * dS)
+    rep.check("RMSNorm delta_mw", rms.delta_mw, Sg * (inv * a * dm).sum(0), Sg * (inv * a * dm).abs().sum(0))
+    rep.check("RMSNorm delta_Sw", rms.delta_Sw, Sg * Sg * (inv * inv * a * a * dS).sum(0))
+    # PositionalEncoding backward: identity (positional_encoding.py:65-68)
+    assert torch.equal(b_pe["out"][0], b_pe["a"]) and torch.equal(b_pe["out"][1], b_pe["b"])
+    # Embedding backward (embedding.py:108-157): per category, Sw-weighted sums of the deltas
+    dm, dS = d64(b_emb["a"]).reshape(-1, D), d64(b_emb["b"]).reshape(-1, D)
+    flat = cat.reshape(-1)
+    V = oemb.mw.shape[0]
+    sum_m = torch.zeros(V, D, dtype=torch.float64).index_add_(0, flat, dm)
+    sum_abs = torch.zeros(V, D, dtype=torch.float64).index_add_(0, flat, dm.abs())
+    sum_S = torch.zeros(V, D, dtype=torch.float64).index_add_(0, flat, dS)
+    rep.check("Embedding delta_mw", emb.delta_mw, oemb.Sw * sum_m, oemb.Sw * sum_abs)
+    rep.check("Embedding delta_Sw", emb.delta_Sw, oemb.Sw ** 2 * sum_S)
+    assert not b_emb["out"][0].any() and not b_emb["out"][1].any()
+
+    # capped update of every parameter tensor from its pre-step value and the GPU's deltas
+    cap = O.get_cap_factor(w.batch)
+    groups = [("Embedding", emb, oemb, ("mw",)), ("q_proj", att.q_proj, oatt.q, ("mw",)),
+              ("k_proj", att.k_proj, oatt.k, ("mw",)), ("v_proj", att.v_proj, oatt.v, ("mw",)),
+              ("RMSNorm", rms, orms, ("mw",)), ("head", head, ohead, ("mw", "mb"))]
+    for tag, layer, ol, means in groups:
+        for mname in means:
+            Sname, dmn, dSn = "S" + mname[1:], "delta_" + mname, "delta_S" + mname[1:]
+            m0, S0 = getattr(ol, mname), getattr(ol, Sname)
+            dmv, dSv = d64(getattr(layer, dmn)).reshape(m0.shape), d64(getattr(layer, dSn)).reshape(m0.shape)
+            um, uS = O.capped_update(m0, S0, dmv, dSv, cap)
+            rep.check(f"{tag} updated {mname}", getattr(layer, mname), um, m0.abs() + (um - m0).abs())
+            rep.check(f"{tag} updated {Sname}", getattr(layer, Sname), uS, S0.abs() + (uS - S0).abs())
     rep.finish()

@@ -71,3 +71,39 @@ def test_graph_replays_match_eager_hrc_steps(dev, name, batch):
         graphed.y.copy_(new)
         eager.y.copy_(new)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("name", ["resnet18", "transformer"])
+def test_graph_replays_with_the_side_stream(dev, name):
+    """Capture of the benchmarked steps (ResNet-18 batch 128, transformer block batch 64 x
+    sequence 256), where the parameter-delta products run on the side stream: the capture
+    must record the fork and the join, and every replay must equal an eager overlapped
+    step bit for bit (network.py:119-152)."""
+    from triton_tagi_amd import _overlap, workloads
+
+    eager = workloads.build(name, device="cuda:0")
+    graphed = workloads.build(name, device="cuda:0")
+    assert eager.net.overlap_param_deltas and graphed.net.overlap_param_deltas
+    forks = [0]
+    orig = _overlap.overlap_param_deltas.fork
+
+    def counting_fork(self, *a):
+        forks[0] += 1
+        return orig(self, *a)
+
+    _overlap.overlap_param_deltas.fork = counting_fork
+    try:
+        g = graphed.net.capture_step(graphed.x, graphed.y, graphed.sigma_v)  # one eager step, then the capture
+    finally:
+        _overlap.overlap_param_deltas.fork = orig
+    assert forks[0] >= 2, "the side stream was not used during the capture: the test would not cover it"
+    eager.net.step(eager.x, eager.y, eager.sigma_v)
+    torch.cuda.synchronize()
+    for r in range(3):
+        mu, var = g.replay()
+        emu, evar = eager.net.step(eager.x, eager.y, eager.sigma_v)
+        torch.cuda.synchronize()
+        assert torch.equal(mu, emu) and torch.equal(var, evar), f"replay {r}: predictions differ"
+        for i, (a, b) in enumerate(zip(_params(eager.net), _params(graphed.net))):
+            assert torch.equal(a, b), f"replay {r}: parameter tensor {i} differs"
+    assert bool(torch.isfinite(mu).all())
