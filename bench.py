@@ -172,6 +172,7 @@ def measure_ceilings(dev: str) -> dict:
             best[per_cu] = round(nbytes / s / 1e9, 1)
         out[name] = max(best.values())
         out[name + "_by_blocks_per_cu"] = best
+    out["stream_variants"] = measure_stream_variants(dev, src, dst, part, n, cus, st)
     del src, dst, part
     torch.backends.cuda.matmul.allow_tf32 = False
     a = torch.randn(8192, 8192, device=dev)
@@ -179,6 +180,49 @@ def measure_ceilings(dev: str) -> dict:
     s = timed(lambda: torch.matmul(a, b), 5)
     out["torch_matmul_fp32_8192_tflops"] = round(2 * 8192**3 / s / 1e12, 1)
     return out
+
+
+def measure_stream_variants(dev, src, dst, part, n, cus, st) -> dict:
+    """HBM streaming forms (tagi_probe_stream_variant) over 1 GiB: copy (read + write),
+    read-only and write-only; 4, 8 or 16 float4 per lane in flight; nontemporal loads
+    and/or stores; grid-stride or one contiguous chunk per block; 8, 32 and 128 blocks of
+    256 threads per CU. GB/s of every form, and the best per mode."""
+    import torch
+
+    from triton_tagi_amd import _lib
+
+    res = {}
+    names = {0: "copy", 1: "read", 2: "write"}
+    nbytes = {0: 2 * n * 4, 1: n * 4, 2: n * 4}
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for mode in (0, 1, 2):
+        d, dn = (part, part.numel()) if mode == 1 else (dst, dst.numel())
+        for unroll in (4, 8, 16):
+            for flags in range(8):
+                for per_cu in (8, 32, 128):
+                    blocks = cus * per_cu
+                    if mode == 1 and blocks * 256 > dn:
+                        continue
+
+                    def go():
+                        _lib.call("tagi_probe_stream_variant", src.data_ptr(), d.data_ptr(), n, dn, blocks, mode,
+                                  unroll, flags, st)
+
+                    go()
+                    ev0.record()
+                    for _ in range(5):
+                        go()
+                    ev1.record()
+                    ev1.synchronize()
+                    s = ev0.elapsed_time(ev1) / 1e3 / 5
+                    key = (f"{names[mode]} u{unroll} {'ntld' if flags & 1 else 'ld'} {'ntst' if flags & 2 else 'st'} "
+                           f"{'chunk' if flags & 4 else 'stride'} {per_cu}/cu")
+                    res[key] = round(nbytes[mode] / s / 1e9, 1)
+    best = {}
+    for mode in names.values():
+        k = max((k for k in res if k.startswith(mode)), key=lambda k: res[k])
+        best[mode] = {"form": k, "gbs": res[k]}
+    return {"best": best, "all": res}
 
 
 def linear_bench(args) -> dict:

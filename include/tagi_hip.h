@@ -73,6 +73,15 @@ int tagi_probe_mfma_mix(float* out, int64_t blocks, int64_t iters, int kind, int
 int tagi_probe_stream(const float* src, float* dst, int64_t n, int64_t blocks, int mode,
                       tagi_stream_t stream);
 
+/* Measurement probe, no counterpart in the reference: variants of tagi_probe_stream to
+ * find the best HBM streaming form on this GPU. mode 0 copies n floats src -> dst, 1 reads
+ * them (per-thread sums into dst, which must hold blocks * 256 floats), 2 writes dst;
+ * unroll 4, 8 or 16 float4 in flight per lane; flags bit 0 nontemporal loads, bit 1
+ * nontemporal stores, bit 2 one contiguous chunk per block instead of a grid-stride walk.
+ * dst_n is the number of floats dst holds (checked). */
+int tagi_probe_stream_variant(const float* src, float* dst, int64_t n, int64_t dst_n, int64_t blocks, int mode,
+                              int unroll, int flags, tagi_stream_t stream);
+
 /* ------------------------------------------------------------------ Linear ---- */
 /* Fused Linear forward moments, one MFMA pass sharing the A/B tiles:
  *   mz = ma @ mw + mb

@@ -225,6 +225,81 @@ __global__ void __launch_bounds__(256) stream_read_kernel(const float4* __restri
   }
   out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;  // keeps the loads live
 }
+
+// Variants of the streaming probe, to settle how close to the HBM datasheet a kernel of
+// this engine can get: MODE 0 copies, 1 reads (summed per thread), 2 writes a constant;
+// U float4 per lane per step, all loads issued before any store; NTL / NTS mark the loads /
+// stores nontemporal (__builtin_nontemporal_load/store: the "nt" cache policy); CHUNK gives
+// each block one contiguous stretch of the array instead of a grid-stride walk.
+typedef float probe_f4 __attribute__((ext_vector_type(4)));
+
+template <int MODE, int U, bool NTL, bool NTS, bool CHUNK>
+__global__ void __launch_bounds__(256) stream_variant_kernel(const probe_f4* __restrict__ src,
+                                                             probe_f4* __restrict__ dst, int64_t n4) {
+  const int64_t step = (int64_t)blockDim.x * U;
+  int64_t begin, end, stride;
+  if constexpr (CHUNK) {
+    const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
+    begin = (int64_t)blockIdx.x * per;
+    end = begin + per < n4 ? begin + per : n4;
+    stride = step;
+  } else {
+    begin = (int64_t)blockIdx.x * step;
+    end = n4;
+    stride = (int64_t)gridDim.x * step;
+  }
+  float acc = 0.f;
+  for (int64_t base = begin + threadIdx.x; base < end; base += stride) {
+    probe_f4 v[U];
+    if constexpr (MODE != 2) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = base + (int64_t)u * blockDim.x;
+        if (i < end) v[u] = NTL ? __builtin_nontemporal_load(src + i) : src[i];
+        else v[u] = probe_f4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    if constexpr (MODE == 1) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = base + (int64_t)u * blockDim.x;
+        if (i < end) {
+          const probe_f4 w = MODE == 0 ? v[u] : probe_f4{1.f, 2.f, 3.f, 4.f};
+          if (NTS) __builtin_nontemporal_store(w, dst + i);
+          else dst[i] = w;
+        }
+      }
+    }
+  }
+  if constexpr (MODE == 1) reinterpret_cast<float*>(dst)[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
+template <int MODE, int U>
+static void launch_stream_variant(int flags, dim3 grid, hipStream_t s, const probe_f4* src, probe_f4* dst, int64_t n4) {
+#define TAGI_SV(L, S, C) hipLaunchKernelGGL((stream_variant_kernel<MODE, U, L, S, C>), grid, dim3(256), 0, s, src, dst, n4)
+  switch (flags & 7) {
+    case 0: TAGI_SV(false, false, false); break;
+    case 1: TAGI_SV(true, false, false); break;
+    case 2: TAGI_SV(false, true, false); break;
+    case 3: TAGI_SV(true, true, false); break;
+    case 4: TAGI_SV(false, false, true); break;
+    case 5: TAGI_SV(true, false, true); break;
+    case 6: TAGI_SV(false, true, true); break;
+    default: TAGI_SV(true, true, true); break;
+  }
+#undef TAGI_SV
+}
+
+template <int MODE>
+static void launch_stream_mode(int unroll, int flags, dim3 grid, hipStream_t s, const probe_f4* src, probe_f4* dst,
+                               int64_t n4) {
+  if (unroll == 4) launch_stream_variant<MODE, 4>(flags, grid, s, src, dst, n4);
+  else if (unroll == 8) launch_stream_variant<MODE, 8>(flags, grid, s, src, dst, n4);
+  else launch_stream_variant<MODE, 16>(flags, grid, s, src, dst, n4);
+}
 }  // namespace
 
 extern "C" int tagi_probe_stream(const float* src, float* dst, int64_t n, int64_t blocks, int mode,
@@ -273,5 +348,25 @@ extern "C" int tagi_probe_mfma_loop(float* out, int64_t blocks, int64_t iters, t
   TAGI_REQUIRE(out != nullptr && blocks > 0 && blocks <= (1 << 20) && iters > 0 && iters < (1ll << 31),
                "%s: bad arguments", what);
   hipLaunchKernelGGL(mfma_loop_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, out, (int)iters);
+  return check_launch(what);
+}
+
+extern "C" int tagi_probe_stream_variant(const float* src, float* dst, int64_t n, int64_t dst_n, int64_t blocks,
+                                         int mode, int unroll, int flags, tagi_stream_t stream) {
+  const char* what = "tagi_probe_stream_variant";
+  TAGI_REQUIRE(src != nullptr && dst != nullptr && n > 0 && n % 4 == 0 && blocks > 0 && blocks <= (1 << 20) &&
+                   mode >= 0 && mode <= 2 && (unroll == 4 || unroll == 8 || unroll == 16) && flags >= 0 &&
+                   flags <= 7 && (((uintptr_t)src | (uintptr_t)dst) & 15u) == 0,
+               "%s: bad arguments (n a positive multiple of 4, mode 0-2, unroll 4/8/16, flags 0-7, buffers "
+               "16-byte aligned)", what);
+  TAGI_REQUIRE(mode == 1 ? dst_n >= blocks * 256 : dst_n >= n, "%s: dst holds %lld floats, needs %lld", what,
+               (long long)dst_n, (long long)(mode == 1 ? blocks * 256 : n));
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)blocks);
+  const auto* src4 = reinterpret_cast<const probe_f4*>(src);
+  auto* dst4 = reinterpret_cast<probe_f4*>(dst);
+  if (mode == 0) launch_stream_mode<0>(unroll, flags, grid, s, src4, dst4, n / 4);
+  else if (mode == 1) launch_stream_mode<1>(unroll, flags, grid, s, src4, dst4, n / 4);
+  else launch_stream_mode<2>(unroll, flags, grid, s, src4, dst4, n / 4);
   return check_launch(what);
 }
