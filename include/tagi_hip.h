@@ -229,6 +229,19 @@ int tagi_attn_score_deltas_qk(const float* d_mu, const float* d_var, int64_t ld_
                               int64_t ld_out, int64_t B, int64_t H, int64_t S, int64_t D, float scale,
                               float scale_sq, int transpose, tagi_stream_t stream);
 
+/* The query and the key deltas of tagi_attn_score_deltas_qk in one launch
+ * (multihead_attention.py:239-260, replacing its two bmm_shared_right calls after the
+ * score-delta product): one block per (batch, head) forms the Jacobian-scaled score deltas
+ * of each block of 32 query rows once, writes that block's query deltas and accumulates the
+ * key deltas over the query blocks in order. dq_* = tagi_attn_score_deltas_qk(transpose 0)
+ * bit for bit; dk_* its transpose-1 values up to the order of the fp32 sums. mu_q and mu_k
+ * have row stride ld_x; the outputs row stride ld_out. S <= 256, D in {16, 32}. */
+int tagi_attn_score_deltas_qk_joint(const float* d_mu, const float* d_var, int64_t ld_d, const float* mu_v,
+                                    const float* mu_q, const float* mu_k, int64_t ld_x, const float* J,
+                                    float* dq_mu, float* dq_var, float* dk_mu, float* dk_var, int64_t ld_out,
+                                    int64_t B, int64_t H, int64_t S, int64_t D, float scale, float scale_sq,
+                                    tagi_stream_t stream);
+
 /* ------------------------------------------------------------------ Conv2D ---- */
 /* 4-D activations and deltas of the conv path (Conv2D, BatchNorm2D, AvgPool2D) are
  * channels-last: element (n, c, h, w) of an (N, C, H, W) tensor sits at ((n*H + h)*W + w)*C + c

@@ -642,6 +642,63 @@ def test_attention_score_deltas_qk_fused(dev, B, H, S, D):
         assert_scaled_close(fS, rS, tS, 1e-5, 1e-7, f"{name} var")
 
 
+@pytest.mark.parametrize("B,H,S,D", [(2, 8, 256, 32), (1, 2, 40, 16), (1, 4, 250, 16), (2, 2, 100, 32),
+                                     (1, 3, 1, 32), (3, 1, 33, 16)])
+def test_attention_score_deltas_qk_joint(dev, B, H, S, D):
+    """tagi_attn_score_deltas_qk_joint (one block per head: the scaled score deltas formed
+    once per query block, feeding the query deltas and register-held key deltas) against
+    tagi_attn_score_deltas_qk called twice. The query deltas are summed in the same order,
+    so they are the same bits; the key deltas sum the query rows 32 at a time instead of 8
+    waves' strided shares, so they are held to 1e-5 of the sum of their terms' magnitudes.
+    The inputs sit in one (B*S, 3E) buffer, as the layer holds them, so the rows past S of
+    the last head are the edge of the allocation."""
+    import math
+
+    from triton_tagi_amd import _lib
+
+    r = g(11 * S + D + 5 * H)
+    E = H * D
+    L = 3 * E
+    qkv = torch.randn(B * S, L, generator=r).to(dev)
+    q, k, v = (qkv[:, i * E:(i + 1) * E] for i in range(3))
+    dmu = torch.randn(B, S, E, generator=r).to(dev)
+    dvar = -torch.rand(B, S, E, generator=r).to(dev)
+    J = torch.rand(B, H, S, S, generator=r).to(dev)
+    sc = 1.0 / math.sqrt(D)
+    st = _lib.stream_of(dmu)
+    ref = {}
+    for x, tr, name in ((k, 0, "dQ"), (q, 1, "dK")):
+        rm, rS = torch.empty(B, S, E, device=dev), torch.empty(B, S, E, device=dev)
+        _lib.call("tagi_attn_score_deltas_qk", dmu.data_ptr(), dvar.data_ptr(), E, v.data_ptr(), x.data_ptr(), L,
+                  J.data_ptr(), rm.data_ptr(), rS.data_ptr(), E, B, H, S, D, sc, sc * sc, tr, st)
+        ref[name] = (rm, rS)
+    # outputs in a strided (B*S, 3E) buffer too, with NaN canaries in the untouched columns
+    out = torch.full((B * S, 2 * E + 8), float("nan"), device=dev)
+    outS = torch.full_like(out, float("nan"))
+    ld = out.shape[1]
+    _lib.call("tagi_attn_score_deltas_qk_joint", dmu.data_ptr(), dvar.data_ptr(), E, v.data_ptr(), q.data_ptr(),
+              k.data_ptr(), L, J.data_ptr(), out.data_ptr(), outS.data_ptr(), out[:, E:].data_ptr(),
+              outS[:, E:].data_ptr(), ld, B, H, S, D, sc, sc * sc, st)
+    torch.cuda.synchronize()
+    assert torch.isnan(out[:, 2 * E:]).all() and torch.isnan(outS[:, 2 * E:]).all(), "wrote past the outputs"
+    qm, qS = out[:, :E].reshape(B, S, E), outS[:, :E].reshape(B, S, E)
+    km, kS = out[:, E:2 * E].reshape(B, S, E), outS[:, E:2 * E].reshape(B, S, E)
+    assert torch.equal(qm, ref["dQ"][0]) and torch.equal(qS, ref["dQ"][1]), "query deltas differ from the dQ kernel"
+    # key-delta term magnitudes: |scaled|^T @ |q| per head, from the materialised scaled deltas
+    hv, hvt = _lib.view(H, S * E, D, E, 1), _lib.view(H, S * E, D, 1, E)
+    sv = _lib.view(1, S * S, 0, S, 1)
+    vc = v.contiguous()
+    smu, svar = torch.empty(B, H, S, S, device=dev), torch.empty(B, H, S, S, device=dev)
+    _lib.call("tagi_bmm_shared_jacobian", dmu.data_ptr(), dvar.data_ptr(), vc.data_ptr(), J.data_ptr(),
+              smu.data_ptr(), svar.data_ptr(), B * H, S, D, S, hv, hvt, sv, 1.0, 1.0, 0, st)
+    qh = q.reshape(B, S, H, D).permute(0, 2, 1, 3).contiguous()
+    tm = sc * torch.matmul(smu.abs().transpose(-1, -2).contiguous(), qh.abs()).permute(0, 2, 1, 3).reshape(B, S, E)
+    tS = sc * sc * torch.matmul(svar.abs().transpose(-1, -2).contiguous(), qh * qh).permute(0, 2, 1, 3).reshape(
+        B, S, E)
+    assert_scaled_close(km, ref["dK"][0], tm, 1e-5, 1e-7, "dK mean")
+    assert_scaled_close(kS, ref["dK"][1], tS, 1e-5, 1e-7, "dK var")
+
+
 @pytest.mark.parametrize("transpose_a,transpose_b", [(False, False), (True, False), (False, True), (True, True)])
 def test_bmm_wrappers_strided(dev, transpose_a, transpose_b):
     from triton_tagi_amd.kernels.attention import bmm_shared_left, bmm_shared_right, bmm_tagi, bmm_tagi_var

@@ -544,6 +544,180 @@ __global__ void __launch_bounds__(512, 4) attn_dqk_kernel(const float* __restric
     }
   }
 }
+
+// The query and key deltas of one head in one block (multihead_attention.py:239-260): for
+// each block of 32 query rows in order, the scaled score deltas (phase 1, as in
+// attn_dqk_kernel) are formed once into LDS; wave w then multiplies the tile's rows over its
+// 32 keys by mu_k (partial query deltas, summed over the waves in wave order and stored, as
+// attn_dqk_kernel does, so the query deltas are the same bits) and the transposed tile's
+// columns -- its own 32 keys -- by mu_q into key-delta accumulators held in registers across
+// all query blocks (summed query block by query block in order: deterministic). Against the
+// two kernels above, the score-delta product and the Jacobian are formed and read once
+// instead of twice.
+template <int HD>
+__global__ void __launch_bounds__(512, 4) attn_dqk_joint_kernel(
+    const float* __restrict__ dmu, const float* __restrict__ dvar, const float* __restrict__ mv,
+    const float* __restrict__ Jg, const float* __restrict__ mq, const float* __restrict__ mk,
+    float* __restrict__ oq_mu, float* __restrict__ oq_var, float* __restrict__ ok_mu, float* __restrict__ ok_var,
+    int H, int S, int ld_d, int ld_x, int ld_o, float scale, float scale_sq) {
+  constexpr int NKT = HD / 16;
+  __shared__ float sm[2 * 32 * kScoreLd];
+  static_assert(8 * 2 * 32 * 32 <= 2 * 32 * kScoreLd, "partials must fit the score tile");
+  const int z = blockIdx.x;
+  const int b = z / H, h = z - b * H;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = lane >> 5, rl = lane & 31;
+  // per-head base pointers (uniform) and 32-bit lane offsets from them
+  const float* hdm = dmu + (int64_t)b * S * ld_d + (int64_t)h * HD;
+  const float* hdv = dvar + (int64_t)b * S * ld_d + (int64_t)h * HD;
+  const float* hv = mv + (int64_t)b * S * ld_x + (int64_t)h * HD;
+  // mu_q, mu_k and J through buffer resources (scalar registers) and 32-bit byte offsets in
+  // the vector offset, the one the hardware checks against the range: rows at or past S lie
+  // beyond the head's range and read as zeros (no per-element masks, no 64-bit addresses);
+  // the scalar offset is left 0 because it is not range-checked
+  const int64_t head_bytes = 4 * ((int64_t)(S - 1) * ld_x + HD);
+  const tagi_i32x4 rq = make_buffer_rsrc(mq + (int64_t)b * S * ld_x + (int64_t)h * HD, head_bytes);
+  const tagi_i32x4 rk = make_buffer_rsrc(mk + (int64_t)b * S * ld_x + (int64_t)h * HD, head_bytes);
+  const tagi_i32x4 rJ = make_buffer_rsrc(Jg + (int64_t)z * S * S, 4 * (int64_t)S * S);
+  const int64_t bo = (int64_t)b * S * ld_o + (int64_t)h * HD;
+  float* hqm = oq_mu + bo;
+  float* hqv = oq_var + bo;
+  float* hkm = ok_mu + bo;
+  float* hkv = ok_var + bo;
+  const bool active = wave * 32 < S;  // this wave's 32 keys exist
+  const int nw = (S + 31) / 32;
+  floatx16 kM, kV;  // key deltas of keys 32 wave + (accumulator row), columns d = rl
+#pragma unroll
+  for (int v = 0; v < 16; ++v) kM[v] = kV[v] = 0.f;
+
+#pragma unroll 1
+  for (int o0 = 0; o0 < S; o0 += 32) {
+    // phase 1: scaled score deltas of query rows o0.. x this wave's keys (attn_dqk_kernel's
+    // products and order; the operands of one 16-wide k-tile at a time and the Jacobian read
+    // at the scaling, which keeps the key-delta accumulators in registers without spilling)
+    if (active) {
+      const int ai = o0 + rl, bj = 32 * wave + rl;
+      floatx16 accM, accV;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) accM[v] = accV[v] = 0.f;
+#pragma unroll
+      for (int t = 0; t < NKT; ++t) {
+        float am[8], av[8], bm[8];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x, w = x;
+          const int ko = 8 * hl + 16 * t + 4 * u;
+          if (ai < S) {
+            x = *reinterpret_cast<const float4*>(hdm + (ko + ai * ld_d));
+            y = *reinterpret_cast<const float4*>(hdv + (ko + ai * ld_d));
+          }
+          if (bj < S) w = *reinterpret_cast<const float4*>(hv + (ko + bj * ld_x));
+          am[4 * u + 0] = x.x, am[4 * u + 1] = x.y, am[4 * u + 2] = x.z, am[4 * u + 3] = x.w;
+          av[4 * u + 0] = y.x, av[4 * u + 1] = y.y, av[4 * u + 2] = y.z, av[4 * u + 3] = y.w;
+          bm[4 * u + 0] = w.x, bm[4 * u + 1] = w.y, bm[4 * u + 2] = w.z, bm[4 * u + 3] = w.w;
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const float b0 = bm[s], bsq = b0 * b0;
+          accM = __builtin_amdgcn_mfma_f32_32x32x2f32(am[s], b0, accM, 0, 0, 0);
+          accV = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s], bsq, accV, 0, 0, 0);
+        }
+      }
+      // J of query rows o0 + 4 hl + c_v, c_v = 8 (v / 4) + v % 4; rows past S read 0, and key
+      // columns past S (last tile) hold score deltas that are exactly 0 (their mu_v was 0)
+      int jvo = 4 * ((o0 + 4 * hl) * S + bj);
+      __asm__ volatile("" : "+v"(jvo));  // one offset per lane; the 16 sums below stay transient
+      float* sw = sm + 4 * hl * kScoreLd + 32 * wave + rl;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int cv = 8 * (v >> 2) + (v & 3);
+        const float jj = tagi_raw_buffer_load_f32(rJ, jvo + 4 * cv * S, 0, 0);
+        float m = accM[v] * 1.f + 0.f, vv = accV[v] * 1.f + 0.f;
+        m *= jj;
+        vv *= jj * jj;
+        sw[cv * kScoreLd] = m;
+        sw[32 * kScoreLd + cv * kScoreLd] = vv;
+      }
+    }
+    __syncthreads();
+    // phase 2: query rows times mu_k over this wave's keys (partials), and this wave's keys
+    // times mu_q over the block's query rows (into the key-delta accumulators)
+    floatx16 pM, pV;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) pM[v] = pV[v] = 0.f;
+    if (active) {
+      // key 32 wave + 8 hl + c_q (query o0 + 8 hl + c_q), c_q = 16 (q / 8) + q % 8, column d = rl;
+      // for head dimension 16 the lanes rl >= 16 read other columns, which only reach
+      // accumulator columns that are never stored
+      float xk[16], xq[16];
+      int xko = 4 * ((32 * wave + 8 * hl) * ld_x + rl);
+      __asm__ volatile("" : "+v"(xko));  // kept per query block: hoisted sums would spill
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        xk[q] = tagi_raw_buffer_load_f32(rk, xko + 4 * (16 * (q >> 3) + (q & 7)) * ld_x, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const int k = 32 * wave + 16 * t + 8 * hl + s;  // key index (reduction of the query deltas)
+          const float a0 = sm[rl * kScoreLd + k], a1 = sm[32 * kScoreLd + rl * kScoreLd + k];
+          const float x = xk[8 * t + s];
+          const float xsq = x * x;
+          pM = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, x, pM, 0, 0, 0);
+          pV = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, xsq, pV, 0, 0, 0);
+        }
+      int xqo = 4 * ((o0 + 8 * hl) * ld_x + rl);
+      __asm__ volatile("" : "+v"(xqo));
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        xq[q] = tagi_raw_buffer_load_f32(rq, xqo + 4 * (16 * (q >> 3) + (q & 7)) * ld_x, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const int q = 16 * t + 8 * hl + s;  // query row in the block (reduction of the key deltas)
+          const float a0 = sm[q * kScoreLd + 32 * wave + rl], a1 = sm[32 * kScoreLd + q * kScoreLd + 32 * wave + rl];
+          const float x = xq[8 * t + s];
+          const float xsq = x * x;
+          kM = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, x, kM, 0, 0, 0);
+          kV = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, xsq, kV, 0, 0, 0);
+        }
+    }
+    __syncthreads();
+    // phase 3: query-delta partials in wave order, then the fixed-order sum (attn_dqk_kernel)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int tr = 8 * (v >> 2) + 4 * hl + (v & 3);
+      sm[(wave * 2 + 0) * 1024 + tr * 32 + rl] = pM[v];
+      sm[(wave * 2 + 1) * 1024 + tr * 32 + rl] = pV[v];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int idx = threadIdx.x + 512 * q;
+      const int mom = idx >> 10, row = (idx >> 5) & 31, d = idx & 31;
+      float acc = 0.f;
+      for (int w = 0; w < nw; ++w) acc += sm[(w * 2 + mom) * 1024 + row * 32 + d];
+      if (o0 + row < S && d < HD) {
+        const int o = (o0 + row) * ld_o + d;
+        if (mom == 0) hqm[o] = acc * scale + 0.f;
+        else hqv[o] = acc * scale_sq + 0.f;
+      }
+    }
+    __syncthreads();  // the tile area is written again by the next query block's phase 1
+  }
+  if (active) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int key = 32 * wave + 8 * (v >> 2) + 4 * hl + (v & 3);
+      if (key < S && rl < HD) {
+        const int o = key * ld_o + rl;
+        hkm[o] = kM[v] * scale + 0.f;
+        hkv[o] = kV[v] * scale_sq + 0.f;
+      }
+    }
+  }
+}
 }  // namespace
 
 extern "C" int tagi_attn_score_deltas_qk(const float* d_mu, const float* d_var, int64_t ld_d, const float* mu_v,
@@ -578,5 +752,36 @@ extern "C" int tagi_attn_score_deltas_qk(const float* d_mu, const float* d_var, 
     else TAGI_DQK(32, false);
   }
 #undef TAGI_DQK
+  return check_launch(what);
+}
+
+extern "C" int tagi_attn_score_deltas_qk_joint(const float* d_mu, const float* d_var, int64_t ld_d, const float* mu_v,
+                                               const float* mu_q, const float* mu_k, int64_t ld_x, const float* J,
+                                               float* dq_mu, float* dq_var, float* dk_mu, float* dk_var,
+                                               int64_t ld_out, int64_t B, int64_t H, int64_t S, int64_t D,
+                                               float scale, float scale_sq, tagi_stream_t stream) {
+  const char* what = "tagi_attn_score_deltas_qk_joint";
+  TAGI_REQUIRE(d_mu && d_var && mu_v && mu_q && mu_k && J && dq_mu && dq_var && dk_mu && dk_var, "%s: null pointer",
+               what);
+  TAGI_REQUIRE(B > 0 && H > 0 && S > 0 && D > 0, "%s: bad sizes", what);
+  if (S > 256 || !(D == 16 || D == 32))
+    return fail(TAGI_ERR_UNSUPPORTED, "%s: needs S <= 256 and head_dim 16 or 32 (S=%lld, D=%lld)", what,
+                (long long)S, (long long)D);
+  TAGI_REQUIRE(ld_d >= H * D && ld_x >= H * D && ld_out >= H * D && ld_d % 4 == 0 && ld_x % 4 == 0,
+               "%s: row strides below H*D (or d/x strides not multiples of 4)", what);
+  TAGI_REQUIRE(al16(d_mu) && al16(d_var) && al16(mu_v), "%s: d_mu, d_var and mu_v must be 16-byte aligned", what);
+  TAGI_REQUIRE(B * H < (1ll << 31) && fits_i32(B * S * ld_d) && fits_i32(B * S * ld_x) && fits_i32(B * S * ld_out) &&
+                   (S + 32) * ld_x * 4 < (1ll << 31) && B * H * S * S < (1ll << 40),
+               "%s: too large", what);
+  hipStream_t s = as_stream(stream);
+  // algorithmic work: the score-delta product and the query and key products (2 moments each)
+  ProfScope ps(FAM_BMM_SHARED, s, 2.0 * 6 * B * H * S * S * D, 4.0 * (B * H * S * S + 7 * B * S * H * D));
+  const dim3 grid((unsigned)(B * H));
+#define TAGI_DQKJ(HD_)                                                                                             \
+  hipLaunchKernelGGL((attn_dqk_joint_kernel<HD_>), grid, dim3(512), 0, s, d_mu, d_var, mu_v, J, mu_q, mu_k, dq_mu, \
+                     dq_var, dk_mu, dk_var, (int)H, (int)S, (int)ld_d, (int)ld_x, (int)ld_out, scale, scale_sq)
+  if (D == 16) TAGI_DQKJ(16);
+  else TAGI_DQKJ(32);
+#undef TAGI_DQKJ
   return check_launch(what);
 }

@@ -79,6 +79,8 @@ _SIGS = {
     "tagi_attn_scores_remax": (c_int, [P, P, P, P, I64, P, P, P, I64, I64, I64, I64, F, F, P]),
     "tagi_attn_fwd": (c_int, [P, P, P, P, P, P, I64, P, P, P, P, P, I64, I64, I64, I64, I64, F, F, P]),
     "tagi_attn_score_deltas_qk": (c_int, [P, P, I64, P, P, I64, P, P, P, I64, I64, I64, I64, I64, F, F, c_int, P]),
+    "tagi_attn_score_deltas_qk_joint": (c_int, [P, P, I64, P, P, P, I64, P, P, P, P, P, I64, I64, I64, I64, I64, F,
+                                                F, P]),
     "tagi_bmm_shared": (c_int, [P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),
     "tagi_bmm_shared_jacobian": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, c_int, P]),
     "tagi_conv2d_fwd": (c_int, [P, P, P, P, P, P, P, P, GP, P, I64, P]),

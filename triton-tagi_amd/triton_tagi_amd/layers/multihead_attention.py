@@ -185,10 +185,10 @@ class MultiheadAttentionV2(LearnableLayer):
             raise ValueError(f"MultiheadAttentionV2: stored Remax Jacobian {tuple(jcb.shape)} vs {(B, H, S, S)}")
         if S <= 256 and D in (16, 32) and B * H < 65536 and all(
                 t.data_ptr() % 16 == 0 for t in (d_mu, d_var, qkv)):
-            # the scaled score deltas are formed per block in LDS, never in memory
-            for x, om, oS, tr in ((k_m, dq_m, dq_S, 0), (q_m, dk_m, dk_S, 1)):
-                _lib.call("tagi_attn_score_deltas_qk", d_mu.data_ptr(), d_var.data_ptr(), E, v_m, x, L,
-                          jcb.data_ptr(), om, oS, L, B, H, S, D, s, s * s, tr, st)
+            # the scaled score deltas are formed once per head in LDS, never in memory, and
+            # feed both the query and the key deltas
+            _lib.call("tagi_attn_score_deltas_qk_joint", d_mu.data_ptr(), d_var.data_ptr(), E, v_m, q_m, k_m, L,
+                      jcb.data_ptr(), dq_m, dq_S, dk_m, dk_S, L, B, H, S, D, s, s * s, st)
         else:
             scaled_mu = torch.empty(B, H, S, S, device=dev)
             scaled_var = torch.empty_like(scaled_mu)
