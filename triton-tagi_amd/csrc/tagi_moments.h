@@ -14,7 +14,7 @@ namespace tagi {
 // the inlined helper, and kernels that share the row math (the fused attention forward
 // and the two-call Remax, the conv epilogue's ReLU statistics and the ReLU/BatchNorm
 // pass) must round the same way to give the same bits.
-// The hardware transcendental instructions (v_rcp_f32, v_rsq_f32, v_exp_f32, v_log_f32)
+// The hardware transcendental instructions (v_rcp_f32, v_rsq_f32, v_exp_f32)
 // are accurate to about 1 ulp on normal operands. The library forms add range reduction,
 // denormal scaling and correct rounding that the moment formulas below do not need: their
 // results are checked at a relative tolerance of 1e-4, and every use here is a few ulp.
@@ -33,33 +33,6 @@ __device__ __forceinline__ float fast_exp(float x) {
   const float p = x * L2E;
   const float e = fmaf(x, L2E_LO, fmaf(x, L2E, -p));
   return __builtin_amdgcn_exp2f(p) * fmaf(e, 0.6931471805599453f, 1.0f);
-}
-
-// Natural logarithm of a normal positive x: log2 from v_log_f32 (accurate to about 1 ulp
-// relative, also next to x = 1) times ln 2.
-__device__ __forceinline__ float fast_log(float x) { return __builtin_amdgcn_logf(x) * 0.6931471805599453f; }
-
-// log(1 + x) for x >= 0 (finite) from one logarithm: with u = fl(1 + x), the factor
-// x / (u - 1) corrects the rounding of u (Goldberg, "What every computer scientist should
-// know about floating-point arithmetic", 1991, theorem 4), a few ulp for every x >= 0.
-__device__ __forceinline__ float log1p_pos(float x) {
-  const float u = 1.0f + x;
-  const float d = u - 1.0f;
-  return d == 0.0f ? x : fast_log(u) * fast_div(x, d);
-}
-
-// exp(x) - 1 for x >= 0: the Taylor polynomial through x^7 below 0.35 (truncation below
-// 3e-9 relative there), exp(x) - 1 above (no cancellation: e^x - 1 > 0.41).
-__device__ __forceinline__ float expm1_pos(float x) {
-  if (x >= 0.35f) return fast_exp(x) - 1.0f;
-  float p = 1.0f / 5040.0f;
-  p = fmaf(p, x, 1.0f / 720.0f);
-  p = fmaf(p, x, 1.0f / 120.0f);
-  p = fmaf(p, x, 1.0f / 24.0f);
-  p = fmaf(p, x, 1.0f / 6.0f);
-  p = fmaf(p, x, 0.5f);
-  p = fmaf(p, x, 1.0f);
-  return p * x;
 }
 
 // Upper tail of the standard normal, Q(a) = 0.5 erfc(a / sqrt 2), for a >= 0, by the
@@ -277,23 +250,34 @@ __device__ __forceinline__ void remax_row(const float (&mz)[EPT], const float (&
   const float mu_mt = fmaxf(wave_sum(s_mu), EPS);
   const float var_mt = fmaxf(wave_sum(s_var), EPS);
   const float inv_mt = fast_rcp(mu_mt);
-  // log1p/expm1 below are the reference's log(1 + x) / exp(x) - 1 without fp32 cancellation
-  const float var_log_mt = log1p_pos(var_mt * inv_mt * inv_mt);
-  const float mu_log_mt = fmaf(-0.5f, var_log_mt, fast_log(mu_mt));
-  float var_log_m[EPT], cov_m_mt[EPT], mu_a_raw[EPT], var_log_a[EPT];
+  // The reference's log-normal stage (remax.py:82-105) in closed form. With
+  //   x = S_m / mu_m^2,  y = S_mt / mu_mt^2,  w = S_m / (mu_m mu_mt)
+  // its logarithms are var_log_m = log(1+x), var_log_mt = log(1+y), cov_log_m_mt = log(1+w),
+  // and its exponentials collapse to
+  //   mu_a_raw = exp(mu_log_a + var_log_a / 2)      = (mu_m / mu_mt) (1+y) / (1+w)
+  //   exp(var_log_a) - 1 = (1+x)(1+y)/(1+w)^2 - 1    = (x - w + y - w + xy - w^2) / (1+w)^2
+  //   exp(cov_log_a_log_m) - 1 = (1+x)/(1+w) - 1     = (x - w) / (1+w)
+  // Both differences are >= 0 in exact arithmetic (mu_m <= mu_mt and S_m <= S_mt give
+  // w <= x and w^2 <= xy, so (1+w)^2 <= (1+x)(1+y)); the reference's clamp of var_log_a at 0
+  // and the one here act on rounding only. No logarithm or exponential is left, and the
+  // small differences are formed from their terms (absolute error a few ulp of x, y, w)
+  // instead of from logarithms of 1 + x (an fp32 emulation against float64 puts this form
+  // at or below the log form's error on every row distribution tried).
+  const float y = var_mt * inv_mt * inv_mt;
+  const float c_mt = inv_mt * (1.0f + y);
+  float x_m[EPT], w_m[EPT], rw_m[EPT], mu_a_raw[EPT];
   float s_a = 0.f;
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const float rm = fast_rcp(mu_m[e]);
-    const float vlm = log1p_pos(var_m[e] * rm * rm);
-    const float mlm = fmaf(-0.5f, vlm, fast_log(mu_m[e]));
-    const float cov = log1p_pos(var_m[e] * rm * inv_mt);
-    const float mla = mlm - mu_log_mt;
-    const float vla = fmaxf(fmaf(-2.0f, cov, vlm + var_log_mt), 0.0f);
-    const float mar = fmaxf(fast_exp(fmaf(0.5f, vla, mla)), EPS);
-    var_log_m[e] = vlm;
-    cov_m_mt[e] = cov;
-    var_log_a[e] = vla;
+    const float vr = var_m[e] * rm;
+    const float x = vr * rm;
+    const float w = vr * inv_mt;
+    const float rw = fast_rcp(1.0f + w);
+    const float mar = fmaxf(mu_m[e] * c_mt * rw, EPS);
+    x_m[e] = x;
+    w_m[e] = w;
+    rw_m[e] = rw;
     mu_a_raw[e] = mar;
     if (lane + 64 * e < K) s_a += mar;
   }
@@ -301,10 +285,11 @@ __device__ __forceinline__ void remax_row(const float (&mz)[EPT], const float (&
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const float mua = mu_a_raw[e] * inv_sum_a;
-    const float vara = expm1_pos(var_log_a[e]) * mua * mua;
-    // log-space covariance of a and m: vlm - cov >= 0 up to rounding, since mu_m <= mu_mt
-    const float cov_la_lm = fmaxf(var_log_m[e] - cov_m_mt[e], 0.0f);
-    const float cov_am = expm1_pos(cov_la_lm) * mua * mu_m[e];
+    const float x = x_m[e], w = w_m[e], rw = rw_m[e];
+    const float xw = x - w;
+    const float num = (xw + (y - w)) + fmaf(x, y, -(w * w));
+    const float vara = fmaxf(num, 0.0f) * rw * rw * mua * mua;
+    const float cov_am = fmaxf(xw, 0.0f) * rw * mua * mu_m[e];
     const float cs = __builtin_amdgcn_sqrtf(vara * var_z[e]);
     const float cov_az = fminf(cs, cov_am * fast_rcp(fmaxf(jcb[e], EPS)));
     ma[e] = mua;
