@@ -150,7 +150,9 @@ __device__ __forceinline__ void rect_moments(float mz, float S, float sd, float 
   p = fmaf(p, t, 1.00002368f);
   p = fmaf(p, t, -1.26551223f);
   const float SQRT_PI_2 = 1.2533141373155003f;  // sqrt(pi / 2)
-  const float mills = SQRT_PI_2 * t * fast_exp(p);
+  // p lies in [-1.266, 0] for t in (0, 1], so the rounding of p log2(e) moves exp(p) by at
+  // most 1e-7 relative: the plain 2^(p log2 e) serves, without fast_exp's split product
+  const float mills = SQRT_PI_2 * t * __builtin_amdgcn_exp2f(p * 1.44269502162933349609375f);
   pdf = INV_SQRT_2PI * fast_exp(-0.5f * a * a);
   const float tail = pdf * mills;
   if (alpha >= 0.0f) {
@@ -234,9 +236,11 @@ __device__ __forceinline__ void remax_row(const float (&mz)[EPT], const float (&
     float mraw, vrect, cdf, pdf;
     rect_moments(m, v, sd, al, mraw, vrect, cdf, pdf);
     const float mm = fmaxf(mraw, EPS);
-    // same variance as -mm^2 + 2 mm m - m sd pdf + (v - m^2) cdf while the mean floor is
-    // inactive (see rect_moments); the floored case keeps the reference's expression
-    const float vraw = (mraw >= EPS) ? vrect : -mm * mm + 2.0f * mm * m - m * sd * pdf + (v - m * m) * cdf;
+    // The reference's variance -mm^2 + 2 mm m - m sd pdf + (v - m^2) cdf (remax.py:68-73)
+    // with mm its floored mean equals vrect + (mraw - mm)(mraw + mm - 2 m) exactly, vrect
+    // being the variance of max(z, 0) at its own mean mraw (see rect_moments): the second
+    // term is 0 while the floor is inactive and is formed from two differences otherwise.
+    const float vraw = (mraw >= EPS) ? vrect : fmaf(mraw - EPS, (mraw + EPS) - 2.0f * m, vrect);
     const float vm = fmaxf(vraw, EPS);
     var_z[e] = v;
     mu_m[e] = mm;
