@@ -227,10 +227,13 @@ def measure_stream_variants(dev, src, dst, part, n, cus, st) -> dict:
 
 def linear_bench(args) -> dict:
     """Linear microbenchmark: per shape, W warm-up then K timed steps of forward moments,
-    backward deltas (input deltas and parameter deltas) and the capped update."""
+    backward deltas (input deltas and parameter deltas) and the capped update. As in
+    Sequential.step, the update is applied by the kernel that forms the parameter deltas
+    (update_in_backward); the layer's update() afterwards finds nothing left to do."""
     import torch
 
     from triton_tagi_amd import workloads
+    from triton_tagi_amd.update.in_backward import update_in_backward
     from triton_tagi_amd.update.parameters import get_cap_factor
 
     shapes, total_flops, total_s = [], 0.0, 0.0
@@ -240,7 +243,8 @@ def linear_bench(args) -> dict:
 
         def step():
             layer.forward(ma, Sa)
-            layer.backward(dmz, dSz)
+            with update_in_backward(cap):
+                layer.backward(dmz, dSz)
             layer.update(cap)
 
         for _ in range(args.warmup):

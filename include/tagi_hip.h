@@ -145,6 +145,22 @@ int tagi_linear_wgrad(const float* ma, const float* dmz, const float* dSz, const
                       tagi_stream_t stream);
 int64_t tagi_linear_wgrad_ws_bytes(int64_t M, int64_t K, int64_t N);
 
+/* tagi_linear_wgrad followed by the capped update of the layer's parameters, in one
+ * pass: the epilogue that forms each delta also applies
+ *   m += sign(dm) min(|dm|, sqrt(max(S, 1e-10)) / cap_factor),
+ *   S += sign(dS) min(|dS|, same bound), S <= 0 -> 1e-5
+ * to mw, Sw (and mb, Sb with the bias) in place, with the variance before the update in
+ * the bound and in the deltas. The deltas are still written to dmw, dSw (dmb, dSb). The
+ * bias needs mb, Sb, dmb and dSb together (or none). mw, Sw, mb, Sb must not overlap the
+ * inputs or the delta outputs, and no other work may read them until the call completes
+ * (the layer's input-delta product reads mw: run it first). ws: tagi_linear_wgrad_ws_bytes.
+ * Replaces linear.py:138-151 followed by the layer's update (parameters.py:58-96,
+ * network.py:146-150) for one Linear layer. */
+int tagi_linear_wgrad_update(const float* ma, const float* dmz, const float* dSz, float* mw,
+                             float* Sw, float* mb, float* Sb, float* dmw, float* dSw, float* dmb,
+                             float* dSb, float cap_factor, int64_t M, int64_t K, int64_t N,
+                             float* ws, int64_t ws_bytes, tagi_stream_t stream);
+
 /* ------------------------------------------------------- batched products ---- */
 /* A strided batched operand: element (z, i, j) of batch z sits at
  *   base + (z / zdiv) * sz1 + (z % zdiv) * sz2 + i * si + j * sj

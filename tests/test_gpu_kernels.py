@@ -82,6 +82,49 @@ def test_linear_param_deltas(dev, M, K, N):
     assert_scaled_close(raw_S, gSw, None, RTOL, ATOL, "raw grad Sw")
 
 
+@pytest.mark.parametrize("M,K,N,bias,offset", [(256, 4096, 1100, True, 0), (64, 96, 80, True, 0), (8192, 64, 32, False, 0),
+                                                (300, 77, 45, True, 1), (5, 3, 7, False, 0)])
+def test_linear_param_deltas_update(dev, M, K, N, bias, offset):
+    """tagi_linear_wgrad_update (the capped update applied by the kernel that forms the
+    parameter deltas) against tagi_linear_wgrad followed by tagi_capped_update: the same
+    deltas and the same updated parameters, bit for bit. Split-K (a long reduction) and
+    unsplit plans, with and without the bias, and an input offset by one float (scalar
+    loaders)."""
+    from triton_tagi_amd.kernels.common import linear_param_deltas, linear_param_deltas_update
+    from triton_tagi_amd.update.parameters import update_parameters
+
+    r = g(3 * M + 7 * K + N + offset)
+    a_buf = torch.randn(M * K + offset, generator=r)
+    a = a_buf[offset:].view(M, K)
+    dmz, dSz = 0.1 * torch.randn(M, N, generator=r), -1e-2 * torch.rand(M, N, generator=r)
+    mw, Sw = torch.randn(K, N, generator=r) / K ** 0.5, torch.rand(K, N, generator=r) / K
+    mb, Sb = torch.randn(1, N, generator=r) * 0.1, torch.rand(1, N, generator=r) * 1e-3
+    Sw[0, :4] = torch.tensor([1e-12, 1e-6, 2.0, 0.0])  # caps at the 1e-10 floor and wide ones
+    a_d = a_buf.to(dev)[offset:].view(M, K)  # offset 1: not 16-byte aligned on the device
+    dmz_d, dSz_d = dmz.to(dev), dSz.to(dev)
+    cap = 2.0
+    ref = [t.to(dev) for t in (mw, Sw, mb, Sb)]
+    rdmw, rdSw, rdmb, rdSb = linear_param_deltas(a_d, dmz_d, dSz_d, ref[1], ref[3] if bias else None)
+    update_parameters(ref[0], ref[1], rdmw, rdSw, cap)
+    if bias:
+        update_parameters(ref[2], ref[3], rdmb, rdSb, cap)
+    got = [t.to(dev) for t in (mw, Sw, mb, Sb)]
+    dmw, dSw, dmb, dSb = linear_param_deltas_update(a_d, dmz_d, dSz_d, got[0], got[1], got[2] if bias else None,
+                                                    got[3] if bias else None, cap)
+    torch.cuda.synchronize()
+    assert torch.equal(dmw, rdmw) and torch.equal(dSw, rdSw), "weight deltas differ"
+    assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1]), "updated weights differ"
+    if bias:
+        assert torch.equal(dmb, rdmb) and torch.equal(dSb, rdSb), "bias deltas differ"
+        assert torch.equal(got[2], ref[2]) and torch.equal(got[3], ref[3]), "updated bias differs"
+    else:
+        assert dmb is None and torch.equal(got[2], mb.to(dev)) and torch.equal(got[3], Sb.to(dev))
+    # the update itself against the oracle's capped rule on the deltas
+    um, uS = O.capped_update(d64(mw), d64(Sw), d64(dmw), d64(dSw), cap)
+    assert_scaled_close(got[0], um, None, RTOL, ATOL, "updated mw")
+    assert_scaled_close(got[1], uS, None, RTOL, ATOL, "updated Sw")
+
+
 def test_relu(dev):
     from triton_tagi_amd.layers.relu import bayesian_relu
 

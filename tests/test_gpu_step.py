@@ -190,3 +190,62 @@ def test_linear_microbench_shapes(dev, batch, fan_in, fan_out):
     um, uS = O.capped_update(mw0[kin][:, cols], Sws, dmw_s, dSw_s, get_cap_factor(batch))
     assert_scaled_close(layer.mw[kin][:, cols], um, None, RTOL, ATOL, "updated mw sample")
     assert_scaled_close(layer.Sw[kin][:, cols], uS, None, RTOL, ATOL, "updated Sw sample")
+
+
+@pytest.mark.parametrize("batch,fan_in,fan_out", [(256, 4096, 11008), (4096, 4096, 4096)])
+def test_linear_update_in_backward_equals_backward_then_update(dev, batch, fan_in, fan_out):
+    """The microbenchmark step as bench.py times it (the capped update applied by the
+    parameter-delta kernel, ``update_in_backward``) against backward followed by
+    ``update`` from the same state: the same input deltas, parameter deltas and updated
+    parameters, bit for bit, and the layer's update() afterwards changes nothing."""
+    from triton_tagi_amd import workloads
+    from triton_tagi_amd.update.in_backward import update_in_backward
+    from triton_tagi_amd.update.parameters import get_cap_factor
+
+    cap = get_cap_factor(batch)
+    res = []
+    for fused in (False, True):
+        layer, ma, Sa, dmz, dSz = workloads.linear_microbench(batch, fan_in, fan_out)
+        layer.forward(ma, Sa)
+        if fused:
+            with update_in_backward(cap):
+                dma, dSa = layer.backward(dmz, dSz)
+            assert layer._updated_in_backward
+            before = [t.clone() for t in (layer.mw, layer.Sw, layer.mb, layer.Sb)]
+            layer.update(cap)
+            assert not layer._updated_in_backward
+            torch.cuda.synchronize()
+            assert all(torch.equal(x, y) for x, y in zip(before, (layer.mw, layer.Sw, layer.mb, layer.Sb)))
+        else:
+            dma, dSa = layer.backward(dmz, dSz)
+            layer.update(cap)
+        torch.cuda.synchronize()
+        res.append([dma, dSa, layer.delta_mw, layer.delta_Sw, layer.delta_mb, layer.delta_Sb, layer.mw, layer.Sw,
+                    layer.mb, layer.Sb])
+    names = ("dma", "dSa", "delta_mw", "delta_Sw", "delta_mb", "delta_Sb", "mw", "Sw", "mb", "Sb")
+    for n, x, y in zip(names, *res):
+        assert torch.equal(x, y), f"{n} differs between the fused and the separate update"
+
+
+@pytest.mark.parametrize("name", ["mlp", "transformer", "cnn"])
+def test_step_update_in_backward_equals_update_after(dev, name, monkeypatch):
+    """Sequential.step (Linear layers updated by their parameter-delta kernels) against the
+    same step with that switched off (every layer updated after the backward pass): every
+    parameter and prediction equal, bit for bit (the transformer's head runs its
+    parameter-delta kernel on the side stream)."""
+    from triton_tagi_amd import workloads
+    from triton_tagi_amd.update import in_backward
+
+    outs = []
+    for fused in (True, False):
+        if not fused:
+            monkeypatch.setattr(in_backward, "active", lambda: None)
+        w = workloads.build(name, device="cuda:0")
+        mu, var = w.net.step(w.x, w.y, w.sigma_v)
+        mu2, var2 = w.net.step(w.x, w.y, w.sigma_v)  # a second step from the updated state
+        torch.cuda.synchronize()
+        outs.append([mu, var, mu2, var2] + [t for m, S in gpu_params(w.net) for t in (m, S)])
+        assert not any(getattr(layer, "_updated_in_backward", False) for layer in w.net.layers)
+    assert len(outs[0]) == len(outs[1])
+    for j, (x, y) in enumerate(zip(*outs)):
+        assert torch.equal(x, y), f"{name}: tensor {j} differs"

@@ -85,15 +85,8 @@ __global__ void innovation_kernel(const float* __restrict__ y, const float* __re
 }
 
 // -------------------------------------------------------------------- Capped update
-__device__ __forceinline__ float signf_(float x) { return x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f); }
-
-__device__ __forceinline__ void capped(float& m, float& S, float dm, float dS, float cap) {
-  const float bar = sqrtf(fmaxf(S, 1e-10f)) / cap;
-  m = m + signf_(dm) * fminf(fabsf(dm), bar);
-  const float Sr = S + signf_(dS) * fminf(fabsf(dS), bar);
-  S = (Sr <= 0.f) ? 1e-5f : Sr;
-}
-
+// capped() (tagi_moments.h) is shared with the parameter-delta GEMM epilogue, which can
+// apply the same update while it forms the deltas.
 template <bool VEC>
 __global__ void update_kernel(float* __restrict__ m, float* __restrict__ S, const float* __restrict__ dm,
                               const float* __restrict__ dS, float cap, int64_t n) {

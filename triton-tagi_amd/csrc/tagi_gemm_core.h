@@ -179,6 +179,15 @@ struct Epi {
   int64_t ldw;
   int perm_C, perm_kk2;  // conv: row r = (kh*kk+kw)*C + c maps to weight row c*kk2 + kh*kk + kw
   FastDiv dperm;         // divider for perm_C
+  // kind 1, optional: the capped update applied in place as the deltas are formed
+  // (upd_mw/upd_Sw the weights, upd_mb/upd_Sb the bias, Sw/Sb their variances before the
+  // update: the same arrays as upd_Sw/upd_Sb); each element is read and written by the
+  // one thread that forms its deltas
+  float* upd_mw;
+  float* upd_Sw;
+  float* upd_mb;
+  float* upd_Sb;
+  float cap;
   // kind 2
   ConvG g;
   // kinds 0 and 2: optional addend laid out like the output (out = result + addend; may
@@ -693,12 +702,26 @@ __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col,
       }
       const int64_t idx = (int64_t)wr * e.ldw + col;
       const float s = e.Sw ? e.Sw[idx] : 1.f;
-      e.om[idx] = s * m;
-      e.ov[idx] = (s * s) * v;
+      const float dm = s * m, dS = (s * s) * v;
+      e.om[idx] = dm;
+      e.ov[idx] = dS;
+      if (e.upd_mw) {
+        float pm = e.upd_mw[idx], pS = s;
+        capped(pm, pS, dm, dS, e.cap);
+        e.upd_mw[idx] = pm;
+        e.upd_Sw[idx] = pS;
+      }
     } else {
       const float s = e.Sb ? e.Sb[col] : 1.f;
-      e.dmb[col] = s * m;
-      e.dSb[col] = (s * s) * v;
+      const float dm = s * m, dS = (s * s) * v;
+      e.dmb[col] = dm;
+      e.dSb[col] = dS;
+      if (e.upd_mb) {
+        float pm = e.upd_mb[col], pS = s;
+        capped(pm, pS, dm, dS, e.cap);
+        e.upd_mb[col] = pm;
+        e.upd_Sb[col] = pS;
+      }
     }
   } else {
     // conv input delta: row = pixel q of phase z, col = input channel
@@ -759,13 +782,30 @@ __device__ __forceinline__ bool epi_apply4(const Epi& e, int z, int row, int col
     const float* sp = wrow ? e.Sw : e.Sb;
     float* om = wrow ? e.om : e.dmb;
     float* ov = wrow ? e.ov : e.dSb;
+    float* um = wrow ? e.upd_mw : e.upd_mb;
+    float* uS = wrow ? e.upd_Sw : e.upd_Sb;
     uintptr_t al = (uintptr_t)(om + idx) | (uintptr_t)(ov + idx);
     if (sp) al |= (uintptr_t)(sp + idx);
+    if (um) al |= (uintptr_t)(um + idx) | (uintptr_t)(uS + idx);
     if (al & 15u) return false;
     const float4 s4 = sp ? *reinterpret_cast<const float4*>(sp + idx) : make_float4(1.f, 1.f, 1.f, 1.f);
-    *reinterpret_cast<float4*>(om + idx) = make_float4(s4.x * m[0], s4.y * m[1], s4.z * m[2], s4.w * m[3]);
-    *reinterpret_cast<float4*>(ov + idx) =
-        make_float4((s4.x * s4.x) * v[0], (s4.y * s4.y) * v[1], (s4.z * s4.z) * v[2], (s4.w * s4.w) * v[3]);
+    const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+    float dm[4], dS[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dm[j] = sv[j] * m[j];
+      dS[j] = (sv[j] * sv[j]) * v[j];
+    }
+    *reinterpret_cast<float4*>(om + idx) = make_float4(dm[0], dm[1], dm[2], dm[3]);
+    *reinterpret_cast<float4*>(ov + idx) = make_float4(dS[0], dS[1], dS[2], dS[3]);
+    if (um) {
+      const float4 m4 = *reinterpret_cast<const float4*>(um + idx);
+      float pm[4] = {m4.x, m4.y, m4.z, m4.w}, pS[4] = {sv[0], sv[1], sv[2], sv[3]};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) capped(pm[j], pS[j], dm[j], dS[j], e.cap);
+      *reinterpret_cast<float4*>(um + idx) = make_float4(pm[0], pm[1], pm[2], pm[3]);
+      *reinterpret_cast<float4*>(uS + idx) = make_float4(pS[0], pS[1], pS[2], pS[3]);
+    }
     return true;
   }
   if (e.kind == 0 && e.scol == 1 && !e.jm && !e.am) {
@@ -800,8 +840,9 @@ __device__ __forceinline__ int kred_of(const GemmArgs& g, int z) {
   return ph.nkh * ph.nkw * g.a.g.Cout;
 }
 
-// EPI 1: the kind-2 epilogue with the BatchNorm2D -> ReLU backward folded in (a separate
-// instantiation: its extra registers would otherwise cost every kernel occupancy)
+// EPI 1: the kind-2 epilogue with the BatchNorm2D -> ReLU backward folded in; EPI 2: the
+// kind-1 epilogue with the capped parameter update applied in place (separate
+// instantiations: their extra registers would otherwise cost every kernel occupancy)
 template <int PROD, class CFG, int KA, int KB, int EPI = 0>
 __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   constexpr int BM = CFG::BM, BN = CFG::BN, BK = CFG::BK, WM = CFG::WM, WN = CFG::WN, NTH = CFG::NTH;
@@ -1301,6 +1342,59 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int col = n0 + wn * WN + j * 32 + rl;
+        if constexpr (EPI == 2) {
+          // with the capped update in place: per group of 4 outputs, the variances and
+          // means are loaded before the group's stores (16 at once would cost occupancy)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float sv4[4], pm4[4];
+            int64_t wi[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int row = m0 + wm * WM + i * 32 + 8 * q + 4 * hl + u;
+              sv4[u] = 1.f;
+              pm4[u] = 0.f;
+              wi[u] = -1;
+              if (row < R && col < g.C) {
+                if (row < e.wrows) {
+                  int wr = row;
+                  if (e.perm_C > 0) {
+                    const int kidx = fdiv(row, e.dperm);
+                    wr = (row - kidx * e.perm_C) * e.perm_kk2 + kidx;
+                  }
+                  wi[u] = (int64_t)wr * e.ldw + col;
+                  sv4[u] = e.Sw[wi[u]];
+                  pm4[u] = e.upd_mw[wi[u]];
+                } else {
+                  sv4[u] = e.Sb[col];
+                  pm4[u] = e.upd_mb[col];
+                }
+              }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int row = m0 + wm * WM + i * 32 + 8 * q + 4 * hl + u;
+              if (row < R && col < g.C) {
+                const float sv = sv4[u];
+                const float dm = sv * accM[i][j][4 * q + u], dS = (sv * sv) * accV[i][j][4 * q + u];
+                float pm = pm4[u], pS = sv;
+                capped(pm, pS, dm, dS, e.cap);
+                if (row < e.wrows) {
+                  e.om[wi[u]] = dm;
+                  e.ov[wi[u]] = dS;
+                  e.upd_mw[wi[u]] = pm;
+                  e.upd_Sw[wi[u]] = pS;
+                } else {
+                  e.dmb[col] = dm;
+                  e.dSb[col] = dS;
+                  e.upd_mb[col] = pm;
+                  e.upd_Sb[col] = pS;
+                }
+              }
+            }
+          }
+          continue;
+        }
         float sf[16];
         int64_t widx[16];
 #pragma unroll
@@ -1618,6 +1712,10 @@ static inline int64_t plan_ws_bytes(const Plan& p, int64_t R, int64_t C, int64_t
 #define TAGI_GEMM_COMBOS_SHARED_B_BNF(X)                                                 \
   X(PROD_SHARED_B, LD_CBWD_A4T, LD_CBWD_BK4T) X(PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4)
 static inline bool bnf_cfg(int cfg) { return cfg == 3 || cfg == 4 || cfg == 5; }
+// The Linear parameter-delta loader pairs that also get the in-place update (EPI 2), in
+// every tile config
+#define TAGI_GEMM_COMBOS_SHARED_A_UPD(X)                                                 \
+  X(PROD_SHARED_A, LD_STR_MN4, LD_STR_MN4) X(PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S)
 
 template <int PROD, class CFG, int KA, int KB, int EPI = 0>
 void launch_cfg(const GemmArgs& g, int64_t grid_x, int64_t grid_y, hipStream_t s)
@@ -1665,13 +1763,27 @@ static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, 
       default: launch_cfg<PROD, C32x32, KA, KB, 1>(g, gx, gy, s); break;
     }
   } else {
-    switch (p.cfg) {
-      case 0: launch_cfg<PROD, C128x128, KA, KB>(g, gx, gy, s); break;
-      case 1: launch_cfg<PROD, C128x64, KA, KB>(g, gx, gy, s); break;
-      case 2: launch_cfg<PROD, C64x128, KA, KB>(g, gx, gy, s); break;
-      case 3: launch_cfg<PROD, C64x64, KA, KB>(g, gx, gy, s); break;
-      case 5: launch_cfg<PROD, C128x32, KA, KB>(g, gx, gy, s); break;
-      default: launch_cfg<PROD, C32x32, KA, KB>(g, gx, gy, s); break;
+    // EPI 2 applies its update in the kernel only when unsplit (the reduction's epilogue
+    // does it otherwise, from the same Epi fields)
+    constexpr int E = EPI == 2 ? 2 : 0;
+    if (E == 2 && p.splits > 1) {
+      switch (p.cfg) {
+        case 0: launch_cfg<PROD, C128x128, KA, KB>(g, gx, gy, s); break;
+        case 1: launch_cfg<PROD, C128x64, KA, KB>(g, gx, gy, s); break;
+        case 2: launch_cfg<PROD, C64x128, KA, KB>(g, gx, gy, s); break;
+        case 3: launch_cfg<PROD, C64x64, KA, KB>(g, gx, gy, s); break;
+        case 5: launch_cfg<PROD, C128x32, KA, KB>(g, gx, gy, s); break;
+        default: launch_cfg<PROD, C32x32, KA, KB>(g, gx, gy, s); break;
+      }
+    } else {
+      switch (p.cfg) {
+        case 0: launch_cfg<PROD, C128x128, KA, KB, E>(g, gx, gy, s); break;
+        case 1: launch_cfg<PROD, C128x64, KA, KB, E>(g, gx, gy, s); break;
+        case 2: launch_cfg<PROD, C64x128, KA, KB, E>(g, gx, gy, s); break;
+        case 3: launch_cfg<PROD, C64x64, KA, KB, E>(g, gx, gy, s); break;
+        case 5: launch_cfg<PROD, C128x32, KA, KB, E>(g, gx, gy, s); break;
+        default: launch_cfg<PROD, C32x32, KA, KB, E>(g, gx, gy, s); break;
+      }
     }
   }
   int rc = check_launch(what);

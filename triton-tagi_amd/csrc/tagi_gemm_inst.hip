@@ -37,6 +37,9 @@ TAGI_GEMM_COMBOS_SHARED_B_BNF(TAGI_INST_BNF)
 #endif
 #else
 TAGI_GEMM_COMBOS_SHARED_A(TAGI_INST)
+#define TAGI_INST_UPD(P, KA, KB) \
+  template void launch_cfg<P, InstCfg, KA, KB, 2>(const GemmArgs&, int64_t, int64_t, hipStream_t);
+TAGI_GEMM_COMBOS_SHARED_A_UPD(TAGI_INST_UPD)
 #endif
 
 }  // namespace tagi

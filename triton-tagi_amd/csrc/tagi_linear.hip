@@ -100,22 +100,32 @@ extern "C" int64_t tagi_linear_wgrad_ws_bytes(int64_t M, int64_t K, int64_t N) {
   return plan_ws_bytes(linear_wgrad_plan(M, K, N), K + 1, N, 1);
 }
 
-extern "C" int tagi_linear_wgrad(const float* ma, const float* dmz, const float* dSz, const float* Sw, const float* Sb,
-                                 float* dmw, float* dSw, float* dmb, float* dSb, int64_t M, int64_t K, int64_t N,
-                                 float* ws, int64_t ws_bytes, tagi_stream_t stream) {
-  const char* what = "tagi_linear_wgrad";
+namespace {
+// The parameter-delta product of tagi_linear_wgrad; with mw non-null, also the capped
+// update of mw, Sw (and of mb, Sb with the bias) in the epilogue.
+int linear_wgrad_impl(const char* what, const float* ma, const float* dmz, const float* dSz, const float* Sw,
+                      const float* Sb, float* dmw, float* dSw, float* dmb, float* dSb, float* mw, float* mb,
+                      float cap, int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
   TAGI_REQUIRE(ma && dmz && dSz && dmw && dSw, "%s: null pointer", what);
   TAGI_REQUIRE((dmb == nullptr) == (dSb == nullptr), "%s: dmb and dSb must both be given or both be NULL", what);
   TAGI_REQUIRE(M > 0 && K > 0 && N > 0, "%s: sizes must be positive", what);
   TAGI_REQUIRE(fits_i32(M * K) && fits_i32((K + 1) * N) && fits_i32(M * N), "%s: too large for 32-bit tiles", what);
   hipStream_t s = as_stream(stream);
-  ProfScope ps(FAM_LINEAR_WGRAD, s, 2.0 * 2 * M * K * N, 4.0 * (M * K + 2 * M * N + 3 * K * N));
+  ProfScope ps(FAM_LINEAR_WGRAD, s, 2.0 * 2 * M * K * N,
+               4.0 * (M * K + 2 * M * N + 3 * K * N + (mw ? 3 * K * N : 0)));
   const bool bias = dmb != nullptr;
   GemmArgs g{};
   g.a = strided_operand(ma, nullptr, 1, 0, 0, 1, K, K, M);
   if (bias) g.a.ones_row = (int)K;
   g.b = strided_operand(dmz, dSz, 1, 0, 0, 1, N, N, M);
   g.epi = epi_wgrad(dmw, dSw, dmb, dSb, Sw, Sb, K, N);
+  if (mw) {
+    g.epi.upd_mw = mw;
+    g.epi.upd_Sw = const_cast<float*>(Sw);
+    g.epi.upd_mb = mb;
+    g.epi.upd_Sb = const_cast<float*>(Sb);
+    g.epi.cap = cap;
+  }
   g.R = (int)(K + (bias ? 1 : 0));
   g.C = (int)N;
   g.Kred = (int)M;
@@ -124,8 +134,33 @@ extern "C" int tagi_linear_wgrad(const float* ma, const float* dmz, const float*
     p = choose_plan(K + 1, N, M, 1, PROD_SHARED_A, false, 1);
   p.tiles_m = (int)cdiv(g.R, kCfg[p.cfg].BM);
   const bool v4 = K % 4 == 0 && N % 4 == 0 && al16(ma) && al16(dmz) && al16(dSz);
+  if (mw) {
+    if (v4) return run_gemm<PROD_SHARED_A, LD_STR_MN4, LD_STR_MN4, 2>(g, 1, p, ws, ws_bytes, s, what);
+    return run_gemm<PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S, 2>(g, 1, p, ws, ws_bytes, s, what);
+  }
   if (v4) return run_gemm<PROD_SHARED_A, LD_STR_MN4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
   return run_gemm<PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
+}
+}  // namespace
+
+extern "C" int tagi_linear_wgrad(const float* ma, const float* dmz, const float* dSz, const float* Sw, const float* Sb,
+                                 float* dmw, float* dSw, float* dmb, float* dSb, int64_t M, int64_t K, int64_t N,
+                                 float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+  return linear_wgrad_impl("tagi_linear_wgrad", ma, dmz, dSz, Sw, Sb, dmw, dSw, dmb, dSb, nullptr, nullptr, 0.f, M,
+                           K, N, ws, ws_bytes, stream);
+}
+
+extern "C" int tagi_linear_wgrad_update(const float* ma, const float* dmz, const float* dSz, float* mw, float* Sw,
+                                        float* mb, float* Sb, float* dmw, float* dSw, float* dmb, float* dSb,
+                                        float cap_factor, int64_t M, int64_t K, int64_t N, float* ws,
+                                        int64_t ws_bytes, tagi_stream_t stream) {
+  const char* what = "tagi_linear_wgrad_update";
+  TAGI_REQUIRE(mw && Sw, "%s: null pointer", what);
+  TAGI_REQUIRE((dmb == nullptr) == (mb == nullptr) && (mb == nullptr) == (Sb == nullptr),
+               "%s: the bias needs mb, Sb, dmb and dSb together (or none of them)", what);
+  TAGI_REQUIRE(cap_factor > 0.f && cap_factor <= 3.4e38f, "%s: cap_factor must be positive and finite", what);
+  return linear_wgrad_impl(what, ma, dmz, dSz, Sw, Sb, dmw, dSw, dmb, dSb, mw, mb, cap_factor, M, K, N, ws, ws_bytes,
+                           stream);
 }
 
 // ------------------------------------------------------------------- Embedding

@@ -63,6 +63,22 @@ __device__ __forceinline__ void normal_cdf_pair(float alpha, float& cdf, float& 
   ccdf = alpha >= 0.0f ? tail : 1.0f - tail;
 }
 
+// ----------------------------------------------------------------------- Capped update
+// One parameter's capped update (parameters.py:58-96): each of the mean and variance
+// deltas is clipped to sqrt(max(S, 1e-10)) / cap in magnitude, keeping its sign, and a
+// variance that would end at or below 0 becomes 1e-5. Used by the update kernels and by
+// the parameter-delta GEMM epilogue that applies the update in place; contraction is off
+// so that both round alike.
+__device__ __forceinline__ float signf_(float x) { return x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f); }
+
+__device__ __forceinline__ void capped(float& m, float& S, float dm, float dS, float cap) {
+#pragma clang fp contract(off)
+  const float bar = sqrtf(fmaxf(S, 1e-10f)) / cap;
+  m = m + signf_(dm) * fminf(fabsf(dm), bar);
+  const float Sr = S + signf_(dS) * fminf(fabsf(dS), bar);
+  S = (Sr <= 0.f) ? 1e-5f : Sr;
+}
+
 // ------------------------------------------------------------------------------ ReLU
 // relu.py:43-86: exact rectified-Gaussian moments; Phi by erf, replaced by the
 // asymptotic pdf/(-alpha) when alpha < -5; variance floored at 0.

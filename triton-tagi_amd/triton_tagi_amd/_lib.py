@@ -74,6 +74,7 @@ _SIGS = {
     "tagi_linear_bwd_delta_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_linear_bwd_delta_add": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
     "tagi_linear_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
+    "tagi_linear_wgrad_update": (c_int, [P, P, P, P, P, P, P, P, P, P, P, F, I64, I64, I64, P, I64, P]),
     "tagi_linear_wgrad_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_bmm_tagi": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, VP, VP, VP, F, F, P]),
     "tagi_attn_scores_remax": (c_int, [P, P, P, P, I64, P, P, P, I64, I64, I64, I64, F, F, P]),

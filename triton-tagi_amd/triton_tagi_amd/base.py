@@ -32,6 +32,11 @@ class Layer(ABC):
 class LearnableLayer(Layer):
     """Base class for layers with parameters updated by the capped TAGI rule."""
 
+    # True after a backward pass that applied the layer's capped update itself (within
+    # update_in_backward); the next update() of the layer, or of the Sequential holding
+    # it, leaves the layer out once and clears it.
+    _updated_in_backward = False
+
     @abstractmethod
     def update(self, cap_factor: float) -> None:
         """Apply the parameter deltas stored by ``backward``."""

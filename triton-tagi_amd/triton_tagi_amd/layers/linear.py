@@ -3,7 +3,8 @@
 Forward (one fused fp32-MFMA launch):
     mu_z = mu_a @ mu_w + mu_b
     S_z  = mu_a^2 @ S_w + S_a @ (mu_w^2 + S_w) + S_b
-Backward (deltas stored, applied by ``update``):
+Backward (deltas stored, applied by ``update``, or by the backward pass itself within
+``update_in_backward``):
     delta_mw = S_w * (mu_a^T @ delta_mz)        delta_mb = S_b * sum delta_mz
     delta_Sw = S_w^2 * ((mu_a^2)^T @ delta_Sz)  delta_Sb = S_b^2 * sum delta_Sz
     delta_ma = delta_mz @ mu_w^T,  delta_Sa = delta_Sz @ (mu_w^2)^T
@@ -18,8 +19,9 @@ from torch import Tensor
 
 from .. import _overlap
 from ..base import LearnableLayer
-from ..kernels.common import fused_backward_delta, linear_forward, linear_param_deltas
+from ..kernels.common import fused_backward_delta, linear_forward, linear_param_deltas, linear_param_deltas_update
 from ..param_init import init_weight_bias_linear
+from ..update import in_backward
 from ..update.parameters import update_parameters
 
 
@@ -58,20 +60,34 @@ class Linear(LearnableLayer):
     def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool, add=None):
         """Parameter deltas, and the input deltas when ``input_deltas``; with ``add`` (a pair
         of contiguous tensors shaped like the input deltas) those are added to it in place
-        and ``add`` is returned."""
+        and ``add`` is returned. Within ``update_in_backward`` the kernel that forms the
+        parameter deltas also applies the capped update (after the input deltas, which read
+        the weight means, are queued)."""
         dmz = delta_mz.reshape(-1, self.out_features).contiguous()
         dSz = delta_Sz.reshape(-1, self.out_features).contiguous()
+        upd = in_backward.active()
+        out = None
+        if upd is not None and input_deltas:
+            out = self._input_deltas(dmz, dSz, add)
         ctx = _overlap.active()
         big = dmz.shape[0] * self.in_features * self.out_features >= _overlap.MIN_MACS_LINEAR
         side = ctx.fork(dmz.device, self.ma_in, dmz, dSz) if ctx is not None and big else None
+        bias = (self.mb, self.Sb) if self.has_bias else (None, None)
         with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
-            dmw, dSw, dmb, dSb = linear_param_deltas(self.ma_in, dmz, dSz, self.Sw,
-                                                     self.Sb if self.has_bias else None)
+            if upd is not None:
+                dmw, dSw, dmb, dSb = linear_param_deltas_update(self.ma_in, dmz, dSz, self.mw, self.Sw, *bias,
+                                                                upd.cap_factor)
+            else:
+                dmw, dSw, dmb, dSb = linear_param_deltas(self.ma_in, dmz, dSz, self.Sw, bias[1])
+        self._updated_in_backward = upd is not None
         self.delta_mw, self.delta_Sw = dmw, dSw
         if self.has_bias:
             self.delta_mb, self.delta_Sb = dmb, dSb
-        if not input_deltas:
-            return None
+        if not input_deltas or upd is not None:
+            return out
+        return self._input_deltas(dmz, dSz, add)
+
+    def _input_deltas(self, dmz: Tensor, dSz: Tensor, add):
         if add is not None:
             fused_backward_delta(dmz, dSz, self.mw, add=(add[0].view(-1, self.in_features),
                                                          add[1].view(-1, self.in_features)))
@@ -87,6 +103,9 @@ class Linear(LearnableLayer):
         return items
 
     def update(self, cap_factor: float) -> None:
+        if self._updated_in_backward:  # the backward pass applied it (update_in_backward)
+            self._updated_in_backward = False
+            return
         for m, S, dm, dS in self._update_items():
             update_parameters(m, S, dm, dS, cap_factor)
 

@@ -20,6 +20,7 @@ from .layers.conv2d import Conv2D
 from .layers.fused import backward_chain, defer_bn_parameter_deltas, forward_chain
 from .layers.multihead_attention import MultiheadAttentionV2
 from .update.observation import compute_innovation, hrc_innovation
+from .update.in_backward import update_in_backward
 from .update.parameters import get_cap_factor, update_parameters_multi
 
 
@@ -78,6 +79,9 @@ class Sequential:
         for layer in self.layers:
             if not isinstance(layer, LearnableLayer):
                 continue
+            if layer._updated_in_backward:  # the backward pass applied it (update_in_backward)
+                layer._updated_in_backward = False
+                continue
             got = layer._update_items()
             if got is None:
                 if items:
@@ -98,19 +102,23 @@ class Sequential:
         batch_size = x_batch.shape[0]
         y_pred_mu, y_pred_var = self.forward(x_batch)
         delta_mu, delta_var = compute_innovation(y_batch, y_pred_mu, y_pred_var, sigma_v)
-        with self._backward_scope():
+        cap = get_cap_factor(batch_size)
+        with self._backward_scope(cap):
             backward_chain(self.layers, delta_mu, delta_var, first_params_only=True)
-        self.update(get_cap_factor(batch_size))
+        self.update(cap)
         return y_pred_mu, y_pred_var
 
-    def _backward_scope(self):
+    def _backward_scope(self, cap_factor: float):
         """One launch forms every BatchNorm2D's parameter deltas at the end of the backward
         pass; with ``overlap_param_deltas`` the Conv2D parameter-delta GEMMs run on a side
-        stream beside the input-delta chain (joined before the update)."""
+        stream beside the input-delta chain (joined before the update); Linear layers apply
+        their capped update in the kernel that forms their parameter deltas
+        (``update_in_backward``), and the update after the backward pass does the rest."""
         stack = contextlib.ExitStack()
         stack.enter_context(defer_bn_parameter_deltas())
         if self.overlap_param_deltas:  # exits first: the side stream is joined before the BN finalize
             stack.enter_context(_overlap.overlap_param_deltas())
+        stack.enter_context(update_in_backward(cap_factor))
         return stack
 
     def step_hrc(self, x_batch: Tensor, labels: Tensor, hrc, sigma_v: float) -> tuple[Tensor, Tensor]:
@@ -125,9 +133,10 @@ class Sequential:
         width = shape[-1]
         delta_mu, delta_var = hrc_innovation(y_pred_mu.reshape(-1, width), y_pred_var.reshape(-1, width), labels,
                                              hrc, sigma_v)
-        with self._backward_scope():
+        cap = get_cap_factor(batch_size)
+        with self._backward_scope(cap):
             backward_chain(self.layers, delta_mu.reshape(shape), delta_var.reshape(shape), first_params_only=True)
-        self.update(get_cap_factor(batch_size))
+        self.update(cap)
         return y_pred_mu, y_pred_var
 
     def capture_step(self, x_batch: Tensor, y_batch: Tensor, sigma_v: float) -> "StepGraph":
