@@ -227,25 +227,40 @@ def test_linear_update_in_backward_equals_backward_then_update(dev, batch, fan_i
         assert torch.equal(x, y), f"{n} differs between the fused and the separate update"
 
 
-@pytest.mark.parametrize("name", ["mlp", "transformer", "cnn"])
-def test_step_update_in_backward_equals_update_after(dev, name, monkeypatch):
+@pytest.mark.parametrize("name,overlap", [("mlp", True), ("cnn", True), ("transformer", False), ("transformer", True)])
+def test_step_update_in_backward_equals_update_after(dev, name, overlap, monkeypatch):
     """Sequential.step (Linear layers updated by their parameter-delta kernels) against the
     same step with that switched off (every layer updated after the backward pass): every
-    parameter and prediction equal, bit for bit (the transformer's head runs its
-    parameter-delta kernel on the side stream)."""
+    parameter and prediction equal, bit for bit, over two steps. With the side stream on,
+    the transformer's head (a product big enough for it) keeps the separate update."""
     from triton_tagi_amd import workloads
+    from triton_tagi_amd.layers import linear as linear_mod
     from triton_tagi_amd.update import in_backward
 
+    fused_calls = []
+    real = linear_mod.linear_param_deltas_update
+
+    def counting(*a, **k):
+        fused_calls.append(1)
+        return real(*a, **k)
+
+    monkeypatch.setattr(linear_mod, "linear_param_deltas_update", counting)
     outs = []
     for fused in (True, False):
         if not fused:
             monkeypatch.setattr(in_backward, "active", lambda: None)
         w = workloads.build(name, device="cuda:0")
+        w.net.overlap_param_deltas = overlap
         mu, var = w.net.step(w.x, w.y, w.sigma_v)
         mu2, var2 = w.net.step(w.x, w.y, w.sigma_v)  # a second step from the updated state
         torch.cuda.synchronize()
         outs.append([mu, var, mu2, var2] + [t for m, S in gpu_params(w.net) for t in (m, S)])
         assert not any(getattr(layer, "_updated_in_backward", False) for layer in w.net.layers)
+        if fused:
+            n_fused = len(fused_calls)
+            n_linear = sum(isinstance(layer, linear_mod.Linear) for layer in w.net.layers)
+    assert n_fused == (0 if (name, overlap) == ("transformer", True) else 2 * n_linear)
+    assert len(fused_calls) == n_fused  # none with the switch off
     assert len(outs[0]) == len(outs[1])
     for j, (x, y) in enumerate(zip(*outs)):
         assert torch.equal(x, y), f"{name}: tensor {j} differs"

@@ -62,15 +62,18 @@ class Linear(LearnableLayer):
         of contiguous tensors shaped like the input deltas) those are added to it in place
         and ``add`` is returned. Within ``update_in_backward`` the kernel that forms the
         parameter deltas also applies the capped update (after the input deltas, which read
-        the weight means, are queued)."""
+        the weight means, are queued), unless that kernel goes to the side stream."""
         dmz = delta_mz.reshape(-1, self.out_features).contiguous()
         dSz = delta_Sz.reshape(-1, self.out_features).contiguous()
-        upd = in_backward.active()
+        ctx = _overlap.active()
+        big = dmz.shape[0] * self.in_features * self.out_features >= _overlap.MIN_MACS_LINEAR
+        # a parameter-delta product bound for the side stream would have to wait for the
+        # input deltas before updating in place, losing its overlap (transformer block
+        # -1.7%): such layers keep the update for after the backward pass
+        upd = in_backward.active() if ctx is None or not big else None
         out = None
         if upd is not None and input_deltas:
             out = self._input_deltas(dmz, dSz, add)
-        ctx = _overlap.active()
-        big = dmz.shape[0] * self.in_features * self.out_features >= _overlap.MIN_MACS_LINEAR
         side = ctx.fork(dmz.device, self.ma_in, dmz, dSz) if ctx is not None and big else None
         bias = (self.mb, self.Sb) if self.has_bias else (None, None)
         with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():

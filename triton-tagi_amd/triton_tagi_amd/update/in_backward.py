@@ -11,10 +11,14 @@ cross HBM once instead of being written, read back and written again (the Linear
 of 4096 x 11008 moves 540 MB less per step).
 
 A layer's own input deltas read its weight means, so that product is queued before the
-update; no other layer reads them during the backward pass. The layer remembers that
-its groups are updated, and its next ``update`` / ``_update_items`` leaves them out
-(once), so ``Sequential.update`` after the backward pass updates every other layer and
-these ones exactly once.
+update; no other layer reads them during the backward pass. A layer whose
+parameter-delta product runs on the side stream (``overlap_param_deltas``) is left to
+the update after the backward pass: there the product starts beside the input deltas,
+and waiting for them to update in place costs more than the traffic it saves.
+
+A layer updated this way is flagged (``_updated_in_backward``); its next ``update()``,
+or that of the Sequential holding it, leaves it out once and clears the flag, so every
+layer is updated exactly once per step.
 """
 
 from __future__ import annotations
