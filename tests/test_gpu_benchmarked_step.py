@@ -534,6 +534,15 @@ def _install_transformer(monkeypatch, rec):
                 return out
 
             monkeypatch.setattr(cls, meth, wrap)
+    # the step's first layer forms only its parameter deltas (the token ids take none)
+    orig_pd = Embedding.backward_param_deltas
+
+    def emb_param_deltas(self, a, b):
+        out = orig_pd(self, a, b)
+        rec.append(dict(kind="backward_param_deltas", layer=self, a=cl(a), b=cl(b), out=None))
+        return out
+
+    monkeypatch.setattr(Embedding, "backward_param_deltas", emb_param_deltas)
 
     orig_f = MultiheadAttentionV2.forward
 
@@ -614,7 +623,7 @@ def test_transformer_b64_s256_step_teacher_forced(dev, monkeypatch):
     expect = [("forward", "Embedding"), ("forward", "PositionalEncoding"), ("mha_forward", "MultiheadAttentionV2"),
               ("forward", "RMSNorm"), ("forward", "Linear"), ("innovation", "NoneType"), ("backward", "Linear"),
               ("backward", "RMSNorm"), ("mha_backward", "MultiheadAttentionV2"), ("backward", "PositionalEncoding"),
-              ("backward", "Embedding")]
+              ("backward_param_deltas", "Embedding")]
     assert kinds == expect, f"passes of the step: {kinds}"
     f_emb, f_pe, f_att, f_rms, f_head, r_inn, b_head, b_rms, b_att, b_pe, b_emb = rec
     D = emb.embedding_dim
@@ -682,7 +691,7 @@ def test_transformer_b64_s256_step_teacher_forced(dev, monkeypatch):
     sum_S = torch.zeros(V, D, dtype=torch.float64).index_add_(0, flat, dS)
     rep.check("Embedding delta_mw", emb.delta_mw, oemb.Sw * sum_m, oemb.Sw * sum_abs)
     rep.check("Embedding delta_Sw", emb.delta_Sw, oemb.Sw ** 2 * sum_S)
-    assert not b_emb["out"][0].any() and not b_emb["out"][1].any()
+    assert b_emb["out"] is None  # no deltas for the token ids
 
     # capped update of every parameter tensor from its pre-step value and the GPU's deltas
     cap = O.get_cap_factor(w.batch)

@@ -47,9 +47,15 @@ class LearnableLayer(Layer):
         """Total number of learnable scalars (means + variances)."""
 
     def _update_items(self):
-        """(m, S, delta_m, delta_S) quadruples ``update`` would apply, in order.
+        """(m, S, delta_m, delta_S) quadruples of the layer's parameter groups, in order.
 
         ``Sequential.step`` uses these to apply every layer's update in one launch; a
         layer that returns None is updated through its own ``update`` instead.
         """
         return None
+
+    def _update_groups(self):
+        """The contiguous (m, S, delta_m, delta_S) groups the update applies: those of
+        ``_update_items`` unless the layer keeps its parameters in larger buffers (the
+        attention layer's projections live side by side)."""
+        return self._update_items()

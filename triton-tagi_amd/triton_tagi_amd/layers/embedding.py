@@ -46,6 +46,13 @@ class Embedding(LearnableLayer):
         return mz, Sz
 
     def backward(self, delta_mz: Tensor, delta_Sz: Tensor) -> tuple[Tensor, Tensor]:
+        tokens = self.backward_param_deltas(delta_mz, delta_Sz)
+        zeros = torch.zeros(tokens.shape, device=tokens.device, dtype=delta_mz.dtype)
+        return zeros, zeros.clone()
+
+    def backward_param_deltas(self, delta_mz: Tensor, delta_Sz: Tensor):
+        """The parameter deltas of ``backward`` without the (zero) deltas of the token ids;
+        returns the ids."""
         tokens = self.cat_idx
         D = self.embedding_dim
         dm = _lib.check(delta_mz.reshape(-1, D).contiguous(), "delta_mz")
@@ -58,8 +65,7 @@ class Embedding(LearnableLayer):
         _lib.call("tagi_embedding_bwd", tokens.data_ptr(), dm.data_ptr(), dS.data_ptr(), self.Sw.data_ptr(),
                   self.delta_mw.data_ptr(), self.delta_Sw.data_ptr(), n, self.num_embeddings, D,
                   int(self.padding_idx), wp, wb, _lib.stream_of(dm))
-        zeros = torch.zeros(tokens.shape, device=tokens.device, dtype=delta_mz.dtype)
-        return zeros, zeros.clone()
+        return tokens
 
     def _update_items(self):
         return [(self.mw, self.Sw, self.delta_mw, self.delta_Sw)]

@@ -12,8 +12,10 @@ Backward (deterministic operand shared per product):
     dscore = d_out @ mu_v^T           (var: mu_v^2), then * J and * J^2
     dQ     = s dscore @ mu_k,  dK = s dscore^T @ mu_q   (var: s^2, squared operand)
 and the three projection backwards are summed: one input-delta product over the (B*S, 3E)
-deltas of Q, K and V, one parameter-delta product whose (E, 3E) result is split into the
-three layers' deltas.
+deltas of Q, K and V, one parameter-delta product whose (E, 3E) result holds the three
+layers' deltas side by side. The projections' parameters live side by side as well (each
+Linear's tensors are column views of (E, 3E) / (1, 3E) buffers), so neither direction
+concatenates or splits tensors.
 """
 
 from __future__ import annotations
@@ -27,6 +29,7 @@ from torch import Tensor
 from .. import _lib, _overlap
 from ..base import LearnableLayer
 from ..kernels.common import fused_backward_delta, linear_forward, linear_param_deltas
+from ..update.parameters import update_parameters_multi
 from .linear import Linear
 from .remax import remax
 
@@ -82,6 +85,42 @@ class MultiheadAttentionV2(LearnableLayer):
     def _projections(self):
         return (self.q_proj, self.k_proj, self.v_proj)
 
+    _QKV_ATTRS = ("mw", "Sw", "mb", "Sb")
+
+    def _qkv_params(self) -> dict:
+        """The three projections' parameters side by side: (E, 3E) weights and (1, 3E)
+        biases, which the fused projection product and the update read directly. Each
+        projection's mw, Sw, mb, Sb are column views of them, so in-place changes to either
+        are seen by both (checkpoint restore copies in place). Built at the first forward;
+        rebuilt from the projections' tensors if any of them was replaced since."""
+        projs = self._projections()
+        bufs = getattr(self, "_qkv", None)
+        if bufs is not None and self._qkv_intact(bufs):
+            return bufs
+        bufs = {}
+        for attr in self._QKV_ATTRS:
+            parts = [getattr(p, attr) for p in projs]
+            if parts[0] is None:
+                continue
+            buf = torch.cat(parts, 1)
+            n = parts[0].shape[1]
+            for i, p in enumerate(projs):
+                setattr(p, attr, buf[:, i * n:(i + 1) * n])
+            bufs[attr] = buf
+        self._qkv = bufs
+        return bufs
+
+    def _qkv_intact(self, bufs: dict) -> bool:
+        for attr, buf in bufs.items():
+            n = buf.shape[1] // 3
+            for i, p in enumerate(self._projections()):
+                t = getattr(p, attr, None)
+                if not (isinstance(t, Tensor) and t.device == buf.device and t.dtype == buf.dtype
+                        and tuple(t.shape) == (buf.shape[0], n) and t.stride() == buf.stride()
+                        and t.data_ptr() == buf.data_ptr() + i * n * buf.element_size()):
+                    return False
+        return True
+
     def sublayers(self) -> tuple:
         return self._projections()
 
@@ -95,10 +134,8 @@ class MultiheadAttentionV2(LearnableLayer):
         ma_flat = ma.reshape(-1, E).contiguous()
         Sa_flat = Sa.reshape(-1, E).contiguous()
         projs = self._projections()
-        w_m = torch.cat([p.mw for p in projs], 1)
-        w_S = torch.cat([p.Sw for p in projs], 1)
-        b_m = torch.cat([p.mb for p in projs], 1) if self.has_bias else None
-        b_S = torch.cat([p.Sb for p in projs], 1) if self.has_bias else None
+        qkv = self._qkv_params()
+        w_m, w_S, b_m, b_S = (qkv.get(a) for a in self._QKV_ATTRS)
         qkv_m, qkv_S = linear_forward(ma_flat, Sa_flat, w_m, w_S, b_m, b_S)
         for p in projs:
             p.ma_in, p._input_shape = ma_flat, ma.shape
@@ -208,24 +245,35 @@ class MultiheadAttentionV2(LearnableLayer):
         side = ctx.fork(dev, ma_in, dqkv_m, dqkv_S, c["w_S"], c["b_S"]) if ctx is not None and big else None
         with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
             dmw, dSw, dmb, dSb = linear_param_deltas(ma_in, dqkv_m, dqkv_S, c["w_S"], c["b_S"])
-            # the (E, 3E) deltas as three contiguous (E, E) blocks: one copy per moment
-            blk_m = dmw.view(E, 3, E).transpose(0, 1).contiguous()
-            blk_S = dSw.view(E, 3, E).transpose(0, 1).contiguous()
-            for i, p in enumerate(projs):
-                p.delta_mw, p.delta_Sw = blk_m[i], blk_S[i]
-                if self.has_bias:
-                    p.delta_mb = dmb[:, i * E:(i + 1) * E].contiguous()
-                    p.delta_Sb = dSb[:, i * E:(i + 1) * E].contiguous()
+        # each projection's deltas are column views of the (E, 3E) ones, as its parameters
+        # are of the side-by-side buffers the update applies them to
+        self._qkv_deltas = (dmw, dSw, dmb, dSb)
+        for i, p in enumerate(projs):
+            cols = slice(i * E, (i + 1) * E)
+            p.delta_mw, p.delta_Sw = dmw[:, cols], dSw[:, cols]
+            if self.has_bias:
+                p.delta_mb, p.delta_Sb = dmb[:, cols], dSb[:, cols]
         dma, dSa = fused_backward_delta(dqkv_m, dqkv_S, c["w_m"])
         return dma.reshape(B, S, E), dSa.reshape(B, S, E)
 
     def _update_items(self):
         return self.q_proj._update_items() + self.k_proj._update_items() + self.v_proj._update_items()
 
+    def _update_groups(self):
+        """The update over the side-by-side buffers: two groups (weights, biases) instead
+        of six, the same values element by element."""
+        bufs = getattr(self, "_qkv", None)
+        deltas = getattr(self, "_qkv_deltas", None)
+        if bufs is None or deltas is None or not self._qkv_intact(bufs):
+            return self._update_items()
+        dmw, dSw, dmb, dSb = deltas
+        groups = [(bufs["mw"], bufs["Sw"], dmw, dSw)]
+        if self.has_bias:
+            groups.append((bufs["mb"], bufs["Sb"], dmb, dSb))
+        return groups
+
     def update(self, cap_factor: float) -> None:
-        self.q_proj.update(cap_factor)
-        self.k_proj.update(cap_factor)
-        self.v_proj.update(cap_factor)
+        update_parameters_multi(self._update_groups(), cap_factor)
 
     @property
     def num_parameters(self) -> int:

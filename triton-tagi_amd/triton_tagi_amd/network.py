@@ -17,6 +17,7 @@ from torch import Tensor
 from . import _overlap
 from .base import Layer, LearnableLayer
 from .layers.conv2d import Conv2D
+from .layers.embedding import Embedding
 from .layers.fused import backward_chain, defer_bn_parameter_deltas, forward_chain
 from .layers.multihead_attention import MultiheadAttentionV2
 from .update.observation import compute_innovation, hrc_innovation
@@ -66,6 +67,8 @@ class Sequential:
             # the conv path keeps activations channels-last: start both moments that way
             x = x.contiguous(memory_format=torch.channels_last)
             Sa = torch.zeros_like(x, memory_format=torch.channels_last)
+        elif self.layers and isinstance(self.layers[0], Embedding):
+            Sa = None  # token ids: the embedding reads no input variance
         else:
             Sa = torch.zeros_like(x)
         return forward_chain(self.layers, x, Sa)
@@ -82,7 +85,7 @@ class Sequential:
             if layer._updated_in_backward:  # the backward pass applied it (update_in_backward)
                 layer._updated_in_backward = False
                 continue
-            got = layer._update_items()
+            got = layer._update_groups()
             if got is None:
                 if items:
                     update_parameters_multi(items, cap_factor)
