@@ -393,3 +393,37 @@ def test_linear_bwd_delta_with_addend(dev, M, K, N):
     assert_scaled_close(om, rm + d64(am), d64(dmz).abs() @ d64(mw).abs().T + d64(am).abs(), RTOL, ATOL,
                         "dma + addend")
     assert_scaled_close(oS, rS + d64(aS), None, RTOL, ATOL, "dSa + addend")
+
+
+@pytest.mark.parametrize("N,C,H,W,k,sc", [(4, 32, 32, 32, 2, False), (3, 5, 12, 12, 3, True), (2, 64, 8, 8, 4, False),
+                                          (128, 32, 16, 16, 2, False)])
+def test_relu_avgpool_fused(dev, N, C, H, W, k, sc):
+    """ReLU -> AvgPool2D as one pass each way (tagi_relu_avgpool2d_fwd, tagi_avgpool2d_relu_bwd)
+    against the two layers' own calls, bit for bit, and against the float64 oracle; C % 4 != 0
+    takes the scalar path."""
+    from triton_tagi_amd.layers.avgpool2d import AvgPool2D
+    from triton_tagi_amd.layers.fused import avgpool_relu_backward, relu_avgpool_forward
+    from triton_tagi_amd.layers.relu import ReLU
+
+    r = g(N + C + H + k)
+    mz = (2 * torch.randn(N, C, H, W, generator=r)).contiguous(memory_format=torch.channels_last).to(dev)
+    Sz = (0.05 + torch.rand(N, C, H, W, generator=r)).contiguous(memory_format=torch.channels_last).to(dev)
+    mz[0, 0, 0, :4] = torch.tensor([-30.0, -6.0, 0.0, 40.0], device=dev)  # both tails of the rectified moments
+    relu, pool = ReLU(), AvgPool2D(k, spatial_correlation=sc)
+    mo, So = relu_avgpool_forward(relu, pool, mz, Sz)
+    relu_u, pool_u = ReLU(), AvgPool2D(k, spatial_correlation=sc)
+    uo, uSo = pool_u.forward(*relu_u.forward(mz, Sz))
+    assert torch.equal(mo, uo) and torch.equal(So, uSo), "pooled moments differ from the separate passes"
+    assert torch.equal(relu.J, relu_u.J), "ReLU Jacobian differs from the separate pass"
+    orelu, opool = O.OReLU(), O.OAvgPool2D(k, sc)
+    rm, rS = opool.forward(*orelu.forward(d64(mz), d64(Sz)))
+    assert_scaled_close(mo, rm, rm.abs() + 1.0, RTOL, ATOL, "pooled mean vs oracle")
+    assert_scaled_close(So, rS, None, RTOL, ATOL, "pooled var vs oracle")
+    dm = torch.randn(mo.shape, generator=r).to(dev)
+    dS = -torch.rand(mo.shape, generator=r).to(dev)
+    om, oS = avgpool_relu_backward(pool, relu, dm, dS)
+    um, uS = relu_u.backward(*pool_u.backward(dm, dS))
+    assert torch.equal(om, um) and torch.equal(oS, uS), "input deltas differ from the separate passes"
+    qm, qS = orelu.backward(*opool.backward(d64(dm), d64(dS)))
+    assert_scaled_close(om, qm, None, RTOL, ATOL, "input delta mean vs oracle")
+    assert_scaled_close(oS, qS, None, RTOL, ATOL, "input delta var vs oracle")

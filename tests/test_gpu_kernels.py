@@ -327,6 +327,8 @@ CONV_CASES = [
     (2, 4, 9, 9, 8, 1, 2, 0, 1),      # 1x1 stride 2: odd pixels get no taps
     (2, 8, 10, 7, 12, 2, 3, 1, 1),    # kernel smaller than the stride, uneven sizes
     (128, 3, 32, 32, 64, 3, 1, 1, 1),  # ResNet-18 stem at full batch
+    (2, 1, 9, 9, 6, 3, 1, 1, 1),      # one and two input channels
+    (3, 2, 10, 10, 5, 5, 2, 2, 1),
 ]
 
 

@@ -214,6 +214,8 @@ struct vec_of<1> {
   static __device__ __forceinline__ T zero() { return 0.f; }
   static __device__ __forceinline__ void add(T& a, T b) { a += b; }
   static __device__ __forceinline__ T scale(T a, float s) { return a * s; }
+  static __device__ __forceinline__ T mul(T a, T b) { return a * b; }
+  static __device__ __forceinline__ void relu(T m, T s, T& a, T& b, T& j) { relu_moments(m, s, a, b, j); }
 };
 template <>
 struct vec_of<4> {
@@ -226,6 +228,13 @@ struct vec_of<4> {
     a.w += b.w;
   }
   static __device__ __forceinline__ T scale(T a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
+  static __device__ __forceinline__ T mul(T a, T b) { return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w); }
+  static __device__ __forceinline__ void relu(T m, T s, T& a, T& b, T& j) {
+    relu_moments(m.x, s.x, a.x, b.x, j.x);
+    relu_moments(m.y, s.y, a.y, b.y, j.y);
+    relu_moments(m.z, s.z, a.z, b.z, j.z);
+    relu_moments(m.w, s.w, a.w, b.w, j.w);
+  }
 };
 
 template <typename IT, int V>
@@ -279,6 +288,73 @@ __global__ void __launch_bounds__(256) avgpool_bwd_kernel(const float* __restric
     }
     reinterpret_cast<T*>(om)[i] = a;
     reinterpret_cast<T*>(oS)[i] = b;
+  }
+}
+
+// ReLU followed by AvgPool2D in one pass (relu.py:94-122, then avgpool2d.py:38-90): each
+// thread takes V channels of one pooled pixel, forms the rectified moments and J of its
+// k x k inputs (J stored for the backward pass) and sums them in avgpool_fwd_kernel's
+// order, so the outputs are the two launches' bit for bit; the ReLU output is never
+// written. H and W are multiples of k (every input lies in one window).
+template <typename IT, int V>
+__global__ void __launch_bounds__(256) relu_avgpool_fwd_kernel(const float* __restrict__ mz,
+                                                               const float* __restrict__ Sz, float* __restrict__ J,
+                                                               float* __restrict__ mo, float* __restrict__ So, IT N,
+                                                               IT H, IT W, IT C, IT k, float inv_k2,
+                                                               float var_scale) {
+  using VO = vec_of<V>;
+  using T = typename VO::T;
+  const T* m = reinterpret_cast<const T*>(mz);
+  const T* S = reinterpret_cast<const T*>(Sz);
+  T* Jv = reinterpret_cast<T*>(J);
+  const IT Ho = H / k, Wo = W / k, Cv = C / V;
+  const IT total = N * Ho * Wo * Cv;
+  const IT stride = (IT)gridDim.x * blockDim.x;
+  for (IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const IT c = i % Cv, pix = i / Cv;
+    const IT ow = pix % Wo, t = pix / Wo;
+    const IT oh = t % Ho, n = t / Ho;
+    const IT base = ((n * H + oh * k) * W + ow * k) * Cv + c;
+    T sm = VO::zero(), ss = VO::zero();
+    for (IT a = 0; a < k; ++a)
+      for (IT b = 0; b < k; ++b) {
+        const IT off = base + (a * W + b) * Cv;
+        T am, as, jj;
+        VO::relu(m[off], S[off], am, as, jj);
+        Jv[off] = jj;
+        VO::add(sm, am);
+        VO::add(ss, as);
+      }
+    reinterpret_cast<T*>(mo)[i] = VO::scale(sm, inv_k2);
+    reinterpret_cast<T*>(So)[i] = VO::scale(ss, var_scale);
+  }
+}
+
+// AvgPool2D backward followed by the ReLU Jacobian (avgpool2d.py:92-130, relu.py:152-169):
+// each input element gets its window's deltas scaled as avgpool_bwd_kernel scales them,
+// times J and J^2 as jacobian_kernel multiplies (the same bits as the two launches; the
+// unpooled deltas are never written). H and W are multiples of k.
+template <typename IT, int V>
+__global__ void __launch_bounds__(256) avgpool_relu_bwd_kernel(const float* __restrict__ dm,
+                                                               const float* __restrict__ dS,
+                                                               const float* __restrict__ J, float* __restrict__ om,
+                                                               float* __restrict__ oS, IT N, IT H, IT W, IT C, IT k,
+                                                               float inv_k2, float var_scale) {
+  using VO = vec_of<V>;
+  using T = typename VO::T;
+  const IT Ho = H / k, Wo = W / k, Cv = C / V;
+  const IT total = N * H * W * Cv;
+  const IT stride = (IT)gridDim.x * blockDim.x;
+  for (IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const IT c = i % Cv, pix = i / Cv;
+    const IT w = pix % W, t = pix / W;
+    const IT h = t % H, n = t / H;
+    const IT j = ((n * Ho + h / k) * Wo + w / k) * Cv + c;
+    const T a = VO::scale(reinterpret_cast<const T*>(dm)[j], inv_k2);
+    const T b = VO::scale(reinterpret_cast<const T*>(dS)[j], var_scale);
+    const T jj = reinterpret_cast<const T*>(J)[i];
+    reinterpret_cast<T*>(om)[i] = VO::mul(a, jj);
+    reinterpret_cast<T*>(oS)[i] = VO::mul(VO::mul(b, jj), jj);
   }
 }
 
@@ -490,6 +566,71 @@ extern "C" int tagi_avgpool2d_bwd(const float* dm, const float* dS, float* dm_ou
   ProfScope ps(FAM_AVGPOOL, s, 0.0, 8.0 * (total + N * C * (H / k) * (W / k)));
   launch_avgpool<false>(dm, dS, dm_out, dS_out, N, C, H, W, k, var_scale, total, s);
   return check_launch("tagi_avgpool2d_bwd");
+}
+
+template <bool FWD, typename IT, int V>
+static void launch_pool_relu_as(const float* a, const float* b, float* J, float* c, float* d, IT N, IT C, IT H, IT W,
+                                IT k, float var_scale, unsigned blocks, hipStream_t s) {
+  const float inv_k2 = 1.0f / (float)(k * k);
+  if constexpr (FWD)
+    hipLaunchKernelGGL((relu_avgpool_fwd_kernel<IT, V>), dim3(blocks), dim3(256), 0, s, a, b, J, c, d, N, H, W, C, k,
+                       inv_k2, var_scale);
+  else
+    hipLaunchKernelGGL((avgpool_relu_bwd_kernel<IT, V>), dim3(blocks), dim3(256), 0, s, a, b, J, c, d, N, H, W, C, k,
+                       inv_k2, var_scale);
+}
+
+// FWD: a, b the conv output moments, J written, c, d the pooled moments; backward: a, b the
+// pooled deltas, J read, c, d the deltas at the ReLU input. items: threads' work units.
+template <bool FWD>
+static void launch_pool_relu(const float* a, const float* b, const float* J, float* c, float* d, int64_t N, int64_t C,
+                             int64_t H, int64_t W, int64_t k, float var_scale, int64_t items, hipStream_t s) {
+  const bool v4 = C % 4 == 0 && aligned16(a) && aligned16(b) && aligned16(J) && aligned16(c) && aligned16(d);
+  const bool small = N * C * H * W < (1ll << 31);
+  const unsigned blocks = ew_blocks(v4 ? items / 4 : items, 256);
+  float* Jm = const_cast<float*>(J);
+  if (small && v4)
+    launch_pool_relu_as<FWD, uint32_t, 4>(a, b, Jm, c, d, (uint32_t)N, (uint32_t)C, (uint32_t)H, (uint32_t)W,
+                                          (uint32_t)k, var_scale, blocks, s);
+  else if (small)
+    launch_pool_relu_as<FWD, uint32_t, 1>(a, b, Jm, c, d, (uint32_t)N, (uint32_t)C, (uint32_t)H, (uint32_t)W,
+                                          (uint32_t)k, var_scale, blocks, s);
+  else if (v4)
+    launch_pool_relu_as<FWD, int64_t, 4>(a, b, Jm, c, d, N, C, H, W, k, var_scale, blocks, s);
+  else
+    launch_pool_relu_as<FWD, int64_t, 1>(a, b, Jm, c, d, N, C, H, W, k, var_scale, blocks, s);
+}
+
+extern "C" int tagi_relu_avgpool2d_fwd(const float* mz, const float* Sz, float* J, float* ma_out, float* Sa_out,
+                                       int64_t N, int64_t C, int64_t H, int64_t W, int64_t k, float var_scale,
+                                       tagi_stream_t stream) {
+  const char* what = "tagi_relu_avgpool2d_fwd";
+  TAGI_REQUIRE(mz && Sz && J && ma_out && Sa_out, "%s: null pointer", what);
+  TAGI_REQUIRE(N > 0 && C > 0 && H > 0 && W > 0 && k > 0 && H >= k && W >= k, "%s: bad sizes", what);
+  if (H % k || W % k)
+    return fail(TAGI_ERR_UNSUPPORTED, "%s: H and W must be multiples of the window (use tagi_relu_fwd and "
+                "tagi_avgpool2d_fwd)", what);
+  hipStream_t s = as_stream(stream);
+  const int64_t out = N * C * (H / k) * (W / k);
+  ProfScope ps(FAM_AVGPOOL, s, 0.0, 12.0 * N * C * H * W + 8.0 * out);
+  launch_pool_relu<true>(mz, Sz, J, ma_out, Sa_out, N, C, H, W, k, var_scale, out, s);
+  return check_launch(what);
+}
+
+extern "C" int tagi_avgpool2d_relu_bwd(const float* dm, const float* dS, const float* J, float* dm_out,
+                                       float* dS_out, int64_t N, int64_t C, int64_t H, int64_t W, int64_t k,
+                                       float var_scale, tagi_stream_t stream) {
+  const char* what = "tagi_avgpool2d_relu_bwd";
+  TAGI_REQUIRE(dm && dS && J && dm_out && dS_out, "%s: null pointer", what);
+  TAGI_REQUIRE(N > 0 && C > 0 && H > 0 && W > 0 && k > 0 && H >= k && W >= k, "%s: bad sizes", what);
+  if (H % k || W % k)
+    return fail(TAGI_ERR_UNSUPPORTED, "%s: H and W must be multiples of the window (use tagi_avgpool2d_bwd and "
+                "tagi_jacobian_bwd)", what);
+  hipStream_t s = as_stream(stream);
+  const int64_t total = N * C * H * W;
+  ProfScope ps(FAM_AVGPOOL, s, 0.0, 12.0 * total + 8.0 * N * C * (H / k) * (W / k));
+  launch_pool_relu<false>(dm, dS, J, dm_out, dS_out, N, C, H, W, k, var_scale, total, s);
+  return check_launch(what);
 }
 
 extern "C" int tagi_remax_fwd(const float* mz, const float* Sz, float* ma, float* Sa, float* J, int64_t rows,

@@ -16,6 +16,9 @@ in how often activations cross HBM:
   follows the pair, that pass is the epilogue of the Conv2D's input-delta GEMM.
 * The merge of the shortcut deltas into the main branch (resblock.py:421-423) is folded
   into the input-delta GEMM of the block's first convolution.
+* ReLU followed by AvgPool2D (relu.py:94-122, avgpool2d.py:38-90) is one pass that writes
+  the ReLU Jacobian and the pooled moments, not the ReLU output; backward, the pooling's
+  deltas and the Jacobian are one pass as well (when H and W are multiples of the window).
 
 Every layer still ends up holding the state its own ``backward`` reads (ReLU.J,
 BatchNorm2D.m_hat and its normalisation variance, Conv2D.ma_in), so per-layer calls keep
@@ -30,6 +33,7 @@ from torch import Tensor
 from .. import _lib
 from ._bn_pending import active as _active_defer
 from ._bn_pending import defer_bn_parameter_deltas  # noqa: F401  (re-exported)
+from .avgpool2d import AvgPool2D
 from .batchnorm2d import BatchNorm2D
 from .conv2d import Conv2D
 from .relu import ReLU
@@ -209,6 +213,50 @@ def conv_bn_relu_backward(conv: Conv2D, bn: BatchNorm2D, relu: ReLU, conv_prev: 
     return d_ma, d_Sa
 
 
+def relu_avgpool_forward(relu: ReLU, pool: AvgPool2D, mz: Tensor, Sz: Tensor) -> tuple[Tensor, Tensor]:
+    """pool.forward(*relu.forward(mz, Sz)) in one pass; stores relu.J and the pool's input
+    shape, as the two calls do."""
+    mz = _lib.check(_lib.channels_last(mz), "mz")
+    Sz = _lib.check(_lib.like(Sz, mz), "Sz")
+    N, C, H, W = mz.shape
+    k = pool.k
+    J = torch.empty_like(mz)
+    mo = _lib.empty_cl(N, C, H // k, W // k, mz.device)
+    So = _lib.empty_cl(N, C, H // k, W // k, mz.device)
+    _lib.call("tagi_relu_avgpool2d_fwd", mz.data_ptr(), Sz.data_ptr(), J.data_ptr(), mo.data_ptr(), So.data_ptr(),
+              N, C, H, W, k, pool._var_scale(), _lib.stream_of(mz))
+    relu.J = J
+    pool.input_shape = mz.shape
+    return mo, So
+
+
+def avgpool_relu_backward(pool: AvgPool2D, relu: ReLU, delta_m: Tensor, delta_S: Tensor) -> tuple[Tensor, Tensor]:
+    """relu.backward(*pool.backward(delta_m, delta_S)) in one pass."""
+    N, C, H, W = pool.input_shape
+    k = pool.k
+    dm = _lib.check(_lib.channels_last(delta_m.reshape(N, C, H // k, W // k)), "delta_m")
+    dS = _lib.check(_lib.channels_last(delta_S.reshape(N, C, H // k, W // k)), "delta_S")
+    J = _lib.check(_lib.channels_last(relu.J), "J")
+    om = _lib.empty_cl(N, C, H, W, dm.device)
+    oS = _lib.empty_cl(N, C, H, W, dm.device)
+    _lib.call("tagi_avgpool2d_relu_bwd", dm.data_ptr(), dS.data_ptr(), J.data_ptr(), om.data_ptr(), oS.data_ptr(),
+              N, C, H, W, k, pool._var_scale(), _lib.stream_of(dm))
+    return om, oS
+
+
+def _fusable_relu_pool(layer, nxt, mu: Tensor) -> bool:
+    return (isinstance(layer, ReLU) and isinstance(nxt, AvgPool2D) and mu.dim() == 4
+            and mu.shape[2] % nxt.k == 0 and mu.shape[3] % nxt.k == 0)
+
+
+def _fusable_pool_relu_backward(layer, prev) -> bool:
+    if not (isinstance(layer, AvgPool2D) and isinstance(prev, ReLU) and prev.J is not None
+            and layer.input_shape is not None):
+        return False
+    N, C, H, W = layer.input_shape
+    return tuple(prev.J.shape) == (N, C, H, W) and H % layer.k == 0 and W % layer.k == 0
+
+
 def _fusable_forward(layer, nxt, mu: Tensor) -> bool:
     return isinstance(layer, ReLU) and isinstance(nxt, BatchNorm2D) and nxt.training and mu.dim() == 4
 
@@ -242,6 +290,9 @@ def forward_chain(layers, mu: Tensor, var: Tensor,
             if last:
                 add = None
             i += 2
+        elif _fusable_relu_pool(layer, nxt, mu):
+            mu, var = relu_avgpool_forward(layer, nxt, mu, var)
+            i += 2
         else:
             mu, var = layer.forward(mu, var)
             i += 1
@@ -271,6 +322,10 @@ def backward_chain(layers, delta_mu: Tensor, delta_var: Tensor, add: tuple[Tenso
         if _fusable_backward(layer, prev):
             conv = layers[i - 2] if i >= 2 and isinstance(layers[i - 2], Conv2D) else None
             delta_mu, delta_var = bn_relu_backward(layer, prev, delta_mu, delta_var, conv)
+            i -= 2
+            continue
+        if _fusable_pool_relu_backward(layer, prev):
+            delta_mu, delta_var = avgpool_relu_backward(layer, prev, delta_mu, delta_var)
             i -= 2
             continue
         if i == 0:
