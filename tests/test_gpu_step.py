@@ -264,3 +264,58 @@ def test_step_update_in_backward_equals_update_after(dev, name, overlap, monkeyp
     assert len(outs[0]) == len(outs[1])
     for j, (x, y) in enumerate(zip(*outs)):
         assert torch.equal(x, y), f"{name}: tensor {j} differs"
+
+
+def test_attention_projection_views_step_like_linear(dev):
+    """After its first forward a MultiheadAttentionV2's projections hold column views of
+    the side-by-side (E, 3E) parameters. Each projection must still work as a Linear on its
+    own: updating the three one by one gives the layer's joint update, bit for bit, and a
+    lone projection's forward, backward (within update_in_backward too) and update give
+    what a Linear holding dense copies of its parameters gives."""
+    from triton_tagi_amd.layers import Linear, MultiheadAttentionV2
+    from triton_tagi_amd.update.in_backward import update_in_backward
+
+    B, S, E, H = 2, 16, 64, 4
+    cap = 2.0
+    params = []
+    for joint in (True, False):
+        torch.manual_seed(7)
+        att = MultiheadAttentionV2(E, H, S, bias=True, gain_weight=0.25, gain_bias=0.5, device=dev)
+        r = torch.Generator().manual_seed(8)
+        ma, Sa = torch.randn(B, S, E, generator=r).to(dev), 0.1 * torch.rand(B, S, E, generator=r).to(dev)
+        dm, dS = 0.1 * torch.randn(B, S, E, generator=r).to(dev), -1e-2 * torch.rand(B, S, E, generator=r).to(dev)
+        att.forward(ma, Sa)
+        att.backward(dm, dS)
+        assert not att.q_proj.mw.is_contiguous()
+        if joint:
+            att.update(cap)
+        else:
+            for p in (att.q_proj, att.k_proj, att.v_proj):
+                p.update(cap)
+        torch.cuda.synchronize()
+        params.append([getattr(p, a).clone() for p in (att.q_proj, att.k_proj, att.v_proj)
+                       for a in ("mw", "Sw", "mb", "Sb")])
+    for j, (x, y) in enumerate(zip(*params)):
+        assert torch.equal(x, y), f"parameter {j}: projection-by-projection update differs from the joint one"
+
+    # the v projection on its own, against a Linear with dense copies of its parameters
+    proj = att.v_proj
+    lin = Linear(E, E, device=dev)
+    lin.mw, lin.Sw, lin.mb, lin.Sb = (getattr(proj, a).clone() for a in ("mw", "Sw", "mb", "Sb"))
+    r = torch.Generator().manual_seed(9)
+    x, Sx = torch.randn(B * S, E, generator=r).to(dev), 0.1 * torch.rand(B * S, E, generator=r).to(dev)
+    dz, dSz = 0.1 * torch.randn(B * S, E, generator=r).to(dev), -1e-2 * torch.rand(B * S, E, generator=r).to(dev)
+    res = []
+    for layer in (proj, lin):
+        mz, Sz = layer.forward(x, Sx)
+        with update_in_backward(cap):
+            dma, dSa = layer.backward(dz, dSz)
+        layer.update(cap)  # applies it for the view, skips it for the dense layer
+        mz2, Sz2 = layer.forward(x, Sx)
+        dma2, dSa2 = layer.backward(dz, dSz)
+        layer.update(cap)
+        torch.cuda.synchronize()
+        res.append([mz, Sz, dma, dSa, mz2, Sz2, dma2, dSa2, layer.mw, layer.Sw, layer.mb, layer.Sb])
+    assert proj.mw.data_ptr() == att._qkv["mw"].data_ptr() + 2 * E * 4  # still a view of the buffer
+    for j, (x1, y1) in enumerate(zip(*res)):
+        assert torch.equal(x1, y1), f"tensor {j}: the projection view differs from a dense Linear"

@@ -8,6 +8,10 @@ Backward (deltas stored, applied by ``update``, or by the backward pass itself w
     delta_mw = S_w * (mu_a^T @ delta_mz)        delta_mb = S_b * sum delta_mz
     delta_Sw = S_w^2 * ((mu_a^2)^T @ delta_Sz)  delta_Sb = S_b^2 * sum delta_Sz
     delta_ma = delta_mz @ mu_w^T,  delta_Sa = delta_Sz @ (mu_w^2)^T
+
+The parameters may be column views of a wider buffer (the projections of a
+MultiheadAttentionV2 are); the kernels read and update a dense copy of such a view and
+the update writes the result back into it, so a lone projection steps like any Linear.
 """
 
 from __future__ import annotations
@@ -23,6 +27,10 @@ from ..kernels.common import fused_backward_delta, linear_forward, linear_param_
 from ..param_init import init_weight_bias_linear
 from ..update import in_backward
 from ..update.parameters import update_parameters
+
+
+def _dense(t):
+    return t if t is None or t.is_contiguous() else t.contiguous()
 
 
 class Linear(LearnableLayer):
@@ -46,7 +54,8 @@ class Linear(LearnableLayer):
         ma_flat = ma.reshape(-1, self.in_features).contiguous()
         Sa_flat = Sa.reshape(-1, self.in_features).contiguous()
         self.ma_in = ma_flat
-        mz, Sz = linear_forward(ma_flat, Sa_flat, self.mw, self.Sw, self.mb, self.Sb)
+        mz, Sz = linear_forward(ma_flat, Sa_flat, _dense(self.mw), _dense(self.Sw), _dense(self.mb),
+                                _dense(self.Sb))
         out_shape = (*self._input_shape[:-1], self.out_features)
         return mz.reshape(out_shape), Sz.reshape(out_shape)
 
@@ -70,18 +79,18 @@ class Linear(LearnableLayer):
         # a parameter-delta product bound for the side stream would have to wait for the
         # input deltas before updating in place, losing its overlap (transformer block
         # -1.7%): such layers keep the update for after the backward pass
-        upd = in_backward.active() if ctx is None or not big else None
+        upd = in_backward.active() if (ctx is None or not big) and self._dense_params() else None
         out = None
         if upd is not None and input_deltas:
             out = self._input_deltas(dmz, dSz, add)
         side = ctx.fork(dmz.device, self.ma_in, dmz, dSz) if ctx is not None and big else None
-        bias = (self.mb, self.Sb) if self.has_bias else (None, None)
+        bias = (_dense(self.mb), _dense(self.Sb)) if self.has_bias else (None, None)
         with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
             if upd is not None:
                 dmw, dSw, dmb, dSb = linear_param_deltas_update(self.ma_in, dmz, dSz, self.mw, self.Sw, *bias,
                                                                 upd.cap_factor)
             else:
-                dmw, dSw, dmb, dSb = linear_param_deltas(self.ma_in, dmz, dSz, self.Sw, bias[1])
+                dmw, dSw, dmb, dSb = linear_param_deltas(self.ma_in, dmz, dSz, _dense(self.Sw), bias[1])
         self._updated_in_backward = upd is not None
         self.delta_mw, self.delta_Sw = dmw, dSw
         if self.has_bias:
@@ -92,10 +101,10 @@ class Linear(LearnableLayer):
 
     def _input_deltas(self, dmz: Tensor, dSz: Tensor, add):
         if add is not None:
-            fused_backward_delta(dmz, dSz, self.mw, add=(add[0].view(-1, self.in_features),
+            fused_backward_delta(dmz, dSz, _dense(self.mw), add=(add[0].view(-1, self.in_features),
                                                          add[1].view(-1, self.in_features)))
             return add
-        dma, dSa = fused_backward_delta(dmz, dSz, self.mw)
+        dma, dSa = fused_backward_delta(dmz, dSz, _dense(self.mw))
         in_shape = (*self._input_shape[:-1], self.in_features)
         return dma.reshape(in_shape), dSa.reshape(in_shape)
 
@@ -110,7 +119,16 @@ class Linear(LearnableLayer):
             self._updated_in_backward = False
             return
         for m, S, dm, dS in self._update_items():
-            update_parameters(m, S, dm, dS, cap_factor)
+            if m.is_contiguous() and S.is_contiguous():
+                update_parameters(m, S, _dense(dm), _dense(dS), cap_factor)
+            else:
+                mc, Sc = m.contiguous(), S.contiguous()
+                update_parameters(mc, Sc, _dense(dm), _dense(dS), cap_factor)
+                m.copy_(mc)
+                S.copy_(Sc)
+
+    def _dense_params(self) -> bool:
+        return all(t is None or t.is_contiguous() for t in (self.mw, self.Sw, self.mb, self.Sb))
 
     @property
     def num_parameters(self) -> int:
