@@ -330,6 +330,21 @@ int tagi_conv2d_bwd_delta_bn_relu(const float* dmz, const float* dSz, const floa
                                   float* dSa, float* part, int64_t part_bytes, const tagi_conv_geom* g, float* ws,
                                   int64_t ws_bytes, tagi_stream_t stream);
 int64_t tagi_conv2d_bwd_delta_bn_relu_part_bytes(const tagi_conv_geom* g);
+/* tagi_conv2d_bwd_delta_add followed by the same fold, across a residual block boundary:
+ * dma/dSa = product + addend as tagi_conv2d_bwd_delta_add stores them (the deltas at the
+ * output of the block in front, which its shortcut reads again), and dmz_prev/dSz_prev the
+ * deltas at the input of that block's closing ReLU (or the stem's), the values
+ * tagi_bn_relu_bwd_partials_bias writes for dma/dSa; part, mhat, J, var, mg as for
+ * tagi_conv2d_bwd_delta_bn_relu, with the same size query and the same
+ * TAGI_ERR_UNSUPPORTED where it does not apply. dma may alias add_m (dSa add_S).
+ * Replaces conv2d.py:357-370, triton_delta_merge (resblock.py:421-423) and the next
+ * block's BatchNorm2D -> ReLU backward (batchnorm2d.py:465-513, relu.py:152-169). */
+int tagi_conv2d_bwd_delta_add_bn_relu(const float* dmz, const float* dSz, const float* mw, const float* add_m,
+                                      const float* add_S, float* dma, float* dSa, const float* mhat,
+                                      const float* J, const float* var, const float* mg, float eps,
+                                      float* dmz_prev, float* dSz_prev, float* part, int64_t part_bytes,
+                                      const tagi_conv_geom* g, float* ws, int64_t ws_bytes,
+                                      tagi_stream_t stream);
 
 /* Parameter deltas of a Conv2D layer (reduction over N*Ho*Wo patches, split-K):
  *   dmw = Sw * P^T @ dmz, dSw = Sw^2 * (P^2)^T @ dSz, dmb = Sb * sum dmz, dSb = Sb^2 * sum dSz.

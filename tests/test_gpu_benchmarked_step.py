@@ -216,6 +216,17 @@ def _install(monkeypatch, rec):
 
     monkeypatch.setattr(fused, "conv_bn_relu_backward", fold)
 
+    orig_xfold = fused.conv_add_bn_relu_backward
+
+    def xfold(conv, dma, dSa, add, bn, relu, conv_prev):
+        out = orig_xfold(conv, dma, dSa, add, bn, relu, conv_prev)
+        if out is not None:  # None: declined, the block's own passes (recorded above) run
+            rec.append(dict(kind="xfold", conv=conv, bn=bn, dmz=cl(dma), dSz=cl(dSa), add=(cl(add[0]), cl(add[1])),
+                            out=(cl(out[0][0]), cl(out[0][1])), fout=(cl(out[1][0]), cl(out[1][1]))))
+        return out
+
+    monkeypatch.setattr(fused, "conv_add_bn_relu_backward", xfold)
+
     orig_cb = Conv2D._backward
 
     def cb(self, dmz, dSz, input_deltas, add=None):
@@ -307,7 +318,7 @@ def test_resnet18_b128_step_teacher_forced(dev, monkeypatch):
     conv_in = {}  # id(conv) -> recorded input mean (float64, NCHW)
     learn = []  # (tag, engine layer) in order, for the update check
     nconv = nbn = 0
-    n_indelta = n_param = n_bnbwd = n_fold = 0  # backward passes by kind
+    n_indelta = n_param = n_bnbwd = n_fold = n_xfold = 0  # backward passes by kind
     for r in rec:
         if r["kind"] == "crb":
             conv, bn = r["conv"], r["bn"]
@@ -435,6 +446,41 @@ def test_resnet18_b128_step_teacher_forced(dev, monkeypatch):
             n_param += 1
             n_indelta += 1
             n_bnbwd += 1
+        elif r["kind"] == "xfold":
+            # a block's first convolution: its input deltas plus the shortcut's (stored: the
+            # block in front reads them through its own shortcut), then, in the same
+            # epilogue, the BatchNorm2D -> ReLU backward of the pair in front of the block
+            # (the previous block's closing pair, or the stem's), over the whole batch
+            conv, bn = r["conv"], r["bn"]
+            oc = omap[id(conv)]
+            tag = [t for t, lay in learn if lay is conv][0]
+            btag = [t for t, lay in learn if lay is bn][0]
+            st = bn_state[id(bn)]
+            x = conv_in[id(conv)]
+            dm, dS = d64(r["dmz"]), d64(r["dSz"])
+            am, aS = d64(r["add"][0]), d64(r["add"][1])
+            q = _transposed_product(conv, dm, oc.mw) + am
+            qS = _transposed_product(conv, dS, oc.mw * oc.mw) + aS
+            sq = _transposed_product(conv, dm.abs(), oc.mw.abs()) + am.abs()
+            rep.check(f"{tag} bwd delta_mu +shortcut (stored by the fold)", r["out"][0], q, sq)
+            rep.check(f"{tag} bwd delta_S +shortcut (stored by the fold)", r["out"][1], qS)
+            v = lambda t: t.view(1, -1, 1, 1)  # noqa: E731
+            g = v(st["gamma"])
+            fm, fS = g / st["sig"] * st["J"], (g / st["sig"]) ** 2 * st["J"] ** 2
+            rep.check(f"{tag}+{btag} folded bwd delta_mu", r["fout"][0], q * fm, sq * fm.abs())
+            rep.check(f"{tag}+{btag} folded bwd delta_S", r["fout"][1], qS * fS)
+            ob, mh, dims = st["ob"], st["mhat"], (0, 2, 3)
+            rep.check(f"{btag} (folded) delta_gamma", bn.delta_mw, ob.Sw * (q * mh).sum(dims),
+                      ob.Sw * (sq * st["mag"]).sum(dims))
+            rep.check(f"{btag} (folded) delta_S_gamma", bn.delta_Sw, ob.Sw ** 2 * (qS * mh * mh).sum(dims),
+                      ob.Sw ** 2 * (qS.abs() * st["mag"] ** 2).sum(dims))
+            rep.check(f"{btag} (folded) delta_beta", bn.delta_mb, ob.Sb * q.sum(dims), ob.Sb * sq.sum(dims))
+            rep.check(f"{btag} (folded) delta_S_beta", bn.delta_Sb, ob.Sb ** 2 * qS.sum(dims))
+            _check_conv_param_deltas(rep, f"{tag} (folded)", conv, oc, x, dm, dS)
+            n_xfold += 1
+            n_param += 1
+            n_indelta += 1
+            n_bnbwd += 1
         elif r["kind"] in ("forward", "backward"):
             layer = r["layer"]
             name = type(layer).__name__
@@ -494,11 +540,13 @@ def test_resnet18_b128_step_teacher_forced(dev, monkeypatch):
     # layers forward; backward, every conv's parameter deltas, the input deltas of all but
     # the stem (the first layer forms none), every BatchNorm2D backward (two-step or folded)
     print(f"\npasses: {nconv} conv forward, {nbn} BatchNorm2D forward, {n_param} conv parameter-delta, "
-          f"{n_indelta} conv input-delta ({n_fold} with the BatchNorm2D -> ReLU backward folded in), "
+          f"{n_indelta} conv input-delta ({n_fold} with the BatchNorm2D -> ReLU backward folded in, {n_xfold} "
+          f"with the shortcut added and the previous block's or the stem's folded in), "
           f"{n_bnbwd} BatchNorm2D backward")
     assert nconv == 20 and nbn == 20
     assert n_param == 20 and n_indelta == 19 and n_bnbwd == 20
     assert n_fold > 0, "the folded BatchNorm2D backward never ran: the test would not cover it"
+    assert n_xfold > 0, "the fold across a block boundary never ran: the test would not cover it"
 
     # capped update of every parameter tensor from its pre-step value and the GPU's deltas
     for tag, layer in learn:

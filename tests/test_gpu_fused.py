@@ -284,6 +284,67 @@ def test_conv_bwd_delta_bn_relu_fold(dev, case):
         close_unfused_rel(a, b, 1e-5, name)
 
 
+@pytest.mark.parametrize("case", FOLD_CASES, ids=[str(c) for c in FOLD_CASES])
+def test_conv_bwd_delta_add_bn_relu_fold(dev, case):
+    """tagi_conv2d_bwd_delta_add_bn_relu (the input deltas plus the shortcut's, then the
+    BatchNorm2D -> ReLU backward of the layers in front, in one GEMM epilogue) against
+    tagi_conv2d_bwd_delta_add followed by tagi_bn_relu_bwd_partials_bias: the stored sum and
+    the propagated deltas bit for bit, the parameter and bias deltas after
+    tagi_bn_bwd_finalize_multi to 1e-5 (per-channel sums grouped by GEMM tile)."""
+    from triton_tagi_amd import _lib
+    from triton_tagi_amd.layers.conv2d import Conv2D
+
+    N, C, H, W, Cout, k = case
+    torch.manual_seed(sum(case) + 1)
+    conv = Conv2D(C, Cout, k, stride=1, padding=k // 2, device="cpu")
+    for a in ("mw", "Sw", "mb", "Sb"):
+        setattr(conv, a, getattr(conv, a).to(dev))
+    r = g(sum(case) + 13)
+    cl = lambda t: t.to(dev).contiguous(memory_format=torch.channels_last)
+    dmz, dSz = cl(torch.randn(N, Cout, H, W, generator=r)), cl(-torch.rand(N, Cout, H, W, generator=r))
+    am, aS = cl(torch.randn(N, C, H, W, generator=r)), cl(-torch.rand(N, C, H, W, generator=r))
+    mhat, J = cl(torch.randn(N, C, H, W, generator=r)), cl(torch.rand(N, C, H, W, generator=r))
+    var = (torch.rand(C, generator=r) + 0.5).to(dev)
+    mg = (1 + 0.1 * torch.randn(C, generator=r)).to(dev)
+    Sg, Sb, cSb = ((torch.rand(C, generator=r) * 0.1 + 0.01).to(dev) for _ in range(3))
+    eps = 1e-5
+    conv.input_shape = (N, C, H, W)
+    geo = conv._geom(N, C, H, W)
+    st = _lib.stream_of(dmz)
+    ws = _lib.workspace(_lib.query("tagi_conv2d_bwd_delta_ws_bytes", geo), dev)
+    wp, wb = _lib.ws_args(ws)
+    part_bytes = _lib.query("tagi_conv2d_bwd_delta_bn_relu_part_bytes", geo)
+    assert part_bytes > 0
+    part = _lib.workspace(part_bytes, dev)
+    sm, sS = _lib.empty_cl(N, C, H, W, dev), _lib.empty_cl(N, C, H, W, dev)
+    fm, fS = _lib.empty_cl(N, C, H, W, dev), _lib.empty_cl(N, C, H, W, dev)
+    _lib.call("tagi_conv2d_bwd_delta_add_bn_relu", dmz.data_ptr(), dSz.data_ptr(), conv.mw.data_ptr(),
+              am.data_ptr(), aS.data_ptr(), sm.data_ptr(), sS.data_ptr(), mhat.data_ptr(), J.data_ptr(),
+              var.data_ptr(), mg.data_ptr(), eps, fm.data_ptr(), fS.data_ptr(), part.data_ptr(), part_bytes, geo, wp,
+              wb, st)
+    # the two calls
+    dma, dSa = _lib.empty_cl(N, C, H, W, dev), _lib.empty_cl(N, C, H, W, dev)
+    _lib.call("tagi_conv2d_bwd_delta_add", dmz.data_ptr(), dSz.data_ptr(), conv.mw.data_ptr(), am.data_ptr(),
+              aS.data_ptr(), dma.data_ptr(), dSa.data_ptr(), geo, wp, wb, st)
+    um, uS = _lib.empty_cl(N, C, H, W, dev), _lib.empty_cl(N, C, H, W, dev)
+    ws2 = _lib.workspace(_lib.query("tagi_bn_relu_bwd_bias_ws_bytes", N, C, H * W), dev)
+    w2p, w2b = _lib.ws_args(ws2)
+    _lib.call("tagi_bn_relu_bwd_partials_bias", dma.data_ptr(), dSa.data_ptr(), mhat.data_ptr(), J.data_ptr(),
+              var.data_ptr(), mg.data_ptr(), um.data_ptr(), uS.data_ptr(), N, C, H * W, eps, w2p, w2b, st)
+    assert torch.equal(sm, dma) and torch.equal(sS, dSa), "stored product + addend differs from the add call"
+    assert torch.equal(fm, um) and torch.equal(fS, uS), "folded deltas differ from the two calls"
+    outs = []
+    for wsx, nblk in ((part, part_bytes // (24 * C)), (ws2, 0)):
+        o = [torch.empty(C, device=dev) for _ in range(6)]
+        item = _lib.BnPending(wsx.data_ptr(), Sg.data_ptr(), Sb.data_ptr(), *(t.data_ptr() for t in o[:4]), N, C,
+                              H * W, cSb.data_ptr(), o[4].data_ptr(), o[5].data_ptr(), nblk)
+        _lib.call("tagi_bn_bwd_finalize_multi", ctypes.byref(item), 1, st)
+        outs.append(o)
+    names = ("delta gamma", "delta Sgamma", "delta beta", "delta Sbeta", "conv bias delta", "conv bias Sdelta")
+    for name, a, b in zip(names, *outs):
+        close_unfused_rel(a, b, 1e-5, name)
+
+
 def test_conv_bwd_delta_bn_relu_fold_refuses_stride2(dev):
     from triton_tagi_amd import _lib
     from triton_tagi_amd.layers.conv2d import Conv2D
@@ -315,10 +376,25 @@ def test_bn_fold_taken_in_step(dev, monkeypatch):
         return out
 
     monkeypatch.setattr(fused, "conv_bn_relu_backward", counting)
+    across = []
+    orig_x = fused.conv_add_bn_relu_backward
+
+    def counting_x(*a, **k):
+        out = orig_x(*a, **k)
+        across.append(out is not None)
+        return out
+
+    monkeypatch.setattr(fused, "conv_add_bn_relu_backward", counting_x)
     w = workloads.build("resnet18", device="cuda:0", batch=16)
     w.net.step(w.x, w.y, w.sigma_v)
     torch.cuda.synchronize()
     assert len(taken) == 8 and sum(taken) >= 2, taken
+    # across block boundaries: tried by all 8 blocks' first convolutions, last block first
+    # (each previous block's closing pair in front of blocks 8..2, the stem's in front of
+    # block 1), taken at least by the two stride-1 stage-1 blocks; never by the stride-2
+    # first blocks of stages 2-4 (blocks 7, 5, 3: entries 1, 3, 5)
+    assert len(across) == 8 and across[-1] and across[-2], across
+    assert not any(across[j] for j in (1, 3, 5)), across
 
 
 def test_fused_step_matches_oracle(dev):

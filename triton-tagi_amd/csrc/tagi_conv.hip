@@ -237,6 +237,9 @@ struct BnBwdFuse {
   const float* mg;
   float eps;
   float* part;
+  // with an addend: where the fold's outputs go (the product + addend goes to dma/dSa)
+  float* out_m;
+  float* out_S;
 };
 
 // Tiles along the rows of the fused launch (the partial sums per channel), or 0 when the
@@ -305,6 +308,8 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
     a.epi.bn_g = bnf->mg;
     a.epi.bn_eps = bnf->eps;
     a.epi.st_ws = bnf->part;
+    a.epi.bn_om = bnf->out_m;
+    a.epi.bn_ov = bnf->out_S;
   }
   a.R = (int)R0;
   a.C = (int)g->C;
@@ -332,6 +337,9 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
   if (bnf) {
     TAGI_REQUIRE(nph == 1 && p.splits == 1 && bnf_cfg(p.cfg),
                  "%s: the folded BatchNorm2D backward needs stride 1 and an unsplit one-tile-per-wave plan", what);
+    // the folded epilogues address the (N, H, W, C) tensors with 32-bit offsets
+    TAGI_REQUIRE(R0 * g->C < (int64_t)1 << 31, "%s: %lld x %lld deltas exceed the fold's 2^31 elements", what,
+                 (long long)R0, (long long)g->C);
     a.epi.st_nblk = p.tiles_m;
   }
   const int64_t gx = (int64_t)p.tiles_m * p.tiles_n;  // phase 0 is the largest
@@ -340,6 +348,12 @@ static int conv_bwd_delta_impl(const char* what, const float* dmz, const float* 
   if (bnf) {
     TAGI_REQUIRE(va && in_place, "%s: the folded BatchNorm2D backward needs Cout %% 4 == 0 and 16-byte aligned "
                  "deltas and weights", what);
+    if (add_m) {
+      TAGI_REQUIRE(bnf->out_m && bnf->out_S, "%s: null pointer", what);
+      if (g->Cout % 16 == 0 && g->k <= 5)
+        return run_gemm<PROD_SHARED_B, LD_CBWD_A4T, LD_CBWD_BK4T, 3>(a, nph, p, part, part_bytes, s, what, gx);
+      return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4, 3>(a, nph, p, part, part_bytes, s, what, gx);
+    }
     if (g->Cout % 16 == 0 && g->k <= 5)
       return run_gemm<PROD_SHARED_B, LD_CBWD_A4T, LD_CBWD_BK4T, 1>(a, nph, p, part, part_bytes, s, what, gx);
     return run_gemm<PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4, 1>(a, nph, p, part, part_bytes, s, what, gx);
@@ -382,8 +396,26 @@ extern "C" int tagi_conv2d_bwd_delta_bn_relu(const float* dmz, const float* dSz,
                 "tagi_conv2d_bwd_delta and tagi_bn_relu_bwd_partials_bias)", what);
   TAGI_REQUIRE(part_bytes >= need, "%s: partial sums need %lld bytes (got %lld)", what, (long long)need,
                (long long)part_bytes);
-  const BnBwdFuse f{mhat, J, var, mg, eps, part};
+  const BnBwdFuse f{mhat, J, var, mg, eps, part, nullptr, nullptr};
   return conv_bwd_delta_impl(what, dmz, dSz, mw, nullptr, nullptr, dma, dSa, g, ws, ws_bytes, stream, &f);
+}
+
+extern "C" int tagi_conv2d_bwd_delta_add_bn_relu(const float* dmz, const float* dSz, const float* mw,
+                                                 const float* add_m, const float* add_S, float* dma, float* dSa,
+                                                 const float* mhat, const float* J, const float* var,
+                                                 const float* mg, float eps, float* dmz_prev, float* dSz_prev,
+                                                 float* part, int64_t part_bytes, const tagi_conv_geom* g,
+                                                 float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+  const char* what = "tagi_conv2d_bwd_delta_add_bn_relu";
+  TAGI_REQUIRE(add_m && add_S && mhat && J && var && mg && part && dmz_prev && dSz_prev, "%s: null pointer", what);
+  const int64_t need = tagi_conv2d_bwd_delta_bn_relu_part_bytes(g);
+  if (need == 0)
+    return fail(TAGI_ERR_UNSUPPORTED, "%s: needs stride 1 and an unsplit input-delta plan (use "
+                "tagi_conv2d_bwd_delta_add and tagi_bn_relu_bwd_partials_bias)", what);
+  TAGI_REQUIRE(part_bytes >= need, "%s: partial sums need %lld bytes (got %lld)", what, (long long)need,
+               (long long)part_bytes);
+  const BnBwdFuse f{mhat, J, var, mg, eps, part, dmz_prev, dSz_prev};
+  return conv_bwd_delta_impl(what, dmz, dSz, mw, add_m, add_S, dma, dSa, g, ws, ws_bytes, stream, &f);
 }
 
 // ============================================================== parameter deltas

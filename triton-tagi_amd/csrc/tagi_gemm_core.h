@@ -213,6 +213,11 @@ struct Epi {
   const float* bn_var;
   const float* bn_g;
   float bn_eps;
+  // EPI 3: the same fold applied to product + addend, which is still stored to om/ov (the
+  // deltas at the BatchNorm2D output, read again by the block's shortcut); the fold's
+  // outputs go to bn_om/bn_ov
+  float* bn_om;
+  float* bn_ov;
 };
 
 struct GemmArgs {
@@ -841,10 +846,14 @@ __device__ __forceinline__ int kred_of(const GemmArgs& g, int z) {
 }
 
 // EPI 1: the kind-2 epilogue with the BatchNorm2D -> ReLU backward folded in; EPI 2: the
-// kind-1 epilogue with the capped parameter update applied in place (separate
-// instantiations: their extra registers would otherwise cost every kernel occupancy)
+// kind-1 epilogue with the capped parameter update applied in place; EPI 3: EPI 1 applied
+// to product + addend, storing both (separate instantiations: their extra registers would
+// otherwise cost every kernel occupancy)
+// (the folded BatchNorm2D epilogues keep 4 waves per SIMD: their prefetched operands would
+// otherwise take the register count just past the 128 that allows it)
 template <int PROD, class CFG, int KA, int KB, int EPI = 0>
-__global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(CFG::NTH, ((EPI == 1 || EPI == 3) && CFG::NTH == 256) ? 4 : CFG::MINB)
+    gemm_kernel(GemmArgs g) {
   constexpr int BM = CFG::BM, BN = CFG::BN, BK = CFG::BK, WM = CFG::WM, WN = CFG::WN, NTH = CFG::NTH;
   constexpr int NA = (PROD == PROD_SHARED_A) ? 1 : 2;
   constexpr int NB = (PROD == PROD_SHARED_B) ? 1 : 2;
@@ -1099,7 +1108,60 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
   // wave reads after the barrier that ended step t-1. The loop runs in periods of two
   // steps so that every buffer and stage index is a compile-time constant.
   constexpr int PERIOD = 2;
-  for (int kt = 0; kt < nk; kt += PERIOD) {
+  // EPI 2 with one 32 x 32 tile per wave: the epilogue's operands (each output's
+  // variance and mean before the update) are loaded during the last period's MFMAs, in
+  // place of that period's fetches, which would only read past the reduction. Without
+  // it every block of a round reaches its epilogue at about the same time and waits
+  // there for those loads with the matrix cores idle (K = 256: a quarter of the time).
+  constexpr bool EPF = EPI == 2 && TM == 1 && TN == 1 && KA == LD_STR_MN4;
+  float epf_s[EPF ? 16 : 1];
+  auto epf_load = [&] {
+    if constexpr (EPF) {
+      const Epi& e = g.epi;
+      const int col = n0 + wn * WN + rl;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * WM + 8 * (v >> 2) + 4 * hl + (v & 3);
+        epf_s[v] = 1.f;
+        if (row < R && col < g.C) {
+          if (row < e.wrows) {
+            int wr = row;
+            if (e.perm_C > 0) {
+              const int kidx = fdiv(row, e.dperm);
+              wr = (row - kidx * e.perm_C) * e.perm_kk2 + kidx;
+            }
+            const int64_t wi = (int64_t)wr * e.ldw + col;
+            epf_s[v] = e.Sw[wi];
+          } else {
+            epf_s[v] = e.Sb[col];
+          }
+        }
+      }
+    }
+  };
+  // EPI 1 and 3 (stride 1: GEMM row r is input pixel r): the BatchNorm2D's saved m_hat
+  // and the ReLU Jacobian of the lane's 16 outputs, loaded the same way (the host keeps
+  // R * C below 2^31, so 32-bit offsets); in the 64 x 64 tiles, the ones the ResNet
+  // stages use (in the others the registers would cost occupancy or spill)
+  constexpr bool EPFB = (EPI == 1 || EPI == 3) && BM == 64 && BN == 64 && TM == 1 && TN == 1;
+  float epb_h[EPFB ? 16 : 1], epb_j[EPFB ? 16 : 1];
+  auto epb_load = [&] {
+    if constexpr (EPFB) {
+      const Epi& e = g.epi;
+      const int col = n0 + wn * WN + rl;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * WM + 8 * (v >> 2) + 4 * hl + (v & 3);
+        const bool ok = row < R && col < g.C;
+        const int off = row * g.C + col;
+        epb_h[v] = ok ? e.bn_mhat[off] : 0.f;
+        epb_j[v] = ok ? e.bn_J[off] : 0.f;
+      }
+    }
+  };
+  constexpr bool PEEL = EPF || EPFB;
+  const int kt_end = (PEEL && nk > 0) ? ((nk - 1) / PERIOD) * PERIOD : nk;
+  for (int kt = 0; kt < kt_end; kt += PERIOD) {
     static_for<0, PERIOD>([&](auto U) {
       constexpr int u = decltype(U)::value;
       const int t = kt + u;
@@ -1112,6 +1174,25 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
       });
       __syncthreads();
     });
+  }
+  if constexpr (PEEL) {
+    static_assert(PERIOD == 2 && PF == 2, "the last period below is written for two steps and two stages");
+    if (nk > 0) {
+      // the last period: tile kt_end (buffer 0), then tile kt_end + 1 (buffer 1, fetched
+      // into stage 1 during the previous period; zeros when nk is odd); nothing is fetched
+      compute_tile(smem, [&] {
+        la.template store<1>(smem + (SA + SB));
+        lb.template store<1>(smem + (SA + SB) + SA);
+        epf_load();
+        epb_load();
+      });
+      __syncthreads();
+      compute_tile(smem + (SA + SB), [] {});
+      __syncthreads();
+    } else {
+      epf_load();
+      epb_load();
+    }
   }
 
   // Epilogue: split-K partial sums, or the layer's epilogue. The epilogue kind is the same
@@ -1231,7 +1312,7 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
     // With an addend (the shortcut deltas, possibly the output itself), a lane's 16 addends
     // of a column are loaded before any of its outputs is stored: a load issued after a
     // store to a possibly aliasing address would wait for it, element by element.
-    constexpr bool bn = EPI == 1;
+    constexpr bool bn = EPI == 1 || EPI == 3;
     float* red = smem;  // BatchNorm sums: [BM / WM][6][BN] column sums per wave row
     static_assert((BM / WM) * 6 * BN <= 2 * (SA + SB), "BatchNorm sums must fit the LDS tiles");
     float bsum[TN][6];
@@ -1239,6 +1320,58 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int q = 0; q < 6; ++q) bsum[j][q] = 0.f;
+    if constexpr (EPFB) {
+      // m_hat and J are in registers (loaded during the last k-period); EPI 3 loads its
+      // addends 8 at a time, each group before its stores (which may alias them)
+      const int col = n0 + wn * WN + rl;
+      if (col < g.C) {
+        const float rv = e.bn_var[col] + e.bn_eps;
+        const float km = e.bn_g[col] * (1.0f / sqrtf(rv));
+        const float kS = e.bn_g[col] * e.bn_g[col] * (1.0f / rv);
+        float ad0[EPI == 3 ? 8 : 1], ad1[EPI == 3 ? 8 : 1];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm * WM + 8 * (v >> 2) + 4 * hl + (v & 3);
+          if constexpr (EPI == 3) {
+            if ((v & 7) == 0) {
+#pragma unroll
+              for (int u = 0; u < 8; ++u) {
+                const int ru = m0 + wm * WM + 8 * ((v + u) >> 2) + 4 * hl + ((v + u) & 3);
+                const int ou = ru * g.C + col;
+                ad0[u] = ru < R ? e.am[ou] : 0.f;
+                ad1[u] = ru < R ? e.av[ou] : 0.f;
+              }
+            }
+          }
+          if (row >= R) continue;
+          const int off = row * g.C + col;
+          float a = accM[0][0][v], b = accV[0][0][v];
+          if constexpr (EPI == 3) {
+            a = a + ad0[v & 7];
+            b = b + ad1[v & 7];
+            e.om[off] = a;
+            e.ov[off] = b;
+          }
+          const float h = epb_h[v], jj = epb_j[v];
+          bsum[0][0] += a * h;
+          bsum[0][1] += b * h * h;
+          bsum[0][2] += a;
+          bsum[0][3] += b;
+          float o0 = a * km, o1 = b * kS;
+          o0 = o0 * jj;
+          o1 = o1 * jj * jj;
+          bsum[0][4] += o0;
+          bsum[0][5] += o1;
+          if constexpr (EPI == 3) {
+            e.bn_om[off] = o0;
+            e.bn_ov[off] = o1;
+          } else {
+            e.om[off] = o0;
+            e.ov[off] = o1;
+          }
+        }
+      }
+    } else
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       int64_t pixc[16];  // pixel offset * C, or -1 past the phase's rows
@@ -1260,28 +1393,52 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
           const float rv = e.bn_var[col] + e.bn_eps;
           const float km = e.bn_g[col] * (1.0f / sqrtf(rv));
           const float kS = e.bn_g[col] * e.bn_g[col] * (1.0f / rv);
-          float hv[16], jv[16];
+          // EPI 3 in two halves of 8 outputs (all four operands of 16 at once would cost
+          // occupancy); each half's loads come before its stores, which may alias the addend
+          constexpr int NH = EPI == 3 ? 2 : 1, HV = 16 / NH;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            hv[v] = pixc[v] >= 0 ? e.bn_mhat[pixc[v] + col] : 0.f;
-            jv[v] = pixc[v] >= 0 ? e.bn_J[pixc[v] + col] : 0.f;
-          }
+          for (int hh = 0; hh < NH; ++hh) {
+            float hv[HV], jv[HV], ad0[HV], ad1[HV];
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            if (pixc[v] < 0) continue;
-            const int64_t off = pixc[v] + col;
-            const float a = accM[i][j][v], b = accV[i][j][v], h = hv[v], jj = jv[v];
-            bsum[j][0] += a * h;
-            bsum[j][1] += b * h * h;
-            bsum[j][2] += a;
-            bsum[j][3] += b;
-            float o0 = a * km, o1 = b * kS;
-            o0 = o0 * jj;
-            o1 = o1 * jj * jj;
-            bsum[j][4] += o0;
-            bsum[j][5] += o1;
-            e.om[off] = o0;
-            e.ov[off] = o1;
+            for (int u = 0; u < HV; ++u) {
+              const int v = hh * HV + u;
+              hv[u] = pixc[v] >= 0 ? e.bn_mhat[pixc[v] + col] : 0.f;
+              jv[u] = pixc[v] >= 0 ? e.bn_J[pixc[v] + col] : 0.f;
+              if constexpr (EPI == 3) {
+                ad0[u] = pixc[v] >= 0 ? e.am[pixc[v] + col] : 0.f;
+                ad1[u] = pixc[v] >= 0 ? e.av[pixc[v] + col] : 0.f;
+              }
+            }
+#pragma unroll
+            for (int u = 0; u < HV; ++u) {
+              const int v = hh * HV + u;
+              if (pixc[v] < 0) continue;
+              const int64_t off = pixc[v] + col;
+              float a = accM[i][j][v], b = accV[i][j][v];
+              if constexpr (EPI == 3) {
+                a = a + ad0[u];
+                b = b + ad1[u];
+                e.om[off] = a;
+                e.ov[off] = b;
+              }
+              const float h = hv[u], jj = jv[u];
+              bsum[j][0] += a * h;
+              bsum[j][1] += b * h * h;
+              bsum[j][2] += a;
+              bsum[j][3] += b;
+              float o0 = a * km, o1 = b * kS;
+              o0 = o0 * jj;
+              o1 = o1 * jj * jj;
+              bsum[j][4] += o0;
+              bsum[j][5] += o1;
+              if constexpr (EPI == 3) {
+                e.bn_om[off] = o0;
+                e.bn_ov[off] = o1;
+              } else {
+                e.om[off] = o0;
+                e.ov[off] = o1;
+              }
+            }
           }
           continue;
         }
@@ -1342,7 +1499,56 @@ __global__ void __launch_bounds__(CFG::NTH, CFG::MINB) gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int col = n0 + wn * WN + j * 32 + rl;
-        if constexpr (EPI == 2) {
+        if constexpr (EPF) {
+          // the variances were loaded during the last k-period; the means are loaded one
+          // group of 4 ahead of the stores (a load after a store that may alias it would
+          // wait for it)
+          auto widx = [&](int v) -> int64_t {
+            const int row = m0 + wm * WM + 8 * (v >> 2) + 4 * hl + (v & 3);
+            if (!(row < R && col < g.C)) return -2;
+            if (row >= e.wrows) return -1;
+            int wr = row;
+            if (e.perm_C > 0) {
+              const int kidx = fdiv(row, e.dperm);
+              wr = (row - kidx * e.perm_C) * e.perm_kk2 + kidx;
+            }
+            return (int64_t)wr * e.ldw + col;
+          };
+          float pm[4][4];
+          auto load_means = [&](int q) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int64_t w = widx(4 * q + u);
+              pm[q][u] = w >= 0 ? e.upd_mw[w] : (w == -1 ? e.upd_mb[col] : 0.f);
+            }
+          };
+          load_means(0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (q < 3) load_means(q + 1);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int64_t w = widx(4 * q + u);
+              if (w == -2) continue;
+              const float sv = epf_s[4 * q + u];
+              const float dm = sv * accM[0][0][4 * q + u], dS = (sv * sv) * accV[0][0][4 * q + u];
+              float pmu = pm[q][u], pS = sv;
+              capped(pmu, pS, dm, dS, e.cap);
+              if (w >= 0) {
+                e.om[w] = dm;
+                e.ov[w] = dS;
+                e.upd_mw[w] = pmu;
+                e.upd_Sw[w] = pS;
+              } else {
+                e.dmb[col] = dm;
+                e.dSb[col] = dS;
+                e.upd_mb[col] = pmu;
+                e.upd_Sb[col] = pS;
+              }
+            }
+          }
+          continue;
+        } else if constexpr (EPI == 2) {
           // with the capped update in place: per group of 4 outputs, the variances and
           // means are loaded before the group's stores (16 at once would cost occupancy)
 #pragma unroll
@@ -1707,8 +1913,8 @@ static inline int64_t plan_ws_bytes(const Plan& p, int64_t R, int64_t C, int64_t
   X(PROD_SHARED_A, LD_STR_K4, LD_STR_K4) X(PROD_SHARED_A, LD_STR_K4, LD_STR_MN4)         \
   X(PROD_SHARED_A, LD_STR_MN4, LD_STR_K4)
 
-// The input-delta loader pairs that also get the folded BatchNorm2D epilogue (EPI 1), in
-// the tile configs with one 32 x 32 tile per wave (64 x 64, 32 x 32, 128 x 32)
+// The input-delta loader pairs that also get the folded BatchNorm2D epilogues (EPI 1 and
+// 3), in the tile configs with one 32 x 32 tile per wave (64 x 64, 32 x 32, 128 x 32)
 #define TAGI_GEMM_COMBOS_SHARED_B_BNF(X)                                                 \
   X(PROD_SHARED_B, LD_CBWD_A4T, LD_CBWD_BK4T) X(PROD_SHARED_B, LD_CBWD_A4, LD_CBWD_BK4)
 static inline bool bnf_cfg(int cfg) { return cfg == 3 || cfg == 4 || cfg == 5; }
@@ -1733,7 +1939,7 @@ void launch_cfg(const GemmArgs& g, int64_t grid_x, int64_t grid_y, hipStream_t s
 template <int PROD, int KA, int KB, int EPI = 0>
 static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, int64_t ws_bytes, hipStream_t s,
                            const char* what, int64_t grid_x_override = 0) {
-  if constexpr (EPI == 1)
+  if constexpr (EPI == 1 || EPI == 3)
     TAGI_REQUIRE(bnf_cfg(p.cfg) && p.splits == 1, "%s: folded epilogue needs an unsplit one-tile-per-wave plan",
                  what);
   // operand byte offsets are 32-bit with the out-of-range sentinel above them
@@ -1756,11 +1962,11 @@ static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, 
   const int64_t gy = batch * p.splits;
   TAGI_REQUIRE(gx > 0 && gx < (1ll << 31) && gy < 65536, "%s: grid out of range (%lld x %lld)", what, (long long)gx,
                (long long)gy);
-  if constexpr (EPI == 1) {
+  if constexpr (EPI == 1 || EPI == 3) {
     switch (p.cfg) {
-      case 3: launch_cfg<PROD, C64x64, KA, KB, 1>(g, gx, gy, s); break;
-      case 5: launch_cfg<PROD, C128x32, KA, KB, 1>(g, gx, gy, s); break;
-      default: launch_cfg<PROD, C32x32, KA, KB, 1>(g, gx, gy, s); break;
+      case 3: launch_cfg<PROD, C64x64, KA, KB, EPI>(g, gx, gy, s); break;
+      case 5: launch_cfg<PROD, C128x32, KA, KB, EPI>(g, gx, gy, s); break;
+      default: launch_cfg<PROD, C32x32, KA, KB, EPI>(g, gx, gy, s); break;
     }
   } else {
     // EPI 2 applies its update in the kernel only when unsplit (the reduction's epilogue

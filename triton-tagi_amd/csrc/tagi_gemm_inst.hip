@@ -32,7 +32,8 @@ TAGI_GEMM_COMBOS_FWD(TAGI_INST)
 TAGI_GEMM_COMBOS_SHARED_B(TAGI_INST)
 #if TAGI_INST_CFG >= 3
 #define TAGI_INST_BNF(P, KA, KB) \
-  template void launch_cfg<P, InstCfg, KA, KB, 1>(const GemmArgs&, int64_t, int64_t, hipStream_t);
+  template void launch_cfg<P, InstCfg, KA, KB, 1>(const GemmArgs&, int64_t, int64_t, hipStream_t); \
+  template void launch_cfg<P, InstCfg, KA, KB, 3>(const GemmArgs&, int64_t, int64_t, hipStream_t);
 TAGI_GEMM_COMBOS_SHARED_B_BNF(TAGI_INST_BNF)
 #endif
 #else

@@ -94,6 +94,7 @@ _SIGS = {
     "tagi_conv2d_bwd_delta_add": (c_int, [P, P, P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_bwd_delta_bn_relu": (c_int, [P, P, P, P, P, P, P, F, P, P, P, I64, GP, P, I64, P]),
     "tagi_conv2d_bwd_delta_bn_relu_part_bytes": (I64, [GP]),
+    "tagi_conv2d_bwd_delta_add_bn_relu": (c_int, [P, P, P, P, P, P, P, P, P, P, P, F, P, P, P, I64, GP, P, I64, P]),
     "tagi_conv2d_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, GP, P, I64, P]),
     "tagi_conv2d_wgrad_ws_bytes": (I64, [GP]),
     "tagi_relu_fwd": (c_int, [P, P, P, P, P, I64, P]),

@@ -16,6 +16,11 @@ in how often activations cross HBM:
   follows the pair, that pass is the epilogue of the Conv2D's input-delta GEMM.
 * The merge of the shortcut deltas into the main branch (resblock.py:421-423) is folded
   into the input-delta GEMM of the block's first convolution.
+* Within ``Sequential.step``, when that convolution has stride 1, the same GEMM also runs
+  the BatchNorm2D -> ReLU backward of the layers in front of the block (the previous
+  block's closing pair, or the stem's): the block's input deltas are still stored (the
+  previous block's shortcut reads them) and the previous block's backward starts at its
+  second convolution.
 * ReLU followed by AvgPool2D (relu.py:94-122, avgpool2d.py:38-90) is one pass that writes
   the ReLU Jacobian and the pooled moments, not the ReLU output; backward, the pooling's
   deltas and the Jacobian are one pass as well (when H and W are multiples of the window).
@@ -37,6 +42,7 @@ from .avgpool2d import AvgPool2D
 from .batchnorm2d import BatchNorm2D
 from .conv2d import Conv2D
 from .relu import ReLU
+from .resblock import ResBlock
 
 
 def _add_in_place(src_m: Tensor, src_S: Tensor, dst_m: Tensor, dst_S: Tensor) -> None:
@@ -213,6 +219,101 @@ def conv_bn_relu_backward(conv: Conv2D, bn: BatchNorm2D, relu: ReLU, conv_prev: 
     return d_ma, d_Sa
 
 
+def conv_add_bn_relu_backward(conv: Conv2D, delta_ma: Tensor, delta_Sa: Tensor, add: tuple[Tensor, Tensor],
+                              bn: BatchNorm2D, relu: ReLU, conv_prev: Conv2D):
+    """``conv._backward(delta, True, add=add)`` (a residual block's first convolution, the
+    shortcut's deltas added) followed by ``bn_relu_backward(bn, relu, ..., conv_prev)`` for
+    the layers conv_prev -> relu -> bn in front of the block, in one input-delta GEMM whose
+    epilogue stores both. Returns ((d_ma, d_Sa), (d_mz, d_Sz)): the deltas at the block's
+    input and at conv_prev's output; or None, having done nothing, where the fold does not
+    apply (outside ``defer_bn_parameter_deltas``, stride 2, split plans). The BatchNorm2D
+    parameter deltas and conv_prev's bias deltas are left pending, as in
+    ``conv_bn_relu_backward``."""
+    ctx = _active_defer()
+    if ctx is None or conv_prev.mb is None or bn.m_hat is None or relu.J is None:
+        return None
+    N, C, H, W = conv.input_shape
+    if (conv_prev.C_out != C or tuple(bn.input_shape) != (N, C, H, W) or tuple(bn.m_hat.shape) != (N, C, H, W)
+            or tuple(relu.J.shape) != (N, C, H, W)):
+        return None
+    g = conv._geom(N, C, H, W)
+    part_bytes = _lib.query("tagi_conv2d_bwd_delta_bn_relu_part_bytes", g)
+    if part_bytes <= 0:
+        return None
+    g, dmz, dSz = conv._output_deltas(delta_ma, delta_Sa)
+    if any(t.data_ptr() % 16 for t in (dmz, dSz, conv.mw)):
+        return None  # the fold reads the deltas and weights as float4
+    conv._param_deltas(g, dmz, dSz)
+    dev = dmz.device
+    d_ma = _lib.empty_cl(N, C, H, W, dev)
+    d_Sa = _lib.empty_cl(N, C, H, W, dev)
+    am = _lib.check(_lib.like(add[0].reshape(N, C, H, W), d_ma), "add_m")
+    aS = _lib.check(_lib.like(add[1].reshape(N, C, H, W), d_ma), "add_S")
+    d_mz = _lib.empty_cl(N, C, H, W, dev)
+    d_Sz = _lib.empty_cl(N, C, H, W, dev)
+    mhat = _lib.check(_lib.like(bn.m_hat, d_ma), "m_hat")
+    J = _lib.check(_lib.like(relu.J, d_ma), "J")
+    bn.delta_mw = torch.empty(C, device=dev, dtype=torch.float32)
+    bn.delta_Sw = torch.empty_like(bn.delta_mw)
+    bn.delta_mb = torch.empty_like(bn.delta_mw)
+    bn.delta_Sb = torch.empty_like(bn.delta_mw)
+    conv_prev.delta_mb = torch.empty(1, C, device=dev, dtype=torch.float32)
+    conv_prev.delta_Sb = torch.empty_like(conv_prev.delta_mb)
+    part = _lib.workspace(part_bytes, dev)
+    ws = _lib.workspace(_lib.query("tagi_conv2d_bwd_delta_ws_bytes", g), dev)
+    wp, wb = _lib.ws_args(ws)
+    _lib.call("tagi_conv2d_bwd_delta_add_bn_relu", dmz.data_ptr(), dSz.data_ptr(), conv.mw.data_ptr(),
+              am.data_ptr(), aS.data_ptr(), d_ma.data_ptr(), d_Sa.data_ptr(), mhat.data_ptr(), J.data_ptr(),
+              _lib.check(bn._norm_var, "norm_var").data_ptr(), _lib.check(bn.mw, "mw").data_ptr(), float(bn.eps),
+              d_mz.data_ptr(), d_Sz.data_ptr(), part.data_ptr(), part_bytes, g, wp, wb, _lib.stream_of(dmz))
+    ctx.add(bn, part, N, C, H * W, conv=conv_prev, nblk=part_bytes // (24 * C))
+    return (d_ma, d_Sa), (d_mz, d_Sz)
+
+
+class _Fold:
+    """The layers conv -> relu -> bn in front of a residual block, whose backward the
+    block's first input-delta GEMM may take over; ``out`` receives the deltas at conv's
+    output when it does."""
+
+    __slots__ = ("conv", "relu", "bn", "out")
+
+    def __init__(self, conv: Conv2D, relu: ReLU, bn: BatchNorm2D) -> None:
+        self.conv, self.relu, self.bn = conv, relu, bn
+        self.out = None
+
+
+def _fold_in_front(layers, i: int):
+    """A _Fold for the layers in front of the ResBlock ``layers[i]`` (the previous block's
+    closing conv2 -> relu2 -> bn2, or three such layers of the list), or None."""
+    if _active_defer() is None or i < 1:
+        return None
+    prev = layers[i - 1]
+    if isinstance(prev, ResBlock):
+        tail = prev._main_layers[3:6]
+    elif i >= 3:
+        tail = layers[i - 3:i]
+    else:
+        return None
+    conv, relu, bn = tail
+    if isinstance(conv, Conv2D) and _fusable_backward(bn, relu):
+        return _Fold(conv, relu, bn)
+    return None
+
+
+def resblock_backward(block: ResBlock, delta_mu: Tensor, delta_var: Tensor, start=None, fold: _Fold | None = None):
+    """Deltas at the block's input (resblock.py:387-430). ``start``: the deltas at conv2's
+    output, when the next block's first input-delta GEMM already ran this block's closing
+    BatchNorm2D -> ReLU backward; ``fold``: the layers in front of this block, whose
+    backward this block's first input-delta GEMM then runs (``fold.out`` is set if it did)."""
+    if block._proj_layers:
+        d_skip = backward_chain(block._proj_layers, delta_mu, delta_var)
+    else:
+        d_skip = (delta_mu, delta_var)
+    if start is None:
+        return backward_chain(block._main_layers, delta_mu, delta_var, add=d_skip, fold=fold)
+    return backward_chain(block._main_layers[:4], start[0], start[1], add=d_skip, fold=fold)
+
+
 def relu_avgpool_forward(relu: ReLU, pool: AvgPool2D, mz: Tensor, Sz: Tensor) -> tuple[Tensor, Tensor]:
     """pool.forward(*relu.forward(mz, Sz)) in one pass; stores relu.J and the pool's input
     shape, as the two calls do."""
@@ -302,16 +403,32 @@ def forward_chain(layers, mu: Tensor, var: Tensor,
 
 
 def backward_chain(layers, delta_mu: Tensor, delta_var: Tensor, add: tuple[Tensor, Tensor] | None = None,
-                   first_params_only: bool = False):
+                   first_params_only: bool = False, fold: _Fold | None = None):
     """Backward through ``layers`` in reverse; ``add`` is added to the returned deltas.
 
     With ``first_params_only`` the first layer forms only its parameter deltas (when it
-    can) and None is returned.
+    can) and None is returned. ``fold`` (with ``add``, the first layer a Conv2D): the
+    layers in front, whose backward that Conv2D's input-delta GEMM runs where it can.
     """
     i = len(layers) - 1
+    start = None  # conv2 output deltas of the ResBlock at i, formed by the block after it
     while i >= 0:
         layer = layers[i]
         prev = layers[i - 1] if i >= 1 else None
+        if isinstance(layer, ResBlock):
+            f = _fold_in_front(layers, i)
+            delta_mu, delta_var = resblock_backward(layer, delta_mu, delta_var, start=start, fold=f)
+            start = None
+            if f is not None and f.out is not None:
+                if isinstance(prev, ResBlock):
+                    start = f.out
+                    i -= 1
+                else:
+                    delta_mu, delta_var = f.out  # on to the conv in front of the ReLU
+                    i -= 3
+                continue
+            i -= 1
+            continue
         if (isinstance(layer, Conv2D) and i >= 3 and _fusable_backward(prev, layers[i - 2])
                 and isinstance(layers[i - 3], Conv2D)):
             out = conv_bn_relu_backward(layer, prev, layers[i - 2], layers[i - 3], delta_mu, delta_var)
@@ -333,6 +450,11 @@ def backward_chain(layers, delta_mu: Tensor, delta_var: Tensor, add: tuple[Tenso
                 layer.backward_param_deltas(delta_mu, delta_var)
                 return None
             if add is not None and isinstance(layer, Conv2D):
+                if fold is not None:
+                    out = conv_add_bn_relu_backward(layer, delta_mu, delta_var, add, fold.bn, fold.relu, fold.conv)
+                    if out is not None:
+                        fold.out = out[1]
+                        return out[0]
                 return layer._backward(delta_mu, delta_var, True, add=add)
         delta_mu, delta_var = layer.backward(delta_mu, delta_var)
         i -= 1

@@ -115,13 +115,9 @@ class ResBlock(LearnableLayer):
     def backward(self, delta_mu: Tensor, delta_var: Tensor) -> tuple[Tensor, Tensor]:
         """Deltas through both branches, summed (resblock.py:387-430); the shortcut's
         deltas are added inside the main branch's first input-delta GEMM."""
-        from .fused import backward_chain
+        from .fused import resblock_backward
 
-        if self._proj_layers:
-            d_skip = backward_chain(self._proj_layers, delta_mu, delta_var)
-        else:
-            d_skip = (delta_mu, delta_var)
-        return backward_chain(self._main_layers, delta_mu, delta_var, add=d_skip)
+        return resblock_backward(self, delta_mu, delta_var)
 
     def _update_items(self):
         items = []
