@@ -169,31 +169,50 @@ def last_error() -> str:
     return msg.decode() if msg else ""
 
 
+_fns: dict = {}  # (library handle id, name) -> bound entry point
+
+
+def _fn(name: str):
+    lib = load()
+    key = (id(lib), name)
+    f = _fns.get(key)
+    if f is None:
+        f = _fns[key] = getattr(lib, name)
+    return f
+
+
 def call(name: str, *args) -> None:
     """Invoke a status-returning entry point; raise RuntimeError on failure."""
-    rc = getattr(load(), name)(*args)
+    rc = _fn(name)(*args)
     if rc != TAGI_OK:
         raise RuntimeError(f"{name} failed (status {rc}): {last_error()}")
 
 
 def query(name: str, *args) -> int:
-    return int(getattr(load(), name)(*args))
+    return int(_fn(name)(*args))
 
 
 # ---------------------------------------------------------------------------------
 # Tensor plumbing
 # ---------------------------------------------------------------------------------
+# torch's current-stream handle without building a Stream object (the public call below
+# costs a few microseconds, a launch-bound step makes about 15 of them)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
     """Handle of torch's current stream on t's device (the stream kernels are queued on)."""
+    if _raw_stream is not None and t.is_cuda:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def check(t: torch.Tensor, name: str, contiguous: bool = True) -> torch.Tensor:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
-    if t.dtype != torch.float32:
+    if t.dtype is not torch.float32:
         raise TypeError(f"{name}: expected float32, got {t.dtype}")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise ValueError(
             f"{name}: tensor is on {t.device}; the TAGI HIP kernels run on the GPU only"
         )
