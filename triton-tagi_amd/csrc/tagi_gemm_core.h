@@ -1806,6 +1806,15 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
   static const int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 20, 24, 32, 40, 48, 64, 80, 96, 128, 160, 192, 256};
   const double kOcc2 = 0.924, kOcc1 = 0.667, kOcc0 = 0.35;
   const double kSplitSecPerByte = 1.82e-13, kSplitLaunch = 5.95e-6;
+  // Small problems (fewer than 128 tiles of 64 x 64, the Linear layers of the MLP and CNN
+  // heads): a block's k-loop waits on its loads' latency rather than on the matrix cores,
+  // so a round takes at least kChainFixed + kChainTile per k-tile of the block, and the
+  // reduction of their few partial sums costs less than a large one's. Fitted to a sweep
+  // of every tile config and split count on those shapes (kernel-trace durations). Not for
+  // the phased conv input deltas, whose unsplit plans carry the folded BatchNorm backward.
+  static const double kChainTile[6] = {2.4e-6, 1.8e-6, 1.8e-6, 0.96e-6, 1.0e-6, 1.05e-6};
+  const double kChainFixed = 3.5e-6, kSplitLaunchSmall = 3.0e-6;
+  const bool small = !phase_k && cdiv(R, 64) * cdiv(C, 64) * batch < 128;
   const int products = prod == PROD_FWD ? 3 : 2;
   Plan best{3, 1, (int)Kred, 1, 1};
   double best_t = DBL_MAX;
@@ -1823,7 +1832,8 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
       const int64_t actual = cdiv(Kred, kc);
       if (actual == prev_actual) continue;
       prev_actual = actual;
-      if (actual > 1 && kc < 64) break;  // splits below 4 k-tiles only add reduction traffic
+      // splits below 4 k-tiles (2 in small problems) only add reduction traffic
+      if (actual > 1 && kc < (small ? 32 : 64)) break;
       int64_t blocks = tm * tn * batch * actual;
       if (phase_k) {
         // a phase with a shorter reduction (or the short last chunk of one) does that
@@ -1837,12 +1847,14 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
       auto round_s = [&](int64_t r) {
         const double wps = (double)r * kWaves[ci] / 4.0;  // waves per SIMD
         const double occ = wps >= 3.0 ? 1.0 : (wps >= 2.0 ? kOcc2 : (wps >= 1.0 ? kOcc1 : kOcc0));
-        return (double)r * block_s / occ;
+        const double t = (double)r * block_s / occ;
+        return small ? fmax(t, kChainFixed + (double)(kc / 16) * kChainTile[ci]) : t;
       };
       const int64_t slots = 256 * (int64_t)bpc;
       const int64_t full = blocks / slots, rem = blocks - full * slots;
       double t = (double)full * round_s(bpc) + (rem > 0 ? round_s(cdiv(rem, 256)) : 0.0);
-      if (actual > 1) t += (double)actual * 16.0 * R * C * batch * kSplitSecPerByte + kSplitLaunch;
+      if (actual > 1)
+        t += (double)actual * 16.0 * R * C * batch * kSplitSecPerByte + (small ? kSplitLaunchSmall : kSplitLaunch);
       if (t < best_t * 0.999) {
         best_t = t;
         best = Plan{ci, (int)actual, (int)kc, (int)tm, (int)tn};
