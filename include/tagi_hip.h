@@ -406,18 +406,21 @@ int tagi_avgpool2d_bwd(const float* dm, const float* dS, float* dm_out, float* d
 
 /* ReLU followed by the average pool above, in one pass over the channels-last (N, C, H, W)
  * input moments mz, Sz: writes the ReLU Jacobian J (N, C, H, W) and the pooled moments
- * (N, C, H/k, W/k); the ReLU output is not written. The same values, bit for bit, as
- * tagi_relu_fwd followed by tagi_avgpool2d_fwd. H and W multiples of k (else
- * TAGI_ERR_UNSUPPORTED). Replaces relu.py:94-122 followed by avgpool2d.py:38-90. */
+ * (N, C, H/k, W/k), channels-last, or row-major NCHW with pooled_nchw != 0 (what a
+ * following Flatten, flatten.py:25-53, reads as a plain view); the ReLU output is not
+ * written. The same values, bit for bit, as tagi_relu_fwd followed by tagi_avgpool2d_fwd.
+ * H and W multiples of k (else TAGI_ERR_UNSUPPORTED). Replaces relu.py:94-122 followed
+ * by avgpool2d.py:38-90. */
 int tagi_relu_avgpool2d_fwd(const float* mz, const float* Sz, float* J, float* ma_out,
                             float* Sa_out, int64_t N, int64_t C, int64_t H, int64_t W, int64_t k,
-                            float var_scale, tagi_stream_t stream);
-/* The backward of that pair: pooled deltas dm, dS (N, C, H/k, W/k) and the stored J give the
- * deltas at the ReLU input (N, C, H, W), bit for bit tagi_avgpool2d_bwd followed by
+                            float var_scale, int pooled_nchw, tagi_stream_t stream);
+/* The backward of that pair: pooled deltas dm, dS (N, C, H/k, W/k; channels-last, or
+ * row-major NCHW with pooled_nchw != 0) and the stored J give the deltas at the ReLU input
+ * (N, C, H, W, channels-last), bit for bit tagi_avgpool2d_bwd followed by
  * tagi_jacobian_bwd. Replaces avgpool2d.py:92-130 followed by relu.py:152-169. */
 int tagi_avgpool2d_relu_bwd(const float* dm, const float* dS, const float* J, float* dm_out,
                             float* dS_out, int64_t N, int64_t C, int64_t H, int64_t W, int64_t k,
-                            float var_scale, tagi_stream_t stream);
+                            float var_scale, int pooled_nchw, tagi_stream_t stream);
 
 /* ----------------------------------------------------------- BatchNorm2D ---- */
 /* Per-channel batch statistics of channels-last moments (batchnorm2d.py:307-339):

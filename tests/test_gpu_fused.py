@@ -471,12 +471,14 @@ def test_linear_bwd_delta_with_addend(dev, M, K, N):
     assert_scaled_close(oS, rS + d64(aS), None, RTOL, ATOL, "dSa + addend")
 
 
+@pytest.mark.parametrize("nchw", [False, True])
 @pytest.mark.parametrize("N,C,H,W,k,sc", [(4, 32, 32, 32, 2, False), (3, 5, 12, 12, 3, True), (2, 64, 8, 8, 4, False),
                                           (128, 32, 16, 16, 2, False)])
-def test_relu_avgpool_fused(dev, N, C, H, W, k, sc):
+def test_relu_avgpool_fused(dev, N, C, H, W, k, sc, nchw):
     """ReLU -> AvgPool2D as one pass each way (tagi_relu_avgpool2d_fwd, tagi_avgpool2d_relu_bwd)
     against the two layers' own calls, bit for bit, and against the float64 oracle; C % 4 != 0
-    takes the scalar path."""
+    takes the scalar path. ``nchw``: the pooled side row-major (as before a Flatten) instead
+    of channels-last, in both directions."""
     from triton_tagi_amd.layers.avgpool2d import AvgPool2D
     from triton_tagi_amd.layers.fused import avgpool_relu_backward, relu_avgpool_forward
     from triton_tagi_amd.layers.relu import ReLU
@@ -486,7 +488,8 @@ def test_relu_avgpool_fused(dev, N, C, H, W, k, sc):
     Sz = (0.05 + torch.rand(N, C, H, W, generator=r)).contiguous(memory_format=torch.channels_last).to(dev)
     mz[0, 0, 0, :4] = torch.tensor([-30.0, -6.0, 0.0, 40.0], device=dev)  # both tails of the rectified moments
     relu, pool = ReLU(), AvgPool2D(k, spatial_correlation=sc)
-    mo, So = relu_avgpool_forward(relu, pool, mz, Sz)
+    mo, So = relu_avgpool_forward(relu, pool, mz, Sz, nchw=nchw)
+    assert mo.is_contiguous() == nchw or mo.shape[2] * mo.shape[3] == 1
     relu_u, pool_u = ReLU(), AvgPool2D(k, spatial_correlation=sc)
     uo, uSo = pool_u.forward(*relu_u.forward(mz, Sz))
     assert torch.equal(mo, uo) and torch.equal(So, uSo), "pooled moments differ from the separate passes"
@@ -497,6 +500,9 @@ def test_relu_avgpool_fused(dev, N, C, H, W, k, sc):
     assert_scaled_close(So, rS, None, RTOL, ATOL, "pooled var vs oracle")
     dm = torch.randn(mo.shape, generator=r).to(dev)
     dS = -torch.rand(mo.shape, generator=r).to(dev)
+    if not nchw:  # channels-last deltas, read as they are
+        dm = dm.contiguous(memory_format=torch.channels_last)
+        dS = dS.contiguous(memory_format=torch.channels_last)
     om, oS = avgpool_relu_backward(pool, relu, dm, dS)
     um, uS = relu_u.backward(*pool_u.backward(dm, dS))
     assert torch.equal(om, um) and torch.equal(oS, uS), "input deltas differ from the separate passes"

@@ -216,6 +216,8 @@ struct vec_of<1> {
   static __device__ __forceinline__ T scale(T a, float s) { return a * s; }
   static __device__ __forceinline__ T mul(T a, T b) { return a * b; }
   static __device__ __forceinline__ void relu(T m, T s, T& a, T& b, T& j) { relu_moments(m, s, a, b, j); }
+  static __device__ __forceinline__ float lane(T a, int) { return a; }
+  static __device__ __forceinline__ void set_lane(T& a, int, float x) { a = x; }
 };
 template <>
 struct vec_of<4> {
@@ -234,6 +236,13 @@ struct vec_of<4> {
     relu_moments(m.y, s.y, a.y, b.y, j.y);
     relu_moments(m.z, s.z, a.z, b.z, j.z);
     relu_moments(m.w, s.w, a.w, b.w, j.w);
+  }
+  static __device__ __forceinline__ float lane(T a, int v) { return v == 0 ? a.x : (v == 1 ? a.y : (v == 2 ? a.z : a.w)); }
+  static __device__ __forceinline__ void set_lane(T& a, int v, float x) {
+    if (v == 0) a.x = x;
+    else if (v == 1) a.y = x;
+    else if (v == 2) a.z = x;
+    else a.w = x;
   }
 };
 
@@ -296,7 +305,7 @@ __global__ void __launch_bounds__(256) avgpool_bwd_kernel(const float* __restric
 // k x k inputs (J stored for the backward pass) and sums them in avgpool_fwd_kernel's
 // order, so the outputs are the two launches' bit for bit; the ReLU output is never
 // written. H and W are multiples of k (every input lies in one window).
-template <typename IT, int V>
+template <typename IT, int V, bool NCHW>
 __global__ void __launch_bounds__(256) relu_avgpool_fwd_kernel(const float* __restrict__ mz,
                                                                const float* __restrict__ Sz, float* __restrict__ J,
                                                                float* __restrict__ mo, float* __restrict__ So, IT N,
@@ -325,8 +334,19 @@ __global__ void __launch_bounds__(256) relu_avgpool_fwd_kernel(const float* __re
         VO::add(sm, am);
         VO::add(ss, as);
       }
-    reinterpret_cast<T*>(mo)[i] = VO::scale(sm, inv_k2);
-    reinterpret_cast<T*>(So)[i] = VO::scale(ss, var_scale);
+    if constexpr (NCHW) {
+      // pooled moments laid out (N, C, Ho, Wo) row-major, as a following Flatten reads them
+      const T pm = VO::scale(sm, inv_k2), ps = VO::scale(ss, var_scale);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const IT o = ((n * C + c * V + v) * Ho + oh) * Wo + ow;
+        mo[o] = VO::lane(pm, v);
+        So[o] = VO::lane(ps, v);
+      }
+    } else {
+      reinterpret_cast<T*>(mo)[i] = VO::scale(sm, inv_k2);
+      reinterpret_cast<T*>(So)[i] = VO::scale(ss, var_scale);
+    }
   }
 }
 
@@ -334,7 +354,7 @@ __global__ void __launch_bounds__(256) relu_avgpool_fwd_kernel(const float* __re
 // each input element gets its window's deltas scaled as avgpool_bwd_kernel scales them,
 // times J and J^2 as jacobian_kernel multiplies (the same bits as the two launches; the
 // unpooled deltas are never written). H and W are multiples of k.
-template <typename IT, int V>
+template <typename IT, int V, bool NCHW>
 __global__ void __launch_bounds__(256) avgpool_relu_bwd_kernel(const float* __restrict__ dm,
                                                                const float* __restrict__ dS,
                                                                const float* __restrict__ J, float* __restrict__ om,
@@ -349,9 +369,22 @@ __global__ void __launch_bounds__(256) avgpool_relu_bwd_kernel(const float* __re
     const IT c = i % Cv, pix = i / Cv;
     const IT w = pix % W, t = pix / W;
     const IT h = t % H, n = t / H;
-    const IT j = ((n * Ho + h / k) * Wo + w / k) * Cv + c;
-    const T a = VO::scale(reinterpret_cast<const T*>(dm)[j], inv_k2);
-    const T b = VO::scale(reinterpret_cast<const T*>(dS)[j], var_scale);
+    T a, b;
+    if constexpr (NCHW) {
+      // pooled deltas laid out (N, C, Ho, Wo) row-major, as a following Flatten passes them
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const IT j = ((n * C + c * V + v) * Ho + h / k) * Wo + w / k;
+        VO::set_lane(a, v, dm[j]);
+        VO::set_lane(b, v, dS[j]);
+      }
+    } else {
+      const IT j = ((n * Ho + h / k) * Wo + w / k) * Cv + c;
+      a = reinterpret_cast<const T*>(dm)[j];
+      b = reinterpret_cast<const T*>(dS)[j];
+    }
+    a = VO::scale(a, inv_k2);
+    b = VO::scale(b, var_scale);
     const T jj = reinterpret_cast<const T*>(J)[i];
     reinterpret_cast<T*>(om)[i] = VO::mul(a, jj);
     reinterpret_cast<T*>(oS)[i] = VO::mul(VO::mul(b, jj), jj);
@@ -568,42 +601,53 @@ extern "C" int tagi_avgpool2d_bwd(const float* dm, const float* dS, float* dm_ou
   return check_launch("tagi_avgpool2d_bwd");
 }
 
-template <bool FWD, typename IT, int V>
-static void launch_pool_relu_as(const float* a, const float* b, float* J, float* c, float* d, IT N, IT C, IT H, IT W,
-                                IT k, float var_scale, unsigned blocks, hipStream_t s) {
+template <bool FWD, typename IT, int V, bool NCHW>
+static void launch_pool_relu_lay(const float* a, const float* b, float* J, float* c, float* d, IT N, IT C, IT H,
+                                 IT W, IT k, float var_scale, unsigned blocks, hipStream_t s) {
   const float inv_k2 = 1.0f / (float)(k * k);
   if constexpr (FWD)
-    hipLaunchKernelGGL((relu_avgpool_fwd_kernel<IT, V>), dim3(blocks), dim3(256), 0, s, a, b, J, c, d, N, H, W, C, k,
-                       inv_k2, var_scale);
+    hipLaunchKernelGGL((relu_avgpool_fwd_kernel<IT, V, NCHW>), dim3(blocks), dim3(256), 0, s, a, b, J, c, d, N, H, W,
+                       C, k, inv_k2, var_scale);
   else
-    hipLaunchKernelGGL((avgpool_relu_bwd_kernel<IT, V>), dim3(blocks), dim3(256), 0, s, a, b, J, c, d, N, H, W, C, k,
-                       inv_k2, var_scale);
+    hipLaunchKernelGGL((avgpool_relu_bwd_kernel<IT, V, NCHW>), dim3(blocks), dim3(256), 0, s, a, b, J, c, d, N, H, W,
+                       C, k, inv_k2, var_scale);
+}
+
+template <bool FWD, typename IT, int V>
+static void launch_pool_relu_as(const float* a, const float* b, float* J, float* c, float* d, IT N, IT C, IT H, IT W,
+                                IT k, float var_scale, bool nchw, unsigned blocks, hipStream_t s) {
+  if (nchw)
+    launch_pool_relu_lay<FWD, IT, V, true>(a, b, J, c, d, N, C, H, W, k, var_scale, blocks, s);
+  else
+    launch_pool_relu_lay<FWD, IT, V, false>(a, b, J, c, d, N, C, H, W, k, var_scale, blocks, s);
 }
 
 // FWD: a, b the conv output moments, J written, c, d the pooled moments; backward: a, b the
 // pooled deltas, J read, c, d the deltas at the ReLU input. items: threads' work units.
 template <bool FWD>
 static void launch_pool_relu(const float* a, const float* b, const float* J, float* c, float* d, int64_t N, int64_t C,
-                             int64_t H, int64_t W, int64_t k, float var_scale, int64_t items, hipStream_t s) {
+                             int64_t H, int64_t W, int64_t k, float var_scale, bool nchw, int64_t items,
+                             hipStream_t s) {
+  // the pooled side (c, d forward; a, b backward) is read or written lane by lane when NCHW
   const bool v4 = C % 4 == 0 && aligned16(a) && aligned16(b) && aligned16(J) && aligned16(c) && aligned16(d);
   const bool small = N * C * H * W < (1ll << 31);
   const unsigned blocks = ew_blocks(v4 ? items / 4 : items, 256);
   float* Jm = const_cast<float*>(J);
   if (small && v4)
     launch_pool_relu_as<FWD, uint32_t, 4>(a, b, Jm, c, d, (uint32_t)N, (uint32_t)C, (uint32_t)H, (uint32_t)W,
-                                          (uint32_t)k, var_scale, blocks, s);
+                                          (uint32_t)k, var_scale, nchw, blocks, s);
   else if (small)
     launch_pool_relu_as<FWD, uint32_t, 1>(a, b, Jm, c, d, (uint32_t)N, (uint32_t)C, (uint32_t)H, (uint32_t)W,
-                                          (uint32_t)k, var_scale, blocks, s);
+                                          (uint32_t)k, var_scale, nchw, blocks, s);
   else if (v4)
-    launch_pool_relu_as<FWD, int64_t, 4>(a, b, Jm, c, d, N, C, H, W, k, var_scale, blocks, s);
+    launch_pool_relu_as<FWD, int64_t, 4>(a, b, Jm, c, d, N, C, H, W, k, var_scale, nchw, blocks, s);
   else
-    launch_pool_relu_as<FWD, int64_t, 1>(a, b, Jm, c, d, N, C, H, W, k, var_scale, blocks, s);
+    launch_pool_relu_as<FWD, int64_t, 1>(a, b, Jm, c, d, N, C, H, W, k, var_scale, nchw, blocks, s);
 }
 
 extern "C" int tagi_relu_avgpool2d_fwd(const float* mz, const float* Sz, float* J, float* ma_out, float* Sa_out,
                                        int64_t N, int64_t C, int64_t H, int64_t W, int64_t k, float var_scale,
-                                       tagi_stream_t stream) {
+                                       int pooled_nchw, tagi_stream_t stream) {
   const char* what = "tagi_relu_avgpool2d_fwd";
   TAGI_REQUIRE(mz && Sz && J && ma_out && Sa_out, "%s: null pointer", what);
   TAGI_REQUIRE(N > 0 && C > 0 && H > 0 && W > 0 && k > 0 && H >= k && W >= k, "%s: bad sizes", what);
@@ -613,13 +657,13 @@ extern "C" int tagi_relu_avgpool2d_fwd(const float* mz, const float* Sz, float* 
   hipStream_t s = as_stream(stream);
   const int64_t out = N * C * (H / k) * (W / k);
   ProfScope ps(FAM_AVGPOOL, s, 0.0, 12.0 * N * C * H * W + 8.0 * out);
-  launch_pool_relu<true>(mz, Sz, J, ma_out, Sa_out, N, C, H, W, k, var_scale, out, s);
+  launch_pool_relu<true>(mz, Sz, J, ma_out, Sa_out, N, C, H, W, k, var_scale, pooled_nchw != 0, out, s);
   return check_launch(what);
 }
 
 extern "C" int tagi_avgpool2d_relu_bwd(const float* dm, const float* dS, const float* J, float* dm_out,
                                        float* dS_out, int64_t N, int64_t C, int64_t H, int64_t W, int64_t k,
-                                       float var_scale, tagi_stream_t stream) {
+                                       float var_scale, int pooled_nchw, tagi_stream_t stream) {
   const char* what = "tagi_avgpool2d_relu_bwd";
   TAGI_REQUIRE(dm && dS && J && dm_out && dS_out, "%s: null pointer", what);
   TAGI_REQUIRE(N > 0 && C > 0 && H > 0 && W > 0 && k > 0 && H >= k && W >= k, "%s: bad sizes", what);
@@ -629,7 +673,7 @@ extern "C" int tagi_avgpool2d_relu_bwd(const float* dm, const float* dS, const f
   hipStream_t s = as_stream(stream);
   const int64_t total = N * C * H * W;
   ProfScope ps(FAM_AVGPOOL, s, 0.0, 12.0 * total + 8.0 * N * C * (H / k) * (W / k));
-  launch_pool_relu<false>(dm, dS, J, dm_out, dS_out, N, C, H, W, k, var_scale, total, s);
+  launch_pool_relu<false>(dm, dS, J, dm_out, dS_out, N, C, H, W, k, var_scale, pooled_nchw != 0, total, s);
   return check_launch(what);
 }
 

@@ -106,8 +106,8 @@ _SIGS = {
     "tagi_add_inplace": (c_int, [P, P, P, P, I64, P]),
     "tagi_avgpool2d_fwd": (c_int, [P, P, P, P, I64, I64, I64, I64, I64, F, P]),
     "tagi_avgpool2d_bwd": (c_int, [P, P, P, P, I64, I64, I64, I64, I64, F, P]),
-    "tagi_relu_avgpool2d_fwd": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, F, P]),
-    "tagi_avgpool2d_relu_bwd": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, F, P]),
+    "tagi_relu_avgpool2d_fwd": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, F, c_int, P]),
+    "tagi_avgpool2d_relu_bwd": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, F, c_int, P]),
     "tagi_bn_stats": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, F, F, c_int, c_int, P, I64, P]),
     "tagi_bn_stats_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_bn_fwd": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, F, P]),

@@ -24,6 +24,8 @@ in how often activations cross HBM:
 * ReLU followed by AvgPool2D (relu.py:94-122, avgpool2d.py:38-90) is one pass that writes
   the ReLU Jacobian and the pooled moments, not the ReLU output; backward, the pooling's
   deltas and the Jacobian are one pass as well (when H and W are multiples of the window).
+  Before a Flatten the pooled moments are written row-major (N, C, H, W), so the Flatten
+  is a view each way instead of two layout copies.
 
 Every layer still ends up holding the state its own ``backward`` reads (ReLU.J,
 BatchNorm2D.m_hat and its normalisation variance, Conv2D.ma_in), so per-layer calls keep
@@ -41,6 +43,7 @@ from ._bn_pending import defer_bn_parameter_deltas  # noqa: F401  (re-exported)
 from .avgpool2d import AvgPool2D
 from .batchnorm2d import BatchNorm2D
 from .conv2d import Conv2D
+from .flatten import Flatten
 from .relu import ReLU
 from .resblock import ResBlock
 
@@ -314,34 +317,46 @@ def resblock_backward(block: ResBlock, delta_mu: Tensor, delta_var: Tensor, star
     return backward_chain(block._main_layers[:4], start[0], start[1], add=d_skip, fold=fold)
 
 
-def relu_avgpool_forward(relu: ReLU, pool: AvgPool2D, mz: Tensor, Sz: Tensor) -> tuple[Tensor, Tensor]:
+def relu_avgpool_forward(relu: ReLU, pool: AvgPool2D, mz: Tensor, Sz: Tensor,
+                         nchw: bool = False) -> tuple[Tensor, Tensor]:
     """pool.forward(*relu.forward(mz, Sz)) in one pass; stores relu.J and the pool's input
-    shape, as the two calls do."""
+    shape, as the two calls do. With ``nchw`` the pooled moments are row-major (N, C, H, W)
+    tensors, which a following Flatten reshapes without a copy; channels-last otherwise."""
     mz = _lib.check(_lib.channels_last(mz), "mz")
     Sz = _lib.check(_lib.like(Sz, mz), "Sz")
     N, C, H, W = mz.shape
     k = pool.k
     J = torch.empty_like(mz)
-    mo = _lib.empty_cl(N, C, H // k, W // k, mz.device)
-    So = _lib.empty_cl(N, C, H // k, W // k, mz.device)
+    if nchw:
+        mo = torch.empty((N, C, H // k, W // k), device=mz.device, dtype=torch.float32)
+        So = torch.empty_like(mo)
+    else:
+        mo = _lib.empty_cl(N, C, H // k, W // k, mz.device)
+        So = _lib.empty_cl(N, C, H // k, W // k, mz.device)
     _lib.call("tagi_relu_avgpool2d_fwd", mz.data_ptr(), Sz.data_ptr(), J.data_ptr(), mo.data_ptr(), So.data_ptr(),
-              N, C, H, W, k, pool._var_scale(), _lib.stream_of(mz))
+              N, C, H, W, k, pool._var_scale(), int(nchw), _lib.stream_of(mz))
     relu.J = J
     pool.input_shape = mz.shape
     return mo, So
 
 
 def avgpool_relu_backward(pool: AvgPool2D, relu: ReLU, delta_m: Tensor, delta_S: Tensor) -> tuple[Tensor, Tensor]:
-    """relu.backward(*pool.backward(delta_m, delta_S)) in one pass."""
+    """relu.backward(*pool.backward(delta_m, delta_S)) in one pass. Row-major pooled deltas
+    (what Flatten passes back) are read in place; any other layout goes through a
+    channels-last copy."""
     N, C, H, W = pool.input_shape
     k = pool.k
-    dm = _lib.check(_lib.channels_last(delta_m.reshape(N, C, H // k, W // k)), "delta_m")
-    dS = _lib.check(_lib.channels_last(delta_S.reshape(N, C, H // k, W // k)), "delta_S")
+    dm = delta_m.reshape(N, C, H // k, W // k)
+    dS = delta_S.reshape(N, C, H // k, W // k)
+    nchw = dm.is_contiguous() and dS.is_contiguous()
+    if not nchw:
+        dm, dS = _lib.channels_last(dm), _lib.channels_last(dS)
+    dm, dS = _lib.check(dm, "delta_m"), _lib.check(dS, "delta_S")
     J = _lib.check(_lib.channels_last(relu.J), "J")
     om = _lib.empty_cl(N, C, H, W, dm.device)
     oS = _lib.empty_cl(N, C, H, W, dm.device)
     _lib.call("tagi_avgpool2d_relu_bwd", dm.data_ptr(), dS.data_ptr(), J.data_ptr(), om.data_ptr(), oS.data_ptr(),
-              N, C, H, W, k, pool._var_scale(), _lib.stream_of(dm))
+              N, C, H, W, k, pool._var_scale(), int(nchw), _lib.stream_of(dm))
     return om, oS
 
 
@@ -392,7 +407,8 @@ def forward_chain(layers, mu: Tensor, var: Tensor,
                 add = None
             i += 2
         elif _fusable_relu_pool(layer, nxt, mu):
-            mu, var = relu_avgpool_forward(layer, nxt, mu, var)
+            # pooled moments in the row-major layout a following Flatten views as is
+            mu, var = relu_avgpool_forward(layer, nxt, mu, var, nchw=i + 2 < n and isinstance(layers[i + 2], Flatten))
             i += 2
         else:
             mu, var = layer.forward(mu, var)
