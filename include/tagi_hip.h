@@ -87,7 +87,9 @@ int tagi_probe_stream_variant(const float* src, float* dst, int64_t n, int64_t d
  *   mz = ma @ mw + mb
  *   Sz = ma^2 @ Sw + Sa @ (mw^2 + Sw) + Sb
  * ma, Sa (M,K); mw, Sw (K,N); mb, Sb (N) or NULL (no bias); mz, Sz (M,N).
- * mz may be NULL: then only Sz is produced (triton_fused_var_forward).
+ * mz may be NULL: then only Sz is produced (triton_fused_var_forward). Sa may be NULL for a
+ * deterministic input (the network input, whose variance the reference passes as zeros,
+ * network.py:92-114): the same values with two products instead of three.
  * Replaces linear.py:99-100 (torch.matmul + triton_fused_var_forward, common.py:170). */
 int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw,
                     const float* mb, const float* Sb, float* mz, float* Sz,
@@ -273,7 +275,8 @@ typedef struct {
 
 /* Implicit-GEMM forward: patches are gathered into LDS, never materialised.
  *   mz = P(ma) @ mw + mb ; Sz = P(ma)^2 @ Sw + P(Sa) @ (mw^2 + Sw) + Sb (channels-last).
- * mw, Sw (C*k*k, Cout) with rows ordered (c, kh, kw); mb, Sb (Cout).
+ * mw, Sw (C*k*k, Cout) with rows ordered (c, kh, kw); mb, Sb (Cout). Sa may be NULL for a
+ * deterministic input (zero variance, as the network input): two products instead of three.
  * Replaces Conv2D.forward (conv2d.py:254-309: im2col + matmul + fused var + permute). */
 int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw,
                     const float* mb, const float* Sb, float* mz, float* Sz,
@@ -284,8 +287,8 @@ int64_t tagi_conv2d_fwd_ws_bytes(const tagi_conv_geom* g);
  * (conv2d.py:254-309, relu.py:135-140, batchnorm2d.py:307-355): mz, Sz as tagi_conv2d_fwd,
  * then J, the batch statistics and the running-stat / gamma bookkeeping as
  * tagi_relu_bn_stats on (mz, Sz). Where the GEMM runs unsplit its epilogue forms J and
- * the per-tile channel sums, so the output is not read back. ws: 16-byte aligned, size
- * from tagi_conv2d_fwd_relu_bn_stats_ws_bytes. */
+ * the per-tile channel sums, so the output is not read back. Sa may be NULL as for
+ * tagi_conv2d_fwd. ws: 16-byte aligned, size from tagi_conv2d_fwd_relu_bn_stats_ws_bytes. */
 int tagi_conv2d_fwd_relu_bn_stats(const float* ma, const float* Sa, const float* mw, const float* Sw,
                                   const float* mb, const float* Sb, float* mz, float* Sz,
                                   const tagi_conv_geom* g, float* J, float* batch_mean,

@@ -326,7 +326,10 @@ def test_resnet18_b128_step_teacher_forced(dev, monkeypatch):
             tag = f"conv{nconv} {tuple(r['ma'].shape[1:])}->{conv.C_out}"
             nconv += 1
             learn.append((tag, conv))
-            x, xS = d64(r["ma"]), d64(r["Sa"])
+            x = d64(r["ma"])
+            # the network input reaches the stem without a variance tensor (zero variance)
+            assert (r["Sa"] is None) == (nconv == 1), "only the stem takes the zero-variance input"
+            xS = torch.zeros_like(x) if r["Sa"] is None else d64(r["Sa"])
             conv_in[id(conv)] = x
             # conv forward on whole images
             xi, xSi = x[IMAGES], xS[IMAGES]

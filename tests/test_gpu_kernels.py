@@ -775,3 +775,59 @@ def test_bmm_wrappers_strided(dev, transpose_a, transpose_b):
     rm4, rv4 = O.bmm_shared_left(d64(ma), d64(mb), d64(vb), 2.0)
     assert_scaled_close(m4, rm4, 2.0 * d64(ma).abs() @ d64(mb).abs(), RTOL, ATOL, "shared left mean")
     assert_scaled_close(v4, rv4, None, RTOL, ATOL, "shared left var")
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 784, 256), (128, 256, 10), (33, 70, 19), (4096, 512, 1024)])
+def test_linear_forward_zero_variance_input(dev, M, K, N):
+    """A deterministic input (Sa None, as Sequential passes the network input): the
+    two-product kernel against the float64 oracle with zero input variance, and against
+    the three-product kernel given explicit zeros (same terms; the plans may split the
+    reduction differently, so within fp32 rounding)."""
+    from triton_tagi_amd.kernels.common import linear_forward
+
+    r = g(M + K + N)
+    ma = torch.randn(M, K, generator=r)
+    mw, Sw = torch.randn(K, N, generator=r) / K**0.5, torch.rand(K, N, generator=r) / K
+    mb, Sb = torch.randn(1, N, generator=r), 1e-3 * torch.rand(1, N, generator=r)
+    mz, Sz = linear_forward(ma.to(dev), None, *(t.to(dev) for t in (mw, Sw, mb, Sb)))
+    rm, rS = O.linear_moments(d64(ma), torch.zeros(M, K, dtype=torch.float64), *(d64(t) for t in (mw, Sw, mb, Sb)))
+    assert_scaled_close(mz, rm, d64(ma).abs() @ d64(mw).abs() + d64(mb).abs(), RTOL, ATOL, "mz")
+    assert_scaled_close(Sz, rS, None, RTOL, ATOL, "Sz")
+    zm, zS = linear_forward(ma.to(dev), torch.zeros(M, K, device=dev), *(t.to(dev) for t in (mw, Sw, mb, Sb)))
+    assert_scaled_close(mz, d64(zm), d64(zm).abs() + 1.0, 1e-6, 1e-9, "mz vs explicit zeros")
+    assert_scaled_close(Sz, d64(zS), None, 1e-6, 1e-12, "Sz vs explicit zeros")
+
+
+@pytest.mark.parametrize("case", [(8, 3, 32, 32, 64, 3, 1, 1, 1), (4, 16, 12, 12, 32, 3, 1, 1, 1),
+                                  (4, 8, 9, 9, 16, 5, 2, 2, 1), (128, 3, 32, 32, 64, 3, 1, 1, 1)])
+def test_conv2d_forward_zero_variance_input(dev, case):
+    """Conv2D forward on a deterministic input (Sa None): against the oracle with zero input
+    variance and against the three-product kernel given explicit zeros; and the stem form
+    that also forms the ReLU -> BatchNorm2D statistics (fused.conv_relu_bn_forward)."""
+    from triton_tagi_amd.layers.batchnorm2d import BatchNorm2D
+    from triton_tagi_amd.layers.conv2d import Conv2D
+    from triton_tagi_amd.layers.fused import conv_relu_bn_forward
+    from triton_tagi_amd.layers.relu import ReLU
+
+    N, C, H, W, Cout, k, s, p, pt = case
+    torch.manual_seed(sum(case) + 3)
+    layer = Conv2D(C, Cout, k, stride=s, padding=p, padding_type=pt, device="cpu")
+    ref = O.mirror(layer)
+    for a in ("mw", "Sw", "mb", "Sb"):
+        setattr(layer, a, getattr(layer, a).to(dev))
+    ma = torch.randn(N, C, H, W, generator=g(sum(case)))
+    mz, Sz = layer.forward(ma.to(dev), None)
+    rm, rS = ref.forward(d64(ma), torch.zeros(N, C, H, W, dtype=torch.float64))
+    scale = (ref.patches.abs() @ ref.mw.abs() + ref.mb.abs()).view(N, *ref.spatial, Cout).permute(0, 3, 1, 2)
+    assert_scaled_close(mz, rm, scale, RTOL, ATOL, "conv mz")
+    assert_scaled_close(Sz, rS, None, RTOL, ATOL, "conv Sz")
+    zm, zS = layer.forward(ma.to(dev), torch.zeros(N, C, H, W, device=dev))
+    assert_scaled_close(mz, d64(zm), d64(zm).abs() + 1.0, 1e-6, 1e-9, "mz vs explicit zeros")
+    assert_scaled_close(Sz, d64(zS), None, 1e-6, 1e-12, "Sz vs explicit zeros")
+    if s == 1:
+        outs = []
+        for Sa in (None, torch.zeros(N, C, H, W, device=dev)):
+            bn = BatchNorm2D(Cout, device=dev)
+            outs.append(conv_relu_bn_forward(layer, ReLU(), bn, ma.to(dev), Sa) + (bn.running_mean.clone(),))
+        for j, (x, y) in enumerate(zip(*outs)):
+            assert_scaled_close(x, d64(y), d64(y).abs() + 1.0, 1e-5, 1e-9, f"stem form output {j}")

@@ -59,8 +59,11 @@ static int check_geom(const tagi_conv_geom* g, const char* what) {
   return TAGI_OK;
 }
 
-static Plan conv_fwd_plan(const tagi_conv_geom* g) {
-  return choose_plan(g->N * g->Ho * g->Wo, g->Cout, g->C * g->k * g->k, 1, PROD_FWD, true, 16);
+// zero_var: a deterministic input (Sa NULL), run as the shared-A product (mean ma mw,
+// variance ma^2 Sw; the Sa (mw^2 + Sw) terms it leaves out are exact zeros)
+static Plan conv_fwd_plan(const tagi_conv_geom* g, bool zero_var = false) {
+  return choose_plan(g->N * g->Ho * g->Wo, g->Cout, g->C * g->k * g->k, 1, zero_var ? PROD_SHARED_A : PROD_FWD, true,
+                     16);
 }
 
 // Largest row count (phase 0) and largest reduction over the stride phases of the
@@ -126,7 +129,9 @@ __global__ void zero2_kernel(float* __restrict__ a, float* __restrict__ b, int64
 // ====================================================================== forward
 extern "C" int64_t tagi_conv2d_fwd_ws_bytes(const tagi_conv_geom* g) {
   if (!g || g->N <= 0 || g->Cout <= 0 || g->Ho <= 0 || g->Wo <= 0 || g->C <= 0 || g->k <= 0) return 0;
-  return plan_ws_bytes(conv_fwd_plan(g), g->N * g->Ho * g->Wo, g->Cout, 1);
+  const int64_t a = plan_ws_bytes(conv_fwd_plan(g), g->N * g->Ho * g->Wo, g->Cout, 1);
+  const int64_t b = plan_ws_bytes(conv_fwd_plan(g, true), g->N * g->Ho * g->Wo, g->Cout, 1);
+  return a > b ? a : b;
 }
 
 // Forward GEMM; with st_J/st_ws set (and no split-K) the epilogue also forms the ReLU
@@ -135,7 +140,9 @@ static int conv_fwd_impl(const char* what, const float* ma, const float* Sa, con
                          const float* mb, const float* Sb, float* mz, float* Sz, const tagi_conv_geom* g,
                          const Plan& p, float* st_J, float* st_ws, float* ws, int64_t ws_bytes, hipStream_t s) {
   const int64_t R = g->N * g->Ho * g->Wo, C = g->Cout, K = g->C * g->k * g->k;
-  ProfScope ps(FAM_CONV_FWD, s, 2.0 * 3 * R * C * K, 4.0 * (2 * g->N * g->C * g->H * g->W + 2 * K * C + 2 * R * C));
+  const bool zero_var = Sa == nullptr;
+  ProfScope ps(FAM_CONV_FWD, s, 2.0 * (zero_var ? 2 : 3) * R * C * K,
+               4.0 * ((zero_var ? 1 : 2) * g->N * g->C * g->H * g->W + 2 * K * C + 2 * R * C));
   GemmArgs a{};
   a.a = conv_operand(ma, Sa, g, R, K, g->N * g->C * g->H * g->W);
   a.b = conv_operand(mw, Sw, g, C, K, K * g->Cout);
@@ -149,8 +156,15 @@ static int conv_fwd_impl(const char* what, const float* ma, const float* Sa, con
   a.R = (int)R;
   a.C = (int)C;
   a.Kred = (int)K;
-  const bool va = g->C % 4 == 0 && al16(ma) && al16(Sa);
+  const bool va = g->C % 4 == 0 && al16(ma) && (zero_var || al16(Sa));
   const bool vb = g->Cout % 4 == 0 && al16(mw) && al16(Sw);
+  if (zero_var) {
+    if (va && vb && g->C % 16 == 0 && g->k <= 5)
+      return run_gemm<PROD_SHARED_A, LD_CFWD_A4T, LD_CFWD_B4T>(a, 1, p, ws, ws_bytes, s, what);
+    if (va && vb) return run_gemm<PROD_SHARED_A, LD_CFWD_A4, LD_CFWD_B4>(a, 1, p, ws, ws_bytes, s, what);
+    if (vb) return run_gemm<PROD_SHARED_A, LD_CFWD_A_S, LD_CFWD_B4>(a, 1, p, ws, ws_bytes, s, what);
+    return run_gemm<PROD_SHARED_A, LD_CFWD_A_S, LD_CFWD_B_S>(a, 1, p, ws, ws_bytes, s, what);
+  }
   // 16 channels per k tile and at most 25 taps: the tile-aligned loaders
   if (va && vb && g->C % 16 == 0 && g->k <= 5)
     return run_gemm<PROD_FWD, LD_CFWD_A4T, LD_CFWD_B4T>(a, 1, p, ws, ws_bytes, s, what);
@@ -165,10 +179,11 @@ extern "C" int tagi_conv2d_fwd(const float* ma, const float* Sa, const float* mw
   const char* what = "tagi_conv2d_fwd";
   int rc = check_geom(g, what);
   if (rc) return rc;
-  TAGI_REQUIRE(ma && Sa && mw && Sw && mz && Sz, "%s: null pointer", what);
+  TAGI_REQUIRE(ma && mw && Sw && mz && Sz, "%s: null pointer", what);
   const int64_t R = g->N * g->Ho * g->Wo, C = g->Cout, K = g->C * g->k * g->k;
-  Plan p = conv_fwd_plan(g);
-  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, R, C, 1))) p = choose_plan(R, C, K, 1, PROD_FWD, false, 1);
+  Plan p = conv_fwd_plan(g, Sa == nullptr);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, R, C, 1)))
+    p = choose_plan(R, C, K, 1, Sa ? PROD_FWD : PROD_SHARED_A, false, 1);
   return conv_fwd_impl(what, ma, Sa, mw, Sw, mb, Sb, mz, Sz, g, p, nullptr, nullptr, ws, ws_bytes,
                        as_stream(stream));
 }
@@ -181,11 +196,15 @@ static int64_t fwd_stats_floats(const tagi_conv_geom* g, const Plan& p) {
   return (int64_t)p.tiles_m * C * 3;
 }
 
-extern "C" int64_t tagi_conv2d_fwd_relu_bn_stats_ws_bytes(const tagi_conv_geom* g) {
-  if (!g || g->N <= 0 || g->Cout <= 0 || g->Ho <= 0 || g->Wo <= 0 || g->C <= 0 || g->k <= 0) return 0;
-  const Plan p = conv_fwd_plan(g);
+static int64_t fwd_stats_ws_bytes(const tagi_conv_geom* g, const Plan& p) {
   const int64_t conv = plan_ws_bytes(p, g->N * g->Ho * g->Wo, g->Cout, 1);
   return (conv + 255) / 256 * 256 + fwd_stats_floats(g, p) * (int64_t)sizeof(float);
+}
+
+extern "C" int64_t tagi_conv2d_fwd_relu_bn_stats_ws_bytes(const tagi_conv_geom* g) {
+  if (!g || g->N <= 0 || g->Cout <= 0 || g->Ho <= 0 || g->Wo <= 0 || g->C <= 0 || g->k <= 0) return 0;
+  const int64_t a = fwd_stats_ws_bytes(g, conv_fwd_plan(g)), b = fwd_stats_ws_bytes(g, conv_fwd_plan(g, true));
+  return a > b ? a : b;
 }
 
 extern "C" int tagi_conv2d_fwd_relu_bn_stats(const float* ma, const float* Sa, const float* mw, const float* Sw,
@@ -197,14 +216,14 @@ extern "C" int tagi_conv2d_fwd_relu_bn_stats(const float* ma, const float* Sa, c
   const char* what = "tagi_conv2d_fwd_relu_bn_stats";
   int rc = check_geom(g, what);
   if (rc) return rc;
-  TAGI_REQUIRE(ma && Sa && mw && Sw && mz && Sz && J && batch_mean && batch_var, "%s: null pointer", what);
+  TAGI_REQUIRE(ma && mw && Sw && mz && Sz && J && batch_mean && batch_var, "%s: null pointer", what);
   const int64_t R = g->N * g->Ho * g->Wo, C = g->Cout;
   TAGI_REQUIRE(R > 1, "%s: BatchNorm2D needs more than one value per channel", what);
   TAGI_REQUIRE(ws && ws_bytes >= tagi_conv2d_fwd_relu_bn_stats_ws_bytes(g) && al16(ws),
                "%s: workspace of %lld bytes (16-byte aligned) needed", what,
                (long long)tagi_conv2d_fwd_relu_bn_stats_ws_bytes(g));
   hipStream_t s = as_stream(stream);
-  const Plan p = conv_fwd_plan(g);
+  const Plan p = conv_fwd_plan(g, Sa == nullptr);
   const int64_t conv = (plan_ws_bytes(p, R, C, 1) + 255) / 256 * 256;
   float* sws = ws + conv / (int64_t)sizeof(float);
   const int64_t sbytes = ws_bytes - conv;

@@ -1918,6 +1918,9 @@ static inline int64_t plan_ws_bytes(const Plan& p, int64_t R, int64_t C, int64_t
   X(PROD_SHARED_B, LD_STR_MN_S, LD_STR_MN_S) X(PROD_SHARED_B, LD_STR_K4, LD_STR_MN4)     \
   X(PROD_SHARED_B, LD_STR_MN4, LD_STR_K4) X(PROD_SHARED_B, LD_STR_MN4, LD_STR_MN4)
 #define TAGI_GEMM_COMBOS_SHARED_A(X)                                                     \
+  X(PROD_SHARED_A, LD_CFWD_A4T, LD_CFWD_B4T)                                             \
+  X(PROD_SHARED_A, LD_CFWD_A4, LD_CFWD_B4) X(PROD_SHARED_A, LD_CFWD_A_S, LD_CFWD_B4)     \
+  X(PROD_SHARED_A, LD_CFWD_A_S, LD_CFWD_B_S)                                             \
   X(PROD_SHARED_A, LD_CWG_A4T, LD_STR_MN4)                                               \
   X(PROD_SHARED_A, LD_CWG_A4, LD_STR_MN4) X(PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN4)       \
   X(PROD_SHARED_A, LD_CWG_A_S, LD_STR_MN_S)                                              \

@@ -9,9 +9,15 @@ Plan tagi::linear_fwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan
 static Plan linear_bwd_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, K, N, 1, PROD_SHARED_B, true, 16); }
 static Plan linear_wgrad_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(K + 1, N, M, 1, PROD_SHARED_A, true, 512); }
 
+// A deterministic input (no variance, Sa NULL): mean = ma mw, variance = ma^2 Sw, the
+// shared-A product (two MFMAs per k-step instead of three; the terms Sa (mw^2 + Sw) it
+// leaves out are exact zeros)
+static Plan linear_fwd0_plan(int64_t M, int64_t K, int64_t N) { return choose_plan(M, N, K, 1, PROD_SHARED_A, true, 16); }
+
 extern "C" int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N) {
   if (M <= 0 || K <= 0 || N <= 0) return 0;
-  return plan_ws_bytes(linear_fwd_plan(M, K, N), M, N, 1);
+  const int64_t a = plan_ws_bytes(linear_fwd_plan(M, K, N), M, N, 1), b = plan_ws_bytes(linear_fwd0_plan(M, K, N), M, N, 1);
+  return a > b ? a : b;
 }
 
 int tagi::linear_fwd_check(const char* what, const float* ma, const float* Sa, const float* mw, const float* Sw,
@@ -39,10 +45,34 @@ int tagi::linear_fwd_run(const char* what, const float* ma, const float* Sa, con
   return run_gemm<PROD_FWD, LD_STR_K_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
 }
 
+static int linear_fwd0(const char* what, const float* ma, const float* mw, const float* Sw, const float* mb,
+                       const float* Sb, float* mz, float* Sz, int64_t M, int64_t K, int64_t N, float* ws,
+                       int64_t ws_bytes, hipStream_t s) {
+  TAGI_REQUIRE(ma && mw && Sw && Sz, "%s: null pointer", what);
+  TAGI_REQUIRE(M > 0 && K > 0 && N > 0, "%s: sizes must be positive (M=%lld K=%lld N=%lld)", what, (long long)M,
+               (long long)K, (long long)N);
+  TAGI_REQUIRE(fits_i32(M * K) && fits_i32(K * N) && fits_i32(M * N), "%s: too large for 32-bit tiles", what);
+  Plan p = linear_fwd0_plan(M, K, N);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, N, 1)))
+    p = choose_plan(M, N, K, 1, PROD_SHARED_A, false, 1);
+  ProfScope ps(FAM_LINEAR_FWD, s, 2.0 * 2 * M * K * N, 4.0 * (M * K + 2 * K * N + 2 * M * N));
+  GemmArgs g{};
+  g.a = strided_operand(ma, nullptr, 1, 0, 0, K, 1, M, K);
+  g.b = strided_operand(mw, Sw, 1, 0, 0, 1, N, N, K);
+  g.epi = epi_store(mz, Sz, mb, Sb, 0, 1, 1.f, 1.f, 1, 0, 0, N, 1);
+  g.R = (int)M;
+  g.C = (int)N;
+  g.Kred = (int)K;
+  const bool v4 = K % 4 == 0 && N % 4 == 0 && al16(ma) && al16(mw) && al16(Sw);
+  if (v4) return run_gemm<PROD_SHARED_A, LD_STR_K4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
+  return run_gemm<PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
+}
+
 extern "C" int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw, const float* mb,
                                const float* Sb, float* mz, float* Sz, int64_t M, int64_t K, int64_t N, float* ws,
                                int64_t ws_bytes, tagi_stream_t stream) {
   const char* what = "tagi_linear_fwd";
+  if (!Sa) return linear_fwd0(what, ma, mw, Sw, mb, Sb, mz, Sz, M, K, N, ws, ws_bytes, as_stream(stream));
   int rc = linear_fwd_check(what, ma, Sa, mw, Sw, Sz, M, K, N);
   if (rc != TAGI_OK) return rc;
   Plan p = linear_fwd_plan(M, K, N);

@@ -23,11 +23,14 @@ def _2d(t, name):
 
 
 def linear_forward(ma, Sa, mw, Sw, mb=None, Sb=None, need_mean=True):
-    """Fused mean and variance of z = a W + b (linear.py:99-100)."""
-    _2d(ma, "ma"), _2d(Sa, "Sa"), _2d(mw, "mw"), _2d(Sw, "Sw")
+    """Fused mean and variance of z = a W + b (linear.py:99-100). Sa None: a deterministic
+    input (the network's), the same values as zeros with one product fewer."""
+    _2d(ma, "ma"), _2d(mw, "mw"), _2d(Sw, "Sw")
+    if Sa is not None:
+        _2d(Sa, "Sa")
     M, K = ma.shape
     K2, N = mw.shape
-    if K2 != K or Sa.shape != ma.shape or Sw.shape != mw.shape:
+    if K2 != K or (Sa is not None and Sa.shape != ma.shape) or Sw.shape != mw.shape:
         raise ValueError(f"linear_forward: shapes ma {tuple(ma.shape)} mw {tuple(mw.shape)} disagree")
     for t, n in ((mb, "mb"), (Sb, "Sb")):
         if t is not None:
@@ -38,7 +41,7 @@ def linear_forward(ma, Sa, mw, Sw, mb=None, Sb=None, need_mean=True):
     Sz = torch.empty(M, N, device=ma.device, dtype=torch.float32)
     ws = _lib.workspace(_lib.query("tagi_linear_fwd_ws_bytes", M, K, N), ma.device)
     wp, wb = _lib.ws_args(ws)
-    _lib.call("tagi_linear_fwd", ma.data_ptr(), Sa.data_ptr(), mw.data_ptr(), Sw.data_ptr(), _lib.ptr(mb),
+    _lib.call("tagi_linear_fwd", ma.data_ptr(), _lib.ptr(Sa), mw.data_ptr(), Sw.data_ptr(), _lib.ptr(mb),
               _lib.ptr(Sb), _lib.ptr(mz), Sz.data_ptr(), M, K, N, wp, wb, _lib.stream_of(ma))
     return mz, Sz
 

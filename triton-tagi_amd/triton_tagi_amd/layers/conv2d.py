@@ -61,7 +61,7 @@ class Conv2D(LearnableLayer):
         ma, Sa, mz, Sz, g = self._forward_prepare(ma, Sa)
         ws = _lib.workspace(_lib.query("tagi_conv2d_fwd_ws_bytes", g), mz.device)
         wp, wb = _lib.ws_args(ws)
-        _lib.call("tagi_conv2d_fwd", ma.data_ptr(), Sa.data_ptr(), self.mw.data_ptr(), self.Sw.data_ptr(),
+        _lib.call("tagi_conv2d_fwd", ma.data_ptr(), _lib.ptr(Sa), self.mw.data_ptr(), self.Sw.data_ptr(),
                   self.mb.data_ptr(), self.Sb.data_ptr(), mz.data_ptr(), Sz.data_ptr(), g, wp, wb,
                   _lib.stream_of(mz))
         return mz, Sz
@@ -70,13 +70,14 @@ class Conv2D(LearnableLayer):
         """Checks the input, records what backward needs and allocates the output moments.
 
         Returns (ma, Sa, mz, Sz, geometry) with the inputs channels-last; the caller
-        launches the forward."""
+        launches the forward. Sa None: a deterministic input (zero variance), passed on."""
         if ma.dim() != 4 or ma.shape[1] != self.C_in:
             raise ValueError(f"Conv2D: expected (N, {self.C_in}, H, W), got {tuple(ma.shape)}")
         ma = _lib.check(_lib.channels_last(ma), "ma")
-        Sa = _lib.check(_lib.channels_last(Sa), "Sa")
-        if Sa.shape != ma.shape:
-            raise ValueError(f"Conv2D: Sa {tuple(Sa.shape)} does not match ma {tuple(ma.shape)}")
+        if Sa is not None:
+            Sa = _lib.check(_lib.channels_last(Sa), "Sa")
+            if Sa.shape != ma.shape:
+                raise ValueError(f"Conv2D: Sa {tuple(Sa.shape)} does not match ma {tuple(ma.shape)}")
         N, C, H, W = ma.shape
         self.input_shape = (N, C, H, W)
         g = self._geom(N, C, H, W)

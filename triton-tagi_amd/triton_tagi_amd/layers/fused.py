@@ -98,7 +98,7 @@ def conv_relu_bn_forward(conv: Conv2D, relu: ReLU, bn: BatchNorm2D, ma: Tensor, 
     first = not bn._is_initialized
     ws = _lib.workspace(_lib.query("tagi_conv2d_fwd_relu_bn_stats_ws_bytes", geom), dev)
     wp, wb = _lib.ws_args(ws)
-    _lib.call("tagi_conv2d_fwd_relu_bn_stats", ma.data_ptr(), Sa.data_ptr(), conv.mw.data_ptr(),
+    _lib.call("tagi_conv2d_fwd_relu_bn_stats", ma.data_ptr(), _lib.ptr(Sa), conv.mw.data_ptr(),
               conv.Sw.data_ptr(), conv.mb.data_ptr(), conv.Sb.data_ptr(), mz.data_ptr(), Sz.data_ptr(), geom,
               J.data_ptr(), bmean.data_ptr(), bvar.data_ptr(), *tail, float(bn.momentum), float(bn.eps), int(first),
               int(bn.preserve_var), wp, wb, _lib.stream_of(mz))

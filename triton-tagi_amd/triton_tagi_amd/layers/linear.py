@@ -52,7 +52,8 @@ class Linear(LearnableLayer):
     def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
         self._input_shape = ma.shape
         ma_flat = ma.reshape(-1, self.in_features).contiguous()
-        Sa_flat = Sa.reshape(-1, self.in_features).contiguous()
+        # Sa None: a deterministic input (zero variance), which the kernel takes as such
+        Sa_flat = None if Sa is None else Sa.reshape(-1, self.in_features).contiguous()
         self.ma_in = ma_flat
         mz, Sz = linear_forward(ma_flat, Sa_flat, _dense(self.mw), _dense(self.Sw), _dense(self.mb),
                                 _dense(self.Sb))

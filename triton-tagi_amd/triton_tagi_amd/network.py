@@ -18,6 +18,7 @@ from . import _overlap
 from .base import Layer, LearnableLayer
 from .layers.conv2d import Conv2D
 from .layers.embedding import Embedding
+from .layers.linear import Linear
 from .layers.fused import backward_chain, defer_bn_parameter_deltas, forward_chain
 from .layers.multihead_attention import MultiheadAttentionV2
 from .update.observation import compute_innovation, hrc_innovation
@@ -63,12 +64,15 @@ class Sequential:
         for layer in self.layers:
             if not isinstance(layer, Layer):
                 raise TypeError(f"Unknown layer type: {type(layer)}")
-        if x.dim() == 4 and self.layers and isinstance(self.layers[0], Conv2D):
-            # the conv path keeps activations channels-last: start both moments that way
+        first = self.layers[0] if self.layers else None
+        if x.dim() == 4 and isinstance(first, Conv2D):
+            # the conv path keeps activations channels-last
             x = x.contiguous(memory_format=torch.channels_last)
-            Sa = torch.zeros_like(x, memory_format=torch.channels_last)
-        elif self.layers and isinstance(self.layers[0], Embedding):
-            Sa = None  # token ids: the embedding reads no input variance
+        if isinstance(first, (Conv2D, Linear, Embedding)):
+            # the input's variance is zero: a Conv2D or Linear first layer then forms the
+            # variance of its output from the weight variances alone (the same values),
+            # and the Embedding reads token ids
+            Sa = None
         else:
             Sa = torch.zeros_like(x)
         return forward_chain(self.layers, x, Sa)
