@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define TAGI_ABI_VERSION 4
+#define TAGI_ABI_VERSION 5
 
 enum {
   TAGI_OK = 0,
@@ -97,6 +97,16 @@ int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw, const flo
                     tagi_stream_t stream);
 int64_t tagi_linear_fwd_ws_bytes(int64_t M, int64_t K, int64_t N);
 
+/* tagi_linear_fwd followed by a ReLU, in one launch: ma_out, Sa_out and J (M,N) receive
+ * the moments of ReLU(z) and its Jacobian in place of z's moments, which are not stored;
+ * the same bits as tagi_linear_fwd then tagi_relu_fwd. Sa may be NULL as in
+ * tagi_linear_fwd. The workspace query is tagi_linear_fwd_ws_bytes. Replaces
+ * Linear.forward followed by ReLU.forward (linear.py:83-103, relu.py:94-122). */
+int tagi_linear_fwd_relu(const float* ma, const float* Sa, const float* mw, const float* Sw,
+                         const float* mb, const float* Sb, float* ma_out, float* Sa_out, float* J,
+                         int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes,
+                         tagi_stream_t stream);
+
 /* Bytes of the fixed device scratch behind tagi_linear_fwd_noalloc, per GPU. */
 #define TAGI_LINEAR_FWD_NOALLOC_SCRATCH_BYTES (128ll << 20)
 
@@ -123,6 +133,17 @@ int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const float* mw,
                           float* dma, float* dSa, int64_t M, int64_t K, int64_t N,
                           float* ws, int64_t ws_bytes, tagi_stream_t stream);
 int64_t tagi_linear_bwd_delta_ws_bytes(int64_t M, int64_t K, int64_t N);
+
+/* tagi_linear_bwd_delta with the Jacobian of the elementwise layer in front (a ReLU's J,
+ * laid out like dma) applied in the epilogue: dma = (dmz @ mw^T) * J and
+ * dSa = (dSz @ (mw^2)^T) * J^2, the deltas at that layer's input. Equal to
+ * tagi_linear_bwd_delta then tagi_jacobian_bwd up to the rounding of the variance's J^2
+ * (v * (J * J) here, (v * J) * J there). The workspace query is
+ * tagi_linear_bwd_delta_ws_bytes. Replaces triton_fused_backward_delta followed by
+ * ReLU.backward (common.py:287, relu.py:152-169). */
+int tagi_linear_bwd_delta_jacobian(const float* dmz, const float* dSz, const float* mw, const float* J,
+                                   float* dma, float* dSa, int64_t M, int64_t K, int64_t N,
+                                   float* ws, int64_t ws_bytes, tagi_stream_t stream);
 
 /* tagi_linear_bwd_delta plus an addend in the epilogue: dma = dmz @ mw^T + add_m,
  * dSa = dSz @ (mw^2)^T + add_S (add_* laid out like dma; they may alias dma/dSa, each

@@ -46,7 +46,7 @@ def test_abi_version_and_error_channel():
     from triton_tagi_amd import _lib
 
     lib = _lib.load()
-    assert lib.tagi_abi_version() == 4
+    assert lib.tagi_abi_version() == 5
     # argument errors are reported without touching the GPU
     rc = lib.tagi_linear_fwd(None, None, None, None, None, None, None, None, 1, 1, 1, None, 0, None)
     assert rc == 1

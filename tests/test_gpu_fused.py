@@ -509,3 +509,110 @@ def test_relu_avgpool_fused(dev, N, C, H, W, k, sc, nchw):
     qm, qS = orelu.backward(*opool.backward(d64(dm), d64(dS)))
     assert_scaled_close(om, qm, None, RTOL, ATOL, "input delta mean vs oracle")
     assert_scaled_close(oS, qS, None, RTOL, ATOL, "input delta var vs oracle")
+
+
+LIN_RELU_CASES = [(256, 784, 256), (256, 256, 128), (300, 70, 45), (33, 2000, 45), (4096, 1024, 1024),
+                  (1024, 512, 513)]
+
+
+@pytest.mark.parametrize("zero_var", [False, True])
+@pytest.mark.parametrize("M,K,N", LIN_RELU_CASES, ids=[str(c) for c in LIN_RELU_CASES])
+def test_linear_relu_forward_fused(dev, M, K, N, zero_var):
+    """Linear -> ReLU as one launch (tagi_linear_fwd_relu) against the two layers' own calls,
+    bit for bit, and against the float64 oracle. The shapes take unsplit plans (vector and
+    scalar loaders) and split-K plans whose reduction applies the ReLU (vector and scalar
+    reduction paths); ``zero_var``: the deterministic-input product (Sa NULL)."""
+    from triton_tagi_amd.kernels.common import linear_forward, linear_relu_forward
+    from triton_tagi_amd.layers.relu import bayesian_relu
+
+    r = g(M + K + N + zero_var)
+    ma = torch.randn(M, K, generator=r)
+    Sa = None if zero_var else 0.5 * torch.rand(M, K, generator=r)
+    mw = torch.randn(K, N, generator=r) / K ** 0.5
+    Sw = torch.rand(K, N, generator=r) / K
+    mb, Sb = 0.1 * torch.randn(N, generator=r), 0.01 * torch.rand(N, generator=r)
+    mb[:3] = torch.tensor([-40.0, 25.0, 0.0])  # both tails of the rectified moments
+    on = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    args = (ma.to(dev), on(Sa), mw.to(dev), Sw.to(dev), mb.to(dev), Sb.to(dev))
+    am, aS, J = linear_relu_forward(*args)
+    um, uS, uJ = bayesian_relu(*linear_forward(*args))
+    assert torch.equal(am, um) and torch.equal(aS, uS) and torch.equal(J, uJ), "differs from the separate passes"
+    Sa64 = torch.zeros(M, K, dtype=torch.float64) if zero_var else d64(Sa)
+    rmz, rSz = O.linear_moments(d64(ma), Sa64, d64(mw), d64(Sw), d64(mb), d64(Sb))
+    orelu = O.OReLU()
+    rm, rS = orelu.forward(rmz, rSz)
+    # first-order error of the product's mean (relative to its absolute terms T) carried
+    # through the ReLU: d mu_a / d mu_z = J <= 1, d S_a / d mu_z = 2 mu_a (1 - J)
+    T = d64(ma).abs() @ d64(mw).abs() + d64(mb).abs()
+    assert_scaled_close(am, rm, T + rm.abs(), RTOL, ATOL, "ReLU mean vs oracle")
+    assert_scaled_close(aS, rS, rS + 2 * rm.abs() * T, RTOL, ATOL, "ReLU var vs oracle")
+    assert_scaled_close(J, orelu.J, None, RTOL, ATOL, "ReLU Jacobian vs oracle")
+
+
+LIN_JAC_CASES = [(256, 784, 256), (300, 70, 45), (1024, 512, 513), (4096, 1024, 1024), (128, 1024, 256)]
+
+
+@pytest.mark.parametrize("M,K,N", LIN_JAC_CASES, ids=[str(c) for c in LIN_JAC_CASES])
+def test_linear_bwd_delta_jacobian(dev, M, K, N):
+    """Input deltas times the ReLU Jacobian in the product's epilogue
+    (tagi_linear_bwd_delta_jacobian) against the product followed by tagi_jacobian_bwd (the
+    variance within one rounding of J^2) and against the float64 oracle."""
+    from triton_tagi_amd.kernels.common import fused_backward_delta
+    from triton_tagi_amd.layers.relu import jacobian_backward
+
+    r = g(M + 2 * K + N)
+    dmz, dSz = 0.1 * torch.randn(M, N, generator=r), -1e-2 * torch.rand(M, N, generator=r)
+    mw = torch.randn(K, N, generator=r) / N ** 0.5
+    J = torch.rand(M, K, generator=r)
+    J[0, :3] = torch.tensor([0.0, 1.0, 1e-20])
+    om, oS = fused_backward_delta(dmz.to(dev), dSz.to(dev), mw.to(dev), jacobian=J.to(dev))
+    um, uS = jacobian_backward(*fused_backward_delta(dmz.to(dev), dSz.to(dev), mw.to(dev)), J.to(dev))
+    assert torch.equal(om, um), "mean differs from the separate passes"
+    close_unfused(oS, uS, "variance")
+    orelu = O.OReLU()
+    orelu.J = d64(J)
+    rm, rS = orelu.backward(*O.linear_backward_delta(d64(dmz), d64(dSz), d64(mw)))
+    assert_scaled_close(om, rm, (d64(dmz).abs() @ d64(mw).abs().T) * d64(J), RTOL, ATOL, "dma * J vs oracle")
+    assert_scaled_close(oS, rS, None, RTOL, ATOL, "dSa * J^2 vs oracle")
+
+
+def test_linear_relu_folds_taken_in_step(dev, monkeypatch):
+    """In the MLP step (784-256-128-10) both Linear -> ReLU pairs run as one forward launch
+    and one input-delta launch each; no ReLU runs its own passes, and the step still
+    matches the oracle's."""
+    from triton_tagi_amd import workloads
+    from triton_tagi_amd.layers.linear import Linear
+    from triton_tagi_amd.layers.relu import ReLU
+
+    w = workloads.build("mlp", device="cuda:0", batch=64)
+    onet = O.mirror_net(w.net)
+    calls = {"fwd": 0, "bwd": 0}
+    fr, bj = Linear.forward_relu, Linear.backward_jacobian
+
+    def fwd(self, *a, **k):
+        calls["fwd"] += 1
+        return fr(self, *a, **k)
+
+    def bwd(self, *a, **k):
+        calls["bwd"] += 1
+        return bj(self, *a, **k)
+
+    def forbid(*a, **k):
+        raise AssertionError("a ReLU ran its own pass")
+
+    monkeypatch.setattr(Linear, "forward_relu", fwd)
+    monkeypatch.setattr(Linear, "backward_jacobian", bwd)
+    monkeypatch.setattr(ReLU, "forward", forbid)
+    monkeypatch.setattr(ReLU, "backward", forbid)
+    mu, var = w.net.step(w.x, w.y, w.sigma_v)
+    torch.cuda.synchronize()
+    assert calls == {"fwd": 2, "bwd": 2}
+    rmu, rvar = onet.step(w.x.cpu().double(), w.y.cpu().double(), w.sigma_v)
+    assert_scaled_close(mu, rmu, rmu.abs() + rmu.abs().mean(), RTOL, ATOL, "predicted mean")
+    assert_scaled_close(var, rvar, None, RTOL, ATOL, "predicted var")
+    for layer, olayer in zip(w.net.layers, onet.layers):
+        if isinstance(layer, Linear):
+            for (m, S, _, _), (o, mn, Sn, _, _) in zip(layer._update_items(), olayer.param_groups()):
+                rm_, rS_ = getattr(o, mn), getattr(o, Sn)
+                assert_scaled_close(m, rm_, rm_.abs() + rm_.abs().mean(), RTOL, ATOL, "updated mean")
+                assert_scaled_close(S, rS_, None, RTOL, ATOL, "updated variance")

@@ -218,6 +218,10 @@ struct Epi {
   // outputs go to bn_om/bn_ov
   float* bn_om;
   float* bn_ov;
+  // kind 0 (EPI 4 in the GEMM kernel, and the split-K reduction): the outputs are the
+  // moments of ReLU(product) instead -- om the mean, ov the variance, relu_J the ReLU
+  // Jacobian, all laid out like the output (the product's own moments are not stored)
+  float* relu_J;
 };
 
 struct GemmArgs {
@@ -696,8 +700,16 @@ __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col,
       rm += e.am[off];
       rv += e.av[off];
     }
-    if (e.om) e.om[off] = rm;
-    e.ov[off] = rv;
+    if (e.relu_J) {
+      float ra, rS, rJ;
+      relu_moments(rm, rv, ra, rS, rJ);
+      e.om[off] = ra;
+      e.ov[off] = rS;
+      e.relu_J[off] = rJ;
+    } else {
+      if (e.om) e.om[off] = rm;
+      e.ov[off] = rv;
+    }
   } else if (e.kind == 1) {
     if (row < e.wrows) {
       int wr = row;
@@ -817,6 +829,7 @@ __device__ __forceinline__ bool epi_apply4(const Epi& e, int z, int row, int col
     const int64_t off = (z / e.zdiv) * e.sz1 + (z % e.zdiv) * e.sz2 + (int64_t)row * e.srow + col;
     uintptr_t al = (uintptr_t)(e.ov + off);
     if (e.om) al |= (uintptr_t)(e.om + off);
+    if (e.relu_J) al |= (uintptr_t)(e.relu_J + off);
     if (al & 15u) return false;
     float rm[4], rv[4];
 #pragma unroll
@@ -824,6 +837,12 @@ __device__ __forceinline__ bool epi_apply4(const Epi& e, int z, int row, int col
       const int64_t bi = (int64_t)row * e.b_sr + (int64_t)(col + j) * e.b_sc;
       rm[j] = m[j] * e.sm + (e.bm ? e.bm[bi] : 0.f);
       rv[j] = v[j] * e.sv + (e.bv ? e.bv[bi] : 0.f);
+    }
+    if (e.relu_J) {
+      float rJ[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) relu_moments(rm[j], rv[j], rm[j], rv[j], rJ[j]);
+      *reinterpret_cast<float4*>(e.relu_J + off) = make_float4(rJ[0], rJ[1], rJ[2], rJ[3]);
     }
     if (e.om) *reinterpret_cast<float4*>(e.om + off) = make_float4(rm[0], rm[1], rm[2], rm[3]);
     *reinterpret_cast<float4*>(e.ov + off) = make_float4(rv[0], rv[1], rv[2], rv[3]);
@@ -847,8 +866,9 @@ __device__ __forceinline__ int kred_of(const GemmArgs& g, int z) {
 
 // EPI 1: the kind-2 epilogue with the BatchNorm2D -> ReLU backward folded in; EPI 2: the
 // kind-1 epilogue with the capped parameter update applied in place; EPI 3: EPI 1 applied
-// to product + addend, storing both (separate instantiations: their extra registers would
-// otherwise cost every kernel occupancy)
+// to product + addend, storing both; EPI 4: the kind-0 plain store of ReLU(product)'s
+// moments and Jacobian (separate instantiations: their extra registers would otherwise
+// cost every kernel occupancy)
 // (the folded BatchNorm2D epilogues keep 4 waves per SIMD: their prefetched operands would
 // otherwise take the register count just past the 128 that allows it)
 template <int PROD, class CFG, int KA, int KB, int EPI = 0>
@@ -1262,6 +1282,14 @@ __global__ void __launch_bounds__(CFG::NTH, ((EPI == 1 || EPI == 3) && CFG::NTH 
             if (e.am) {
               m += PRE ? av0[v] : e.am[off];
               vv += PRE ? av1[v] : e.av[off];
+            }
+            if constexpr (EPI == 4) {
+              float ra, rS, rJ;
+              relu_moments(m, vv, ra, rS, rJ);
+              e.om[off] = ra;
+              e.ov[off] = rS;
+              e.relu_J[off] = rJ;
+              continue;
             }
             if (e.om) e.om[off] = m;
             e.ov[off] = vv;
@@ -1937,6 +1965,12 @@ static inline bool bnf_cfg(int cfg) { return cfg == 3 || cfg == 4 || cfg == 5; }
 // every tile config
 #define TAGI_GEMM_COMBOS_SHARED_A_UPD(X)                                                 \
   X(PROD_SHARED_A, LD_STR_MN4, LD_STR_MN4) X(PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S)
+// The Linear forward loader pairs that also store ReLU(product) (EPI 4), in every tile
+// config: the three-product forward, and the two-product one of a zero-variance input
+#define TAGI_GEMM_COMBOS_FWD_RELU(X)                                                     \
+  X(PROD_FWD, LD_STR_K4, LD_STR_MN4) X(PROD_FWD, LD_STR_K_S, LD_STR_MN_S)
+#define TAGI_GEMM_COMBOS_SHARED_A_RELU(X)                                                \
+  X(PROD_SHARED_A, LD_STR_K4, LD_STR_MN4) X(PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S)
 
 template <int PROD, class CFG, int KA, int KB, int EPI = 0>
 void launch_cfg(const GemmArgs& g, int64_t grid_x, int64_t grid_y, hipStream_t s)
@@ -1984,10 +2018,10 @@ static inline int run_gemm(GemmArgs g, int64_t batch, const Plan& p, float* ws, 
       default: launch_cfg<PROD, C32x32, KA, KB, EPI>(g, gx, gy, s); break;
     }
   } else {
-    // EPI 2 applies its update in the kernel only when unsplit (the reduction's epilogue
-    // does it otherwise, from the same Epi fields)
-    constexpr int E = EPI == 2 ? 2 : 0;
-    if (E == 2 && p.splits > 1) {
+    // EPI 2 and 4 apply their epilogue in the kernel only when unsplit (the reduction's
+    // epilogue does it otherwise, from the same Epi fields)
+    constexpr int E = (EPI == 2 || EPI == 4) ? EPI : 0;
+    if (E != 0 && p.splits > 1) {
       switch (p.cfg) {
         case 0: launch_cfg<PROD, C128x128, KA, KB>(g, gx, gy, s); break;
         case 1: launch_cfg<PROD, C128x64, KA, KB>(g, gx, gy, s); break;

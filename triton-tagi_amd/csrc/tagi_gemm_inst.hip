@@ -26,8 +26,11 @@ using InstCfg = C128x32;
 #endif
 
 #define TAGI_INST(P, KA, KB) template void launch_cfg<P, InstCfg, KA, KB>(const GemmArgs&, int64_t, int64_t, hipStream_t);
+#define TAGI_INST_RELU(P, KA, KB) \
+  template void launch_cfg<P, InstCfg, KA, KB, 4>(const GemmArgs&, int64_t, int64_t, hipStream_t);
 #if TAGI_INST_PROD == 0
 TAGI_GEMM_COMBOS_FWD(TAGI_INST)
+TAGI_GEMM_COMBOS_FWD_RELU(TAGI_INST_RELU)
 #elif TAGI_INST_PROD == 1
 TAGI_GEMM_COMBOS_SHARED_B(TAGI_INST)
 #if TAGI_INST_CFG >= 3
@@ -41,6 +44,7 @@ TAGI_GEMM_COMBOS_SHARED_A(TAGI_INST)
 #define TAGI_INST_UPD(P, KA, KB) \
   template void launch_cfg<P, InstCfg, KA, KB, 2>(const GemmArgs&, int64_t, int64_t, hipStream_t);
 TAGI_GEMM_COMBOS_SHARED_A_UPD(TAGI_INST_UPD)
+TAGI_GEMM_COMBOS_SHARED_A_RELU(TAGI_INST_RELU)
 #endif
 
 }  // namespace tagi

@@ -31,23 +31,31 @@ int tagi::linear_fwd_check(const char* what, const float* ma, const float* Sa, c
 
 int tagi::linear_fwd_run(const char* what, const float* ma, const float* Sa, const float* mw, const float* Sw,
                          const float* mb, const float* Sb, float* mz, float* Sz, int64_t M, int64_t K, int64_t N,
-                         const Plan& p, float* ws, int64_t ws_bytes, hipStream_t s) {
-  ProfScope ps(FAM_LINEAR_FWD, s, 2.0 * 3 * M * K * N, 4.0 * (2 * M * K + 2 * K * N + 2 * M * N));
+                         const Plan& p, float* ws, int64_t ws_bytes, hipStream_t s, float* relu_J) {
+  ProfScope ps(FAM_LINEAR_FWD, s, 2.0 * 3 * M * K * N,
+               4.0 * (2 * M * K + 2 * K * N + (relu_J ? 3 : 2) * M * N));
   GemmArgs g{};
   g.a = strided_operand(ma, Sa, 1, 0, 0, K, 1, M, K);
   g.b = strided_operand(mw, Sw, 1, 0, 0, 1, N, N, K);
   g.epi = epi_store(mz, Sz, mb, Sb, 0, 1, 1.f, 1.f, 1, 0, 0, N, 1);
+  g.epi.relu_J = relu_J;
   g.R = (int)M;
   g.C = (int)N;
   g.Kred = (int)K;
   const bool v4 = K % 4 == 0 && N % 4 == 0 && al16(ma) && al16(Sa) && al16(mw) && al16(Sw);
+  if (relu_J) {
+    if (v4) return run_gemm<PROD_FWD, LD_STR_K4, LD_STR_MN4, 4>(g, 1, p, ws, ws_bytes, s, what);
+    return run_gemm<PROD_FWD, LD_STR_K_S, LD_STR_MN_S, 4>(g, 1, p, ws, ws_bytes, s, what);
+  }
   if (v4) return run_gemm<PROD_FWD, LD_STR_K4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
   return run_gemm<PROD_FWD, LD_STR_K_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
 }
 
+// The forward of a zero-variance input (Sa == NULL): two products, mean ma mw and variance
+// ma^2 Sw (the Sa terms are exact zeros). With relu_J, ReLU(z)'s moments and Jacobian.
 static int linear_fwd0(const char* what, const float* ma, const float* mw, const float* Sw, const float* mb,
                        const float* Sb, float* mz, float* Sz, int64_t M, int64_t K, int64_t N, float* ws,
-                       int64_t ws_bytes, hipStream_t s) {
+                       int64_t ws_bytes, hipStream_t s, float* relu_J) {
   TAGI_REQUIRE(ma && mw && Sw && Sz, "%s: null pointer", what);
   TAGI_REQUIRE(M > 0 && K > 0 && N > 0, "%s: sizes must be positive (M=%lld K=%lld N=%lld)", what, (long long)M,
                (long long)K, (long long)N);
@@ -55,29 +63,48 @@ static int linear_fwd0(const char* what, const float* ma, const float* mw, const
   Plan p = linear_fwd0_plan(M, K, N);
   if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, N, 1)))
     p = choose_plan(M, N, K, 1, PROD_SHARED_A, false, 1);
-  ProfScope ps(FAM_LINEAR_FWD, s, 2.0 * 2 * M * K * N, 4.0 * (M * K + 2 * K * N + 2 * M * N));
+  ProfScope ps(FAM_LINEAR_FWD, s, 2.0 * 2 * M * K * N, 4.0 * (M * K + 2 * K * N + (relu_J ? 3 : 2) * M * N));
   GemmArgs g{};
   g.a = strided_operand(ma, nullptr, 1, 0, 0, K, 1, M, K);
   g.b = strided_operand(mw, Sw, 1, 0, 0, 1, N, N, K);
   g.epi = epi_store(mz, Sz, mb, Sb, 0, 1, 1.f, 1.f, 1, 0, 0, N, 1);
+  g.epi.relu_J = relu_J;
   g.R = (int)M;
   g.C = (int)N;
   g.Kred = (int)K;
   const bool v4 = K % 4 == 0 && N % 4 == 0 && al16(ma) && al16(mw) && al16(Sw);
+  if (relu_J) {
+    if (v4) return run_gemm<PROD_SHARED_A, LD_STR_K4, LD_STR_MN4, 4>(g, 1, p, ws, ws_bytes, s, what);
+    return run_gemm<PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S, 4>(g, 1, p, ws, ws_bytes, s, what);
+  }
   if (v4) return run_gemm<PROD_SHARED_A, LD_STR_K4, LD_STR_MN4>(g, 1, p, ws, ws_bytes, s, what);
   return run_gemm<PROD_SHARED_A, LD_STR_MN_S, LD_STR_MN_S>(g, 1, p, ws, ws_bytes, s, what);
+}
+
+static int linear_fwd_impl(const char* what, const float* ma, const float* Sa, const float* mw, const float* Sw,
+                           const float* mb, const float* Sb, float* mz, float* Sz, float* relu_J, int64_t M,
+                           int64_t K, int64_t N, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+  if (!Sa) return linear_fwd0(what, ma, mw, Sw, mb, Sb, mz, Sz, M, K, N, ws, ws_bytes, as_stream(stream), relu_J);
+  int rc = linear_fwd_check(what, ma, Sa, mw, Sw, Sz, M, K, N);
+  if (rc != TAGI_OK) return rc;
+  Plan p = linear_fwd_plan(M, K, N);
+  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, N, 1))) p = choose_plan(M, N, K, 1, PROD_FWD, false, 1);
+  return linear_fwd_run(what, ma, Sa, mw, Sw, mb, Sb, mz, Sz, M, K, N, p, ws, ws_bytes, as_stream(stream), relu_J);
 }
 
 extern "C" int tagi_linear_fwd(const float* ma, const float* Sa, const float* mw, const float* Sw, const float* mb,
                                const float* Sb, float* mz, float* Sz, int64_t M, int64_t K, int64_t N, float* ws,
                                int64_t ws_bytes, tagi_stream_t stream) {
-  const char* what = "tagi_linear_fwd";
-  if (!Sa) return linear_fwd0(what, ma, mw, Sw, mb, Sb, mz, Sz, M, K, N, ws, ws_bytes, as_stream(stream));
-  int rc = linear_fwd_check(what, ma, Sa, mw, Sw, Sz, M, K, N);
-  if (rc != TAGI_OK) return rc;
-  Plan p = linear_fwd_plan(M, K, N);
-  if (p.splits > 1 && (ws == nullptr || ws_bytes < plan_ws_bytes(p, M, N, 1))) p = choose_plan(M, N, K, 1, PROD_FWD, false, 1);
-  return linear_fwd_run(what, ma, Sa, mw, Sw, mb, Sb, mz, Sz, M, K, N, p, ws, ws_bytes, as_stream(stream));
+  return linear_fwd_impl("tagi_linear_fwd", ma, Sa, mw, Sw, mb, Sb, mz, Sz, nullptr, M, K, N, ws, ws_bytes, stream);
+}
+
+extern "C" int tagi_linear_fwd_relu(const float* ma, const float* Sa, const float* mw, const float* Sw,
+                                    const float* mb, const float* Sb, float* ma_out, float* Sa_out, float* J,
+                                    int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes,
+                                    tagi_stream_t stream) {
+  const char* what = "tagi_linear_fwd_relu";
+  TAGI_REQUIRE(ma_out && Sa_out && J, "%s: null pointer", what);
+  return linear_fwd_impl(what, ma, Sa, mw, Sw, mb, Sb, ma_out, Sa_out, J, M, K, N, ws, ws_bytes, stream);
 }
 
 extern "C" int64_t tagi_linear_bwd_delta_ws_bytes(int64_t M, int64_t K, int64_t N) {
@@ -86,8 +113,9 @@ extern "C" int64_t tagi_linear_bwd_delta_ws_bytes(int64_t M, int64_t K, int64_t 
 }
 
 static int linear_bwd_delta_impl(const char* what, const float* dmz, const float* dSz, const float* mw,
-                                 const float* add_m, const float* add_S, float* dma, float* dSa, int64_t M, int64_t K,
-                                 int64_t N, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
+                                 const float* add_m, const float* add_S, const float* J, float* dma, float* dSa,
+                                 int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes,
+                                 tagi_stream_t stream) {
   TAGI_REQUIRE(dmz && dSz && mw && dma && dSa, "%s: null pointer", what);
   TAGI_REQUIRE((add_m == nullptr) == (add_S == nullptr), "%s: add_m and add_S must both be given or both be NULL",
                what);
@@ -101,6 +129,7 @@ static int linear_bwd_delta_impl(const char* what, const float* dmz, const float
   g.epi = epi_store(dma, dSa, nullptr, nullptr, 0, 0, 1.f, 1.f, 1, 0, 0, K, 1);
   g.epi.am = add_m;
   g.epi.av = add_S;
+  g.epi.jm = J;
   g.R = (int)M;
   g.C = (int)K;
   g.Kred = (int)N;
@@ -114,15 +143,23 @@ static int linear_bwd_delta_impl(const char* what, const float* dmz, const float
 extern "C" int tagi_linear_bwd_delta(const float* dmz, const float* dSz, const float* mw, float* dma, float* dSa,
                                      int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes,
                                      tagi_stream_t stream) {
-  return linear_bwd_delta_impl("tagi_linear_bwd_delta", dmz, dSz, mw, nullptr, nullptr, dma, dSa, M, K, N, ws,
-                               ws_bytes, stream);
+  return linear_bwd_delta_impl("tagi_linear_bwd_delta", dmz, dSz, mw, nullptr, nullptr, nullptr, dma, dSa, M, K, N,
+                               ws, ws_bytes, stream);
+}
+
+extern "C" int tagi_linear_bwd_delta_jacobian(const float* dmz, const float* dSz, const float* mw, const float* J,
+                                              float* dma, float* dSa, int64_t M, int64_t K, int64_t N, float* ws,
+                                              int64_t ws_bytes, tagi_stream_t stream) {
+  const char* what = "tagi_linear_bwd_delta_jacobian";
+  TAGI_REQUIRE(J, "%s: null pointer", what);
+  return linear_bwd_delta_impl(what, dmz, dSz, mw, nullptr, nullptr, J, dma, dSa, M, K, N, ws, ws_bytes, stream);
 }
 
 extern "C" int tagi_linear_bwd_delta_add(const float* dmz, const float* dSz, const float* mw, const float* add_m,
                                          const float* add_S, float* dma, float* dSa, int64_t M, int64_t K, int64_t N,
                                          float* ws, int64_t ws_bytes, tagi_stream_t stream) {
-  return linear_bwd_delta_impl("tagi_linear_bwd_delta_add", dmz, dSz, mw, add_m, add_S, dma, dSa, M, K, N, ws,
-                               ws_bytes, stream);
+  return linear_bwd_delta_impl("tagi_linear_bwd_delta_add", dmz, dSz, mw, add_m, add_S, nullptr, dma, dSa, M, K, N,
+                               ws, ws_bytes, stream);
 }
 
 extern "C" int64_t tagi_linear_wgrad_ws_bytes(int64_t M, int64_t K, int64_t N) {

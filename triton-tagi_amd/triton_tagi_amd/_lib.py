@@ -68,9 +68,11 @@ _SIGS = {
     "tagi_probe_stream": (c_int, [P, P, I64, I64, c_int, P]),
     "tagi_probe_stream_variant": (c_int, [P, P, I64, I64, I64, c_int, c_int, c_int, P]),
     "tagi_linear_fwd": (c_int, [P, P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
+    "tagi_linear_fwd_relu": (c_int, [P, P, P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
     "tagi_linear_fwd_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_linear_fwd_noalloc": (c_int, [P, P, P, P, P, P, P, P, I64, I64, I64, P]),
     "tagi_linear_bwd_delta": (c_int, [P, P, P, P, P, I64, I64, I64, P, I64, P]),
+    "tagi_linear_bwd_delta_jacobian": (c_int, [P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
     "tagi_linear_bwd_delta_ws_bytes": (I64, [I64, I64, I64]),
     "tagi_linear_bwd_delta_add": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),
     "tagi_linear_wgrad": (c_int, [P, P, P, P, P, P, P, P, P, I64, I64, I64, P, I64, P]),

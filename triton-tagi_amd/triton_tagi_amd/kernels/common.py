@@ -46,22 +46,54 @@ def linear_forward(ma, Sa, mw, Sw, mb=None, Sb=None, need_mean=True):
     return mz, Sz
 
 
+def linear_relu_forward(ma, Sa, mw, Sw, mb=None, Sb=None):
+    """(mu_a, S_a, J) of ReLU(a W + b) in one launch: the Linear forward (linear.py:99-100)
+    whose epilogue applies the ReLU moments (relu.py:94-122) in place of storing z; the same
+    bits as linear_forward followed by bayesian_relu. Sa None as in linear_forward."""
+    _2d(ma, "ma"), _2d(mw, "mw"), _2d(Sw, "Sw")
+    if Sa is not None:
+        _2d(Sa, "Sa")
+    M, K = ma.shape
+    K2, N = mw.shape
+    if K2 != K or (Sa is not None and Sa.shape != ma.shape) or Sw.shape != mw.shape:
+        raise ValueError(f"linear_relu_forward: shapes ma {tuple(ma.shape)} mw {tuple(mw.shape)} disagree")
+    for t, n in ((mb, "mb"), (Sb, "Sb")):
+        if t is not None:
+            _lib.check(t, n)
+            if t.numel() != N:
+                raise ValueError(f"{n}: expected {N} elements, got {t.numel()}")
+    # one allocation, each plane starting on a 256-byte boundary
+    plane = -(-(M * N) // 64) * 64
+    buf = torch.empty(3 * plane, device=ma.device, dtype=torch.float32)
+    am, aS, J = (buf[i * plane:i * plane + M * N].view(M, N) for i in range(3))
+    ws = _lib.workspace(_lib.query("tagi_linear_fwd_ws_bytes", M, K, N), ma.device)
+    wp, wb = _lib.ws_args(ws)
+    _lib.call("tagi_linear_fwd_relu", ma.data_ptr(), _lib.ptr(Sa), mw.data_ptr(), Sw.data_ptr(), _lib.ptr(mb),
+              _lib.ptr(Sb), am.data_ptr(), aS.data_ptr(), J.data_ptr(), M, K, N, wp, wb, _lib.stream_of(ma))
+    return am, aS, J
+
+
 def fused_var_forward(ma, Sa, mw, Sw, Sb):
     """Sz = ma^2 @ Sw + Sa @ (mw^2 + Sw) + Sb (common.py:170-210)."""
     return linear_forward(ma, Sa, mw, Sw, None, Sb, need_mean=False)[1]
 
 
-def fused_backward_delta(dmz, dSz, mw, add=None):
+def fused_backward_delta(dmz, dSz, mw, add=None, jacobian=None):
     """(dmz @ mw^T, dSz @ (mw^2)^T) (common.py:287-327).
 
     With ``add = (am, aS)`` (contiguous (M, K) tensors) the products are added to them in
-    place, in the GEMM epilogue, and ``add`` is returned.
+    place, in the GEMM epilogue, and ``add`` is returned. With ``jacobian`` (a contiguous
+    (M, K) tensor, the Jacobian of the elementwise layer in front, such as a ReLU's J) the
+    epilogue returns (dmz @ mw^T) * J and (dSz @ (mw^2)^T) * J^2 instead: the deltas at that
+    layer's input (relu.py:152-169).
     """
     _2d(dmz, "dmz"), _2d(dSz, "dSz"), _2d(mw, "mw")
     M, N = dmz.shape
     K = mw.shape[0]
     if mw.shape[1] != N or dSz.shape != dmz.shape:
         raise ValueError(f"fused_backward_delta: dmz {tuple(dmz.shape)} vs mw {tuple(mw.shape)}")
+    if add is not None and jacobian is not None:
+        raise ValueError("fused_backward_delta: an addend and a Jacobian cannot both be applied")
     ws = _lib.workspace(_lib.query("tagi_linear_bwd_delta_ws_bytes", M, K, N), dmz.device)
     wp, wb = _lib.ws_args(ws)
     if add is not None:
@@ -73,6 +105,13 @@ def fused_backward_delta(dmz, dSz, mw, add=None):
         return dma, dSa
     dma = torch.empty(M, K, device=dmz.device, dtype=torch.float32)
     dSa = torch.empty(M, K, device=dmz.device, dtype=torch.float32)
+    if jacobian is not None:
+        J = _lib.check(jacobian, "jacobian")
+        if tuple(J.shape) != (M, K) or not J.is_contiguous():
+            raise ValueError(f"fused_backward_delta: Jacobian {tuple(J.shape)} is not a contiguous ({M}, {K}) tensor")
+        _lib.call("tagi_linear_bwd_delta_jacobian", dmz.data_ptr(), dSz.data_ptr(), mw.data_ptr(), J.data_ptr(),
+                  dma.data_ptr(), dSa.data_ptr(), M, K, N, wp, wb, _lib.stream_of(dmz))
+        return dma, dSa
     _lib.call("tagi_linear_bwd_delta", dmz.data_ptr(), dSz.data_ptr(), mw.data_ptr(), dma.data_ptr(),
               dSa.data_ptr(), M, K, N, wp, wb, _lib.stream_of(dmz))
     return dma, dSa

@@ -44,6 +44,7 @@ from .avgpool2d import AvgPool2D
 from .batchnorm2d import BatchNorm2D
 from .conv2d import Conv2D
 from .flatten import Flatten
+from .linear import Linear
 from .relu import ReLU
 from .resblock import ResBlock
 
@@ -406,6 +407,10 @@ def forward_chain(layers, mu: Tensor, var: Tensor,
             if last:
                 add = None
             i += 2
+        elif isinstance(layer, Linear) and isinstance(nxt, ReLU) and mu.is_cuda:
+            # the ReLU's moments formed in the Linear product's epilogue
+            mu, var = layer.forward_relu(mu, var, nxt)
+            i += 2
         elif _fusable_relu_pool(layer, nxt, mu):
             # pooled moments in the row-major layout a following Flatten views as is
             mu, var = relu_avgpool_forward(layer, nxt, mu, var, nchw=i + 2 < n and isinstance(layers[i + 2], Flatten))
@@ -459,6 +464,12 @@ def backward_chain(layers, delta_mu: Tensor, delta_var: Tensor, add: tuple[Tenso
             continue
         if _fusable_pool_relu_backward(layer, prev):
             delta_mu, delta_var = avgpool_relu_backward(layer, prev, delta_mu, delta_var)
+            i -= 2
+            continue
+        if (isinstance(layer, Linear) and isinstance(prev, ReLU) and prev.J is not None
+                and layer.ma_in is not None and prev.J.numel() == layer.ma_in.numel() and delta_mu.is_cuda):
+            # the ReLU's Jacobian applied in the Linear input-delta product's epilogue
+            delta_mu, delta_var = layer.backward_jacobian(delta_mu, delta_var, prev.J)
             i -= 2
             continue
         if i == 0:

@@ -23,7 +23,8 @@ from torch import Tensor
 
 from .. import _overlap
 from ..base import LearnableLayer
-from ..kernels.common import fused_backward_delta, linear_forward, linear_param_deltas, linear_param_deltas_update
+from ..kernels.common import (fused_backward_delta, linear_forward, linear_param_deltas, linear_param_deltas_update,
+                              linear_relu_forward)
 from ..param_init import init_weight_bias_linear
 from ..update import in_backward
 from ..update.parameters import update_parameters
@@ -49,28 +50,48 @@ class Linear(LearnableLayer):
         self.ma_in = None
         self.delta_mw = self.delta_Sw = self.delta_mb = self.delta_Sb = None
 
-    def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
+    def _forward_input(self, ma: Tensor, Sa: Tensor | None):
         self._input_shape = ma.shape
         ma_flat = ma.reshape(-1, self.in_features).contiguous()
         # Sa None: a deterministic input (zero variance), which the kernel takes as such
         Sa_flat = None if Sa is None else Sa.reshape(-1, self.in_features).contiguous()
         self.ma_in = ma_flat
+        return ma_flat, Sa_flat, (*self._input_shape[:-1], self.out_features)
+
+    def forward(self, ma: Tensor, Sa: Tensor) -> tuple[Tensor, Tensor]:
+        ma_flat, Sa_flat, out_shape = self._forward_input(ma, Sa)
         mz, Sz = linear_forward(ma_flat, Sa_flat, _dense(self.mw), _dense(self.Sw), _dense(self.mb),
                                 _dense(self.Sb))
-        out_shape = (*self._input_shape[:-1], self.out_features)
         return mz.reshape(out_shape), Sz.reshape(out_shape)
+
+    def forward_relu(self, ma: Tensor, Sa: Tensor, relu) -> tuple[Tensor, Tensor]:
+        """``forward`` followed by ``relu.forward`` in one launch: the ReLU's moments are
+        formed in the product's epilogue and its Jacobian stored on ``relu`` as its own
+        forward stores it; z itself is never written."""
+        ma_flat, Sa_flat, out_shape = self._forward_input(ma, Sa)
+        am, aS, J = linear_relu_forward(ma_flat, Sa_flat, _dense(self.mw), _dense(self.Sw), _dense(self.mb),
+                                        _dense(self.Sb))
+        relu.J = J.reshape(out_shape)
+        return am.reshape(out_shape), aS.reshape(out_shape)
 
     def backward(self, delta_mz: Tensor, delta_Sz: Tensor) -> tuple[Tensor, Tensor]:
         return self._backward(delta_mz, delta_Sz, True)
+
+    def backward_jacobian(self, delta_mz: Tensor, delta_Sz: Tensor, J: Tensor) -> tuple[Tensor, Tensor]:
+        """``backward`` with the Jacobian ``J`` of the elementwise layer in front (a ReLU)
+        applied in the input-delta product's epilogue: returns the deltas at that layer's
+        input, as ``backward`` followed by its backward would."""
+        return self._backward(delta_mz, delta_Sz, True, jacobian=J)
 
     def backward_param_deltas(self, delta_mz: Tensor, delta_Sz: Tensor) -> None:
         """The parameter deltas of ``backward`` without forming the input deltas."""
         self._backward(delta_mz, delta_Sz, False)
 
-    def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool, add=None):
+    def _backward(self, delta_mz: Tensor, delta_Sz: Tensor, input_deltas: bool, add=None, jacobian=None):
         """Parameter deltas, and the input deltas when ``input_deltas``; with ``add`` (a pair
         of contiguous tensors shaped like the input deltas) those are added to it in place
-        and ``add`` is returned. Within ``update_in_backward`` the kernel that forms the
+        and ``add`` is returned; with ``jacobian`` (shaped like the input) the input deltas
+        are multiplied by it (variances by its square). Within ``update_in_backward`` the kernel that forms the
         parameter deltas also applies the capped update (after the input deltas, which read
         the weight means, are queued), unless that kernel goes to the side stream."""
         dmz = delta_mz.reshape(-1, self.out_features).contiguous()
@@ -83,7 +104,7 @@ class Linear(LearnableLayer):
         upd = in_backward.active() if (ctx is None or not big) and self._dense_params() else None
         out = None
         if upd is not None and input_deltas:
-            out = self._input_deltas(dmz, dSz, add)
+            out = self._input_deltas(dmz, dSz, add, jacobian)
         side = ctx.fork(dmz.device, self.ma_in, dmz, dSz) if ctx is not None and big else None
         bias = (_dense(self.mb), _dense(self.Sb)) if self.has_bias else (None, None)
         with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
@@ -98,14 +119,15 @@ class Linear(LearnableLayer):
             self.delta_mb, self.delta_Sb = dmb, dSb
         if not input_deltas or upd is not None:
             return out
-        return self._input_deltas(dmz, dSz, add)
+        return self._input_deltas(dmz, dSz, add, jacobian)
 
-    def _input_deltas(self, dmz: Tensor, dSz: Tensor, add):
+    def _input_deltas(self, dmz: Tensor, dSz: Tensor, add, jacobian=None):
         if add is not None:
             fused_backward_delta(dmz, dSz, _dense(self.mw), add=(add[0].view(-1, self.in_features),
                                                          add[1].view(-1, self.in_features)))
             return add
-        dma, dSa = fused_backward_delta(dmz, dSz, _dense(self.mw))
+        J = None if jacobian is None else jacobian.reshape(-1, self.in_features).contiguous()
+        dma, dSa = fused_backward_delta(dmz, dSz, _dense(self.mw), jacobian=J)
         in_shape = (*self._input_shape[:-1], self.in_features)
         return dma.reshape(in_shape), dSa.reshape(in_shape)
 
