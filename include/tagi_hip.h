@@ -38,6 +38,15 @@ int tagi_abi_version(void);
 /* Message of the last failing call on this host thread ("" if none). */
 const char* tagi_last_error(void);
 
+/* Orders stream `waiter` after the work queued on `producer` so far (both on one GPU):
+ * what is queued on `waiter` after the call starts once that work has finished. The event
+ * behind it carries no timing and no system-scope fence, so a fork or join between two
+ * streams costs no cache writeback. Also valid while the streams are being captured into
+ * a HIP graph (the wait becomes a graph edge). Replaces torch.cuda.Stream.wait_stream for
+ * the side stream of the parameter deltas; no counterpart in the reference, whose step
+ * runs on one stream (network.py:119-152). */
+int tagi_stream_wait(tagi_stream_t waiter, tagi_stream_t producer);
+
 /* Live per-kernel-family timer (HIP events around each launch, on the launch stream).
  * family_mask: bit f enables family f (TAGI_FAM_*). Events are created at begin. */
 int tagi_prof_begin(uint64_t family_mask);

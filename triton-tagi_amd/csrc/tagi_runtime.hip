@@ -79,13 +79,46 @@ extern "C" int tagi_abi_version(void) { return TAGI_ABI_VERSION; }
 
 extern "C" const char* tagi_last_error(void) { return g_err; }
 
+// Stream ordering through one untimed event per device and host thread, recorded without
+// the system-scope fence: a wait between two streams of one GPU needs the producer's work
+// to have finished, and the kernels' own device-scope release already makes their writes
+// visible to the device's other kernels. hipStreamWaitEvent orders the waiter after the
+// record that precedes the call, so the event is recorded again for the next call.
+extern "C" int tagi_stream_wait(tagi_stream_t waiter, tagi_stream_t producer) {
+  hipStream_t w = (hipStream_t)waiter, pr = (hipStream_t)producer;
+  if (w == pr) return TAGI_OK;
+  int dev = 0;
+  if (hipStreamGetDevice(pr, &dev) != hipSuccess) return fail(TAGI_ERR_ARG, "tagi_stream_wait: unknown producer stream");
+  constexpr int kMaxDev = 64;
+  thread_local hipEvent_t ev[kMaxDev] = {};
+  if (dev < 0 || dev >= kMaxDev) return fail(TAGI_ERR_ARG, "tagi_stream_wait: device %d out of range", dev);
+  if (!ev[dev]) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess || hipSetDevice(dev) != hipSuccess)
+      return fail(TAGI_ERR_LAUNCH, "tagi_stream_wait: cannot select device %d", dev);
+    const hipError_t e = hipEventCreateWithFlags(&ev[dev], hipEventDisableTiming | hipEventDisableSystemFence);
+    hipSetDevice(cur);
+    if (e != hipSuccess) {
+      ev[dev] = nullptr;
+      return fail(TAGI_ERR_LAUNCH, "tagi_stream_wait: hipEventCreate failed");
+    }
+  }
+  if (hipEventRecord(ev[dev], pr) != hipSuccess) return fail(TAGI_ERR_LAUNCH, "tagi_stream_wait: event record failed");
+  if (hipStreamWaitEvent(w, ev[dev], 0) != hipSuccess) return fail(TAGI_ERR_LAUNCH, "tagi_stream_wait: wait failed");
+  return TAGI_OK;
+}
+
 extern "C" int tagi_prof_begin(uint64_t family_mask) {
   Prof& p = prof();
   std::lock_guard<std::mutex> lk(p.mu);
   if (p.ev.empty()) {
     p.ev.resize(2 * kMaxSlots);
+    // timing-only events: no system-scope fence when they are recorded (that fence writes
+    // back the L2 and holds the queue for about 5 us per record; their timestamps are read
+    // after a device synchronisation)
     for (auto& e : p.ev) {
-      if (hipEventCreate(&e) != hipSuccess) return fail(TAGI_ERR_LAUNCH, "tagi_prof_begin: hipEventCreate failed");
+      if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess)
+        return fail(TAGI_ERR_LAUNCH, "tagi_prof_begin: hipEventCreate failed");
     }
     p.fam.resize(kMaxSlots);
     p.flops.resize(kMaxSlots);

@@ -62,6 +62,7 @@ _SIGS = {
     "tagi_abi_version": (c_int, []),
     "tagi_last_error": (c_char_p, []),
     "tagi_prof_begin": (c_int, [c_uint64]),
+    "tagi_stream_wait": (c_int, [P, P]),
     "tagi_prof_end": (c_int, [P, P, P, P]),
     "tagi_probe_mfma_loop": (c_int, [P, I64, I64, P]),
     "tagi_probe_mfma_mix": (c_int, [P, I64, I64, c_int, c_int, P]),
@@ -207,6 +208,12 @@ def stream_of(t: torch.Tensor) -> int:
     if _raw_stream is not None and t.is_cuda:
         return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def stream_wait(waiter: torch.cuda.Stream, producer: torch.cuda.Stream) -> None:
+    """Work queued on ``waiter`` from now on starts after the work queued on ``producer``
+    so far (torch.cuda.Stream.wait_stream without the event's system-scope fence)."""
+    call("tagi_stream_wait", waiter.cuda_stream, producer.cuda_stream)
 
 
 def check(t: torch.Tensor, name: str, contiguous: bool = True) -> torch.Tensor:

@@ -6,7 +6,9 @@ step. Within ``overlap_param_deltas`` such a layer queues its parameter-delta GE
 side stream (default priority) that first waits for everything queued so far on the
 current stream, so it runs beside the input-delta GEMMs and BatchNorm passes that follow
 and fills the CUs their tail rounds leave idle. Leaving the context makes the current
-stream wait for the side stream. The tensors the side stream reads (the layer input and
+stream wait for the side stream. Both waits go through tagi_stream_wait, whose event
+carries no system-scope fence (a torch event's fence holds the recording stream for
+about 5 us each time). The tensors the side stream reads (the layer input and
 the output deltas) are kept alive until then, so the caching allocator cannot hand their
 memory to later work on the current stream while the side stream still reads it.
 Running a ResBlock's projection branch on the side stream as well (beside the main
@@ -22,6 +24,8 @@ from __future__ import annotations
 import threading
 
 import torch
+
+from . import _lib
 
 # Products smaller than these (multiply-adds of one moment product) stay on the step's
 # stream. Measured on MI355X: the side stream gains 5% on ResNet-18 b128 (convs of 1-5 G
@@ -61,7 +65,7 @@ def fork(device) -> torch.cuda.Stream:
     side = side_stream(idx)
     cur = torch.cuda.current_stream(idx)
     if cur != side:
-        side.wait_stream(cur)
+        _lib.stream_wait(side, cur)
     return side
 
 
@@ -87,6 +91,6 @@ class overlap_param_deltas:
     def __exit__(self, exc_type, exc, tb):
         _tls.ctx = self._outer
         for idx, main in self._main.items():
-            main.wait_stream(side_stream(idx))
+            _lib.stream_wait(main, side_stream(idx))
         self._keep.clear()
         return False
