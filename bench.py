@@ -229,7 +229,9 @@ def linear_bench(args) -> dict:
     """Linear microbenchmark: per shape, W warm-up then K timed steps of forward moments,
     backward deltas (input deltas and parameter deltas) and the capped update. As in
     Sequential.step, the update is applied by the kernel that forms the parameter deltas
-    (update_in_backward); the layer's update() afterwards finds nothing left to do."""
+    (update_in_backward); the layer's update() afterwards finds nothing left to do. The
+    parameter deltas are applied without being stored (keep_deltas=False): the step's
+    result is the updated parameters, the same bits as with the deltas stored."""
     import torch
 
     from triton_tagi_amd import workloads
@@ -243,7 +245,7 @@ def linear_bench(args) -> dict:
 
         def step():
             layer.forward(ma, Sa)
-            with update_in_backward(cap):
+            with update_in_backward(cap, keep_deltas=False):
                 layer.backward(dmz, dSz)
             layer.update(cap)
 

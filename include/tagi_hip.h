@@ -182,8 +182,10 @@ int64_t tagi_linear_wgrad_ws_bytes(int64_t M, int64_t K, int64_t N);
  *   m += sign(dm) min(|dm|, sqrt(max(S, 1e-10)) / cap_factor),
  *   S += sign(dS) min(|dS|, same bound), S <= 0 -> 1e-5
  * to mw, Sw (and mb, Sb with the bias) in place, with the variance before the update in
- * the bound and in the deltas. The deltas are still written to dmw, dSw (dmb, dSb). The
- * bias needs mb, Sb, dmb and dSb together (or none). mw, Sw, mb, Sb must not overlap the
+ * the bound and in the deltas. The deltas are also written to dmw, dSw (dmb, dSb), unless
+ * those are all NULL: then they are applied without being stored (half the epilogue's
+ * writes). The bias needs mb and Sb together, and dmb, dSb with them when the deltas are
+ * stored. mw, Sw, mb, Sb must not overlap the
  * inputs or the delta outputs, and no other work may read them until the call completes
  * (the layer's input-delta product reads mw: run it first). ws: tagi_linear_wgrad_ws_bytes.
  * Replaces linear.py:138-151 followed by the layer's update (parameters.py:58-96,

@@ -192,23 +192,25 @@ def test_linear_microbench_shapes(dev, batch, fan_in, fan_out):
     assert_scaled_close(layer.Sw[kin][:, cols], uS, None, RTOL, ATOL, "updated Sw sample")
 
 
-@pytest.mark.parametrize("batch,fan_in,fan_out", [(256, 4096, 11008), (4096, 4096, 4096)])
+@pytest.mark.parametrize("batch,fan_in,fan_out", [(256, 4096, 11008), (4096, 4096, 4096), (300, 70, 45)])
 def test_linear_update_in_backward_equals_backward_then_update(dev, batch, fan_in, fan_out):
     """The microbenchmark step as bench.py times it (the capped update applied by the
-    parameter-delta kernel, ``update_in_backward``) against backward followed by
-    ``update`` from the same state: the same input deltas, parameter deltas and updated
-    parameters, bit for bit, and the layer's update() afterwards changes nothing."""
+    parameter-delta kernel, ``update_in_backward``, without storing the deltas) and the
+    same with the deltas stored, against backward followed by ``update`` from the same
+    state: the same input deltas, parameter deltas (where stored) and updated parameters,
+    bit for bit, and the layer's update() afterwards changes nothing. The shapes take the
+    update in the GEMM epilogue (vector and scalar loaders) and in the split-K reduction."""
     from triton_tagi_amd import workloads
     from triton_tagi_amd.update.in_backward import update_in_backward
     from triton_tagi_amd.update.parameters import get_cap_factor
 
     cap = get_cap_factor(batch)
     res = []
-    for fused in (False, True):
+    for fused in (False, True, "applied"):
         layer, ma, Sa, dmz, dSz = workloads.linear_microbench(batch, fan_in, fan_out)
         layer.forward(ma, Sa)
         if fused:
-            with update_in_backward(cap):
+            with update_in_backward(cap, keep_deltas=fused is True):
                 dma, dSa = layer.backward(dmz, dSz)
             assert layer._updated_in_backward
             before = [t.clone() for t in (layer.mw, layer.Sw, layer.mb, layer.Sb)]
@@ -223,8 +225,12 @@ def test_linear_update_in_backward_equals_backward_then_update(dev, batch, fan_i
         res.append([dma, dSa, layer.delta_mw, layer.delta_Sw, layer.delta_mb, layer.delta_Sb, layer.mw, layer.Sw,
                     layer.mb, layer.Sb])
     names = ("dma", "dSa", "delta_mw", "delta_Sw", "delta_mb", "delta_Sb", "mw", "Sw", "mb", "Sb")
-    for n, x, y in zip(names, *res):
+    for n, x, y, z in zip(names, *res):
         assert torch.equal(x, y), f"{n} differs between the fused and the separate update"
+        if n.startswith("delta"):
+            assert z is None, f"{n} stored although the deltas were only applied"
+        else:
+            assert torch.equal(x, z), f"{n} differs between the applied-only and the separate update"
 
 
 @pytest.mark.parametrize("name,overlap", [("mlp", True), ("cnn", True), ("transformer", False), ("transformer", True)])

@@ -182,7 +182,8 @@ struct Epi {
   // kind 1, optional: the capped update applied in place as the deltas are formed
   // (upd_mw/upd_Sw the weights, upd_mb/upd_Sb the bias, Sw/Sb their variances before the
   // update: the same arrays as upd_Sw/upd_Sb); each element is read and written by the
-  // one thread that forms its deltas
+  // one thread that forms its deltas. With the update, om/ov and dmb/dSb may be null:
+  // the deltas are then applied without being stored
   float* upd_mw;
   float* upd_Sw;
   float* upd_mb;
@@ -683,6 +684,10 @@ struct Loader {
 // ------------------------------------------------------------------------------------
 // Epilogue
 // ------------------------------------------------------------------------------------
+// OPT_DELTAS: the kind-1 deltas are stored only where om (dmb) is given -- the split-K
+// reduction's form; the GEMM kernel's, whose kind-1 outputs always exist, keeps the plain
+// stores (the extra branch, inlined per output, costs its 128-row tiles a stack frame).
+template <bool OPT_DELTAS = false>
 __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col, float m, float v) {
   if (e.kind == 0) {
     const int64_t off = (z / e.zdiv) * e.sz1 + (z % e.zdiv) * e.sz2 + (int64_t)row * e.srow + (int64_t)col * e.scol;
@@ -720,8 +725,10 @@ __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col,
       const int64_t idx = (int64_t)wr * e.ldw + col;
       const float s = e.Sw ? e.Sw[idx] : 1.f;
       const float dm = s * m, dS = (s * s) * v;
-      e.om[idx] = dm;
-      e.ov[idx] = dS;
+      if (!OPT_DELTAS || e.om) {
+        e.om[idx] = dm;
+        e.ov[idx] = dS;
+      }
       if (e.upd_mw) {
         float pm = e.upd_mw[idx], pS = s;
         capped(pm, pS, dm, dS, e.cap);
@@ -731,8 +738,10 @@ __device__ __forceinline__ void epi_apply(const Epi& e, int z, int row, int col,
     } else {
       const float s = e.Sb ? e.Sb[col] : 1.f;
       const float dm = s * m, dS = (s * s) * v;
-      e.dmb[col] = dm;
-      e.dSb[col] = dS;
+      if (!OPT_DELTAS || e.dmb) {
+        e.dmb[col] = dm;
+        e.dSb[col] = dS;
+      }
       if (e.upd_mb) {
         float pm = e.upd_mb[col], pS = s;
         capped(pm, pS, dm, dS, e.cap);
@@ -801,7 +810,7 @@ __device__ __forceinline__ bool epi_apply4(const Epi& e, int z, int row, int col
     float* ov = wrow ? e.ov : e.dSb;
     float* um = wrow ? e.upd_mw : e.upd_mb;
     float* uS = wrow ? e.upd_Sw : e.upd_Sb;
-    uintptr_t al = (uintptr_t)(om + idx) | (uintptr_t)(ov + idx);
+    uintptr_t al = om ? ((uintptr_t)(om + idx) | (uintptr_t)(ov + idx)) : 0;
     if (sp) al |= (uintptr_t)(sp + idx);
     if (um) al |= (uintptr_t)(um + idx) | (uintptr_t)(uS + idx);
     if (al & 15u) return false;
@@ -813,8 +822,10 @@ __device__ __forceinline__ bool epi_apply4(const Epi& e, int z, int row, int col
       dm[j] = sv[j] * m[j];
       dS[j] = (sv[j] * sv[j]) * v[j];
     }
-    *reinterpret_cast<float4*>(om + idx) = make_float4(dm[0], dm[1], dm[2], dm[3]);
-    *reinterpret_cast<float4*>(ov + idx) = make_float4(dS[0], dS[1], dS[2], dS[3]);
+    if (om) {
+      *reinterpret_cast<float4*>(om + idx) = make_float4(dm[0], dm[1], dm[2], dm[3]);
+      *reinterpret_cast<float4*>(ov + idx) = make_float4(dS[0], dS[1], dS[2], dS[3]);
+    }
     if (um) {
       const float4 m4 = *reinterpret_cast<const float4*>(um + idx);
       float pm[4] = {m4.x, m4.y, m4.z, m4.w}, pS[4] = {sv[0], sv[1], sv[2], sv[3]};
@@ -1522,6 +1533,8 @@ __global__ void __launch_bounds__(CFG::NTH, ((EPI == 1 || EPI == 3) && CFG::NTH 
     // parameter deltas (unsplit): the Sw (Sb) factors of a lane's 16 outputs are loaded
     // before any of them is stored -- the stores may alias them as far as the compiler
     // knows, so a load issued after a store would wait for it, element by element
+    const bool keep = e.om != nullptr;  // the update without stored deltas: om, dmb null
+    (void)keep;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -1563,13 +1576,17 @@ __global__ void __launch_bounds__(CFG::NTH, ((EPI == 1 || EPI == 3) && CFG::NTH 
               float pmu = pm[q][u], pS = sv;
               capped(pmu, pS, dm, dS, e.cap);
               if (w >= 0) {
-                e.om[w] = dm;
-                e.ov[w] = dS;
+                if (keep) {
+                  e.om[w] = dm;
+                  e.ov[w] = dS;
+                }
                 e.upd_mw[w] = pmu;
                 e.upd_Sw[w] = pS;
               } else {
-                e.dmb[col] = dm;
-                e.dSb[col] = dS;
+                if (keep) {
+                  e.dmb[col] = dm;
+                  e.dSb[col] = dS;
+                }
                 e.upd_mb[col] = pmu;
                 e.upd_Sb[col] = pS;
               }
@@ -1614,13 +1631,17 @@ __global__ void __launch_bounds__(CFG::NTH, ((EPI == 1 || EPI == 3) && CFG::NTH 
                 float pm = pm4[u], pS = sv;
                 capped(pm, pS, dm, dS, e.cap);
                 if (row < e.wrows) {
-                  e.om[wi[u]] = dm;
-                  e.ov[wi[u]] = dS;
+                  if (keep) {
+                    e.om[wi[u]] = dm;
+                    e.ov[wi[u]] = dS;
+                  }
                   e.upd_mw[wi[u]] = pm;
                   e.upd_Sw[wi[u]] = pS;
                 } else {
-                  e.dmb[col] = dm;
-                  e.dSb[col] = dS;
+                  if (keep) {
+                    e.dmb[col] = dm;
+                    e.dSb[col] = dS;
+                  }
                   e.upd_mb[col] = pm;
                   e.upd_Sb[col] = pS;
                 }
@@ -1756,7 +1777,7 @@ __global__ void __launch_bounds__(64 * G) splitk_reduce_kernel(const float* __re
     if (V > 1 && idx0 + e >= total) break;
     const int row = (int)(r / C);
     const int col = (int)(r - (int64_t)row * C);
-    epi_apply(epi, z, row, col, m[e], v[e]);
+    epi_apply<true>(epi, z, row, col, m[e], v[e]);
   }
 }
 

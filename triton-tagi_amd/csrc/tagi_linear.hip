@@ -173,14 +173,17 @@ namespace {
 int linear_wgrad_impl(const char* what, const float* ma, const float* dmz, const float* dSz, const float* Sw,
                       const float* Sb, float* dmw, float* dSw, float* dmb, float* dSb, float* mw, float* mb,
                       float cap, int64_t M, int64_t K, int64_t N, float* ws, int64_t ws_bytes, tagi_stream_t stream) {
-  TAGI_REQUIRE(ma && dmz && dSz && dmw && dSw, "%s: null pointer", what);
+  // with the update (mw given) the delta outputs may all be NULL: applied, not stored
+  const bool keep = dmw != nullptr;
+  TAGI_REQUIRE(ma && dmz && dSz && (keep || mw) && (dSw != nullptr) == keep, "%s: null pointer", what);
   TAGI_REQUIRE((dmb == nullptr) == (dSb == nullptr), "%s: dmb and dSb must both be given or both be NULL", what);
+  TAGI_REQUIRE(keep || dmb == nullptr, "%s: bias deltas without the weight deltas", what);
   TAGI_REQUIRE(M > 0 && K > 0 && N > 0, "%s: sizes must be positive", what);
   TAGI_REQUIRE(fits_i32(M * K) && fits_i32((K + 1) * N) && fits_i32(M * N), "%s: too large for 32-bit tiles", what);
   hipStream_t s = as_stream(stream);
   ProfScope ps(FAM_LINEAR_WGRAD, s, 2.0 * 2 * M * K * N,
-               4.0 * (M * K + 2 * M * N + 3 * K * N + (mw ? 3 * K * N : 0)));
-  const bool bias = dmb != nullptr;
+               4.0 * (M * K + 2 * M * N + (keep ? 3 : 1) * K * N + (mw ? 3 * K * N : 0)));
+  const bool bias = mw ? mb != nullptr : dmb != nullptr;
   GemmArgs g{};
   g.a = strided_operand(ma, nullptr, 1, 0, 0, 1, K, K, M);
   if (bias) g.a.ones_row = (int)K;
@@ -223,8 +226,9 @@ extern "C" int tagi_linear_wgrad_update(const float* ma, const float* dmz, const
                                         int64_t ws_bytes, tagi_stream_t stream) {
   const char* what = "tagi_linear_wgrad_update";
   TAGI_REQUIRE(mw && Sw, "%s: null pointer", what);
-  TAGI_REQUIRE((dmb == nullptr) == (mb == nullptr) && (mb == nullptr) == (Sb == nullptr),
-               "%s: the bias needs mb, Sb, dmb and dSb together (or none of them)", what);
+  TAGI_REQUIRE((mb == nullptr) == (Sb == nullptr) && (dmw == nullptr || (dmb == nullptr) == (mb == nullptr)),
+               "%s: the bias needs mb, Sb, dmb and dSb together (or none of them; dmb, dSb NULL when the deltas "
+               "are not stored)", what);
   TAGI_REQUIRE(cap_factor > 0.f && cap_factor <= 3.4e38f, "%s: cap_factor must be positive and finite", what);
   return linear_wgrad_impl(what, ma, dmz, dSz, Sw, Sb, dmw, dSw, dmb, dSb, mw, mb, cap_factor, M, K, N, ws, ws_bytes,
                            stream);

@@ -135,11 +135,12 @@ def _wgrad(a, dmz, dSz, Sw, Sb, bias):
     return dmw, dSw, dmb, dSb
 
 
-def linear_param_deltas_update(ma_in, dmz, dSz, mw, Sw, mb, Sb, cap_factor):
+def linear_param_deltas_update(ma_in, dmz, dSz, mw, Sw, mb, Sb, cap_factor, keep_deltas=True):
     """``linear_param_deltas`` followed by the capped update of mw, Sw (and mb, Sb when
     given) with ``cap_factor`` (parameters.py:58-96), applied in place by the kernel that
-    forms the deltas; returns the deltas. mw must not be read by work still queued (the
-    layer's input-delta product reads it: queue that first)."""
+    forms the deltas; returns the deltas (four Nones with ``keep_deltas=False``: applied,
+    not stored). mw must not be read by work still queued (the layer's input-delta product
+    reads it: queue that first)."""
     for t, n in ((mw, "mw"), (Sw, "Sw")):
         _lib.check(t, n)
     if mb is not None:
@@ -151,16 +152,16 @@ def linear_param_deltas_update(ma_in, dmz, dSz, mw, Sw, mb, Sb, cap_factor):
         raise ValueError(f"weight deltas: a {tuple(ma_in.shape)} vs dmz {tuple(dmz.shape)}, mw {tuple(mw.shape)}")
     if mb is not None and (mb.numel() != N or Sb.numel() != N):
         raise ValueError(f"weight deltas: bias of {mb.numel()} for {N} outputs")
-    bias = mb is not None
+    bias = mb is not None and keep_deltas
     dev = ma_in.device
-    dmw = torch.empty(K, N, device=dev, dtype=torch.float32)
-    dSw = torch.empty(K, N, device=dev, dtype=torch.float32)
+    dmw = torch.empty(K, N, device=dev, dtype=torch.float32) if keep_deltas else None
+    dSw = torch.empty(K, N, device=dev, dtype=torch.float32) if keep_deltas else None
     dmb = torch.empty(1, N, device=dev, dtype=torch.float32) if bias else None
     dSb = torch.empty(1, N, device=dev, dtype=torch.float32) if bias else None
     ws = _lib.workspace(_lib.query("tagi_linear_wgrad_ws_bytes", M, K, N), dev)
     wp, wb = _lib.ws_args(ws)
     _lib.call("tagi_linear_wgrad_update", ma_in.data_ptr(), dmz.data_ptr(), dSz.data_ptr(), mw.data_ptr(),
-              Sw.data_ptr(), _lib.ptr(mb), _lib.ptr(Sb), dmw.data_ptr(), dSw.data_ptr(), _lib.ptr(dmb),
+              Sw.data_ptr(), _lib.ptr(mb), _lib.ptr(Sb), _lib.ptr(dmw), _lib.ptr(dSw), _lib.ptr(dmb),
               _lib.ptr(dSb), float(cap_factor), M, K, N, wp, wb, _lib.stream_of(ma_in))
     return dmw, dSw, dmb, dSb
 

@@ -110,7 +110,7 @@ class Linear(LearnableLayer):
         with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
             if upd is not None:
                 dmw, dSw, dmb, dSb = linear_param_deltas_update(self.ma_in, dmz, dSz, self.mw, self.Sw, *bias,
-                                                                upd.cap_factor)
+                                                                upd.cap_factor, upd.keep_deltas)
             else:
                 dmw, dSw, dmb, dSb = linear_param_deltas(self.ma_in, dmz, dSz, _dense(self.Sw), bias[1])
         self._updated_in_backward = upd is not None
