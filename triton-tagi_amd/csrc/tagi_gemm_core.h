@@ -1852,7 +1852,10 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
   static const double kEff[6][3] = {{0.624, 0.353, 0.483}, {0.595, 0.632, 0.608}, {0.465, 0.519, 0.492},
                                     {0.655, 0.639, 0.687}, {0.300, 0.398, 0.442}, {0.655, 0.374, 0.427}};
   static const int kWaves[] = {8, 4, 4, 4, 1, 4};
-  static const int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 20, 24, 32, 40, 48, 64, 80, 96, 128, 160, 192, 256};
+  // (up to 512: the parameter deltas of a conv on a 3-channel input reduce over all N*H*W
+  // pixels into one or two tiles, so their splits are the whole launch)
+  static const int kSplits[] = {1,  2,  3,  4,  5,  6,   8,   10,  12,  16,  20,  24,  32,
+                                40, 48, 64, 80, 96, 128, 160, 192, 256, 320, 384, 512};
   const double kOcc2 = 0.924, kOcc1 = 0.667, kOcc0 = 0.35;
   const double kSplitSecPerByte = 1.82e-13, kSplitLaunch = 5.95e-6;
   // Small problems (fewer than 128 tiles of 64 x 64, the Linear layers of the MLP and CNN
@@ -1868,7 +1871,7 @@ static inline Plan choose_plan_uncached(int64_t R, int64_t C, int64_t Kred, int6
   Plan best{3, 1, (int)Kred, 1, 1};
   double best_t = DBL_MAX;
   const double peak_cu = 157.3e12 / 256.0;
-  const int64_t max_sp = allow_split ? (max_splits < 256 ? max_splits : 256) : 1;
+  const int64_t max_sp = allow_split ? (max_splits < 512 ? max_splits : 512) : 1;
   for (int ci = 0; ci < kNumCfg; ++ci) {
     const int BM = kCfg[ci].BM, BN = kCfg[ci].BN;
     const int64_t tm = cdiv(R, BM), tn = cdiv(C, BN);
