@@ -191,7 +191,18 @@ def call(name: str, *args) -> None:
         raise RuntimeError(f"{name} failed (status {rc}): {last_error()}")
 
 
+_queries: dict = {}
+
+
 def query(name: str, *args) -> int:
+    """Value of a size query. Queries taking only integers (the workspace sizes of a shape,
+    fixed by the deterministic plan choice) are answered once per argument tuple."""
+    if all(type(a) is int for a in args):
+        key = (name, *args)
+        v = _queries.get(key)
+        if v is None:
+            v = _queries[key] = int(_fn(name)(*args))
+        return v
     return int(_fn(name)(*args))
 
 

@@ -62,10 +62,7 @@ def linear_relu_forward(ma, Sa, mw, Sw, mb=None, Sb=None):
             _lib.check(t, n)
             if t.numel() != N:
                 raise ValueError(f"{n}: expected {N} elements, got {t.numel()}")
-    # one allocation, each plane starting on a 256-byte boundary
-    plane = -(-(M * N) // 64) * 64
-    buf = torch.empty(3 * plane, device=ma.device, dtype=torch.float32)
-    am, aS, J = (buf[i * plane:i * plane + M * N].view(M, N) for i in range(3))
+    am, aS, J = (torch.empty(M, N, device=ma.device, dtype=torch.float32) for _ in range(3))
     ws = _lib.workspace(_lib.query("tagi_linear_fwd_ws_bytes", M, K, N), ma.device)
     wp, wb = _lib.ws_args(ws)
     _lib.call("tagi_linear_fwd_relu", ma.data_ptr(), _lib.ptr(Sa), mw.data_ptr(), Sw.data_ptr(), _lib.ptr(mb),
