@@ -101,3 +101,20 @@ def test_heads_refuse_cpu_tensors():
         compute_innovation_with_indices(t, t, torch.zeros(2, 4), torch.zeros(2, 4), torch.ones(2, 4, dtype=torch.int32))
     with pytest.raises(ValueError, match="GPU only"):
         tt.MaxPool2D(2).forward(torch.zeros(1, 1, 4, 4), torch.zeros(1, 1, 4, 4))
+
+
+def test_size_queries_and_their_cache():
+    """Workspace sizes come from the plan choice, on the host. The parameter deltas of a
+    76 x 32 output reduced over 131072 pixels (a 5 x 5 conv on a 3-channel input, with its
+    bias row, at batch 128 on 32 x 32) split 512 ways, each split writing both moments; and
+    the Python side's cache answers integer-only queries exactly as the library does."""
+    from triton_tagi_amd import _lib
+
+    lib = _lib.load()
+    assert lib.tagi_linear_wgrad_ws_bytes(131072, 75, 32) == 512 * 2 * 76 * 32 * 4
+    for args in ((256, 784, 256), (300, 70, 45), (131072, 75, 32)):
+        for name in ("tagi_linear_fwd_ws_bytes", "tagi_linear_bwd_delta_ws_bytes", "tagi_linear_wgrad_ws_bytes"):
+            direct = getattr(lib, name)(*args)
+            assert _lib.query(name, *args) == direct
+            assert (name, *args) in _lib._queries
+            assert _lib.query(name, *args) == direct
